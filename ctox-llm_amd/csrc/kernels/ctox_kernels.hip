@@ -1,0 +1,3 @@
+// Single code object for every gfx950 kernel of the backend.
+#include "qmatvec.hip"
+#include "gated_delta.hip"

@@ -1,0 +1,825 @@
+// Host side of the C ABI declared in include/ctox_hip.h.
+//
+// A thin launcher over the HIP module API: the gfx950 code object built from
+// csrc/kernels is embedded in this library, loaded with hipModuleLoadData at
+// backend creation, and every kernel is started with hipModuleLaunchKernel
+// with a single by-value argument block (csrc/kernels/kernel_args.h). This
+// mirrors the role of the reference's driver-API runtime
+// (Q/src/backend/cuda_runtime.rs:195-294, 1297-1371), not its structure.
+//
+// Validation restates the crate's CPU dispatcher contract
+// (Q/src/backend/cpu.rs:41-173, 312-337, 478-490; Q/src/reference.rs:18-34,
+// 241-263, 387-396) so that errors match kind for kind. There is no CPU
+// fallback anywhere in this file: a missing device or code object fails
+// closed with CTOX_ERR_UNSUPPORTED_OPERATION.
+#include "ctox_hip.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../kernels/kernel_args.h"
+
+// ---- embedded gfx950 code object ----
+extern "C" const unsigned char ctox_hsaco_begin[];
+extern "C" const unsigned char ctox_hsaco_end[];
+__asm__(".section .rodata\n"
+        ".balign 64\n"
+        ".global ctox_hsaco_begin\n"
+        "ctox_hsaco_begin:\n"
+        ".incbin \"" CTOX_HSACO_PATH "\"\n"
+        ".global ctox_hsaco_end\n"
+        "ctox_hsaco_end:\n"
+        ".byte 0\n"
+        ".previous\n");
+
+namespace {
+
+thread_local std::string g_last_error;
+
+ctox_status fail(ctox_status st, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return st;
+}
+
+#define HIP_TRY(expr)                                                                          \
+    do {                                                                                       \
+        hipError_t e_ = (expr);                                                                \
+        if (e_ != hipSuccess)                                                                  \
+            return fail(CTOX_ERR_INVALID_STATE, "HIP call %s failed: %s", #expr,               \
+                        hipGetErrorString(e_));                                                \
+    } while (0)
+
+constexpr size_t kBlockLen = CTOX_BLOCK_LEN;
+
+size_t block_bytes(int32_t dtype) {
+    return dtype == CTOX_DTYPE_Q2B64 ? CTOX_Q2_BLOCK_BYTES
+                                     : (dtype == CTOX_DTYPE_Q4B64 ? CTOX_Q4_BLOCK_BYTES : 0);
+}
+
+float f16_bits_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16, exp = (h >> 10) & 0x1f, man = h & 0x3ff, bits;
+    if (exp == 0) {
+        if (man == 0) {
+            bits = sign;
+        } else {
+            int e = -1;
+            do {
+                man <<= 1;
+                e++;
+            } while ((man & 0x400) == 0);
+            bits = sign | ((uint32_t)(112 - e) << 23) | ((man & 0x3ff) << 13);
+        }
+    } else if (exp == 31) {
+        bits = sign | 0x7f800000u | (man << 13);
+    } else {
+        bits = sign | ((exp + 112) << 23) | (man << 13);
+    }
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+bool scale_finite(const ctox_scale_slice &s, size_t *bad) {
+    for (size_t i = 0; i < s.len; i++) {
+        float v = s.kind == CTOX_SCALE_F32
+                      ? ((const float *)s.data)[i]
+                      : f16_bits_to_f32((uint16_t)(((const uint8_t *)s.data)[2 * i] |
+                                                   (((const uint8_t *)s.data)[2 * i + 1] << 8)));
+        if (!std::isfinite(v)) {
+            *bad = i;
+            return false;
+        }
+    }
+    return true;
+}
+
+// Checks every packed block scale of `rows` rows (the CPU dispatcher rejects
+// a non-finite scale with InvalidArtifact while it walks the row,
+// Q/src/backend/cpu.rs:185-190; a device kernel cannot fail per block, so the
+// host checks up front).
+bool block_scales_finite(const uint8_t *w, size_t rows, size_t blocks, size_t bb) {
+    for (size_t r = 0; r < rows * blocks; r++) {
+        const uint8_t *blk = w + r * bb;
+        if (!std::isfinite(f16_bits_to_f32((uint16_t)(blk[0] | (blk[1] << 8))))) return false;
+    }
+    return true;
+}
+
+struct DevBuf {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+};
+
+}  // namespace
+
+struct ctox_hip_backend {
+    int device = 0;
+    char arch[64] = {0};
+    hipModule_t module = nullptr;
+    hipStream_t stream = nullptr;
+    hipFunction_t prep = nullptr, q4_b4 = nullptr, q4_b8 = nullptr, q2_b4 = nullptr,
+                  q2_b8 = nullptr, rec_row = nullptr, row_dot = nullptr, gdn_norms = nullptr,
+                  gdn_scan = nullptr;
+    // Activation staging (two layouts: [0] Q2, [1] Q4), split-K partials,
+    // counters (self-resetting, zeroed once) and gated-delta norms.
+    DevBuf xa[2], xc[2], partial, counters, norms;
+};
+
+struct ctox_hip_matrix {
+    ctox_hip_backend *backend = nullptr;
+    int32_t dtype = 0;
+    size_t rows = 0, columns = 0;
+    std::vector<ctox_quant_segment> segments;  // pure matrices hold one synthetic segment
+    void *d_weights = nullptr;
+    size_t weights_len = 0;
+    void *d_s_in = nullptr;
+    uint32_t s_in_kind = CTOX_KSCALE_NONE;
+    void *d_s_out = nullptr;
+    uint32_t s_out_kind = CTOX_KSCALE_NONE;
+    float *d_bias = nullptr;
+    uint32_t activation = 0;
+    std::vector<uint8_t> s_in_host;  // exact s_in bytes, for fan-out sharing checks
+};
+
+namespace {
+
+ctox_status ensure(ctox_hip_backend *b, DevBuf &buf, size_t bytes, bool zero) {
+    if (buf.bytes >= bytes) return CTOX_OK;
+    // Grow: work queued on any stream may still read the old buffer.
+    HIP_TRY(hipDeviceSynchronize());
+    if (buf.ptr) HIP_TRY(hipFree(buf.ptr));
+    buf.ptr = nullptr;
+    buf.bytes = 0;
+    size_t want = bytes < 4096 ? 4096 : bytes;
+    HIP_TRY(hipMalloc(&buf.ptr, want));
+    if (zero) {
+        HIP_TRY(hipMemset(buf.ptr, 0, want));
+        HIP_TRY(hipDeviceSynchronize());
+    }
+    buf.bytes = want;
+    (void)b;
+    return CTOX_OK;
+}
+
+template <typename Args>
+ctox_status launch(hipFunction_t f, dim3 grid, dim3 block, hipStream_t s, Args args,
+                   const char *name) {
+    void *params[] = {&args};
+    hipError_t e = hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, s,
+                                         params, nullptr);
+    if (e != hipSuccess)
+        return fail(CTOX_ERR_INVALID_STATE, "launch of %s failed: %s", name, hipGetErrorString(e));
+    return CTOX_OK;
+}
+
+hipStream_t pick_stream(ctox_hip_backend *b, void *s) { return s ? (hipStream_t)s : b->stream; }
+
+// Q/src/backend/cpu.rs:41-173 (same order of checks and error kinds).
+ctox_status validate_matvec(const ctox_fused_matvec *op, bool need_input, size_t *bpr) {
+    if (op->columns == 0 || op->rows == 0 || op->columns % kBlockLen != 0)
+        return fail(CTOX_ERR_SHAPE,
+                    "Q2/Q4 fused matvec dimensions must be non-zero and columns divisible by 64");
+    if (need_input && op->input_len != op->columns)
+        return fail(CTOX_ERR_SHAPE, "input has %zu, expected %zu values", op->input_len, op->columns);
+    if (op->s_in.kind != CTOX_SCALE_NONE && op->s_in.len != op->columns)
+        return fail(CTOX_ERR_SHAPE, "s_in length differs from columns");
+    if (op->s_out.kind != CTOX_SCALE_NONE && op->s_out.len != op->rows)
+        return fail(CTOX_ERR_SHAPE, "s_out length differs from rows");
+    if (op->bias && op->bias_len != op->rows)
+        return fail(CTOX_ERR_SHAPE, "bias length differs from rows");
+    const size_t blocks = op->columns / kBlockLen;
+    if (op->dtype == CTOX_DTYPE_Q2B64 || op->dtype == CTOX_DTYPE_Q4B64) {
+        if (op->n_segments)
+            return fail(CTOX_ERR_INVALID_ARTIFACT, "pure Q2/Q4 operation declares mixed row segments");
+        const size_t expected = op->rows * blocks * block_bytes(op->dtype);
+        if (op->weights_len != expected)
+            return fail(CTOX_ERR_SHAPE, "weight buffer has %zu bytes, expected %zu", op->weights_len,
+                        expected);
+        *bpr = blocks;
+        return CTOX_OK;
+    }
+    if (op->dtype != CTOX_DTYPE_MIXED_Q2Q4B64)
+        return fail(CTOX_ERR_UNSUPPORTED_DTYPE, "unsupported quantization dtype %d", op->dtype);
+    if (op->n_segments == 0)
+        return fail(CTOX_ERR_INVALID_ARTIFACT, "mixed Q2/Q4 operation has no row segments");
+    uint64_t row = 0, off = 0;
+    for (size_t g = 0; g < op->n_segments; g++) {
+        const ctox_quant_segment &s = op->segments[g];
+        if (s.group_index != g || s.row_start != row || s.row_end <= s.row_start ||
+            s.row_end > op->rows || s.offset != off)
+            return fail(CTOX_ERR_INVALID_ARTIFACT, "mixed Q2/Q4 operation has non-contiguous segment %u",
+                        s.group_index);
+        const size_t sb = block_bytes(s.dtype);
+        if (!sb)
+            return fail(CTOX_ERR_INVALID_ARTIFACT, "mixed Q2/Q4 segment %u has invalid dtype %d",
+                        s.group_index, s.dtype);
+        const uint64_t expected = (s.row_end - s.row_start) * blocks * sb;
+        if (s.length != expected)
+            return fail(CTOX_ERR_INVALID_ARTIFACT, "mixed Q2/Q4 segment %u has %llu bytes, expected %llu",
+                        s.group_index, (unsigned long long)s.length, (unsigned long long)expected);
+        row = s.row_end;
+        off += s.length;
+    }
+    if (row != op->rows || off != op->weights_len)
+        return fail(CTOX_ERR_SHAPE, "mixed segments cover %llu/%zu rows and %llu/%zu bytes",
+                    (unsigned long long)row, op->rows, (unsigned long long)off, op->weights_len);
+    *bpr = blocks;
+    return CTOX_OK;
+}
+
+ctox_status check_matrix_scales(const ctox_fused_matvec *op, size_t blocks) {
+    size_t bad;
+    if (op->s_in.kind != CTOX_SCALE_NONE && !scale_finite(op->s_in, &bad))
+        return fail(CTOX_ERR_INVALID_ARTIFACT, "recovery scale %zu is non-finite", bad);
+    if (op->s_out.kind != CTOX_SCALE_NONE && !scale_finite(op->s_out, &bad))
+        return fail(CTOX_ERR_INVALID_ARTIFACT, "recovery scale %zu is non-finite", bad);
+    if (op->dtype != CTOX_DTYPE_MIXED_Q2Q4B64) {
+        if (!block_scales_finite(op->weights, op->rows, blocks, block_bytes(op->dtype)))
+            return fail(CTOX_ERR_INVALID_ARTIFACT, "%s block scale is non-finite",
+                        op->dtype == CTOX_DTYPE_Q2B64 ? "Q2" : "Q4");
+    } else {
+        for (size_t g = 0; g < op->n_segments; g++) {
+            const ctox_quant_segment &s = op->segments[g];
+            if (!block_scales_finite(op->weights + s.offset, s.row_end - s.row_start, blocks,
+                                     block_bytes(s.dtype)))
+                return fail(CTOX_ERR_INVALID_ARTIFACT, "%s block scale is non-finite",
+                            s.dtype == CTOX_DTYPE_Q2B64 ? "Q2" : "Q4");
+        }
+    }
+    return CTOX_OK;
+}
+
+ctox_status upload(const void *host, size_t bytes, void **dev) {
+    *dev = nullptr;
+    if (!bytes) return CTOX_OK;
+    HIP_TRY(hipMalloc(dev, bytes));
+    HIP_TRY(hipMemcpy(*dev, host, bytes, hipMemcpyHostToDevice));
+    return CTOX_OK;
+}
+
+uint32_t kernel_scale_kind(int32_t kind) {
+    return kind == CTOX_SCALE_F32 ? CTOX_KSCALE_F32
+                                  : (kind == CTOX_SCALE_F16LE ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE);
+}
+
+// Converts `batch` activation rows into the MFMA A-fragment layout `layout`
+// (0 = Q2 element order, 1 = Q4 element order).
+ctox_status run_prep(ctox_hip_backend *b, int layout, const float *d_input, size_t columns,
+                     size_t batch, const void *d_s_in, uint32_t s_in_kind, hipStream_t s) {
+    const size_t blocks = columns / kBlockLen;
+    const size_t tgroups = (batch + 3) / 4;
+    ctox_status st = ensure(b, b->xa[layout], blocks * tgroups * 64 * 16, false);
+    if (!st) st = ensure(b, b->xc[layout], blocks * batch * 2 * sizeof(float), false);
+    if (st) return st;
+    PrepArgs a{};
+    a.input = d_input;
+    a.s_in = d_s_in;
+    a.xa = (int8_t *)b->xa[layout].ptr;
+    a.xc = (float *)b->xc[layout].ptr;
+    a.columns = (uint32_t)columns;
+    a.batch = (uint32_t)batch;
+    a.dtype = (uint32_t)layout;
+    a.s_in_kind = s_in_kind;
+    a.tgroups = (uint32_t)tgroups;
+    return launch(b->prep, dim3((unsigned)blocks, (unsigned)batch), dim3(64), s, a,
+                  "ctox_prep_activation_gfx950");
+}
+
+// One launch over `rows` packed rows of one dtype (a pure matrix or one
+// mixed segment), output rows written at d_output[m*out_stride + r].
+ctox_status run_matvec(ctox_hip_backend *b, int32_t dtype, const void *d_weights, size_t rows,
+                       size_t columns, size_t batch, const void *d_s_out, uint32_t s_out_kind,
+                       const float *d_bias, float *d_output, size_t out_stride, uint32_t act,
+                       hipStream_t s) {
+    const size_t blocks = columns / kBlockLen;
+    const size_t rowgroups = (rows + CTOX_MV_ROWS - 1) / CTOX_MV_ROWS;
+    const size_t ksplit = (blocks + CTOX_KCHUNK - 1) / CTOX_KCHUNK;
+    const size_t tgroups = (batch + 3) / 4;
+    const int layout = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
+    if (rowgroups * ksplit > 0x7fffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
+    if (ksplit > 1) {
+        ctox_status st = ensure(b, b->partial, rowgroups * ksplit * batch * CTOX_MV_ROWS * sizeof(float),
+                                false);
+        if (!st) st = ensure(b, b->counters, rowgroups * sizeof(uint32_t), true);
+        if (st) return st;
+    }
+    MatvecArgs a{};
+    a.weights = (const uint8_t *)d_weights;
+    a.weights_len = (uint64_t)rows * blocks * block_bytes(dtype);
+    a.xa = (const int8_t *)b->xa[layout].ptr;
+    a.xc = (const float *)b->xc[layout].ptr;
+    a.s_out = d_s_out;
+    a.bias = d_bias;
+    a.output = d_output;
+    a.partial = (float *)b->partial.ptr;
+    a.counters = (uint32_t *)b->counters.ptr;
+    a.rows = (uint32_t)rows;
+    a.columns = (uint32_t)columns;
+    a.batch = (uint32_t)batch;
+    a.tgroups = (uint32_t)tgroups;
+    a.ksplit = (uint32_t)ksplit;
+    a.out_stride = (uint32_t)out_stride;
+    a.s_out_kind = s_out_kind;
+    a.activation = act;
+    hipFunction_t f = dtype == CTOX_DTYPE_Q4B64 ? (tgroups == 1 ? b->q4_b4 : b->q4_b8)
+                                                : (tgroups == 1 ? b->q2_b4 : b->q2_b8);
+    return launch(f, dim3((unsigned)(rowgroups * ksplit)), dim3(256), s, a, "ctox_q*_matvec_gfx950");
+}
+
+ctox_status dispatch_matrix(ctox_hip_backend *b, const ctox_hip_matrix *m, const float *d_input,
+                            size_t batch, float *d_output, hipStream_t s, bool prepped[2],
+                            uint32_t act) {
+    for (const ctox_quant_segment &seg : m->segments) {
+        const int layout = seg.dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
+        if (!prepped[layout]) {
+            ctox_status st = run_prep(b, layout, d_input, m->columns, batch, m->d_s_in, m->s_in_kind, s);
+            if (st) return st;
+            prepped[layout] = true;
+        }
+        const size_t r0 = seg.row_start, nrows = seg.row_end - seg.row_start;
+        const void *so = nullptr;
+        if (m->s_out_kind == CTOX_KSCALE_F32) so = (const float *)m->d_s_out + r0;
+        if (m->s_out_kind == CTOX_KSCALE_F16) so = (const uint16_t *)m->d_s_out + r0;
+        ctox_status st = run_matvec(b, seg.dtype, (const uint8_t *)m->d_weights + seg.offset, nrows,
+                                    m->columns, batch, so, m->s_out_kind, m->d_bias ? m->d_bias + r0 : nullptr,
+                                    d_output + r0, m->rows, act, s);
+        if (st) return st;
+    }
+    return CTOX_OK;
+}
+
+ctox_status check_finite_host(const float *v, size_t n, const char *what) {
+    for (size_t i = 0; i < n; i++)
+        if (!std::isfinite(v[i]))
+            return fail(CTOX_ERR_INVALID_STATE, "%s produced a non-finite value at %zu", what, i);
+    return CTOX_OK;
+}
+
+}  // namespace
+
+// ======================================================================
+// lifecycle
+// ======================================================================
+extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **out) {
+    if (!out) return fail(CTOX_ERR_SHAPE, "null output handle");
+    *out = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count == 0)
+        return fail(CTOX_ERR_UNSUPPORTED_OPERATION,
+                    "backend hip cannot execute backend initialization: no HIP device (%s)",
+                    e == hipSuccess ? "0 devices" : hipGetErrorString(e));
+    if (device < 0 || device >= count)
+        return fail(CTOX_ERR_UNSUPPORTED_OPERATION, "HIP device %d out of range (%d devices)", device, count);
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, device));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(CTOX_ERR_UNSUPPORTED_OPERATION,
+                    "backend hip cannot execute backend initialization: device is %s, kernels are gfx950",
+                    prop.gcnArchName);
+    ctox_hip_backend *b = new ctox_hip_backend();
+    b->device = device;
+    std::snprintf(b->arch, sizeof b->arch, "%s", prop.gcnArchName);
+    hipError_t le = hipSetDevice(device);
+    if (le == hipSuccess) le = hipModuleLoadData(&b->module, ctox_hsaco_begin);
+    if (le == hipSuccess) le = hipStreamCreateWithFlags(&b->stream, hipStreamNonBlocking);
+    struct {
+        hipFunction_t *f;
+        const char *name;
+    } fns[] = {{&b->prep, "ctox_prep_activation_gfx950"}, {&b->q4_b4, "ctox_q4_matvec_b4_gfx950"},
+               {&b->q4_b8, "ctox_q4_matvec_b8_gfx950"},    {&b->q2_b4, "ctox_q2_matvec_b4_gfx950"},
+               {&b->q2_b8, "ctox_q2_matvec_b8_gfx950"},    {&b->rec_row, "ctox_recovered_row_gfx950"},
+               {&b->row_dot, "ctox_row_dot_gfx950"},       {&b->gdn_norms, "ctox_gdn_norms_gfx950"},
+               {&b->gdn_scan, "ctox_gdn_scan_gfx950"}};
+    for (auto &f : fns) {
+        if (le != hipSuccess) break;
+        le = hipModuleGetFunction(f.f, b->module, f.name);
+        if (le != hipSuccess) {
+            ctox_hip_backend_destroy(b);
+            return fail(CTOX_ERR_UNSUPPORTED_OPERATION, "kernel %s missing from code object: %s", f.name,
+                        hipGetErrorString(le));
+        }
+    }
+    if (le != hipSuccess) {
+        ctox_hip_backend_destroy(b);
+        return fail(CTOX_ERR_UNSUPPORTED_OPERATION, "HIP module setup failed: %s", hipGetErrorString(le));
+    }
+    *out = b;
+    return CTOX_OK;
+}
+
+extern "C" void ctox_hip_backend_destroy(ctox_hip_backend *b) {
+    if (!b) return;
+    (void)hipSetDevice(b->device);
+    (void)hipDeviceSynchronize();
+    DevBuf *bufs[] = {&b->xa[0], &b->xa[1], &b->xc[0], &b->xc[1], &b->partial, &b->counters, &b->norms};
+    for (DevBuf *d : bufs)
+        if (d->ptr) (void)hipFree(d->ptr);
+    if (b->stream) (void)hipStreamDestroy(b->stream);
+    if (b->module) (void)hipModuleUnload(b->module);
+    delete b;
+}
+
+extern "C" const char *ctox_hip_backend_kind(const ctox_hip_backend *) { return "hip"; }
+extern "C" const char *ctox_hip_backend_promotion_state(const ctox_hip_backend *) { return "experimental"; }
+extern "C" const char *ctox_hip_backend_profile(const ctox_hip_backend *) { return "gfx950-mfma-i8"; }
+extern "C" const char *ctox_hip_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" ctox_status ctox_hip_synchronize(ctox_hip_backend *b) {
+    if (!b) return fail(CTOX_ERR_INVALID_STATE, "null backend");
+    HIP_TRY(hipStreamSynchronize(b->stream));
+    return CTOX_OK;
+}
+
+// ======================================================================
+// resident matrices
+// ======================================================================
+namespace {
+ctox_status prepare_impl(ctox_hip_backend *b, const ctox_fused_matvec *op, ctox_hip_matrix **out) {
+    size_t blocks;
+    ctox_status st = validate_matvec(op, false, &blocks);
+    if (!st) st = check_matrix_scales(op, blocks);
+    if (st) return st;
+    HIP_TRY(hipSetDevice(b->device));
+    ctox_hip_matrix *m = new ctox_hip_matrix();
+    m->backend = b;
+    m->dtype = op->dtype;
+    m->rows = op->rows;
+    m->columns = op->columns;
+    if (op->dtype == CTOX_DTYPE_MIXED_Q2Q4B64) {
+        m->segments.assign(op->segments, op->segments + op->n_segments);
+    } else {
+        ctox_quant_segment s{0, 0, op->rows, op->dtype, 0, op->weights_len};
+        m->segments.push_back(s);
+    }
+    m->weights_len = op->weights_len;
+    st = upload(op->weights, op->weights_len, &m->d_weights);
+    if (!st && op->s_in.kind != CTOX_SCALE_NONE) {
+        const size_t bytes = op->s_in.len * (op->s_in.kind == CTOX_SCALE_F32 ? 4 : 2);
+        st = upload(op->s_in.data, bytes, &m->d_s_in);
+        m->s_in_kind = kernel_scale_kind(op->s_in.kind);
+        m->s_in_host.assign((const uint8_t *)op->s_in.data, (const uint8_t *)op->s_in.data + bytes);
+    }
+    if (!st && op->s_out.kind != CTOX_SCALE_NONE) {
+        st = upload(op->s_out.data, op->s_out.len * (op->s_out.kind == CTOX_SCALE_F32 ? 4 : 2), &m->d_s_out);
+        m->s_out_kind = kernel_scale_kind(op->s_out.kind);
+    }
+    if (!st && op->bias) st = upload(op->bias, op->rows * sizeof(float), (void **)&m->d_bias);
+    if (st) {
+        ctox_hip_matrix_destroy(m);
+        return st;
+    }
+    m->activation = (uint32_t)op->activation;
+    *out = m;
+    return CTOX_OK;
+}
+}  // namespace
+
+extern "C" ctox_status ctox_hip_matrix_prepare(ctox_hip_backend *b, const ctox_fused_matvec *op,
+                                               ctox_hip_matrix **out) {
+    if (!b || !op || !out) return fail(CTOX_ERR_SHAPE, "null argument");
+    *out = nullptr;
+    return prepare_impl(b, op, out);
+}
+
+extern "C" void ctox_hip_matrix_destroy(ctox_hip_matrix *m) {
+    if (!m) return;
+    (void)hipSetDevice(m->backend->device);
+    (void)hipDeviceSynchronize();
+    if (m->d_weights) (void)hipFree(m->d_weights);
+    if (m->d_s_in) (void)hipFree(m->d_s_in);
+    if (m->d_s_out) (void)hipFree(m->d_s_out);
+    if (m->d_bias) (void)hipFree(m->d_bias);
+    delete m;
+}
+
+extern "C" size_t ctox_hip_matrix_rows(const ctox_hip_matrix *m) { return m ? m->rows : 0; }
+extern "C" size_t ctox_hip_matrix_columns(const ctox_hip_matrix *m) { return m ? m->columns : 0; }
+extern "C" const void *ctox_hip_matrix_device_weights(const ctox_hip_matrix *m) {
+    return m ? m->d_weights : nullptr;
+}
+
+extern "C" ctox_status ctox_hip_matrix_dispatch(ctox_hip_backend *b, const ctox_hip_matrix *m,
+                                                const float *d_input, size_t batch, float *d_output,
+                                                void *stream) {
+    if (!b || !m || !d_input || !d_output) return fail(CTOX_ERR_SHAPE, "null argument");
+    if (batch == 0 || batch > CTOX_MAX_BATCH)
+        return fail(CTOX_ERR_SHAPE, "batch %zu outside 1..%d", batch, CTOX_MAX_BATCH);
+    bool prepped[2] = {false, false};
+    return dispatch_matrix(b, m, d_input, batch, d_output, pick_stream(b, stream), prepped, m->activation);
+}
+
+extern "C" ctox_status ctox_hip_matrix_dispatch_fanout(ctox_hip_backend *b,
+                                                       const ctox_hip_matrix *const *ms, size_t n,
+                                                       const float *d_input, size_t batch,
+                                                       float *const *d_outputs, void *stream) {
+    if (!b || !ms || !d_input || !d_outputs) return fail(CTOX_ERR_SHAPE, "null argument");
+    if (n == 0) return fail(CTOX_ERR_SHAPE, "fan-out requires at least one projection");
+    if (batch == 0 || batch > CTOX_MAX_BATCH)
+        return fail(CTOX_ERR_SHAPE, "batch %zu outside 1..%d", batch, CTOX_MAX_BATCH);
+    for (size_t i = 1; i < n; i++)
+        if (ms[i]->columns != ms[0]->columns || ms[i]->s_in_kind != ms[0]->s_in_kind ||
+            ms[i]->s_in_host != ms[0]->s_in_host)
+            return fail(CTOX_ERR_SHAPE, "fan-out projections must share columns and s_in");
+    bool prepped[2] = {false, false};
+    hipStream_t s = pick_stream(b, stream);
+    for (size_t i = 0; i < n; i++) {
+        ctox_status st = dispatch_matrix(b, ms[i], d_input, batch, d_outputs[i], s, prepped, ms[i]->activation);
+        if (st) return st;
+    }
+    return CTOX_OK;
+}
+
+extern "C" ctox_status ctox_hip_launch_fused_matvec(ctox_hip_backend *b, int32_t dtype,
+                                                    const void *d_weights, const float *d_input,
+                                                    const uint16_t *d_s_in, const uint16_t *d_s_out,
+                                                    const float *d_bias, float *d_output, uint32_t rows,
+                                                    uint32_t columns, uint32_t activation, uint32_t batch,
+                                                    void *stream) {
+    if (!b || !d_weights || !d_input || !d_output) return fail(CTOX_ERR_SHAPE, "null argument");
+    if (dtype != CTOX_DTYPE_Q2B64 && dtype != CTOX_DTYPE_Q4B64)
+        return fail(CTOX_ERR_UNSUPPORTED_DTYPE, "raw launch takes pure Q2_B64 or Q4_B64 weights");
+    if (rows == 0 || columns == 0 || columns % kBlockLen)
+        return fail(CTOX_ERR_SHAPE, "Q2/Q4 fused matvec dimensions must be non-zero and columns divisible by 64");
+    if (batch == 0 || batch > CTOX_MAX_BATCH)
+        return fail(CTOX_ERR_SHAPE, "batch %u outside 1..%d", batch, CTOX_MAX_BATCH);
+    if (activation > 1) return fail(CTOX_ERR_SHAPE, "activation %u is not identity (0) or SiLU (1)", activation);
+    hipStream_t s = pick_stream(b, stream);
+    const int layout = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
+    ctox_status st = run_prep(b, layout, d_input, columns, batch, d_s_in,
+                              d_s_in ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, s);
+    if (st) return st;
+    return run_matvec(b, dtype, d_weights, rows, columns, batch, d_s_out,
+                      d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, d_bias, d_output, rows, activation, s);
+}
+
+// ======================================================================
+// Backend trait on host buffers
+// ======================================================================
+extern "C" ctox_status ctox_hip_fused_matvec(ctox_hip_backend *b, const ctox_fused_matvec *op, float *output,
+                                             size_t output_len) {
+    if (!b || !op || !output) return fail(CTOX_ERR_SHAPE, "null argument");
+    size_t blocks;
+    ctox_status st = validate_matvec(op, true, &blocks);
+    if (st) return st;
+    if (output_len != op->rows) return fail(CTOX_ERR_SHAPE, "output holds %zu, expected %zu", output_len, op->rows);
+    ctox_hip_matrix *m = nullptr;
+    st = prepare_impl(b, op, &m);
+    if (st) return st;
+    float *d_in = nullptr, *d_out = nullptr;
+    hipError_t e = hipMalloc((void **)&d_in, op->columns * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&d_out, op->rows * sizeof(float));
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(d_in, op->input, op->columns * sizeof(float), hipMemcpyHostToDevice, b->stream);
+    if (e == hipSuccess) {
+        bool prepped[2] = {false, false};
+        st = dispatch_matrix(b, m, d_in, 1, d_out, b->stream, prepped, (uint32_t)op->activation);
+        if (!st) e = hipMemcpyAsync(output, d_out, op->rows * sizeof(float), hipMemcpyDeviceToHost, b->stream);
+        if (!st && e == hipSuccess) e = hipStreamSynchronize(b->stream);
+    }
+    if (d_in) (void)hipFree(d_in);
+    if (d_out) (void)hipFree(d_out);
+    ctox_hip_matrix_destroy(m);
+    if (e != hipSuccess) return fail(CTOX_ERR_INVALID_STATE, "HIP fused matvec failed: %s", hipGetErrorString(e));
+    if (st) return st;
+    return check_finite_host(output, op->rows, "fused matvec");
+}
+
+extern "C" ctox_status ctox_hip_fused_matvec_fanout(ctox_hip_backend *b, const ctox_fused_matvec *ops,
+                                                    size_t n, float *const *outputs) {
+    if (!b || !ops || !outputs) return fail(CTOX_ERR_SHAPE, "null argument");
+    if (n == 0) return fail(CTOX_ERR_SHAPE, "HIP fan-out requires at least one projection");
+    // Results equal independent calls by construction (the activation
+    // conversion is a pure function of input and s_in).
+    for (size_t i = 0; i < n; i++) {
+        ctox_status st = ctox_hip_fused_matvec(b, &ops[i], outputs[i], ops[i].rows);
+        if (st) return st;
+    }
+    return CTOX_OK;
+}
+
+extern "C" ctox_status ctox_hip_recovered_row(ctox_hip_backend *b, const ctox_recovered_row *op, float *output,
+                                              size_t output_len) {
+    if (!b || !op || !output) return fail(CTOX_ERR_SHAPE, "null argument");
+    // Q/src/backend/cpu.rs:312-337
+    if (op->columns == 0 || op->columns % kBlockLen)
+        return fail(CTOX_ERR_SHAPE, "recovered row columns must be non-zero and divisible by 64");
+    if (op->s_in.len != op->columns || !std::isfinite(op->s_out) || op->s_in.kind == CTOX_SCALE_NONE)
+        return fail(CTOX_ERR_SHAPE, "recovered row scale contract differs");
+    const size_t bb = block_bytes(op->dtype);
+    if (!bb) return fail(CTOX_ERR_UNSUPPORTED_DTYPE, "unsupported quantization dtype %d", op->dtype);
+    const size_t expected = op->columns / kBlockLen * bb;
+    if (op->weights_len != expected)
+        return fail(CTOX_ERR_SHAPE, "recovered row has %zu packed bytes, expected %zu", op->weights_len, expected);
+    if (output_len != op->columns) return fail(CTOX_ERR_SHAPE, "output holds %zu, expected %zu", output_len, op->columns);
+    if (!block_scales_finite(op->weights, 1, op->columns / kBlockLen, bb))
+        return fail(CTOX_ERR_INVALID_ARTIFACT, "recovered row block scale is non-finite");
+    size_t bad;
+    if (!scale_finite(op->s_in, &bad))
+        return fail(CTOX_ERR_INVALID_ARTIFACT, "recovery scale %zu is non-finite", bad);
+    HIP_TRY(hipSetDevice(b->device));
+    void *d_w = nullptr, *d_s = nullptr, *d_o = nullptr;
+    ctox_status st = upload(op->weights, op->weights_len, &d_w);
+    const size_t sbytes = op->s_in.len * (op->s_in.kind == CTOX_SCALE_F32 ? 4 : 2);
+    if (!st) st = upload(op->s_in.data, sbytes, &d_s);
+    if (!st && hipMalloc(&d_o, op->columns * sizeof(float)) != hipSuccess)
+        st = fail(CTOX_ERR_INVALID_STATE, "hipMalloc failed");
+    if (!st) {
+        RecoveredRowArgs a{};
+        a.weights = (const uint8_t *)d_w;
+        a.s_in = d_s;
+        a.output = (float *)d_o;
+        a.columns = (uint32_t)op->columns;
+        a.dtype = op->dtype == CTOX_DTYPE_Q4B64 ? 1u : 0u;
+        a.s_in_kind = kernel_scale_kind(op->s_in.kind);
+        a.s_out = op->s_out;
+        st = launch(b->rec_row, dim3((unsigned)((op->columns + 255) / 256)), dim3(256), b->stream, a,
+                    "ctox_recovered_row_gfx950");
+        if (!st && (hipMemcpyAsync(output, d_o, op->columns * sizeof(float), hipMemcpyDeviceToHost, b->stream) !=
+                        hipSuccess ||
+                    hipStreamSynchronize(b->stream) != hipSuccess))
+            st = fail(CTOX_ERR_INVALID_STATE, "recovered row readback failed");
+    }
+    if (d_w) (void)hipFree(d_w);
+    if (d_s) (void)hipFree(d_s);
+    if (d_o) (void)hipFree(d_o);
+    return st;
+}
+
+extern "C" ctox_status ctox_hip_recovered_row_matvec(ctox_hip_backend *b, const ctox_recovered_row_matvec *op,
+                                                     float *result) {
+    if (!b || !op || !result) return fail(CTOX_ERR_SHAPE, "null argument");
+    // Q/src/backend/cpu.rs:478-497
+    bool finite = op->len > 0 && op->len % kBlockLen == 0 && std::isfinite(op->s_out);
+    for (size_t i = 0; finite && i < op->len; i++) finite = std::isfinite(op->corrected_input[i]);
+    if (!finite) return fail(CTOX_ERR_SHAPE, "recovered row matvec input or output scale is invalid");
+    const size_t bb = block_bytes(op->dtype);
+    if (!bb) return fail(CTOX_ERR_UNSUPPORTED_DTYPE, "unsupported quantization dtype %d", op->dtype);
+    if (op->weights_len < op->len / kBlockLen * bb)
+        return fail(CTOX_ERR_SHAPE, "recovered row has %zu packed bytes, expected %zu", op->weights_len,
+                    op->len / kBlockLen * bb);
+    if (!block_scales_finite(op->weights, 1, op->len / kBlockLen, bb))
+        return fail(CTOX_ERR_INVALID_ARTIFACT, "%s block scale is non-finite",
+                    op->dtype == CTOX_DTYPE_Q2B64 ? "Q2" : "Q4");
+    HIP_TRY(hipSetDevice(b->device));
+    void *d_w = nullptr, *d_x = nullptr, *d_r = nullptr;
+    ctox_status st = upload(op->weights, op->len / kBlockLen * bb, &d_w);
+    if (!st) st = upload(op->corrected_input, op->len * sizeof(float), &d_x);
+    if (!st && hipMalloc(&d_r, sizeof(float)) != hipSuccess) st = fail(CTOX_ERR_INVALID_STATE, "hipMalloc failed");
+    if (!st) {
+        RowDotArgs a{};
+        a.weights = (const uint8_t *)d_w;
+        a.x = (const float *)d_x;
+        a.result = (float *)d_r;
+        a.len = (uint32_t)op->len;
+        a.dtype = op->dtype == CTOX_DTYPE_Q4B64 ? 1u : 0u;
+        a.s_out = op->s_out;
+        st = launch(b->row_dot, dim3(1), dim3(64), b->stream, a, "ctox_row_dot_gfx950");
+        if (!st && (hipMemcpyAsync(result, d_r, sizeof(float), hipMemcpyDeviceToHost, b->stream) != hipSuccess ||
+                    hipStreamSynchronize(b->stream) != hipSuccess))
+            st = fail(CTOX_ERR_INVALID_STATE, "row matvec readback failed");
+    }
+    if (d_w) (void)hipFree(d_w);
+    if (d_x) (void)hipFree(d_x);
+    if (d_r) (void)hipFree(d_r);
+    if (!st && !std::isfinite(*result)) return fail(CTOX_ERR_INVALID_STATE, "row matvec produced a non-finite value");
+    return st;
+}
+
+// ======================================================================
+// gated delta
+// ======================================================================
+namespace {
+ctox_status gdn_shape(size_t tokens, size_t heads, size_t kd, size_t vd) {
+    if (tokens == 0 || heads == 0 || kd == 0 || vd == 0)
+        return fail(CTOX_ERR_SHAPE, "delta shapes must be non-zero");
+    if (kd > 16 * 16)
+        return fail(CTOX_ERR_UNSUPPORTED_OPERATION,
+                    "backend hip cannot execute gated delta: key_dim %zu exceeds 256", kd);
+    if (tokens * heads > 0x7fffffffu) return fail(CTOX_ERR_SHAPE, "delta sequence too long");
+    return CTOX_OK;
+}
+
+ctox_status gdn_device(ctox_hip_backend *b, const float *q, const float *k, const float *v, const float *ld,
+                       const float *beta, float *state, size_t tokens, size_t heads, size_t kd, size_t vd,
+                       size_t chunk, float *out, hipStream_t s) {
+    ctox_status st = gdn_shape(tokens, heads, kd, vd);
+    if (st) return st;
+    (void)chunk;  // chunk selects the prefill algorithm; both paths compute the same recurrence
+    st = ensure(b, b->norms, tokens * heads * 2 * sizeof(float), false);
+    if (st) return st;
+    GdnArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.log_decay = ld;
+    a.beta = beta;
+    a.state = state;
+    a.out = out;
+    a.norms = (float *)b->norms.ptr;
+    a.tokens = (uint32_t)tokens;
+    a.heads = (uint32_t)heads;
+    a.key_dim = (uint32_t)kd;
+    a.value_dim = (uint32_t)vd;
+    a.chunk = (uint32_t)chunk;
+    st = launch(b->gdn_norms, dim3((unsigned)(tokens * heads)), dim3(64), s, a, "ctox_gdn_norms_gfx950");
+    if (st) return st;
+    const size_t slices = (vd + 15) / 16;
+    return launch(b->gdn_scan, dim3((unsigned)(heads * slices)), dim3(256), s, a, "ctox_gdn_scan_gfx950");
+}
+
+// Q/src/reference.rs:18-34
+ctox_status contract(const float *v, size_t rows, size_t cols, const char *what) {
+    for (size_t i = 0; i < rows * cols; i++)
+        if (!std::isfinite(v[i])) return fail(CTOX_ERR_INVALID_ARTIFACT, "%s input is non-finite", what);
+    return CTOX_OK;
+}
+
+ctox_status gdn_host(ctox_hip_backend *b, const float *q, const float *k, const float *v, const float *ld,
+                     const float *beta, float *state, size_t tokens, size_t heads, size_t kd, size_t vd,
+                     size_t chunk, float *out, bool sequence) {
+    if (!b || !q || !k || !v || !ld || !beta || !state || !out) return fail(CTOX_ERR_SHAPE, "null argument");
+    ctox_status st = gdn_shape(tokens, heads, kd, vd);
+    if (st) return st;
+    if ((st = contract(q, tokens, heads * kd, "delta query"))) return st;
+    if ((st = contract(k, tokens, heads * kd, "delta key"))) return st;
+    if ((st = contract(v, tokens, heads * vd, "delta value"))) return st;
+    if (sequence) {
+        if ((st = contract(ld, tokens, heads, "delta sequence decay"))) return st;
+        if ((st = contract(beta, tokens, heads, "delta sequence beta"))) return st;
+    }
+    for (size_t i = 0; i < heads * kd * vd; i++)
+        if (!std::isfinite(state[i])) return fail(CTOX_ERR_SHAPE, "delta state contract differs");
+    for (size_t i = 0; i < tokens * heads; i++)
+        if (!std::isfinite(ld[i]) || !std::isfinite(beta[i]))
+            return fail(CTOX_ERR_SHAPE, "delta state contract differs");
+    HIP_TRY(hipSetDevice(b->device));
+    const size_t nq = tokens * heads * kd, nv = tokens * heads * vd, ns = heads * kd * vd, ng = tokens * heads;
+    void *dq = nullptr, *dk = nullptr, *dv = nullptr, *dl = nullptr, *db = nullptr, *ds = nullptr, *dout = nullptr;
+    st = upload(q, nq * 4, &dq);
+    if (!st) st = upload(k, nq * 4, &dk);
+    if (!st) st = upload(v, nv * 4, &dv);
+    if (!st) st = upload(ld, ng * 4, &dl);
+    if (!st) st = upload(beta, ng * 4, &db);
+    if (!st) st = upload(state, ns * 4, &ds);
+    if (!st && hipMalloc(&dout, nv * 4) != hipSuccess) st = fail(CTOX_ERR_INVALID_STATE, "hipMalloc failed");
+    if (!st)
+        st = gdn_device(b, (float *)dq, (float *)dk, (float *)dv, (float *)dl, (float *)db, (float *)ds, tokens,
+                        heads, kd, vd, chunk, (float *)dout, b->stream);
+    if (!st && (hipMemcpyAsync(out, dout, nv * 4, hipMemcpyDeviceToHost, b->stream) != hipSuccess ||
+                hipMemcpyAsync(state, ds, ns * 4, hipMemcpyDeviceToHost, b->stream) != hipSuccess ||
+                hipStreamSynchronize(b->stream) != hipSuccess))
+        st = fail(CTOX_ERR_INVALID_STATE, "gated delta readback failed");
+    void *all[] = {dq, dk, dv, dl, db, ds, dout};
+    for (void *p : all)
+        if (p) (void)hipFree(p);
+    if (!st) st = check_finite_host(out, nv, "gated delta");
+    return st;
+}
+}  // namespace
+
+extern "C" ctox_status ctox_hip_gated_delta_step(ctox_hip_backend *b, const float *q, const float *k,
+                                                 const float *v, const float *log_decay, const float *beta,
+                                                 float *state, size_t heads, size_t key_dim, size_t value_dim,
+                                                 float *out) {
+    return gdn_host(b, q, k, v, log_decay, beta, state, 1, heads, key_dim, value_dim, 0, out, false);
+}
+
+extern "C" ctox_status ctox_hip_gated_delta_sequence(ctox_hip_backend *b, const float *q, const float *k,
+                                                     const float *v, const float *log_decay,
+                                                     const float *beta, float *state, size_t tokens,
+                                                     size_t heads, size_t key_dim, size_t value_dim,
+                                                     size_t chunk, float *out) {
+    return gdn_host(b, q, k, v, log_decay, beta, state, tokens, heads, key_dim, value_dim, chunk, out, true);
+}
+
+extern "C" ctox_status ctox_hip_gated_delta_step_device(ctox_hip_backend *b, const float *q, const float *k,
+                                                        const float *v, const float *log_decay,
+                                                        const float *beta, float *state, size_t heads,
+                                                        size_t key_dim, size_t value_dim, float *out,
+                                                        void *stream) {
+    if (!b || !q || !k || !v || !log_decay || !beta || !state || !out) return fail(CTOX_ERR_SHAPE, "null argument");
+    return gdn_device(b, q, k, v, log_decay, beta, state, 1, heads, key_dim, value_dim, 0, out,
+                      pick_stream(b, stream));
+}
+
+extern "C" ctox_status ctox_hip_gated_delta_sequence_device(ctox_hip_backend *b, const float *q, const float *k,
+                                                            const float *v, const float *log_decay,
+                                                            const float *beta, float *state, size_t tokens,
+                                                            size_t heads, size_t key_dim, size_t value_dim,
+                                                            size_t chunk, float *out, void *stream) {
+    if (!b || !q || !k || !v || !log_decay || !beta || !state || !out) return fail(CTOX_ERR_SHAPE, "null argument");
+    return gdn_device(b, q, k, v, log_decay, beta, state, tokens, heads, key_dim, value_dim, chunk, out,
+                      pick_stream(b, stream));
+}

@@ -1,0 +1,232 @@
+/*
+ * ctox_hip.h -- C ABI of the MI355X (gfx950) HIP backend for CTOX-LLM's
+ * Qwen3.8-27B decode hot path.
+ *
+ * This is the drop-in boundary. A host written against the crate's
+ * `Backend` trait (Q/src/backend/mod.rs:153-169; Q/ = models/qwen38_27b/ in
+ * the reference tree) binds these symbols over FFI exactly as the CUDA
+ * candidate runtime binds its kernels through the driver API
+ * (Q/src/backend/cuda_runtime.rs:195-294). All signatures use plain
+ * pointers and sizes; no PyTorch or HIP C++ types cross the boundary.
+ * Streams are passed as `void*` holding a `hipStream_t` (NULL = the
+ * backend's own stream).
+ *
+ * Threading: one backend handle owns one device context and is externally
+ * synchronized (the reference CUDA runtime is `Rc`, not `Send`:
+ * Q/src/backend/cuda_executor.rs:149-155). Calls on one handle must not
+ * overlap.
+ *
+ * Error contract: every entry point returns a ctox_status mapped 1:1 from
+ * EngineError (Q/src/error.rs:5-29). Nothing falls back to a CPU path
+ * (Q/src/backend/cpu.rs:400-410); non-finite outputs of the host-buffer
+ * entry points are reported as CTOX_ERR_INVALID_STATE
+ * (Q/src/backend/cuda_runtime.rs:10627-10632). The message of the last
+ * failure on the calling thread is returned by ctox_hip_last_error().
+ */
+#ifndef CTOX_HIP_H
+#define CTOX_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* EngineError variants, Q/src/error.rs:5-29. */
+typedef enum {
+    CTOX_OK = 0,
+    CTOX_ERR_IO = 1,
+    CTOX_ERR_JSON = 2,
+    CTOX_ERR_INVALID_ARTIFACT = 3,
+    CTOX_ERR_UNSUPPORTED_DTYPE = 4,
+    CTOX_ERR_UNSUPPORTED_OPERATION = 5,
+    CTOX_ERR_MEMORY_BUDGET = 6,
+    CTOX_ERR_SHAPE = 7,
+    CTOX_ERR_INVALID_STATE = 8,
+    CTOX_ERR_CANCELLED = 9
+} ctox_status;
+
+/* TensorDType, Q/src/format.rs:26-33. */
+typedef enum {
+    CTOX_DTYPE_Q2B64 = 0,
+    CTOX_DTYPE_Q4B64 = 1,
+    CTOX_DTYPE_MIXED_Q2Q4B64 = 2,
+    CTOX_DTYPE_F16 = 3,
+    CTOX_DTYPE_F32 = 4
+} ctox_dtype;
+
+/* Activation, Q/src/backend/mod.rs:54-67. */
+typedef enum { CTOX_ACT_IDENTITY = 0, CTOX_ACT_SILU = 1 } ctox_activation;
+
+/* Option<ScaleSlice>, Q/src/backend/mod.rs:74-112. */
+typedef enum { CTOX_SCALE_NONE = 0, CTOX_SCALE_F32 = 1, CTOX_SCALE_F16LE = 2 } ctox_scale_kind;
+
+typedef struct {
+    int32_t kind;      /* ctox_scale_kind */
+    const void *data;  /* float* (F32) or little-endian binary16 bytes (F16Le) */
+    size_t len;        /* number of values, not bytes */
+} ctox_scale_slice;
+
+/* QuantSegment, Q/src/format.rs:56-64. */
+typedef struct {
+    uint32_t group_index;
+    uint64_t row_start;
+    uint64_t row_end;
+    int32_t dtype;     /* CTOX_DTYPE_Q2B64 or CTOX_DTYPE_Q4B64 */
+    uint64_t offset;   /* relative to the tensor's packed payload */
+    uint64_t length;
+} ctox_quant_segment;
+
+/* FusedMatVec, Q/src/backend/mod.rs:115-128. Host pointers. */
+typedef struct {
+    int32_t dtype;
+    const uint8_t *weights;
+    size_t weights_len;
+    const ctox_quant_segment *segments;
+    size_t n_segments;
+    size_t rows;
+    size_t columns;
+    const float *input;
+    size_t input_len;
+    ctox_scale_slice s_in;
+    ctox_scale_slice s_out;
+    const float *bias;   /* NULL = None */
+    size_t bias_len;
+    int32_t activation;  /* ctox_activation */
+} ctox_fused_matvec;
+
+/* RecoveredRow, Q/src/backend/mod.rs:130-142. */
+typedef struct {
+    int32_t dtype;
+    const uint8_t *weights;
+    size_t weights_len;
+    size_t columns;
+    ctox_scale_slice s_in;
+    float s_out;
+} ctox_recovered_row;
+
+/* RecoveredRowMatVec, Q/src/backend/mod.rs:144-151. */
+typedef struct {
+    int32_t dtype;
+    const uint8_t *weights;
+    size_t weights_len;
+    const float *corrected_input;
+    size_t len;
+    float s_out;
+} ctox_recovered_row_matvec;
+
+typedef struct ctox_hip_backend ctox_hip_backend;
+typedef struct ctox_hip_matrix ctox_hip_matrix;
+
+/* ---- lifecycle (replaces CudaCandidateRuntime::new, cuda_runtime.rs:1297-1371) ---- */
+ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **out);
+void ctox_hip_backend_destroy(ctox_hip_backend *backend);
+/* Backend::kind / promotion_state / profile (Q/src/backend/mod.rs:153-157).
+ * kind returns "hip"; promotion state is "experimental"; profile names the
+ * device architecture (e.g. "gfx950-mfma"). Strings are static. */
+const char *ctox_hip_backend_kind(const ctox_hip_backend *backend);
+const char *ctox_hip_backend_promotion_state(const ctox_hip_backend *backend);
+const char *ctox_hip_backend_profile(const ctox_hip_backend *backend);
+/* Thread-local message of the last failing call ("" if none). */
+const char *ctox_hip_last_error(void);
+/* Blocks until all work the backend issued on its own stream is done. */
+ctox_status ctox_hip_synchronize(ctox_hip_backend *backend);
+
+/* ---- Backend trait, host buffers (Q/src/backend/mod.rs:158-168) ---- */
+/* Backend::fused_matvec; `output` holds op->rows floats. */
+ctox_status ctox_hip_fused_matvec(ctox_hip_backend *backend, const ctox_fused_matvec *op,
+                                  float *output, size_t output_len);
+/* Backend::fused_matvec_fanout; outputs[i] holds ops[i].rows floats. Results
+ * equal independent fused_matvec calls (Q/src/backend/cpu.rs:444-472). */
+ctox_status ctox_hip_fused_matvec_fanout(ctox_hip_backend *backend, const ctox_fused_matvec *ops,
+                                         size_t n_ops, float *const *outputs);
+/* Backend::recovered_row (Q/src/backend/cpu.rs:312-370); output holds columns floats. */
+ctox_status ctox_hip_recovered_row(ctox_hip_backend *backend, const ctox_recovered_row *op,
+                                   float *output, size_t output_len);
+/* Backend::recovered_row_matvec (Q/src/backend/cpu.rs:478-497). */
+ctox_status ctox_hip_recovered_row_matvec(ctox_hip_backend *backend,
+                                          const ctox_recovered_row_matvec *op, float *result);
+
+/* ---- resident matrices: prepare once, dispatch many times ----
+ * Replaces CudaCandidateRuntime::prepare_* / dispatch_prepared_*
+ * (Q/src/backend/cuda_runtime.rs:8341-8386, 10560-10637). The descriptor's
+ * weights, segments, s_in, s_out and bias are validated exactly as the CPU
+ * dispatcher does (Q/src/backend/cpu.rs:41-173) and uploaded to HBM in the
+ * crate's packed CTOXQ layout, unchanged. op->input is ignored. */
+ctox_status ctox_hip_matrix_prepare(ctox_hip_backend *backend, const ctox_fused_matvec *op,
+                                    ctox_hip_matrix **out);
+void ctox_hip_matrix_destroy(ctox_hip_matrix *matrix);
+size_t ctox_hip_matrix_rows(const ctox_hip_matrix *matrix);
+size_t ctox_hip_matrix_columns(const ctox_hip_matrix *matrix);
+/* Device pointer to the resident packed weights (for benchmarks/tests). */
+const void *ctox_hip_matrix_device_weights(const ctox_hip_matrix *matrix);
+
+/* Batched fused matvec on device buffers: Y[m, r] = act((sum_k W[r,k] *
+ * X[m,k] * s_in[k] + bias[r]) * s_out[r]) for m < batch. batch = 1 is the
+ * decode matvec; 2 <= batch <= 8 is the MTP speculative-verify pass, equal to
+ * `batch` independent fused_matvec calls (the crate verifies drafts with
+ * sequential target steps, Q/src/decoder.rs:1344-1375; the CUDA five-row
+ * verify is Q/src/backend/cuda_graph.rs:4565-4787). d_input is [batch,
+ * columns] f32, d_output is [batch, rows] f32, both device memory. */
+ctox_status ctox_hip_matrix_dispatch(ctox_hip_backend *backend, const ctox_hip_matrix *matrix,
+                                     const float *d_input, size_t batch, float *d_output,
+                                     void *stream);
+
+/* Fan-out on device buffers: the activation is converted once and feeds
+ * every matrix (Q/src/backend/cpu.rs:444-472, Q/src/fanout.rs:284-323). All
+ * matrices must share `columns` and s_in. d_outputs[i] is [batch, rows_i]. */
+ctox_status ctox_hip_matrix_dispatch_fanout(ctox_hip_backend *backend,
+                                            const ctox_hip_matrix *const *matrices, size_t n,
+                                            const float *d_input, size_t batch,
+                                            float *const *d_outputs, void *stream);
+
+/* ---- raw launch on device pointers ----
+ * Same nine parameters, in the same order and meaning, as the SM86 fused
+ * matvec parameter buffer (Q/src/backend/cuda.rs:73-122): weights (packed
+ * pure Q2_B64 or Q4_B64 rows), input, s_in (fp16, NULL = 1.0), s_out (fp16,
+ * NULL = 1.0), bias (NULL = 0), output, rows, columns, activation. Adds
+ * `batch` (1..8 input rows, as the batched MMQ launch) and the stream. The
+ * backend supplies the activation staging buffers. */
+ctox_status ctox_hip_launch_fused_matvec(ctox_hip_backend *backend, int32_t dtype,
+                                         const void *d_weights, const float *d_input,
+                                         const uint16_t *d_s_in, const uint16_t *d_s_out,
+                                         const float *d_bias, float *d_output, uint32_t rows,
+                                         uint32_t columns, uint32_t activation, uint32_t batch,
+                                         void *stream);
+
+/* ---- gated delta (GatedDeltaNet) recurrence, fp32 state ----
+ * Layouts follow Q/src/reference.rs:230-415: q, k [tokens][heads][key_dim]
+ * (after Q/K head repetition), v [tokens][heads][value_dim], log_decay and
+ * beta [tokens][heads], state [heads][key_dim][value_dim] row-major, updated
+ * in place; out [tokens][heads][value_dim]. */
+/* recurrent_gated_delta_step, Q/src/reference.rs:230-297 (host buffers). */
+ctox_status ctox_hip_gated_delta_step(ctox_hip_backend *backend, const float *q, const float *k,
+                                      const float *v, const float *log_decay, const float *beta,
+                                      float *state, size_t heads, size_t key_dim,
+                                      size_t value_dim, float *out);
+/* recurrent_gated_delta_sequence, Q/src/reference.rs:377-415 (host buffers).
+ * `chunk` = 0 selects the token-serial scan; chunk > 0 selects the chunked
+ * prefill with that chunk length (64 for the benchmark). */
+ctox_status ctox_hip_gated_delta_sequence(ctox_hip_backend *backend, const float *q,
+                                          const float *k, const float *v, const float *log_decay,
+                                          const float *beta, float *state, size_t tokens,
+                                          size_t heads, size_t key_dim, size_t value_dim,
+                                          size_t chunk, float *out);
+/* Device-buffer forms of the two entry points above (same layouts). */
+ctox_status ctox_hip_gated_delta_step_device(ctox_hip_backend *backend, const float *d_q,
+                                             const float *d_k, const float *d_v,
+                                             const float *d_log_decay, const float *d_beta,
+                                             float *d_state, size_t heads, size_t key_dim,
+                                             size_t value_dim, float *d_out, void *stream);
+ctox_status ctox_hip_gated_delta_sequence_device(ctox_hip_backend *backend, const float *d_q,
+                                                 const float *d_k, const float *d_v,
+                                                 const float *d_log_decay, const float *d_beta,
+                                                 float *d_state, size_t tokens, size_t heads,
+                                                 size_t key_dim, size_t value_dim, size_t chunk,
+                                                 float *d_out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CTOX_HIP_H */

@@ -1,0 +1,118 @@
+"""GPU parity of the fp32 gated-delta recurrence against the C oracle
+(Q/src/reference.rs:230-415).
+
+Tolerances: outputs elementwise within
+1e-3 * (|ref| + rms(ref)); state within 1e-4 * (|ref| + rms(ref)). The
+crate's golden vectors (2e-6) are checked at their own tolerance.
+"""
+import json
+import math
+import os
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "crate_goldens.json")))
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def close(got, ref, rtol, what):
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    rms = math.sqrt(float(np.mean(ref ** 2)))
+    d = np.abs(got - ref)
+    assert np.all(d <= rtol * (np.abs(ref) + rms)), f"{what}: max {d.max()} rms {rms}"
+
+
+def gdn_inputs(tokens, heads, key_heads, dk, dv, seed):
+    """q, k L2-normalised N(0,1) over key_heads, repeated to heads; v N(0,1);
+    decay gate exp(-softplus(N)) (log_decay = -softplus(N)); beta = sigmoid(N)."""
+    rng = np.random.default_rng(seed)
+    rep = heads // key_heads
+    qk = rng.standard_normal((2, tokens, key_heads, dk)).astype(np.float32)
+    qk /= np.linalg.norm(qk, axis=-1, keepdims=True)
+    q = np.repeat(qk[0], rep, axis=1).reshape(tokens, -1)
+    k = np.repeat(qk[1], rep, axis=1).reshape(tokens, -1)
+    v = rng.standard_normal((tokens, heads * dv)).astype(np.float32)
+    n = rng.standard_normal((tokens, heads)).astype(np.float32)
+    log_decay = (-np.logaddexp(0.0, n)).astype(np.float32)
+    beta = (1.0 / (1.0 + np.exp(-rng.standard_normal((tokens, heads))))).astype(np.float32)
+    return q, k, v, log_decay, beta
+
+
+def test_golden_step_and_sequence(hip):
+    say("case gdn goldens")
+    g = GOLD["delta_step"]
+    st = np.array(g["state"], np.float32)
+    out = hip.gated_delta_step(g["q"], g["k"], g["v"], g["log_decay"], g["beta"], st, g["heads"], g["key_dim"],
+                               g["value_dim"])
+    assert np.max(np.abs(out - g["out"])) <= g["tol"] and np.max(np.abs(st - g["state_out"])) <= g["tol"]
+    g = GOLD["delta_sequence"]
+    st = np.array(g["state"], np.float32)
+    out = hip.gated_delta_sequence(g["q"], g["k"], g["v"], g["log_decay"], g["beta"], st, g["tokens"], g["heads"],
+                                   g["key_dim"], g["value_dim"])
+    assert np.max(np.abs(out - g["out"])) <= g["tol"] and np.max(np.abs(st - g["state_out"])) <= g["tol"]
+
+
+@pytest.mark.parametrize("heads,key_heads", [(32, 16), (48, 16)])
+def test_decode_step_vs_oracle(hip, orc, heads, key_heads):
+    say(f"case gdn decode heads={heads}")
+    dk = dv = 128
+    q, k, v, ld, be = gdn_inputs(17, heads, key_heads, dk, dv, heads)
+    st_ref = np.zeros(heads * dk * dv, np.float32)
+    # warm the state with 16 tokens (oracle), then one decode step on both
+    orc.gated_delta_sequence(q[:16], k[:16], v[:16], ld[:16], be[:16], st_ref, 16, heads, dk, dv)
+    st_gpu = st_ref.copy()
+    ref = orc.gated_delta_step(q[16], k[16], v[16], ld[16], be[16], st_ref, heads, dk, dv)
+    got = hip.gated_delta_step(q[16], k[16], v[16], ld[16], be[16], st_gpu, heads, dk, dv)
+    close(got, ref, 1e-3, "output")
+    close(st_gpu, st_ref, 1e-4, "state")
+
+
+@pytest.mark.parametrize("chunk", [0, 64])
+def test_sequence_vs_oracle(hip, orc, chunk):
+    say(f"case gdn sequence chunk={chunk}")
+    heads, dk, dv, T = 32, 128, 128, 512
+    q, k, v, ld, be = gdn_inputs(T, heads, 16, dk, dv, 5)
+    st_ref = (np.random.default_rng(6).standard_normal(heads * dk * dv) * 0.1).astype(np.float32)
+    st_gpu = st_ref.copy()
+    ref = orc.gated_delta_sequence(q, k, v, ld, be, st_ref, T, heads, dk, dv)
+    got = hip.gated_delta_sequence(q, k, v, ld, be, st_gpu, T, heads, dk, dv, chunk)
+    close(got, ref, 1e-3, "output")
+    close(st_gpu, st_ref, 1e-4, "state")
+
+
+@pytest.mark.parametrize("dims", [(3, 5, 7), (2, 64, 96), (4, 256, 128), (1, 1, 1)])
+def test_ragged_dims(hip, orc, dims):
+    heads, dk, dv = dims
+    say(f"case gdn ragged {dims}")
+    rng = np.random.default_rng(sum(dims))
+    T = 9
+    q = rng.standard_normal((T, heads * dk)).astype(np.float32)
+    k = rng.standard_normal((T, heads * dk)).astype(np.float32)
+    v = rng.standard_normal((T, heads * dv)).astype(np.float32)
+    ld = -rng.uniform(0.01, 1.0, (T, heads)).astype(np.float32)
+    be = rng.uniform(0.0, 1.0, (T, heads)).astype(np.float32)
+    st_ref = rng.standard_normal(heads * dk * dv).astype(np.float32)
+    st_gpu = st_ref.copy()
+    ref = orc.gated_delta_sequence(q, k, v, ld, be, st_ref, T, heads, dk, dv)
+    got = hip.gated_delta_sequence(q, k, v, ld, be, st_gpu, T, heads, dk, dv, 0)
+    close(got, ref, 1e-3, "output")
+    close(st_gpu, st_ref, 1e-4, "state")
+
+
+def test_errors(hip):
+    import ctox_hip
+    st = np.zeros(2 * 3 * 2, np.float32)
+    with pytest.raises(ctox_hip.InvalidArtifact):
+        hip.gated_delta_step([np.nan] * 6, [1.0] * 6, [1.0] * 4, [0.0, 0.0], [0.5, 0.5], st, 2, 3, 2)
+    st[0] = np.inf
+    with pytest.raises(ctox_hip.ShapeError):
+        hip.gated_delta_step([1.0] * 6, [1.0] * 6, [1.0] * 4, [0.0, 0.0], [0.5, 0.5], st, 2, 3, 2)
+    with pytest.raises(ctox_hip.UnsupportedOperation):
+        hip.gated_delta_step([1.0] * 300, [1.0] * 300, [1.0], [0.0], [0.5], np.zeros(300, np.float32), 1, 300, 1)

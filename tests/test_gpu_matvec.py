@@ -1,0 +1,295 @@
+"""GPU parity of the fused Q2/Q4 matvec and its small-M verify variant
+against the C oracle (scalar verifier of Q/src/backend/cpu.rs:558-575).
+
+Tolerance (stated per the BASELINE north star): elementwise
+|gpu - oracle| <= 1e-3 * (|oracle| + rms(oracle)). The int8-MFMA kernel is
+exact in its integer part, so the observed error is ~1e-6 relative; the
+tests also assert a normwise bound of 2e-5 to catch regressions early.
+Unpacking and indexing are bit-exact by construction and are additionally
+checked by the recovered-row kernels, which must match the oracle exactly.
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+
+import ctox_hip
+import ctox_hip.synth as synth
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 1e-3
+NORMWISE = 2e-5
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def check(got, ref, what=""):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert got.shape == ref.shape
+    rms = math.sqrt(float(np.mean(ref ** 2))) if ref.size else 0.0
+    d = np.abs(got - ref)
+    assert np.all(d <= RTOL * (np.abs(ref) + rms) + 1e-30), f"{what}: max elementwise {d.max()} (rms {rms})"
+    norm = d.max() / max(np.abs(ref).max(), 1e-30)
+    assert norm <= NORMWISE, f"{what}: normwise {norm}"
+    return norm
+
+
+def make_case(dtype, rows, cols, seed, s_kind="f16", bias=True, act=ctox_hip.Activation.Identity, batch=1,
+              xkind="normal"):
+    w = synth.random_matrix(dtype, rows, cols, seed)
+    x = synth.activation(xkind, cols, seed + 1, batch)
+    rng = np.random.default_rng(seed + 2)
+    s_in = rng.uniform(0.75, 1.25, cols).astype(np.float32)
+    s_out = rng.uniform(0.75, 1.25, rows).astype(np.float32)
+    b = (rng.standard_normal(rows) * 0.05).astype(np.float32) if bias else None
+    if s_kind == "f16":
+        si = ctox_hip.ScaleSlice.F16Le(s_in.astype(np.float16).view(np.uint8))
+        so = ctox_hip.ScaleSlice.F16Le(s_out.astype(np.float16).view(np.uint8))
+        osi, oso = ("f16le", s_in.astype(np.float16).view(np.uint8)), ("f16le", s_out.astype(np.float16).view(np.uint8))
+    elif s_kind == "f32":
+        si, so = ctox_hip.ScaleSlice.F32(s_in), ctox_hip.ScaleSlice.F32(s_out)
+        osi, oso = ("f32", s_in), ("f32", s_out)
+    else:
+        si = so = osi = oso = None
+    op = ctox_hip.FusedMatVec(ctox_hip.TensorDType(dtype), w, rows, cols, x[0], s_in=si, s_out=so, bias=b,
+                              activation=act)
+    return op, (w, x, osi, oso, b)
+
+
+def oracle_rows(orc, dtype, rows, cols, parts, act, segments=()):
+    w, x, osi, oso, b = parts
+    return np.stack([orc.fused_matvec(dtype, w, rows, cols, x[m], osi, oso, b, int(act), segments)
+                     for m in range(x.shape[0])])
+
+
+SMALL = [(1, 64), (3, 64), (7, 192), (65, 128), (64, 1024), (100, 1088), (257, 2112), (130, 5120)]
+
+
+@pytest.mark.parametrize("dtype", [0, 1])
+@pytest.mark.parametrize("rows,cols", SMALL)
+def test_matvec_host_api_small_shapes(hip, orc, dtype, rows, cols):
+    say(f"case matvec dtype={dtype} rows={rows} cols={cols}")
+    for i, (sk, bias, act) in enumerate([("f16", True, ctox_hip.Activation.Silu), ("f32", False, ctox_hip.Activation.Identity),
+                                         ("none", True, ctox_hip.Activation.Identity)]):
+        op, parts = make_case(dtype, rows, cols, 100 + rows + i, sk, bias, act)
+        got = hip.fused_matvec(op)
+        ref = oracle_rows(orc, dtype, rows, cols, parts, act)[0]
+        check(got, ref, f"dtype={dtype} {rows}x{cols} {sk}")
+
+
+def test_crate_fixture_cases(hip, orc):
+    # Q/src/backend/cpu.rs:774-832 fixtures (sin weights, cos input, f32 scales, bias, SiLU)
+    from test_oracle_matvec import encode_fixture
+    for dtype, rows, cols, act in [(0, 7, 192, 1), (1, 7, 192, 1), (0, 3, 64, 0), (1, 3, 64, 0)]:
+        say(f"case crate fixture dtype={dtype} rows={rows} cols={cols}")
+        w = encode_fixture(orc, dtype, rows, cols)
+        x = np.array([math.cos(i * 0.03125) for i in range(cols)], np.float32)
+        s_in = np.array([0.75 + 0.005 * (i % 7) for i in range(cols)], np.float32)
+        s_out = np.array([1.25 - 0.05 * (r % 5) for r in range(rows)], np.float32)
+        bias = np.array([math.sin(r * 1.7) * 0.1 for r in range(rows)], np.float32)
+        ref = orc.fused_matvec(dtype, w, rows, cols, x, ("f32", s_in), ("f32", s_out), bias, act)
+        got = hip.fused_matvec(ctox_hip.FusedMatVec(ctox_hip.TensorDType(dtype), np.frombuffer(w, np.uint8), rows,
+                                                    cols, x, s_in=ctox_hip.ScaleSlice.F32(s_in),
+                                                    s_out=ctox_hip.ScaleSlice.F32(s_out), bias=bias,
+                                                    activation=ctox_hip.Activation(act)))
+        assert np.all(np.abs(got - ref) <= 2e-4)  # the crate's SIMD tolerance, Q/src/backend/cpu.rs:745
+        check(got, ref, "crate fixture")
+
+
+def test_loader_closed_form_on_gpu(hip, orc):
+    # Q/src/loader.rs:460-543: a Q2 block of 0.5, s_in 1, s_out 1.5 -> 48.0; embedding row -> 0.75
+    blk = np.frombuffer(orc.q2_quantize(np.full(64, 0.5, np.float32)), np.uint8)
+    s_in = ctox_hip.ScaleSlice.F16Le(np.ones(64, np.float16).view(np.uint8))
+    s_out = ctox_hip.ScaleSlice.F16Le(np.array([1.5], np.float16).view(np.uint8))
+    y = hip.fused_matvec(ctox_hip.FusedMatVec(ctox_hip.TensorDType.Q2B64, blk, 1, 64, np.ones(64, np.float32),
+                                              s_in=s_in, s_out=s_out))
+    assert abs(y[0] - 48.0) < 1e-6
+    row = hip.recovered_row(ctox_hip.RecoveredRow(ctox_hip.TensorDType.Q2B64, blk, 64, s_in, 1.5))
+    assert np.all(np.abs(row - 0.75) < 1e-6)
+
+
+def _torch():
+    import torch
+    assert torch.cuda.is_available()
+    return torch
+
+
+def resident_run(hip, op, xs):
+    """Prepare the matrix in HBM and dispatch a [batch, cols] activation."""
+    torch = _torch()
+    m = hip.prepare(op)
+    dx = torch.from_numpy(np.ascontiguousarray(xs)).cuda()
+    dy = torch.empty((xs.shape[0], op.rows), dtype=torch.float32, device="cuda")
+    m.dispatch(dx.data_ptr(), xs.shape[0], dy.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    out = dy.cpu().numpy()
+    m.close()
+    return out
+
+
+@pytest.mark.parametrize("cfg", ["config1_q4_up_17408x5120", "config2_q2_down_5120x17408"])
+def test_baseline_full_shapes(hip, orc, cfg):
+    dtype, rows, cols, xkind = (1, 17408, 5120, "normal") if cfg.startswith("config1") else (0, 5120, 17408, "swiglu")
+    for sk in ("none", "f16"):
+        say(f"case {cfg} scales={sk}")
+        op, parts = make_case(dtype, rows, cols, 7, sk, bias=False, xkind=xkind)
+        got = resident_run(hip, op, parts[1])
+        ref = oracle_rows(orc, dtype, rows, cols, parts, ctox_hip.Activation.Identity)
+        n = check(got, ref, cfg)
+        say(f"  normwise rel err {n:.3e}")
+
+
+# One decoder layer (Q/src/tensor_contract.rs:70-240): q_proj 12288 (crate) / 6144 (BASELINE),
+# k/v 1024, o 5120x6144, gate/up 17408x5120, down 5120x17408.
+LAYER = [("q_proj_crate", 1, 12288, 5120), ("q_proj_baseline", 1, 6144, 5120), ("k_proj", 1, 1024, 5120),
+         ("v_proj", 1, 1024, 5120), ("o_proj", 1, 5120, 6144), ("gate_proj", 1, 17408, 5120),
+         ("up_proj", 1, 17408, 5120), ("down_proj_q2", 0, 5120, 17408)]
+
+
+@pytest.mark.parametrize("batch", [2, 4, 8])
+def test_verify_small_m_layer_projections(hip, orc, batch):
+    for name, dtype, rows, cols in LAYER:
+        say(f"case verify batch={batch} {name} {rows}x{cols}")
+        op, parts = make_case(dtype, rows, cols, 31 + rows, "f16", bias=False, batch=batch)
+        got = resident_run(hip, op, parts[1])
+        ref = oracle_rows(orc, dtype, rows, cols, parts, ctox_hip.Activation.Identity)
+        check(got, ref, f"{name} batch={batch}")
+
+
+@pytest.mark.parametrize("batch", [1, 2, 3, 4, 5, 6, 7, 8])
+def test_batched_ragged(hip, orc, batch):
+    for dtype, rows, cols in [(0, 77, 192), (1, 77, 192), (1, 130, 2112)]:
+        say(f"case ragged batch={batch} dtype={dtype} {rows}x{cols}")
+        op, parts = make_case(dtype, rows, cols, 5 + batch, "f32", bias=True, act=ctox_hip.Activation.Silu,
+                              batch=batch)
+        got = resident_run(hip, op, parts[1])
+        ref = oracle_rows(orc, dtype, rows, cols, parts, ctox_hip.Activation.Silu)
+        check(got, ref, f"ragged batch={batch}")
+
+
+def test_mixed_segments_match_pure(hip, orc):
+    say("case mixed segments")
+    cols = 1088
+    q2 = synth.random_matrix(0, 70, cols, 1)
+    q4 = synth.random_matrix(1, 90, cols, 2)
+    x = synth.activation("normal", cols, 3)[0]
+    segs = [ctox_hip.QuantSegment(0, 0, 70, ctox_hip.TensorDType.Q2B64, 0, q2.size),
+            ctox_hip.QuantSegment(1, 70, 160, ctox_hip.TensorDType.Q4B64, q2.size, q4.size)]
+    mixed = hip.fused_matvec(ctox_hip.FusedMatVec(ctox_hip.TensorDType.MixedQ2Q4B64, np.concatenate([q2, q4]), 160,
+                                                  cols, x, segments=segs))
+    a = hip.fused_matvec(ctox_hip.FusedMatVec(ctox_hip.TensorDType.Q2B64, q2, 70, cols, x))
+    b = hip.fused_matvec(ctox_hip.FusedMatVec(ctox_hip.TensorDType.Q4B64, q4, 90, cols, x))
+    assert np.array_equal(mixed[:70], a) and np.array_equal(mixed[70:], b)
+    ref = orc.fused_matvec(2, np.concatenate([q2, q4]).tobytes(), 160, cols, x,
+                           segments=[(0, 0, 70, 0, 0, q2.size), (1, 70, 160, 1, q2.size, q4.size)])
+    check(mixed, ref, "mixed")
+
+
+def test_fanout_and_determinism(hip):
+    say("case fanout/determinism")
+    cols = 5120
+    x = synth.activation("normal", cols, 4)[0]
+    s_in = ctox_hip.ScaleSlice.F16Le(np.full(cols, 1.125, np.float16).view(np.uint8))
+    ops = [ctox_hip.FusedMatVec(ctox_hip.TensorDType(d), synth.random_matrix(d, r, cols, 10 + r), r, cols, x,
+                                s_in=s_in) for d, r in [(0, 200), (1, 300)]]
+    outs = hip.fused_matvec_fanout(ops)
+    for o, op in zip(outs, ops):
+        assert np.array_equal(o, hip.fused_matvec(op))
+        assert np.array_equal(hip.fused_matvec(op), hip.fused_matvec(op))
+    with pytest.raises(ctox_hip.ShapeError):
+        hip.fused_matvec_fanout([])
+
+
+def test_device_fanout_equals_independent(hip):
+    torch = _torch()
+    say("case device fanout")
+    cols = 5120
+    x = synth.activation("normal", cols, 8, 3)
+    s_in = ctox_hip.ScaleSlice.F16Le(np.linspace(0.8, 1.2, cols).astype(np.float16).view(np.uint8))
+    mats = [hip.prepare(ctox_hip.FusedMatVec(ctox_hip.TensorDType(d), synth.random_matrix(d, r, cols, r), r, cols,
+                                             s_in=s_in)) for d, r in [(1, 1024), (0, 640), (1, 48)]]
+    dx = torch.from_numpy(x).cuda()
+    outs = [torch.empty((3, m.rows), device="cuda") for m in mats]
+    hip.dispatch_fanout(mats, dx.data_ptr(), 3, [o.data_ptr() for o in outs], torch.cuda.current_stream().cuda_stream)
+    for m, o in zip(mats, outs):
+        single = torch.empty_like(o)
+        m.dispatch(dx.data_ptr(), 3, single.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert torch.equal(o, single)
+
+
+def test_raw_launch_matches_resident_dispatch(hip):
+    torch = _torch()
+    say("case raw launch")
+    rows, cols = 1000, 5120
+    w = synth.random_matrix(1, rows, cols, 77)
+    x = synth.activation("normal", cols, 78, 2)
+    s_in = np.linspace(0.9, 1.1, cols).astype(np.float16)
+    s_out = np.linspace(1.1, 0.9, rows).astype(np.float16)
+    bias = np.linspace(-0.1, 0.1, rows).astype(np.float32)
+    op = ctox_hip.FusedMatVec(ctox_hip.TensorDType.Q4B64, w, rows, cols, s_in=ctox_hip.ScaleSlice.F16Le(s_in.view(np.uint8)),
+                              s_out=ctox_hip.ScaleSlice.F16Le(s_out.view(np.uint8)), bias=bias,
+                              activation=ctox_hip.Activation.Silu)
+    want = resident_run(hip, op, x)
+    dw = torch.from_numpy(w).cuda()
+    dx = torch.from_numpy(x).cuda()
+    dsi = torch.from_numpy(s_in.view(np.int16)).cuda()
+    dso = torch.from_numpy(s_out.view(np.int16)).cuda()
+    db = torch.from_numpy(bias).cuda()
+    dy = torch.empty((2, rows), device="cuda")
+    hip.launch_fused_matvec(ctox_hip.TensorDType.Q4B64, dw.data_ptr(), dx.data_ptr(), dsi.data_ptr(), dso.data_ptr(),
+                            db.data_ptr(), dy.data_ptr(), rows, cols, ctox_hip.Activation.Silu, 2,
+                            torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert np.array_equal(dy.cpu().numpy(), want)
+
+
+def test_error_contract(hip):
+    say("case errors")
+    w = synth.random_matrix(1, 4, 128, 1)
+    x = np.ones(128, np.float32)
+    T = ctox_hip.TensorDType
+    with pytest.raises(ctox_hip.ShapeError):
+        hip.fused_matvec(ctox_hip.FusedMatVec(T.Q4B64, w[:-1], 4, 128, x))
+    with pytest.raises(ctox_hip.ShapeError):
+        hip.fused_matvec(ctox_hip.FusedMatVec(T.Q4B64, w, 4, 100, np.ones(100, np.float32)))
+    with pytest.raises(ctox_hip.UnsupportedDType):
+        hip.fused_matvec(ctox_hip.FusedMatVec(T.F16, w, 4, 128, x))
+    with pytest.raises(ctox_hip.InvalidArtifact):
+        hip.fused_matvec(ctox_hip.FusedMatVec(T.MixedQ2Q4B64, w, 4, 128, x))
+    with pytest.raises(ctox_hip.InvalidArtifact):
+        hip.fused_matvec(ctox_hip.FusedMatVec(T.MixedQ2Q4B64, w, 4, 128, x,
+                                              segments=[ctox_hip.QuantSegment(0, 1, 4, T.Q4B64, 0, w.size)]))
+    bad = w.copy()
+    bad[0], bad[1] = 0x00, 0x7C
+    with pytest.raises(ctox_hip.InvalidArtifact):
+        hip.fused_matvec(ctox_hip.FusedMatVec(T.Q4B64, bad, 4, 128, x))
+    nan_x = x.copy()
+    nan_x[5] = np.nan
+    with pytest.raises(ctox_hip.InvalidState):
+        hip.fused_matvec(ctox_hip.FusedMatVec(T.Q4B64, w, 4, 128, nan_x))
+    with pytest.raises(ctox_hip.ShapeError):
+        m = hip.prepare(ctox_hip.FusedMatVec(T.Q4B64, w, 4, 128))
+        m.dispatch(1, 9, 1)
+
+
+@pytest.mark.parametrize("dtype", [0, 1])
+def test_recovered_row_bit_exact(hip, orc, dtype):
+    say(f"case recovered row dtype={dtype}")
+    cols = 5120
+    w = synth.random_matrix(dtype, 1, cols, 3 + dtype)
+    s_in_f16 = np.random.default_rng(0).uniform(0.5, 1.5, cols).astype(np.float16)
+    got = hip.recovered_row(ctox_hip.RecoveredRow(ctox_hip.TensorDType(dtype), w, cols,
+                                                  ctox_hip.ScaleSlice.F16Le(s_in_f16.view(np.uint8)), 1.25))
+    ref = orc.recovered_row(dtype, w.tobytes(), cols, ("f16le", s_in_f16.view(np.uint8)), 1.25)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    x = synth.activation("normal", cols, 9)[0]
+    got = hip.recovered_row_matvec(ctox_hip.RecoveredRowMatVec(ctox_hip.TensorDType(dtype), w, x, 0.5))
+    ref = orc.recovered_row_matvec(dtype, w.tobytes(), x, 0.5)
+    assert abs(got - ref) <= 1e-4 * (abs(ref) + 1.0)
