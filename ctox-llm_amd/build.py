@@ -20,7 +20,7 @@ HIPCC = os.path.join(ROCM, "bin", "hipcc")
 
 # Packed-FP32 instructions are kept out of every code object on this pool.
 HIP_FLAGS = [
-    "--offload-arch=gfx950", "-O3", "-std=c++17",
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-mcode-object-version=5",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 

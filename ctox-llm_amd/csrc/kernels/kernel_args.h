@@ -7,11 +7,10 @@
 #define CTOX_BLOCK_LEN 64
 #define CTOX_Q2_BLOCK_BYTES 18
 #define CTOX_Q4_BLOCK_BYTES 34
-// Matvec tiling: a workgroup is 4 waves x 16 rows and covers CTOX_KCHUNK
-// quant blocks (1024 columns) of the K dimension.
+// Matvec tiling: a workgroup is 4 waves sharing 16 rows; each wave covers a
+// quarter of the K dimension.
 #define CTOX_MV_WAVES 4
-#define CTOX_MV_ROWS 64
-#define CTOX_KCHUNK 16
+#define CTOX_MV_ROWS 16
 #define CTOX_MAX_BATCH 8
 // Activation fixed-point: |X| <= 2^22 per 64-column block, three signed
 // 8-bit limbs (X = X0 + 2^8 X1 + 2^16 X2).
@@ -23,14 +22,15 @@
 #define CTOX_KSCALE_F16 2
 
 // Converts a [batch][columns] f32 activation (times s_in) into the int8
-// MFMA A-fragments consumed by ctox_qmatvec_*: for every 64-column block b
-// and token group tg (4 tokens), 64 lanes x 16 bytes. Per (block, token) it
-// also writes {quantum q, offset term K} (float2).
+// MFMA A-fragment rows consumed by ctox_q*_matvec_*: for every 64-column
+// block b and token t, three limbs x four k-groups x 16 bytes (192 bytes).
+// Per (block, token) it also writes the float4 epilogue constants
+// {2q, 512q, 131072q, K*q} (q = quantum, K = -off * sum of the limbs).
 struct PrepArgs {
     const float *input;     // [batch][columns]
     const void *s_in;       // NULL, f32[columns] or f16[columns]
-    int8_t *xa;             // [blocks][tgroups][64][16]
-    float *xc;              // [blocks][batch][2]
+    int8_t *xa;             // [blocks][batch][3 limbs][4 k-groups][16]
+    float *xc;              // [blocks][batch][4]
     uint32_t columns;
     uint32_t batch;
     uint32_t dtype;         // 0 = Q2 layout, 1 = Q4 layout
@@ -39,6 +39,8 @@ struct PrepArgs {
     uint32_t pad;
 };
 
+// One workgroup per 16 output rows (grid = ceil(rows / 16)); its four waves
+// split the K dimension.
 struct MatvecArgs {
     const uint8_t *weights; // packed rows of this launch (pure Q2 or Q4)
     uint64_t weights_len;   // bytes readable from `weights`
@@ -47,13 +49,9 @@ struct MatvecArgs {
     const void *s_out;      // NULL, f32[rows] or f16[rows]
     const float *bias;      // NULL or f32[rows]
     float *output;          // [batch][out_stride], row r at output[m*out_stride + r]
-    float *partial;         // [rowgroups][ksplit][batch][64] (ksplit > 1)
-    uint32_t *counters;     // [rowgroups], zero between launches (ksplit > 1)
     uint32_t rows;
     uint32_t columns;
     uint32_t batch;
-    uint32_t tgroups;
-    uint32_t ksplit;        // number of K chunks = ceil(blocks / CTOX_KCHUNK)
     uint32_t out_stride;
     uint32_t s_out_kind;
     uint32_t activation;

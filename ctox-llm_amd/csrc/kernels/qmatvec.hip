@@ -7,25 +7,32 @@
 // the crate's AVX2 path uses, Q/src/backend/cpu.rs:595-658).
 //
 // Design (MI355X-first, not a translation of the SM86 warp-per-row kernel):
-//  * The weights stay in the crate's packed CTOXQ layout (34- / 18-byte
-//    blocks, rows dense). Each wave stages 16 rows x 16 blocks of packed bytes
-//    into LDS with 128-bit buffer loads (hardware bounds-checked), so HBM is
-//    read with fully coalesced aligned 16-byte accesses even though blocks
-//    are only 2-byte aligned.
-//  * The contraction runs on the int8 matrix cores:
-//    v_mfma_i32_16x16x64_i8 with B = 16 rows x 64 codes (one quant block,
-//    codes 0..15 / 0..3 unpacked with two mask ops per dword) and A = the
-//    activation as exact fixed point: per 64-column block X = x'/q with
-//    q = 2^(e-22), split into three signed 8-bit limbs in A rows 4t+l.
-//    The integer products are exact; the only rounding is x' -> X (at most
-//    2^-23 of the block maximum) and the fp32 epilogue, so results agree with
-//    the fp32 scalar oracle to ~1e-6 relative.
-//  * C lane (g, j) holds limbs of token g for row j: the per-block dequant
-//    epilogue f = 2*sum(c*X) - off*sum(X), acc += scale*q*f is lane-local.
-//  * K is split into chunks of 16 blocks across workgroups when the row
-//    count alone cannot fill 256 CUs; the last workgroup of a row group sums
-//    the partials in fixed chunk order (deterministic) and applies bias,
-//    s_out and the activation.
+//  * Weights stay in the crate's packed CTOXQ layout (34- / 18-byte blocks,
+//    rows dense). Each wave stages 16 rows x 16 blocks of packed bytes into
+//    LDS with 128-bit buffer loads (hardware bounds-checked), so HBM is read
+//    with coalesced aligned 16-byte accesses although blocks are only 2-byte
+//    aligned. Lane (row = lane/4, part = lane%4) owns units part, part+4, ...
+//    of one row, so the staging addresses are per-lane constants plus
+//    immediates.
+//  * The contraction runs on the int8 matrix cores (v_mfma_i32_16x16x64_i8):
+//    B = 16 rows x 64 codes (codes 0..15 / 0..3 unpacked with mask ops), A =
+//    the activation as exact fixed point: per 64-column block X = x'/q with
+//    q = 2^(e-22), split into three signed 8-bit limbs (A rows). Integer
+//    products are exact; the only rounding is x' -> X (at most 2^-23 of the
+//    block maximum) and the fp32 epilogue, so results agree with the fp32
+//    scalar oracle to ~1e-6 relative.
+//  * Batch 1 ("block-diagonal"): A row group t (rows 4t..4t+2) carries the
+//    limbs of block t of a 4-block group, and only in k-group t; B k-group g
+//    carries quarter q of block g. Four MFMAs (q = 0..3) accumulate the four
+//    blocks' full 64-element sums, and C lane (g, j) ends up owning
+//    (block g, row j): every lane does useful dequant work.
+//  * Batch 2..8 ("token-stacked"): A rows 4t..4t+2 are token t's limbs of
+//    the current block; C lane (g, j) owns (token g, row j).
+//  * Per-block epilogue: f = 2q*C0 + 512q*C1 + 131072q*C2 + K*q with
+//    K = -off*sum(X); acc += scale * f.
+//  * K is split into chunks of 16 blocks across workgroups; the last
+//    workgroup of a row group sums the partials in a fixed association
+//    (deterministic) and applies bias, s_out and the activation.
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
@@ -62,7 +69,9 @@ __device__ __forceinline__ int frag_pos(uint32_t dtype, int w) {
     return dtype ? ((w & 1) ? 8 + (w >> 1) : (w >> 1)) : ((w & 3) * 4 + (w >> 2));
 }
 
-// One wave (64 threads) per (block, token).
+// One wave (64 threads) per (block, token). Output layout:
+//   xa: [block][token][limb 0..2][quarter 0..3][16 bytes]
+//   xc: [block][token] float4 {2q, 512q, 131072q, K*q}, K = -off*sum(X)
 extern "C" __global__ __launch_bounds__(64) void ctox_prep_activation_gfx950(PrepArgs a) {
     const uint32_t b = blockIdx.x, t = blockIdx.y, e = threadIdx.x;
     const uint32_t col = b * CTOX_BLOCK_LEN + e;
@@ -90,28 +99,54 @@ extern "C" __global__ __launch_bounds__(64) void ctox_prep_activation_gfx950(Pre
 
     const uint32_t g = e >> 4, w = e & 15;
     const int v = frag_pos(a.dtype, (int)w);
-    const uint32_t tg = t >> 2, slot = (t & 3) * 4;
-    int8_t *frag = a.xa + (((size_t)b * a.tgroups + tg) * 64) * 16;
-    frag[(g * 16 + slot + 0) * 16 + v] = (int8_t)x0;
-    frag[(g * 16 + slot + 1) * 16 + v] = (int8_t)x1;
-    frag[(g * 16 + slot + 2) * 16 + v] = (int8_t)x2;
-    frag[(g * 16 + slot + 3) * 16 + v] = 0;
+    int8_t *frag = a.xa + ((size_t)b * a.batch + t) * (3 * 64);
+    frag[(0 * 4 + g) * 16 + v] = (int8_t)x0;
+    frag[(1 * 4 + g) * 16 + v] = (int8_t)x1;
+    frag[(2 * 4 + g) * 16 + v] = (int8_t)x2;
     if (e == 0) {
         const long long sx = (long long)s0 + 256LL * s1 + 65536LL * s2;
         const long long off = a.dtype ? 15 : 3;
-        float *c = a.xc + ((size_t)b * a.batch + t) * 2;
-        c[0] = q;
-        c[1] = (float)(-off * sx);
+        float4 c;
+        c.x = 2.0f * q;
+        c.y = 512.0f * q;
+        c.z = 131072.0f * q;
+        c.w = (float)(-off * sx) * q;
+        ((float4 *)a.xc)[(size_t)b * a.batch + t] = c;
     }
 }
 
-template <int DT>
-struct QFmt {
+template <int DT, int MODE>  // MODE 0: batch 1, 1: batch 2..4, 2: batch 5..8
+struct MvCfg {
     static constexpr int BB = DT ? CTOX_Q4_BLOCK_BYTES : CTOX_Q2_BLOCK_BYTES;
-    static constexpr int QB = DT ? 8 : 4;                     // code bytes per quarter block
-    static constexpr int UMAX = (15 + CTOX_KCHUNK * BB + 15) / 16;  // 16B units per staged row
-    static constexpr int STRIDE = UMAX * 16;                  // LDS bytes per staged row
+    static constexpr int QB = DT ? 8 : 4;                    // code bytes per quarter block
+    static constexpr int CD = DT ? 8 : 4;                    // code dwords per block
+    static constexpr int CB = MODE == 0 ? 16 : 8;            // blocks per chunk
+    static constexpr int MAXB = MODE == 0 ? 1 : (MODE == 1 ? 4 : 8);
+    static constexpr int TG = MODE == 2 ? 2 : 1;
+    static constexpr int UMAX = (15 + CB * BB + 15) / 16;    // 16-byte units per staged row
+    static constexpr int STRIDE = UMAX * 16;                 // LDS bytes per staged row
+    static constexpr int ROUNDS = (UMAX + 3) / 4;            // staging loads per lane
+    static constexpr int XA_UNITS = CB * MAXB * 12;          // 16-byte units of fragments
+    static constexpr int XA_ROUNDS = (XA_UNITS + 63) / 64;
+    static constexpr int XC_N = CB * MAXB;
     static constexpr float DEN = DT ? 15.0f : 3.0f;
+};
+
+// Per-wave LDS: staged rows of the current chunk, its activation fragments
+// and block constants.
+template <int DT, int MODE>
+struct MvWave {
+    using C = MvCfg<DT, MODE>;
+    uint8_t rows[16 * C::STRIDE + 64];  // +64: the last block's dword reads may run 12 bytes past
+    int8_t xa[C::CB * C::MAXB * 192];
+    float4 xc[C::XC_N];
+};
+
+template <int DT, int MODE>
+struct MvShared {
+    MvWave<DT, MODE> w[CTOX_MV_WAVES];
+    int8_t zero[MODE == 0 ? 3 * 1024 + 64 : 16];  // zero A fragments (batch 1)
+    float red[CTOX_MV_WAVES][MvCfg<DT, MODE>::MAXB][16];
 };
 
 __device__ __forceinline__ float epilogue(float v, uint32_t row, const MatvecArgs &a) {
@@ -121,160 +156,226 @@ __device__ __forceinline__ float epilogue(float v, uint32_t row, const MatvecArg
     return v;
 }
 
-template <int DT, int TG>
+// B fragment (16 codes as int8) of one quarter block from its code dword(s).
+template <int DT>
+__device__ __forceinline__ v4i unpack_quarter(uint32_t w0, uint32_t w1) {
+    if (DT)
+        return (v4i){(int)(w0 & 0x0f0f0f0fu), (int)(w1 & 0x0f0f0f0fu), (int)((w0 >> 4) & 0x0f0f0f0fu),
+                     (int)((w1 >> 4) & 0x0f0f0f0fu)};
+    return (v4i){(int)(w0 & 0x03030303u), (int)((w0 >> 2) & 0x03030303u), (int)((w0 >> 4) & 0x03030303u),
+                 (int)((w0 >> 6) & 0x03030303u)};
+}
+
+// Register copy of one chunk in flight (weights, fragments, constants).
+template <int DT, int MODE>
+struct MvPrefetch {
+    using C = MvCfg<DT, MODE>;
+    v4i rows[C::ROUNDS];
+    v4i xa[C::XA_ROUNDS];
+    float4 xc;
+};
+
+// Issues the global loads of chunk [cb0, cb0 + nbc) for this wave.
+template <int DT, int MODE>
+__device__ __forceinline__ void mv_fetch(MvPrefetch<DT, MODE> &pf, const MatvecArgs &a,
+                                         __amdgpu_buffer_rsrc_t rsrc, uint32_t P, uint32_t rowbytes,
+                                         uint32_t rows_here, uint32_t cb0, uint32_t nbc, uint32_t lane) {
+    using C = MvCfg<DT, MODE>;
+    const uint32_t srow = lane >> 2, part = lane & 3;
+    const uint32_t o = P + srow * rowbytes + cb0 * C::BB;
+    const uint32_t nu = ((o & 15) + nbc * C::BB + 15) >> 4;
+    const bool rowok = srow < rows_here;
+    const uint32_t gbase = ((o >> 4) + part) * 16;
+#pragma unroll
+    for (int it = 0; it < C::ROUNDS; it++) {
+        pf.rows[it] = (v4i){0, 0, 0, 0};
+        if (rowok && part + 4 * it < nu)
+            pf.rows[it] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, gbase + it * 64, 0, 0);
+    }
+    const uint32_t nxa = nbc * a.batch * 12;
+    const v4i *src = (const v4i *)(a.xa + (size_t)cb0 * a.batch * 192);
+#pragma unroll
+    for (int it = 0; it < C::XA_ROUNDS; it++) {
+        const uint32_t u = it * 64 + lane;
+        pf.xa[it] = u < nxa ? src[u] : (v4i){0, 0, 0, 0};
+    }
+    pf.xc = lane < nbc * a.batch ? ((const float4 *)a.xc)[(size_t)cb0 * a.batch + lane]
+                                 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+}
+
+template <int DT, int MODE>
+__device__ __forceinline__ void mv_store(const MvPrefetch<DT, MODE> &pf, MvWave<DT, MODE> &wl, uint32_t lane) {
+    using C = MvCfg<DT, MODE>;
+    const uint32_t srow = lane >> 2, part = lane & 3;
+#pragma unroll
+    for (int it = 0; it < C::ROUNDS; it++)
+        if (part + 4 * it < (uint32_t)C::UMAX) *(v4i *)(wl.rows + srow * C::STRIDE + part * 16 + it * 64) = pf.rows[it];
+#pragma unroll
+    for (int it = 0; it < C::XA_ROUNDS; it++) {
+        const uint32_t u = it * 64 + lane;
+        if (u < (uint32_t)C::XA_UNITS) ((v4i *)wl.xa)[u] = pf.xa[it];
+    }
+    if (lane < (uint32_t)C::XC_N) wl.xc[lane] = pf.xc;
+}
+
+// Workgroup = 16 rows; wave w covers quant blocks [w*nb/4, (w+1)*nb/4) of
+// those rows in chunks of CB blocks, prefetching chunk c+1 into registers
+// while chunk c is computed from LDS. The four wave partials are added in
+// LDS in fixed order, so results are deterministic.
+template <int DT, int MODE>
 __device__ __forceinline__ void qmatvec_body(const MatvecArgs &a) {
-    using F = QFmt<DT>;
-    // +64 bytes of slack: the 3-dword code read of the last block may touch
-    // up to 12 bytes past a wave's last staged row.
-    __shared__ __align__(16) uint8_t lds[CTOX_MV_WAVES * 16 * F::STRIDE + 64];
-    __shared__ uint32_t s_last;
+    using C = MvCfg<DT, MODE>;
+    constexpr int TG = C::TG;
+    __shared__ __align__(16) MvShared<DT, MODE> sh;
 
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t nblocks = a.columns / CTOX_BLOCK_LEN;
-    const uint32_t rowbytes = nblocks * F::BB;
-    const uint32_t kc = blockIdx.x % a.ksplit, rg = blockIdx.x / a.ksplit;
-    const uint32_t b0 = kc * CTOX_KCHUNK;
-    const uint32_t nb = min((uint32_t)CTOX_KCHUNK, nblocks - b0);
-    const uint32_t rbase = rg * CTOX_MV_ROWS + wave * 16;
+    const uint32_t rowbytes = nblocks * C::BB;
+    const uint32_t r0 = blockIdx.x * 16;
+    const uint32_t rows_here = min(16u, a.rows - r0);
+    const uint32_t wb0 = wave * nblocks / CTOX_MV_WAVES, wb1 = (wave + 1) * nblocks / CTOX_MV_WAVES;
+    const uint32_t nchunks = (wb1 - wb0 + C::CB - 1) / C::CB;
+    MvWave<DT, MODE> &wl = sh.w[wave];
 
-    // ---- issue activation-fragment and per-block constant loads early ----
-    const uint32_t g = lane >> 4, j = lane & 15;
-    v4i afrag[CTOX_KCHUNK][TG];
-    float2 xcv[CTOX_KCHUNK][TG];
-#pragma unroll
-    for (int bl = 0; bl < CTOX_KCHUNK; bl++) {
-#pragma unroll
-        for (int tg = 0; tg < TG; tg++) {
-            afrag[bl][tg] = (v4i){0, 0, 0, 0};
-            xcv[bl][tg] = make_float2(0.0f, 0.0f);
-            if ((uint32_t)bl < nb) {
-                const uint32_t slot_tok = tg * 4 + (j >> 2);
-                if ((j & 3) < 3 && slot_tok < a.batch)
-                    afrag[bl][tg] = ((const v4i *)a.xa)[((size_t)(b0 + bl) * a.tgroups + tg) * 64 + lane];
-                const uint32_t tok = tg * 4 + g;
-                if (tok < a.batch)
-                    xcv[bl][tg] = ((const float2 *)a.xc)[(size_t)(b0 + bl) * a.batch + tok];
-            }
-        }
-    }
-
-    // ---- stage 16 rows x nb blocks of packed bytes into this wave's LDS ----
-    const uint64_t wg_off = (uint64_t)rg * CTOX_MV_ROWS * rowbytes + (uint64_t)b0 * F::BB;
+    const uint64_t wg_off = (uint64_t)r0 * rowbytes;
     const uintptr_t base = (uintptr_t)a.weights + wg_off;
     const uintptr_t aligned = base & ~(uintptr_t)15;
     const uint32_t P = (uint32_t)(base - aligned);
-    const uint64_t remain = a.weights_len - wg_off + P;
-    const int nrec = (int)(remain > 0x7fffffffULL ? 0x7fffffffULL : remain);
-    __amdgpu_buffer_rsrc_t rsrc =
-        __builtin_amdgcn_make_buffer_rsrc((void *)aligned, (short)0, nrec, 0x00020000);
-    uint8_t *wlds = lds + wave * 16 * F::STRIDE;
-    constexpr int ITEMS = 16 * F::UMAX;
-    constexpr int ROUNDS = (ITEMS + 63) / 64;
-    v4i stage[ROUNDS];
-#pragma unroll
-    for (int it = 0; it < ROUNDS; it++) {
-        const uint32_t idx = it * 64 + lane;
-        const uint32_t rj = idx / F::UMAX, u = idx % F::UMAX;
-        const uint32_t o = P + (wave * 16 + rj) * rowbytes;
-        const uint32_t nu = ((o & 15) + nb * F::BB + 15) >> 4;
-        stage[it] = (v4i){0, 0, 0, 0};
-        if (rj < 16 && u < nu && rbase + rj < a.rows)
-            stage[it] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, ((o >> 4) + u) * 16, 0, 0);
-    }
-#pragma unroll
-    for (int it = 0; it < ROUNDS; it++) {
-        const uint32_t idx = it * 64 + lane;
-        const uint32_t rj = idx / F::UMAX, u = idx % F::UMAX;
-        if (rj < 16) *(v4i *)(wlds + rj * F::STRIDE + u * 16) = stage[it];
-    }
-    __syncthreads();
+    // The buffer range check rejects a whole 16-byte load that straddles
+    // num_records, so the range is rounded up to the 16-byte granule that
+    // holds the last weight byte. That granule lies inside the same page as
+    // the last byte (pages are 16-byte aligned), so the extra bytes are
+    // mapped; they are never used.
+    const uint64_t remain = (a.weights_len - wg_off + P + 15) & ~15ULL;
+    const int nrec = (int)(remain > 0x7ffffff0ULL ? 0x7ffffff0ULL : remain);
+    __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)aligned, (short)0, nrec, 0x00020000);
 
-    // ---- one int8 MFMA per quant block, lane-local dequant epilogue ----
-    const uint32_t ph = (P + (wave * 16 + j) * rowbytes) & 15;
-    const uint8_t *rowl = wlds + j * F::STRIDE + ph;
+    if (MODE == 0) {
+        for (uint32_t i = threadIdx.x; i < sizeof(sh.zero) / 16; i += blockDim.x)
+            ((v4i *)sh.zero)[i] = (v4i){0, 0, 0, 0};
+        __syncthreads();
+    }
+
+    const uint32_t g = lane >> 4, j = lane & 15;
+    const uint32_t *lds32 = (const uint32_t *)wl.rows;
+    const uint16_t *lds16 = (const uint16_t *)wl.rows;
     float acc[TG];
 #pragma unroll
     for (int tg = 0; tg < TG; tg++) acc[tg] = 0.0f;
+
+    MvPrefetch<DT, MODE> pf;
+    if (nchunks > 0) mv_fetch<DT, MODE>(pf, a, rsrc, P, rowbytes, rows_here, wb0, min((uint32_t)C::CB, wb1 - wb0), lane);
+    for (uint32_t c = 0; c < nchunks; c++) {
+        const uint32_t cb0 = wb0 + c * C::CB;
+        const uint32_t nbc = min((uint32_t)C::CB, wb1 - cb0);
+        mv_store<DT, MODE>(pf, wl, lane);
+        // LDS operations of one wave complete in issue order; the fence only
+        // keeps the compiler from moving the reads below above the writes.
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        if (c + 1 < nchunks)
+            mv_fetch<DT, MODE>(pf, a, rsrc, P, rowbytes, rows_here, cb0 + C::CB,
+                               min((uint32_t)C::CB, wb1 - cb0 - C::CB), lane);
+        const uint32_t ph = (P + j * rowbytes + cb0 * C::BB) & 15;
+        const uint32_t rowoff = j * C::STRIDE + ph;
+
+        if (MODE == 0) {
+            // Block-diagonal: lane (g, j) owns block 4G+g of row j.
+            const uint32_t boff = rowoff + g * C::BB;
+            const uint32_t d0 = (boff + 2) >> 2, sft = (boff + 2) & 3;
+            const bool scale_hi = sft == 0;  // scale in the upper half of dword d0-1
+            const uint32_t i = lane & 15, t = i >> 2, limb = i & 3;
+            const bool aok = t == g && limb < 3;
+            const int8_t *xab = (aok ? wl.xa : sh.zero) + g * 192 + min(limb, 2u) * 64;
+            const uint32_t ngroups = (nbc + 3) >> 2;
+            for (uint32_t G = 0; G < ngroups; G++) {
+                constexpr int GD = C::BB;  // dwords per 4-block step (4*BB bytes)
+                uint32_t d[C::CD + 2];
 #pragma unroll
-    for (int bl = 0; bl < CTOX_KCHUNK; bl++) {
-        if ((uint32_t)bl >= nb) break;
-        const uint8_t *blk = rowl + bl * F::BB;
-        const float scale = half_bits_to_float(*(const uint16_t *)blk);
-        const uintptr_t ca = (uintptr_t)(blk + 2 + F::QB * g);
-        const uint32_t *cw = (const uint32_t *)(ca & ~(uintptr_t)3);
-        const uint32_t sh = (uint32_t)(ca & 3);
-        v4i bfrag;
-        if (DT) {
-            const uint32_t d0 = cw[0], d1 = cw[1], d2 = cw[2];
-            const uint32_t w0 = __builtin_amdgcn_alignbyte(d1, d0, sh);
-            const uint32_t w1 = __builtin_amdgcn_alignbyte(d2, d1, sh);
-            bfrag = (v4i){(int)(w0 & 0x0f0f0f0fu), (int)(w1 & 0x0f0f0f0fu),
-                          (int)((w0 >> 4) & 0x0f0f0f0fu), (int)((w1 >> 4) & 0x0f0f0f0fu)};
+                for (int k = 0; k < C::CD + 2; k++) d[k] = lds32[d0 + G * GD + k - 1];
+                uint32_t cd[C::CD];
+#pragma unroll
+                for (int k = 0; k < C::CD; k++) cd[k] = __builtin_amdgcn_alignbyte(d[k + 2], d[k + 1], sft);
+                const uint32_t sbits = scale_hi ? (d[0] >> 16) : d[1];
+                v4i cc = (v4i){0, 0, 0, 0};
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const v4i bf = DT ? unpack_quarter<DT>(cd[2 * q], cd[2 * q + 1]) : unpack_quarter<DT>(cd[q], 0);
+                    const v4i af = *(const v4i *)(xab + G * 768 + q * 16);
+                    cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf, cc, 0, 0, 0);
+                }
+                const float4 kq = wl.xc[G * 4 + g];
+                const float scale = G * 4 + g < nbc ? half_bits_to_float(sbits) : 0.0f;
+                float f = fmaf((float)cc[0], kq.x, kq.w);
+                f = fmaf((float)cc[1], kq.y, f);
+                f = fmaf((float)cc[2], kq.z, f);
+                acc[0] = fmaf(f, scale, acc[0]);
+            }
         } else {
-            const uint32_t d0 = cw[0], d1 = cw[1];
-            const uint32_t w = __builtin_amdgcn_alignbyte(d1, d0, sh);
-            bfrag = (v4i){(int)(w & 0x03030303u), (int)((w >> 2) & 0x03030303u),
-                          (int)((w >> 4) & 0x03030303u), (int)((w >> 6) & 0x03030303u)};
-        }
+            // Token-stacked: lane (g, j) reads quarter g of every block of row j.
+            constexpr int NW = DT ? 3 : 2;
+            for (uint32_t bl = 0; bl < nbc; bl++) {
+                const uint32_t boff = rowoff + bl * C::BB;
+                const uint32_t sbits = lds16[boff >> 1];
+                const uint32_t ca = boff + 2 + C::QB * g;
+                const uint32_t sftq = ca & 3;
+                uint32_t cw[NW];
 #pragma unroll
-        for (int tg = 0; tg < TG; tg++) {
-            const v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(afrag[bl][tg], bfrag,
-                                                                 (v4i){0, 0, 0, 0}, 0, 0, 0);
-            const float2 xc = xcv[bl][tg];
-            float f = fmaf((float)c[0], 2.0f, xc.y);
-            f = fmaf((float)c[1], 512.0f, f);
-            f = fmaf((float)c[2], 131072.0f, f);
-            acc[tg] = fmaf(f, scale * xc.x, acc[tg]);
+                for (int w = 0; w < NW; w++) cw[w] = lds32[(ca >> 2) + w];
+                const uint32_t w0 = __builtin_amdgcn_alignbyte(cw[1], cw[0], sftq);
+                const uint32_t w1 = DT ? __builtin_amdgcn_alignbyte(cw[NW - 1], cw[1], sftq) : 0u;
+                const v4i bf = unpack_quarter<DT>(w0, w1);
+                const float scale = half_bits_to_float(sbits);
+#pragma unroll
+                for (int tg = 0; tg < TG; tg++) {
+                    const uint32_t tok = tg * 4 + (j >> 2), limb = j & 3;
+                    const bool aok = limb < 3 && tok < a.batch;
+                    const uint32_t tok_c = min(tok, a.batch - 1), limb_c = min(limb, 2u);
+                    const v4i av = *(const v4i *)(wl.xa + ((bl * a.batch + tok_c) * 3 + limb_c) * 64 + g * 16);
+                    const v4i af = aok ? av : (v4i){0, 0, 0, 0};
+                    const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf, (v4i){0, 0, 0, 0}, 0, 0, 0);
+                    const float4 kq = wl.xc[bl * a.batch + min((uint32_t)(tg * 4) + g, a.batch - 1)];
+                    float f = fmaf((float)cc[0], kq.x, kq.w);
+                    f = fmaf((float)cc[1], kq.y, f);
+                    f = fmaf((float)cc[2], kq.z, f);
+                    acc[tg] = fmaf(f, scale, acc[tg]);
+                }
+            }
         }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     }
 
-    const uint32_t row = rbase + j;
-    if (a.ksplit == 1) {
+    // Lane (g, j) owns row r0+j for token 0 (batch 1, after summing the four
+    // block lanes) or token tg*4+g.
+    if (MODE == 0) {
+        acc[0] += __shfl_xor(acc[0], 16);
+        acc[0] += __shfl_xor(acc[0], 32);
+        if (g == 0) sh.red[wave][0][j] = acc[0];
+    } else {
 #pragma unroll
         for (int tg = 0; tg < TG; tg++) {
             const uint32_t tok = tg * 4 + g;
-            if (tok < a.batch && row < a.rows)
-                a.output[(size_t)tok * a.out_stride + row] = epilogue(acc[tg] / F::DEN, row, a);
+            if (tok < a.batch) sh.red[wave][tok][j] = acc[tg];
         }
-        return;
-    }
-
-    // ---- split-K: publish partials, last workgroup of the row group combines ----
-#pragma unroll
-    for (int tg = 0; tg < TG; tg++) {
-        const uint32_t tok = tg * 4 + g;
-        if (tok < a.batch)
-            a.partial[(((size_t)rg * a.ksplit + kc) * a.batch + tok) * CTOX_MV_ROWS + wave * 16 + j] =
-                acc[tg];
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t old = __hip_atomic_fetch_add(&a.counters[rg], 1u, __ATOMIC_ACQ_REL,
-                                                    __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (old == a.ksplit - 1) ? 1u : 0u;
     }
     __syncthreads();
-    if (!s_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    for (uint32_t idx = threadIdx.x; idx < a.batch * CTOX_MV_ROWS; idx += blockDim.x) {
-        const uint32_t tok = idx / CTOX_MV_ROWS, rr = idx % CTOX_MV_ROWS;
-        const uint32_t orow = rg * CTOX_MV_ROWS + rr;
-        float s = 0.0f;
-        for (uint32_t c = 0; c < a.ksplit; c++)
-            s += __builtin_nontemporal_load(
-                &a.partial[(((size_t)rg * a.ksplit + c) * a.batch + tok) * CTOX_MV_ROWS + rr]);
-        if (orow < a.rows) a.output[(size_t)tok * a.out_stride + orow] = epilogue(s / F::DEN, orow, a);
+    if (threadIdx.x < a.batch * 16) {
+        const uint32_t tok = threadIdx.x >> 4, jj = threadIdx.x & 15, row = r0 + jj;
+        const float s = ((sh.red[0][tok][jj] + sh.red[1][tok][jj]) + sh.red[2][tok][jj]) + sh.red[3][tok][jj];
+        if (jj < rows_here) a.output[(size_t)tok * a.out_stride + row] = epilogue(s / C::DEN, row, a);
     }
-    if (threadIdx.x == 0)
-        __hip_atomic_store(&a.counters[rg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+extern "C" __global__ __launch_bounds__(256) void ctox_q4_matvec_b1_gfx950(MatvecArgs a) {
+    qmatvec_body<1, 0>(a);
+}
 extern "C" __global__ __launch_bounds__(256) void ctox_q4_matvec_b4_gfx950(MatvecArgs a) {
     qmatvec_body<1, 1>(a);
 }
 extern "C" __global__ __launch_bounds__(256) void ctox_q4_matvec_b8_gfx950(MatvecArgs a) {
     qmatvec_body<1, 2>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void ctox_q2_matvec_b1_gfx950(MatvecArgs a) {
+    qmatvec_body<0, 0>(a);
 }
 extern "C" __global__ __launch_bounds__(256) void ctox_q2_matvec_b4_gfx950(MatvecArgs a) {
     qmatvec_body<0, 1>(a);

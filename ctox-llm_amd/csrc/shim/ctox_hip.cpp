@@ -128,12 +128,11 @@ struct ctox_hip_backend {
     char arch[64] = {0};
     hipModule_t module = nullptr;
     hipStream_t stream = nullptr;
-    hipFunction_t prep = nullptr, q4_b4 = nullptr, q4_b8 = nullptr, q2_b4 = nullptr,
-                  q2_b8 = nullptr, rec_row = nullptr, row_dot = nullptr, gdn_norms = nullptr,
+    hipFunction_t prep = nullptr, q4_b1 = nullptr, q4_b4 = nullptr, q4_b8 = nullptr, q2_b1 = nullptr,
+                  q2_b4 = nullptr, q2_b8 = nullptr, rec_row = nullptr, row_dot = nullptr, gdn_norms = nullptr,
                   gdn_scan = nullptr;
-    // Activation staging (two layouts: [0] Q2, [1] Q4), split-K partials,
-    // counters (self-resetting, zeroed once) and gated-delta norms.
-    DevBuf xa[2], xc[2], partial, counters, norms;
+    // Activation staging (two layouts: [0] Q2, [1] Q4) and gated-delta norms.
+    DevBuf xa[2], xc[2], norms;
 };
 
 struct ctox_hip_matrix {
@@ -183,7 +182,9 @@ ctox_status launch(hipFunction_t f, dim3 grid, dim3 block, hipStream_t s, Args a
     return CTOX_OK;
 }
 
-hipStream_t pick_stream(ctox_hip_backend *b, void *s) { return s ? (hipStream_t)s : b->stream; }
+// Device entry points run on the caller's stream exactly as given; NULL is
+// HIP's null stream, as everywhere in the HIP API.
+hipStream_t pick_stream(ctox_hip_backend *, void *s) { return (hipStream_t)s; }
 
 // Q/src/backend/cpu.rs:41-173 (same order of checks and error kinds).
 ctox_status validate_matvec(const ctox_fused_matvec *op, bool need_input, size_t *bpr) {
@@ -279,8 +280,8 @@ ctox_status run_prep(ctox_hip_backend *b, int layout, const float *d_input, size
                      size_t batch, const void *d_s_in, uint32_t s_in_kind, hipStream_t s) {
     const size_t blocks = columns / kBlockLen;
     const size_t tgroups = (batch + 3) / 4;
-    ctox_status st = ensure(b, b->xa[layout], blocks * tgroups * 64 * 16, false);
-    if (!st) st = ensure(b, b->xc[layout], blocks * batch * 2 * sizeof(float), false);
+    ctox_status st = ensure(b, b->xa[layout], blocks * batch * 192, false);
+    if (!st) st = ensure(b, b->xc[layout], blocks * batch * 4 * sizeof(float), false);
     if (st) return st;
     PrepArgs a{};
     a.input = d_input;
@@ -303,17 +304,10 @@ ctox_status run_matvec(ctox_hip_backend *b, int32_t dtype, const void *d_weights
                        const float *d_bias, float *d_output, size_t out_stride, uint32_t act,
                        hipStream_t s) {
     const size_t blocks = columns / kBlockLen;
-    const size_t rowgroups = (rows + CTOX_MV_ROWS - 1) / CTOX_MV_ROWS;
-    const size_t ksplit = (blocks + CTOX_KCHUNK - 1) / CTOX_KCHUNK;
+    const size_t groups = (rows + CTOX_MV_ROWS - 1) / CTOX_MV_ROWS;
     const size_t tgroups = (batch + 3) / 4;
     const int layout = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
-    if (rowgroups * ksplit > 0x7fffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
-    if (ksplit > 1) {
-        ctox_status st = ensure(b, b->partial, rowgroups * ksplit * batch * CTOX_MV_ROWS * sizeof(float),
-                                false);
-        if (!st) st = ensure(b, b->counters, rowgroups * sizeof(uint32_t), true);
-        if (st) return st;
-    }
+    if (groups > 0x7fffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
     MatvecArgs a{};
     a.weights = (const uint8_t *)d_weights;
     a.weights_len = (uint64_t)rows * blocks * block_bytes(dtype);
@@ -322,19 +316,15 @@ ctox_status run_matvec(ctox_hip_backend *b, int32_t dtype, const void *d_weights
     a.s_out = d_s_out;
     a.bias = d_bias;
     a.output = d_output;
-    a.partial = (float *)b->partial.ptr;
-    a.counters = (uint32_t *)b->counters.ptr;
     a.rows = (uint32_t)rows;
     a.columns = (uint32_t)columns;
     a.batch = (uint32_t)batch;
-    a.tgroups = (uint32_t)tgroups;
-    a.ksplit = (uint32_t)ksplit;
     a.out_stride = (uint32_t)out_stride;
     a.s_out_kind = s_out_kind;
     a.activation = act;
-    hipFunction_t f = dtype == CTOX_DTYPE_Q4B64 ? (tgroups == 1 ? b->q4_b4 : b->q4_b8)
-                                                : (tgroups == 1 ? b->q2_b4 : b->q2_b8);
-    return launch(f, dim3((unsigned)(rowgroups * ksplit)), dim3(256), s, a, "ctox_q*_matvec_gfx950");
+    hipFunction_t f = dtype == CTOX_DTYPE_Q4B64 ? (batch == 1 ? b->q4_b1 : (tgroups == 1 ? b->q4_b4 : b->q4_b8))
+                                                : (batch == 1 ? b->q2_b1 : (tgroups == 1 ? b->q2_b4 : b->q2_b8));
+    return launch(f, dim3((unsigned)groups), dim3(256), s, a, "ctox_q*_matvec_gfx950");
 }
 
 ctox_status dispatch_matrix(ctox_hip_backend *b, const ctox_hip_matrix *m, const float *d_input,
@@ -397,7 +387,8 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
     struct {
         hipFunction_t *f;
         const char *name;
-    } fns[] = {{&b->prep, "ctox_prep_activation_gfx950"}, {&b->q4_b4, "ctox_q4_matvec_b4_gfx950"},
+    } fns[] = {{&b->prep, "ctox_prep_activation_gfx950"}, {&b->q4_b1, "ctox_q4_matvec_b1_gfx950"},
+               {&b->q2_b1, "ctox_q2_matvec_b1_gfx950"},    {&b->q4_b4, "ctox_q4_matvec_b4_gfx950"},
                {&b->q4_b8, "ctox_q4_matvec_b8_gfx950"},    {&b->q2_b4, "ctox_q2_matvec_b4_gfx950"},
                {&b->q2_b8, "ctox_q2_matvec_b8_gfx950"},    {&b->rec_row, "ctox_recovered_row_gfx950"},
                {&b->row_dot, "ctox_row_dot_gfx950"},       {&b->gdn_norms, "ctox_gdn_norms_gfx950"},
@@ -423,7 +414,7 @@ extern "C" void ctox_hip_backend_destroy(ctox_hip_backend *b) {
     if (!b) return;
     (void)hipSetDevice(b->device);
     (void)hipDeviceSynchronize();
-    DevBuf *bufs[] = {&b->xa[0], &b->xa[1], &b->xc[0], &b->xc[1], &b->partial, &b->counters, &b->norms};
+    DevBuf *bufs[] = {&b->xa[0], &b->xa[1], &b->xc[0], &b->xc[1], &b->norms};
     for (DevBuf *d : bufs)
         if (d->ptr) (void)hipFree(d->ptr);
     if (b->stream) (void)hipStreamDestroy(b->stream);

@@ -230,6 +230,13 @@ def load_library() -> ctypes.CDLL:
     """Loads lib/libctox_hip.so (raises OSError if it was not built)."""
     global _lib
     if _lib is None:
+        # A process holds one HIP runtime. When PyTorch is installed its
+        # bundled libamdhip64.so.7 is loaded first, and this library (same
+        # SONAME) binds to it instead of loading /opt/rocm's copy beside it.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         if not os.path.exists(LIB_PATH):
             raise OSError(f"{LIB_PATH} is missing: run `python ctox-llm_amd/build.py`")
         lib = ctypes.CDLL(LIB_PATH)

@@ -8,8 +8,8 @@
  * candidate runtime binds its kernels through the driver API
  * (Q/src/backend/cuda_runtime.rs:195-294). All signatures use plain
  * pointers and sizes; no PyTorch or HIP C++ types cross the boundary.
- * Streams are passed as `void*` holding a `hipStream_t` (NULL = the
- * backend's own stream).
+ * Streams are passed as `void*` holding a `hipStream_t`; NULL is HIP's
+ * null stream. Host-buffer entry points use a stream the backend owns.
  *
  * Threading: one backend handle owns one device context and is externally
  * synchronized (the reference CUDA runtime is `Rc`, not `Send`:
