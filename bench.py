@@ -29,8 +29,8 @@ sys.path.insert(0, os.path.join(ROOT, "ctox-llm_amd"))
 
 HBM_PEAK_GBS = 8000.0
 INFINITY_CACHE = 256 << 20
-HEAD_KERNEL = "ctox_q2_matvec_b1_gfx950"
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "ctox_q2_matvec_b1_gfx950.config2.traffic.txt")
+HEAD_KERNEL = "ctox_q2_matvec_sl_gfx950"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "ctox_q2_matvec_sl_gfx950.config2.traffic.txt")
 
 
 def log(*a):

@@ -1,3 +1,4 @@
 // Single code object for every gfx950 kernel of the backend.
 #include "qmatvec.hip"
+#include "qmatvec_slices.hip"
 #include "gated_delta.hip"

@@ -57,6 +57,12 @@ struct MatvecArgs {
     uint32_t activation;
 };
 
+// Batch-1 slice kernels (rows of whole 16-byte units): a workgroup of
+// CTOX_SLICE_WAVES waves walks a 16-row tile in slices of 28 (Q4) / 56 (Q2)
+// blocks, each slice one 1 KiB coalesced load per row.
+constexpr uint32_t ctox_slice_blocks(uint32_t dtype) { return dtype ? 28u : 56u; }
+#define CTOX_SLICE_WAVES 8
+
 struct RecoveredRowArgs {
     const uint8_t *weights; // one packed row
     const void *s_in;       // f32 or f16 [columns]

@@ -131,6 +131,10 @@ struct ctox_hip_backend {
     hipFunction_t prep = nullptr, q4_b1 = nullptr, q4_b4 = nullptr, q4_b8 = nullptr, q2_b1 = nullptr,
                   q2_b4 = nullptr, q2_b8 = nullptr, rec_row = nullptr, row_dot = nullptr, gdn_norms = nullptr,
                   gdn_scan = nullptr;
+    // Batch-1 slice kernels per dtype [Q2, Q4]: [0] walks the slices, [n]
+    // requests all n slices up front.
+    hipFunction_t sl[2][4] = {};
+    int cus = 0;
     // Activation staging (two layouts: [0] Q2, [1] Q4) and gated-delta norms.
     DevBuf xa[2], xc[2], norms;
 };
@@ -274,6 +278,8 @@ uint32_t kernel_scale_kind(int32_t kind) {
                                   : (kind == CTOX_SCALE_F16LE ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE);
 }
 
+size_t packed_row_bytes(int32_t dtype, size_t columns) { return columns / kBlockLen * block_bytes(dtype); }
+
 // Converts `batch` activation rows into the MFMA A-fragment layout `layout`
 // (0 = Q2 element order, 1 = Q4 element order).
 ctox_status run_prep(ctox_hip_backend *b, int layout, const float *d_input, size_t columns,
@@ -298,19 +304,18 @@ ctox_status run_prep(ctox_hip_backend *b, int layout, const float *d_input, size
 }
 
 // One launch over `rows` packed rows of one dtype (a pure matrix or one
-// mixed segment), output rows written at d_output[m*out_stride + r].
-ctox_status run_matvec(ctox_hip_backend *b, int32_t dtype, const void *d_weights, size_t rows,
+// mixed segment), output rows written at d_output[m*out_stride + r], with
+// the activation already staged in `layout`.
+ctox_status run_matvec(ctox_hip_backend *b, int layout, int32_t dtype, const void *d_weights, size_t rows,
                        size_t columns, size_t batch, const void *d_s_out, uint32_t s_out_kind,
                        const float *d_bias, float *d_output, size_t out_stride, uint32_t act,
                        hipStream_t s) {
-    const size_t blocks = columns / kBlockLen;
     const size_t groups = (rows + CTOX_MV_ROWS - 1) / CTOX_MV_ROWS;
     const size_t tgroups = (batch + 3) / 4;
-    const int layout = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
     if (groups > 0x7fffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
     MatvecArgs a{};
     a.weights = (const uint8_t *)d_weights;
-    a.weights_len = (uint64_t)rows * blocks * block_bytes(dtype);
+    a.weights_len = (uint64_t)rows * packed_row_bytes(dtype, columns);
     a.xa = (const int8_t *)b->xa[layout].ptr;
     a.xc = (const float *)b->xc[layout].ptr;
     a.s_out = d_s_out;
@@ -322,15 +327,27 @@ ctox_status run_matvec(ctox_hip_backend *b, int32_t dtype, const void *d_weights
     a.out_stride = (uint32_t)out_stride;
     a.s_out_kind = s_out_kind;
     a.activation = act;
-    hipFunction_t f = dtype == CTOX_DTYPE_Q4B64 ? (batch == 1 ? b->q4_b1 : (tgroups == 1 ? b->q4_b4 : b->q4_b8))
-                                                : (batch == 1 ? b->q2_b1 : (tgroups == 1 ? b->q2_b4 : b->q2_b8));
+    const bool q4 = dtype == CTOX_DTYPE_Q4B64;
+    // Batch 1 on rows of whole 16-byte units: the slice kernels (all slices
+    // requested up front when there are at most three, else walked).
+    const size_t rb = packed_row_bytes(dtype, columns);
+    if (batch == 1 && rb % 16 == 0 && ((uintptr_t)d_weights & 15) == 0) {
+        const size_t ns = (columns / kBlockLen + ctox_slice_blocks(q4) - 1) / ctox_slice_blocks(q4);
+        hipFunction_t f = b->sl[q4 ? 1 : 0][ns <= 3 ? ns : 0];
+        return launch(f, dim3((unsigned)groups), dim3(CTOX_SLICE_WAVES * 64), s, a, "ctox_q*_matvec_sl*_gfx950");
+    }
+    hipFunction_t f = q4 ? (batch == 1 ? b->q4_b1 : (tgroups == 1 ? b->q4_b4 : b->q4_b8))
+                         : (batch == 1 ? b->q2_b1 : (tgroups == 1 ? b->q2_b4 : b->q2_b8));
     return launch(f, dim3((unsigned)groups), dim3(256), s, a, "ctox_q*_matvec_gfx950");
 }
 
+// `prepped` marks the layouts already staged for this input in this call
+// sequence (fan-out shares them).
 ctox_status dispatch_matrix(ctox_hip_backend *b, const ctox_hip_matrix *m, const float *d_input,
                             size_t batch, float *d_output, hipStream_t s, bool prepped[2],
                             uint32_t act) {
     for (const ctox_quant_segment &seg : m->segments) {
+        const void *w = (const uint8_t *)m->d_weights + seg.offset;
         const int layout = seg.dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
         if (!prepped[layout]) {
             ctox_status st = run_prep(b, layout, d_input, m->columns, batch, m->d_s_in, m->s_in_kind, s);
@@ -341,9 +358,8 @@ ctox_status dispatch_matrix(ctox_hip_backend *b, const ctox_hip_matrix *m, const
         const void *so = nullptr;
         if (m->s_out_kind == CTOX_KSCALE_F32) so = (const float *)m->d_s_out + r0;
         if (m->s_out_kind == CTOX_KSCALE_F16) so = (const uint16_t *)m->d_s_out + r0;
-        ctox_status st = run_matvec(b, seg.dtype, (const uint8_t *)m->d_weights + seg.offset, nrows,
-                                    m->columns, batch, so, m->s_out_kind, m->d_bias ? m->d_bias + r0 : nullptr,
-                                    d_output + r0, m->rows, act, s);
+        ctox_status st = run_matvec(b, layout, seg.dtype, w, nrows, m->columns, batch, so, m->s_out_kind,
+                                    m->d_bias ? m->d_bias + r0 : nullptr, d_output + r0, m->rows, act, s);
         if (st) return st;
     }
     return CTOX_OK;
@@ -392,7 +408,11 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->q4_b8, "ctox_q4_matvec_b8_gfx950"},    {&b->q2_b4, "ctox_q2_matvec_b4_gfx950"},
                {&b->q2_b8, "ctox_q2_matvec_b8_gfx950"},    {&b->rec_row, "ctox_recovered_row_gfx950"},
                {&b->row_dot, "ctox_row_dot_gfx950"},       {&b->gdn_norms, "ctox_gdn_norms_gfx950"},
-               {&b->gdn_scan, "ctox_gdn_scan_gfx950"}};
+               {&b->gdn_scan, "ctox_gdn_scan_gfx950"},
+               {&b->sl[0][0], "ctox_q2_matvec_sl_gfx950"}, {&b->sl[0][1], "ctox_q2_matvec_sl1_gfx950"},
+               {&b->sl[0][2], "ctox_q2_matvec_sl2_gfx950"}, {&b->sl[0][3], "ctox_q2_matvec_sl3_gfx950"},
+               {&b->sl[1][0], "ctox_q4_matvec_sl_gfx950"}, {&b->sl[1][1], "ctox_q4_matvec_sl1_gfx950"},
+               {&b->sl[1][2], "ctox_q4_matvec_sl2_gfx950"}, {&b->sl[1][3], "ctox_q4_matvec_sl3_gfx950"}};
     for (auto &f : fns) {
         if (le != hipSuccess) break;
         le = hipModuleGetFunction(f.f, b->module, f.name);
@@ -406,6 +426,7 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
         ctox_hip_backend_destroy(b);
         return fail(CTOX_ERR_UNSUPPORTED_OPERATION, "HIP module setup failed: %s", hipGetErrorString(le));
     }
+    b->cus = prop.multiProcessorCount;
     *out = b;
     return CTOX_OK;
 }
@@ -551,7 +572,7 @@ extern "C" ctox_status ctox_hip_launch_fused_matvec(ctox_hip_backend *b, int32_t
     ctox_status st = run_prep(b, layout, d_input, columns, batch, d_s_in,
                               d_s_in ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, s);
     if (st) return st;
-    return run_matvec(b, dtype, d_weights, rows, columns, batch, d_s_out,
+    return run_matvec(b, layout, dtype, d_weights, rows, columns, batch, d_s_out,
                       d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, d_bias, d_output, rows, activation, s);
 }
 

@@ -27,7 +27,7 @@ def test_library_embeds_a_gfx950_code_object():
     import ctox_hip
     blob = open(ctox_hip.LIB_PATH, "rb").read()
     assert b"amdgcn-amd-amdhsa--gfx950" in blob
-    for k in ("ctox_q4_matvec_b1_gfx950", "ctox_q2_matvec_b1_gfx950", "ctox_q4_matvec_b4_gfx950", "ctox_q2_matvec_b8_gfx950", "ctox_prep_activation_gfx950",
+    for k in ("ctox_q4_matvec_b1_gfx950", "ctox_q2_matvec_b1_gfx950", "ctox_q4_matvec_sl_gfx950", "ctox_q2_matvec_sl3_gfx950", "ctox_q4_matvec_b4_gfx950", "ctox_q2_matvec_b8_gfx950", "ctox_prep_activation_gfx950",
               "ctox_gdn_scan_gfx950"):
         assert k.encode() in blob
 

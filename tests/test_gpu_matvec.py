@@ -83,6 +83,23 @@ def test_matvec_host_api_small_shapes(hip, orc, dtype, rows, cols):
         check(got, ref, f"dtype={dtype} {rows}x{cols} {sk}")
 
 
+# Batch 1 on columns % 512 == 0 runs the slice kernels: 28 (Q4) / 56 (Q2)
+# blocks per slice, all slices requested up front for 1..3 slices, walked
+# beyond. These widths give every slice count of both dtypes at least once.
+SLICE_COLS = [512, 1536, 3584, 5120, 7168, 10752, 17408]
+
+
+@pytest.mark.parametrize("dtype", [0, 1])
+@pytest.mark.parametrize("cols", SLICE_COLS)
+def test_batch1_slice_counts(hip, orc, dtype, cols):
+    for rows in (16, 37):
+        say(f"case slices dtype={dtype} rows={rows} cols={cols}")
+        op, parts = make_case(dtype, rows, cols, 7 * cols + rows, "f16", True, ctox_hip.Activation.Silu)
+        got = hip.fused_matvec(op)
+        ref = oracle_rows(orc, dtype, rows, cols, parts, ctox_hip.Activation.Silu)[0]
+        check(got, ref, f"slices dtype={dtype} {rows}x{cols}")
+
+
 def test_crate_fixture_cases(hip, orc):
     # Q/src/backend/cpu.rs:774-832 fixtures (sin weights, cos input, f32 scales, bias, SiLU)
     from test_oracle_matvec import encode_fixture
