@@ -2,3 +2,4 @@
 #include "qmatvec.hip"
 #include "qmatvec_slices.hip"
 #include "gated_delta.hip"
+#include "gated_delta_chunk.hip"

@@ -1,0 +1,358 @@
+// Chunked (WY-form) gated-delta prefill, fp32, gfx950.
+//
+// The token recurrence of Q/src/reference.rs:230-297 / 377-415,
+//   S_t = a_t (I - b_t k_t k_t^T) S_{t-1} + b_t k_t v_t^T,   o_t = S_t^T q_t
+// (k, q L2-normalised, q also scaled by 1/sqrt(key_dim), a_t = exp(log_decay_t),
+// b_t = beta_t), is evaluated chunk by chunk. Within a chunk of C tokens, with
+// G_t = sum_{s<=t} log_decay_s (relative to the chunk start) and
+// g_t = exp(G_t):
+//   S_t = g_t S_0 + sum_{r<=t} exp(G_t - G_r) k_r d_r^T
+//   d_s = b_s (v_s - g_s S_0^T k_s - sum_{r<s} exp(G_s - G_r) (k_s.k_r) d_r)
+// i.e. (I + diag(b) M) D = diag(b) V - diag(b g) K S_0 with M the strictly
+// lower, decay-weighted K K^T, so D = T (diag(b) V - diag(b g) K S_0),
+// T = (I + diag(b) M)^{-1} (unit lower triangular). Then
+//   O   = diag(g) Q S_0 + A D,       A[t][r] = exp(G_t - G_r) (q_t.k_r), r <= t
+//   S_C = g_C S_0 + sum_r exp(G_C - G_r) k_r d_r^T.
+// Every decay factor is exp of a non-positive difference (<= 1), so nothing
+// overflows however strong the decay.
+//
+// Pass 1 (ctox_gdn_chunk_prep_gfx950, one workgroup per (head, chunk), all
+// chunks in parallel): norms, G, M and A by LDS-tiled dot products, T by
+// forward substitution (one thread per column, the column in registers).
+// Pass 2 (ctox_gdn_chunk_scan_gfx950, one workgroup per (head, 16 value
+// columns), chunks in order): the 128 x 16 state slice stays in LDS across
+// chunks; the five small products per chunk run on v_mfma_f32_16x16x4_f32.
+// Value columns are independent in the recurrence, so slices need no
+// exchange. Padded tokens of a partial last chunk have k = q = v = 0,
+// beta = 0 and log_decay = 0: identity steps.
+
+#include <hip/hip_runtime.h>
+
+#include "kernel_args.h"
+
+#define GC 64        // max chunk length
+#define GKD 128      // max key_dim of the chunked path
+#define GVS 16       // value columns per pass-2 workgroup
+#define GPAD 129     // LDS row stride (floats) of K / Q tiles: odd, conflict-free
+#define TPAD 65      // LDS row stride of T / A / M
+
+typedef float gv4f __attribute__((ext_vector_type(4)));
+
+// Scratch per (head, chunk): T[64][64], A[64][64], then G[64], kinv[64], qinv[64].
+__host__ __device__ constexpr uint32_t ctox_gdn_chunk_floats() { return 2 * GC * GC + 3 * GC; }
+
+extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_prep_gfx950(GdnArgs a) {
+    __shared__ float kh[GC * GPAD];
+    __shared__ float qh[GC * GPAD];  // q^ rows, then M (after the dot-product tiles)
+    __shared__ float G[GC], bt[GC], kinv_s[GC], qinv_s[GC];
+    float *mm = qh;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t nch = (a.tokens + a.chunk - 1) / a.chunk;
+    const uint32_t h = blockIdx.x / nch, c = blockIdx.x % nch;
+    const uint32_t t0 = c * a.chunk;
+    const uint32_t n = min(a.chunk, a.tokens - t0);
+    const uint32_t dk = a.key_dim;
+    const float qscale = 1.0f / sqrtf((float)dk);
+
+    // Rows s < n: raw k, q; four threads per row accumulate the squares.
+    {
+        const uint32_t s = tid >> 2, p = tid & 3;
+        float sk = 0.0f, sq = 0.0f;
+        if (s < n) {
+            const float *kr = a.k + ((size_t)(t0 + s) * a.heads + h) * dk;
+            const float *qr = a.q + ((size_t)(t0 + s) * a.heads + h) * dk;
+            for (uint32_t i = p; i < dk; i += 4) {
+                const float kv = kr[i], qv = qr[i];
+                kh[s * GPAD + i] = kv;
+                qh[s * GPAD + i] = qv;
+                sk += kv * kv;
+                sq += qv * qv;
+            }
+        }
+        sk += __shfl_xor(sk, 1);
+        sk += __shfl_xor(sk, 2);
+        sq += __shfl_xor(sq, 1);
+        sq += __shfl_xor(sq, 2);
+        if (p == 0) {
+            kinv_s[s] = s < n ? 1.0f / sqrtf(sk + 1e-6f) : 0.0f;
+            qinv_s[s] = s < n ? 1.0f / sqrtf(sq + 1e-6f) : 0.0f;
+        }
+    }
+    if (tid < GC) {
+        const size_t th = (size_t)(t0 + tid) * a.heads + h;
+        const float ld = tid < n ? a.log_decay[th] : 0.0f;
+        bt[tid] = tid < n ? a.beta[th] : 0.0f;
+        // inclusive prefix sum of log decay over the chunk (one wave)
+        float g = ld;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const float up = __shfl_up(g, o);
+            if (tid >= (uint32_t)o) g += up;
+        }
+        G[tid] = g;
+    }
+    __syncthreads();
+    // Normalise in place (zero rows beyond n and columns beyond dk).
+    for (uint32_t e = tid; e < GC * GKD; e += 256) {
+        const uint32_t s = e / GKD, i = e % GKD;
+        const bool ok = s < n && i < dk;
+        kh[s * GPAD + i] = ok ? kh[s * GPAD + i] * kinv_s[s] : 0.0f;
+        qh[s * GPAD + i] = ok ? qh[s * GPAD + i] * qinv_s[s] * qscale : 0.0f;
+    }
+    __syncthreads();
+    // 4 x 4 tiles of K K^T and Q K^T: rows s = 4*(tid/16)+x, cols r = 4*(tid%16)+y.
+    {
+        const uint32_t sb = (tid >> 4) * 4, rb = (tid & 15) * 4;
+        float kk[4][4] = {}, qk[4][4] = {};
+        for (uint32_t i = 0; i < GKD; i++) {
+            float ks[4], qs[4], kr[4];
+#pragma unroll
+            for (int x = 0; x < 4; x++) {
+                ks[x] = kh[(sb + x) * GPAD + i];
+                qs[x] = qh[(sb + x) * GPAD + i];
+                kr[x] = kh[(rb + x) * GPAD + i];
+            }
+#pragma unroll
+            for (int x = 0; x < 4; x++)
+#pragma unroll
+                for (int y = 0; y < 4; y++) {
+                    kk[x][y] = fmaf(ks[x], kr[y], kk[x][y]);
+                    qk[x][y] = fmaf(qs[x], kr[y], qk[x][y]);
+                }
+        }
+        float *Aout = a.norms + ((size_t)h * ((a.tokens + a.chunk - 1) / a.chunk) + c) * ctox_gdn_chunk_floats() + GC * GC;
+        __syncthreads();  // every tile has read q^: its rows become M
+#pragma unroll
+        for (int x = 0; x < 4; x++)
+#pragma unroll
+            for (int y = 0; y < 4; y++) {
+                const uint32_t s = sb + x, r = rb + y;
+                const float dec = expf(G[s] - G[r]);
+                mm[s * TPAD + r] = r < s ? dec * kk[x][y] : 0.0f;
+                Aout[s * GC + r] = r <= s ? dec * qk[x][y] : 0.0f;
+            }
+    }
+    __syncthreads();
+    float *base = a.norms + ((size_t)h * nch + c) * ctox_gdn_chunk_floats();
+    // T = (I + diag(b) M)^{-1}: thread cc owns column cc; rows in order.
+    if (tid < GC) {
+        const uint32_t cc = tid;
+        float col[GC];
+#pragma unroll
+        for (int s = 0; s < GC; s++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int r = 0; r < s; r++) acc = fmaf(mm[s * TPAD + r], col[r], acc);
+            col[s] = ((uint32_t)s == cc ? 1.0f : 0.0f) - bt[s] * acc;
+            base[s * GC + cc] = col[s];
+        }
+        base[2 * GC * GC + tid] = G[tid];
+        base[2 * GC * GC + GC + tid] = kinv_s[tid];
+        base[2 * GC * GC + 2 * GC + tid] = qinv_s[tid];
+    }
+}
+
+__device__ __forceinline__ gv4f mfma4(float a, float b, gv4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+#define SPAD 132  // LDS row stride (floats) of pass-2 K / Q tiles and of S^T
+#define TSPAD 68  // LDS row stride of pass-2 T / A / Y^T / (b v)^T
+
+// Registers holding the next chunk while the current one computes.
+struct GdnPrefetch {
+    float4 k[8], q[8];   // 64 x 128 each: float4 index tid + 256 m
+    float4 t[4], am[4];  // T, A: 64 x 64 each
+    float4 v;            // 64 x 16 value slice: row tid / 4, part tid % 4
+    float4 aux;          // G / kinv / qinv (threads 0..47), float4 tid % 16 of array tid / 16
+    float beta;          // threads 0..63
+};
+
+// 16 x 16 tile of A[16 x K] * B[K x 16] with both operands stored k-contiguous
+// (A row-major [m][k], B as B^T [n][k]): lane (m = l % 16, kq = l / 16)
+// covers k = kq * (K / 4) + u for MFMA u, so each lane reads a contiguous
+// run of K / 4 floats of both operands.
+template <int K, int LDA, int LDB>
+__device__ __forceinline__ gv4f tile_kk(const float *a, const float *bt, gv4f acc, uint32_t lane) {
+    const uint32_t m = lane & 15, kq = lane >> 4;
+    const float *ap = a + m * LDA + kq * (K / 4);
+    const float *bp = bt + m * LDB + kq * (K / 4);
+    // Four independent accumulation chains, summed at the end.
+    gv4f c1 = {0.0f, 0.0f, 0.0f, 0.0f}, c2 = c1, c3 = c1;
+#pragma unroll
+    for (int u = 0; u < K / 4; u += 4) {
+        const float4 av = *(const float4 *)(ap + u), bv = *(const float4 *)(bp + u);
+        acc = mfma4(av.x, bv.x, acc);
+        c1 = mfma4(av.y, bv.y, c1);
+        c2 = mfma4(av.z, bv.z, c2);
+        c3 = mfma4(av.w, bv.w, c3);
+    }
+    return (acc + c1) + (c2 + c3);
+}
+
+extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_scan_gfx950(GdnArgs a) {
+    // k^ rows [s][i]; (g q^) rows [s][i]; T [s][r]; A [t][r]; S^T [n][i] (x2);
+    // Y^T / D^T [n][s]; (b v)^T [n][s]; D [r][n] for the state update; K~^T [i][r].
+    __shared__ __align__(16) float kh[GC * SPAD];
+    __shared__ __align__(16) float qh[GC * SPAD];
+    __shared__ __align__(16) float tm[GC * TSPAD];
+    __shared__ __align__(16) float am[GC * TSPAD];
+    __shared__ __align__(16) float st[2][GVS * SPAD];
+    __shared__ __align__(16) float yt[GVS * TSPAD];
+    __shared__ __align__(16) float vt[GVS * TSPAD];
+    __shared__ float G[GC], kinv[GC], qinv[GC], bt[GC];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const uint32_t m16 = lane & 15, kq = lane >> 4;
+    const uint32_t slices = (a.value_dim + GVS - 1) / GVS;
+    const uint32_t h = blockIdx.x / slices, j0 = (blockIdx.x % slices) * GVS;
+    const uint32_t nch = (a.tokens + a.chunk - 1) / a.chunk;
+    const uint32_t dk = a.key_dim, dv = a.value_dim;
+    const float qscale = 1.0f / sqrtf((float)dk);
+    const size_t rowq = (size_t)a.heads * dk, rowv = (size_t)a.heads * dv;
+    float *S = a.state + (size_t)h * dk * dv;
+    for (uint32_t e = tid; e < GKD * GVS; e += 256) {
+        const uint32_t i = e / GVS, n = e % GVS;
+        st[0][n * SPAD + i] = (i < dk && j0 + n < dv) ? S[(size_t)i * dv + j0 + n] : 0.0f;
+    }
+    const bool vec_k = (dk & 3) == 0 && (((uintptr_t)a.k | (uintptr_t)a.q) & 15) == 0;
+    const bool vec_v = (dv & 3) == 0 && (j0 + GVS <= dv) && (((uintptr_t)a.v) & 15) == 0;
+
+    auto fetch = [&](GdnPrefetch &p, uint32_t c) {
+        const uint32_t t0 = c * a.chunk, n = min(a.chunk, a.tokens - t0);
+        const float *base = a.norms + ((size_t)h * nch + c) * ctox_gdn_chunk_floats();
+#pragma unroll
+        for (int m = 0; m < 8; m++) {
+            const uint32_t f = tid + 256 * m, s = f >> 5, i = (f & 31) * 4;
+            const bool ok = s < n && i < dk;
+            const size_t off = (size_t)(t0 + (ok ? s : 0)) * rowq + (size_t)h * dk + (ok ? i : 0);
+            if (vec_k) {
+                p.k[m] = ok ? *(const float4 *)(a.k + off) : make_float4(0, 0, 0, 0);
+                p.q[m] = ok ? *(const float4 *)(a.q + off) : make_float4(0, 0, 0, 0);
+            } else {
+                float kk4[4], qq4[4];
+#pragma unroll
+                for (int x = 0; x < 4; x++) {
+                    const bool ox = s < n && i + x < dk;
+                    kk4[x] = ox ? a.k[off + x] : 0.0f;
+                    qq4[x] = ox ? a.q[off + x] : 0.0f;
+                }
+                p.k[m] = make_float4(kk4[0], kk4[1], kk4[2], kk4[3]);
+                p.q[m] = make_float4(qq4[0], qq4[1], qq4[2], qq4[3]);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            p.t[m] = ((const float4 *)base)[tid + 256 * m];
+            p.am[m] = ((const float4 *)(base + GC * GC))[tid + 256 * m];
+        }
+        {
+            const uint32_t s = tid >> 2, part = tid & 3;
+            const bool ok = s < n;
+            const size_t off = (size_t)(t0 + (ok ? s : 0)) * rowv + (size_t)h * dv + j0 + 4 * part;
+            if (vec_v) {
+                p.v = ok ? *(const float4 *)(a.v + off) : make_float4(0, 0, 0, 0);
+            } else {
+                float v4[4];
+#pragma unroll
+                for (int x = 0; x < 4; x++) v4[x] = (ok && j0 + 4 * part + x < dv) ? a.v[off + x] : 0.0f;
+                p.v = make_float4(v4[0], v4[1], v4[2], v4[3]);
+            }
+        }
+        p.aux = tid < 48 ? ((const float4 *)(base + 2 * GC * GC))[tid] : make_float4(0, 0, 0, 0);
+        p.beta = (tid < GC && tid < n) ? a.beta[(size_t)(t0 + tid) * a.heads + h] : 0.0f;
+    };
+
+    GdnPrefetch pf;
+    fetch(pf, 0);
+    uint32_t cur = 0;
+    for (uint32_t c = 0; c < nch; c++) {
+        const uint32_t t0 = c * a.chunk, n = min(a.chunk, a.tokens - t0);
+        __syncthreads();  // the previous chunk is done with every buffer
+        if (tid < 48) ((float4 *)(tid < 16 ? G : (tid < 32 ? kinv : qinv)))[tid & 15] = pf.aux;
+        if (tid < GC) bt[tid] = pf.beta;
+        __syncthreads();
+        // Stage: k^ = k kinv; (g q^) = q qinv qscale exp(G); T; A; (b v)^T.
+#pragma unroll
+        for (int m = 0; m < 8; m++) {
+            const uint32_t f = tid + 256 * m, s = f >> 5, i = (f & 31) * 4;
+            const float ks = kinv[s], qs = qinv[s] * qscale * expf(G[s]);
+            *(float4 *)(kh + s * SPAD + i) = make_float4(pf.k[m].x * ks, pf.k[m].y * ks, pf.k[m].z * ks, pf.k[m].w * ks);
+            *(float4 *)(qh + s * SPAD + i) = make_float4(pf.q[m].x * qs, pf.q[m].y * qs, pf.q[m].z * qs, pf.q[m].w * qs);
+        }
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const uint32_t f = tid + 256 * m, s = f >> 4, r = (f & 15) * 4;
+            *(float4 *)(tm + s * TSPAD + r) = pf.t[m];
+            *(float4 *)(am + s * TSPAD + r) = pf.am[m];
+        }
+        {
+            const uint32_t s = tid >> 2, part = tid & 3;
+            const float b = bt[s];
+            vt[(4 * part + 0) * TSPAD + s] = pf.v.x * b;
+            vt[(4 * part + 1) * TSPAD + s] = pf.v.y * b;
+            vt[(4 * part + 2) * TSPAD + s] = pf.v.z * b;
+            vt[(4 * part + 3) * TSPAD + s] = pf.v.w * b;
+        }
+        __syncthreads();
+        if (c + 1 < nch) fetch(pf, c + 1);  // lands while this chunk computes
+        const float *Sc = st[cur];
+        // Y^T[n][s] = (b v)^T - b_s g_s (K S)[s][n]   (wave w: rows s = 16w..16w+15)
+        {
+            gv4f acc = tile_kk<GKD, SPAD, SPAD>(kh + 16 * w * SPAD, Sc, (gv4f){0, 0, 0, 0}, lane);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t s = 16 * w + 4 * kq + r;
+                yt[m16 * TSPAD + s] = vt[m16 * TSPAD + s] - bt[s] * expf(G[s]) * acc[r];
+            }
+        }
+        __syncthreads();
+        // D = T Y  (T rows [s][r] and Y^T [n][r] are both r-contiguous)
+        gv4f dacc = tile_kk<GC, TSPAD, TSPAD>(tm + 16 * w * TSPAD, yt, (gv4f){0, 0, 0, 0}, lane);
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < 4; r++) yt[m16 * TSPAD + 16 * w + 4 * kq + r] = dacc[r];  // D^T [n][s]
+        __syncthreads();
+        // O = (g Q) S + A D
+        {
+            gv4f acc = tile_kk<GKD, SPAD, SPAD>(qh + 16 * w * SPAD, Sc, (gv4f){0, 0, 0, 0}, lane);
+            acc = tile_kk<GC, TSPAD, TSPAD>(am + 16 * w * TSPAD, yt, acc, lane);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t s = 16 * w + 4 * kq + r, j = j0 + m16;
+                if (s < n && j < dv) a.out[(size_t)(t0 + s) * rowv + (size_t)h * dv + j] = acc[r];
+            }
+        }
+        // S'^T[n][i] = g_C S^T[n][i] + sum_r D^T[n][r] exp(G_C - G_r) k^[r][i]
+        //   as a 16 x 16 tile per (n, i-block): A = D^T [n][r] (r-contiguous),
+        //   B = (K~)[r][i] read column-wise, scaled on the fly.
+        {
+            const float gC = G[GC - 1], decC = expf(gC);
+            float *Sn = st[cur ^ 1];
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+                const uint32_t i0 = 32 * w + 16 * half;
+                gv4f acc;
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[r] = decC * Sc[(4 * kq + r) * SPAD + i0 + m16];
+                const float *ap = yt + m16 * TSPAD + kq * (GC / 4);
+                gv4f c1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int u = 0; u < GC / 4; u += 2) {
+                    const uint32_t rr = kq * (GC / 4) + u;
+                    acc = mfma4(ap[u], kh[rr * SPAD + i0 + m16] * expf(gC - G[rr]), acc);
+                    c1 = mfma4(ap[u + 1], kh[(rr + 1) * SPAD + i0 + m16] * expf(gC - G[rr + 1]), c1);
+                }
+                acc += c1;
+                // acc rows = n (4 kq + r), columns = i0 + m16
+#pragma unroll
+                for (int r = 0; r < 4; r++) Sn[(4 * kq + r) * SPAD + i0 + m16] = acc[r];
+            }
+        }
+        cur ^= 1;
+    }
+    __syncthreads();
+    for (uint32_t e = tid; e < GKD * GVS; e += 256) {
+        const uint32_t i = e / GVS, n = e % GVS;
+        if (i < dk && j0 + n < dv) S[(size_t)i * dv + j0 + n] = st[cur][n * SPAD + i];
+    }
+}

@@ -130,7 +130,7 @@ struct ctox_hip_backend {
     hipStream_t stream = nullptr;
     hipFunction_t prep = nullptr, q4_b1 = nullptr, q4_b4 = nullptr, q4_b8 = nullptr, q2_b1 = nullptr,
                   q2_b4 = nullptr, q2_b8 = nullptr, rec_row = nullptr, row_dot = nullptr, gdn_norms = nullptr,
-                  gdn_scan = nullptr;
+                  gdn_scan = nullptr, gdn_chunk_prep = nullptr, gdn_chunk_scan = nullptr;
     // Batch-1 slice kernels per dtype [Q2, Q4]: [0] walks the slices, [n]
     // requests all n slices up front.
     hipFunction_t sl[2][4] = {};
@@ -408,7 +408,8 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->q4_b8, "ctox_q4_matvec_b8_gfx950"},    {&b->q2_b4, "ctox_q2_matvec_b4_gfx950"},
                {&b->q2_b8, "ctox_q2_matvec_b8_gfx950"},    {&b->rec_row, "ctox_recovered_row_gfx950"},
                {&b->row_dot, "ctox_row_dot_gfx950"},       {&b->gdn_norms, "ctox_gdn_norms_gfx950"},
-               {&b->gdn_scan, "ctox_gdn_scan_gfx950"},
+               {&b->gdn_scan, "ctox_gdn_scan_gfx950"},    {&b->gdn_chunk_prep, "ctox_gdn_chunk_prep_gfx950"},
+               {&b->gdn_chunk_scan, "ctox_gdn_chunk_scan_gfx950"},
                {&b->sl[0][0], "ctox_q2_matvec_sl_gfx950"}, {&b->sl[0][1], "ctox_q2_matvec_sl1_gfx950"},
                {&b->sl[0][2], "ctox_q2_matvec_sl2_gfx950"}, {&b->sl[0][3], "ctox_q2_matvec_sl3_gfx950"},
                {&b->sl[1][0], "ctox_q4_matvec_sl_gfx950"}, {&b->sl[1][1], "ctox_q4_matvec_sl1_gfx950"},
@@ -728,8 +729,12 @@ ctox_status gdn_device(ctox_hip_backend *b, const float *q, const float *k, cons
                        size_t chunk, float *out, hipStream_t s) {
     ctox_status st = gdn_shape(tokens, heads, kd, vd);
     if (st) return st;
-    (void)chunk;  // chunk selects the prefill algorithm; both paths compute the same recurrence
-    st = ensure(b, b->norms, tokens * heads * 2 * sizeof(float), false);
+    // chunk >= 1 selects the chunked (WY) prefill for key/value dims up to
+    // 128 and chunks up to 64 tokens; otherwise the token-serial scan.
+    const bool chunked = tokens > 1 && chunk >= 1 && chunk <= 64 && kd <= 128 && vd <= 128;
+    const size_t nch = chunked ? (tokens + chunk - 1) / chunk : 0;
+    const size_t scratch = chunked ? heads * nch * (2 * 64 * 64 + 3 * 64) : tokens * heads * 2;
+    st = ensure(b, b->norms, scratch * sizeof(float), false);
     if (st) return st;
     GdnArgs a{};
     a.q = q;
@@ -745,9 +750,15 @@ ctox_status gdn_device(ctox_hip_backend *b, const float *q, const float *k, cons
     a.key_dim = (uint32_t)kd;
     a.value_dim = (uint32_t)vd;
     a.chunk = (uint32_t)chunk;
+    const size_t slices = (vd + 15) / 16;
+    if (chunked) {
+        st = launch(b->gdn_chunk_prep, dim3((unsigned)(heads * nch)), dim3(256), s, a, "ctox_gdn_chunk_prep_gfx950");
+        if (st) return st;
+        return launch(b->gdn_chunk_scan, dim3((unsigned)(heads * slices)), dim3(256), s, a,
+                      "ctox_gdn_chunk_scan_gfx950");
+    }
     st = launch(b->gdn_norms, dim3((unsigned)(tokens * heads)), dim3(64), s, a, "ctox_gdn_norms_gfx950");
     if (st) return st;
-    const size_t slices = (vd + 15) / 16;
     return launch(b->gdn_scan, dim3((unsigned)(heads * slices)), dim3(256), s, a, "ctox_gdn_scan_gfx950");
 }
 

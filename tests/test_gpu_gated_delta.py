@@ -87,6 +87,34 @@ def test_sequence_vs_oracle(hip, orc, chunk):
     close(st_gpu, st_ref, 1e-4, "state")
 
 
+@pytest.mark.parametrize("case", [(150, 2, 96, 40, 64), (150, 3, 128, 128, 16), (70, 1, 5, 7, 1),
+                                  (64, 4, 128, 128, 64), (65, 2, 128, 128, 64), (33, 2, 64, 128, 7)])
+def test_chunked_prefill_ragged(hip, orc, case):
+    """Chunked (WY) path: partial last chunks, chunk lengths 1..64, dims below 128."""
+    T, heads, dk, dv, chunk = case
+    say(f"case gdn chunked {case}")
+    q, k, v, ld, be = gdn_inputs(T, heads, heads, dk, dv, T + dk)
+    st_ref = (np.random.default_rng(T).standard_normal(heads * dk * dv) * 0.1).astype(np.float32)
+    st_gpu = st_ref.copy()
+    ref = orc.gated_delta_sequence(q, k, v, ld, be, st_ref, T, heads, dk, dv)
+    got = hip.gated_delta_sequence(q, k, v, ld, be, st_gpu, T, heads, dk, dv, chunk)
+    close(got, ref, 1e-3, "output")
+    close(st_gpu, st_ref, 1e-4, "state")
+
+
+def test_chunked_prefill_long(hip, orc):
+    """1024 tokens of BASELINE config 4 shapes through the chunk-64 path."""
+    say("case gdn chunked long")
+    heads, dk, dv, T = 32, 128, 128, 1024
+    q, k, v, ld, be = gdn_inputs(T, heads, 16, dk, dv, 11)
+    st_ref = np.zeros(heads * dk * dv, np.float32)
+    st_gpu = st_ref.copy()
+    ref = orc.gated_delta_sequence(q, k, v, ld, be, st_ref, T, heads, dk, dv)
+    got = hip.gated_delta_sequence(q, k, v, ld, be, st_gpu, T, heads, dk, dv, 64)
+    close(got, ref, 1e-3, "output")
+    close(st_gpu, st_ref, 1e-4, "state")
+
+
 @pytest.mark.parametrize("dims", [(3, 5, 7), (2, 64, 96), (4, 256, 128), (1, 1, 1)])
 def test_ragged_dims(hip, orc, dims):
     heads, dk, dv = dims
