@@ -14,8 +14,7 @@
 // keeps rows i = ig + 16r of column jj in registers, so one token reads and
 // writes each state element exactly once; the token-serial scan keeps the
 // slice register-resident across all tokens. Column reductions over i go
-// through LDS. Products are evaluated in the oracle's order
-// ((S*k)*k_inv, (k*k_inv)*delta, ((S*q)*q_inv)*scale).
+// through LDS.
 #include <hip/hip_runtime.h>
 
 #include "kernel_args.h"
@@ -24,32 +23,14 @@
 #define GDN_GROUPS 16
 #define GDN_MAX_ROWS 16  // key_dim <= 256
 
-// Per-(token, head) inverse L2 norms of q and k (one wave per pair).
-extern "C" __global__ __launch_bounds__(64) void ctox_gdn_norms_gfx950(GdnArgs a) {
-    const uint32_t th = blockIdx.x;  // token * heads + head
-    const float *q = a.q + (size_t)th * a.key_dim;
-    const float *k = a.k + (size_t)th * a.key_dim;
-    float sq = 0.0f, sk = 0.0f;
-    for (uint32_t i = threadIdx.x; i < a.key_dim; i += 64) {
-        sq += q[i] * q[i];
-        sk += k[i] * k[i];
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        sq += __shfl_xor(sq, o);
-        sk += __shfl_xor(sk, o);
-    }
-    if (threadIdx.x == 0) {
-        a.norms[(size_t)th * 2 + 0] = 1.0f / sqrtf(sq + 1e-6f);
-        a.norms[(size_t)th * 2 + 1] = 1.0f / sqrtf(sk + 1e-6f);
-    }
-}
-
 // Token-serial scan over a.tokens tokens (tokens = 1 is the decode step).
-// grid = heads * ceil(value_dim / 16), block = 256.
+// grid = heads * ceil(value_dim / 16), block = 256. The inverse norms of q and
+// k are reduced in the same pass as k.S (no separate norms launch):
+// mem_j = (sum_i S'[i,j] k_i) * k_inv and o_j = (sum_i S''[i,j] q_i) * q_inv / sqrt(key_dim).
 extern "C" __global__ __launch_bounds__(256) void ctox_gdn_scan_gfx950(GdnArgs a) {
     __shared__ float red_mem[GDN_GROUPS][GDN_COLS];
     __shared__ float red_out[GDN_GROUPS][GDN_COLS];
+    __shared__ float red_nrm[2][GDN_GROUPS];
 
     const uint32_t slices = (a.value_dim + GDN_COLS - 1) / GDN_COLS;
     const uint32_t h = blockIdx.x / slices, slice = blockIdx.x % slices;
@@ -71,33 +52,43 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_scan_gfx950(GdnArgs a
         const size_t th = (size_t)t * a.heads + h;
         const float *q = a.q + th * a.key_dim;
         const float *k = a.k + th * a.key_dim;
-        const float qinv = a.norms[th * 2 + 0], kinv = a.norms[th * 2 + 1];
         const float decay = expf(a.log_decay[th]);
         const float beta = a.beta[th];
         const float vj = colok ? a.v[th * a.value_dim + j] : 0.0f;
 
         float kk[GDN_MAX_ROWS], qq[GDN_MAX_ROWS];
-        float mem = 0.0f;
+        float mem = 0.0f, sk = 0.0f, sq = 0.0f;
 #pragma unroll
         for (int r = 0; r < GDN_MAX_ROWS; r++) {
             const uint32_t i = ig + GDN_GROUPS * r;
             const bool ok = (uint32_t)r < nrows && i < a.key_dim;
             kk[r] = ok ? k[i] : 0.0f;
             qq[r] = ok ? q[i] : 0.0f;
+            sk += kk[r] * kk[r];
+            sq += qq[r] * qq[r];
             s[r] = s[r] * decay;
-            mem += s[r] * kk[r] * kinv;
+            mem += s[r] * kk[r];
         }
         red_mem[ig][jj] = mem;
+        if (jj == 0) {
+            red_nrm[0][ig] = sk;
+            red_nrm[1][ig] = sq;
+        }
         __syncthreads();
-        float memj = 0.0f;
+        float memj = 0.0f, ssk = 0.0f, ssq = 0.0f;
 #pragma unroll
-        for (int gi = 0; gi < GDN_GROUPS; gi++) memj += red_mem[gi][jj];
-        const float delta = (vj - memj) * beta;
+        for (int gi = 0; gi < GDN_GROUPS; gi++) {
+            memj += red_mem[gi][jj];
+            ssk += red_nrm[0][gi];
+            ssq += red_nrm[1][gi];
+        }
+        const float kinv = 1.0f / sqrtf(ssk + 1e-6f), qinv = 1.0f / sqrtf(ssq + 1e-6f);
+        const float delta = (vj - memj * kinv) * beta;
         float o = 0.0f;
 #pragma unroll
         for (int r = 0; r < GDN_MAX_ROWS; r++) {
             s[r] += kk[r] * kinv * delta;
-            o += s[r] * qq[r] * qinv * qscale;
+            o += s[r] * qq[r];
         }
         red_out[ig][jj] = o;
         __syncthreads();
@@ -105,10 +96,10 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_scan_gfx950(GdnArgs a
             float oj = 0.0f;
 #pragma unroll
             for (int gi = 0; gi < GDN_GROUPS; gi++) oj += red_out[gi][jj];
-            a.out[th * a.value_dim + j] = oj;
+            a.out[th * a.value_dim + j] = oj * qinv * qscale;
         }
-        // red_mem / red_out are rewritten next token only after every thread
-        // has passed the second barrier of this token and read red_mem; the
+        // red_* are rewritten next token only after every thread has passed
+        // the second barrier of this token and read red_mem / red_nrm; the
         // reads of red_out happen before the next token's first barrier.
         __syncthreads();
     }

@@ -200,11 +200,17 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_scan_gfx950(Gdn
     __shared__ __align__(16) float st[2][GVS * SPAD];
     __shared__ __align__(16) float yt[GVS * TSPAD];
     __shared__ __align__(16) float vt[GVS * TSPAD];
-    __shared__ float G[GC], kinv[GC], qinv[GC], bt[GC];
+    __shared__ float G[GC], kinv[GC], qinv[GC], bt[GC], eg[GC], ec[GC];
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const uint32_t m16 = lane & 15, kq = lane >> 4;
     const uint32_t slices = (a.value_dim + GVS - 1) / GVS;
-    const uint32_t h = blockIdx.x / slices, j0 = (blockIdx.x % slices) * GVS;
+    // Workgroup b runs on XCD b % 8. All slices of one head are placed on the
+    // same XCD so that they share the chunk's k, q, T and A in that XCD's L2:
+    // XCD x takes heads x, x + 8, ..., its q-th workgroup being slice q % slices
+    // of head x + 8 (q / slices). The grid is 8 * ceil(heads / 8) * slices.
+    const uint32_t xcd = blockIdx.x & 7, qx = blockIdx.x >> 3;
+    const uint32_t h = xcd + 8 * (qx / slices), j0 = (qx % slices) * GVS;
+    if (h >= a.heads) return;
     const uint32_t nch = (a.tokens + a.chunk - 1) / a.chunk;
     const uint32_t dk = a.key_dim, dv = a.value_dim;
     const float qscale = 1.0f / sqrtf((float)dk);
@@ -271,11 +277,16 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_scan_gfx950(Gdn
         if (tid < 48) ((float4 *)(tid < 16 ? G : (tid < 32 ? kinv : qinv)))[tid & 15] = pf.aux;
         if (tid < GC) bt[tid] = pf.beta;
         __syncthreads();
+        if (tid < GC) {
+            eg[tid] = expf(G[tid]);               // g_s
+            ec[tid] = expf(G[GC - 1] - G[tid]);   // g_C / g_r
+        }
+        __syncthreads();
         // Stage: k^ = k kinv; (g q^) = q qinv qscale exp(G); T; A; (b v)^T.
 #pragma unroll
         for (int m = 0; m < 8; m++) {
             const uint32_t f = tid + 256 * m, s = f >> 5, i = (f & 31) * 4;
-            const float ks = kinv[s], qs = qinv[s] * qscale * expf(G[s]);
+            const float ks = kinv[s], qs = qinv[s] * qscale * eg[s];
             *(float4 *)(kh + s * SPAD + i) = make_float4(pf.k[m].x * ks, pf.k[m].y * ks, pf.k[m].z * ks, pf.k[m].w * ks);
             *(float4 *)(qh + s * SPAD + i) = make_float4(pf.q[m].x * qs, pf.q[m].y * qs, pf.q[m].z * qs, pf.q[m].w * qs);
         }
@@ -302,7 +313,7 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_scan_gfx950(Gdn
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const uint32_t s = 16 * w + 4 * kq + r;
-                yt[m16 * TSPAD + s] = vt[m16 * TSPAD + s] - bt[s] * expf(G[s]) * acc[r];
+                yt[m16 * TSPAD + s] = vt[m16 * TSPAD + s] - bt[s] * eg[s] * acc[r];
             }
         }
         __syncthreads();
@@ -339,8 +350,8 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_scan_gfx950(Gdn
 #pragma unroll
                 for (int u = 0; u < GC / 4; u += 2) {
                     const uint32_t rr = kq * (GC / 4) + u;
-                    acc = mfma4(ap[u], kh[rr * SPAD + i0 + m16] * expf(gC - G[rr]), acc);
-                    c1 = mfma4(ap[u + 1], kh[(rr + 1) * SPAD + i0 + m16] * expf(gC - G[rr + 1]), c1);
+                    acc = mfma4(ap[u], kh[rr * SPAD + i0 + m16] * ec[rr], acc);
+                    c1 = mfma4(ap[u + 1], kh[(rr + 1) * SPAD + i0 + m16] * ec[rr + 1], c1);
                 }
                 acc += c1;
                 // acc rows = n (4 kq + r), columns = i0 + m16

@@ -92,7 +92,7 @@ struct GdnArgs {
     const float *beta;      // [tokens][heads]
     float *state;
     float *out;             // [tokens][heads][value_dim]
-    float *norms;           // [tokens][heads][2] {q_inv, k_inv} scratch (scan)
+    float *norms;           // chunked prefill scratch: per (head, chunk) T, A, G, k_inv, q_inv
     uint32_t tokens;
     uint32_t heads;
     uint32_t key_dim;

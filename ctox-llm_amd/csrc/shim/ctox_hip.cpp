@@ -129,7 +129,7 @@ struct ctox_hip_backend {
     hipModule_t module = nullptr;
     hipStream_t stream = nullptr;
     hipFunction_t prep = nullptr, q4_b1 = nullptr, q4_b4 = nullptr, q4_b8 = nullptr, q2_b1 = nullptr,
-                  q2_b4 = nullptr, q2_b8 = nullptr, rec_row = nullptr, row_dot = nullptr, gdn_norms = nullptr,
+                  q2_b4 = nullptr, q2_b8 = nullptr, rec_row = nullptr, row_dot = nullptr,
                   gdn_scan = nullptr, gdn_chunk_prep = nullptr, gdn_chunk_scan = nullptr;
     // Batch-1 slice kernels per dtype [Q2, Q4]: [0] walks the slices, [n]
     // requests all n slices up front.
@@ -407,7 +407,7 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->q2_b1, "ctox_q2_matvec_b1_gfx950"},    {&b->q4_b4, "ctox_q4_matvec_b4_gfx950"},
                {&b->q4_b8, "ctox_q4_matvec_b8_gfx950"},    {&b->q2_b4, "ctox_q2_matvec_b4_gfx950"},
                {&b->q2_b8, "ctox_q2_matvec_b8_gfx950"},    {&b->rec_row, "ctox_recovered_row_gfx950"},
-               {&b->row_dot, "ctox_row_dot_gfx950"},       {&b->gdn_norms, "ctox_gdn_norms_gfx950"},
+               {&b->row_dot, "ctox_row_dot_gfx950"},
                {&b->gdn_scan, "ctox_gdn_scan_gfx950"},    {&b->gdn_chunk_prep, "ctox_gdn_chunk_prep_gfx950"},
                {&b->gdn_chunk_scan, "ctox_gdn_chunk_scan_gfx950"},
                {&b->sl[0][0], "ctox_q2_matvec_sl_gfx950"}, {&b->sl[0][1], "ctox_q2_matvec_sl1_gfx950"},
@@ -733,7 +733,7 @@ ctox_status gdn_device(ctox_hip_backend *b, const float *q, const float *k, cons
     // 128 and chunks up to 64 tokens; otherwise the token-serial scan.
     const bool chunked = tokens > 1 && chunk >= 1 && chunk <= 64 && kd <= 128 && vd <= 128;
     const size_t nch = chunked ? (tokens + chunk - 1) / chunk : 0;
-    const size_t scratch = chunked ? heads * nch * (2 * 64 * 64 + 3 * 64) : tokens * heads * 2;
+    const size_t scratch = chunked ? heads * nch * (2 * 64 * 64 + 3 * 64) : 1;
     st = ensure(b, b->norms, scratch * sizeof(float), false);
     if (st) return st;
     GdnArgs a{};
@@ -754,11 +754,11 @@ ctox_status gdn_device(ctox_hip_backend *b, const float *q, const float *k, cons
     if (chunked) {
         st = launch(b->gdn_chunk_prep, dim3((unsigned)(heads * nch)), dim3(256), s, a, "ctox_gdn_chunk_prep_gfx950");
         if (st) return st;
-        return launch(b->gdn_chunk_scan, dim3((unsigned)(heads * slices)), dim3(256), s, a,
+        // 8 * ceil(heads / 8) * slices workgroups: the kernel maps them so
+        // that all slices of a head run on one XCD (surplus ones exit).
+        return launch(b->gdn_chunk_scan, dim3((unsigned)(8 * ((heads + 7) / 8) * slices)), dim3(256), s, a,
                       "ctox_gdn_chunk_scan_gfx950");
     }
-    st = launch(b->gdn_norms, dim3((unsigned)(tokens * heads)), dim3(64), s, a, "ctox_gdn_norms_gfx950");
-    if (st) return st;
     return launch(b->gdn_scan, dim3((unsigned)(heads * slices)), dim3(256), s, a, "ctox_gdn_scan_gfx950");
 }
 
