@@ -183,6 +183,32 @@ def bench_gdn(torch, hip, steps):
     return out
 
 
+def bench_token_selection(torch, hip, steps):
+    """Config 5's per-step token selection: k = 4 drafts, vocab 151936, greedy
+    verification and the T = 0.7 rejection-sampling accept."""
+    K, V = 4, 151936
+    g = torch.Generator(device="cuda").manual_seed(5)
+    target = torch.randn(K, V, device="cuda", generator=g) * 2.5
+    draft = target + torch.randn(K, V, device="cuda", generator=g)
+    bonus = torch.randn(V, device="cuda", generator=g) * 2.5
+    toks = torch.argmax(draft, dim=1).to(torch.int32)
+    rng = torch.tensor([12345], dtype=torch.int64, device="cuda")
+    out = torch.zeros(3 + K, dtype=torch.int32, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    res = {}
+    for name, fn in (("verify_greedy_k4", lambda: hip.verify_greedy_mtp_device(
+                          draft.data_ptr(), target.data_ptr(), bonus.data_ptr(), K, V, out.data_ptr(), s)),
+                     ("mtp_accept_t0.7_k4", lambda: hip.mtp_accept_device(
+                          draft.data_ptr(), target.data_ptr(), bonus.data_ptr(), toks.data_ptr(), K, V, 0.7,
+                          rng.data_ptr(), out.data_ptr(), s))):
+        fn()
+        with Timer(torch) as t:
+            for _ in range(steps):
+                fn()
+        res[name] = {"us": t.ms * 1e3 / steps, "vocab": V, "drafts": K}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -223,6 +249,8 @@ def main():
             log("config3", batch, extra[f"config3_verify_layer_M{batch}"])
         extra["config4_gated_delta"] = bench_gdn(torch, hip, args.steps)
         log("config4", extra["config4_gated_delta"])
+        extra["config5_token_selection"] = bench_token_selection(torch, hip, args.steps)
+        log("config5", extra["config5_token_selection"])
 
     extra["copy_reference"] = copy_reference(torch)
     log("copy", extra["copy_reference"])

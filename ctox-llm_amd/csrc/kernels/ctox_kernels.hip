@@ -3,3 +3,4 @@
 #include "qmatvec_slices.hip"
 #include "gated_delta.hip"
 #include "gated_delta_chunk.hip"
+#include "decode_ops.hip"

@@ -100,3 +100,76 @@ struct GdnArgs {
     uint32_t chunk;
     uint32_t pad;
 };
+
+// Decode-step glue and token selection (decode_ops.hip).
+struct GateArgs {
+    const float *a;          // [tokens][heads]
+    const float *b;          // [tokens][heads]
+    const float *a_log;      // [heads]
+    const float *dt_bias;    // [heads]
+    float *log_decay;        // [tokens][heads]
+    float *beta;             // [tokens][heads]
+    uint32_t tokens;
+    uint32_t heads;
+};
+
+struct RepeatArgs {
+    const float *in;         // [rows][heads][dim]
+    float *out;              // [rows][heads * repeats][dim]
+    uint32_t rows;
+    uint32_t heads;
+    uint32_t dim;
+    uint32_t repeats;
+};
+
+// Per-(row, part) partial reductions over 2 * drafts + 1 logits rows:
+// rows [0, drafts) from `draft`, [drafts, 2 drafts) from `target`, row
+// 2 drafts is `bonus`. mode 0: {total-order key, index} of the maximum;
+// mode 1: {max(x / T), sum exp(x / T - max)}.
+struct PartialArgs {
+    const float *draft;
+    const float *target;
+    const float *bonus;
+    float *out;              // [rows][parts][2] (mode 0: key and index bit patterns)
+    uint32_t drafts;
+    uint32_t vocab;
+    uint32_t parts;
+    uint32_t mode;
+    float temperature;
+    uint32_t pad;
+};
+
+// Token-selection decision state shared by the accept kernels.
+struct PickState {
+    float thr_draw;          // the draw u of the cumulative search
+    float m_t, z_t;          // softmax stats of the weight row (target or bonus)
+    float m_d, z_d;          // draft row stats (residual mode)
+    uint32_t row;            // draft index of the rejection (residual) or drafts (bonus)
+    uint32_t accepted;
+    uint32_t mode;           // 0 residual max(0, p - q), 1 bonus softmax, 2 invalid token
+};
+
+struct VerifyArgs {
+    const float *partials;   // PartialArgs mode 0 output
+    uint32_t *out;           // [3 + drafts]: next, verified, accepted count, accepted tokens
+    uint32_t drafts;
+    uint32_t parts;
+};
+
+struct AcceptArgs {
+    const float *draft;      // [drafts][vocab]
+    const float *target;     // [drafts][vocab]
+    const float *bonus;      // [vocab]
+    const uint32_t *tokens;  // [drafts] proposed draft tokens
+    const float *partials;   // PartialArgs mode 1 output
+    float *sums;             // [parts2] per-part weight sums
+    PickState *state;
+    uint64_t *rng;           // Pcg32 state, advanced in place
+    uint32_t *out;           // [2]: next token, accepted count
+    uint32_t drafts;
+    uint32_t vocab;
+    uint32_t parts;          // partials per row
+    uint32_t parts2;         // parts of the cumulative search
+    float temperature;
+    uint32_t pad;
+};

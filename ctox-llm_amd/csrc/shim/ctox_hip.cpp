@@ -16,6 +16,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -130,13 +131,17 @@ struct ctox_hip_backend {
     hipStream_t stream = nullptr;
     hipFunction_t prep = nullptr, q4_b1 = nullptr, q4_b4 = nullptr, q4_b8 = nullptr, q2_b1 = nullptr,
                   q2_b4 = nullptr, q2_b8 = nullptr, rec_row = nullptr, row_dot = nullptr,
-                  gdn_scan = nullptr, gdn_chunk_prep = nullptr, gdn_chunk_scan = nullptr;
+                  gdn_scan = nullptr, gdn_chunk_prep = nullptr, gdn_chunk_scan = nullptr, gates = nullptr,
+                  repeat = nullptr, partials = nullptr, argmax_final = nullptr, verify = nullptr, decide = nullptr,
+                  pick_sums = nullptr, pick_final = nullptr;
     // Batch-1 slice kernels per dtype [Q2, Q4]: [0] walks the slices, [n]
     // requests all n slices up front.
     hipFunction_t sl[2][4] = {};
     int cus = 0;
     // Activation staging (two layouts: [0] Q2, [1] Q4) and gated-delta norms.
     DevBuf xa[2], xc[2], norms;
+    // Token selection scratch: per-part partials, pick sums and state.
+    DevBuf tok, stats;
 };
 
 struct ctox_hip_matrix {
@@ -409,7 +414,11 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->q2_b8, "ctox_q2_matvec_b8_gfx950"},    {&b->rec_row, "ctox_recovered_row_gfx950"},
                {&b->row_dot, "ctox_row_dot_gfx950"},
                {&b->gdn_scan, "ctox_gdn_scan_gfx950"},    {&b->gdn_chunk_prep, "ctox_gdn_chunk_prep_gfx950"},
-               {&b->gdn_chunk_scan, "ctox_gdn_chunk_scan_gfx950"},
+               {&b->gdn_chunk_scan, "ctox_gdn_chunk_scan_gfx950"}, {&b->gates, "ctox_gdn_gates_gfx950"},
+               {&b->repeat, "ctox_repeat_heads_gfx950"},   {&b->partials, "ctox_row_partials_gfx950"},
+               {&b->argmax_final, "ctox_argmax_final_gfx950"}, {&b->verify, "ctox_verify_greedy_gfx950"},
+               {&b->decide, "ctox_mtp_decide_gfx950"},     {&b->pick_sums, "ctox_pick_sums_gfx950"},
+               {&b->pick_final, "ctox_pick_final_gfx950"},
                {&b->sl[0][0], "ctox_q2_matvec_sl_gfx950"}, {&b->sl[0][1], "ctox_q2_matvec_sl1_gfx950"},
                {&b->sl[0][2], "ctox_q2_matvec_sl2_gfx950"}, {&b->sl[0][3], "ctox_q2_matvec_sl3_gfx950"},
                {&b->sl[1][0], "ctox_q4_matvec_sl_gfx950"}, {&b->sl[1][1], "ctox_q4_matvec_sl1_gfx950"},
@@ -436,7 +445,7 @@ extern "C" void ctox_hip_backend_destroy(ctox_hip_backend *b) {
     if (!b) return;
     (void)hipSetDevice(b->device);
     (void)hipDeviceSynchronize();
-    DevBuf *bufs[] = {&b->xa[0], &b->xa[1], &b->xc[0], &b->xc[1], &b->norms};
+    DevBuf *bufs[] = {&b->xa[0], &b->xa[1], &b->xc[0], &b->xc[1], &b->norms, &b->tok, &b->stats};
     for (DevBuf *d : bufs)
         if (d->ptr) (void)hipFree(d->ptr);
     if (b->stream) (void)hipStreamDestroy(b->stream);
@@ -845,4 +854,101 @@ extern "C" ctox_status ctox_hip_gated_delta_sequence_device(ctox_hip_backend *b,
     if (!b || !q || !k || !v || !log_decay || !beta || !state || !out) return fail(CTOX_ERR_SHAPE, "null argument");
     return gdn_device(b, q, k, v, log_decay, beta, state, tokens, heads, key_dim, value_dim, chunk, out,
                       pick_stream(b, stream));
+}
+
+// ======================================================================
+// decode-step glue and token selection
+// ======================================================================
+namespace {
+constexpr size_t kMaxDrafts = 64;
+}
+
+extern "C" ctox_status ctox_hip_gdn_gates_device(ctox_hip_backend *b, const float *d_a, const float *d_b,
+                                                 const float *d_a_log, const float *d_dt_bias, size_t tokens,
+                                                 size_t heads, float *d_log_decay, float *d_beta, void *stream) {
+    if (!b || !d_a || !d_b || !d_a_log || !d_dt_bias || !d_log_decay || !d_beta)
+        return fail(CTOX_ERR_SHAPE, "null argument");
+    if (tokens == 0 || heads == 0 || tokens * heads > 0x7fffffffu) return fail(CTOX_ERR_SHAPE, "gate shapes");
+    GateArgs a{d_a, d_b, d_a_log, d_dt_bias, d_log_decay, d_beta, (uint32_t)tokens, (uint32_t)heads};
+    return launch(b->gates, dim3((unsigned)((tokens * heads + 255) / 256)), dim3(256), pick_stream(b, stream), a,
+                  "ctox_gdn_gates_gfx950");
+}
+
+extern "C" ctox_status ctox_hip_repeat_heads_device(ctox_hip_backend *b, const float *d_in, size_t rows,
+                                                    size_t heads, size_t dim, size_t repeats, float *d_out,
+                                                    void *stream) {
+    if (!b || !d_in || !d_out) return fail(CTOX_ERR_SHAPE, "null argument");
+    // Q/src/decoder.rs:47-65 rejects empty shapes.
+    if (rows == 0 || heads == 0 || dim == 0 || repeats == 0) return fail(CTOX_ERR_SHAPE, "repeat_heads shapes must be non-zero");
+    const size_t n = rows * heads * repeats * dim;
+    if (n / repeats != rows * heads * dim || (n + 255) / 256 > 0x7fffffffu) return fail(CTOX_ERR_SHAPE, "repeat_heads too large");
+    RepeatArgs a{d_in, d_out, (uint32_t)rows, (uint32_t)heads, (uint32_t)dim, (uint32_t)repeats};
+    return launch(b->repeat, dim3((unsigned)((n + 255) / 256)), dim3(256), pick_stream(b, stream), a,
+                  "ctox_repeat_heads_gfx950");
+}
+
+namespace {
+// Parts per vocabulary row for the partial reductions: ~2.4k logits each.
+uint32_t row_parts(size_t vocab) { return (uint32_t)std::min<size_t>(64, std::max<size_t>(1, vocab / 2048)); }
+}
+
+extern "C" ctox_status ctox_hip_greedy_tokens_device(ctox_hip_backend *b, const float *d_logits, size_t rows,
+                                                     size_t vocab, uint32_t *d_tokens, void *stream) {
+    if (!b || !d_logits || !d_tokens) return fail(CTOX_ERR_SHAPE, "null argument");
+    if (vocab == 0) return fail(CTOX_ERR_INVALID_ARTIFACT, "cannot select a token from empty logits");
+    if (rows == 0 || rows > 65535 || vocab > 0xffffffffu) return fail(CTOX_ERR_SHAPE, "logits shape");
+    hipStream_t s = pick_stream(b, stream);
+    const uint32_t parts = row_parts(vocab);
+    ctox_status st = ensure(b, b->tok, rows * parts * 2 * sizeof(float), false);
+    if (st) return st;
+    PartialArgs p{d_logits, d_logits, d_logits, (float *)b->tok.ptr, (uint32_t)rows, (uint32_t)vocab, parts, 0, 1.0f, 0};
+    if ((st = launch(b->partials, dim3((unsigned)rows, parts), dim3(256), s, p, "ctox_row_partials_gfx950"))) return st;
+    VerifyArgs v{(const float *)b->tok.ptr, d_tokens, (uint32_t)rows, parts};
+    return launch(b->argmax_final, dim3((unsigned)rows), dim3(64), s, v, "ctox_argmax_final_gfx950");
+}
+
+extern "C" ctox_status ctox_hip_verify_greedy_mtp_device(ctox_hip_backend *b, const float *d_draft,
+                                                         const float *d_target, const float *d_bonus, size_t drafts,
+                                                         size_t vocab, uint32_t *d_out, void *stream) {
+    if (!b || !d_draft || !d_target || !d_bonus || !d_out) return fail(CTOX_ERR_SHAPE, "null argument");
+    if (vocab == 0) return fail(CTOX_ERR_INVALID_ARTIFACT, "cannot select a token from empty logits");
+    if (drafts == 0 || drafts > kMaxDrafts || vocab > 0xffffffffu) return fail(CTOX_ERR_SHAPE, "drafts outside 1..64");
+    hipStream_t s = pick_stream(b, stream);
+    const uint32_t parts = row_parts(vocab);
+    const size_t rows = 2 * drafts + 1;
+    ctox_status st = ensure(b, b->tok, rows * parts * 2 * sizeof(float), false);
+    if (st) return st;
+    PartialArgs p{d_draft, d_target, d_bonus, (float *)b->tok.ptr, (uint32_t)drafts, (uint32_t)vocab, parts, 0, 1.0f, 0};
+    if ((st = launch(b->partials, dim3((unsigned)rows, parts), dim3(256), s, p, "ctox_row_partials_gfx950"))) return st;
+    VerifyArgs v{(const float *)b->tok.ptr, d_out, (uint32_t)drafts, parts};
+    return launch(b->verify, dim3(1), dim3(64), s, v, "ctox_verify_greedy_gfx950");
+}
+
+extern "C" ctox_status ctox_hip_mtp_accept_device(ctox_hip_backend *b, const float *d_draft, const float *d_target,
+                                                  const float *d_bonus, const uint32_t *d_tokens, size_t drafts,
+                                                  size_t vocab, float temperature, uint64_t *d_rng, uint32_t *d_out,
+                                                  void *stream) {
+    if (!b || !d_draft || !d_target || !d_bonus || !d_tokens || !d_rng || !d_out)
+        return fail(CTOX_ERR_SHAPE, "null argument");
+    if (!(temperature > 0.0f) || !std::isfinite(temperature) || !std::isfinite(1.0f / temperature))
+        return fail(CTOX_ERR_INVALID_ARTIFACT, "sampling temperature must be finite and positive");
+    if (vocab == 0) return fail(CTOX_ERR_INVALID_ARTIFACT, "cannot sample from empty logits");
+    // The final search scans one part per pass with 1024 threads.
+    if (drafts > kMaxDrafts || vocab > (size_t)1024 * 1024) return fail(CTOX_ERR_SHAPE, "drafts outside 0..64 or vocab above 2^20");
+    hipStream_t s = pick_stream(b, stream);
+    const uint32_t parts = row_parts(vocab);
+    const uint32_t parts2 = (uint32_t)std::max<size_t>(256, (vocab + 1023) / 1024);
+    const size_t rows = 2 * drafts + 1;
+    const size_t state_off = ((rows * parts * 2 + parts2) * sizeof(float) + 255) & ~(size_t)255;
+    ctox_status st = ensure(b, b->stats, state_off + sizeof(PickState), false);
+    if (st) return st;
+    float *partials = (float *)b->stats.ptr;
+    AcceptArgs a{d_draft, d_target, d_bonus, d_tokens, partials, partials + rows * parts * 2,
+                 (PickState *)((char *)b->stats.ptr + state_off), d_rng, d_out, (uint32_t)drafts, (uint32_t)vocab,
+                 parts, parts2, temperature, 0};
+    PartialArgs p{d_draft, d_target, d_bonus, partials, (uint32_t)drafts, (uint32_t)vocab, parts, 1, temperature, 0};
+    if ((st = launch(b->partials, dim3((unsigned)rows, parts), dim3(256), s, p, "ctox_row_partials_gfx950"))) return st;
+    if ((st = launch(b->decide, dim3(1), dim3(64), s, a, "ctox_mtp_decide_gfx950"))) return st;
+    if ((st = launch(b->pick_sums, dim3(parts2), dim3(256), s, a, "ctox_pick_sums_gfx950"))) return st;
+    return launch(b->pick_final, dim3(1), dim3(1024), s, a, "ctox_pick_final_gfx950");
 }

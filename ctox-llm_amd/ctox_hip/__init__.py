@@ -221,6 +221,11 @@ SIGNATURES = {
     "ctox_hip_gated_delta_sequence": (_I32, [_P, _P, _P, _P, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P]),
     "ctox_hip_gated_delta_step_device": (_I32, [_P, _P, _P, _P, _P, _P, _P, _SZ, _SZ, _SZ, _P, _P]),
     "ctox_hip_gated_delta_sequence_device": (_I32, [_P, _P, _P, _P, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P]),
+    "ctox_hip_gdn_gates_device": (_I32, [_P, _P, _P, _P, _P, _SZ, _SZ, _P, _P, _P]),
+    "ctox_hip_repeat_heads_device": (_I32, [_P, _P, _SZ, _SZ, _SZ, _SZ, _P, _P]),
+    "ctox_hip_greedy_tokens_device": (_I32, [_P, _P, _SZ, _SZ, _P, _P]),
+    "ctox_hip_verify_greedy_mtp_device": (_I32, [_P, _P, _P, _P, _SZ, _SZ, _P, _P]),
+    "ctox_hip_mtp_accept_device": (_I32, [_P, _P, _P, _P, _P, _SZ, _SZ, ctypes.c_float, _P, _P, _P]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -430,6 +435,36 @@ class HipBackend:
         _check(load_library().ctox_hip_gated_delta_step_device(
             self.handle, d_q, d_k, d_v, d_log_decay, d_beta, d_state, heads, key_dim, value_dim, d_out,
             stream))
+
+    # ---- decode-step glue and token selection (device pointers) ----
+    def gdn_gates_device(self, d_a: int, d_b: int, d_a_log: int, d_dt_bias: int, tokens: int, heads: int,
+                         d_log_decay: int, d_beta: int, stream: Optional[int] = None) -> None:
+        """Q/src/decoder.rs:881-902."""
+        _check(load_library().ctox_hip_gdn_gates_device(self.handle, d_a, d_b, d_a_log, d_dt_bias, tokens, heads,
+                                                        d_log_decay, d_beta, stream))
+
+    def repeat_heads_device(self, d_in: int, rows: int, heads: int, dim: int, repeats: int, d_out: int,
+                            stream: Optional[int] = None) -> None:
+        """Q/src/decoder.rs:47-65."""
+        _check(load_library().ctox_hip_repeat_heads_device(self.handle, d_in, rows, heads, dim, repeats, d_out,
+                                                           stream))
+
+    def greedy_tokens_device(self, d_logits: int, rows: int, vocab: int, d_tokens: int,
+                             stream: Optional[int] = None) -> None:
+        """Q/src/engine.rs:906-913 per row."""
+        _check(load_library().ctox_hip_greedy_tokens_device(self.handle, d_logits, rows, vocab, d_tokens, stream))
+
+    def verify_greedy_mtp_device(self, d_draft: int, d_target: int, d_bonus: int, drafts: int, vocab: int,
+                                 d_out: int, stream: Optional[int] = None) -> None:
+        """Q/src/engine.rs:915-963; d_out: 3 + drafts uint32."""
+        _check(load_library().ctox_hip_verify_greedy_mtp_device(self.handle, d_draft, d_target, d_bonus, drafts,
+                                                                vocab, d_out, stream))
+
+    def mtp_accept_device(self, d_draft: int, d_target: int, d_bonus: int, d_tokens: int, drafts: int, vocab: int,
+                          temperature: float, d_rng: int, d_out: int, stream: Optional[int] = None) -> None:
+        """Rejection-sampling accept (no crate counterpart); d_rng: Pcg32 state, d_out: 2 uint32."""
+        _check(load_library().ctox_hip_mtp_accept_device(self.handle, d_draft, d_target, d_bonus, d_tokens, drafts,
+                                                         vocab, temperature, d_rng, d_out, stream))
 
     def synchronize(self) -> None:
         _check(load_library().ctox_hip_synchronize(self.handle))

@@ -226,6 +226,39 @@ ctox_status ctox_hip_gated_delta_sequence_device(ctox_hip_backend *backend, cons
                                                  size_t key_dim, size_t value_dim, size_t chunk,
                                                  float *d_out, void *stream);
 
+/* ---- decode-step glue and token selection (device buffers) ---- */
+/* GatedDeltaNet gates, Q/src/decoder.rs:881-902 (softplus :29-35):
+ * beta = sigmoid(b), log_decay = -exp(A_log) * softplus(a + dt_bias), over
+ * [tokens][heads] (A_log, dt_bias per head). */
+ctox_status ctox_hip_gdn_gates_device(ctox_hip_backend *backend, const float *d_a, const float *d_b,
+                                      const float *d_a_log, const float *d_dt_bias, size_t tokens,
+                                      size_t heads, float *d_log_decay, float *d_beta, void *stream);
+/* repeat_heads, Q/src/decoder.rs:47-65: out[row][h * repeats + r] = in[row][h]. */
+ctox_status ctox_hip_repeat_heads_device(ctox_hip_backend *backend, const float *d_in, size_t rows,
+                                         size_t heads, size_t dim, size_t repeats, float *d_out,
+                                         void *stream);
+/* Greedy token per logits row: argmax under f32::total_cmp, later index wins
+ * ties (Q/src/engine.rs:906-913). d_tokens holds `rows` uint32. */
+ctox_status ctox_hip_greedy_tokens_device(ctox_hip_backend *backend, const float *d_logits, size_t rows,
+                                          size_t vocab, uint32_t *d_tokens, void *stream);
+/* verify_greedy_mtp, Q/src/engine.rs:915-963 (full-logits branch): draft and
+ * target are [drafts][vocab], bonus [vocab]. d_out receives 3 + drafts uint32:
+ * next token, verified count, accepted count, accepted tokens. */
+ctox_status ctox_hip_verify_greedy_mtp_device(ctox_hip_backend *backend, const float *d_draft,
+                                              const float *d_target, const float *d_bonus, size_t drafts,
+                                              size_t vocab, uint32_t *d_out, void *stream);
+/* Speculative rejection-sampling accept at temperature > 0. No counterpart in
+ * the crate (its MTP path is greedy-only, Q/src/engine.rs:583-590); draws are
+ * the crate's Pcg32 (Q/src/sampler.rs:149-174), the replacement / bonus draw
+ * uses the cumulative search of Q/src/sampler.rs:134-143. d_tokens: the
+ * `drafts` proposed tokens; d_rng: Pcg32 state (uint64, advanced in place);
+ * d_out receives 2 uint32: next token, accepted count; a proposed token
+ * outside the vocabulary stops the pass with next token 0xFFFFFFFF. */
+ctox_status ctox_hip_mtp_accept_device(ctox_hip_backend *backend, const float *d_draft, const float *d_target,
+                                       const float *d_bonus, const uint32_t *d_tokens, size_t drafts,
+                                       size_t vocab, float temperature, uint64_t *d_rng, uint32_t *d_out,
+                                       void *stream);
+
 #ifdef __cplusplus
 }
 #endif
