@@ -61,6 +61,8 @@ struct MatvecArgs {
 // CTOX_SLICE_WAVES waves walks a 16-row tile in slices of 28 (Q4) / 56 (Q2)
 // blocks, each slice one 1 KiB coalesced load per row.
 constexpr uint32_t ctox_slice_blocks(uint32_t dtype) { return dtype ? 28u : 56u; }
+// Slices of the small-M (2..8 activation rows) slice kernels.
+constexpr uint32_t ctox_slice_blocks_tok(uint32_t dtype) { return dtype ? 28u : 26u; }
 #define CTOX_SLICE_WAVES 8
 
 struct RecoveredRowArgs {

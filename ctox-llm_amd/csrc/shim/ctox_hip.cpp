@@ -137,6 +137,8 @@ struct ctox_hip_backend {
     // Batch-1 slice kernels per dtype [Q2, Q4]: [0] walks the slices, [n]
     // requests all n slices up front.
     hipFunction_t sl[2][4] = {};
+    // Small-M slice kernels per dtype [Q2, Q4]: [0] M = 2..4, [1] M = 5..8.
+    hipFunction_t st[2][2] = {};
     int cus = 0;
     // Activation staging (two layouts: [0] Q2, [1] Q4) and gated-delta norms.
     DevBuf xa[2], xc[2], norms;
@@ -341,6 +343,10 @@ ctox_status run_matvec(ctox_hip_backend *b, int layout, int32_t dtype, const voi
         hipFunction_t f = b->sl[q4 ? 1 : 0][ns <= 3 ? ns : 0];
         return launch(f, dim3((unsigned)groups), dim3(CTOX_SLICE_WAVES * 64), s, a, "ctox_q*_matvec_sl*_gfx950");
     }
+    if (batch >= 2 && rb % 16 == 0 && ((uintptr_t)d_weights & 15) == 0) {
+        hipFunction_t f = b->st[q4 ? 1 : 0][tgroups == 1 ? 0 : 1];
+        return launch(f, dim3((unsigned)groups), dim3(CTOX_SLICE_WAVES * 64), s, a, "ctox_q*_matvec_st*_gfx950");
+    }
     hipFunction_t f = q4 ? (batch == 1 ? b->q4_b1 : (tgroups == 1 ? b->q4_b4 : b->q4_b8))
                          : (batch == 1 ? b->q2_b1 : (tgroups == 1 ? b->q2_b4 : b->q2_b8));
     return launch(f, dim3((unsigned)groups), dim3(256), s, a, "ctox_q*_matvec_gfx950");
@@ -422,7 +428,9 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->sl[0][0], "ctox_q2_matvec_sl_gfx950"}, {&b->sl[0][1], "ctox_q2_matvec_sl1_gfx950"},
                {&b->sl[0][2], "ctox_q2_matvec_sl2_gfx950"}, {&b->sl[0][3], "ctox_q2_matvec_sl3_gfx950"},
                {&b->sl[1][0], "ctox_q4_matvec_sl_gfx950"}, {&b->sl[1][1], "ctox_q4_matvec_sl1_gfx950"},
-               {&b->sl[1][2], "ctox_q4_matvec_sl2_gfx950"}, {&b->sl[1][3], "ctox_q4_matvec_sl3_gfx950"}};
+               {&b->sl[1][2], "ctox_q4_matvec_sl2_gfx950"}, {&b->sl[1][3], "ctox_q4_matvec_sl3_gfx950"},
+               {&b->st[0][0], "ctox_q2_matvec_st4_gfx950"}, {&b->st[0][1], "ctox_q2_matvec_st8_gfx950"},
+               {&b->st[1][0], "ctox_q4_matvec_st4_gfx950"}, {&b->st[1][1], "ctox_q4_matvec_st8_gfx950"}};
     for (auto &f : fns) {
         if (le != hipSuccess) break;
         le = hipModuleGetFunction(f.f, b->module, f.name);

@@ -190,6 +190,21 @@ def test_batched_ragged(hip, orc, batch):
         check(got, ref, f"ragged batch={batch}")
 
 
+@pytest.mark.parametrize("batch", [2, 3, 5, 8])
+@pytest.mark.parametrize("dtype", [0, 1])
+def test_small_m_slice_counts(hip, orc, batch, dtype):
+    """M = 2..8 on columns % 512 == 0 runs the small-M slice kernels (28 / 26
+    blocks per slice, partial last slices, rows not a multiple of 16)."""
+    for cols in (512, 1664, 3584, 7168, 17408):
+        rows = 37
+        say(f"case small-m slices batch={batch} dtype={dtype} {rows}x{cols}")
+        op, parts = make_case(dtype, rows, cols, 3 * cols + batch, "f16", bias=True, act=ctox_hip.Activation.Silu,
+                              batch=batch)
+        got = resident_run(hip, op, parts[1])
+        ref = oracle_rows(orc, dtype, rows, cols, parts, ctox_hip.Activation.Silu)
+        check(got, ref, f"small-m slices batch={batch} dtype={dtype} {rows}x{cols}")
+
+
 def test_mixed_segments_match_pure(hip, orc):
     say("case mixed segments")
     cols = 1088
