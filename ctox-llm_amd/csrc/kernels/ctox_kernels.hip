@@ -4,3 +4,4 @@
 #include "gated_delta.hip"
 #include "gated_delta_chunk.hip"
 #include "decode_ops.hip"
+#include "layer_ops.hip"

@@ -175,3 +175,43 @@ struct AcceptArgs {
     float temperature;
     uint32_t pad;
 };
+
+// Layer glue (layer_ops.hip).
+struct NormArgs {
+    const float *x;          // [rows][cols]
+    const float *gate;       // [rows][cols] (mode 1) or NULL
+    const float *w;          // [cols]
+    float *out;              // [rows][cols]
+    uint32_t cols;
+    uint32_t mode;           // 0: x * inv * (1 + w); 1: x * inv * w * silu(gate)
+    float eps;
+    uint32_t pad;
+};
+
+struct EltArgs {
+    const float *a;
+    const float *b;
+    float *out;
+    uint64_t n;
+};
+
+struct ConvArgs {
+    const float *input;      // [channels]
+    float *state;            // [channels][kernel], updated in place
+    const float *weight;     // [channels][kernel]
+    float *out;              // [channels]
+    uint32_t channels;
+    uint32_t kernel;
+};
+
+struct RopeArgs {
+    float *q;                // [rows][qh][hd], in place
+    float *k;                // [rows][kh][hd], in place
+    uint32_t qh;
+    uint32_t kh;
+    uint32_t hd;
+    uint32_t rd;
+    uint64_t position;       // position of row 0; row t is at position + t
+    float theta;
+    uint32_t pad;
+};

@@ -133,7 +133,8 @@ struct ctox_hip_backend {
                   q2_b4 = nullptr, q2_b8 = nullptr, rec_row = nullptr, row_dot = nullptr,
                   gdn_scan = nullptr, gdn_chunk_prep = nullptr, gdn_chunk_scan = nullptr, gates = nullptr,
                   repeat = nullptr, partials = nullptr, argmax_final = nullptr, verify = nullptr, decide = nullptr,
-                  pick_sums = nullptr, pick_final = nullptr;
+                  pick_sums = nullptr, pick_final = nullptr, rms = nullptr, swiglu = nullptr, sgate = nullptr,
+                  conv = nullptr, rope = nullptr;
     // Batch-1 slice kernels per dtype [Q2, Q4]: [0] walks the slices, [n]
     // requests all n slices up front.
     hipFunction_t sl[2][4] = {};
@@ -424,7 +425,9 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->repeat, "ctox_repeat_heads_gfx950"},   {&b->partials, "ctox_row_partials_gfx950"},
                {&b->argmax_final, "ctox_argmax_final_gfx950"}, {&b->verify, "ctox_verify_greedy_gfx950"},
                {&b->decide, "ctox_mtp_decide_gfx950"},     {&b->pick_sums, "ctox_pick_sums_gfx950"},
-               {&b->pick_final, "ctox_pick_final_gfx950"},
+               {&b->pick_final, "ctox_pick_final_gfx950"},  {&b->rms, "ctox_rms_norm_gfx950"},
+               {&b->swiglu, "ctox_swiglu_gfx950"},         {&b->sgate, "ctox_sigmoid_gate_gfx950"},
+               {&b->conv, "ctox_conv_update_gfx950"},      {&b->rope, "ctox_rope_gfx950"},
                {&b->sl[0][0], "ctox_q2_matvec_sl_gfx950"}, {&b->sl[0][1], "ctox_q2_matvec_sl1_gfx950"},
                {&b->sl[0][2], "ctox_q2_matvec_sl2_gfx950"}, {&b->sl[0][3], "ctox_q2_matvec_sl3_gfx950"},
                {&b->sl[1][0], "ctox_q4_matvec_sl_gfx950"}, {&b->sl[1][1], "ctox_q4_matvec_sl1_gfx950"},
@@ -959,4 +962,75 @@ extern "C" ctox_status ctox_hip_mtp_accept_device(ctox_hip_backend *b, const flo
     if ((st = launch(b->decide, dim3(1), dim3(64), s, a, "ctox_mtp_decide_gfx950"))) return st;
     if ((st = launch(b->pick_sums, dim3(parts2), dim3(256), s, a, "ctox_pick_sums_gfx950"))) return st;
     return launch(b->pick_final, dim3(1), dim3(1024), s, a, "ctox_pick_final_gfx950");
+}
+
+// ======================================================================
+// layer glue
+// ======================================================================
+namespace {
+ctox_status norm_launch(ctox_hip_backend *b, const float *x, const float *gate, size_t rows, size_t cols,
+                        const float *w, float eps, float *out, uint32_t mode, void *stream) {
+    if (!b || !x || !w || !out || (mode == 1 && !gate)) return fail(CTOX_ERR_SHAPE, "null argument");
+    // Q/src/reference.rs:18-34 matrix contract and the eps check of :38-93.
+    if (rows == 0 || cols == 0 || rows > 0x7fffffffu || cols > 0xffffffffu)
+        return fail(CTOX_ERR_SHAPE, "norm matrix shape is empty or too large");
+    if (!std::isfinite(eps) || eps <= 0.0f) return fail(CTOX_ERR_SHAPE, "norm epsilon must be finite and positive");
+    NormArgs a{x, gate, w, out, (uint32_t)cols, mode, eps, 0};
+    return launch(b->rms, dim3((unsigned)rows), dim3(256), pick_stream(b, stream), a, "ctox_rms_norm_gfx950");
+}
+ctox_status elt_launch(ctox_hip_backend *b, hipFunction_t f, const float *x, const float *y, float *out, size_t n,
+                       void *stream, const char *name) {
+    if (!b || !x || !y || !out) return fail(CTOX_ERR_SHAPE, "null argument");
+    if (n == 0 || (n + 255) / 256 > 0x7fffffffu) return fail(CTOX_ERR_SHAPE, "%s length is empty or too large", name);
+    EltArgs a{x, y, out, (uint64_t)n};
+    return launch(f, dim3((unsigned)((n + 255) / 256)), dim3(256), pick_stream(b, stream), a, name);
+}
+}  // namespace
+
+extern "C" ctox_status ctox_hip_rms_norm_device(ctox_hip_backend *b, const float *d_x, size_t rows, size_t cols,
+                                                const float *d_w, float eps, float *d_out, void *stream) {
+    return norm_launch(b, d_x, nullptr, rows, cols, d_w, eps, d_out, 0, stream);
+}
+
+extern "C" ctox_status ctox_hip_rms_norm_gated_device(ctox_hip_backend *b, const float *d_x, const float *d_gate,
+                                                      size_t rows, size_t cols, const float *d_w, float eps,
+                                                      float *d_out, void *stream) {
+    return norm_launch(b, d_x, d_gate, rows, cols, d_w, eps, d_out, 1, stream);
+}
+
+extern "C" ctox_status ctox_hip_swiglu_device(ctox_hip_backend *b, const float *d_gate, const float *d_up, size_t n,
+                                              float *d_out, void *stream) {
+    return elt_launch(b, b ? b->swiglu : nullptr, d_gate, d_up, d_out, n, stream, "ctox_swiglu_gfx950");
+}
+
+extern "C" ctox_status ctox_hip_sigmoid_gate_device(ctox_hip_backend *b, float *d_values, const float *d_gate,
+                                                    size_t n, void *stream) {
+    return elt_launch(b, b ? b->sgate : nullptr, d_values, d_gate, d_values, n, stream, "ctox_sigmoid_gate_gfx950");
+}
+
+extern "C" ctox_status ctox_hip_causal_conv_update_device(ctox_hip_backend *b, const float *d_input, float *d_state,
+                                                          const float *d_weight, size_t channels, size_t kernel,
+                                                          float *d_out, void *stream) {
+    if (!b || !d_input || !d_state || !d_weight || !d_out) return fail(CTOX_ERR_SHAPE, "null argument");
+    if (channels == 0 || kernel == 0 || channels > 0x7fffffffu || kernel > 4096)
+        return fail(CTOX_ERR_SHAPE, "conv state shape is empty or too large");
+    ConvArgs a{d_input, d_state, d_weight, d_out, (uint32_t)channels, (uint32_t)kernel};
+    return launch(b->conv, dim3((unsigned)((channels + 255) / 256)), dim3(256), pick_stream(b, stream), a,
+                  "ctox_conv_update_gfx950");
+}
+
+extern "C" ctox_status ctox_hip_partial_rope_device(ctox_hip_backend *b, float *d_q, float *d_k, size_t rows,
+                                                    size_t q_heads, size_t k_heads, size_t head_dim,
+                                                    size_t rotary_dim, uint64_t position, float theta, void *stream) {
+    if (!b || !d_q || !d_k) return fail(CTOX_ERR_SHAPE, "null argument");
+    // Q/src/reference.rs:115-155: the rotary dimension is even, non-zero and within the head.
+    if (rotary_dim == 0 || rotary_dim > head_dim || rotary_dim % 2 || !std::isfinite(theta) || theta <= 0.0f)
+        return fail(CTOX_ERR_SHAPE, "rotary dimension or theta is invalid");
+    if (rows == 0 || q_heads == 0 || k_heads == 0 || rotary_dim > 512 || rows > 65535 || q_heads + k_heads > 65535 ||
+        position > UINT64_MAX - rows)
+        return fail(CTOX_ERR_SHAPE, "rope shape is empty or too large");
+    RopeArgs a{d_q, d_k, (uint32_t)q_heads, (uint32_t)k_heads, (uint32_t)head_dim, (uint32_t)rotary_dim,
+               (uint64_t)position, theta, 0};
+    return launch(b->rope, dim3((unsigned)rows, (unsigned)(q_heads + k_heads)), dim3(256), pick_stream(b, stream), a,
+                  "ctox_rope_gfx950");
 }

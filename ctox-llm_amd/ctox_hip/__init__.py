@@ -226,6 +226,12 @@ SIGNATURES = {
     "ctox_hip_greedy_tokens_device": (_I32, [_P, _P, _SZ, _SZ, _P, _P]),
     "ctox_hip_verify_greedy_mtp_device": (_I32, [_P, _P, _P, _P, _SZ, _SZ, _P, _P]),
     "ctox_hip_mtp_accept_device": (_I32, [_P, _P, _P, _P, _P, _SZ, _SZ, ctypes.c_float, _P, _P, _P]),
+    "ctox_hip_rms_norm_device": (_I32, [_P, _P, _SZ, _SZ, _P, ctypes.c_float, _P, _P]),
+    "ctox_hip_rms_norm_gated_device": (_I32, [_P, _P, _P, _SZ, _SZ, _P, ctypes.c_float, _P, _P]),
+    "ctox_hip_swiglu_device": (_I32, [_P, _P, _P, _SZ, _P, _P]),
+    "ctox_hip_sigmoid_gate_device": (_I32, [_P, _P, _P, _SZ, _P]),
+    "ctox_hip_causal_conv_update_device": (_I32, [_P, _P, _P, _P, _SZ, _SZ, _P, _P]),
+    "ctox_hip_partial_rope_device": (_I32, [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_uint64, ctypes.c_float, _P]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -465,6 +471,38 @@ class HipBackend:
         """Rejection-sampling accept (no crate counterpart); d_rng: Pcg32 state, d_out: 2 uint32."""
         _check(load_library().ctox_hip_mtp_accept_device(self.handle, d_draft, d_target, d_bonus, d_tokens, drafts,
                                                          vocab, temperature, d_rng, d_out, stream))
+
+    # ---- layer glue (device pointers, fp32) ----
+    def rms_norm_device(self, d_x: int, rows: int, cols: int, d_w: int, eps: float, d_out: int,
+                        stream: Optional[int] = None) -> None:
+        """Q/src/reference.rs:38-62."""
+        _check(load_library().ctox_hip_rms_norm_device(self.handle, d_x, rows, cols, d_w, eps, d_out, stream))
+
+    def rms_norm_gated_device(self, d_x: int, d_gate: int, rows: int, cols: int, d_w: int, eps: float, d_out: int,
+                              stream: Optional[int] = None) -> None:
+        """Q/src/reference.rs:66-93."""
+        _check(load_library().ctox_hip_rms_norm_gated_device(self.handle, d_x, d_gate, rows, cols, d_w, eps, d_out,
+                                                             stream))
+
+    def swiglu_device(self, d_gate: int, d_up: int, n: int, d_out: int, stream: Optional[int] = None) -> None:
+        """Q/src/reference.rs:96-112."""
+        _check(load_library().ctox_hip_swiglu_device(self.handle, d_gate, d_up, n, d_out, stream))
+
+    def sigmoid_gate_device(self, d_values: int, d_gate: int, n: int, stream: Optional[int] = None) -> None:
+        """Q/src/reference.rs:502-515 (in place)."""
+        _check(load_library().ctox_hip_sigmoid_gate_device(self.handle, d_values, d_gate, n, stream))
+
+    def causal_conv_update_device(self, d_input: int, d_state: int, d_weight: int, channels: int, kernel: int,
+                                  d_out: int, stream: Optional[int] = None) -> None:
+        """Q/src/reference.rs:159-187."""
+        _check(load_library().ctox_hip_causal_conv_update_device(self.handle, d_input, d_state, d_weight, channels,
+                                                                 kernel, d_out, stream))
+
+    def partial_rope_device(self, d_q: int, d_k: int, rows: int, q_heads: int, k_heads: int, head_dim: int,
+                            rotary_dim: int, position: int, theta: float, stream: Optional[int] = None) -> None:
+        """Q/src/reference.rs:115-155 (in place; row t at position + t)."""
+        _check(load_library().ctox_hip_partial_rope_device(self.handle, d_q, d_k, rows, q_heads, k_heads, head_dim,
+                                                           rotary_dim, position, theta, stream))
 
     def synchronize(self) -> None:
         _check(load_library().ctox_hip_synchronize(self.handle))

@@ -259,6 +259,31 @@ ctox_status ctox_hip_mtp_accept_device(ctox_hip_backend *backend, const float *d
                                        size_t vocab, float temperature, uint64_t *d_rng, uint32_t *d_out,
                                        void *stream);
 
+/* ---- layer glue (device buffers, fp32) ---- */
+/* rms_norm with (1 + w) weight, Q/src/reference.rs:38-62, per row of [rows][cols]. */
+ctox_status ctox_hip_rms_norm_device(ctox_hip_backend *backend, const float *d_x, size_t rows, size_t cols,
+                                     const float *d_w, float eps, float *d_out, void *stream);
+/* rms_norm_gated, Q/src/reference.rs:66-93: x * rsqrt(mean(x^2) + eps) * w * silu(gate). */
+ctox_status ctox_hip_rms_norm_gated_device(ctox_hip_backend *backend, const float *d_x, const float *d_gate,
+                                           size_t rows, size_t cols, const float *d_w, float eps, float *d_out,
+                                           void *stream);
+/* swiglu, Q/src/reference.rs:96-112: out = silu(gate) * up. */
+ctox_status ctox_hip_swiglu_device(ctox_hip_backend *backend, const float *d_gate, const float *d_up, size_t n,
+                                   float *d_out, void *stream);
+/* sigmoid_gate, Q/src/reference.rs:502-515: values *= sigmoid(gate), in place. */
+ctox_status ctox_hip_sigmoid_gate_device(ctox_hip_backend *backend, float *d_values, const float *d_gate,
+                                         size_t n, void *stream);
+/* causal_conv_silu update, Q/src/reference.rs:159-187: the [channels][kernel]
+ * state shifts left by one, the input is appended, out = silu(state . weight). */
+ctox_status ctox_hip_causal_conv_update_device(ctox_hip_backend *backend, const float *d_input, float *d_state,
+                                               const float *d_weight, size_t channels, size_t kernel,
+                                               float *d_out, void *stream);
+/* apply_partial_rope, Q/src/reference.rs:115-155, in place on q [rows][q_heads][head_dim]
+ * and k [rows][k_heads][head_dim]; row t is at position + t. */
+ctox_status ctox_hip_partial_rope_device(ctox_hip_backend *backend, float *d_q, float *d_k, size_t rows,
+                                         size_t q_heads, size_t k_heads, size_t head_dim, size_t rotary_dim,
+                                         uint64_t position, float theta, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

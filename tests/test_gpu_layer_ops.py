@@ -1,0 +1,125 @@
+"""GPU parity of the layer glue kernels against the oracle.
+
+* rms_norm (1 + w) and gated rms_norm: Q/src/reference.rs:38-93. The GPU
+  reduces the sum of squares as a tree, the oracle sequentially, so outputs
+  agree to 1e-5 relative (well inside the 1e-3 bar).
+* swiglu / sigmoid_gate: Q/src/reference.rs:96-112 and :502-515, elementwise
+  with the device expf (within a few ulp of glibc's).
+* causal conv update: Q/src/reference.rs:159-187. The state shift is bit-exact;
+  the dot runs in the oracle's order but contracted to fused multiply-adds,
+  so outputs near zero (where the dot cancels) get an absolute 1e-6 floor.
+* partial RoPE: Q/src/reference.rs:115-155, rows at consecutive positions.
+  The angle is position * theta^(-2i/rd) in f32: one ulp of the device powf
+  moves the angle by one ulp of its own magnitude, so the tolerance is
+  4 ulp of the largest angle (times |x|), and exact outside the rotary dims.
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def dev(x, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dtype).cuda()
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 5120), (5, 5120), (3, 128), (2, 17), (1, 1)])
+def test_rms_norm(hip, orc, rows, cols):
+    say(f"case rms_norm rows={rows} cols={cols}")
+    rng = np.random.default_rng(cols + rows)
+    x = (rng.standard_normal((rows, cols)) * 3).astype(np.float32)
+    w = (rng.standard_normal(cols) * 0.2).astype(np.float32)
+    g = (rng.standard_normal((rows, cols)) * 2).astype(np.float32)
+    keep = [dev(x), dev(w), dev(g)]
+    out = torch.empty(rows, cols, device="cuda")
+    out2 = torch.empty(rows, cols, device="cuda")
+    hip.rms_norm_device(keep[0].data_ptr(), rows, cols, keep[1].data_ptr(), 1e-6, out.data_ptr())
+    hip.rms_norm_gated_device(keep[0].data_ptr(), keep[2].data_ptr(), rows, cols, keep[1].data_ptr(), 1e-6,
+                              out2.data_ptr())
+    torch.cuda.synchronize()
+    ref = orc.rms_norm_1p_weight(x.reshape(-1), rows, cols, w, 1e-6).reshape(rows, cols)
+    ref2 = orc.rms_norm_gated(x.reshape(-1), g.reshape(-1), rows, cols, w, 1e-6).reshape(rows, cols)
+    np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(out2.cpu().numpy(), ref2, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("n", [1, 255, 17408, 100003])
+def test_swiglu_sigmoid_gate(hip, orc, n):
+    say(f"case swiglu/sigmoid n={n}")
+    rng = np.random.default_rng(n)
+    a = (rng.standard_normal(n) * 5).astype(np.float32)
+    b = (rng.standard_normal(n) * 5).astype(np.float32)
+    da, db = dev(a), dev(b)
+    out = torch.empty(n, device="cuda")
+    hip.swiglu_device(da.data_ptr(), db.data_ptr(), n, out.data_ptr())
+    hip.sigmoid_gate_device(da.data_ptr(), db.data_ptr(), n)   # in place on a
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(out.cpu().numpy(), orc.swiglu(a, b), rtol=2e-6, atol=1e-30)
+    ref = a.copy()
+    orc.sigmoid_gate(ref, b)
+    np.testing.assert_allclose(da.cpu().numpy(), ref, rtol=2e-6, atol=1e-30)
+
+
+@pytest.mark.parametrize("channels,kernel", [(10240, 4), (300, 4), (7, 1), (33, 6)])
+def test_causal_conv_update(hip, orc, channels, kernel):
+    say(f"case conv channels={channels} kernel={kernel}")
+    rng = np.random.default_rng(channels * kernel)
+    state = rng.standard_normal((channels, kernel)).astype(np.float32)
+    weight = rng.standard_normal((channels, kernel)).astype(np.float32)
+    ds, dw = dev(state), dev(weight)
+    ref_state = state.reshape(-1).copy()
+    for step in range(3):  # consecutive decode steps carry the state
+        x = rng.standard_normal(channels).astype(np.float32)
+        dx = dev(x)
+        out = torch.empty(channels, device="cuda")
+        hip.causal_conv_update_device(dx.data_ptr(), ds.data_ptr(), dw.data_ptr(), channels, kernel, out.data_ptr())
+        torch.cuda.synchronize()
+        ref = orc.causal_conv_silu_update(x, ref_state, weight.reshape(-1), channels, kernel)
+        assert np.array_equal(ds.cpu().numpy().reshape(-1), ref_state), step
+        np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=2e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("rows,qh,kh,hd,rd,pos", [(1, 24, 4, 256, 64, 0), (5, 24, 4, 256, 64, 4093),
+                                                   (2, 3, 1, 128, 128, 70000), (3, 2, 2, 10, 2, 12)])
+def test_partial_rope(hip, orc, rows, qh, kh, hd, rd, pos):
+    say(f"case rope rows={rows} qh={qh} kh={kh} hd={hd} rd={rd} pos={pos}")
+    rng = np.random.default_rng(rows + hd + pos)
+    q = rng.standard_normal((rows, qh, hd)).astype(np.float32)
+    k = rng.standard_normal((rows, kh, hd)).astype(np.float32)
+    dq, dk = dev(q), dev(k)
+    hip.partial_rope_device(dq.data_ptr(), dk.data_ptr(), rows, qh, kh, hd, rd, pos, 1e7)
+    torch.cuda.synchronize()
+    gq, gk = dq.cpu().numpy(), dk.cpu().numpy()
+    for t in range(rows):
+        rq, rk = q[t].reshape(-1).copy(), k[t].reshape(-1).copy()
+        orc.apply_partial_rope(rq, rk, qh, kh, hd, rd, pos + t, 1e7)
+        tol = 4 * float(np.spacing(np.float32(max(pos + t, 1)))) * 2 * 4.5 + 1e-6
+        for got, ref, src in ((gq[t], rq.reshape(qh, hd), q[t]), (gk[t], rk.reshape(kh, hd), k[t])):
+            np.testing.assert_allclose(got[:, :rd], ref[:, :rd], rtol=0, atol=tol)
+            assert np.array_equal(got[:, rd:], src[:, rd:])
+
+
+def test_layer_ops_errors(hip):
+    import ctox_hip
+    t = torch.zeros(16, device="cuda")
+    p = t.data_ptr()
+    with pytest.raises(ctox_hip.ShapeError):
+        hip.rms_norm_device(p, 1, 16, p, 0.0, p)
+    with pytest.raises(ctox_hip.ShapeError):
+        hip.rms_norm_device(p, 0, 16, p, 1e-6, p)
+    with pytest.raises(ctox_hip.ShapeError):
+        hip.swiglu_device(p, p, 0, p)
+    with pytest.raises(ctox_hip.ShapeError):
+        hip.partial_rope_device(p, p, 1, 1, 1, 8, 3, 0, 1e7)
+    with pytest.raises(ctox_hip.ShapeError):
+        hip.partial_rope_device(p, p, 1, 1, 1, 8, 10, 0, 1e7)
+    with pytest.raises(ctox_hip.ShapeError):
+        hip.causal_conv_update_device(p, p, p, 4, 0, p)
