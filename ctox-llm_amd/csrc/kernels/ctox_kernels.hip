@@ -5,3 +5,4 @@
 #include "gated_delta_chunk.hip"
 #include "decode_ops.hip"
 #include "layer_ops.hip"
+#include "paged_attention.hip"

@@ -215,3 +215,54 @@ struct RopeArgs {
     float theta;
     uint32_t pad;
 };
+
+// Paged KV cache and attention (paged_attention.hip).
+struct PagedKvDesc {         // one logical page
+    uint32_t precision;      // 0 = Q2 pool, otherwise Q4 pool
+    uint32_t physical_slot;  // page index inside its pool
+    uint32_t tokens;         // tokens held
+    uint32_t first_token;    // logical index of the page's first token
+};
+
+struct KvPackArgs {
+    uint8_t *q4_pages;
+    const float *keys;       // [tokens][component_values]
+    const float *values;     // [tokens][component_values]
+    uint32_t physical_slot;
+    uint32_t first_token_in_page;
+    uint32_t component_values;
+    uint32_t q4_token_bytes;
+    uint64_t q4_page_bytes;
+};
+
+struct KvDemoteArgs {
+    const uint8_t *q4_page;
+    uint8_t *q2_page;
+    uint64_t blocks;         // tokens * blocks per token
+};
+
+struct GqaArgs {
+    const float *query;      // [rows][query_heads][256]
+    const uint8_t *q2;
+    const uint8_t *q4;
+    const PagedKvDesc *desc; // [page_count]
+    float *part_out;         // [kv heads][splits][queries][256]
+    float *part_stats;       // [kv heads][splits][queries][2] = (max, denominator)
+    float *out;              // [rows][query_heads][256]
+    uint64_t q2_page_bytes;
+    uint64_t q4_page_bytes;
+    uint32_t query_heads;
+    uint32_t group;          // query heads per kv head
+    uint32_t tokens;         // cached tokens, the query rows included
+    uint32_t rows;           // query rows (the last `rows` cached tokens)
+    uint32_t queries;        // group * rows
+    uint32_t page_tokens;
+    uint32_t page_count;
+    uint32_t component_values;
+    uint32_t q2_token_bytes;
+    uint32_t q4_token_bytes;
+    uint32_t tiles;          // ceil(tokens / 16)
+    uint32_t tiles_per_wave;
+    uint32_t splits;
+    float scale;
+};

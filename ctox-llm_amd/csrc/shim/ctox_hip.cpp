@@ -134,7 +134,8 @@ struct ctox_hip_backend {
                   gdn_scan = nullptr, gdn_chunk_prep = nullptr, gdn_chunk_scan = nullptr, gates = nullptr,
                   repeat = nullptr, partials = nullptr, argmax_final = nullptr, verify = nullptr, decide = nullptr,
                   pick_sums = nullptr, pick_final = nullptr, rms = nullptr, swiglu = nullptr, sgate = nullptr,
-                  conv = nullptr, rope = nullptr;
+                  conv = nullptr, rope = nullptr, kv_pack = nullptr, kv_demote = nullptr, gqa_part[2] = {},
+                  gqa_combine = nullptr;
     // Batch-1 slice kernels per dtype [Q2, Q4]: [0] walks the slices, [n]
     // requests all n slices up front.
     hipFunction_t sl[2][4] = {};
@@ -145,6 +146,8 @@ struct ctox_hip_backend {
     DevBuf xa[2], xc[2], norms;
     // Token selection scratch: per-part partials, pick sums and state.
     DevBuf tok, stats;
+    // Split-attention partials.
+    DevBuf attn;
 };
 
 struct ctox_hip_matrix {
@@ -428,6 +431,10 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->pick_final, "ctox_pick_final_gfx950"},  {&b->rms, "ctox_rms_norm_gfx950"},
                {&b->swiglu, "ctox_swiglu_gfx950"},         {&b->sgate, "ctox_sigmoid_gate_gfx950"},
                {&b->conv, "ctox_conv_update_gfx950"},      {&b->rope, "ctox_rope_gfx950"},
+               {&b->kv_pack, "ctox_kv_pack_q4_gfx950"},    {&b->kv_demote, "ctox_kv_demote_gfx950"},
+               {&b->gqa_part[0], "ctox_paged_gqa_partial_r1_gfx950"},
+               {&b->gqa_part[1], "ctox_paged_gqa_partial_r2_gfx950"},
+               {&b->gqa_combine, "ctox_paged_gqa_combine_gfx950"},
                {&b->sl[0][0], "ctox_q2_matvec_sl_gfx950"}, {&b->sl[0][1], "ctox_q2_matvec_sl1_gfx950"},
                {&b->sl[0][2], "ctox_q2_matvec_sl2_gfx950"}, {&b->sl[0][3], "ctox_q2_matvec_sl3_gfx950"},
                {&b->sl[1][0], "ctox_q4_matvec_sl_gfx950"}, {&b->sl[1][1], "ctox_q4_matvec_sl1_gfx950"},
@@ -456,7 +463,7 @@ extern "C" void ctox_hip_backend_destroy(ctox_hip_backend *b) {
     if (!b) return;
     (void)hipSetDevice(b->device);
     (void)hipDeviceSynchronize();
-    DevBuf *bufs[] = {&b->xa[0], &b->xa[1], &b->xc[0], &b->xc[1], &b->norms, &b->tok, &b->stats};
+    DevBuf *bufs[] = {&b->xa[0], &b->xa[1], &b->xc[0], &b->xc[1], &b->norms, &b->tok, &b->stats, &b->attn};
     for (DevBuf *d : bufs)
         if (d->ptr) (void)hipFree(d->ptr);
     if (b->stream) (void)hipStreamDestroy(b->stream);
@@ -1034,3 +1041,78 @@ extern "C" ctox_status ctox_hip_partial_rope_device(ctox_hip_backend *b, float *
     return launch(b->rope, dim3((unsigned)rows, (unsigned)(q_heads + k_heads)), dim3(256), pick_stream(b, stream), a,
                   "ctox_rope_gfx950");
 }
+
+// ======================================================================
+// paged KV cache and attention
+// ======================================================================
+extern "C" ctox_status ctox_hip_kv_pack_q4_device(ctox_hip_backend *b, uint8_t *d_q4_pages, const float *d_keys,
+                                                  const float *d_values, size_t token_count, size_t component_values,
+                                                  uint32_t physical_slot, uint32_t first_token_in_page,
+                                                  uint32_t q4_page_bytes, void *stream) {
+    if (!b || !d_q4_pages || !d_keys || !d_values) return fail(CTOX_ERR_SHAPE, "null argument");
+    // Q/src/kv_cache.rs:238-252: a non-zero multiple of 64 values per component.
+    if (component_values == 0 || component_values % 64 || component_values > (1u << 24))
+        return fail(CTOX_ERR_SHAPE, "KV component width must be a non-zero multiple of 64");
+    const uint64_t token_bytes = component_values * 2 / 64 * 34;
+    if (token_count == 0 || token_count > 65535 ||
+        (first_token_in_page + token_count) * token_bytes > (uint64_t)q4_page_bytes)
+        return fail(CTOX_ERR_SHAPE, "KV tokens do not fit the Q4 page");
+    KvPackArgs a{d_q4_pages, d_keys, d_values, physical_slot, first_token_in_page, (uint32_t)component_values,
+                 (uint32_t)token_bytes, q4_page_bytes};
+    return launch(b->kv_pack, dim3((unsigned)(component_values * 2 / 64), (unsigned)token_count), dim3(64),
+                  pick_stream(b, stream), a, "ctox_kv_pack_q4_gfx950");
+}
+
+extern "C" ctox_status ctox_hip_kv_demote_device(ctox_hip_backend *b, const uint8_t *d_q4_page, uint8_t *d_q2_page,
+                                                 size_t tokens, size_t blocks_per_token, void *stream) {
+    if (!b || !d_q4_page || !d_q2_page) return fail(CTOX_ERR_SHAPE, "null argument");
+    if (tokens == 0 || blocks_per_token == 0 || tokens > (1u << 20) || blocks_per_token > (1u << 20))
+        return fail(CTOX_ERR_SHAPE, "KV page geometry is empty or too large");
+    const uint64_t blocks = (uint64_t)tokens * blocks_per_token;
+    KvDemoteArgs a{d_q4_page, d_q2_page, blocks};
+    return launch(b->kv_demote, dim3((unsigned)((blocks * 16 + 255) / 256)), dim3(256), pick_stream(b, stream), a,
+                  "ctox_kv_demote_gfx950");
+}
+
+extern "C" ctox_status ctox_hip_paged_gqa_device(ctox_hip_backend *b, const float *d_query, const uint8_t *d_q2_pages,
+                                                 const uint8_t *d_q4_pages,
+                                                 const ctox_paged_kv_descriptor *d_descriptors,
+                                                 const ctox_paged_gqa_params *p, size_t rows, float *d_out,
+                                                 void *stream) {
+    if (!b || !d_query || !d_q2_pages || !d_q4_pages || !d_descriptors || !p || !d_out)
+        return fail(CTOX_ERR_SHAPE, "null argument");
+    if (p->head_dim != 256) return fail(CTOX_ERR_UNSUPPORTED_OPERATION, "paged attention needs head_dim 256");
+    // Q/src/reference.rs:420-440 contract: heads divide, the query rows are cached.
+    if (p->key_value_heads == 0 || p->query_heads == 0 || p->query_heads % p->key_value_heads || rows == 0 ||
+        rows > p->tokens || p->page_tokens == 0 || p->page_count == 0 || !std::isfinite(p->scale))
+        return fail(CTOX_ERR_SHAPE, "invalid paged attention contract");
+    const uint32_t group = p->query_heads / p->key_value_heads;
+    if ((uint64_t)group * rows > 32)
+        return fail(CTOX_ERR_UNSUPPORTED_OPERATION, "query heads per kv head times rows exceeds 32");
+    const uint64_t cv = (uint64_t)p->key_value_heads * 256;
+    if (p->combined_values != 2 * cv || p->q2_token_bytes != 2 * cv / 64 * 18 ||
+        p->q4_token_bytes != 2 * cv / 64 * 34 || (uint64_t)p->q2_page_bytes < (uint64_t)p->page_tokens * p->q2_token_bytes ||
+        (uint64_t)p->q4_page_bytes < (uint64_t)p->page_tokens * p->q4_token_bytes || p->q2_page_bytes % 4 ||
+        p->q4_page_bytes % 4 || p->tokens > (1u << 30))
+        return fail(CTOX_ERR_SHAPE, "paged KV geometry differs from the attention contract");
+    const uint32_t queries = group * (uint32_t)rows;
+    const uint32_t tiles = (p->tokens + 15) / 16;
+    uint32_t splits = std::max<uint32_t>(1, (uint32_t)((b->cus + p->key_value_heads - 1) / p->key_value_heads));
+    splits = std::min<uint32_t>(splits, (tiles + 3) / 4);
+    const uint32_t tpw = (tiles + 4 * splits - 1) / (4 * splits);
+    splits = (tiles + 4 * tpw - 1) / (4 * tpw);
+    const size_t part = (size_t)p->key_value_heads * splits * queries;
+    ctox_status st = ensure(b, b->attn, part * (256 + 2) * sizeof(float), false);
+    if (st) return st;
+    float *part_out = (float *)b->attn.ptr;
+    GqaArgs a{d_query, d_q2_pages, d_q4_pages, (const PagedKvDesc *)d_descriptors, part_out, part_out + part * 256,
+              d_out, p->q2_page_bytes, p->q4_page_bytes, p->query_heads, group, p->tokens, (uint32_t)rows, queries,
+              p->page_tokens, p->page_count, (uint32_t)cv, p->q2_token_bytes, p->q4_token_bytes, tiles, tpw, splits,
+              p->scale};
+    hipStream_t s = pick_stream(b, stream);
+    st = launch(b->gqa_part[queries > 16 ? 1 : 0], dim3(splits, p->key_value_heads), dim3(256), s, a,
+                "ctox_paged_gqa_partial_gfx950");
+    if (st) return st;
+    return launch(b->gqa_combine, dim3(queries, p->key_value_heads), dim3(256), s, a, "ctox_paged_gqa_combine_gfx950");
+}
+static_assert(sizeof(ctox_paged_kv_descriptor) == sizeof(PagedKvDesc), "page descriptor layout");

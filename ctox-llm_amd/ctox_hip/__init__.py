@@ -192,6 +192,13 @@ class _RecoveredRowMatVec(ctypes.Structure):
                 ("len", ctypes.c_size_t), ("s_out", ctypes.c_float)]
 
 
+class PagedGqaParams(ctypes.Structure):
+    """ctox_paged_gqa_params (CtoxPagedGqaParams, q2q4_fused_matvec_sm86.cu:1621-1634)."""
+    _fields_ = [(n, ctypes.c_uint32) for n in (
+        "query_heads", "key_value_heads", "head_dim", "tokens", "page_tokens", "page_count", "combined_values",
+        "q2_token_bytes", "q4_token_bytes", "q2_page_bytes", "q4_page_bytes")] + [("scale", ctypes.c_float)]
+
+
 # Every symbol include/ctox_hip.h declares: name -> (restype, argtypes).
 _P = ctypes.c_void_p
 _SZ = ctypes.c_size_t
@@ -232,6 +239,9 @@ SIGNATURES = {
     "ctox_hip_sigmoid_gate_device": (_I32, [_P, _P, _P, _SZ, _P]),
     "ctox_hip_causal_conv_update_device": (_I32, [_P, _P, _P, _P, _SZ, _SZ, _P, _P]),
     "ctox_hip_partial_rope_device": (_I32, [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_uint64, ctypes.c_float, _P]),
+    "ctox_hip_kv_pack_q4_device": (_I32, [_P, _P, _P, _P, _SZ, _SZ, _U32, _U32, _U32, _P]),
+    "ctox_hip_kv_demote_device": (_I32, [_P, _P, _P, _SZ, _SZ, _P]),
+    "ctox_hip_paged_gqa_device": (_I32, [_P, _P, _P, _P, _P, ctypes.POINTER(PagedGqaParams), _SZ, _P, _P]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -503,6 +513,27 @@ class HipBackend:
         """Q/src/reference.rs:115-155 (in place; row t at position + t)."""
         _check(load_library().ctox_hip_partial_rope_device(self.handle, d_q, d_k, rows, q_heads, k_heads, head_dim,
                                                            rotary_dim, position, theta, stream))
+
+    # ---- paged KV cache (device pointers) ----
+    def kv_pack_q4_device(self, d_q4_pages: int, d_keys: int, d_values: int, token_count: int,
+                          component_values: int, physical_slot: int, first_token_in_page: int, q4_page_bytes: int,
+                          stream: Optional[int] = None) -> None:
+        """Q/src/kv_cache.rs:200-206 on the device."""
+        _check(load_library().ctox_hip_kv_pack_q4_device(self.handle, d_q4_pages, d_keys, d_values, token_count,
+                                                         component_values, physical_slot, first_token_in_page,
+                                                         q4_page_bytes, stream))
+
+    def kv_demote_device(self, d_q4_page: int, d_q2_page: int, tokens: int, blocks_per_token: int,
+                         stream: Optional[int] = None) -> None:
+        """Q/src/kv_cache.rs:216-236 on the device."""
+        _check(load_library().ctox_hip_kv_demote_device(self.handle, d_q4_page, d_q2_page, tokens, blocks_per_token,
+                                                        stream))
+
+    def paged_gqa_device(self, d_query: int, d_q2_pages: int, d_q4_pages: int, d_descriptors: int,
+                         params: PagedGqaParams, rows: int, d_out: int, stream: Optional[int] = None) -> None:
+        """Q/src/reference.rs:420-499 over the paged cache."""
+        _check(load_library().ctox_hip_paged_gqa_device(self.handle, d_query, d_q2_pages, d_q4_pages, d_descriptors,
+                                                        ctypes.byref(params), rows, d_out, stream))
 
     def synchronize(self) -> None:
         _check(load_library().ctox_hip_synchronize(self.handle))

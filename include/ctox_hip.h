@@ -284,6 +284,58 @@ ctox_status ctox_hip_partial_rope_device(ctox_hip_backend *backend, float *d_q, 
                                          size_t q_heads, size_t k_heads, size_t head_dim, size_t rotary_dim,
                                          uint64_t position, float theta, void *stream);
 
+/* ---- paged mixed Q2/Q4 KV cache (device buffers) ----
+ * Page layout of Q/src/kv_cache.rs:280-300: token-major [K heads, V heads]
+ * canonical Q4_B64 / Q2_B64 blocks; a page is wholly Q2 or Q4 and lives at
+ * pool + physical_slot * page_bytes in its pool. */
+typedef struct {                /* CtoxPagedKvDescriptor, q2q4_fused_matvec_sm86.cu:1614-1619 */
+    uint32_t precision;         /* 0 = Q2 pool, otherwise Q4 pool */
+    uint32_t physical_slot;
+    uint32_t tokens;
+    uint32_t first_token;
+} ctox_paged_kv_descriptor;
+
+typedef struct {                /* CtoxPagedGqaParams, q2q4_fused_matvec_sm86.cu:1621-1634 */
+    uint32_t query_heads;
+    uint32_t key_value_heads;
+    uint32_t head_dim;          /* 256 */
+    uint32_t tokens;            /* cached tokens, the query rows included */
+    uint32_t page_tokens;
+    uint32_t page_count;
+    uint32_t combined_values;   /* 2 * key_value_heads * head_dim */
+    uint32_t q2_token_bytes;
+    uint32_t q4_token_bytes;
+    uint32_t q2_page_bytes;
+    uint32_t q4_page_bytes;
+    float scale;                /* 1 / sqrt(head_dim) in Q/src/reference.rs:420-499 */
+} ctox_paged_gqa_params;
+
+/* Quantize token_count K/V rows ([token][component_values] each) into
+ * consecutive slots of one Q4 page starting at first_token_in_page,
+ * bit-exact with QuantizedKvPage::push (Q/src/kv_cache.rs:200-206,
+ * Q4Block64::quantize Q/src/quant.rs:144-168). Replaces
+ * ctox_pack_paged_kv_q4_batch_f32_sm86 (q2q4_fused_matvec_sm86.cu:1734-1799). */
+ctox_status ctox_hip_kv_pack_q4_device(ctox_hip_backend *backend, uint8_t *d_q4_pages, const float *d_keys,
+                                       const float *d_values, size_t token_count, size_t component_values,
+                                       uint32_t physical_slot, uint32_t first_token_in_page,
+                                       uint32_t q4_page_bytes, void *stream);
+/* Rewrite one Q4 page as Q2, byte-identical to QuantizedKvPage::requantize
+ * (Q/src/kv_cache.rs:216-236). Replaces ctox_demote_paged_kv_q4_to_q2_sm86
+ * (q2q4_fused_matvec_sm86.cu:1801-1834). */
+ctox_status ctox_hip_kv_demote_device(ctox_hip_backend *backend, const uint8_t *d_q4_page, uint8_t *d_q2_page,
+                                      size_t tokens, size_t blocks_per_token, void *stream);
+/* Grouped-query attention of query_tokens rows (d_query [rows][query_heads][256],
+ * the last rows cached tokens; row t sees tokens 0 ..= tokens - rows + t) over
+ * the paged cache; d_out [rows][query_heads][256]. Q/src/reference.rs:420-499
+ * over flattened pages (Q/src/kv_cache.rs:579-605). Replaces the split-KV pair
+ * ctox_paged_q2q4_gqa_split_partial/_combine_f32_sm86
+ * (q2q4_fused_matvec_sm86.cu:2296-2558) and the one-row decode kernel
+ * (:2026-2100). Limits: head_dim 256, (query_heads / key_value_heads) * rows <= 32. */
+ctox_status ctox_hip_paged_gqa_device(ctox_hip_backend *backend, const float *d_query, const uint8_t *d_q2_pages,
+                                      const uint8_t *d_q4_pages, const ctox_paged_kv_descriptor *d_descriptors,
+                                      const ctox_paged_gqa_params *params, size_t query_tokens, float *d_out,
+                                      void *stream);
+
 #ifdef __cplusplus
 }
 #endif
