@@ -209,6 +209,35 @@ def bench_token_selection(torch, hip, steps):
     return res
 
 
+def bench_paged_attention(torch, hip, steps, tokens=32768):
+    """Config 5's full-attention read: 24 query heads over 4 KV heads of 256,
+    `tokens` cached at page size 16 with the crate's 128-sink / 256-recent Q4
+    policy (older pages Q2), for the 1-row decode and the 5-row MTP verify."""
+    from ctox_hip.paged_kv import DevicePagedKvCache
+    qh, kvh, hd = 24, 4, 256
+    cache = DevicePagedKvCache(hip, tokens, kvh, hd, page_tokens=16, sink_tokens=128, recent_tokens=256)
+    g = torch.Generator(device="cuda").manual_seed(7)
+    for i in range(0, tokens, 4096):
+        n = min(4096, tokens - i)
+        cache.push(torch.randn(n, kvh * hd, device="cuda", generator=g),
+                   torch.randn(n, kvh * hd, device="cuda", generator=g))
+    kv_bytes = cache.q2_tokens() * cache.q2_token_bytes + cache.q4_tokens() * cache.q4_token_bytes
+    res = {"tokens": tokens, "page_tokens": 16, "q2_tokens": cache.q2_tokens(), "q4_tokens": cache.q4_tokens()}
+    for rows in (1, 5):
+        q = torch.randn(rows, qh, hd, device="cuda", generator=g)
+        out = torch.empty(rows, qh, hd, device="cuda")
+        cache.attention(q, rows, qh, out)
+        n = max(10, steps // 4)
+        with Timer(torch) as t:
+            for _ in range(n):
+                cache.attention(q, rows, qh, out)
+        us = t.ms * 1e3 / n
+        flops = 4.0 * qh * rows * tokens * hd
+        res[f"rows{rows}"] = {"us": us, "kv_bytes": kv_bytes, "GBps": kv_bytes / (us * 1e-6) / 1e9,
+                              "TFLOPs": flops / (us * 1e-6) / 1e12}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -251,6 +280,8 @@ def main():
         log("config4", extra["config4_gated_delta"])
         extra["config5_token_selection"] = bench_token_selection(torch, hip, args.steps)
         log("config5", extra["config5_token_selection"])
+        extra["config5_paged_attention"] = bench_paged_attention(torch, hip, args.steps)
+        log("config5 attention", extra["config5_paged_attention"])
 
     extra["copy_reference"] = copy_reference(torch)
     log("copy", extra["copy_reference"])

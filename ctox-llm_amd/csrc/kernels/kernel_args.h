@@ -265,4 +265,6 @@ struct GqaArgs {
     uint32_t tiles_per_wave;
     uint32_t splits;
     float scale;
+    uint32_t tile_pages;     // 1 when page_tokens % 16 == 0: a 16-token tile lies in one page
+    uint32_t pad;
 };

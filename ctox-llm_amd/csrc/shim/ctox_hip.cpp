@@ -1097,8 +1097,10 @@ extern "C" ctox_status ctox_hip_paged_gqa_device(ctox_hip_backend *b, const floa
         return fail(CTOX_ERR_SHAPE, "paged KV geometry differs from the attention contract");
     const uint32_t queries = group * (uint32_t)rows;
     const uint32_t tiles = (p->tokens + 15) / 16;
-    uint32_t splits = std::max<uint32_t>(1, (uint32_t)((b->cus + p->key_value_heads - 1) / p->key_value_heads));
-    splits = std::min<uint32_t>(splits, (tiles + 3) / 4);
+    // Two workgroups per CU for the 16-query kernel (it fits two per CU), one for the 32-query one.
+    const uint32_t per_cu = queries > 16 ? 1 : 2;
+    uint32_t splits = std::max<uint32_t>(1, (uint32_t)((per_cu * b->cus + p->key_value_heads - 1) / p->key_value_heads));
+    splits = std::min<uint32_t>(std::min<uint32_t>(splits, (tiles + 3) / 4), 1024);
     const uint32_t tpw = (tiles + 4 * splits - 1) / (4 * splits);
     splits = (tiles + 4 * tpw - 1) / (4 * tpw);
     const size_t part = (size_t)p->key_value_heads * splits * queries;
@@ -1108,7 +1110,7 @@ extern "C" ctox_status ctox_hip_paged_gqa_device(ctox_hip_backend *b, const floa
     GqaArgs a{d_query, d_q2_pages, d_q4_pages, (const PagedKvDesc *)d_descriptors, part_out, part_out + part * 256,
               d_out, p->q2_page_bytes, p->q4_page_bytes, p->query_heads, group, p->tokens, (uint32_t)rows, queries,
               p->page_tokens, p->page_count, (uint32_t)cv, p->q2_token_bytes, p->q4_token_bytes, tiles, tpw, splits,
-              p->scale};
+              p->scale, p->page_tokens % 16 == 0 ? 1u : 0u, 0};
     hipStream_t s = pick_stream(b, stream);
     st = launch(b->gqa_part[queries > 16 ? 1 : 0], dim3(splits, p->key_value_heads), dim3(256), s, a,
                 "ctox_paged_gqa_partial_gfx950");

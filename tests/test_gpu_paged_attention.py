@@ -104,6 +104,7 @@ def attention_case(hip, tokens, rows, page, sink, recent, seed):
 @pytest.mark.parametrize("tokens,rows,page,sink,recent", [
     (1, 1, 16, 0, 16), (7, 5, 16, 0, 16), (16, 1, 16, 16, 16), (37, 3, 16, 16, 16),
     (300, 5, 16, 32, 64), (300, 1, 16, 32, 64), (1000, 2, 128, 128, 256), (4096, 5, 128, 128, 256),
+    (300, 5, 24, 48, 64), (100, 3, 8, 0, 16),   # pages that split 16-token tiles
 ])
 def test_paged_attention_matches_oracle(hip, tokens, rows, page, sink, recent):
     say(f"case paged attention tokens={tokens} rows={rows} page={page}")
