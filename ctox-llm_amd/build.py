@@ -43,11 +43,12 @@ def build_kernels() -> str:
 def build_shim(hsaco: str) -> str:
     out = os.path.join(LIB, "libctox_hip.so")
     src = os.path.join(PKG, "csrc", "shim", "ctox_hip.cpp")
+    engine = os.path.join(PKG, "csrc", "shim", "engine.cpp")
     _run([
         "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra",
         "-D__HIP_PLATFORM_AMD__", f"-DCTOX_HSACO_PATH=\"{hsaco}\"",
         f"-I{os.path.join(ROOT, 'include')}", f"-I{os.path.join(ROCM, 'include')}",
-        src, "-o", out,
+        src, engine, "-o", out,
         f"-L{os.path.join(ROCM, 'lib')}", "-lamdhip64", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}",
     ])
     return out

@@ -6,3 +6,4 @@
 #include "decode_ops.hip"
 #include "layer_ops.hip"
 #include "paged_attention.hip"
+#include "engine_ops.hip"

@@ -32,9 +32,10 @@
 extern "C" __global__ __launch_bounds__(256) void ctox_gdn_gates_gfx950(GateArgs a) {
     const uint32_t e = blockIdx.x * 256 + threadIdx.x;
     if (e >= a.tokens * a.heads) return;
-    const uint32_t h = e % a.heads;
-    a.beta[e] = 1.0f / (1.0f + expf(-a.b[e]));
-    const float x = a.a[e] + a.dt_bias[h];
+    const uint32_t h = e % a.heads, t = e / a.heads;
+    const size_t in = (size_t)t * a.in_stride + h;
+    a.beta[e] = 1.0f / (1.0f + expf(-a.b[in]));
+    const float x = a.a[in] + a.dt_bias[h];
     const float sp = x > 20.0f ? x : log1pf(expf(x));
     a.log_decay[e] = -expf(a.a_log[h]) * sp;
 }

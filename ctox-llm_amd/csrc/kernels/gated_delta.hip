@@ -50,11 +50,12 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_scan_gfx950(GdnArgs a
 
     for (uint32_t t = 0; t < a.tokens; t++) {
         const size_t th = (size_t)t * a.heads + h;
-        const float *q = a.q + th * a.key_dim;
-        const float *k = a.k + th * a.key_dim;
+        const size_t qk = (size_t)t * a.qk_stride + (size_t)(h / a.rep) * a.key_dim;
+        const float *q = a.q + qk;
+        const float *k = a.k + qk;
         const float decay = expf(a.log_decay[th]);
         const float beta = a.beta[th];
-        const float vj = colok ? a.v[th * a.value_dim + j] : 0.0f;
+        const float vj = colok ? a.v[(size_t)t * a.v_stride + (size_t)h * a.value_dim + j] : 0.0f;
 
         float kk[GDN_MAX_ROWS], qq[GDN_MAX_ROWS];
         float mem = 0.0f, sk = 0.0f, sq = 0.0f;

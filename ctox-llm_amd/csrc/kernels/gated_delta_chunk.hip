@@ -59,8 +59,9 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_prep_gfx950(Gdn
         const uint32_t s = tid >> 2, p = tid & 3;
         float sk = 0.0f, sq = 0.0f;
         if (s < n) {
-            const float *kr = a.k + ((size_t)(t0 + s) * a.heads + h) * dk;
-            const float *qr = a.q + ((size_t)(t0 + s) * a.heads + h) * dk;
+            const size_t qk = (size_t)(t0 + s) * a.qk_stride + (size_t)(h / a.rep) * dk;
+            const float *kr = a.k + qk;
+            const float *qr = a.q + qk;
             for (uint32_t i = p; i < dk; i += 4) {
                 const float kv = kr[i], qv = qr[i];
                 kh[s * GPAD + i] = kv;
@@ -214,14 +215,14 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_scan_gfx950(Gdn
     const uint32_t nch = (a.tokens + a.chunk - 1) / a.chunk;
     const uint32_t dk = a.key_dim, dv = a.value_dim;
     const float qscale = 1.0f / sqrtf((float)dk);
-    const size_t rowq = (size_t)a.heads * dk, rowv = (size_t)a.heads * dv;
+    const size_t rowv = (size_t)a.heads * dv;
     float *S = a.state + (size_t)h * dk * dv;
     for (uint32_t e = tid; e < GKD * GVS; e += 256) {
         const uint32_t i = e / GVS, n = e % GVS;
         st[0][n * SPAD + i] = (i < dk && j0 + n < dv) ? S[(size_t)i * dv + j0 + n] : 0.0f;
     }
-    const bool vec_k = (dk & 3) == 0 && (((uintptr_t)a.k | (uintptr_t)a.q) & 15) == 0;
-    const bool vec_v = (dv & 3) == 0 && (j0 + GVS <= dv) && (((uintptr_t)a.v) & 15) == 0;
+    const bool vec_k = (dk & 3) == 0 && (a.qk_stride & 3) == 0 && (((uintptr_t)a.k | (uintptr_t)a.q) & 15) == 0;
+    const bool vec_v = (dv & 3) == 0 && (a.v_stride & 3) == 0 && (j0 + GVS <= dv) && (((uintptr_t)a.v) & 15) == 0;
 
     auto fetch = [&](GdnPrefetch &p, uint32_t c) {
         const uint32_t t0 = c * a.chunk, n = min(a.chunk, a.tokens - t0);
@@ -230,7 +231,7 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_scan_gfx950(Gdn
         for (int m = 0; m < 8; m++) {
             const uint32_t f = tid + 256 * m, s = f >> 5, i = (f & 31) * 4;
             const bool ok = s < n && i < dk;
-            const size_t off = (size_t)(t0 + (ok ? s : 0)) * rowq + (size_t)h * dk + (ok ? i : 0);
+            const size_t off = (size_t)(t0 + (ok ? s : 0)) * a.qk_stride + (size_t)(h / a.rep) * dk + (ok ? i : 0);
             if (vec_k) {
                 p.k[m] = ok ? *(const float4 *)(a.k + off) : make_float4(0, 0, 0, 0);
                 p.q[m] = ok ? *(const float4 *)(a.q + off) : make_float4(0, 0, 0, 0);
@@ -254,7 +255,7 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_scan_gfx950(Gdn
         {
             const uint32_t s = tid >> 2, part = tid & 3;
             const bool ok = s < n;
-            const size_t off = (size_t)(t0 + (ok ? s : 0)) * rowv + (size_t)h * dv + j0 + 4 * part;
+            const size_t off = (size_t)(t0 + (ok ? s : 0)) * a.v_stride + (size_t)h * dv + j0 + 4 * part;
             if (vec_v) {
                 p.v = ok ? *(const float4 *)(a.v + off) : make_float4(0, 0, 0, 0);
             } else {

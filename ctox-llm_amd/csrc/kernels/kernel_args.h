@@ -100,6 +100,9 @@ struct GdnArgs {
     uint32_t key_dim;
     uint32_t value_dim;
     uint32_t chunk;
+    uint32_t rep;           // value heads per key head: q, k of head h are key head h / rep
+    uint32_t qk_stride;     // floats between tokens of q and of k
+    uint32_t v_stride;      // floats between tokens of v
     uint32_t pad;
 };
 
@@ -113,6 +116,8 @@ struct GateArgs {
     float *beta;             // [tokens][heads]
     uint32_t tokens;
     uint32_t heads;
+    uint32_t in_stride;      // floats between tokens of a and of b
+    uint32_t pad;
 };
 
 struct RepeatArgs {
@@ -202,6 +207,8 @@ struct ConvArgs {
     float *out;              // [channels]
     uint32_t channels;
     uint32_t kernel;
+    uint32_t rows;           // consecutive tokens, applied in order
+    uint32_t in_stride;      // floats between tokens of input (out is dense)
 };
 
 struct RopeArgs {
@@ -267,4 +274,68 @@ struct GqaArgs {
     float scale;
     uint32_t tile_pages;     // 1 when page_tokens % 16 == 0: a 16-token tile lies in one page
     uint32_t pad;
+};
+
+// Decode engine helpers (engine_ops.hip).
+struct FillArgs {
+    void *ptr;
+    uint64_t count;          // elements (kinds 2..4) or blocks (kinds 0, 1) of this launch
+    uint64_t index_base;     // global index of element 0 (keeps chunked fills reproducible)
+    uint64_t seed;
+    uint32_t kind;           // 0 Q4 blocks, 1 Q2 blocks, 2 f32 normal, 3 f16 uniform, 4 f32 uniform
+    float p0;                // mean (2) or low bound (3, 4)
+    float p1;                // std (2), high bound (3, 4), scale sigma (0, 1)
+    uint32_t pad;
+};
+
+struct EmbedArgs {
+    const uint8_t *weights;  // [vocab][cols / 64] blocks
+    const uint16_t *s_in;    // [cols] fp16 or NULL
+    const uint16_t *s_out;   // [vocab] fp16 or NULL
+    const uint32_t *tokens;  // [rows] on the device
+    float *out;              // [rows][cols]
+    uint32_t cols;
+    uint32_t vocab;
+    uint32_t dtype;          // 0 Q2, 1 Q4
+    uint32_t pad;
+};
+
+struct NormRowsArgs {
+    float *x;                // rows at (r / inner) * x_outer + (r % inner) * x_inner
+    const float *delta;      // [rows][cols] added to x first (x updated) or NULL
+    const float *gate;       // mode 1, same two-level addressing with g_*
+    const float *w;          // [cols]
+    float *out;              // rows at r * out_stride
+    uint32_t cols;
+    uint32_t mode;           // 0: (1 + w); 1: w * silu(gate)
+    float eps;
+    uint32_t inner;
+    uint64_t x_inner, x_outer, g_inner, g_outer, out_stride;
+};
+
+struct AttnGateArgs {
+    float *values;           // [rows][heads][head_dim]
+    const float *qg;         // token rows of q_proj output: per head [q (head_dim), gate (head_dim)]
+    uint32_t rows;
+    uint32_t heads;
+    uint32_t head_dim;
+    uint32_t qg_stride;      // floats between tokens of qg
+};
+
+struct RowsArgs {
+    const float *in;
+    float *out;
+    uint32_t rows;
+    uint32_t cols;
+    uint32_t in_stride;
+    uint32_t out_stride;
+    uint32_t offset;         // swiglu: offset of up within an input row; copy: offset of the copied columns
+    uint32_t pad;
+};
+
+struct WordsArgs {           // small host-to-device writes carried in the kernel arguments
+    uint32_t *dst;
+    uint32_t count;          // <= 32
+    uint32_t pad;
+    uint32_t words[32];
 };

@@ -51,16 +51,18 @@ extern "C" __global__ __launch_bounds__(256) void ctox_conv_update_gfx950(ConvAr
     if (c >= a.channels) return;
     float *s = a.state + (size_t)c * a.kernel;
     const float *w = a.weight + (size_t)c * a.kernel;
-    float sum = 0.0f;
-    for (uint32_t i = 0; i + 1 < a.kernel; i++) {
-        const float v = s[i + 1];
-        s[i] = v;
-        sum += v * w[i];
+    for (uint32_t t = 0; t < a.rows; t++) {
+        float sum = 0.0f;
+        for (uint32_t i = 0; i + 1 < a.kernel; i++) {
+            const float v = s[i + 1];
+            s[i] = v;
+            sum += v * w[i];
+        }
+        const float x = a.input[(size_t)t * a.in_stride + c];
+        s[a.kernel - 1] = x;
+        sum += x * w[a.kernel - 1];
+        a.out[(size_t)t * a.channels + c] = silu_f(sum);
     }
-    const float x = a.input[c];
-    s[a.kernel - 1] = x;
-    sum += x * w[a.kernel - 1];
-    a.out[c] = silu_f(sum);
 }
 
 // grid (rows, qh + kh), block = rd / 2 threads (<= 256).

@@ -135,7 +135,8 @@ struct ctox_hip_backend {
                   repeat = nullptr, partials = nullptr, argmax_final = nullptr, verify = nullptr, decide = nullptr,
                   pick_sums = nullptr, pick_final = nullptr, rms = nullptr, swiglu = nullptr, sgate = nullptr,
                   conv = nullptr, rope = nullptr, kv_pack = nullptr, kv_demote = nullptr, gqa_part[2] = {},
-                  gqa_combine = nullptr;
+                  gqa_combine = nullptr, fill = nullptr, embed = nullptr, norm_rows = nullptr, attn_gate = nullptr,
+                  swiglu_rows = nullptr, copy_rows = nullptr, write_words = nullptr;
     // Batch-1 slice kernels per dtype [Q2, Q4]: [0] walks the slices, [n]
     // requests all n slices up front.
     hipFunction_t sl[2][4] = {};
@@ -435,6 +436,10 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->gqa_part[0], "ctox_paged_gqa_partial_r1_gfx950"},
                {&b->gqa_part[1], "ctox_paged_gqa_partial_r2_gfx950"},
                {&b->gqa_combine, "ctox_paged_gqa_combine_gfx950"},
+               {&b->fill, "ctox_fill_random_gfx950"},      {&b->embed, "ctox_embed_rows_gfx950"},
+               {&b->norm_rows, "ctox_norm_rows_gfx950"},   {&b->attn_gate, "ctox_attn_gate_gfx950"},
+               {&b->swiglu_rows, "ctox_swiglu_rows_gfx950"}, {&b->copy_rows, "ctox_copy_rows_gfx950"},
+               {&b->write_words, "ctox_write_words_gfx950"},
                {&b->sl[0][0], "ctox_q2_matvec_sl_gfx950"}, {&b->sl[0][1], "ctox_q2_matvec_sl1_gfx950"},
                {&b->sl[0][2], "ctox_q2_matvec_sl2_gfx950"}, {&b->sl[0][3], "ctox_q2_matvec_sl3_gfx950"},
                {&b->sl[1][0], "ctox_q4_matvec_sl_gfx950"}, {&b->sl[1][1], "ctox_q4_matvec_sl1_gfx950"},
@@ -475,6 +480,9 @@ extern "C" const char *ctox_hip_backend_kind(const ctox_hip_backend *) { return 
 extern "C" const char *ctox_hip_backend_promotion_state(const ctox_hip_backend *) { return "experimental"; }
 extern "C" const char *ctox_hip_backend_profile(const ctox_hip_backend *) { return "gfx950-mfma-i8"; }
 extern "C" const char *ctox_hip_last_error(void) { return g_last_error.c_str(); }
+
+// Error text of the engine translation unit (same thread-local slot).
+void ctox_set_last_error(const char *msg) { g_last_error = msg; }
 
 extern "C" ctox_status ctox_hip_synchronize(ctox_hip_backend *b) {
     if (!b) return fail(CTOX_ERR_INVALID_STATE, "null backend");
@@ -751,11 +759,20 @@ ctox_status gdn_shape(size_t tokens, size_t heads, size_t kd, size_t vd) {
     return CTOX_OK;
 }
 
+// key_heads = 0 means heads (no repeat); strides of 0 mean dense token rows.
 ctox_status gdn_device(ctox_hip_backend *b, const float *q, const float *k, const float *v, const float *ld,
                        const float *beta, float *state, size_t tokens, size_t heads, size_t kd, size_t vd,
-                       size_t chunk, float *out, hipStream_t s) {
+                       size_t chunk, float *out, hipStream_t s, size_t key_heads = 0, size_t qk_stride = 0,
+                       size_t v_stride = 0) {
     ctox_status st = gdn_shape(tokens, heads, kd, vd);
     if (st) return st;
+    if (key_heads == 0) key_heads = heads;
+    if (qk_stride == 0) qk_stride = key_heads * kd;
+    if (v_stride == 0) v_stride = heads * vd;
+    // Q/src/decoder.rs:868-880: value heads repeat whole key heads.
+    if (heads % key_heads || qk_stride < key_heads * kd || v_stride < heads * vd || qk_stride > 0xffffffffu ||
+        v_stride > 0xffffffffu)
+        return fail(CTOX_ERR_SHAPE, "delta head repeat or token strides do not fit the heads");
     // chunk >= 1 selects the chunked (WY) prefill for key/value dims up to
     // 128 and chunks up to 64 tokens; otherwise the token-serial scan.
     const bool chunked = tokens > 1 && chunk >= 1 && chunk <= 64 && kd <= 128 && vd <= 128;
@@ -777,6 +794,9 @@ ctox_status gdn_device(ctox_hip_backend *b, const float *q, const float *k, cons
     a.key_dim = (uint32_t)kd;
     a.value_dim = (uint32_t)vd;
     a.chunk = (uint32_t)chunk;
+    a.rep = (uint32_t)(heads / key_heads);
+    a.qk_stride = (uint32_t)qk_stride;
+    a.v_stride = (uint32_t)v_stride;
     const size_t slices = (vd + 15) / 16;
     if (chunked) {
         st = launch(b->gdn_chunk_prep, dim3((unsigned)(heads * nch)), dim3(256), s, a, "ctox_gdn_chunk_prep_gfx950");
@@ -874,6 +894,18 @@ extern "C" ctox_status ctox_hip_gated_delta_sequence_device(ctox_hip_backend *b,
                       pick_stream(b, stream));
 }
 
+extern "C" ctox_status ctox_hip_gated_delta_strided_device(ctox_hip_backend *b, const float *q, const float *k,
+                                                           const float *v, size_t qk_stride, size_t v_stride,
+                                                           const float *log_decay, const float *beta, float *state,
+                                                           size_t tokens, size_t heads, size_t key_heads,
+                                                           size_t key_dim, size_t value_dim, size_t chunk,
+                                                           float *out, void *stream) {
+    if (!b || !q || !k || !v || !log_decay || !beta || !state || !out) return fail(CTOX_ERR_SHAPE, "null argument");
+    if (key_heads == 0) return fail(CTOX_ERR_SHAPE, "delta key heads must be non-zero");
+    return gdn_device(b, q, k, v, log_decay, beta, state, tokens, heads, key_dim, value_dim, chunk, out,
+                      pick_stream(b, stream), key_heads, qk_stride, v_stride);
+}
+
 // ======================================================================
 // decode-step glue and token selection
 // ======================================================================
@@ -887,7 +919,21 @@ extern "C" ctox_status ctox_hip_gdn_gates_device(ctox_hip_backend *b, const floa
     if (!b || !d_a || !d_b || !d_a_log || !d_dt_bias || !d_log_decay || !d_beta)
         return fail(CTOX_ERR_SHAPE, "null argument");
     if (tokens == 0 || heads == 0 || tokens * heads > 0x7fffffffu) return fail(CTOX_ERR_SHAPE, "gate shapes");
-    GateArgs a{d_a, d_b, d_a_log, d_dt_bias, d_log_decay, d_beta, (uint32_t)tokens, (uint32_t)heads};
+    GateArgs a{d_a, d_b, d_a_log, d_dt_bias, d_log_decay, d_beta, (uint32_t)tokens, (uint32_t)heads, (uint32_t)heads, 0};
+    return launch(b->gates, dim3((unsigned)((tokens * heads + 255) / 256)), dim3(256), pick_stream(b, stream), a,
+                  "ctox_gdn_gates_gfx950");
+}
+
+extern "C" ctox_status ctox_hip_gdn_gates_strided_device(ctox_hip_backend *b, const float *d_a, const float *d_b,
+                                                         size_t in_stride, const float *d_a_log,
+                                                         const float *d_dt_bias, size_t tokens, size_t heads,
+                                                         float *d_log_decay, float *d_beta, void *stream) {
+    if (!b || !d_a || !d_b || !d_a_log || !d_dt_bias || !d_log_decay || !d_beta)
+        return fail(CTOX_ERR_SHAPE, "null argument");
+    if (tokens == 0 || heads == 0 || tokens * heads > 0x7fffffffu || in_stride < heads || in_stride > 0x7fffffffu)
+        return fail(CTOX_ERR_SHAPE, "gate shapes");
+    GateArgs a{d_a, d_b, d_a_log, d_dt_bias, d_log_decay, d_beta, (uint32_t)tokens, (uint32_t)heads,
+               (uint32_t)in_stride, 0};
     return launch(b->gates, dim3((unsigned)((tokens * heads + 255) / 256)), dim3(256), pick_stream(b, stream), a,
                   "ctox_gdn_gates_gfx950");
 }
@@ -1021,7 +1067,7 @@ extern "C" ctox_status ctox_hip_causal_conv_update_device(ctox_hip_backend *b, c
     if (!b || !d_input || !d_state || !d_weight || !d_out) return fail(CTOX_ERR_SHAPE, "null argument");
     if (channels == 0 || kernel == 0 || channels > 0x7fffffffu || kernel > 4096)
         return fail(CTOX_ERR_SHAPE, "conv state shape is empty or too large");
-    ConvArgs a{d_input, d_state, d_weight, d_out, (uint32_t)channels, (uint32_t)kernel};
+    ConvArgs a{d_input, d_state, d_weight, d_out, (uint32_t)channels, (uint32_t)kernel, 1, (uint32_t)channels};
     return launch(b->conv, dim3((unsigned)((channels + 255) / 256)), dim3(256), pick_stream(b, stream), a,
                   "ctox_conv_update_gfx950");
 }
@@ -1118,3 +1164,115 @@ extern "C" ctox_status ctox_hip_paged_gqa_device(ctox_hip_backend *b, const floa
     return launch(b->gqa_combine, dim3(queries, p->key_value_heads), dim3(256), s, a, "ctox_paged_gqa_combine_gfx950");
 }
 static_assert(sizeof(ctox_paged_kv_descriptor) == sizeof(PagedKvDesc), "page descriptor layout");
+
+extern "C" ctox_status ctox_hip_causal_conv_rows_device(ctox_hip_backend *b, const float *d_input, size_t in_stride,
+                                                        float *d_state, const float *d_weight, size_t channels,
+                                                        size_t kernel, size_t rows, float *d_out, void *stream) {
+    if (!b || !d_input || !d_state || !d_weight || !d_out) return fail(CTOX_ERR_SHAPE, "null argument");
+    if (channels == 0 || kernel == 0 || channels > 0x7fffffffu || kernel > 4096 || rows == 0 || rows > 65536 ||
+        in_stride < channels || in_stride > 0x7fffffffu)
+        return fail(CTOX_ERR_SHAPE, "conv state shape is empty or too large");
+    ConvArgs a{d_input, d_state, d_weight, d_out, (uint32_t)channels, (uint32_t)kernel, (uint32_t)rows,
+               (uint32_t)in_stride};
+    return launch(b->conv, dim3((unsigned)((channels + 255) / 256)), dim3(256), pick_stream(b, stream), a,
+                  "ctox_conv_update_gfx950");
+}
+
+// ======================================================================
+// decode engine helpers
+// ======================================================================
+extern "C" ctox_status ctox_hip_fill_random_device(ctox_hip_backend *b, void *d_ptr, uint64_t count, uint32_t kind,
+                                                   uint64_t seed, float p0, float p1, void *stream) {
+    if (!b || !d_ptr) return fail(CTOX_ERR_SHAPE, "null argument");
+    if (kind > 4 || !std::isfinite(p0) || !std::isfinite(p1)) return fail(CTOX_ERR_SHAPE, "invalid fill request");
+    const size_t unit = kind == 0 ? 34 : kind == 1 ? 18 : kind == 3 ? 2 : 4;
+    hipStream_t s = pick_stream(b, stream);
+    const uint64_t chunk = (uint64_t)1 << 26;
+    for (uint64_t base = 0; base < count; base += chunk) {
+        const uint64_t n = std::min<uint64_t>(chunk, count - base);
+        FillArgs a{(char *)d_ptr + base * unit, n, base, seed, kind, p0, p1, 0};
+        ctox_status st = launch(b->fill, dim3((unsigned)((n + 255) / 256)), dim3(256), s, a, "ctox_fill_random_gfx950");
+        if (st) return st;
+    }
+    return CTOX_OK;
+}
+
+extern "C" ctox_status ctox_hip_embedding_rows_device(ctox_hip_backend *b, int32_t dtype, const uint8_t *d_weights,
+                                                      const uint16_t *d_s_in, const uint16_t *d_s_out,
+                                                      const uint32_t *d_tokens, size_t rows, size_t vocab,
+                                                      size_t cols, float *d_out, void *stream) {
+    if (!b || !d_weights || !d_tokens || !d_out) return fail(CTOX_ERR_SHAPE, "null argument");
+    if (dtype != CTOX_DTYPE_Q2B64 && dtype != CTOX_DTYPE_Q4B64) return fail(CTOX_ERR_UNSUPPORTED_DTYPE, "embedding rows must be Q2 or Q4");
+    if (rows == 0 || rows > 65535 || cols == 0 || cols % 64 || cols > 0x7fffffffu || vocab == 0 || vocab > 0xffffffffu)
+        return fail(CTOX_ERR_SHAPE, "embedding shape is empty or too large");
+    EmbedArgs a{d_weights, d_s_in, d_s_out, d_tokens, d_out, (uint32_t)cols, (uint32_t)vocab,
+                dtype == CTOX_DTYPE_Q4B64 ? 1u : 0u, 0};
+    return launch(b->embed, dim3((unsigned)((cols + 255) / 256), (unsigned)rows), dim3(256), pick_stream(b, stream), a,
+                  "ctox_embed_rows_gfx950");
+}
+
+extern "C" ctox_status ctox_hip_norm_rows_device(ctox_hip_backend *b, const ctox_norm_rows *d, void *stream) {
+    if (!b || !d || !d->x || !d->w || !d->out || (d->mode == 1 && !d->gate)) return fail(CTOX_ERR_SHAPE, "null argument");
+    if (d->rows == 0 || d->cols == 0 || d->inner == 0 || d->mode > 1)
+        return fail(CTOX_ERR_SHAPE, "norm rows shape is empty or mode unknown");
+    if (!std::isfinite(d->eps) || d->eps <= 0.0f) return fail(CTOX_ERR_SHAPE, "norm epsilon must be finite and positive");
+    NormRowsArgs a{d->x, d->delta, d->gate, d->w, d->out, d->cols, d->mode, d->eps, d->inner,
+                   d->x_inner, d->x_outer, d->g_inner, d->g_outer, d->out_stride};
+    return launch(b->norm_rows, dim3(d->rows), dim3(256), pick_stream(b, stream), a, "ctox_norm_rows_gfx950");
+}
+
+extern "C" ctox_status ctox_hip_attention_gate_device(ctox_hip_backend *b, float *d_values, const float *d_qg,
+                                                      size_t rows, size_t heads, size_t head_dim, size_t qg_stride,
+                                                      void *stream) {
+    if (!b || !d_values || !d_qg) return fail(CTOX_ERR_SHAPE, "null argument");
+    const uint64_t n = (uint64_t)rows * heads * head_dim;
+    if (n == 0 || (n + 255) / 256 > 0x7fffffffu || qg_stride < 2 * heads * head_dim || qg_stride > 0xffffffffu)
+        return fail(CTOX_ERR_SHAPE, "attention gate shape");
+    AttnGateArgs a{d_values, d_qg, (uint32_t)rows, (uint32_t)heads, (uint32_t)head_dim, (uint32_t)qg_stride};
+    return launch(b->attn_gate, dim3((unsigned)((n + 255) / 256)), dim3(256), pick_stream(b, stream), a,
+                  "ctox_attn_gate_gfx950");
+}
+
+namespace {
+ctox_status rows_launch(ctox_hip_backend *b, hipFunction_t f, const float *in, size_t in_stride, size_t offset,
+                        size_t rows, size_t cols, float *out, size_t out_stride, void *stream, const char *name) {
+    if (!b || !in || !out) return fail(CTOX_ERR_SHAPE, "null argument");
+    const uint64_t n = (uint64_t)rows * cols;
+    if (n == 0 || (n + 255) / 256 > 0x7fffffffu || in_stride > 0xffffffffu || out_stride > 0xffffffffu ||
+        offset > 0xffffffffu || out_stride < cols)
+        return fail(CTOX_ERR_SHAPE, "%s shape", name);
+    RowsArgs a{in, out, (uint32_t)rows, (uint32_t)cols, (uint32_t)in_stride, (uint32_t)out_stride, (uint32_t)offset, 0};
+    return launch(f, dim3((unsigned)((n + 255) / 256)), dim3(256), pick_stream(b, stream), a, name);
+}
+}  // namespace
+
+extern "C" ctox_status ctox_hip_swiglu_rows_device(ctox_hip_backend *b, const float *d_in, size_t in_stride,
+                                                   size_t up_offset, size_t rows, size_t cols, float *d_out,
+                                                   size_t out_stride, void *stream) {
+    if (up_offset < cols || in_stride < up_offset + cols) return fail(CTOX_ERR_SHAPE, "swiglu rows geometry");
+    return rows_launch(b, b ? b->swiglu_rows : nullptr, d_in, in_stride, up_offset, rows, cols, d_out, out_stride,
+                       stream, "ctox_swiglu_rows_gfx950");
+}
+
+extern "C" ctox_status ctox_hip_copy_rows_device(ctox_hip_backend *b, const float *d_in, size_t in_stride,
+                                                 size_t col_offset, size_t rows, size_t cols, float *d_out,
+                                                 size_t out_stride, void *stream) {
+    if (in_stride < col_offset + cols) return fail(CTOX_ERR_SHAPE, "copy rows geometry");
+    return rows_launch(b, b ? b->copy_rows : nullptr, d_in, in_stride, col_offset, rows, cols, d_out, out_stride,
+                       stream, "ctox_copy_rows_gfx950");
+}
+
+extern "C" ctox_status ctox_hip_write_words_device(ctox_hip_backend *b, uint32_t *d_dst, const uint32_t *words,
+                                                   size_t count, void *stream) {
+    if (!b || !d_dst || (!words && count)) return fail(CTOX_ERR_SHAPE, "null argument");
+    hipStream_t s = pick_stream(b, stream);
+    for (size_t i = 0; i < count; i += 32) {
+        WordsArgs a{};
+        a.dst = d_dst + i;
+        a.count = (uint32_t)std::min<size_t>(32, count - i);
+        std::memcpy(a.words, words + i, a.count * sizeof(uint32_t));
+        ctox_status st = launch(b->write_words, dim3(1), dim3(64), s, a, "ctox_write_words_gfx950");
+        if (st) return st;
+    }
+    return CTOX_OK;
+}

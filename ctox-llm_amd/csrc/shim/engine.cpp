@@ -1,0 +1,821 @@
+// Device-resident Qwen3.8 decode engine over the ctox_hip C ABI.
+//
+// The crate's model graph (Q/src/decoder.rs) composed from the HIP entry
+// points: every tensor and state lives in HBM, one process drives one GPU,
+// and a step is a sequence of launches on one stream with a single
+// device-to-host read (the speculative result) per MTP step.
+//
+//  * Target step over R rows (R = 1 decode, R = k + 1 MTP verification):
+//    embedding (decoder.rs:531-537), per layer a GatedDeltaNet
+//    (decoder.rs:806-938) or full-attention (:687-800) token mixer, the MLP
+//    (:636-670), the final norm and the LM head (:940-951). Residual adds are
+//    folded into the next RMS norm; projections that share an input are one
+//    row-concatenated matrix (qkv|z|a|b, q|k|v, gate|up), which computes the
+//    same rows as the crate's fan-out (cpu.rs:444-472) because rows are
+//    independent and their s_in is shared.
+//  * MTP draft (decoder.rs:1009-1046): embed, the two pre-fc norms, fc over
+//    [embedding, hidden], one full-attention layer with its own paged cache,
+//    the MLP, the MTP norm, the shared LM head; the token is sampled at the
+//    requested temperature from the crate's Pcg32 stream.
+//  * Speculative step: k chained drafts (each fed the previous draft's MTP
+//    hidden), one batched target pass over [t0, d1..dk], rejection-sampling
+//    acceptance (ctox_hip_mtp_accept_device), then commit: GatedDeltaNet and
+//    conv states are restored from a checkpoint and replayed over the
+//    committed tokens, paged caches are truncated, and the MTP cache is
+//    replayed with target hiddens as commit_speculative does
+//    (decoder.rs:1397-1458).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "ctox_hip.h"
+
+void ctox_set_last_error(const char *msg);  // ctox_hip.cpp
+
+namespace {
+
+struct Mat {
+    int32_t dtype = CTOX_DTYPE_Q4B64;
+    uint32_t rows = 0, cols = 0;
+    uint8_t *w = nullptr;
+    uint16_t *s_in = nullptr, *s_out = nullptr;
+    size_t bytes() const { return (size_t)rows * (cols / 64) * (dtype == CTOX_DTYPE_Q4B64 ? 34 : 18); }
+};
+
+struct Mlp {
+    float *norm = nullptr;  // post_attention_layernorm
+    Mat gate_up, down;
+};
+
+struct GdnLayer {
+    float *norm = nullptr;  // input_layernorm
+    Mat in;                 // [qkv | z | a | b]
+    float *conv_w = nullptr, *a_log = nullptr, *dt_bias = nullptr, *gnorm = nullptr;
+    Mat out;
+    float *state = nullptr, *conv = nullptr;  // views into the engine's state blocks
+    float *proj = nullptr, *ld = nullptr, *beta = nullptr;  // per-layer rows kept for the commit replay
+};
+
+// Host bookkeeping of one paged cache (Q/src/kv_cache.rs:303-478 policy).
+struct Cache {
+    uint8_t *q4 = nullptr, *q2 = nullptr;
+    ctox_paged_kv_descriptor *d_desc = nullptr;
+    std::vector<ctox_paged_kv_descriptor> desc;
+    std::vector<uint32_t> free_q4, free_q2;
+    uint32_t pages = 0, tokens = 0;
+    uint32_t dirty = 0;  // lowest page whose descriptor changed since the last upload
+};
+
+struct AttnLayer {
+    float *norm = nullptr;
+    Mat qkv;                // [q|gate per head, k, v]
+    float *q_norm = nullptr, *k_norm = nullptr;
+    Mat o;
+    Cache cache;
+};
+
+struct Layer {
+    bool full = false;
+    GdnLayer g;
+    AttnLayer f;
+    Mlp mlp;
+};
+
+}  // namespace
+
+struct ctox_hip_engine {
+    ctox_hip_backend *b = nullptr;
+    ctox_engine_config c{};
+    hipStream_t s = nullptr;
+    std::vector<void *> allocs;
+    std::vector<Layer> layers;
+    Mat embed, lm_head;
+    float *final_norm = nullptr;
+    // MTP
+    bool mtp = false;
+    float *mtp_norm_emb = nullptr, *mtp_norm_hid = nullptr, *mtp_norm = nullptr;
+    Mat mtp_fc;
+    AttnLayer mtp_attn;
+    Mlp mtp_mlp;
+    // geometry
+    uint32_t H = 0, I = 0, Kw = 0, Vw = 0, C = 0, Rin = 0, Rq = 0, kvw = 0, V = 0, R = 0;
+    uint32_t q4_token_bytes = 0, q2_token_bytes = 0, q4_page_bytes = 0, q2_page_bytes = 0;
+    // state blocks
+    float *gdn_state = nullptr, *gdn_ckpt = nullptr, *conv_state = nullptr, *conv_ckpt = nullptr;
+    size_t gdn_floats = 0, conv_floats = 0;
+    // activations (sized for R rows)
+    float *hid = nullptr, *xn = nullptr, *proj = nullptr, *convo = nullptr, *core = nullptr, *coren = nullptr,
+          *delta = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *gu = nullptr, *act = nullptr,
+          *fin = nullptr, *logits = nullptr, *ld = nullptr, *beta = nullptr, *fcin = nullptr;
+    float *draft_logits = nullptr, *mtp_hidden = nullptr, *prev_hidden = nullptr, *target_hidden = nullptr;
+    uint32_t *d_tokens = nullptr, *d_drafts = nullptr, *d_result = nullptr;
+    uint64_t *d_rng = nullptr;
+    uint32_t position = 0;   // tokens processed by the target model
+    uint32_t mtp_tokens = 0; // entries in the MTP cache
+    bool have_prev = false;  // prev_hidden holds the last target final hidden
+};
+
+namespace {
+
+ctox_status efail(ctox_status st, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    ctox_set_last_error(buf);
+    return st;
+}
+
+#define TRY(x)                                  \
+    do {                                        \
+        ctox_status st_ = (x);                  \
+        if (st_ != CTOX_OK) return st_;         \
+    } while (0)
+
+ctox_status dalloc(ctox_hip_engine *e, void **p, size_t bytes) {
+    if (bytes == 0) bytes = 256;
+    if (hipMalloc(p, bytes) != hipSuccess) return efail(CTOX_ERR_MEMORY_BUDGET, "device allocation of %zu bytes failed", bytes);
+    e->allocs.push_back(*p);
+    return CTOX_OK;
+}
+
+template <typename T>
+ctox_status dalloc_t(ctox_hip_engine *e, T **p, size_t count) {
+    return dalloc(e, (void **)p, count * sizeof(T));
+}
+
+ctox_status fill(ctox_hip_engine *e, void *p, uint64_t n, uint32_t kind, uint64_t seed, float p0, float p1) {
+    return ctox_hip_fill_random_device(e->b, p, n, kind, seed, p0, p1, e->s);
+}
+
+// A quantized matrix with fp16 s_in / s_out in U(0.75, 1.25) and block scales |N(0, 0.02)|.
+ctox_status make_mat(ctox_hip_engine *e, Mat &m, int32_t dtype, uint32_t rows, uint32_t cols, uint64_t &seed,
+                     uint16_t *shared_s_in = nullptr) {
+    m.dtype = dtype;
+    m.rows = rows;
+    m.cols = cols;
+    TRY(dalloc(e, (void **)&m.w, m.bytes()));
+    TRY(fill(e, m.w, (uint64_t)rows * (cols / 64), dtype == CTOX_DTYPE_Q4B64 ? 0 : 1, seed++, 0.0f, 0.02f));
+    if (shared_s_in) {
+        m.s_in = shared_s_in;
+    } else {
+        TRY(dalloc_t(e, &m.s_in, cols));
+        TRY(fill(e, m.s_in, cols, 3, seed++, 0.75f, 1.25f));
+    }
+    TRY(dalloc_t(e, &m.s_out, rows));
+    TRY(fill(e, m.s_out, rows, 3, seed++, 0.75f, 1.25f));
+    return CTOX_OK;
+}
+
+ctox_status make_vec(ctox_hip_engine *e, float **p, size_t n, uint64_t &seed, float mean, float std) {
+    TRY(dalloc_t(e, p, n));
+    return fill(e, *p, n, 2, seed++, mean, std);
+}
+
+ctox_status matvec(ctox_hip_engine *e, const Mat &m, const float *in, float *out, uint32_t rows) {
+    return ctox_hip_launch_fused_matvec(e->b, m.dtype, m.w, in, m.s_in, m.s_out, nullptr, out, m.rows, m.cols, 0, rows,
+                                        e->s);
+}
+
+// Norm of `rows` dense rows of width cols; x += delta first when delta is set.
+ctox_status norm(ctox_hip_engine *e, float *x, const float *delta, const float *w, uint32_t rows, uint32_t cols,
+                 float *out, size_t out_stride) {
+    ctox_norm_rows d{};
+    d.x = x;
+    d.delta = delta;
+    d.w = w;
+    d.out = out;
+    d.rows = rows;
+    d.cols = cols;
+    d.mode = 0;
+    d.inner = rows;
+    d.eps = e->c.rms_norm_epsilon;
+    d.x_inner = cols;
+    d.x_outer = 0;
+    d.out_stride = out_stride;
+    return ctox_hip_norm_rows_device(e->b, &d, e->s);
+}
+
+// ---- paged cache bookkeeping ----
+ctox_status cache_init(ctox_hip_engine *e, Cache &c) {
+    const uint32_t pages = (e->c.max_tokens + e->c.page_tokens - 1) / e->c.page_tokens;
+    const uint32_t q4_slots =
+        std::min(pages, e->c.sink_tokens / e->c.page_tokens + (e->c.recent_tokens + e->c.page_tokens - 1) / e->c.page_tokens +
+                            2 + (e->R + e->c.page_tokens - 1) / e->c.page_tokens);
+    TRY(dalloc(e, (void **)&c.q4, (size_t)q4_slots * e->q4_page_bytes));
+    TRY(dalloc(e, (void **)&c.q2, (size_t)pages * e->q2_page_bytes));
+    TRY(dalloc_t(e, &c.d_desc, pages));
+    c.desc.assign(pages, ctox_paged_kv_descriptor{0, 0, 0, 0});
+    for (uint32_t i = q4_slots; i-- > 0;) c.free_q4.push_back(i);
+    for (uint32_t i = pages; i-- > 0;) c.free_q2.push_back(i);
+    return CTOX_OK;
+}
+
+// Descriptors [dirty, pages) to the device, in stream order (kernel-argument writes).
+ctox_status cache_upload(ctox_hip_engine *e, Cache &c) {
+    if (c.dirty < c.pages)
+        TRY(ctox_hip_write_words_device(e->b, (uint32_t *)(c.d_desc + c.dirty), (const uint32_t *)(c.desc.data() + c.dirty),
+                                        (size_t)(c.pages - c.dirty) * 4, e->s));
+    c.dirty = c.pages;
+    return CTOX_OK;
+}
+
+// Append `rows` tokens (k, v: [rows][cv] dense) into Q4 pages.
+ctox_status cache_push(ctox_hip_engine *e, Cache &c, const float *k, const float *v, uint32_t rows) {
+    if (c.tokens + rows > e->c.max_tokens) return efail(CTOX_ERR_MEMORY_BUDGET, "paged KV cache is full");
+    uint32_t done = 0;
+    while (done < rows) {
+        if (c.pages == 0 || c.desc[c.pages - 1].tokens == e->c.page_tokens) {
+            if (c.free_q4.empty()) return efail(CTOX_ERR_MEMORY_BUDGET, "no free Q4 page slot");
+            c.desc[c.pages] = ctox_paged_kv_descriptor{1, c.free_q4.back(), 0, c.pages * e->c.page_tokens};
+            c.free_q4.pop_back();
+            c.pages++;
+        }
+        ctox_paged_kv_descriptor &d = c.desc[c.pages - 1];
+        c.dirty = std::min(c.dirty, c.pages - 1);
+        const uint32_t take = std::min(rows - done, e->c.page_tokens - d.tokens);
+        TRY(ctox_hip_kv_pack_q4_device(e->b, c.q4, k + (size_t)done * e->kvw, v + (size_t)done * e->kvw, take, e->kvw,
+                                       d.physical_slot, d.tokens, e->q4_page_bytes, e->s));
+        d.tokens += take;
+        done += take;
+        c.tokens += take;
+    }
+    return CTOX_OK;
+}
+
+// Drop the last `n` tokens (speculative rollback; pages emptied go back to the pool).
+void cache_truncate(Cache &c, uint32_t n) {
+    while (n > 0 && c.pages > 0) {
+        ctox_paged_kv_descriptor &d = c.desc[c.pages - 1];
+        c.dirty = std::min(c.dirty, c.pages - 1);
+        const uint32_t drop = std::min(n, d.tokens);
+        d.tokens -= drop;
+        c.tokens -= drop;
+        n -= drop;
+        if (d.tokens == 0) {
+            (d.precision ? c.free_q4 : c.free_q2).push_back(d.physical_slot);
+            c.pages--;
+        }
+    }
+}
+
+// Q/src/kv_cache.rs:463-478: pages past the sink and wholly older than the recent window become Q2.
+ctox_status cache_demote(ctox_hip_engine *e, Cache &c) {
+    const uint32_t recent_start = c.tokens > e->c.recent_tokens ? c.tokens - e->c.recent_tokens : 0;
+    for (uint32_t i = 0; i < c.pages; i++) {
+        ctox_paged_kv_descriptor &d = c.desc[i];
+        if (d.precision && d.first_token >= e->c.sink_tokens && d.first_token + d.tokens <= recent_start) {
+            if (c.free_q2.empty()) return efail(CTOX_ERR_MEMORY_BUDGET, "no free Q2 page slot");
+            const uint32_t q2 = c.free_q2.back();
+            c.free_q2.pop_back();
+            TRY(ctox_hip_kv_demote_device(e->b, c.q4 + (size_t)d.physical_slot * e->q4_page_bytes,
+                                          c.q2 + (size_t)q2 * e->q2_page_bytes, d.tokens, 2 * e->kvw / 64, e->s));
+            c.free_q4.push_back(d.physical_slot);
+            d.precision = 0;
+            d.physical_slot = q2;
+            c.dirty = std::min(c.dirty, i);
+        }
+    }
+    return CTOX_OK;
+}
+
+ctox_paged_gqa_params gqa_params(ctox_hip_engine *e, const Cache &c) {
+    ctox_paged_gqa_params p{};
+    p.query_heads = e->c.num_attention_heads;
+    p.key_value_heads = e->c.num_key_value_heads;
+    p.head_dim = e->c.head_dim;
+    p.tokens = c.tokens;
+    p.page_tokens = e->c.page_tokens;
+    p.page_count = std::max(1u, c.pages);
+    p.combined_values = 2 * e->kvw;
+    p.q2_token_bytes = e->q2_token_bytes;
+    p.q4_token_bytes = e->q4_token_bytes;
+    p.q2_page_bytes = e->q2_page_bytes;
+    p.q4_page_bytes = e->q4_page_bytes;
+    p.scale = 1.0f / std::sqrt((float)e->c.head_dim);
+    return p;
+}
+
+// ---- layers ----
+ctox_status make_attn(ctox_hip_engine *e, AttnLayer &a, uint64_t &seed) {
+    const uint32_t H = e->H, qh = e->c.num_attention_heads, hd = e->c.head_dim;
+    TRY(make_vec(e, &a.norm, H, seed, 0.0f, 0.1f));
+    TRY(make_mat(e, a.qkv, CTOX_DTYPE_Q4B64, e->Rq, H, seed));
+    TRY(make_vec(e, &a.q_norm, hd, seed, 0.0f, 0.1f));
+    TRY(make_vec(e, &a.k_norm, hd, seed, 0.0f, 0.1f));
+    TRY(make_mat(e, a.o, CTOX_DTYPE_Q4B64, H, qh * hd, seed));
+    return cache_init(e, a.cache);
+}
+
+ctox_status make_mlp(ctox_hip_engine *e, Mlp &m, uint64_t &seed) {
+    TRY(make_vec(e, &m.norm, e->H, seed, 0.0f, 0.1f));
+    TRY(make_mat(e, m.gate_up, CTOX_DTYPE_Q4B64, 2 * e->I, e->H, seed));
+    return make_mat(e, m.down, CTOX_DTYPE_Q2B64, e->H, e->I, seed);
+}
+
+// Full-attention token mixer over R rows at rope positions rope0.. (the
+// cache's last R tokens after the push); writes the residual delta. Unless
+// `retain` (a speculative branch, kv_cache.rs:372-381), pages are demoted
+// right after the push, before attention reads them, as
+// FullAttentionState::append does (decoder.rs:774).
+ctox_status attn_forward(ctox_hip_engine *e, AttnLayer &a, uint32_t R, uint32_t rope0, float *delta, bool retain) {
+    const uint32_t qh = e->c.num_attention_heads, kvh = e->c.num_key_value_heads, hd = e->c.head_dim;
+    TRY(matvec(e, a.qkv, e->xn, e->proj, R));
+    ctox_norm_rows d{};
+    d.x = e->proj;
+    d.w = a.q_norm;
+    d.out = e->q;
+    d.rows = R * qh;
+    d.cols = hd;
+    d.inner = qh;
+    d.eps = e->c.rms_norm_epsilon;
+    d.x_inner = 2 * hd;
+    d.x_outer = e->Rq;
+    d.out_stride = hd;
+    TRY(ctox_hip_norm_rows_device(e->b, &d, e->s));
+    d.x = e->proj + 2 * qh * hd;
+    d.w = a.k_norm;
+    d.out = e->k;
+    d.rows = R * kvh;
+    d.inner = kvh;
+    d.x_inner = hd;
+    TRY(ctox_hip_norm_rows_device(e->b, &d, e->s));
+    TRY(ctox_hip_partial_rope_device(e->b, e->q, e->k, R, qh, kvh, hd, e->c.rotary_dim, rope0, e->c.rope_theta, e->s));
+    TRY(ctox_hip_copy_rows_device(e->b, e->proj, e->Rq, 2 * qh * hd + e->kvw, R, e->kvw, e->v, e->kvw, e->s));
+    TRY(cache_push(e, a.cache, e->k, e->v, R));
+    if (!retain) TRY(cache_demote(e, a.cache));
+    TRY(cache_upload(e, a.cache));
+    const ctox_paged_gqa_params p = gqa_params(e, a.cache);
+    TRY(ctox_hip_paged_gqa_device(e->b, e->q, a.cache.q2, a.cache.q4, a.cache.d_desc, &p, R, e->attn, e->s));
+    TRY(ctox_hip_attention_gate_device(e->b, e->attn, e->proj, R, qh, hd, e->Rq, e->s));
+    return matvec(e, a.o, e->attn, delta, R);
+}
+
+ctox_status gdn_forward(ctox_hip_engine *e, GdnLayer &g, uint32_t R, float *delta, bool keep_rows) {
+    const uint32_t Hv = e->c.linear_num_value_heads, Hk = e->c.linear_num_key_heads;
+    const uint32_t dk = e->c.linear_key_head_dim, dv = e->c.linear_value_head_dim;
+    float *proj = keep_rows ? g.proj : e->proj;
+    float *ld = keep_rows ? g.ld : e->ld, *beta = keep_rows ? g.beta : e->beta;
+    TRY(matvec(e, g.in, e->xn, proj, R));
+    TRY(ctox_hip_causal_conv_rows_device(e->b, proj, e->Rin, g.conv, g.conv_w, e->C, e->c.linear_conv_kernel_dim, R,
+                                         e->convo, e->s));
+    TRY(ctox_hip_gdn_gates_strided_device(e->b, proj + e->C + e->Vw, proj + e->C + e->Vw + Hv, e->Rin, g.a_log,
+                                          g.dt_bias, R, Hv, ld, beta, e->s));
+    TRY(ctox_hip_gated_delta_strided_device(e->b, e->convo, e->convo + e->Kw, e->convo + 2 * e->Kw, e->C, e->C, ld,
+                                            beta, g.state, R, Hv, Hk, dk, dv, 0, e->core, e->s));
+    ctox_norm_rows d{};
+    d.x = e->core;
+    d.gate = proj + e->C;
+    d.w = g.gnorm;
+    d.out = e->coren;
+    d.rows = R * Hv;
+    d.cols = dv;
+    d.mode = 1;
+    d.inner = Hv;
+    d.eps = e->c.rms_norm_epsilon;
+    d.x_inner = dv;
+    d.x_outer = (uint64_t)Hv * dv;
+    d.g_inner = dv;
+    d.g_outer = e->Rin;
+    d.out_stride = dv;
+    TRY(ctox_hip_norm_rows_device(e->b, &d, e->s));
+    return matvec(e, g.out, e->coren, delta, R);
+}
+
+ctox_status mlp_forward(ctox_hip_engine *e, Mlp &m, uint32_t R, float *h, const float *delta_in, float *delta_out) {
+    TRY(norm(e, h, delta_in, m.norm, R, e->H, e->xn, e->H));
+    TRY(matvec(e, m.gate_up, e->xn, e->gu, R));
+    TRY(ctox_hip_swiglu_rows_device(e->b, e->gu, 2 * e->I, e->I, R, e->I, e->act, e->I, e->s));
+    return matvec(e, m.down, e->act, delta_out, R);
+}
+
+// Target model over R rows (tokens in d_tok, positions position..position+R-1).
+// Leaves logits [R][V] and final hiddens [R][H] (e->fin).
+ctox_status target_forward(ctox_hip_engine *e, const uint32_t *d_tok, uint32_t R, bool keep_rows) {
+    TRY(ctox_hip_embedding_rows_device(e->b, e->embed.dtype, e->embed.w, e->embed.s_in, e->embed.s_out, d_tok, R, e->V,
+                                       e->H, e->hid, e->s));
+    bool pending = false;
+    for (Layer &L : e->layers) {
+        TRY(norm(e, e->hid, pending ? e->delta : nullptr, L.full ? L.f.norm : L.g.norm, R, e->H, e->xn, e->H));
+        if (L.full)
+            TRY(attn_forward(e, L.f, R, e->position, e->delta, keep_rows));
+        else
+            TRY(gdn_forward(e, L.g, R, e->delta, keep_rows));
+        TRY(mlp_forward(e, L.mlp, R, e->hid, e->delta, e->delta));
+        pending = true;
+    }
+    TRY(norm(e, e->hid, e->delta, e->final_norm, R, e->H, e->fin, e->H));
+    return matvec(e, e->lm_head, e->fin, e->logits, R);
+}
+
+// MTP over R rows: tokens d_tok, previous hiddens prev [R][H], rope positions rope0..;
+// leaves the MTP final hidden in mtp_hidden and, when `logits` is set, its LM head rows there.
+ctox_status mtp_forward(ctox_hip_engine *e, const uint32_t *d_tok, const float *prev, uint32_t R, uint32_t rope0,
+                        float *logits, bool retain) {
+    TRY(ctox_hip_embedding_rows_device(e->b, e->embed.dtype, e->embed.w, e->embed.s_in, e->embed.s_out, d_tok, R, e->V,
+                                       e->H, e->hid, e->s));
+    // [norm(embedding), norm(previous hidden)] (decoder.rs:1023-1033)
+    TRY(norm(e, e->hid, nullptr, e->mtp_norm_emb, R, e->H, e->fcin, 2 * e->H));
+    TRY(ctox_hip_copy_rows_device(e->b, prev, e->H, 0, R, e->H, e->xn, e->H, e->s));
+    TRY(norm(e, e->xn, nullptr, e->mtp_norm_hid, R, e->H, e->fcin + e->H, 2 * e->H));
+    TRY(matvec(e, e->mtp_fc, e->fcin, e->hid, R));
+    TRY(norm(e, e->hid, nullptr, e->mtp_attn.norm, R, e->H, e->xn, e->H));
+    TRY(attn_forward(e, e->mtp_attn, R, rope0, e->delta, retain));
+    TRY(mlp_forward(e, e->mtp_mlp, R, e->hid, e->delta, e->delta));
+    TRY(norm(e, e->hid, e->delta, e->mtp_norm, R, e->H, e->mtp_hidden, e->H));
+    if (logits) TRY(matvec(e, e->lm_head, e->mtp_hidden, logits, R));
+    return CTOX_OK;
+}
+
+ctox_status demote_all(ctox_hip_engine *e) {
+    for (Layer &L : e->layers)
+        if (L.full) {
+            TRY(cache_demote(e, L.f.cache));
+            TRY(cache_upload(e, L.f.cache));
+        }
+    if (e->mtp) {
+        TRY(cache_demote(e, e->mtp_attn.cache));
+        TRY(cache_upload(e, e->mtp_attn.cache));
+    }
+    return CTOX_OK;
+}
+
+ctox_status sync(ctox_hip_engine *e) {
+    hipError_t err = hipStreamSynchronize(e->s);
+    return err == hipSuccess ? CTOX_OK : efail(CTOX_ERR_INVALID_STATE, "engine stream failed: %s", hipGetErrorString(err));
+}
+
+ctox_status copy_d2d(ctox_hip_engine *e, void *dst, const void *src, size_t bytes) {
+    return hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, e->s) == hipSuccess
+               ? CTOX_OK
+               : efail(CTOX_ERR_INVALID_STATE, "device copy failed");
+}
+
+}  // namespace
+
+extern "C" ctox_status ctox_hip_engine_create(ctox_hip_backend *b, const ctox_engine_config *cfg, uint64_t seed,
+                                              ctox_hip_engine **out) {
+    if (!b || !cfg || !out) return efail(CTOX_ERR_SHAPE, "null argument");
+    *out = nullptr;
+    const ctox_engine_config &c = *cfg;
+    // Q/src/config.rs:35-73 geometry; the attention kernel needs head_dim 256.
+    if (c.hidden_size == 0 || c.hidden_size % 64 || c.intermediate_size % 64 || c.num_hidden_layers == 0 ||
+        c.full_attention_interval == 0 || c.num_key_value_heads == 0 ||
+        c.num_attention_heads % c.num_key_value_heads || c.head_dim != 256 || c.linear_num_key_heads == 0 ||
+        c.linear_num_value_heads % c.linear_num_key_heads || c.linear_key_head_dim > 128 ||
+        c.linear_value_head_dim > 128 || c.linear_conv_kernel_dim == 0 || c.vocab_size == 0 || c.max_tokens == 0 ||
+        c.page_tokens == 0 || c.sink_tokens % c.page_tokens || c.draft_tokens > 7 ||
+        (c.num_attention_heads * c.head_dim) % 64 || (c.linear_num_value_heads * c.linear_value_head_dim) % 64 ||
+        !(c.rms_norm_epsilon > 0.0f) || !(c.rope_theta > 0.0f) || c.rotary_dim == 0 || c.rotary_dim % 2 ||
+        c.rotary_dim > c.head_dim)
+        return efail(CTOX_ERR_SHAPE, "engine configuration is invalid");
+    ctox_hip_engine *e = new ctox_hip_engine();
+    e->b = b;
+    e->c = c;
+    e->mtp = c.mtp_layers > 0 && c.draft_tokens > 0;
+    e->R = e->mtp ? c.draft_tokens + 1 : 1;
+    e->H = c.hidden_size;
+    e->I = c.intermediate_size;
+    e->Kw = c.linear_num_key_heads * c.linear_key_head_dim;
+    e->Vw = c.linear_num_value_heads * c.linear_value_head_dim;
+    e->C = 2 * e->Kw + e->Vw;
+    e->Rin = e->C + e->Vw + 2 * c.linear_num_value_heads;
+    e->kvw = c.num_key_value_heads * c.head_dim;
+    e->Rq = 2 * c.num_attention_heads * c.head_dim + 2 * e->kvw;
+    e->V = c.vocab_size;
+    e->q4_token_bytes = 2 * e->kvw / 64 * 34;
+    e->q2_token_bytes = 2 * e->kvw / 64 * 18;
+    e->q4_page_bytes = c.page_tokens * e->q4_token_bytes;
+    e->q2_page_bytes = c.page_tokens * e->q2_token_bytes;
+    auto cleanup = [&](ctox_status st) {
+        ctox_hip_engine_destroy(e);
+        return st;
+    };
+    if (hipStreamCreate(&e->s) != hipSuccess) return cleanup(efail(CTOX_ERR_INVALID_STATE, "stream creation failed"));
+    ctox_status st;
+    uint64_t sd = seed * 1000003ull + 17;
+    if ((st = make_mat(e, e->embed, CTOX_DTYPE_Q4B64, e->V, e->H, sd))) return cleanup(st);
+    if ((st = make_mat(e, e->lm_head, CTOX_DTYPE_Q4B64, e->V, e->H, sd))) return cleanup(st);
+    if ((st = make_vec(e, &e->final_norm, e->H, sd, 0.0f, 0.1f))) return cleanup(st);
+    uint32_t n_gdn = 0;
+    for (uint32_t l = 0; l < c.num_hidden_layers; l++) n_gdn += ((l + 1) % c.full_attention_interval) != 0;
+    const uint32_t Hv = c.linear_num_value_heads;
+    e->gdn_floats = (size_t)n_gdn * Hv * c.linear_key_head_dim * c.linear_value_head_dim;
+    e->conv_floats = (size_t)n_gdn * e->C * c.linear_conv_kernel_dim;
+    if ((st = dalloc_t(e, &e->gdn_state, e->gdn_floats)) || (st = dalloc_t(e, &e->conv_state, e->conv_floats)))
+        return cleanup(st);
+    if (e->mtp && ((st = dalloc_t(e, &e->gdn_ckpt, e->gdn_floats)) || (st = dalloc_t(e, &e->conv_ckpt, e->conv_floats))))
+        return cleanup(st);
+    hipMemsetAsync(e->gdn_state, 0, e->gdn_floats * 4, e->s);
+    hipMemsetAsync(e->conv_state, 0, e->conv_floats * 4, e->s);
+    e->layers.resize(c.num_hidden_layers);
+    uint32_t gi = 0;
+    for (uint32_t l = 0; l < c.num_hidden_layers; l++) {
+        Layer &L = e->layers[l];
+        L.full = ((l + 1) % c.full_attention_interval) == 0;  // config.rs:61-72
+        if (L.full) {
+            if ((st = make_attn(e, L.f, sd))) return cleanup(st);
+        } else {
+            GdnLayer &g = L.g;
+            if ((st = make_vec(e, &g.norm, e->H, sd, 0.0f, 0.1f))) return cleanup(st);
+            if ((st = make_mat(e, g.in, CTOX_DTYPE_Q4B64, e->Rin, e->H, sd))) return cleanup(st);
+            if ((st = make_vec(e, &g.conv_w, (size_t)e->C * c.linear_conv_kernel_dim, sd, 0.0f, 0.5f))) return cleanup(st);
+            if ((st = dalloc_t(e, &g.a_log, Hv)) || (st = fill(e, g.a_log, Hv, 4, sd++, -2.0f, 1.0f))) return cleanup(st);
+            if ((st = dalloc_t(e, &g.dt_bias, Hv)) || (st = fill(e, g.dt_bias, Hv, 4, sd++, -1.0f, 1.0f))) return cleanup(st);
+            if ((st = make_vec(e, &g.gnorm, c.linear_value_head_dim, sd, 1.0f, 0.1f))) return cleanup(st);
+            if ((st = make_mat(e, g.out, CTOX_DTYPE_Q4B64, e->H, e->Vw, sd))) return cleanup(st);
+            g.state = e->gdn_state + (size_t)gi * Hv * c.linear_key_head_dim * c.linear_value_head_dim;
+            g.conv = e->conv_state + (size_t)gi * e->C * c.linear_conv_kernel_dim;
+            if (e->mtp && ((st = dalloc_t(e, &g.proj, (size_t)e->R * e->Rin)) || (st = dalloc_t(e, &g.ld, (size_t)e->R * Hv)) ||
+                           (st = dalloc_t(e, &g.beta, (size_t)e->R * Hv))))
+                return cleanup(st);
+            gi++;
+        }
+        if ((st = make_mlp(e, L.mlp, sd))) return cleanup(st);
+    }
+    if (e->mtp) {
+        if ((st = make_vec(e, &e->mtp_norm_emb, e->H, sd, 0.0f, 0.1f)) ||
+            (st = make_vec(e, &e->mtp_norm_hid, e->H, sd, 0.0f, 0.1f)) ||
+            (st = make_vec(e, &e->mtp_norm, e->H, sd, 0.0f, 0.1f)) ||
+            (st = make_mat(e, e->mtp_fc, CTOX_DTYPE_Q4B64, e->H, 2 * e->H, sd)) ||
+            (st = make_attn(e, e->mtp_attn, sd)) || (st = make_mlp(e, e->mtp_mlp, sd)))
+            return cleanup(st);
+    }
+    const size_t R = e->R, qh = c.num_attention_heads, hd = c.head_dim;
+    const size_t widest = std::max<size_t>({e->Rin, e->Rq, 2 * (size_t)e->I, e->H});
+    if ((st = dalloc_t(e, &e->hid, R * e->H)) || (st = dalloc_t(e, &e->xn, R * e->H)) ||
+        (st = dalloc_t(e, &e->proj, R * widest)) || (st = dalloc_t(e, &e->convo, R * e->C)) ||
+        (st = dalloc_t(e, &e->core, R * e->Vw)) || (st = dalloc_t(e, &e->coren, R * e->Vw)) ||
+        (st = dalloc_t(e, &e->delta, R * e->H)) || (st = dalloc_t(e, &e->q, R * qh * hd)) ||
+        (st = dalloc_t(e, &e->k, R * e->kvw)) || (st = dalloc_t(e, &e->v, R * e->kvw)) ||
+        (st = dalloc_t(e, &e->attn, R * qh * hd)) || (st = dalloc_t(e, &e->gu, R * 2 * e->I)) ||
+        (st = dalloc_t(e, &e->act, R * e->I)) || (st = dalloc_t(e, &e->fin, R * e->H)) ||
+        (st = dalloc_t(e, &e->logits, R * e->V)) || (st = dalloc_t(e, &e->ld, R * Hv)) ||
+        (st = dalloc_t(e, &e->beta, R * Hv)) || (st = dalloc_t(e, &e->fcin, R * 2 * e->H)) ||
+        (st = dalloc_t(e, &e->draft_logits, (size_t)std::max(1u, c.draft_tokens) * e->V)) ||
+        (st = dalloc_t(e, &e->mtp_hidden, R * e->H)) || (st = dalloc_t(e, &e->prev_hidden, R * e->H)) ||
+        (st = dalloc_t(e, &e->target_hidden, (R + 1) * e->H)) || (st = dalloc_t(e, &e->d_tokens, 16)) ||
+        (st = dalloc_t(e, &e->d_drafts, 16)) || (st = dalloc_t(e, &e->d_result, 16)) || (st = dalloc_t(e, &e->d_rng, 1)))
+        return cleanup(st);
+    if ((st = sync(e))) return cleanup(st);
+    *out = e;
+    return CTOX_OK;
+}
+
+extern "C" void ctox_hip_engine_destroy(ctox_hip_engine *e) {
+    if (!e) return;
+    if (e->s) hipStreamSynchronize(e->s);
+    for (void *p : e->allocs) hipFree(p);
+    if (e->s) hipStreamDestroy(e->s);
+    delete e;
+}
+
+extern "C" void *ctox_hip_engine_stream(ctox_hip_engine *e) { return e ? (void *)e->s : nullptr; }
+
+extern "C" ctox_status ctox_hip_engine_set_rng(ctox_hip_engine *e, uint64_t state) {
+    if (!e) return efail(CTOX_ERR_SHAPE, "null argument");
+    if (hipMemcpyAsync(e->d_rng, &state, 8, hipMemcpyHostToDevice, e->s) != hipSuccess)
+        return efail(CTOX_ERR_INVALID_STATE, "rng upload failed");
+    return sync(e);
+}
+
+// One target step (CpuCorrectnessExecutor::decode without MTP, decoder.rs:956-998):
+// logits of the next position in the engine's logits buffer; *d_logits points there.
+extern "C" ctox_status ctox_hip_engine_decode(ctox_hip_engine *e, uint32_t token, const float **d_logits) {
+    if (!e) return efail(CTOX_ERR_SHAPE, "null argument");
+    if (token >= e->V) return efail(CTOX_ERR_SHAPE, "token outside the vocabulary");
+    if (e->position >= e->c.max_tokens) return efail(CTOX_ERR_MEMORY_BUDGET, "context is full");
+    TRY(ctox_hip_write_words_device(e->b, e->d_tokens, &token, 1, e->s));
+    // MTP prefill semantics (decoder.rs:1248-1261): the MTP cache advances with
+    // (token, previous target hidden) for every position after the first.
+    if (e->mtp && e->have_prev) {
+        TRY(mtp_forward(e, e->d_tokens, e->prev_hidden, 1, e->position, nullptr, false));
+        e->mtp_tokens++;
+    }
+    TRY(target_forward(e, e->d_tokens, 1, false));
+    TRY(copy_d2d(e, e->prev_hidden, e->fin, (size_t)e->H * 4));
+    e->have_prev = true;
+    e->position++;
+    TRY(demote_all(e));
+    if (d_logits) *d_logits = e->logits;
+    return sync(e);
+}
+
+// One speculative step: k drafts sampled at `temperature`, one batched target
+// pass over [token, d1..dk], acceptance and commit. out[0] = next token,
+// out[1] = accepted drafts n, out[2..2+n) = the accepted drafts.
+extern "C" ctox_status ctox_hip_engine_mtp_step(ctox_hip_engine *e, uint32_t token, float temperature,
+                                                uint32_t *out) {
+    if (!e || !out) return efail(CTOX_ERR_SHAPE, "null argument");
+    if (!e->mtp) return efail(CTOX_ERR_UNSUPPORTED_OPERATION, "engine was created without an MTP head");
+    if (!e->have_prev) return efail(CTOX_ERR_INVALID_STATE, "MTP step needs a previous target step");
+    if (token >= e->V) return efail(CTOX_ERR_SHAPE, "token outside the vocabulary");
+    const uint32_t k = e->c.draft_tokens, R = k + 1, p = e->position;
+    if (p + R > e->c.max_tokens) return efail(CTOX_ERR_MEMORY_BUDGET, "context is full");
+    TRY(ctox_hip_write_words_device(e->b, e->d_tokens, &token, 1, e->s));
+    // Drafts: d_{i+1} ~ softmax(MTP(x_i, g_i) / T) with x_0 = token, g_0 = the last
+    // target hidden, then x_i = d_i, g_i = the MTP hidden of step i.
+    TRY(copy_d2d(e, e->d_drafts, e->d_tokens, 4));
+    TRY(copy_d2d(e, e->target_hidden, e->prev_hidden, (size_t)e->H * 4));
+    for (uint32_t i = 0; i < k; i++) {
+        TRY(mtp_forward(e, e->d_drafts + i, i == 0 ? e->prev_hidden : e->mtp_hidden, 1, p + i,
+                        e->draft_logits + (size_t)i * e->V, true));
+        // drafts = 0 samples the bonus row: the draft token from its own softmax.
+        TRY(ctox_hip_mtp_accept_device(e->b, e->draft_logits, e->draft_logits, e->draft_logits + (size_t)i * e->V,
+                                       e->d_drafts, 0, e->V, temperature, e->d_rng, e->d_drafts + i + 1, e->s));
+    }
+    // Checkpoint the recurrent states, then verify [token, d1..dk] in one pass.
+    TRY(copy_d2d(e, e->gdn_ckpt, e->gdn_state, e->gdn_floats * 4));
+    TRY(copy_d2d(e, e->conv_ckpt, e->conv_state, e->conv_floats * 4));
+    TRY(target_forward(e, e->d_drafts, R, true));
+    TRY(ctox_hip_mtp_accept_device(e->b, e->draft_logits, e->logits, e->logits + (size_t)k * e->V, e->d_drafts + 1, k,
+                                   e->V, temperature, e->d_rng, e->d_result, e->s));
+    uint32_t host[16] = {0};
+    if (hipMemcpyAsync(host, e->d_result, 8, hipMemcpyDeviceToHost, e->s) != hipSuccess ||
+        hipMemcpyAsync(host + 2, e->d_drafts, 4 * R, hipMemcpyDeviceToHost, e->s) != hipSuccess)
+        return efail(CTOX_ERR_INVALID_STATE, "result read failed");
+    TRY(sync(e));
+    const uint32_t next = host[0], n = host[1];
+    if (n > k || next >= e->V) return efail(CTOX_ERR_INVALID_STATE, "acceptance produced an invalid result");
+    // Commit n + 1 target tokens.
+    for (Layer &L : e->layers)
+        if (L.full) cache_truncate(L.f.cache, k - n);
+    if (n < k) {
+        TRY(copy_d2d(e, e->gdn_state, e->gdn_ckpt, e->gdn_floats * 4));
+        TRY(copy_d2d(e, e->conv_state, e->conv_ckpt, e->conv_floats * 4));
+        const uint32_t Hv = e->c.linear_num_value_heads;
+        for (Layer &L : e->layers) {
+            if (L.full) continue;
+            GdnLayer &g = L.g;
+            TRY(ctox_hip_causal_conv_rows_device(e->b, g.proj, e->Rin, g.conv, g.conv_w, e->C,
+                                                 e->c.linear_conv_kernel_dim, n + 1, e->convo, e->s));
+            TRY(ctox_hip_gated_delta_strided_device(e->b, e->convo, e->convo + e->Kw, e->convo + 2 * e->Kw, e->C, e->C,
+                                                    g.ld, g.beta, g.state, n + 1, Hv, e->c.linear_num_key_heads,
+                                                    e->c.linear_key_head_dim, e->c.linear_value_head_dim, 0, e->core,
+                                                    e->s));
+        }
+    }
+    // Final hiddens of the committed rows: h_p .. h_{p+n}.
+    TRY(copy_d2d(e, e->target_hidden + e->H, e->fin, (size_t)(n + 1) * e->H * 4));
+    // MTP cache: keep the first draft's entry (token, previous hidden), replay
+    // d1..dn with the target hiddens h_p..h_{p+n-1} (commit_speculative).
+    cache_truncate(e->mtp_attn.cache, k - 1);
+    if (n > 0) TRY(mtp_forward(e, e->d_drafts + 1, e->target_hidden + e->H, n, p + 1, nullptr, true));
+    e->mtp_tokens = e->mtp_attn.cache.tokens;
+    TRY(copy_d2d(e, e->prev_hidden, e->target_hidden + (size_t)(n + 1) * e->H, (size_t)e->H * 4));
+    e->position = p + n + 1;
+    TRY(demote_all(e));  // uploads every changed descriptor
+    out[0] = next;
+    out[1] = n;
+    for (uint32_t i = 0; i < n; i++) out[2 + i] = host[3 + i];
+    return sync(e);
+}
+
+// Context of `tokens` random K/V rows in every paged cache (and the MTP cache),
+// position = tokens; recurrent states stay as they are. Config 5's "context
+// filled with random K/V".
+extern "C" ctox_status ctox_hip_engine_fill_context(ctox_hip_engine *e, uint32_t tokens, uint64_t seed) {
+    if (!e) return efail(CTOX_ERR_SHAPE, "null argument");
+    if (e->position != 0 || tokens == 0 || tokens + e->R > e->c.max_tokens)
+        return efail(CTOX_ERR_SHAPE, "context fill needs an empty engine and room for a step");
+    const uint32_t chunk = 1024;
+    float *kbuf = nullptr, *vbuf = nullptr;
+    TRY(dalloc_t(e, &kbuf, (size_t)chunk * e->kvw));
+    TRY(dalloc_t(e, &vbuf, (size_t)chunk * e->kvw));
+    auto fill_cache = [&](Cache &c, uint64_t sd) -> ctox_status {
+        for (uint32_t t = 0; t < tokens; t += chunk) {
+            const uint32_t n = std::min(chunk, tokens - t);
+            TRY(fill(e, kbuf, (uint64_t)n * e->kvw, 2, sd + 2 * t, 0.0f, 1.0f));
+            TRY(fill(e, vbuf, (uint64_t)n * e->kvw, 2, sd + 2 * t + 1, 0.0f, 1.0f));
+            TRY(cache_push(e, c, kbuf, vbuf, n));
+            TRY(cache_demote(e, c));
+            TRY(cache_upload(e, c));
+        }
+        return CTOX_OK;
+    };
+    uint64_t sd = seed * 7919 + 3;
+    for (Layer &L : e->layers)
+        if (L.full) TRY(fill_cache(L.f.cache, sd += 1000003));
+    if (e->mtp) TRY(fill_cache(e->mtp_attn.cache, sd += 1000003));
+    // A previous target hidden so that the first MTP step has its input.
+    TRY(fill(e, e->prev_hidden, e->H, 2, sd + 11, 0.0f, 1.0f));
+    e->have_prev = true;
+    e->position = tokens;
+    e->mtp_tokens = e->mtp ? tokens : 0;
+    if (e->mtp) {
+        // the MTP cache holds position - 1 entries (decoder.rs:1018-1021)
+        cache_truncate(e->mtp_attn.cache, 1);
+        TRY(cache_upload(e, e->mtp_attn.cache));
+        e->mtp_tokens = tokens - 1;
+    }
+    return sync(e);
+}
+
+// Device views for tests and tools. which: 0 logits [R][V], 1 final hidden
+// [R][H], 2 previous target hidden [H], 3 GatedDeltaNet states, 4 conv states,
+// 5 draft logits [k][V].
+extern "C" ctox_status ctox_hip_engine_buffer(ctox_hip_engine *e, uint32_t which, void **ptr, size_t *bytes) {
+    if (!e || !ptr || !bytes) return efail(CTOX_ERR_SHAPE, "null argument");
+    switch (which) {
+    case 0: *ptr = e->logits; *bytes = (size_t)e->R * e->V * 4; break;
+    case 1: *ptr = e->fin; *bytes = (size_t)e->R * e->H * 4; break;
+    case 2: *ptr = e->prev_hidden; *bytes = (size_t)e->H * 4; break;
+    case 3: *ptr = e->gdn_state; *bytes = e->gdn_floats * 4; break;
+    case 4: *ptr = e->conv_state; *bytes = e->conv_floats * 4; break;
+    case 5: *ptr = e->draft_logits; *bytes = (size_t)std::max(1u, e->c.draft_tokens) * e->V * 4; break;
+    default: return efail(CTOX_ERR_SHAPE, "unknown engine buffer");
+    }
+    return CTOX_OK;
+}
+
+extern "C" uint32_t ctox_hip_engine_position(const ctox_hip_engine *e) { return e ? e->position : 0; }
+
+// Weights by name, as the crate's tensor names (Q/src/tensor_contract.rs) with
+// the fused matrices named by their first member: "embed", "lm_head",
+// "final_norm", "L<i>.<part>" with part in {norm, in (qkv|z|a|b), conv_w,
+// a_log, dt_bias, gnorm, out, qkv (q|gate, k, v), q_norm, k_norm, o,
+// mlp_norm, gate_up, down} and the MTP parts "mtp.<part>" with part in
+// {norm_emb, norm_hid, norm, fc, attn_norm, qkv, q_norm, k_norm, o, mlp_norm,
+// gate_up, down}.
+extern "C" ctox_status ctox_hip_engine_tensor(ctox_hip_engine *e, const char *name, ctox_engine_tensor *t) {
+    if (!e || !name || !t) return efail(CTOX_ERR_SHAPE, "null argument");
+    std::memset(t, 0, sizeof *t);
+    auto mat = [&](const Mat &m) {
+        t->data = m.w;
+        t->bytes = m.bytes();
+        t->rows = m.rows;
+        t->cols = m.cols;
+        t->dtype = m.dtype;
+        t->s_in = m.s_in;
+        t->s_out = m.s_out;
+        return CTOX_OK;
+    };
+    auto vec = [&](const float *p, size_t n) {
+        t->data = (void *)p;
+        t->bytes = n * 4;
+        t->rows = 1;
+        t->cols = (uint32_t)n;
+        t->dtype = -1;
+        return CTOX_OK;
+    };
+    const std::string s(name);
+    if (s == "embed") return mat(e->embed);
+    if (s == "lm_head") return mat(e->lm_head);
+    if (s == "final_norm") return vec(e->final_norm, e->H);
+    auto attn_part = [&](const AttnLayer &a, const std::string &part) -> ctox_status {
+        if (part == "attn_norm" || part == "norm") return vec(a.norm, e->H);
+        if (part == "qkv") return mat(a.qkv);
+        if (part == "q_norm") return vec(a.q_norm, e->c.head_dim);
+        if (part == "k_norm") return vec(a.k_norm, e->c.head_dim);
+        if (part == "o") return mat(a.o);
+        return efail(CTOX_ERR_SHAPE, "unknown tensor %s", name);
+    };
+    auto mlp_part = [&](const Mlp &m, const std::string &part, bool *hit) -> ctox_status {
+        *hit = true;
+        if (part == "mlp_norm") return vec(m.norm, e->H);
+        if (part == "gate_up") return mat(m.gate_up);
+        if (part == "down") return mat(m.down);
+        *hit = false;
+        return CTOX_OK;
+    };
+    if (s.rfind("mtp.", 0) == 0) {
+        if (!e->mtp) return efail(CTOX_ERR_SHAPE, "engine has no MTP head");
+        const std::string part = s.substr(4);
+        if (part == "norm_emb") return vec(e->mtp_norm_emb, e->H);
+        if (part == "norm_hid") return vec(e->mtp_norm_hid, e->H);
+        if (part == "norm") return vec(e->mtp_norm, e->H);
+        if (part == "fc") return mat(e->mtp_fc);
+        bool hit;
+        ctox_status st = mlp_part(e->mtp_mlp, part, &hit);
+        if (hit) return st;
+        return attn_part(e->mtp_attn, part == "attn_norm" ? "norm" : part);
+    }
+    if (s.size() > 1 && s[0] == 'L') {
+        const size_t dot = s.find('.');
+        if (dot == std::string::npos) return efail(CTOX_ERR_SHAPE, "unknown tensor %s", name);
+        const uint32_t l = (uint32_t)std::strtoul(s.substr(1, dot - 1).c_str(), nullptr, 10);
+        if (l >= e->layers.size()) return efail(CTOX_ERR_SHAPE, "layer out of range");
+        const std::string part = s.substr(dot + 1);
+        const Layer &L = e->layers[l];
+        bool hit;
+        ctox_status st = mlp_part(L.mlp, part, &hit);
+        if (hit) return st;
+        if (L.full) return attn_part(L.f, part);
+        const GdnLayer &g = L.g;
+        if (part == "norm") return vec(g.norm, e->H);
+        if (part == "in") return mat(g.in);
+        if (part == "conv_w") return vec(g.conv_w, (size_t)e->C * e->c.linear_conv_kernel_dim);
+        if (part == "a_log") return vec(g.a_log, e->c.linear_num_value_heads);
+        if (part == "dt_bias") return vec(g.dt_bias, e->c.linear_num_value_heads);
+        if (part == "gnorm") return vec(g.gnorm, e->c.linear_value_head_dim);
+        if (part == "out") return mat(g.out);
+    }
+    return efail(CTOX_ERR_SHAPE, "unknown tensor %s", name);
+}

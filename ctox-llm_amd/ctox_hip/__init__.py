@@ -239,9 +239,32 @@ SIGNATURES = {
     "ctox_hip_sigmoid_gate_device": (_I32, [_P, _P, _P, _SZ, _P]),
     "ctox_hip_causal_conv_update_device": (_I32, [_P, _P, _P, _P, _SZ, _SZ, _P, _P]),
     "ctox_hip_partial_rope_device": (_I32, [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_uint64, ctypes.c_float, _P]),
+    "ctox_hip_gated_delta_strided_device": (_I32, [_P, _P, _P, _P, _SZ, _SZ, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, _SZ,
+                                                    _SZ, _P, _P]),
+    "ctox_hip_gdn_gates_strided_device": (_I32, [_P, _P, _P, _SZ, _P, _P, _SZ, _SZ, _P, _P, _P]),
+    "ctox_hip_causal_conv_rows_device": (_I32, [_P, _P, _SZ, _P, _P, _SZ, _SZ, _SZ, _P, _P]),
     "ctox_hip_kv_pack_q4_device": (_I32, [_P, _P, _P, _P, _SZ, _SZ, _U32, _U32, _U32, _P]),
     "ctox_hip_kv_demote_device": (_I32, [_P, _P, _P, _SZ, _SZ, _P]),
     "ctox_hip_paged_gqa_device": (_I32, [_P, _P, _P, _P, _P, ctypes.POINTER(PagedGqaParams), _SZ, _P, _P]),
+    "ctox_hip_fill_random_device": (_I32, [_P, _P, ctypes.c_uint64, _U32, ctypes.c_uint64, ctypes.c_float,
+                                           ctypes.c_float, _P]),
+    "ctox_hip_embedding_rows_device": (_I32, [_P, _I32, _P, _P, _P, _P, _SZ, _SZ, _SZ, _P, _P]),
+    "ctox_hip_norm_rows_device": (_I32, [_P, _P, _P]),
+    "ctox_hip_attention_gate_device": (_I32, [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, _P]),
+    "ctox_hip_swiglu_rows_device": (_I32, [_P, _P, _SZ, _SZ, _SZ, _SZ, _P, _SZ, _P]),
+    "ctox_hip_copy_rows_device": (_I32, [_P, _P, _SZ, _SZ, _SZ, _SZ, _P, _SZ, _P]),
+    "ctox_hip_write_words_device": (_I32, [_P, _P, _P, _SZ, _P]),
+    # decode engine (struct arguments passed by reference)
+    "ctox_hip_engine_create": (_I32, [_P, _P, ctypes.c_uint64, ctypes.POINTER(_P)]),
+    "ctox_hip_engine_destroy": (None, [_P]),
+    "ctox_hip_engine_stream": (_P, [_P]),
+    "ctox_hip_engine_set_rng": (_I32, [_P, ctypes.c_uint64]),
+    "ctox_hip_engine_decode": (_I32, [_P, _U32, ctypes.POINTER(_P)]),
+    "ctox_hip_engine_mtp_step": (_I32, [_P, _U32, ctypes.c_float, ctypes.POINTER(_U32)]),
+    "ctox_hip_engine_fill_context": (_I32, [_P, _U32, ctypes.c_uint64]),
+    "ctox_hip_engine_buffer": (_I32, [_P, _U32, ctypes.POINTER(_P), ctypes.POINTER(_SZ)]),
+    "ctox_hip_engine_position": (_U32, [_P]),
+    "ctox_hip_engine_tensor": (_I32, [_P, ctypes.c_char_p, _P]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -513,6 +536,28 @@ class HipBackend:
         """Q/src/reference.rs:115-155 (in place; row t at position + t)."""
         _check(load_library().ctox_hip_partial_rope_device(self.handle, d_q, d_k, rows, q_heads, k_heads, head_dim,
                                                            rotary_dim, position, theta, stream))
+
+    def gated_delta_strided_device(self, d_q: int, d_k: int, d_v: int, qk_stride: int, v_stride: int, d_log_decay: int,
+                                   d_beta: int, d_state: int, tokens: int, heads: int, key_heads: int, key_dim: int,
+                                   value_dim: int, chunk: int, d_out: int, stream: Optional[int] = None) -> None:
+        """Recurrence over strided q/k/v with repeated key heads (Q/src/decoder.rs:868-913)."""
+        _check(load_library().ctox_hip_gated_delta_strided_device(self.handle, d_q, d_k, d_v, qk_stride, v_stride,
+                                                                  d_log_decay, d_beta, d_state, tokens, heads,
+                                                                  key_heads, key_dim, value_dim, chunk, d_out,
+                                                                  stream))
+
+    def gdn_gates_strided_device(self, d_a: int, d_b: int, in_stride: int, d_a_log: int, d_dt_bias: int,
+                                 tokens: int, heads: int, d_log_decay: int, d_beta: int,
+                                 stream: Optional[int] = None) -> None:
+        """Q/src/decoder.rs:881-902 on token rows of a fused projection."""
+        _check(load_library().ctox_hip_gdn_gates_strided_device(self.handle, d_a, d_b, in_stride, d_a_log, d_dt_bias,
+                                                                tokens, heads, d_log_decay, d_beta, stream))
+
+    def causal_conv_rows_device(self, d_input: int, in_stride: int, d_state: int, d_weight: int, channels: int,
+                                kernel: int, rows: int, d_out: int, stream: Optional[int] = None) -> None:
+        """Q/src/reference.rs:159-187 over consecutive tokens."""
+        _check(load_library().ctox_hip_causal_conv_rows_device(self.handle, d_input, in_stride, d_state, d_weight,
+                                                               channels, kernel, rows, d_out, stream))
 
     # ---- paged KV cache (device pointers) ----
     def kv_pack_q4_device(self, d_q4_pages: int, d_keys: int, d_values: int, token_count: int,

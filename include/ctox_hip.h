@@ -226,6 +226,23 @@ ctox_status ctox_hip_gated_delta_sequence_device(ctox_hip_backend *backend, cons
                                                  size_t key_dim, size_t value_dim, size_t chunk,
                                                  float *d_out, void *stream);
 
+/* GatedDeltaNet gates with a and b read at t * in_stride + h (token rows of a
+ * fused projection output); outputs stay [tokens][heads]. */
+ctox_status ctox_hip_gdn_gates_strided_device(ctox_hip_backend *backend, const float *d_a, const float *d_b,
+                                              size_t in_stride, const float *d_a_log, const float *d_dt_bias,
+                                              size_t tokens, size_t heads, float *d_log_decay, float *d_beta,
+                                              void *stream);
+/* The same recurrence reading q, k, v straight out of a fused projection /
+ * convolution output: token t's q and k rows start at t * qk_stride floats,
+ * v rows at t * v_stride; value head h uses key head h / (heads / key_heads),
+ * which is repeat_heads (Q/src/decoder.rs:47-65, :868-880) without the copy.
+ * chunk as in ctox_hip_gated_delta_sequence_device (0: token-serial scan). */
+ctox_status ctox_hip_gated_delta_strided_device(ctox_hip_backend *backend, const float *d_q, const float *d_k,
+                                                const float *d_v, size_t qk_stride, size_t v_stride,
+                                                const float *d_log_decay, const float *d_beta, float *d_state,
+                                                size_t tokens, size_t heads, size_t key_heads, size_t key_dim,
+                                                size_t value_dim, size_t chunk, float *d_out, void *stream);
+
 /* ---- decode-step glue and token selection (device buffers) ---- */
 /* GatedDeltaNet gates, Q/src/decoder.rs:881-902 (softplus :29-35):
  * beta = sigmoid(b), log_decay = -exp(A_log) * softplus(a + dt_bias), over
@@ -278,6 +295,12 @@ ctox_status ctox_hip_sigmoid_gate_device(ctox_hip_backend *backend, float *d_val
 ctox_status ctox_hip_causal_conv_update_device(ctox_hip_backend *backend, const float *d_input, float *d_state,
                                                const float *d_weight, size_t channels, size_t kernel,
                                                float *d_out, void *stream);
+/* causal_conv_silu_update over `rows` consecutive tokens, in order; token t's
+ * input starts at t * in_stride floats (a slice of a fused projection
+ * output), out is [rows][channels]. */
+ctox_status ctox_hip_causal_conv_rows_device(ctox_hip_backend *backend, const float *d_input, size_t in_stride,
+                                             float *d_state, const float *d_weight, size_t channels, size_t kernel,
+                                             size_t rows, float *d_out, void *stream);
 /* apply_partial_rope, Q/src/reference.rs:115-155, in place on q [rows][q_heads][head_dim]
  * and k [rows][k_heads][head_dim]; row t is at position + t. */
 ctox_status ctox_hip_partial_rope_device(ctox_hip_backend *backend, float *d_q, float *d_k, size_t rows,
@@ -335,6 +358,101 @@ ctox_status ctox_hip_paged_gqa_device(ctox_hip_backend *backend, const float *d_
                                       const uint8_t *d_q4_pages, const ctox_paged_kv_descriptor *d_descriptors,
                                       const ctox_paged_gqa_params *params, size_t query_tokens, float *d_out,
                                       void *stream);
+
+/* ---- decode engine helpers (device buffers) ---- */
+/* Seeded synthetic tensors (counter-based, reproducible for any sub-range):
+ * kind 0 Q4_B64 blocks and 1 Q2_B64 blocks (uniform codes, fp16 scale
+ * |N(0, p1)|; count = blocks), 2 f32 N(p0, p1), 3 fp16 U(p0, p1), 4 f32
+ * U(p0, p1). No counterpart in the crate, which loads real artifacts. */
+ctox_status ctox_hip_fill_random_device(ctox_hip_backend *backend, void *d_ptr, uint64_t count, uint32_t kind,
+                                        uint64_t seed, float p0, float p1, void *stream);
+/* ArtifactDecoder::embedding (Q/src/decoder.rs:531-537) for `rows` token ids
+ * held on the device: recovered_row (Q/src/backend/cpu.rs:474-476) of each. */
+ctox_status ctox_hip_embedding_rows_device(ctox_hip_backend *backend, int32_t dtype, const uint8_t *d_weights,
+                                           const uint16_t *d_s_in, const uint16_t *d_s_out, const uint32_t *d_tokens,
+                                           size_t rows, size_t vocab, size_t cols, float *d_out, void *stream);
+/* RMS norms of Q/src/reference.rs:38-93 over rows addressed with two-level
+ * strides (row r at (r / inner) * x_outer + (r % inner) * x_inner floats),
+ * optionally adding a residual delta first (x += delta, written back). */
+typedef struct {
+    float *x;
+    const float *delta;  /* [rows][cols] or NULL */
+    const float *gate;   /* mode 1 only, addressed like x with g_inner / g_outer */
+    const float *w;
+    float *out;          /* row r at r * out_stride */
+    uint32_t rows, cols, mode, inner;  /* mode 0: (1 + w); 1: w * silu(gate) */
+    float eps;
+    uint32_t pad;
+    uint64_t x_inner, x_outer, g_inner, g_outer, out_stride;
+} ctox_norm_rows;
+ctox_status ctox_hip_norm_rows_device(ctox_hip_backend *backend, const ctox_norm_rows *desc, void *stream);
+/* values[t][h][d] *= sigmoid(gate): the gate half of each head's [q, gate]
+ * in q_proj's output rows (Q/src/decoder.rs:727-737, :788). */
+ctox_status ctox_hip_attention_gate_device(ctox_hip_backend *backend, float *d_values, const float *d_qg, size_t rows,
+                                           size_t heads, size_t head_dim, size_t qg_stride, void *stream);
+/* swiglu (Q/src/reference.rs:96-112) over token rows of a fused gate|up
+ * projection: out[t][c] = silu(in[t][c]) * in[t][up_offset + c]. */
+ctox_status ctox_hip_swiglu_rows_device(ctox_hip_backend *backend, const float *d_in, size_t in_stride,
+                                        size_t up_offset, size_t rows, size_t cols, float *d_out, size_t out_stride,
+                                        void *stream);
+/* out[t][c] = in[t * in_stride + col_offset + c]. */
+ctox_status ctox_hip_copy_rows_device(ctox_hip_backend *backend, const float *d_in, size_t in_stride,
+                                      size_t col_offset, size_t rows, size_t cols, float *d_out, size_t out_stride,
+                                      void *stream);
+
+/* Writes `count` 32-bit words to device memory in stream order; the words
+ * travel in kernel arguments, so the host array may be reused on return. */
+ctox_status ctox_hip_write_words_device(ctox_hip_backend *backend, uint32_t *d_dst, const uint32_t *words,
+                                        size_t count, void *stream);
+
+/* ---- device-resident decode engine (engine.cpp) ----
+ * The crate's model graph (Q/src/decoder.rs:427-1114) and MTP executor
+ * (:1217-1458, CUDA MTP4 flow cuda_executor.rs:797-889) over the entry points
+ * above, with synthetic seeded weights of the configured shapes (the crate
+ * would hand its loaded tensors instead). Geometry as Qwen38Config
+ * (Q/src/config.rs:35-73). */
+typedef struct {
+    uint32_t hidden_size, intermediate_size, num_hidden_layers, full_attention_interval;
+    uint32_t num_attention_heads, num_key_value_heads, head_dim, rotary_dim;
+    uint32_t linear_num_key_heads, linear_num_value_heads, linear_key_head_dim, linear_value_head_dim;
+    uint32_t linear_conv_kernel_dim, vocab_size, max_tokens;
+    uint32_t page_tokens, sink_tokens, recent_tokens;  /* paged KV policy, Q/src/kv_cache.rs:10-12 */
+    uint32_t mtp_layers;      /* 0 or 1 */
+    uint32_t draft_tokens;    /* k drafts per speculative step, 0..7 */
+    float rms_norm_epsilon, rope_theta;
+} ctox_engine_config;
+
+typedef struct {
+    void *data;               /* device pointer */
+    size_t bytes;
+    uint32_t rows, cols;
+    int32_t dtype;            /* CTOX_DTYPE_* for quantized matrices, -1 for f32 vectors */
+    uint32_t pad;
+    const uint16_t *s_in, *s_out;  /* fp16 device vectors of quantized matrices */
+} ctox_engine_tensor;
+
+typedef struct ctox_hip_engine ctox_hip_engine;
+
+ctox_status ctox_hip_engine_create(ctox_hip_backend *backend, const ctox_engine_config *config, uint64_t seed,
+                                   ctox_hip_engine **out);
+void ctox_hip_engine_destroy(ctox_hip_engine *engine);
+void *ctox_hip_engine_stream(ctox_hip_engine *engine);
+/* Pcg32 state of the sampler (Q/src/sampler.rs:149-174). */
+ctox_status ctox_hip_engine_set_rng(ctox_hip_engine *engine, uint64_t state);
+/* One target step, decode_target_step (Q/src/decoder.rs:956-998) plus the MTP
+ * cache advance of prefill (:1248-1261); *d_logits = the next-token logits. */
+ctox_status ctox_hip_engine_decode(ctox_hip_engine *engine, uint32_t token, const float **d_logits);
+/* One speculative step at `temperature`: out[0] next token, out[1] accepted
+ * drafts n, out[2 .. 2 + n) the accepted drafts (out holds >= 2 + k words). */
+ctox_status ctox_hip_engine_mtp_step(ctox_hip_engine *engine, uint32_t token, float temperature, uint32_t *out);
+/* Fill every paged cache with `tokens` random K/V rows (an empty engine only). */
+ctox_status ctox_hip_engine_fill_context(ctox_hip_engine *engine, uint32_t tokens, uint64_t seed);
+/* which: 0 logits [R][V], 1 final hiddens [R][H], 2 previous target hidden,
+ * 3 GatedDeltaNet states, 4 conv states, 5 draft logits [k][V]. */
+ctox_status ctox_hip_engine_buffer(ctox_hip_engine *engine, uint32_t which, void **d_ptr, size_t *bytes);
+uint32_t ctox_hip_engine_position(const ctox_hip_engine *engine);
+/* Weights by name ("embed", "lm_head", "final_norm", "L<i>.<part>", "mtp.<part>"). */
+ctox_status ctox_hip_engine_tensor(ctox_hip_engine *engine, const char *name, ctox_engine_tensor *out);
 
 #ifdef __cplusplus
 }

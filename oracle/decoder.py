@@ -1,0 +1,197 @@
+"""CPU restatement of the crate's decoder graph and MTP executor, the oracle
+of the device engine (ctox_hip_engine_*).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/ as the checker; the product
+path (ctox-llm_amd/) never imports it.
+
+Follows Q/src/decoder.rs (Q = models/qwen38_27b):
+  * decode_target_step (:956-998): embedding (:531-537), per layer
+    linear_attention_residual (:806-938) or full_attention_residual_at
+    (:687-800), decoder_mlp_residual (:636-670), final norm, LM head;
+  * mtp_final_hidden (:1009-1046) and the prefill-time MTP advance
+    (:1248-1261);
+  * the speculative step the engine runs (the crate's executor is greedy
+    only, so this is the build's specification, stated once here): k drafts
+    where draft i + 1 is sampled at temperature T from MTP(x_i, g_i) with
+    x_0 = token, g_0 = the previous target hidden, x_i = d_i and g_i the MTP
+    hidden of step i; one target pass over [token, d1..dk] with KV pushes
+    that retain Q4 pages (push_retaining_q4, kv_cache.rs:372-381); the
+    rejection-sampling acceptance (oracle.mtp_accept_sample); commit of the
+    n + 1 accepted target tokens, and the MTP cache rebuilt as
+    commit_speculative does (:1397-1458): the first draft's entry kept, the
+    accepted drafts replayed with target hiddens; then page demotion.
+
+Every operator is the oracle restatement of Q/src/reference.rs,
+Q/src/backend/cpu.rs and Q/src/kv_cache.rs; weights are the engine's own
+(downloaded), with the same row-concatenated fused matrices, which compute
+the same rows as the crate's fan-out.
+"""
+from __future__ import annotations
+
+import copy
+import math
+
+import numpy as np
+
+from . import oracle as orc
+from . import paged_kv as pk
+
+
+class OracleDecoder:
+    def __init__(self, cfg: dict, tensor):
+        """cfg: EngineConfig.as_dict(); tensor(name) -> the engine tensor dict."""
+        self.c = cfg
+        self.t = {}
+        self.fetch = tensor
+        c = cfg
+        self.H, self.I = c["hidden_size"], c["intermediate_size"]
+        self.qh, self.kvh, self.hd = c["num_attention_heads"], c["num_key_value_heads"], c["head_dim"]
+        self.hk, self.hv = c["linear_num_key_heads"], c["linear_num_value_heads"]
+        self.dk, self.dv = c["linear_key_head_dim"], c["linear_value_head_dim"]
+        self.Kw, self.Vw = self.hk * self.dk, self.hv * self.dv
+        self.C = 2 * self.Kw + self.Vw
+        self.K = c["linear_conv_kernel_dim"]
+        self.eps = c["rms_norm_epsilon"]
+        self.full = [((l + 1) % c["full_attention_interval"]) == 0 for l in range(c["num_hidden_layers"])]
+        self.gdn_state = {l: np.zeros(self.hv * self.dk * self.dv, np.float32)
+                          for l in range(len(self.full)) if not self.full[l]}
+        self.conv_state = {l: np.zeros(self.C * self.K, np.float32) for l in self.gdn_state}
+        self.caches = {l: self._cache() for l in range(len(self.full)) if self.full[l]}
+        self.mtp_cache = self._cache() if c["mtp_layers"] else None
+        self.position = 0
+        self.prev_hidden = None
+
+    def _cache(self):
+        c = self.c
+        return pk.PagedKvCache(c["max_tokens"], self.kvh * self.hd, c["page_tokens"], c["sink_tokens"],
+                               c["recent_tokens"])
+
+    # -- weights --------------------------------------------------------------
+    def w(self, name):
+        if name not in self.t:
+            self.t[name] = self.fetch(name)
+        return self.t[name]
+
+    def matvec(self, name, x):
+        m = self.w(name)
+        return orc.fused_matvec(m["dtype"], m["data"], m["rows"], m["cols"], x, s_in=("f16le", m["s_in"]),
+                                s_out=("f16le", m["s_out"]))
+
+    def norm(self, x, name, rows=1):
+        x = np.asarray(x, np.float32).reshape(-1)
+        return orc.rms_norm_1p_weight(x, rows, x.size // rows, self.w(name)["data"], self.eps)
+
+    def embedding(self, token):
+        m = self.w("embed")
+        rb = m["cols"] // 64 * (34 if m["dtype"] == orc.Q4B64 else 18)
+        s_out = float(np.frombuffer(m["s_out"].tobytes(), np.float16)[token])
+        return orc.recovered_row(m["dtype"], m["data"][token * rb:(token + 1) * rb], m["cols"],
+                                 ("f16le", m["s_in"]), s_out)
+
+    # -- mixers ---------------------------------------------------------------
+    def attention(self, prefix, x, rope_pos, cache, retain):
+        """full_attention_residual_at (Q/src/decoder.rs:687-800) minus the residual."""
+        qh, kvh, hd = self.qh, self.kvh, self.hd
+        out = self.matvec(f"{prefix}.qkv", x)
+        qg = out[:2 * qh * hd].reshape(qh, 2 * hd)
+        q = self.norm(qg[:, :hd].reshape(-1), f"{prefix}.q_norm", qh)
+        gate = qg[:, hd:].reshape(-1).copy()
+        k = self.norm(out[2 * qh * hd:2 * qh * hd + kvh * hd], f"{prefix}.k_norm", kvh)
+        v = out[2 * qh * hd + kvh * hd:].copy()
+        orc.apply_partial_rope(q, k, qh, kvh, hd, self.c["rotary_dim"], rope_pos, self.c["rope_theta"])
+        cache.push(k, v, demote=not retain)
+        att = pk.paged_attention(cache, q.reshape(1, qh, hd), 1, qh, kvh, hd)
+        orc.sigmoid_gate(att, gate)
+        return self.matvec(f"{prefix}.o", att)
+
+    def gdn(self, l, x):
+        """linear_attention_residual (Q/src/decoder.rs:806-938) minus the residual."""
+        p = f"L{l}"
+        out = self.matvec(f"{p}.in", x)
+        mixed, z = out[:self.C], out[self.C:self.C + self.Vw]
+        a = out[self.C + self.Vw:self.C + self.Vw + self.hv]
+        b = out[self.C + self.Vw + self.hv:]
+        conv = orc.causal_conv_silu_update(mixed, self.conv_state[l], self.w(f"{p}.conv_w")["data"], self.C, self.K)
+        rep = self.hv // self.hk
+        q = orc.repeat_heads(conv[:self.Kw], self.hk, self.dk, rep)
+        k = orc.repeat_heads(conv[self.Kw:2 * self.Kw], self.hk, self.dk, rep)
+        ld, beta = orc.gdn_gates(a, b, self.w(f"{p}.a_log")["data"], self.w(f"{p}.dt_bias")["data"])
+        core = orc.gated_delta_step(q, k, conv[2 * self.Kw:], ld, beta, self.gdn_state[l], self.hv, self.dk, self.dv)
+        core = orc.rms_norm_gated(core, z, self.hv, self.dv, self.w(f"{p}.gnorm")["data"], self.eps)
+        return self.matvec(f"{p}.out", core)
+
+    def mlp(self, prefix, h):
+        """decoder_mlp_residual (Q/src/decoder.rs:636-670)."""
+        x = self.norm(h, f"{prefix}.mlp_norm")
+        gu = self.matvec(f"{prefix}.gate_up", x)
+        act = orc.swiglu(gu[:self.I], gu[self.I:])
+        return h + self.matvec(f"{prefix}.down", act)
+
+    # -- steps ----------------------------------------------------------------
+    def target_step(self, token, retain=False):
+        """decode_target_step (Q/src/decoder.rs:956-998): (logits, final hidden)."""
+        h = self.embedding(token)
+        for l, full in enumerate(self.full):
+            x = self.norm(h, f"L{l}.norm")
+            d = self.attention(f"L{l}", x, self.position, self.caches[l], retain) if full else self.gdn(l, x)
+            h = self.mlp(f"L{l}", h + d)
+        fin = self.norm(h, "final_norm")
+        self.position += 1
+        return self.matvec("lm_head", fin), fin
+
+    def mtp(self, token, prev, rope_pos, retain, logits=True):
+        """mtp_final_hidden (Q/src/decoder.rs:1009-1046) (+ the shared LM head)."""
+        e = self.norm(self.embedding(token), "mtp.norm_emb")
+        hn = self.norm(prev, "mtp.norm_hid")
+        h = self.matvec("mtp.fc", np.concatenate([e, hn]))
+        x = self.norm(h, "mtp.attn_norm")
+        h = self.mlp("mtp", h + self.attention("mtp", x, rope_pos, self.mtp_cache, retain))
+        fin = self.norm(h, "mtp.norm")
+        return fin, (self.matvec("lm_head", fin) if logits else None)
+
+    def decode(self, token):
+        """One target step with the prefill-time MTP advance (:1248-1261)."""
+        if self.mtp_cache is not None and self.prev_hidden is not None:
+            self.mtp(token, self.prev_hidden, self.position, retain=False, logits=False)
+        logits, fin = self.target_step(token)
+        self.prev_hidden = fin
+        return logits
+
+    def _demote_all(self):
+        for c in list(self.caches.values()) + ([self.mtp_cache] if self.mtp_cache is not None else []):
+            c.demote_old_pages()
+
+    def mtp_step(self, token, temperature, rng: orc.Pcg32, drafts: int):
+        """The speculative step described in the module docstring:
+        returns (next token, accepted drafts)."""
+        p = self.position
+        xs, g = [token], self.prev_hidden
+        draft_logits = []
+        mtp_after_first = None
+        for i in range(drafts):
+            g, lg = self.mtp(xs[-1], g, p + i, retain=True)
+            if i == 0:
+                mtp_after_first = copy.deepcopy(self.mtp_cache)
+            draft_logits.append(lg)
+            empty = np.zeros((0, lg.size), np.float32)
+            d, _ = orc.mtp_accept_sample(empty, empty, lg, np.zeros(0, np.uint32), temperature, rng)
+            xs.append(d)
+        saved = (copy.deepcopy(self.gdn_state), copy.deepcopy(self.conv_state), copy.deepcopy(self.caches),
+                 self.position)
+        target, hiddens = [], []
+        for x in xs:
+            lg, fin = self.target_step(x, retain=True)
+            target.append(lg)
+            hiddens.append(fin)
+        nxt, n = orc.mtp_accept_sample(np.stack(draft_logits), np.stack(target[:drafts]), target[drafts],
+                                       np.array(xs[1:], np.uint32), temperature, rng)
+        # commit n + 1 target tokens
+        self.gdn_state, self.conv_state, self.caches, self.position = saved
+        for x in xs[:n + 1]:
+            self.target_step(x, retain=True)
+        self.mtp_cache = mtp_after_first
+        for i in range(1, n + 1):
+            self.mtp(xs[i], hiddens[i - 1], p + i, retain=True, logits=False)
+        self.prev_hidden = hiddens[n]
+        self._demote_all()
+        return nxt, xs[1:n + 1], {"draft_logits": draft_logits, "target_logits": target, "drafts": xs[1:]}

@@ -144,3 +144,36 @@ def test_errors(hip):
         hip.gated_delta_step([1.0] * 6, [1.0] * 6, [1.0] * 4, [0.0, 0.0], [0.5, 0.5], st, 2, 3, 2)
     with pytest.raises(ctox_hip.UnsupportedOperation):
         hip.gated_delta_step([1.0] * 300, [1.0] * 300, [1.0], [0.0], [0.5], np.zeros(300, np.float32), 1, 300, 1)
+
+
+@pytest.mark.parametrize("tokens,chunk", [(1, 0), (5, 0), (40, 16)])
+def test_strided_repeated_key_heads(hip, orc, tokens, chunk):
+    """q, k, v read in place from a fused [q | k | v] token row with 16 key
+    heads repeated to 48 value heads (Q/src/decoder.rs:868-913) against the
+    oracle on explicitly repeated inputs."""
+    import torch
+    print(f"case gdn strided tokens={tokens} chunk={chunk}", flush=True)
+    rng = np.random.default_rng(tokens + chunk)
+    hk, hv, d = 16, 48, 128
+    width = 2 * hk * d + hv * d + 96          # padded token row
+    row = (rng.standard_normal((tokens, width))).astype(np.float32)
+    q = row[:, :hk * d].reshape(tokens, hk, d)
+    k = row[:, hk * d:2 * hk * d].reshape(tokens, hk, d)
+    v = row[:, 2 * hk * d:2 * hk * d + hv * d].reshape(tokens, hv, d)
+    ld = -np.abs(rng.standard_normal((tokens, hv))).astype(np.float32)
+    beta = (1 / (1 + np.exp(-rng.standard_normal((tokens, hv))))).astype(np.float32)
+    state = (rng.standard_normal((hv, d, d)) * 0.1).astype(np.float32)
+    qr = np.repeat(q, 3, axis=1).reshape(-1)
+    kr = np.repeat(k, 3, axis=1).reshape(-1)
+    ref_state = state.reshape(-1).copy()
+    ref = orc.gated_delta_sequence(qr, kr, v.reshape(-1), ld.reshape(-1), beta.reshape(-1), ref_state, tokens, hv, d, d)
+    drow = torch.from_numpy(row).cuda()
+    keep = [torch.from_numpy(x).cuda() for x in (ld, beta)]
+    dstate = torch.from_numpy(state).cuda()
+    out = torch.empty(tokens, hv, d, device="cuda")
+    base = drow.data_ptr()
+    hip.gated_delta_strided_device(base, base + hk * d * 4, base + 2 * hk * d * 4, width, width, keep[0].data_ptr(),
+                                   keep[1].data_ptr(), dstate.data_ptr(), tokens, hv, hk, d, d, chunk, out.data_ptr())
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(out.cpu().numpy().reshape(-1), ref, rtol=1e-3, atol=1e-4 * float(np.abs(ref).max()))
+    np.testing.assert_allclose(dstate.cpu().numpy().reshape(-1), ref_state, rtol=1e-4, atol=1e-5)

@@ -123,3 +123,34 @@ def test_layer_ops_errors(hip):
         hip.partial_rope_device(p, p, 1, 1, 1, 8, 10, 0, 1e7)
     with pytest.raises(ctox_hip.ShapeError):
         hip.causal_conv_update_device(p, p, p, 4, 0, p)
+
+
+def test_strided_gates_and_conv_rows(hip, orc):
+    """Gates and the causal conv over token rows of a fused projection
+    output (stride > width), tokens applied in order."""
+    say("case strided gates / conv rows")
+    rng = np.random.default_rng(21)
+    T, H, C, K, stride = 5, 48, 10240, 4, 16480
+    rows = rng.standard_normal((T, stride)).astype(np.float32)
+    a_log = rng.uniform(-2, 1, H).astype(np.float32)
+    dt = rng.uniform(-1, 1, H).astype(np.float32)
+    drows = dev(rows)
+    ka, kd = dev(a_log), dev(dt)
+    ld, be = torch.empty(T, H, device="cuda"), torch.empty(T, H, device="cuda")
+    off_a, off_b = 16384, 16384 + H
+    hip.gdn_gates_strided_device(drows.data_ptr() + off_a * 4, drows.data_ptr() + off_b * 4, stride, ka.data_ptr(),
+                                 kd.data_ptr(), T, H, ld.data_ptr(), be.data_ptr())
+    state = rng.standard_normal((C, K)).astype(np.float32)
+    weight = rng.standard_normal((C, K)).astype(np.float32)
+    ds, dw = dev(state), dev(weight)
+    out = torch.empty(T, C, device="cuda")
+    hip.causal_conv_rows_device(drows.data_ptr(), stride, ds.data_ptr(), dw.data_ptr(), C, K, T, out.data_ptr())
+    torch.cuda.synchronize()
+    ref_state = state.reshape(-1).copy()
+    for t in range(T):
+        rl, rb = orc.gdn_gates(rows[t, off_a:off_a + H], rows[t, off_b:off_b + H], a_log, dt)
+        np.testing.assert_allclose(ld[t].cpu().numpy(), rl, rtol=4e-7, atol=1e-30)
+        np.testing.assert_allclose(be[t].cpu().numpy(), rb, rtol=4e-7, atol=1e-30)
+        ref = orc.causal_conv_silu_update(rows[t, :C], ref_state, weight.reshape(-1), C, K)
+        np.testing.assert_allclose(out[t].cpu().numpy(), ref, rtol=2e-6, atol=1e-6)
+    assert np.array_equal(ds.cpu().numpy().reshape(-1), ref_state)
