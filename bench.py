@@ -238,6 +238,44 @@ def bench_paged_attention(torch, hip, steps, tokens=32768):
     return res
 
 
+def bench_decode_27b(torch, hip, steps, context=32768):
+    """Config 5: the device engine on the 27B shapes (64 layers, 48 GatedDeltaNet
+    and 16 full attention, Q4 projections and LM head, Q2 down projections,
+    vocab 151936), paged KV page 16 with `context` random tokens; plain
+    batch-1 decode and MTP k = 4 at T = 0.7 (seeded Pcg32). Weights are
+    synthetic, so draft acceptance reflects random heads."""
+    import time
+    from ctox_hip.engine import Engine, EngineConfig
+    cfg = EngineConfig.qwen38_27b(max_tokens=context + 256)
+    eng = Engine(hip, cfg, seed=5)
+    eng.fill_context(context, seed=9)
+    q4 = (48 * (16480 * 5120 + 5120 * 6144) + 16 * (14336 * 5120 + 5120 * 6144) + 64 * 34816 * 5120
+          + 151936 * 5120) * 34 // 64
+    q2 = 64 * 5120 * 17408 * 18 // 64
+    tok = 1234
+    for _ in range(3):
+        eng.decode(tok)
+    n = max(10, min(steps, 40))
+    t0 = time.time()
+    for _ in range(n):
+        eng.decode(tok)
+    plain = (time.time() - t0) / n
+    eng.set_rng(0x5EED)
+    tokens = 0
+    t0 = time.time()
+    for _ in range(n):
+        nxt, acc = eng.mtp_step(tok, 0.7)
+        tokens += 1 + len(acc)
+        tok = nxt
+    mtp = time.time() - t0
+    eng.close()
+    return {"context": context, "page_tokens": 16, "weight_bytes_per_token": q4 + q2,
+            "plain_ms_per_token": plain * 1e3, "plain_tokens_per_s": 1.0 / plain,
+            "plain_weight_GBps": (q4 + q2) / plain / 1e9,
+            "mtp_k4_T0.7_ms_per_step": mtp / n * 1e3, "mtp_tokens_per_s": tokens / mtp,
+            "mtp_accepted_drafts_per_step": tokens / n - 1, "steps": n}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -282,6 +320,8 @@ def main():
         log("config5", extra["config5_token_selection"])
         extra["config5_paged_attention"] = bench_paged_attention(torch, hip, args.steps)
         log("config5 attention", extra["config5_paged_attention"])
+        extra["config5_decode_27b"] = bench_decode_27b(torch, hip, args.steps)
+        log("config5 decode", extra["config5_decode_27b"])
 
     extra["copy_reference"] = copy_reference(torch)
     log("copy", extra["copy_reference"])

@@ -694,8 +694,11 @@ extern "C" ctox_status ctox_hip_engine_fill_context(ctox_hip_engine *e, uint32_t
             const uint32_t n = std::min(chunk, tokens - t);
             TRY(fill(e, kbuf, (uint64_t)n * e->kvw, 2, sd + 2 * t, 0.0f, 1.0f));
             TRY(fill(e, vbuf, (uint64_t)n * e->kvw, 2, sd + 2 * t + 1, 0.0f, 1.0f));
-            TRY(cache_push(e, c, kbuf, vbuf, n));
-            TRY(cache_demote(e, c));
+            for (uint32_t o = 0; o < n; o += e->c.page_tokens) {  // demote as the pages fill
+                const uint32_t m = std::min(e->c.page_tokens, n - o);
+                TRY(cache_push(e, c, kbuf + (size_t)o * e->kvw, vbuf + (size_t)o * e->kvw, m));
+                TRY(cache_demote(e, c));
+            }
             TRY(cache_upload(e, c));
         }
         return CTOX_OK;
