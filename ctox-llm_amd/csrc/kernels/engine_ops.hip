@@ -108,34 +108,51 @@ extern "C" __global__ __launch_bounds__(256) void ctox_embed_rows_gfx950(EmbedAr
 
 __device__ __forceinline__ float eo_silu(float v) { return v / (1.0f + expf(-v)); }
 
-// One workgroup per row; sums of squares reduced in a fixed order.
-extern "C" __global__ __launch_bounds__(256) void ctox_norm_rows_gfx950(NormRowsArgs a) {
-    __shared__ float red[4];
-    const uint32_t r = blockIdx.x;
+// One workgroup per row, blockDim.x = 64 * waves threads; each thread keeps its
+// (up to NR_PER) columns c = tid + k * blockDim.x in registers, so every load
+// of the row is in flight at once. Sums of squares reduced in a fixed order.
+#define NR_PER 8
+extern "C" __global__ __launch_bounds__(1024) void ctox_norm_rows_gfx950(NormRowsArgs a) {
+    __shared__ float red[16];
+    const uint32_t r = blockIdx.x, T = blockDim.x, tid = threadIdx.x;
     const size_t xo = (size_t)(r / a.inner) * a.x_outer + (size_t)(r % a.inner) * a.x_inner;
     float *x = a.x + xo;
+    const float *dl = a.delta ? a.delta + (size_t)r * a.cols : nullptr;
+    float v[NR_PER];
     float s = 0.0f;
-    if (a.delta) {
-        const float *dl = a.delta + (size_t)r * a.cols;
-        for (uint32_t c = threadIdx.x; c < a.cols; c += 256) {
-            const float v = x[c] + dl[c];
-            x[c] = v;
-            s += v * v;
+#pragma unroll
+    for (int k = 0; k < NR_PER; k++) {
+        const uint32_t c = tid + k * T;
+        v[k] = c < a.cols ? x[c] : 0.0f;
+    }
+    if (dl) {
+#pragma unroll
+        for (int k = 0; k < NR_PER; k++) {
+            const uint32_t c = tid + k * T;
+            if (c < a.cols) {
+                v[k] += dl[c];
+                x[c] = v[k];
+            }
         }
-    } else {
-        for (uint32_t c = threadIdx.x; c < a.cols; c += 256) s += x[c] * x[c];
     }
 #pragma unroll
+    for (int k = 0; k < NR_PER; k++) s += v[k] * v[k];
+#pragma unroll
     for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    if ((tid & 63) == 0) red[tid >> 6] = s;
     __syncthreads();
-    const float var = ((red[0] + red[1]) + (red[2] + red[3])) / (float)a.cols;
-    const float inv = 1.0f / sqrtf(var + a.eps);
+    float tot = 0.0f;
+    for (uint32_t w = 0; w < T / 64; w++) tot += red[w];
+    const float inv = 1.0f / sqrtf(tot / (float)a.cols + a.eps);
     float *y = a.out + (size_t)r * a.out_stride;
     const float *g = a.gate ? a.gate + (size_t)(r / a.inner) * a.g_outer + (size_t)(r % a.inner) * a.g_inner : nullptr;
-    for (uint32_t c = threadIdx.x; c < a.cols; c += 256) {
-        const float n = x[c] * inv;
-        y[c] = a.mode == 0 ? n * (1.0f + a.w[c]) : n * a.w[c] * eo_silu(g[c]);
+#pragma unroll
+    for (int k = 0; k < NR_PER; k++) {
+        const uint32_t c = tid + k * T;
+        if (c < a.cols) {
+            const float n = v[k] * inv;
+            y[c] = a.mode == 0 ? n * (1.0f + a.w[c]) : n * a.w[c] * eo_silu(g[c]);
+        }
     }
 }
 

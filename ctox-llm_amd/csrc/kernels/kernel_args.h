@@ -39,6 +39,18 @@ struct PrepArgs {
     uint32_t pad;
 };
 
+// Residual add + RMS norm fused with the activation staging (qmatvec.hip).
+struct NormPrepArgs {
+    PrepArgs p;             // input unused; columns, batch, dtype, s_in as for the prep
+    const float *x;         // [batch][columns]
+    const float *delta;     // [batch][columns] or NULL
+    float *x_out;           // x + delta when delta is set (must not alias x)
+    const float *w;         // [columns], (1 + w) weight
+    float *out;             // normalized rows [batch][columns] or NULL
+    float eps;
+    uint32_t pad;
+};
+
 // One workgroup per 16 output rows (grid = ceil(rows / 16)); its four waves
 // split the K dimension.
 struct MatvecArgs {

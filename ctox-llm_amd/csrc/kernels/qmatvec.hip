@@ -72,11 +72,9 @@ __device__ __forceinline__ int frag_pos(uint32_t dtype, int w) {
 // One wave (64 threads) per (block, token). Output layout:
 //   xa: [block][token][limb 0..2][quarter 0..3][16 bytes]
 //   xc: [block][token] float4 {2q, 512q, 131072q, K*q}, K = -off*sum(X)
-extern "C" __global__ __launch_bounds__(64) void ctox_prep_activation_gfx950(PrepArgs a) {
-    const uint32_t b = blockIdx.x, t = blockIdx.y, e = threadIdx.x;
-    const uint32_t col = b * CTOX_BLOCK_LEN + e;
-    float x = a.input[(size_t)t * a.columns + col];
-    if (a.s_in_kind != CTOX_KSCALE_NONE) x = x * load_scale(a.s_in, a.s_in_kind, col);
+// Prepares one 64-value block of token t from one value per lane (x already
+// multiplied by s_in); every lane of the wave takes part.
+__device__ __forceinline__ void prep_block(const PrepArgs &a, float x, uint32_t b, uint32_t t, uint32_t e) {
     const bool bad = !__builtin_isfinite(x);
     const bool any_bad = __any(bad);
     const float m = wave_max(bad ? 0.0f : fabsf(x));
@@ -113,6 +111,58 @@ extern "C" __global__ __launch_bounds__(64) void ctox_prep_activation_gfx950(Pre
         c.w = (float)(-off * sx) * q;
         ((float4 *)a.xc)[(size_t)b * a.batch + t] = c;
     }
+}
+
+extern "C" __global__ __launch_bounds__(64) void ctox_prep_activation_gfx950(PrepArgs a) {
+    const uint32_t b = blockIdx.x, t = blockIdx.y, e = threadIdx.x;
+    const uint32_t col = b * CTOX_BLOCK_LEN + e;
+    float x = a.input[(size_t)t * a.columns + col];
+    if (a.s_in_kind != CTOX_KSCALE_NONE) x = x * load_scale(a.s_in, a.s_in_kind, col);
+    prep_block(a, x, b, t, e);
+}
+
+// Residual add + (1 + w) RMS norm of token row t (Q/src/reference.rs:38-62),
+// then the activation staging of prep_block from the normalized row.
+// grid (ceil(blocks / 4), batch), 256 threads: every workgroup reduces the
+// whole row's sum of squares itself (the row is L2-resident, a few KB), then
+// each of its four waves stages one 64-value block. The residual sum goes to
+// x_out, so no workgroup reads a value another one has already updated.
+extern "C" __global__ __launch_bounds__(256) void ctox_norm_prep_gfx950(NormPrepArgs a) {
+    __shared__ float red[4];
+    const uint32_t t = blockIdx.y, tid = threadIdx.x, cols = a.p.columns;
+    const float *x = a.x + (size_t)t * cols;
+    const float *dl = a.delta ? a.delta + (size_t)t * cols : nullptr;
+    float s = 0.0f;
+    const uint32_t n4 = cols / 4;
+#pragma unroll 4
+    for (uint32_t i = tid; i < n4; i += 256) {
+        float4 v = ((const float4 *)x)[i];
+        if (dl) {
+            const float4 d = ((const float4 *)dl)[i];
+            v.x += d.x;
+            v.y += d.y;
+            v.z += d.z;
+            v.w += d.w;
+        }
+        s += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    if ((tid & 63) == 0) red[tid >> 6] = s;
+    __syncthreads();
+    const float inv = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)cols + a.eps);
+    const uint32_t wave = tid >> 6, e = tid & 63;
+    const uint32_t b = blockIdx.x * 4 + wave;
+    if (b >= cols / CTOX_BLOCK_LEN) return;
+    const uint32_t col = b * CTOX_BLOCK_LEN + e;
+    float v = x[col];
+    if (dl) {
+        v += dl[col];
+        a.x_out[(size_t)t * cols + col] = v;
+    }
+    const float y = v * inv * (1.0f + a.w[col]);
+    if (a.out) a.out[(size_t)t * cols + col] = y;
+    prep_block(a.p, a.p.s_in_kind != CTOX_KSCALE_NONE ? y * load_scale(a.p.s_in, a.p.s_in_kind, col) : y, b, t, e);
 }
 
 template <int DT, int MODE>  // MODE 0: batch 1, 1: batch 2..4, 2: batch 5..8

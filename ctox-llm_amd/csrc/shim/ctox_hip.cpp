@@ -136,7 +136,7 @@ struct ctox_hip_backend {
                   pick_sums = nullptr, pick_final = nullptr, rms = nullptr, swiglu = nullptr, sgate = nullptr,
                   conv = nullptr, rope = nullptr, kv_pack = nullptr, kv_demote = nullptr, gqa_part[2] = {},
                   gqa_combine = nullptr, fill = nullptr, embed = nullptr, norm_rows = nullptr, attn_gate = nullptr,
-                  swiglu_rows = nullptr, copy_rows = nullptr, write_words = nullptr;
+                  swiglu_rows = nullptr, copy_rows = nullptr, write_words = nullptr, norm_prep = nullptr;
     // Batch-1 slice kernels per dtype [Q2, Q4]: [0] walks the slices, [n]
     // requests all n slices up front.
     hipFunction_t sl[2][4] = {};
@@ -439,7 +439,7 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->fill, "ctox_fill_random_gfx950"},      {&b->embed, "ctox_embed_rows_gfx950"},
                {&b->norm_rows, "ctox_norm_rows_gfx950"},   {&b->attn_gate, "ctox_attn_gate_gfx950"},
                {&b->swiglu_rows, "ctox_swiglu_rows_gfx950"}, {&b->copy_rows, "ctox_copy_rows_gfx950"},
-               {&b->write_words, "ctox_write_words_gfx950"},
+               {&b->write_words, "ctox_write_words_gfx950"}, {&b->norm_prep, "ctox_norm_prep_gfx950"},
                {&b->sl[0][0], "ctox_q2_matvec_sl_gfx950"}, {&b->sl[0][1], "ctox_q2_matvec_sl1_gfx950"},
                {&b->sl[0][2], "ctox_q2_matvec_sl2_gfx950"}, {&b->sl[0][3], "ctox_q2_matvec_sl3_gfx950"},
                {&b->sl[1][0], "ctox_q4_matvec_sl_gfx950"}, {&b->sl[1][1], "ctox_q4_matvec_sl1_gfx950"},
@@ -615,6 +615,48 @@ extern "C" ctox_status ctox_hip_launch_fused_matvec(ctox_hip_backend *b, int32_t
 // ======================================================================
 // Backend trait on host buffers
 // ======================================================================
+extern "C" ctox_status ctox_hip_norm_matvec_device(ctox_hip_backend *b, const float *d_x, const float *d_delta,
+                                                  float *d_x_out, const float *d_norm_w, float eps,
+                                                  float *d_norm_out, int32_t dtype,
+                                                  const void *d_weights, const uint16_t *d_s_in,
+                                                  const uint16_t *d_s_out, float *d_output, uint32_t rows,
+                                                  uint32_t columns, uint32_t batch, void *stream) {
+    if (!b || !d_x || !d_norm_w || !d_weights || !d_output || (d_delta && !d_x_out))
+        return fail(CTOX_ERR_SHAPE, "null argument");
+    if (d_delta && d_x_out == d_x) return fail(CTOX_ERR_SHAPE, "norm-matvec residual output must not alias its input");
+    if (dtype != CTOX_DTYPE_Q2B64 && dtype != CTOX_DTYPE_Q4B64)
+        return fail(CTOX_ERR_UNSUPPORTED_DTYPE, "norm-matvec takes pure Q2_B64 or Q4_B64 weights");
+    if (rows == 0 || columns == 0 || columns % kBlockLen || columns > 16384)
+        return fail(CTOX_ERR_SHAPE, "norm-matvec columns must be a non-zero multiple of 64 up to 16384");
+    if (batch == 0 || batch > CTOX_MAX_BATCH) return fail(CTOX_ERR_SHAPE, "batch %u outside 1..%d", batch, CTOX_MAX_BATCH);
+    if (!std::isfinite(eps) || eps <= 0.0f) return fail(CTOX_ERR_SHAPE, "norm epsilon must be finite and positive");
+    hipStream_t s = pick_stream(b, stream);
+    const int layout = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
+    const size_t blocks = columns / kBlockLen;
+    ctox_status st = ensure(b, b->xa[layout], blocks * batch * 192, false);
+    if (!st) st = ensure(b, b->xc[layout], blocks * batch * 4 * sizeof(float), false);
+    if (st) return st;
+    NormPrepArgs a{};
+    a.p.s_in = d_s_in;
+    a.p.xa = (int8_t *)b->xa[layout].ptr;
+    a.p.xc = (float *)b->xc[layout].ptr;
+    a.p.columns = columns;
+    a.p.batch = batch;
+    a.p.dtype = (uint32_t)layout;
+    a.p.s_in_kind = d_s_in ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE;
+    a.p.tgroups = (batch + 3) / 4;
+    a.x = d_x;
+    a.delta = d_delta;
+    a.x_out = d_x_out;
+    a.w = d_norm_w;
+    a.out = d_norm_out;
+    a.eps = eps;
+    if ((st = launch(b->norm_prep, dim3((unsigned)((blocks + 3) / 4), batch), dim3(256), s, a, "ctox_norm_prep_gfx950")))
+        return st;
+    return run_matvec(b, layout, dtype, d_weights, rows, columns, batch, d_s_out,
+                      d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, nullptr, d_output, rows, 0, s);
+}
+
 extern "C" ctox_status ctox_hip_fused_matvec(ctox_hip_backend *b, const ctox_fused_matvec *op, float *output,
                                              size_t output_len) {
     if (!b || !op || !output) return fail(CTOX_ERR_SHAPE, "null argument");
@@ -1216,9 +1258,12 @@ extern "C" ctox_status ctox_hip_norm_rows_device(ctox_hip_backend *b, const ctox
     if (d->rows == 0 || d->cols == 0 || d->inner == 0 || d->mode > 1)
         return fail(CTOX_ERR_SHAPE, "norm rows shape is empty or mode unknown");
     if (!std::isfinite(d->eps) || d->eps <= 0.0f) return fail(CTOX_ERR_SHAPE, "norm epsilon must be finite and positive");
+    // Up to 8 columns per thread, 64..1024 threads.
+    if (d->cols > 8 * 1024) return fail(CTOX_ERR_SHAPE, "norm rows wider than 8192");
+    const uint32_t threads = std::min<uint32_t>(1024, 64 * ((d->cols + 511) / 512));
     NormRowsArgs a{d->x, d->delta, d->gate, d->w, d->out, d->cols, d->mode, d->eps, d->inner,
                    d->x_inner, d->x_outer, d->g_inner, d->g_outer, d->out_stride};
-    return launch(b->norm_rows, dim3(d->rows), dim3(256), pick_stream(b, stream), a, "ctox_norm_rows_gfx950");
+    return launch(b->norm_rows, dim3(d->rows), dim3(threads), pick_stream(b, stream), a, "ctox_norm_rows_gfx950");
 }
 
 extern "C" ctox_status ctox_hip_attention_gate_device(ctox_hip_backend *b, float *d_values, const float *d_qg,

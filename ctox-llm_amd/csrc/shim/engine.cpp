@@ -110,7 +110,7 @@ struct ctox_hip_engine {
     float *gdn_state = nullptr, *gdn_ckpt = nullptr, *conv_state = nullptr, *conv_ckpt = nullptr;
     size_t gdn_floats = 0, conv_floats = 0;
     // activations (sized for R rows)
-    float *hid = nullptr, *xn = nullptr, *proj = nullptr, *convo = nullptr, *core = nullptr, *coren = nullptr,
+    float *hid = nullptr, *hid2 = nullptr, *xn = nullptr, *proj = nullptr, *convo = nullptr, *core = nullptr, *coren = nullptr,
           *delta = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *gu = nullptr, *act = nullptr,
           *fin = nullptr, *logits = nullptr, *ld = nullptr, *beta = nullptr, *fcin = nullptr;
     float *draft_logits = nullptr, *mtp_hidden = nullptr, *prev_hidden = nullptr, *target_hidden = nullptr;
@@ -182,6 +182,18 @@ ctox_status make_vec(ctox_hip_engine *e, float **p, size_t n, uint64_t &seed, fl
 ctox_status matvec(ctox_hip_engine *e, const Mat &m, const float *in, float *out, uint32_t rows) {
     return ctox_hip_launch_fused_matvec(e->b, m.dtype, m.w, in, m.s_in, m.s_out, nullptr, out, m.rows, m.cols, 0, rows,
                                         e->s);
+}
+
+// x += delta (when set), (1 + w) RMS norm, then the projection m of the
+// normalized rows into out; the normalized rows also go to norm_out if set.
+// The residual stream ping-pongs between e->hid and e->hid2: with a delta the
+// sum goes to the other buffer, which becomes the stream.
+ctox_status norm_mv(ctox_hip_engine *e, const float *delta, const float *w, uint32_t rows, const Mat &m, float *out,
+                    float *norm_out = nullptr) {
+    TRY(ctox_hip_norm_matvec_device(e->b, e->hid, delta, delta ? e->hid2 : nullptr, w, e->c.rms_norm_epsilon, norm_out,
+                                    m.dtype, m.w, m.s_in, m.s_out, out, m.rows, m.cols, rows, e->s));
+    if (delta) std::swap(e->hid, e->hid2);
+    return CTOX_OK;
 }
 
 // Norm of `rows` dense rows of width cols; x += delta first when delta is set.
@@ -327,7 +339,7 @@ ctox_status make_mlp(ctox_hip_engine *e, Mlp &m, uint64_t &seed) {
 // FullAttentionState::append does (decoder.rs:774).
 ctox_status attn_forward(ctox_hip_engine *e, AttnLayer &a, uint32_t R, uint32_t rope0, float *delta, bool retain) {
     const uint32_t qh = e->c.num_attention_heads, kvh = e->c.num_key_value_heads, hd = e->c.head_dim;
-    TRY(matvec(e, a.qkv, e->xn, e->proj, R));
+    // the q|k|v projection is already in e->proj (norm_mv)
     ctox_norm_rows d{};
     d.x = e->proj;
     d.w = a.q_norm;
@@ -361,9 +373,8 @@ ctox_status attn_forward(ctox_hip_engine *e, AttnLayer &a, uint32_t R, uint32_t 
 ctox_status gdn_forward(ctox_hip_engine *e, GdnLayer &g, uint32_t R, float *delta, bool keep_rows) {
     const uint32_t Hv = e->c.linear_num_value_heads, Hk = e->c.linear_num_key_heads;
     const uint32_t dk = e->c.linear_key_head_dim, dv = e->c.linear_value_head_dim;
-    float *proj = keep_rows ? g.proj : e->proj;
+    float *proj = keep_rows ? g.proj : e->proj;  // the in-projection, already computed (norm_mv)
     float *ld = keep_rows ? g.ld : e->ld, *beta = keep_rows ? g.beta : e->beta;
-    TRY(matvec(e, g.in, e->xn, proj, R));
     TRY(ctox_hip_causal_conv_rows_device(e->b, proj, e->Rin, g.conv, g.conv_w, e->C, e->c.linear_conv_kernel_dim, R,
                                          e->convo, e->s));
     TRY(ctox_hip_gdn_gates_strided_device(e->b, proj + e->C + e->Vw, proj + e->C + e->Vw + Hv, e->Rin, g.a_log,
@@ -389,9 +400,8 @@ ctox_status gdn_forward(ctox_hip_engine *e, GdnLayer &g, uint32_t R, float *delt
     return matvec(e, g.out, e->coren, delta, R);
 }
 
-ctox_status mlp_forward(ctox_hip_engine *e, Mlp &m, uint32_t R, float *h, const float *delta_in, float *delta_out) {
-    TRY(norm(e, h, delta_in, m.norm, R, e->H, e->xn, e->H));
-    TRY(matvec(e, m.gate_up, e->xn, e->gu, R));
+ctox_status mlp_forward(ctox_hip_engine *e, Mlp &m, uint32_t R, const float *delta_in, float *delta_out) {
+    TRY(norm_mv(e, delta_in, m.norm, R, m.gate_up, e->gu));
     TRY(ctox_hip_swiglu_rows_device(e->b, e->gu, 2 * e->I, e->I, R, e->I, e->act, e->I, e->s));
     return matvec(e, m.down, e->act, delta_out, R);
 }
@@ -403,16 +413,18 @@ ctox_status target_forward(ctox_hip_engine *e, const uint32_t *d_tok, uint32_t R
                                        e->H, e->hid, e->s));
     bool pending = false;
     for (Layer &L : e->layers) {
-        TRY(norm(e, e->hid, pending ? e->delta : nullptr, L.full ? L.f.norm : L.g.norm, R, e->H, e->xn, e->H));
-        if (L.full)
+        const float *dl = pending ? e->delta : nullptr;
+        if (L.full) {
+            TRY(norm_mv(e, dl, L.f.norm, R, L.f.qkv, e->proj));
             TRY(attn_forward(e, L.f, R, e->position, e->delta, keep_rows));
-        else
+        } else {
+            TRY(norm_mv(e, dl, L.g.norm, R, L.g.in, keep_rows ? L.g.proj : e->proj));
             TRY(gdn_forward(e, L.g, R, e->delta, keep_rows));
-        TRY(mlp_forward(e, L.mlp, R, e->hid, e->delta, e->delta));
+        }
+        TRY(mlp_forward(e, L.mlp, R, e->delta, e->delta));
         pending = true;
     }
-    TRY(norm(e, e->hid, e->delta, e->final_norm, R, e->H, e->fin, e->H));
-    return matvec(e, e->lm_head, e->fin, e->logits, R);
+    return norm_mv(e, e->delta, e->final_norm, R, e->lm_head, e->logits, e->fin);
 }
 
 // MTP over R rows: tokens d_tok, previous hiddens prev [R][H], rope positions rope0..;
@@ -426,12 +438,11 @@ ctox_status mtp_forward(ctox_hip_engine *e, const uint32_t *d_tok, const float *
     TRY(ctox_hip_copy_rows_device(e->b, prev, e->H, 0, R, e->H, e->xn, e->H, e->s));
     TRY(norm(e, e->xn, nullptr, e->mtp_norm_hid, R, e->H, e->fcin + e->H, 2 * e->H));
     TRY(matvec(e, e->mtp_fc, e->fcin, e->hid, R));
-    TRY(norm(e, e->hid, nullptr, e->mtp_attn.norm, R, e->H, e->xn, e->H));
+    TRY(norm_mv(e, nullptr, e->mtp_attn.norm, R, e->mtp_attn.qkv, e->proj));
     TRY(attn_forward(e, e->mtp_attn, R, rope0, e->delta, retain));
-    TRY(mlp_forward(e, e->mtp_mlp, R, e->hid, e->delta, e->delta));
-    TRY(norm(e, e->hid, e->delta, e->mtp_norm, R, e->H, e->mtp_hidden, e->H));
-    if (logits) TRY(matvec(e, e->lm_head, e->mtp_hidden, logits, R));
-    return CTOX_OK;
+    TRY(mlp_forward(e, e->mtp_mlp, R, e->delta, e->delta));
+    if (logits) return norm_mv(e, e->delta, e->mtp_norm, R, e->lm_head, logits, e->mtp_hidden);
+    return norm(e, e->hid, e->delta, e->mtp_norm, R, e->H, e->mtp_hidden, e->H);
 }
 
 ctox_status demote_all(ctox_hip_engine *e) {
@@ -550,7 +561,7 @@ extern "C" ctox_status ctox_hip_engine_create(ctox_hip_backend *b, const ctox_en
     }
     const size_t R = e->R, qh = c.num_attention_heads, hd = c.head_dim;
     const size_t widest = std::max<size_t>({e->Rin, e->Rq, 2 * (size_t)e->I, e->H});
-    if ((st = dalloc_t(e, &e->hid, R * e->H)) || (st = dalloc_t(e, &e->xn, R * e->H)) ||
+    if ((st = dalloc_t(e, &e->hid, R * e->H)) || (st = dalloc_t(e, &e->hid2, R * e->H)) || (st = dalloc_t(e, &e->xn, R * e->H)) ||
         (st = dalloc_t(e, &e->proj, R * widest)) || (st = dalloc_t(e, &e->convo, R * e->C)) ||
         (st = dalloc_t(e, &e->core, R * e->Vw)) || (st = dalloc_t(e, &e->coren, R * e->Vw)) ||
         (st = dalloc_t(e, &e->delta, R * e->H)) || (st = dalloc_t(e, &e->q, R * qh * hd)) ||

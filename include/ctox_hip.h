@@ -195,6 +195,20 @@ ctox_status ctox_hip_launch_fused_matvec(ctox_hip_backend *backend, int32_t dtyp
                                          uint32_t columns, uint32_t activation, uint32_t batch,
                                          void *stream);
 
+/* Residual add + (1 + w) RMS norm (Q/src/reference.rs:38-62) of `batch`
+ * dense rows: h = d_x + d_delta (d_delta may be NULL: h = d_x), written to
+ * d_x_out (required with d_delta, must not alias d_x); then the fused matvec
+ * of ctox_hip_launch_fused_matvec (identity activation, no bias) on the
+ * normalized rows, which also go to d_norm_out when it is set. The crate's
+ * residual + norm -> projection pairs (Q/src/decoder.rs:640-657, :718-731,
+ * :822-853) in one staging pass. columns <= 16384. */
+ctox_status ctox_hip_norm_matvec_device(ctox_hip_backend *backend, const float *d_x, const float *d_delta,
+                                        float *d_x_out, const float *d_norm_w, float eps, float *d_norm_out,
+                                        int32_t dtype,
+                                        const void *d_weights, const uint16_t *d_s_in, const uint16_t *d_s_out,
+                                        float *d_output, uint32_t rows, uint32_t columns, uint32_t batch,
+                                        void *stream);
+
 /* ---- gated delta (GatedDeltaNet) recurrence, fp32 state ----
  * Layouts follow Q/src/reference.rs:230-415: q, k [tokens][heads][key_dim]
  * (after Q/K head repetition), v [tokens][heads][value_dim], log_decay and

@@ -154,3 +154,46 @@ def test_strided_gates_and_conv_rows(hip, orc):
         ref = orc.causal_conv_silu_update(rows[t, :C], ref_state, weight.reshape(-1), C, K)
         np.testing.assert_allclose(out[t].cpu().numpy(), ref, rtol=2e-6, atol=1e-6)
     assert np.array_equal(ds.cpu().numpy().reshape(-1), ref_state)
+
+
+@pytest.mark.parametrize("batch,with_delta,dtype", [(1, True, 1), (3, False, 1), (5, True, 0)])
+def test_norm_matvec(hip, orc, batch, with_delta, dtype):
+    """Residual add + (1 + w) RMS norm fused with the projection's activation
+    staging, against the oracle norm followed by the oracle fused matvec."""
+    say(f"case norm_matvec batch={batch} delta={with_delta} dtype={dtype}")
+    from ctox_hip import synth  # noqa: F401  (weights built here directly)
+    rng = np.random.default_rng(batch * 10 + dtype)
+    rows, cols = 300, 5120
+    bb = 34 if dtype == 1 else 18
+    blocks = rng.integers(0, 256, size=(rows, cols // 64, bb), dtype=np.uint8)
+    scales = (np.abs(rng.standard_normal((rows, cols // 64))) * 0.02).astype(np.float16)
+    blocks[:, :, :2] = scales.view(np.uint8).reshape(rows, cols // 64, 2)
+    w_bytes = blocks.tobytes()
+    s_in = rng.uniform(0.75, 1.25, cols).astype(np.float16)
+    s_out = rng.uniform(0.75, 1.25, rows).astype(np.float16)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    d = rng.standard_normal((batch, cols)).astype(np.float32)
+    nw = (rng.standard_normal(cols) * 0.1).astype(np.float32)
+    dx, dd, dw = dev(x), dev(d), dev(nw)
+    dwt = torch.from_numpy(np.frombuffer(w_bytes, np.uint8).copy()).cuda()
+    dsi = torch.from_numpy(s_in.view(np.int16).copy()).cuda()
+    dso = torch.from_numpy(s_out.view(np.int16).copy()).cuda()
+    xo = torch.empty(batch, cols, device="cuda")
+    no = torch.empty(batch, cols, device="cuda")
+    out = torch.empty(batch, rows, device="cuda")
+    hip_lib = __import__("ctox_hip").load_library()
+    st = hip_lib.ctox_hip_norm_matvec_device(hip.handle, dx.data_ptr(), dd.data_ptr() if with_delta else None,
+                                             xo.data_ptr() if with_delta else None, dw.data_ptr(), 1e-6,
+                                             no.data_ptr(), dtype, dwt.data_ptr(), dsi.data_ptr(), dso.data_ptr(),
+                                             out.data_ptr(), rows, cols, batch, None)
+    assert st == 0, hip_lib.ctox_hip_last_error()
+    torch.cuda.synchronize()
+    for t in range(batch):
+        h = (x[t] + d[t]) if with_delta else x[t]
+        if with_delta:
+            assert np.array_equal(xo[t].cpu().numpy(), h)
+        y = orc.rms_norm_1p_weight(h, 1, cols, nw, 1e-6)
+        np.testing.assert_allclose(no[t].cpu().numpy(), y, rtol=1e-5, atol=1e-6)
+        ref = orc.fused_matvec(dtype, w_bytes, rows, cols, y, s_in=("f16le", s_in.view(np.uint8)),
+                               s_out=("f16le", s_out.view(np.uint8)))
+        np.testing.assert_allclose(out[t].cpu().numpy(), ref, rtol=1e-3, atol=1e-4 * float(np.abs(ref).max()))
