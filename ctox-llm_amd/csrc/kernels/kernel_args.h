@@ -51,6 +51,20 @@ struct NormPrepArgs {
     uint32_t pad;
 };
 
+// Activation staging of a transformed input (qmatvec.hip, ctox_prep_transform_gfx950).
+struct PrepXArgs {
+    PrepArgs p;             // input unused
+    const float *a;
+    const float *b;
+    const float *w;
+    uint32_t mode;          // 1 swiglu, 2 gated norm, 3 attention gate
+    uint32_t a_stride;
+    uint32_t b_stride;
+    uint32_t off;
+    uint32_t head_dim;
+    float eps;
+};
+
 // One workgroup per 16 output rows (grid = ceil(rows / 16)); its four waves
 // split the K dimension.
 struct MatvecArgs {

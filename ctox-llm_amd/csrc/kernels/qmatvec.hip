@@ -165,6 +165,46 @@ extern "C" __global__ __launch_bounds__(256) void ctox_norm_prep_gfx950(NormPrep
     prep_block(a.p, a.p.s_in_kind != CTOX_KSCALE_NONE ? y * load_scale(a.p.s_in, a.p.s_in_kind, col) : y, b, t, e);
 }
 
+// Activation staging of a value computed on the fly (one wave per 64-value
+// block and token, as the prep kernel): the producer of a projection's input
+// fused into its staging.
+//   mode 1  swiglu:   x = silu(a[t][c]) * a[t][off + c]       Q/src/reference.rs:96-112
+//   mode 2  gated norm per head of head_dim values:
+//           x = a[t][c] * rsqrt(mean_head(a^2) + eps) * w[c % head_dim] * silu(b[t][c])
+//                                                            Q/src/reference.rs:66-93
+//   mode 3  attention gate: x = a[t][c] * sigmoid(b[t][h * 2 hd + hd + d]),
+//           h = c / head_dim, d = c % head_dim              Q/src/decoder.rs:727-737, :788
+// a rows are a_stride floats apart, b rows b_stride.
+__device__ __forceinline__ float px_silu(float v) { return v / (1.0f + expf(-v)); }
+
+extern "C" __global__ __launch_bounds__(64) void ctox_prep_transform_gfx950(PrepXArgs a) {
+    const uint32_t b = blockIdx.x, t = blockIdx.y, e = threadIdx.x;
+    const uint32_t col = b * CTOX_BLOCK_LEN + e;
+    const float *ar = a.a + (size_t)t * a.a_stride;
+    float x;
+    if (a.mode == 1) {
+        x = px_silu(ar[col]) * ar[a.off + col];
+    } else if (a.mode == 2) {
+        const uint32_t head0 = col / a.head_dim * a.head_dim;
+        float ss = 0.0f;
+        for (uint32_t i = e; i < a.head_dim; i += 64) {  // this head's values, same order for every wave
+            const float v = ar[head0 + i];
+            ss += v * v;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        const float inv = 1.0f / sqrtf(ss / (float)a.head_dim + a.eps);
+        const float g = a.b[(size_t)t * a.b_stride + col];
+        x = ar[col] * inv * a.w[col % a.head_dim] * px_silu(g);
+    } else {
+        const uint32_t h = col / a.head_dim, d = col % a.head_dim;
+        const float g = a.b[(size_t)t * a.b_stride + (size_t)h * 2 * a.head_dim + a.head_dim + d];
+        x = ar[col] * (1.0f / (1.0f + expf(-g)));
+    }
+    if (a.p.s_in_kind != CTOX_KSCALE_NONE) x = x * load_scale(a.p.s_in, a.p.s_in_kind, col);
+    prep_block(a.p, x, b, t, e);
+}
+
 template <int DT, int MODE>  // MODE 0: batch 1, 1: batch 2..4, 2: batch 5..8
 struct MvCfg {
     static constexpr int BB = DT ? CTOX_Q4_BLOCK_BYTES : CTOX_Q2_BLOCK_BYTES;

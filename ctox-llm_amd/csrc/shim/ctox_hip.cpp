@@ -136,7 +136,8 @@ struct ctox_hip_backend {
                   pick_sums = nullptr, pick_final = nullptr, rms = nullptr, swiglu = nullptr, sgate = nullptr,
                   conv = nullptr, rope = nullptr, kv_pack = nullptr, kv_demote = nullptr, gqa_part[2] = {},
                   gqa_combine = nullptr, fill = nullptr, embed = nullptr, norm_rows = nullptr, attn_gate = nullptr,
-                  swiglu_rows = nullptr, copy_rows = nullptr, write_words = nullptr, norm_prep = nullptr;
+                  swiglu_rows = nullptr, copy_rows = nullptr, write_words = nullptr, norm_prep = nullptr,
+                  prep_x = nullptr;
     // Batch-1 slice kernels per dtype [Q2, Q4]: [0] walks the slices, [n]
     // requests all n slices up front.
     hipFunction_t sl[2][4] = {};
@@ -440,6 +441,7 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->norm_rows, "ctox_norm_rows_gfx950"},   {&b->attn_gate, "ctox_attn_gate_gfx950"},
                {&b->swiglu_rows, "ctox_swiglu_rows_gfx950"}, {&b->copy_rows, "ctox_copy_rows_gfx950"},
                {&b->write_words, "ctox_write_words_gfx950"}, {&b->norm_prep, "ctox_norm_prep_gfx950"},
+               {&b->prep_x, "ctox_prep_transform_gfx950"},
                {&b->sl[0][0], "ctox_q2_matvec_sl_gfx950"}, {&b->sl[0][1], "ctox_q2_matvec_sl1_gfx950"},
                {&b->sl[0][2], "ctox_q2_matvec_sl2_gfx950"}, {&b->sl[0][3], "ctox_q2_matvec_sl3_gfx950"},
                {&b->sl[1][0], "ctox_q4_matvec_sl_gfx950"}, {&b->sl[1][1], "ctox_q4_matvec_sl1_gfx950"},
@@ -653,6 +655,52 @@ extern "C" ctox_status ctox_hip_norm_matvec_device(ctox_hip_backend *b, const fl
     a.eps = eps;
     if ((st = launch(b->norm_prep, dim3((unsigned)((blocks + 3) / 4), batch), dim3(256), s, a, "ctox_norm_prep_gfx950")))
         return st;
+    return run_matvec(b, layout, dtype, d_weights, rows, columns, batch, d_s_out,
+                      d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, nullptr, d_output, rows, 0, s);
+}
+
+extern "C" ctox_status ctox_hip_transform_matvec_device(ctox_hip_backend *b, const ctox_input_transform *x,
+                                                       int32_t dtype, const void *d_weights, const uint16_t *d_s_in,
+                                                       const uint16_t *d_s_out, float *d_output, uint32_t rows,
+                                                       uint32_t columns, uint32_t batch, void *stream) {
+    if (!b || !x || !x->a || !d_weights || !d_output || ((x->mode == 2 || x->mode == 3) && !x->b) ||
+        (x->mode == 2 && !x->w))
+        return fail(CTOX_ERR_SHAPE, "null argument");
+    if (x->mode < 1 || x->mode > 3) return fail(CTOX_ERR_SHAPE, "unknown input transform %u", x->mode);
+    if (dtype != CTOX_DTYPE_Q2B64 && dtype != CTOX_DTYPE_Q4B64)
+        return fail(CTOX_ERR_UNSUPPORTED_DTYPE, "transform-matvec takes pure Q2_B64 or Q4_B64 weights");
+    if (rows == 0 || columns == 0 || columns % kBlockLen) return fail(CTOX_ERR_SHAPE, "transform-matvec dimensions");
+    if (batch == 0 || batch > CTOX_MAX_BATCH) return fail(CTOX_ERR_SHAPE, "batch %u outside 1..%d", batch, CTOX_MAX_BATCH);
+    if ((x->mode != 1 && (x->head_dim == 0 || columns % x->head_dim)) ||
+        (x->mode == 1 && x->a_stride < x->off + columns) || (x->mode != 1 && x->a_stride < columns) ||
+        (x->mode == 2 && (!std::isfinite(x->eps) || x->eps <= 0.0f || x->b_stride < columns)) ||
+        (x->mode == 3 && x->b_stride < 2 * columns))
+        return fail(CTOX_ERR_SHAPE, "transform-matvec input geometry");
+    hipStream_t s = pick_stream(b, stream);
+    const int layout = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
+    const size_t blocks = columns / kBlockLen;
+    ctox_status st = ensure(b, b->xa[layout], blocks * batch * 192, false);
+    if (!st) st = ensure(b, b->xc[layout], blocks * batch * 4 * sizeof(float), false);
+    if (st) return st;
+    PrepXArgs a{};
+    a.p.s_in = d_s_in;
+    a.p.xa = (int8_t *)b->xa[layout].ptr;
+    a.p.xc = (float *)b->xc[layout].ptr;
+    a.p.columns = columns;
+    a.p.batch = batch;
+    a.p.dtype = (uint32_t)layout;
+    a.p.s_in_kind = d_s_in ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE;
+    a.p.tgroups = (batch + 3) / 4;
+    a.a = x->a;
+    a.b = x->b;
+    a.w = x->w;
+    a.mode = x->mode;
+    a.a_stride = x->a_stride;
+    a.b_stride = x->b_stride;
+    a.off = x->off;
+    a.head_dim = x->head_dim;
+    a.eps = x->eps;
+    if ((st = launch(b->prep_x, dim3((unsigned)blocks, batch), dim3(64), s, a, "ctox_prep_transform_gfx950"))) return st;
     return run_matvec(b, layout, dtype, d_weights, rows, columns, batch, d_s_out,
                       d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, nullptr, d_output, rows, 0, s);
 }

@@ -366,8 +366,9 @@ ctox_status attn_forward(ctox_hip_engine *e, AttnLayer &a, uint32_t R, uint32_t 
     TRY(cache_upload(e, a.cache));
     const ctox_paged_gqa_params p = gqa_params(e, a.cache);
     TRY(ctox_hip_paged_gqa_device(e->b, e->q, a.cache.q2, a.cache.q4, a.cache.d_desc, &p, R, e->attn, e->s));
-    TRY(ctox_hip_attention_gate_device(e->b, e->attn, e->proj, R, qh, hd, e->Rq, e->s));
-    return matvec(e, a.o, e->attn, delta, R);
+    ctox_input_transform x{e->attn, e->proj, nullptr, 3, qh * hd, e->Rq, 0, hd, 0.0f};
+    return ctox_hip_transform_matvec_device(e->b, &x, a.o.dtype, a.o.w, a.o.s_in, a.o.s_out, delta, a.o.rows, a.o.cols, R,
+                                            e->s);
 }
 
 ctox_status gdn_forward(ctox_hip_engine *e, GdnLayer &g, uint32_t R, float *delta, bool keep_rows) {
@@ -381,29 +382,16 @@ ctox_status gdn_forward(ctox_hip_engine *e, GdnLayer &g, uint32_t R, float *delt
                                           g.dt_bias, R, Hv, ld, beta, e->s));
     TRY(ctox_hip_gated_delta_strided_device(e->b, e->convo, e->convo + e->Kw, e->convo + 2 * e->Kw, e->C, e->C, ld,
                                             beta, g.state, R, Hv, Hk, dk, dv, 0, e->core, e->s));
-    ctox_norm_rows d{};
-    d.x = e->core;
-    d.gate = proj + e->C;
-    d.w = g.gnorm;
-    d.out = e->coren;
-    d.rows = R * Hv;
-    d.cols = dv;
-    d.mode = 1;
-    d.inner = Hv;
-    d.eps = e->c.rms_norm_epsilon;
-    d.x_inner = dv;
-    d.x_outer = (uint64_t)Hv * dv;
-    d.g_inner = dv;
-    d.g_outer = e->Rin;
-    d.out_stride = dv;
-    TRY(ctox_hip_norm_rows_device(e->b, &d, e->s));
-    return matvec(e, g.out, e->coren, delta, R);
+    ctox_input_transform x{e->core, proj + e->C, g.gnorm, 2, e->Vw, e->Rin, 0, dv, e->c.rms_norm_epsilon};
+    return ctox_hip_transform_matvec_device(e->b, &x, g.out.dtype, g.out.w, g.out.s_in, g.out.s_out, delta, g.out.rows,
+                                            g.out.cols, R, e->s);
 }
 
 ctox_status mlp_forward(ctox_hip_engine *e, Mlp &m, uint32_t R, const float *delta_in, float *delta_out) {
     TRY(norm_mv(e, delta_in, m.norm, R, m.gate_up, e->gu));
-    TRY(ctox_hip_swiglu_rows_device(e->b, e->gu, 2 * e->I, e->I, R, e->I, e->act, e->I, e->s));
-    return matvec(e, m.down, e->act, delta_out, R);
+    ctox_input_transform x{e->gu, nullptr, nullptr, 1, 2 * e->I, 0, e->I, 0, 0.0f};
+    return ctox_hip_transform_matvec_device(e->b, &x, m.down.dtype, m.down.w, m.down.s_in, m.down.s_out, delta_out,
+                                            m.down.rows, m.down.cols, R, e->s);
 }
 
 // Target model over R rows (tokens in d_tok, positions position..position+R-1).

@@ -209,6 +209,23 @@ ctox_status ctox_hip_norm_matvec_device(ctox_hip_backend *backend, const float *
                                         float *d_output, uint32_t rows, uint32_t columns, uint32_t batch,
                                         void *stream);
 
+/* The projection of a value computed on the fly from its producer's output,
+ * staged in the same pass (rows of a at t * a_stride, of b at t * b_stride):
+ *   mode 1 swiglu (Q/src/reference.rs:96-112): silu(a[c]) * a[off + c];
+ *   mode 2 rms_norm_gated per head of head_dim values (Q/src/reference.rs:66-93):
+ *          a = core, b = gate z, w = norm weight [head_dim];
+ *   mode 3 attention sigmoid gate (Q/src/decoder.rs:727-737, :788): a = attention
+ *          output, b = q_proj rows holding [q, gate] per head. */
+typedef struct {
+    const float *a, *b, *w;
+    uint32_t mode, a_stride, b_stride, off, head_dim;
+    float eps;
+} ctox_input_transform;
+ctox_status ctox_hip_transform_matvec_device(ctox_hip_backend *backend, const ctox_input_transform *x, int32_t dtype,
+                                             const void *d_weights, const uint16_t *d_s_in, const uint16_t *d_s_out,
+                                             float *d_output, uint32_t rows, uint32_t columns, uint32_t batch,
+                                             void *stream);
+
 /* ---- gated delta (GatedDeltaNet) recurrence, fp32 state ----
  * Layouts follow Q/src/reference.rs:230-415: q, k [tokens][heads][key_dim]
  * (after Q/K head repetition), v [tokens][heads][value_dim], log_decay and
