@@ -130,7 +130,9 @@ extern "C" __global__ __launch_bounds__(1024) void ctox_norm_rows_gfx950(NormRow
         for (int k = 0; k < NR_PER; k++) {
             const uint32_t c = tid + k * T;
             if (c < a.cols) {
-                v[k] += dl[c];
+                float d = dl[c];
+                for (uint32_t p = 1; p < a.delta_parts; p++) d += dl[(size_t)p * a.delta_stride + c];
+                v[k] += d;
                 x[c] = v[k];
             }
         }

@@ -43,8 +43,10 @@ struct PrepArgs {
 struct NormPrepArgs {
     PrepArgs p;             // input unused; columns, batch, dtype, s_in as for the prep
     const float *x;         // [batch][columns]
-    const float *delta;     // [batch][columns] or NULL
+    const float *delta;     // [delta_parts][batch][columns] partial sums (added in part order) or NULL
     float *x_out;           // x + delta when delta is set (must not alias x)
+    uint32_t delta_parts;
+    uint32_t delta_stride;  // floats between parts
     const float *w;         // [columns], (1 + w) weight
     float *out;             // normalized rows [batch][columns] or NULL
     float eps;
@@ -81,6 +83,9 @@ struct MatvecArgs {
     uint32_t out_stride;
     uint32_t s_out_kind;
     uint32_t activation;
+    uint32_t part_stride;   // split K (slice kernels, gridDim.y > 1): workgroup y takes
+                            // slice y and writes its partial at output + y * part_stride
+    uint32_t pad;
 };
 
 // Batch-1 slice kernels (rows of whole 16-byte units): a workgroup of
@@ -337,6 +342,8 @@ struct NormRowsArgs {
     float eps;
     uint32_t inner;
     uint64_t x_inner, x_outer, g_inner, g_outer, out_stride;
+    uint32_t delta_parts;    // partial sums in delta (>= 1)
+    uint32_t delta_stride;   // floats between parts
 };
 
 struct AttnGateArgs {

@@ -134,18 +134,49 @@ extern "C" __global__ __launch_bounds__(256) void ctox_norm_prep_gfx950(NormPrep
     const float *dl = a.delta ? a.delta + (size_t)t * cols : nullptr;
     float s = 0.0f;
     const uint32_t n4 = cols / 4;
-#pragma unroll 4
-    for (uint32_t i = tid; i < n4; i += 256) {
-        float4 v = ((const float4 *)x)[i];
-        if (dl) {
-            const float4 d = ((const float4 *)dl)[i];
-            v.x += d.x;
-            v.y += d.y;
-            v.z += d.z;
-            v.w += d.w;
-        }
-        s += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    // Every load of a thread's row share (up to 8 float4 per array, all parts)
+    // is issued before the first use; parts are added in part order.
+#define NP_V4 8
+#define NP_PARTS 8
+    float4 v[NP_V4];
+#pragma unroll
+    for (int k = 0; k < NP_V4; k++) {
+        const uint32_t i = tid + 256 * k;
+        v[k] = i < n4 ? ((const float4 *)x)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
+    if (dl) {
+        float4 d[NP_V4];
+#pragma unroll
+        for (int k = 0; k < NP_V4; k++) {
+            const uint32_t i = tid + 256 * k;
+            d[k] = i < n4 ? ((const float4 *)dl)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int p = 1; p < NP_PARTS; p++) {
+            if ((uint32_t)p < a.delta_parts) {
+#pragma unroll
+                for (int k = 0; k < NP_V4; k++) {
+                    const uint32_t i = tid + 256 * k;
+                    if (i < n4) {
+                        const float4 d2 = ((const float4 *)(dl + (size_t)p * a.delta_stride))[i];
+                        d[k].x += d2.x;
+                        d[k].y += d2.y;
+                        d[k].z += d2.z;
+                        d[k].w += d2.w;
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < NP_V4; k++) {
+            v[k].x += d[k].x;
+            v[k].y += d[k].y;
+            v[k].z += d[k].z;
+            v[k].w += d[k].w;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < NP_V4; k++) s += v[k].x * v[k].x + v[k].y * v[k].y + v[k].z * v[k].z + v[k].w * v[k].w;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
     if ((tid & 63) == 0) red[tid >> 6] = s;
@@ -155,12 +186,14 @@ extern "C" __global__ __launch_bounds__(256) void ctox_norm_prep_gfx950(NormPrep
     const uint32_t b = blockIdx.x * 4 + wave;
     if (b >= cols / CTOX_BLOCK_LEN) return;
     const uint32_t col = b * CTOX_BLOCK_LEN + e;
-    float v = x[col];
+    float xv = x[col];
     if (dl) {
-        v += dl[col];
-        a.x_out[(size_t)t * cols + col] = v;
+        float d = dl[col];
+        for (uint32_t p = 1; p < a.delta_parts; p++) d += dl[(size_t)p * a.delta_stride + col];
+        xv += d;
+        a.x_out[(size_t)t * cols + col] = xv;
     }
-    const float y = v * inv * (1.0f + a.w[col]);
+    const float y = xv * inv * (1.0f + a.w[col]);
     if (a.out) a.out[(size_t)t * cols + col] = y;
     prep_block(a.p, a.p.s_in_kind != CTOX_KSCALE_NONE ? y * load_scale(a.p.s_in, a.p.s_in_kind, col) : y, b, t, e);
 }

@@ -145,14 +145,17 @@ __device__ __forceinline__ void qmatvec_slices(const MatvecArgs &a) {
     };
 
     if (NS > 0) {
+        // Split K (gridDim.y > 1): workgroup y takes slices NS y .. NS y + NS - 1;
+        // slices past the row are masked (their blocks count as zero).
+        const uint32_t s0 = blockIdx.y * NS;
         SlLoad<DT> sl[NS > 0 ? NS : 1];
 #pragma unroll
         for (int s = 0; s < NS; s++) {
-            issue(sl[s], min((uint32_t)s, ns - 1));
+            issue(sl[s], min(s0 + (uint32_t)s, ns - 1));
             __builtin_amdgcn_sched_barrier(0);  // keep slices in request order
         }
 #pragma unroll
-        for (int s = 0; s < NS; s++) consume(sl[s], s);
+        for (int s = 0; s < NS; s++) consume(sl[s], s0 + s);
     } else {
         SlLoad<DT> cur;
         issue(cur, 0);
@@ -171,7 +174,7 @@ __device__ __forceinline__ void qmatvec_slices(const MatvecArgs &a) {
         float sum = 0.0f;
 #pragma unroll
         for (int q = 0; q < (int)C::NW; q++) sum += red[q][tid];
-        a.output[row0 + tid] = epilogue(sum / C::DEN, row0 + tid, a);
+        a.output[(size_t)blockIdx.y * a.part_stride + row0 + tid] = epilogue(sum / C::DEN, row0 + tid, a);
     }
 }
 

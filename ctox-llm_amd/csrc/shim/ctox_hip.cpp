@@ -319,10 +319,13 @@ ctox_status run_prep(ctox_hip_backend *b, int layout, const float *d_input, size
 // One launch over `rows` packed rows of one dtype (a pure matrix or one
 // mixed segment), output rows written at d_output[m*out_stride + r], with
 // the activation already staged in `layout`.
+// split: split K into one partial per slice where the batch-1 slice kernel
+// applies (outputs [parts][rows]; *parts reports the count, 1 otherwise).
 ctox_status run_matvec(ctox_hip_backend *b, int layout, int32_t dtype, const void *d_weights, size_t rows,
                        size_t columns, size_t batch, const void *d_s_out, uint32_t s_out_kind,
                        const float *d_bias, float *d_output, size_t out_stride, uint32_t act,
-                       hipStream_t s) {
+                       hipStream_t s, bool split = false, uint32_t *parts = nullptr) {
+    if (parts) *parts = 1;
     const size_t groups = (rows + CTOX_MV_ROWS - 1) / CTOX_MV_ROWS;
     const size_t tgroups = (batch + 3) / 4;
     if (groups > 0x7fffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
@@ -346,6 +349,14 @@ ctox_status run_matvec(ctox_hip_backend *b, int layout, int32_t dtype, const voi
     const size_t rb = packed_row_bytes(dtype, columns);
     if (batch == 1 && rb % 16 == 0 && ((uintptr_t)d_weights & 15) == 0) {
         const size_t ns = (columns / kBlockLen + ctox_slice_blocks(q4) - 1) / ctox_slice_blocks(q4);
+        // Split K for tile counts that leave CUs idle: two slices per part.
+        if (split && ns > 2 && !d_bias && act == 0 && ns <= 65535 && groups < 2 * (size_t)b->cus) {
+            const uint32_t np = (uint32_t)((ns + 1) / 2);
+            a.part_stride = (uint32_t)rows;
+            if (parts) *parts = np;
+            return launch(b->sl[q4 ? 1 : 0][2], dim3((unsigned)groups, np), dim3(CTOX_SLICE_WAVES * 64), s, a,
+                          "ctox_q*_matvec_sl2_gfx950");
+        }
         hipFunction_t f = b->sl[q4 ? 1 : 0][ns <= 3 ? ns : 0];
         return launch(f, dim3((unsigned)groups), dim3(CTOX_SLICE_WAVES * 64), s, a, "ctox_q*_matvec_sl*_gfx950");
     }
@@ -618,6 +629,7 @@ extern "C" ctox_status ctox_hip_launch_fused_matvec(ctox_hip_backend *b, int32_t
 // Backend trait on host buffers
 // ======================================================================
 extern "C" ctox_status ctox_hip_norm_matvec_device(ctox_hip_backend *b, const float *d_x, const float *d_delta,
+                                                  uint32_t delta_parts, size_t delta_part_stride,
                                                   float *d_x_out, const float *d_norm_w, float eps,
                                                   float *d_norm_out, int32_t dtype,
                                                   const void *d_weights, const uint16_t *d_s_in,
@@ -626,10 +638,13 @@ extern "C" ctox_status ctox_hip_norm_matvec_device(ctox_hip_backend *b, const fl
     if (!b || !d_x || !d_norm_w || !d_weights || !d_output || (d_delta && !d_x_out))
         return fail(CTOX_ERR_SHAPE, "null argument");
     if (d_delta && d_x_out == d_x) return fail(CTOX_ERR_SHAPE, "norm-matvec residual output must not alias its input");
+    if (d_delta && (delta_parts == 0 || delta_parts > 8 || (delta_parts > 1 && delta_part_stride < (size_t)batch * columns) ||
+                    delta_part_stride > 0xffffffffu || delta_part_stride % 4))
+        return fail(CTOX_ERR_SHAPE, "norm-matvec delta parts geometry");
     if (dtype != CTOX_DTYPE_Q2B64 && dtype != CTOX_DTYPE_Q4B64)
         return fail(CTOX_ERR_UNSUPPORTED_DTYPE, "norm-matvec takes pure Q2_B64 or Q4_B64 weights");
-    if (rows == 0 || columns == 0 || columns % kBlockLen || columns > 16384)
-        return fail(CTOX_ERR_SHAPE, "norm-matvec columns must be a non-zero multiple of 64 up to 16384");
+    if (rows == 0 || columns == 0 || columns % kBlockLen || columns > 8192)
+        return fail(CTOX_ERR_SHAPE, "norm-matvec columns must be a non-zero multiple of 64 up to 8192");
     if (batch == 0 || batch > CTOX_MAX_BATCH) return fail(CTOX_ERR_SHAPE, "batch %u outside 1..%d", batch, CTOX_MAX_BATCH);
     if (!std::isfinite(eps) || eps <= 0.0f) return fail(CTOX_ERR_SHAPE, "norm epsilon must be finite and positive");
     hipStream_t s = pick_stream(b, stream);
@@ -649,6 +664,8 @@ extern "C" ctox_status ctox_hip_norm_matvec_device(ctox_hip_backend *b, const fl
     a.p.tgroups = (batch + 3) / 4;
     a.x = d_x;
     a.delta = d_delta;
+    a.delta_parts = d_delta ? delta_parts : 0;
+    a.delta_stride = (uint32_t)delta_part_stride;
     a.x_out = d_x_out;
     a.w = d_norm_w;
     a.out = d_norm_out;
@@ -662,7 +679,9 @@ extern "C" ctox_status ctox_hip_norm_matvec_device(ctox_hip_backend *b, const fl
 extern "C" ctox_status ctox_hip_transform_matvec_device(ctox_hip_backend *b, const ctox_input_transform *x,
                                                        int32_t dtype, const void *d_weights, const uint16_t *d_s_in,
                                                        const uint16_t *d_s_out, float *d_output, uint32_t rows,
-                                                       uint32_t columns, uint32_t batch, void *stream) {
+                                                       uint32_t columns, uint32_t batch, uint32_t split_k,
+                                                       uint32_t *parts, void *stream) {
+    if (parts) *parts = 1;
     if (!b || !x || !x->a || !d_weights || !d_output || ((x->mode == 2 || x->mode == 3) && !x->b) ||
         (x->mode == 2 && !x->w))
         return fail(CTOX_ERR_SHAPE, "null argument");
@@ -702,7 +721,7 @@ extern "C" ctox_status ctox_hip_transform_matvec_device(ctox_hip_backend *b, con
     a.eps = x->eps;
     if ((st = launch(b->prep_x, dim3((unsigned)blocks, batch), dim3(64), s, a, "ctox_prep_transform_gfx950"))) return st;
     return run_matvec(b, layout, dtype, d_weights, rows, columns, batch, d_s_out,
-                      d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, nullptr, d_output, rows, 0, s);
+                      d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, nullptr, d_output, rows, 0, s, split_k != 0, parts);
 }
 
 extern "C" ctox_status ctox_hip_fused_matvec(ctox_hip_backend *b, const ctox_fused_matvec *op, float *output,
@@ -1309,8 +1328,12 @@ extern "C" ctox_status ctox_hip_norm_rows_device(ctox_hip_backend *b, const ctox
     // Up to 8 columns per thread, 64..1024 threads.
     if (d->cols > 8 * 1024) return fail(CTOX_ERR_SHAPE, "norm rows wider than 8192");
     const uint32_t threads = std::min<uint32_t>(1024, 64 * ((d->cols + 511) / 512));
+    if (d->delta && (d->delta_parts > 64 || (d->delta_parts > 1 && (d->delta_stride < (uint64_t)d->rows * d->cols ||
+                                                                      d->delta_stride > 0xffffffffu))))
+        return fail(CTOX_ERR_SHAPE, "norm rows delta parts geometry");
     NormRowsArgs a{d->x, d->delta, d->gate, d->w, d->out, d->cols, d->mode, d->eps, d->inner,
-                   d->x_inner, d->x_outer, d->g_inner, d->g_outer, d->out_stride};
+                   d->x_inner, d->x_outer, d->g_inner, d->g_outer, d->out_stride,
+                   std::max<uint32_t>(1, d->delta_parts), (uint32_t)d->delta_stride};
     return launch(b->norm_rows, dim3(d->rows), dim3(threads), pick_stream(b, stream), a, "ctox_norm_rows_gfx950");
 }
 

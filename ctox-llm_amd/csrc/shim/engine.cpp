@@ -116,6 +116,7 @@ struct ctox_hip_engine {
     float *draft_logits = nullptr, *mtp_hidden = nullptr, *prev_hidden = nullptr, *target_hidden = nullptr;
     uint32_t *d_tokens = nullptr, *d_drafts = nullptr, *d_result = nullptr;
     uint64_t *d_rng = nullptr;
+    uint32_t delta_parts = 1;  // partial sums held in delta (split-K producers)
     uint32_t position = 0;   // tokens processed by the target model
     uint32_t mtp_tokens = 0; // entries in the MTP cache
     bool have_prev = false;  // prev_hidden holds the last target final hidden
@@ -190,8 +191,9 @@ ctox_status matvec(ctox_hip_engine *e, const Mat &m, const float *in, float *out
 // sum goes to the other buffer, which becomes the stream.
 ctox_status norm_mv(ctox_hip_engine *e, const float *delta, const float *w, uint32_t rows, const Mat &m, float *out,
                     float *norm_out = nullptr) {
-    TRY(ctox_hip_norm_matvec_device(e->b, e->hid, delta, delta ? e->hid2 : nullptr, w, e->c.rms_norm_epsilon, norm_out,
-                                    m.dtype, m.w, m.s_in, m.s_out, out, m.rows, m.cols, rows, e->s));
+    TRY(ctox_hip_norm_matvec_device(e->b, e->hid, delta, e->delta_parts, (size_t)rows * e->H, delta ? e->hid2 : nullptr,
+                                    w, e->c.rms_norm_epsilon, norm_out, m.dtype, m.w, m.s_in, m.s_out, out, m.rows,
+                                    m.cols, rows, e->s));
     if (delta) std::swap(e->hid, e->hid2);
     return CTOX_OK;
 }
@@ -212,6 +214,8 @@ ctox_status norm(ctox_hip_engine *e, float *x, const float *delta, const float *
     d.x_inner = cols;
     d.x_outer = 0;
     d.out_stride = out_stride;
+    d.delta_parts = delta ? e->delta_parts : 0;
+    d.delta_stride = (uint64_t)rows * cols;
     return ctox_hip_norm_rows_device(e->b, &d, e->s);
 }
 
@@ -368,7 +372,7 @@ ctox_status attn_forward(ctox_hip_engine *e, AttnLayer &a, uint32_t R, uint32_t 
     TRY(ctox_hip_paged_gqa_device(e->b, e->q, a.cache.q2, a.cache.q4, a.cache.d_desc, &p, R, e->attn, e->s));
     ctox_input_transform x{e->attn, e->proj, nullptr, 3, qh * hd, e->Rq, 0, hd, 0.0f};
     return ctox_hip_transform_matvec_device(e->b, &x, a.o.dtype, a.o.w, a.o.s_in, a.o.s_out, delta, a.o.rows, a.o.cols, R,
-                                            e->s);
+                                            1, &e->delta_parts, e->s);
 }
 
 ctox_status gdn_forward(ctox_hip_engine *e, GdnLayer &g, uint32_t R, float *delta, bool keep_rows) {
@@ -384,14 +388,14 @@ ctox_status gdn_forward(ctox_hip_engine *e, GdnLayer &g, uint32_t R, float *delt
                                             beta, g.state, R, Hv, Hk, dk, dv, 0, e->core, e->s));
     ctox_input_transform x{e->core, proj + e->C, g.gnorm, 2, e->Vw, e->Rin, 0, dv, e->c.rms_norm_epsilon};
     return ctox_hip_transform_matvec_device(e->b, &x, g.out.dtype, g.out.w, g.out.s_in, g.out.s_out, delta, g.out.rows,
-                                            g.out.cols, R, e->s);
+                                            g.out.cols, R, 1, &e->delta_parts, e->s);
 }
 
 ctox_status mlp_forward(ctox_hip_engine *e, Mlp &m, uint32_t R, const float *delta_in, float *delta_out) {
     TRY(norm_mv(e, delta_in, m.norm, R, m.gate_up, e->gu));
     ctox_input_transform x{e->gu, nullptr, nullptr, 1, 2 * e->I, 0, e->I, 0, 0.0f};
     return ctox_hip_transform_matvec_device(e->b, &x, m.down.dtype, m.down.w, m.down.s_in, m.down.s_out, delta_out,
-                                            m.down.rows, m.down.cols, R, e->s);
+                                            m.down.rows, m.down.cols, R, 1, &e->delta_parts, e->s);
 }
 
 // Target model over R rows (tokens in d_tok, positions position..position+R-1).
@@ -552,7 +556,7 @@ extern "C" ctox_status ctox_hip_engine_create(ctox_hip_backend *b, const ctox_en
     if ((st = dalloc_t(e, &e->hid, R * e->H)) || (st = dalloc_t(e, &e->hid2, R * e->H)) || (st = dalloc_t(e, &e->xn, R * e->H)) ||
         (st = dalloc_t(e, &e->proj, R * widest)) || (st = dalloc_t(e, &e->convo, R * e->C)) ||
         (st = dalloc_t(e, &e->core, R * e->Vw)) || (st = dalloc_t(e, &e->coren, R * e->Vw)) ||
-        (st = dalloc_t(e, &e->delta, R * e->H)) || (st = dalloc_t(e, &e->q, R * qh * hd)) ||
+        (st = dalloc_t(e, &e->delta, 16 * R * e->H)) || (st = dalloc_t(e, &e->q, R * qh * hd)) ||
         (st = dalloc_t(e, &e->k, R * e->kvw)) || (st = dalloc_t(e, &e->v, R * e->kvw)) ||
         (st = dalloc_t(e, &e->attn, R * qh * hd)) || (st = dalloc_t(e, &e->gu, R * 2 * e->I)) ||
         (st = dalloc_t(e, &e->act, R * e->I)) || (st = dalloc_t(e, &e->fin, R * e->H)) ||

@@ -199,12 +199,14 @@ ctox_status ctox_hip_launch_fused_matvec(ctox_hip_backend *backend, int32_t dtyp
  * dense rows: h = d_x + d_delta (d_delta may be NULL: h = d_x), written to
  * d_x_out (required with d_delta, must not alias d_x); then the fused matvec
  * of ctox_hip_launch_fused_matvec (identity activation, no bias) on the
- * normalized rows, which also go to d_norm_out when it is set. The crate's
+ * normalized rows, which also go to d_norm_out when it is set. A delta given
+ * as delta_parts partial sums (d_delta + p * delta_part_stride, the output of
+ * a split-K transform-matvec) is summed in part order first. The crate's
  * residual + norm -> projection pairs (Q/src/decoder.rs:640-657, :718-731,
- * :822-853) in one staging pass. columns <= 16384. */
+ * :822-853) in one staging pass. columns <= 8192, delta_parts <= 8. */
 ctox_status ctox_hip_norm_matvec_device(ctox_hip_backend *backend, const float *d_x, const float *d_delta,
-                                        float *d_x_out, const float *d_norm_w, float eps, float *d_norm_out,
-                                        int32_t dtype,
+                                        uint32_t delta_parts, size_t delta_part_stride, float *d_x_out,
+                                        const float *d_norm_w, float eps, float *d_norm_out, int32_t dtype,
                                         const void *d_weights, const uint16_t *d_s_in, const uint16_t *d_s_out,
                                         float *d_output, uint32_t rows, uint32_t columns, uint32_t batch,
                                         void *stream);
@@ -221,10 +223,14 @@ typedef struct {
     uint32_t mode, a_stride, b_stride, off, head_dim;
     float eps;
 } ctox_input_transform;
+/* split_k != 0 lets a batch-1 projection split its K range into one partial
+ * per 1 KiB slice of a row (balancing few-row, long-K matrices over the
+ * CUs): d_output then holds *parts partial outputs [parts][rows] whose sum
+ * (in part order) is the result; *parts = 1 when no split was made. */
 ctox_status ctox_hip_transform_matvec_device(ctox_hip_backend *backend, const ctox_input_transform *x, int32_t dtype,
                                              const void *d_weights, const uint16_t *d_s_in, const uint16_t *d_s_out,
                                              float *d_output, uint32_t rows, uint32_t columns, uint32_t batch,
-                                             void *stream);
+                                             uint32_t split_k, uint32_t *parts, void *stream);
 
 /* ---- gated delta (GatedDeltaNet) recurrence, fp32 state ----
  * Layouts follow Q/src/reference.rs:230-415: q, k [tokens][heads][key_dim]
@@ -413,8 +419,8 @@ typedef struct {
     float *out;          /* row r at r * out_stride */
     uint32_t rows, cols, mode, inner;  /* mode 0: (1 + w); 1: w * silu(gate) */
     float eps;
-    uint32_t pad;
-    uint64_t x_inner, x_outer, g_inner, g_outer, out_stride;
+    uint32_t delta_parts;  /* 0 or 1: one delta; n: n partial sums delta_stride floats apart */
+    uint64_t x_inner, x_outer, g_inner, g_outer, out_stride, delta_stride;
 } ctox_norm_rows;
 ctox_status ctox_hip_norm_rows_device(ctox_hip_backend *backend, const ctox_norm_rows *desc, void *stream);
 /* values[t][h][d] *= sigmoid(gate): the gate half of each head's [q, gate]

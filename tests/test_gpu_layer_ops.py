@@ -182,7 +182,7 @@ def test_norm_matvec(hip, orc, batch, with_delta, dtype):
     no = torch.empty(batch, cols, device="cuda")
     out = torch.empty(batch, rows, device="cuda")
     hip_lib = __import__("ctox_hip").load_library()
-    st = hip_lib.ctox_hip_norm_matvec_device(hip.handle, dx.data_ptr(), dd.data_ptr() if with_delta else None,
+    st = hip_lib.ctox_hip_norm_matvec_device(hip.handle, dx.data_ptr(), dd.data_ptr() if with_delta else None, 1, 0,
                                              xo.data_ptr() if with_delta else None, dw.data_ptr(), 1e-6,
                                              no.data_ptr(), dtype, dwt.data_ptr(), dsi.data_ptr(), dso.data_ptr(),
                                              out.data_ptr(), rows, cols, batch, None)
