@@ -283,6 +283,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only")
+    ap.add_argument("--only", choices=["decode", "attention", "gdn", "selection"],
+                    help="run one extra workload alone and print its result (for profiling)")
+    ap.add_argument("--context", type=int, default=32768, help="context of --only decode / attention")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -295,6 +298,13 @@ def main():
 
     hip = ctox_hip.HipBackend(0)
     log("backend", hip.kind(), hip.profile(), torch.cuda.get_device_name(0))
+    if args.only:
+        res = {"decode": lambda: bench_decode_27b(torch, hip, args.steps, args.context),
+               "attention": lambda: bench_paged_attention(torch, hip, args.steps, args.context),
+               "gdn": lambda: bench_gdn(torch, hip, args.steps),
+               "selection": lambda: bench_token_selection(torch, hip, args.steps)}[args.only]()
+        print(json.dumps({"only": args.only, "result": res}), flush=True)
+        return
 
     head, host2 = bench_matvec(torch, hip, ctox_hip, synth, 0, 5120, 17408, "swiglu", args.steps, args.warmup)
     log("config2", head)
