@@ -139,7 +139,8 @@ struct ctox_hip_backend {
                   swiglu_rows = nullptr, copy_rows = nullptr, write_words = nullptr, norm_prep = nullptr,
                   prep_x = nullptr;
     // Batch-1 slice kernels per dtype [Q2, Q4]: [0] walks the slices, [n]
-    // requests all n slices up front.
+    // requests all n slices up front (n <= 3: more slices up front measured
+    // slower than walking them).
     hipFunction_t sl[2][4] = {};
     // Small-M slice kernels per dtype [Q2, Q4]: [0] M = 2..4, [1] M = 5..8.
     hipFunction_t st[2][2] = {};
