@@ -238,6 +238,19 @@ def bench_paged_attention(torch, hip, steps, tokens=32768):
     return res
 
 
+def bench_verify_layer(torch, hip, ctox_hip, synth, batch, steps):
+    """Config 3: every projection of one decoder layer (q at the crate's
+    12288 rows, k, v, o, gate, up as Q4; down as Q2) on `batch` rows."""
+    tot_b, tot_us = 0, 0.0
+    for name, dt, r, c in [("q", 1, 12288, 5120), ("k", 1, 1024, 5120), ("v", 1, 1024, 5120),
+                           ("o", 1, 5120, 6144), ("gate", 1, 17408, 5120), ("up", 1, 17408, 5120),
+                           ("down", 0, 5120, 17408)]:
+        res, _ = bench_matvec(torch, hip, ctox_hip, synth, dt, r, c, "normal", max(20, steps // 4), 5, batch=batch)
+        tot_b += res["bytes_per_call"]
+        tot_us += res["step_us"]
+    return {"us": tot_us, "GBps": tot_b / (tot_us * 1e-6) / 1e9}
+
+
 def bench_decode_27b(torch, hip, steps, context=32768):
     """Config 5: the device engine on the 27B shapes (64 layers, 48 GatedDeltaNet
     and 16 full attention, Q4 projections and LM head, Q2 down projections,
@@ -283,7 +296,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only")
-    ap.add_argument("--only", choices=["decode", "attention", "gdn", "selection"],
+    ap.add_argument("--only", choices=["decode", "attention", "gdn", "selection", "verify", "config1", "config2"],
                     help="run one extra workload alone and print its result (for profiling)")
     ap.add_argument("--context", type=int, default=32768, help="context of --only decode / attention")
     args = ap.parse_args()
@@ -302,7 +315,12 @@ def main():
         res = {"decode": lambda: bench_decode_27b(torch, hip, args.steps, args.context),
                "attention": lambda: bench_paged_attention(torch, hip, args.steps, args.context),
                "gdn": lambda: bench_gdn(torch, hip, args.steps),
-               "selection": lambda: bench_token_selection(torch, hip, args.steps)}[args.only]()
+               "selection": lambda: bench_token_selection(torch, hip, args.steps),
+               "verify": lambda: bench_verify_layer(torch, hip, ctox_hip, synth, 5, args.steps),
+               "config1": lambda: bench_matvec(torch, hip, ctox_hip, synth, 1, 17408, 5120, "normal", args.steps,
+                                               args.warmup)[0],
+               "config2": lambda: bench_matvec(torch, hip, ctox_hip, synth, 0, 5120, 17408, "swiglu", args.steps,
+                                               args.warmup)[0]}[args.only]()
         print(json.dumps({"only": args.only, "result": res}), flush=True)
         return
 
@@ -314,15 +332,7 @@ def main():
         log("config1", c1)
         extra["config1_q4_up"] = c1
         for batch in (2, 4, 8):
-            tot_b, tot_us = 0, 0.0
-            for name, dt, r, c in [("q", 1, 12288, 5120), ("k", 1, 1024, 5120), ("v", 1, 1024, 5120),
-                                   ("o", 1, 5120, 6144), ("gate", 1, 17408, 5120), ("up", 1, 17408, 5120),
-                                   ("down", 0, 5120, 17408)]:
-                res, _ = bench_matvec(torch, hip, ctox_hip, synth, dt, r, c, "normal", max(20, args.steps // 4),
-                                      5, batch=batch)
-                tot_b += res["bytes_per_call"]
-                tot_us += res["step_us"]
-            extra[f"config3_verify_layer_M{batch}"] = {"us": tot_us, "GBps": tot_b / (tot_us * 1e-6) / 1e9}
+            extra[f"config3_verify_layer_M{batch}"] = bench_verify_layer(torch, hip, ctox_hip, synth, batch, args.steps)
             log("config3", batch, extra[f"config3_verify_layer_M{batch}"])
         extra["config4_gated_delta"] = bench_gdn(torch, hip, args.steps)
         log("config4", extra["config4_gated_delta"])
