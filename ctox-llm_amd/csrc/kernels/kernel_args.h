@@ -96,6 +96,60 @@ constexpr uint32_t ctox_slice_blocks(uint32_t dtype) { return dtype ? 28u : 56u;
 constexpr uint32_t ctox_slice_blocks_tok(uint32_t dtype) { return dtype ? 28u : 26u; }
 #define CTOX_SLICE_WAVES 8
 
+// Tiled weight layout (resident matrices): a unit is 16 rows x 16 blocks.
+// Unit (c, t) = column chunk c (blocks 16c..16c+15), row tile t (rows
+// 16t..16t+15) sits at byte ((c * tiles) + t) * unit_bytes. Inside a unit:
+//   codes: 4 groups G, each Q2: [lane][16 B], Q4: [half][lane][16 B], where
+//          lane (g, j) = 16 g + j holds the code bytes (Q4: bytes 16 half ..)
+//          of block 16c + 4G + g of row 16t + j;
+//   scales (after the codes): [lane][4 x fp16], scale of group G's block.
+// Blocks and rows past the matrix are zero (zero scale).
+#define CTOX_TILE_ROWS 16
+#define CTOX_TILE_BLOCKS 16
+constexpr uint32_t ctox_tile_code_bytes(uint32_t dtype) { return dtype ? 8192u : 4096u; }
+constexpr uint32_t ctox_tile_unit_bytes(uint32_t dtype) { return ctox_tile_code_bytes(dtype) + 512u; }
+// Row tiles one wave of the tiled matvec handles at most.
+#define CTOX_TILE_MAXU 4
+
+struct TileRepackArgs {
+    const uint8_t *src;     // crate rows, [rows][blocks * block_bytes]
+    uint8_t *dst;           // tiled units
+    uint32_t rows;
+    uint32_t blocks;
+    uint32_t tiles;
+    uint32_t chunks;
+    uint32_t dtype;
+    uint32_t pad;
+};
+
+// Tiled fused matvec. Wave v of the grid takes chunk c = v / segs and row
+// tiles [s * tpw, min(tiles, s * tpw + tpw)) with s = v % segs. With more
+// than one chunk the per-chunk row sums go to `partial` ([chunks][tiles *
+// 16]) and the wave that brings a tile's arrival count to `chunks` adds them
+// in chunk order, applies the epilogue and resets the count to zero.
+struct TileMatvecArgs {
+    const uint8_t *weights; // tiled units
+    const int8_t *xa;       // activation fragments (prep output) or NULL (mode 1)
+    const float *xc;        // epilogue constants (prep output)
+    const float *input;     // mode 1: f32 activation [columns]
+    const void *s_in;       // mode 1: NULL, f32 or f16 [columns]
+    const void *s_out;      // NULL, f32[rows] or f16[rows]
+    const float *bias;      // NULL or f32[rows]
+    float *output;          // [rows]
+    float *partial;         // [chunks][tiles * 16] when chunks > 1
+    uint32_t *counts;       // [tiles], zero between launches
+    uint32_t rows;
+    uint32_t blocks;
+    uint32_t tiles;
+    uint32_t chunks;
+    uint32_t segs;          // waves per chunk
+    uint32_t tpw;           // row tiles per wave (<= CTOX_TILE_MAXU)
+    uint32_t s_out_kind;
+    uint32_t activation;
+    uint32_t s_in_kind;
+    uint32_t pad;
+};
+
 struct RecoveredRowArgs {
     const uint8_t *weights; // one packed row
     const void *s_in;       // f32 or f16 [columns]

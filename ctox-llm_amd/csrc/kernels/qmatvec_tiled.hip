@@ -1,0 +1,305 @@
+// Batch-1 fused matvec over the tiled weight layout (resident matrices).
+//
+// Same result as Q/src/backend/cpu.rs:242-310 and the same exact int8
+// arithmetic as qmatvec.hip (block-diagonal MFMA over fixed-point activation
+// limbs). What differs is how the weights reach the matrix cores:
+//  * At prepare time every matrix is rewritten once into 16-row x 16-block
+//    units whose bytes are already in MFMA B-fragment order (layout in
+//    kernel_args.h). A lane's 16-byte load is its own fragment, a wave's
+//    load is one contiguous, aligned KiB, and nothing is staged in LDS.
+//  * A wave owns one 16-block column chunk for all its row tiles: the
+//    chunk's activation fragments (4 groups x 4 quarters) and epilogue
+//    constants sit in registers. They are either loaded from a prep
+//    kernel's output or (AB = 1) built by the wave itself from x and s_in,
+//    so a batch-1 dispatch is a single launch.
+//  * Each wave takes up to U row tiles of its chunk; every
+//    load of all of them is issued before the first MFMA (straight-line
+//    code, loads past the wave's tiles fall outside the buffer range and
+//    return zeros without memory traffic).
+//  * Splitting K into chunks spreads any matrix evenly over the CUs. The
+//    chunk sums of a row tile are combined by the wave that arrives last at
+//    the tile's counter, in chunk order, so the result is deterministic.
+#include "kernel_args.h"
+
+// Cache policy of streamed weight loads: non-temporal.
+#define CTOX_LOAD_NT 2
+
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+
+template <int DT>
+struct TlCfg {
+    static constexpr uint32_t LPU = DT ? 8 : 4;  // 16-byte code loads per lane per unit
+    static constexpr uint32_t CB = ctox_tile_code_bytes(DT);
+    static constexpr uint32_t UB = ctox_tile_unit_bytes(DT);
+    static constexpr float DEN = DT ? 15.0f : 3.0f;
+};
+
+__device__ __forceinline__ float tile_epilogue(float v, uint32_t row, const TileMatvecArgs &a) {
+    if (a.bias) v += a.bias[row];
+    if (a.s_out_kind != CTOX_KSCALE_NONE) v *= load_scale(a.s_out, a.s_out_kind, row);
+    if (a.activation == 1) v = v / (1.0f + expf(-v));
+    return v;
+}
+
+template <int DT>
+struct TileUnit {
+    v4i w[TlCfg<DT>::LPU];
+    v2u s;
+};
+
+// Builds the chunk's activation fragments from x (times s_in) inside the
+// wave, with exactly the arithmetic of prep_block in qmatvec.hip: per
+// 64-column block the fixed point X = rint(x' * 2^(22 - e)) (|x'| < 2^e),
+// three balanced int8 limbs, and the epilogue constants
+// {2q, 512q, 131072q, -off * sum(X) * q}, q = 2^(e - 22); a block holding a
+// non-finite value gets q = NaN. Lane 16 t + m of group G holds elements
+// 4m .. 4m + 3 of block 4G + t, so a block is one 16-lane row and every
+// reduction stays inside it. The limbs go through a wave-private LDS area
+// into the A-fragment order (the B unpack order of frag_pos).
+// The loads of tile_build_fragments, issued ahead of the weight loads (they
+// are branch-free: out-of-range offsets read zeros).
+__device__ __forceinline__ void tile_fragment_loads(const TileMatvecArgs &a, uint32_t c, uint32_t lane, v4i (&xv)[4],
+                                                    v4i (&sv)[4]) {
+    const uint32_t g = lane >> 4, m = lane & 15;
+    const uint32_t sbytes = a.s_in_kind == CTOX_KSCALE_F32 ? 4u : 2u;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void *)a.input, (short)0, (int)(a.blocks * 256), 0x00020000);
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)a.s_in, (short)0, a.s_in_kind == CTOX_KSCALE_NONE ? 0 : (int)(a.blocks * 64 * sbytes), 0x00020000);
+#pragma unroll
+    for (int G = 0; G < 4; G++) {
+        const uint32_t col = (c * CTOX_TILE_BLOCKS + 4 * G + g) * CTOX_BLOCK_LEN + 4 * m;
+        xv[G] = __builtin_amdgcn_raw_buffer_load_b128(xr, col * 4, 0, 0);
+        sv[G] = __builtin_amdgcn_raw_buffer_load_b128(sr, col * sbytes, 0, 0);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void tile_build_fragments(const TileMatvecArgs &a, uint32_t lane, const v4i (&xv)[4],
+                                                     const v4i (&sv)[4], v4i (&af)[4][4], float4 (&kq)[4]) {
+    __shared__ __align__(16) int8_t xs[4][CTOX_TILE_BLOCKS * 192];
+    int8_t *mys = xs[threadIdx.x >> 6];
+    const uint32_t g = lane >> 4, m = lane & 15, j = lane & 15, limb = j & 3;
+    const bool aok = (j >> 2) == g && limb < 3;
+#pragma unroll
+    for (int G = 0; G < 4; G++) {
+        float v[4] = {__int_as_float(xv[G][0]), __int_as_float(xv[G][1]), __int_as_float(xv[G][2]), __int_as_float(xv[G][3])};
+        if (a.s_in_kind == CTOX_KSCALE_F16) {
+            v[0] *= half_bits_to_float((uint32_t)sv[G][0] & 0xffffu);
+            v[1] *= half_bits_to_float((uint32_t)sv[G][0] >> 16);
+            v[2] *= half_bits_to_float((uint32_t)sv[G][1] & 0xffffu);
+            v[3] *= half_bits_to_float((uint32_t)sv[G][1] >> 16);
+        } else if (a.s_in_kind == CTOX_KSCALE_F32) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] *= __int_as_float(sv[G][i]);
+        }
+        bool bad = false;
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            bad = bad || !__builtin_isfinite(v[i]);
+            mx = fmaxf(mx, __builtin_isfinite(v[i]) ? fabsf(v[i]) : 0.0f);
+        }
+        int badi = bad;
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+            mx = fmaxf(mx, __shfl_xor(mx, o));
+            badi |= __shfl_xor(badi, o);
+        }
+        int ex = 0;
+        if (mx > 0.0f) frexpf(mx, &ex);
+        int X[4];
+        int sx = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            X[i] = (mx > 0.0f && !badi) ? (int)rintf(ldexpf(v[i], CTOX_XFRAC_BITS - ex)) : 0;
+            sx += X[i];
+        }
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) sx += __shfl_xor(sx, o);
+        const float q = badi ? __builtin_nanf("") : (mx > 0.0f ? ldexpf(1.0f, ex - CTOX_XFRAC_BITS) : 0.0f);
+        const long long off = DT ? 15 : 3;
+        kq[G] = make_float4(2.0f * q, 512.0f * q, 131072.0f * q, (float)(-off * (long long)sx) * q);
+        // Limbs X = X0 + 256 X1 + 65536 X2 (X0, X1 in [-128, 127]) to their
+        // fragment bytes: block 4G + g, element 4m + i -> quarter m / 4,
+        // element w = 4 (m % 4) + i of the quarter.
+        int8_t *blkp = mys + (4 * G + g) * 192 + (m >> 2) * 16;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int x0 = (int)(int8_t)(X[i] & 0xff);
+            const int r1 = (X[i] - x0) >> 8;
+            const int x1 = (int)(int8_t)(r1 & 0xff);
+            const int x2 = (r1 - x1) >> 8;
+            const int pos = frag_pos(DT, (int)(4 * (m & 3) + i));
+            blkp[0 * 64 + pos] = (int8_t)x0;
+            blkp[1 * 64 + pos] = (int8_t)x1;
+            blkp[2 * 64 + pos] = (int8_t)x2;
+        }
+    }
+    // LDS operations of one wave complete in issue order.
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+    for (int G = 0; G < 4; G++)
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            af[G][q] = aok ? *(const v4i *)(mys + (4 * G + g) * 192 + limb * 64 + q * 16) : (v4i){0, 0, 0, 0};
+}
+
+template <int DT, int U, int AB>
+__device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
+    using C = TlCfg<DT>;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t v = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
+    const uint32_t c = v / a.segs, s = v - c * a.segs;
+    const uint32_t t0 = s * U;
+    if (c >= a.chunks || t0 >= a.tiles) return;
+    const uint32_t n = min((uint32_t)U, a.tiles - t0);
+    const uint8_t *base = a.weights + ((size_t)c * a.tiles + t0) * C::UB;
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)(n * C::UB), 0x00020000);
+    const __amdgpu_buffer_rsrc_t fr = __builtin_amdgcn_make_buffer_rsrc((void *)a.xa, (short)0, (int)(a.blocks * 192), 0x00020000);
+    const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc((void *)a.xc, (short)0, (int)(a.blocks * 16), 0x00020000);
+    const uint32_t g = lane >> 4, j = lane & 15, limb = j & 3;
+    const bool aok = (j >> 2) == g && limb < 3;
+
+    // Activation fragments of the chunk: A lane (g, j) of quarter q carries
+    // limb j % 4 of block 4G + g when j / 4 == g (zero elsewhere).
+    v4i af[4][4];
+    float4 kq[4];
+    if (!AB) {
+#pragma unroll
+        for (int G = 0; G < 4; G++) {
+            const uint32_t blk = c * CTOX_TILE_BLOCKS + 4 * G + g;
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                af[G][q] = __builtin_amdgcn_raw_buffer_load_b128(fr, aok ? blk * 192 + limb * 64 + q * 16 : 0x7ffffff0u, 0, 0);
+            const v4i k4 = __builtin_amdgcn_raw_buffer_load_b128(cr, blk * 16, 0, 0);
+            kq[G] = make_float4(__int_as_float(k4[0]), __int_as_float(k4[1]), __int_as_float(k4[2]), __int_as_float(k4[3]));
+        }
+    }
+    v4i xv[4], sv[4];
+    if (AB) tile_fragment_loads(a, c, lane, xv, sv);
+    TileUnit<DT> u[U];
+#pragma unroll
+    for (int k = 0; k < U; k++) {
+#pragma unroll
+        for (int i = 0; i < (int)C::LPU; i++)
+            u[k].w[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, lane * 16, k * C::UB + i * 1024, CTOX_LOAD_NT);
+        u[k].s = __builtin_amdgcn_raw_buffer_load_b64(wr, C::CB + lane * 8, k * C::UB, CTOX_LOAD_NT);
+    }
+    if (AB) tile_build_fragments<DT>(a, lane, xv, sv, af, kq);
+
+    float part[U];
+#pragma unroll
+    for (int k = 0; k < U; k++) {
+        // Every unit is computed (a unit past the wave's tiles reads zeros):
+        // a branch here would let the compiler sink its loads behind it.
+        float acc = 0.0f;
+        {
+#pragma unroll
+            for (int G = 0; G < 4; G++) {
+                v4i cc = (v4i){0, 0, 0, 0};
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    uint32_t w0, w1 = 0;
+                    if (DT) {
+                        const v4i W = u[k].w[2 * G + (q >> 1)];
+                        w0 = (uint32_t)W[2 * (q & 1)];
+                        w1 = (uint32_t)W[2 * (q & 1) + 1];
+                    } else {
+                        w0 = (uint32_t)u[k].w[G][q];
+                    }
+                    cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[G][q], unpack_quarter<DT>(w0, w1), cc, 0, 0, 0);
+                }
+                const uint32_t sw = u[k].s[G >> 1];
+                const float scale = half_bits_to_float((G & 1) ? (sw >> 16) : (sw & 0xffffu));
+                float f = fmaf((float)cc[0], kq[G].x, kq[G].w);
+                f = fmaf((float)cc[1], kq[G].y, f);
+                f = fmaf((float)cc[2], kq[G].z, f);
+                acc = fmaf(f, scale, acc);
+            }
+        }
+        acc += __shfl_xor(acc, 16);
+        acc += __shfl_xor(acc, 32);
+        part[k] = acc;
+    }
+    // Lane (g, j) reports row j of the wave's tile g.
+    float val = part[0];
+#pragma unroll
+    for (int k = 1; k < U; k++)
+        if (g == (uint32_t)k) val = part[k];
+    const uint32_t tile = t0 + g, row = tile * CTOX_TILE_ROWS + j;
+    const bool mine = g < n;
+    if (a.chunks == 1) {
+        if (mine && row < a.rows) a.output[row] = tile_epilogue(val / C::DEN, row, a);
+        return;
+    }
+    // Cross-chunk combine without cache maintenance: the partials are
+    // written and read with agent-scope atomic stores/loads (coherent across
+    // the XCDs' L2s by themselves), the stores are complete before the
+    // arrival count is raised, and the last arrival's reads depend on the
+    // count it got back.
+    const size_t cstride = (size_t)a.tiles * CTOX_TILE_ROWS;
+    if (mine) __hip_atomic_store(&a.partial[(size_t)c * cstride + row], val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    uint32_t old = 0;
+    if (mine && j == 0) old = __hip_atomic_fetch_add(&a.counts[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __shfl(old, lane & 0x30);
+    if (mine && old == a.chunks - 1) {
+        // Up to 32 partial loads in flight at a time, added in chunk order.
+        float sum = 0.0f;
+        for (uint32_t c0 = 0; c0 < a.chunks; c0 += 32) {
+            float pv[32];
+#pragma unroll
+            for (int i = 0; i < 32; i++)
+                pv[i] = __hip_atomic_load(&a.partial[(size_t)min(c0 + i, a.chunks - 1) * cstride + row],
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int i = 0; i < 32; i++)
+                if (c0 + i < a.chunks) sum += pv[i];
+        }
+        if (row < a.rows) a.output[row] = tile_epilogue(sum / C::DEN, row, a);
+        if (j == 0) __hip_atomic_store(&a.counts[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// ctox_q{2,4}_mv_tile{U}_gfx950 take prep-staged fragments; the _x
+// variants build them from x and s_in.
+#define CTOX_TILE_KERNEL(name, dt, u, ab) \
+    extern "C" __global__ __launch_bounds__(256) void name(TileMatvecArgs a) { tile_matvec<dt, u, ab>(a); }
+CTOX_TILE_KERNEL(ctox_q2_mv_tile1_gfx950, 0, 1, 0)
+CTOX_TILE_KERNEL(ctox_q2_mv_tile2_gfx950, 0, 2, 0)
+CTOX_TILE_KERNEL(ctox_q2_mv_tile3_gfx950, 0, 3, 0)
+CTOX_TILE_KERNEL(ctox_q2_mv_tile4_gfx950, 0, 4, 0)
+CTOX_TILE_KERNEL(ctox_q4_mv_tile1_gfx950, 1, 1, 0)
+CTOX_TILE_KERNEL(ctox_q4_mv_tile2_gfx950, 1, 2, 0)
+CTOX_TILE_KERNEL(ctox_q4_mv_tile3_gfx950, 1, 3, 0)
+CTOX_TILE_KERNEL(ctox_q4_mv_tile4_gfx950, 1, 4, 0)
+CTOX_TILE_KERNEL(ctox_q2_mv_tile1x_gfx950, 0, 1, 1)
+CTOX_TILE_KERNEL(ctox_q2_mv_tile2x_gfx950, 0, 2, 1)
+CTOX_TILE_KERNEL(ctox_q2_mv_tile3x_gfx950, 0, 3, 1)
+CTOX_TILE_KERNEL(ctox_q2_mv_tile4x_gfx950, 0, 4, 1)
+CTOX_TILE_KERNEL(ctox_q4_mv_tile1x_gfx950, 1, 1, 1)
+CTOX_TILE_KERNEL(ctox_q4_mv_tile2x_gfx950, 1, 2, 1)
+CTOX_TILE_KERNEL(ctox_q4_mv_tile3x_gfx950, 1, 3, 1)
+CTOX_TILE_KERNEL(ctox_q4_mv_tile4x_gfx950, 1, 4, 1)
+
+// Rewrites crate rows (Q/src/quant.rs:20-29 block layout, rows dense) into
+// the tiled layout; one workgroup per unit, lane (g, j) moves its fragment
+// of each of the unit's four groups. Runs once per matrix at prepare time.
+extern "C" __global__ __launch_bounds__(64) void ctox_tile_repack_gfx950(TileRepackArgs a) {
+    const uint32_t u = blockIdx.x, lane = threadIdx.x;
+    const uint32_t c = u / a.tiles, t = u - c * a.tiles;
+    const uint32_t g = lane >> 4, j = lane & 15, row = t * CTOX_TILE_ROWS + j;
+    const uint32_t bb = a.dtype ? CTOX_Q4_BLOCK_BYTES : CTOX_Q2_BLOCK_BYTES, cbytes = bb - 2;
+    const uint32_t codes = ctox_tile_code_bytes(a.dtype);
+    uint8_t *dst = a.dst + (size_t)u * ctox_tile_unit_bytes(a.dtype);
+    for (uint32_t G = 0; G < 4; G++) {
+        const uint32_t blk = c * CTOX_TILE_BLOCKS + 4 * G + g;
+        const bool ok = row < a.rows && blk < a.blocks;
+        const uint8_t *src = a.src + ((size_t)row * a.blocks + blk) * bb;
+        for (uint32_t h = 0; h < cbytes / 16; h++)
+            for (uint32_t e = 0; e < 16; e++)
+                dst[G * cbytes * 64 + h * 1024 + lane * 16 + e] = ok ? src[2 + 16 * h + e] : 0;
+        dst[codes + lane * 8 + 2 * G] = ok ? src[0] : 0;
+        dst[codes + lane * 8 + 2 * G + 1] = ok ? src[1] : 0;
+    }
+}

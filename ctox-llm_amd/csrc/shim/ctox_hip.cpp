@@ -20,6 +20,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -144,7 +145,16 @@ struct ctox_hip_backend {
     hipFunction_t sl[2][4] = {};
     // Small-M slice kernels per dtype [Q2, Q4]: [0] M = 2..4, [1] M = 5..8.
     hipFunction_t st[2][2] = {};
+    // Tiled-layout batch-1 kernels per dtype [Q2, Q4] and row tiles per wave
+    // (1..4), and the prepare-time repack.
+    hipFunction_t tile[2][CTOX_TILE_MAXU] = {};
+    // The same with the activation fragments built inside the kernel.
+    hipFunction_t tilex[2][CTOX_TILE_MAXU] = {};
+    hipFunction_t repack = nullptr;
     int cus = 0;
+    uint32_t tile_u = 0;  // CTOX_TILE_U: fixed row tiles per wave (0 = planned)
+    // Tiled matvec chunk partials and per-tile arrival counts (zero between launches).
+    DevBuf tpart, tcnt;
     // Activation staging (two layouts: [0] Q2, [1] Q4) and gated-delta norms.
     DevBuf xa[2], xc[2], norms;
     // Token selection scratch: per-part partials, pick sums and state.
@@ -167,6 +177,12 @@ struct ctox_hip_matrix {
     float *d_bias = nullptr;
     uint32_t activation = 0;
     std::vector<uint8_t> s_in_host;  // exact s_in bytes, for fan-out sharing checks
+    // Per segment: the same rows rewritten into the tiled layout (kernel_args.h).
+    struct Tiled {
+        void *d = nullptr;
+        uint32_t tiles = 0, chunks = 0;
+    };
+    std::vector<Tiled> tiled;
 };
 
 namespace {
@@ -370,14 +386,73 @@ ctox_status run_matvec(ctox_hip_backend *b, int layout, int32_t dtype, const voi
     return launch(f, dim3((unsigned)groups), dim3(256), s, a, "ctox_q*_matvec_gfx950");
 }
 
+// One launch of the tiled batch-1 matvec over a prepared segment. Plan: the
+// chunks x tiles units are spread so that one pass of about eight waves per
+// CU covers them, at most CTOX_TILE_MAXU row tiles per wave. With d_input
+// set the kernel builds the activation fragments itself (no prep launch);
+// otherwise it reads the ones staged in the backend's xa/xc.
+ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const ctox_hip_matrix::Tiled &t, size_t rows,
+                            size_t columns, const void *d_s_out, uint32_t s_out_kind, const float *d_bias,
+                            float *d_output, uint32_t act, hipStream_t s, const float *d_input = nullptr,
+                            const void *d_s_in = nullptr, uint32_t s_in_kind = CTOX_KSCALE_NONE) {
+    const int q4 = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
+    const size_t units = (size_t)t.tiles * t.chunks;
+    const size_t slots = (size_t)(b->cus > 0 ? b->cus : 256) * 8;
+    uint32_t u = b->tile_u ? b->tile_u : (uint32_t)std::min<size_t>(CTOX_TILE_MAXU, std::max<size_t>(1, (units + slots - 1) / slots));
+    const uint32_t segs = (t.tiles + u - 1) / u;
+    const size_t waves = (size_t)segs * t.chunks;
+    if ((waves + 3) / 4 > 0x7fffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
+    if (t.chunks > 1) {
+        ctox_status st = ensure(b, b->tpart, (size_t)t.chunks * t.tiles * CTOX_TILE_ROWS * sizeof(float), false);
+        if (!st) st = ensure(b, b->tcnt, (size_t)t.tiles * sizeof(uint32_t), true);
+        if (st) return st;
+    }
+    TileMatvecArgs a{};
+    a.weights = (const uint8_t *)t.d;
+    a.xa = (const int8_t *)b->xa[q4].ptr;
+    a.xc = (const float *)b->xc[q4].ptr;
+    a.s_out = d_s_out;
+    a.bias = d_bias;
+    a.output = d_output;
+    a.partial = (float *)b->tpart.ptr;
+    a.counts = (uint32_t *)b->tcnt.ptr;
+    a.rows = (uint32_t)rows;
+    a.blocks = (uint32_t)(columns / kBlockLen);
+    a.tiles = t.tiles;
+    a.chunks = t.chunks;
+    a.segs = segs;
+    a.tpw = u;
+    a.s_out_kind = s_out_kind;
+    a.activation = act;
+    a.input = d_input;
+    a.s_in = d_s_in;
+    a.s_in_kind = s_in_kind;
+    hipFunction_t f = d_input ? b->tilex[q4][u - 1] : b->tile[q4][u - 1];
+    return launch(f, dim3((unsigned)((waves + 3) / 4)), dim3(256), s, a, "ctox_q*_mv_tile*_gfx950");
+}
+
 // `prepped` marks the layouts already staged for this input in this call
 // sequence (fan-out shares them).
 ctox_status dispatch_matrix(ctox_hip_backend *b, const ctox_hip_matrix *m, const float *d_input,
                             size_t batch, float *d_output, hipStream_t s, bool prepped[2],
                             uint32_t act) {
+    size_t si = 0;
     for (const ctox_quant_segment &seg : m->segments) {
         const void *w = (const uint8_t *)m->d_weights + seg.offset;
         const int layout = seg.dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
+        if (batch == 1 && si < m->tiled.size()) {
+            // Batch 1: one launch, activation fragments built in the kernel.
+            const size_t r0 = seg.row_start, nrows = seg.row_end - seg.row_start;
+            const void *so = nullptr;
+            if (m->s_out_kind == CTOX_KSCALE_F32) so = (const float *)m->d_s_out + r0;
+            if (m->s_out_kind == CTOX_KSCALE_F16) so = (const uint16_t *)m->d_s_out + r0;
+            ctox_status st = run_tile_matvec(b, seg.dtype, m->tiled[si], nrows, m->columns, so, m->s_out_kind,
+                                             m->d_bias ? m->d_bias + r0 : nullptr, d_output + r0, act, s, d_input,
+                                             m->d_s_in, m->s_in_kind);
+            if (st) return st;
+            si++;
+            continue;
+        }
         if (!prepped[layout]) {
             ctox_status st = run_prep(b, layout, d_input, m->columns, batch, m->d_s_in, m->s_in_kind, s);
             if (st) return st;
@@ -387,6 +462,7 @@ ctox_status dispatch_matrix(ctox_hip_backend *b, const ctox_hip_matrix *m, const
         const void *so = nullptr;
         if (m->s_out_kind == CTOX_KSCALE_F32) so = (const float *)m->d_s_out + r0;
         if (m->s_out_kind == CTOX_KSCALE_F16) so = (const uint16_t *)m->d_s_out + r0;
+        si++;
         ctox_status st = run_matvec(b, layout, seg.dtype, w, nrows, m->columns, batch, so, m->s_out_kind,
                                     m->d_bias ? m->d_bias + r0 : nullptr, d_output + r0, m->rows, act, s);
         if (st) return st;
@@ -459,7 +535,16 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->sl[1][0], "ctox_q4_matvec_sl_gfx950"}, {&b->sl[1][1], "ctox_q4_matvec_sl1_gfx950"},
                {&b->sl[1][2], "ctox_q4_matvec_sl2_gfx950"}, {&b->sl[1][3], "ctox_q4_matvec_sl3_gfx950"},
                {&b->st[0][0], "ctox_q2_matvec_st4_gfx950"}, {&b->st[0][1], "ctox_q2_matvec_st8_gfx950"},
-               {&b->st[1][0], "ctox_q4_matvec_st4_gfx950"}, {&b->st[1][1], "ctox_q4_matvec_st8_gfx950"}};
+               {&b->st[1][0], "ctox_q4_matvec_st4_gfx950"}, {&b->st[1][1], "ctox_q4_matvec_st8_gfx950"},
+               {&b->tile[0][0], "ctox_q2_mv_tile1_gfx950"}, {&b->tile[0][1], "ctox_q2_mv_tile2_gfx950"},
+               {&b->tile[0][2], "ctox_q2_mv_tile3_gfx950"}, {&b->tile[0][3], "ctox_q2_mv_tile4_gfx950"},
+               {&b->tile[1][0], "ctox_q4_mv_tile1_gfx950"}, {&b->tile[1][1], "ctox_q4_mv_tile2_gfx950"},
+               {&b->tile[1][2], "ctox_q4_mv_tile3_gfx950"}, {&b->tile[1][3], "ctox_q4_mv_tile4_gfx950"},
+               {&b->tilex[0][0], "ctox_q2_mv_tile1x_gfx950"}, {&b->tilex[0][1], "ctox_q2_mv_tile2x_gfx950"},
+               {&b->tilex[0][2], "ctox_q2_mv_tile3x_gfx950"}, {&b->tilex[0][3], "ctox_q2_mv_tile4x_gfx950"},
+               {&b->tilex[1][0], "ctox_q4_mv_tile1x_gfx950"}, {&b->tilex[1][1], "ctox_q4_mv_tile2x_gfx950"},
+               {&b->tilex[1][2], "ctox_q4_mv_tile3x_gfx950"}, {&b->tilex[1][3], "ctox_q4_mv_tile4x_gfx950"},
+               {&b->repack, "ctox_tile_repack_gfx950"}};
     for (auto &f : fns) {
         if (le != hipSuccess) break;
         le = hipModuleGetFunction(f.f, b->module, f.name);
@@ -474,6 +559,10 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
         return fail(CTOX_ERR_UNSUPPORTED_OPERATION, "HIP module setup failed: %s", hipGetErrorString(le));
     }
     b->cus = prop.multiProcessorCount;
+    if (const char *u = std::getenv("CTOX_TILE_U")) {
+        const int v = std::atoi(u);
+        if (v >= 1 && v <= CTOX_TILE_MAXU) b->tile_u = (uint32_t)v;
+    }
     *out = b;
     return CTOX_OK;
 }
@@ -482,7 +571,8 @@ extern "C" void ctox_hip_backend_destroy(ctox_hip_backend *b) {
     if (!b) return;
     (void)hipSetDevice(b->device);
     (void)hipDeviceSynchronize();
-    DevBuf *bufs[] = {&b->xa[0], &b->xa[1], &b->xc[0], &b->xc[1], &b->norms, &b->tok, &b->stats, &b->attn};
+    DevBuf *bufs[] = {&b->xa[0], &b->xa[1], &b->xc[0], &b->xc[1], &b->norms, &b->tok, &b->stats, &b->attn,
+                      &b->tpart, &b->tcnt};
     for (DevBuf *d : bufs)
         if (d->ptr) (void)hipFree(d->ptr);
     if (b->stream) (void)hipStreamDestroy(b->stream);
@@ -508,6 +598,35 @@ extern "C" ctox_status ctox_hip_synchronize(ctox_hip_backend *b) {
 // resident matrices
 // ======================================================================
 namespace {
+// Rewrites every segment of a resident matrix into the tiled layout on the
+// device (one pass at prepare time; the crate-layout copy stays for batch > 1).
+ctox_status tile_segments(ctox_hip_backend *b, ctox_hip_matrix *m) {
+    const uint32_t blocks = (uint32_t)(m->columns / kBlockLen);
+    for (const ctox_quant_segment &seg : m->segments) {
+        ctox_hip_matrix::Tiled t;
+        const size_t rows = seg.row_end - seg.row_start;
+        t.tiles = (uint32_t)((rows + CTOX_TILE_ROWS - 1) / CTOX_TILE_ROWS);
+        t.chunks = (blocks + CTOX_TILE_BLOCKS - 1) / CTOX_TILE_BLOCKS;
+        const uint32_t q4 = seg.dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
+        const size_t units = (size_t)t.tiles * t.chunks;
+        if (units > 0x7fffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large to tile");
+        HIP_TRY(hipMalloc(&t.d, units * ctox_tile_unit_bytes(q4)));
+        m->tiled.push_back(t);
+        TileRepackArgs a{};
+        a.src = (const uint8_t *)m->d_weights + seg.offset;
+        a.dst = (uint8_t *)t.d;
+        a.rows = (uint32_t)rows;
+        a.blocks = blocks;
+        a.tiles = t.tiles;
+        a.chunks = t.chunks;
+        a.dtype = q4;
+        ctox_status st = launch(b->repack, dim3((unsigned)units), dim3(64), b->stream, a, "ctox_tile_repack_gfx950");
+        if (st) return st;
+    }
+    HIP_TRY(hipStreamSynchronize(b->stream));
+    return CTOX_OK;
+}
+
 ctox_status prepare_impl(ctox_hip_backend *b, const ctox_fused_matvec *op, ctox_hip_matrix **out) {
     size_t blocks;
     ctox_status st = validate_matvec(op, false, &blocks);
@@ -538,6 +657,7 @@ ctox_status prepare_impl(ctox_hip_backend *b, const ctox_fused_matvec *op, ctox_
         m->s_out_kind = kernel_scale_kind(op->s_out.kind);
     }
     if (!st && op->bias) st = upload(op->bias, op->rows * sizeof(float), (void **)&m->d_bias);
+    if (!st) st = tile_segments(b, m);
     if (st) {
         ctox_hip_matrix_destroy(m);
         return st;
@@ -563,6 +683,8 @@ extern "C" void ctox_hip_matrix_destroy(ctox_hip_matrix *m) {
     if (m->d_s_in) (void)hipFree(m->d_s_in);
     if (m->d_s_out) (void)hipFree(m->d_s_out);
     if (m->d_bias) (void)hipFree(m->d_bias);
+    for (auto &t : m->tiled)
+        if (t.d) (void)hipFree(t.d);
     delete m;
 }
 
