@@ -22,6 +22,8 @@ HIPCC = os.path.join(ROCM, "bin", "hipcc")
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-mcode-object-version=5",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs (no accumulation-register round trips in the epilogues).
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

@@ -56,92 +56,91 @@ struct TileUnit {
 // 4m .. 4m + 3 of block 4G + t, so a block is one 16-lane row and every
 // reduction stays inside it. The limbs go through a wave-private LDS area
 // into the A-fragment order (the B unpack order of frag_pos).
-// The loads of tile_build_fragments, issued ahead of the weight loads (they
-// are branch-free: out-of-range offsets read zeros).
-__device__ __forceinline__ void tile_fragment_loads(const TileMatvecArgs &a, uint32_t c, uint32_t lane, v4i (&xv)[4],
-                                                    v4i (&sv)[4]) {
-    const uint32_t g = lane >> 4, m = lane & 15;
+// Reductions over one 16-lane row with DPP (VALU speed, no LDS round
+// trips): quad xor 1, quad xor 2, half-row mirror, row mirror.
+template <typename T, typename F>
+__device__ __forceinline__ T row16_reduce(T v, F op) {
+    v = op(v, __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
+    v = op(v, __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
+    v = op(v, __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
+    v = op(v, __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)));
+    return v;
+}
+
+// Loads of one 4-block group's activation (x and s_in) for the fragment
+// builder; branch-free (out-of-range offsets read zeros), so no wait lands
+// in a divergent block ahead of weight loads already in flight. Lane
+// 16 t + m takes elements 4m .. 4m + 3 of block 4 grp + t.
+__device__ __forceinline__ void frag_group_loads(const TileMatvecArgs &a, uint32_t grp, uint32_t lane, v4i &xv,
+                                                 v4i &sv) {
     const uint32_t sbytes = a.s_in_kind == CTOX_KSCALE_F32 ? 4u : 2u;
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void *)a.input, (short)0, (int)(a.blocks * 256), 0x00020000);
     const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
         (void *)a.s_in, (short)0, a.s_in_kind == CTOX_KSCALE_NONE ? 0 : (int)(a.blocks * 64 * sbytes), 0x00020000);
-#pragma unroll
-    for (int G = 0; G < 4; G++) {
-        const uint32_t col = (c * CTOX_TILE_BLOCKS + 4 * G + g) * CTOX_BLOCK_LEN + 4 * m;
-        xv[G] = __builtin_amdgcn_raw_buffer_load_b128(xr, col * 4, 0, 0);
-        sv[G] = __builtin_amdgcn_raw_buffer_load_b128(sr, col * sbytes, 0, 0);
-    }
+    const uint32_t col = (4 * grp + (lane >> 4)) * CTOX_BLOCK_LEN + 4 * (lane & 15);
+    xv = __builtin_amdgcn_raw_buffer_load_b128(xr, col * 4, 0, 0);
+    sv = __builtin_amdgcn_raw_buffer_load_b128(sr, col * sbytes, 0, 0);
 }
 
+// Builds one group's activation fragments with exactly the arithmetic of
+// prep_block in qmatvec.hip: per 64-column block the fixed point
+// X = rint(x' * 2^(22 - e)) (|x'| < 2^e), three balanced int8 limbs, and the
+// epilogue constants {2q, 512q, 131072q, -off * sum(X) * q}, q = 2^(e - 22);
+// a block holding a non-finite value gets q = NaN. A block is one 16-lane
+// row, so every reduction stays inside it (DPP). The limbs are written to
+// `frag` (4 blocks x 192 bytes, the prep kernel's xa order); lane (g, j)
+// receives the constants of block g.
 template <int DT>
-__device__ __forceinline__ void tile_build_fragments(const TileMatvecArgs &a, uint32_t lane, const v4i (&xv)[4],
-                                                     const v4i (&sv)[4], v4i (&af)[4][4], float4 (&kq)[4]) {
-    __shared__ __align__(16) int8_t xs[4][CTOX_TILE_BLOCKS * 192];
-    int8_t *mys = xs[threadIdx.x >> 6];
-    const uint32_t g = lane >> 4, m = lane & 15, j = lane & 15, limb = j & 3;
-    const bool aok = (j >> 2) == g && limb < 3;
+__device__ __forceinline__ float4 frag_group_build(const TileMatvecArgs &a, uint32_t lane, const v4i &xv,
+                                                   const v4i &sv, int8_t *frag) {
+    const uint32_t g = lane >> 4, m = lane & 15;
+    float v[4] = {__int_as_float(xv[0]), __int_as_float(xv[1]), __int_as_float(xv[2]), __int_as_float(xv[3])};
+    if (a.s_in_kind == CTOX_KSCALE_F16) {
+        v[0] *= half_bits_to_float((uint32_t)sv[0] & 0xffffu);
+        v[1] *= half_bits_to_float((uint32_t)sv[0] >> 16);
+        v[2] *= half_bits_to_float((uint32_t)sv[1] & 0xffffu);
+        v[3] *= half_bits_to_float((uint32_t)sv[1] >> 16);
+    } else if (a.s_in_kind == CTOX_KSCALE_F32) {
 #pragma unroll
-    for (int G = 0; G < 4; G++) {
-        float v[4] = {__int_as_float(xv[G][0]), __int_as_float(xv[G][1]), __int_as_float(xv[G][2]), __int_as_float(xv[G][3])};
-        if (a.s_in_kind == CTOX_KSCALE_F16) {
-            v[0] *= half_bits_to_float((uint32_t)sv[G][0] & 0xffffu);
-            v[1] *= half_bits_to_float((uint32_t)sv[G][0] >> 16);
-            v[2] *= half_bits_to_float((uint32_t)sv[G][1] & 0xffffu);
-            v[3] *= half_bits_to_float((uint32_t)sv[G][1] >> 16);
-        } else if (a.s_in_kind == CTOX_KSCALE_F32) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) v[i] *= __int_as_float(sv[G][i]);
-        }
-        bool bad = false;
-        float mx = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            bad = bad || !__builtin_isfinite(v[i]);
-            mx = fmaxf(mx, __builtin_isfinite(v[i]) ? fabsf(v[i]) : 0.0f);
-        }
-        int badi = bad;
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) {
-            mx = fmaxf(mx, __shfl_xor(mx, o));
-            badi |= __shfl_xor(badi, o);
-        }
-        int ex = 0;
-        if (mx > 0.0f) frexpf(mx, &ex);
-        int X[4];
-        int sx = 0;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            X[i] = (mx > 0.0f && !badi) ? (int)rintf(ldexpf(v[i], CTOX_XFRAC_BITS - ex)) : 0;
-            sx += X[i];
-        }
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) sx += __shfl_xor(sx, o);
-        const float q = badi ? __builtin_nanf("") : (mx > 0.0f ? ldexpf(1.0f, ex - CTOX_XFRAC_BITS) : 0.0f);
-        const long long off = DT ? 15 : 3;
-        kq[G] = make_float4(2.0f * q, 512.0f * q, 131072.0f * q, (float)(-off * (long long)sx) * q);
-        // Limbs X = X0 + 256 X1 + 65536 X2 (X0, X1 in [-128, 127]) to their
-        // fragment bytes: block 4G + g, element 4m + i -> quarter m / 4,
-        // element w = 4 (m % 4) + i of the quarter.
-        int8_t *blkp = mys + (4 * G + g) * 192 + (m >> 2) * 16;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int x0 = (int)(int8_t)(X[i] & 0xff);
-            const int r1 = (X[i] - x0) >> 8;
-            const int x1 = (int)(int8_t)(r1 & 0xff);
-            const int x2 = (r1 - x1) >> 8;
-            const int pos = frag_pos(DT, (int)(4 * (m & 3) + i));
-            blkp[0 * 64 + pos] = (int8_t)x0;
-            blkp[1 * 64 + pos] = (int8_t)x1;
-            blkp[2 * 64 + pos] = (int8_t)x2;
-        }
+        for (int i = 0; i < 4; i++) v[i] *= __int_as_float(sv[i]);
     }
-    // LDS operations of one wave complete in issue order.
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    // A non-finite value anywhere in the block makes its quantum NaN (the
+    // lane sum of a finite row can only overflow for |x'| near 2^128).
+    const bool bad = !__builtin_isfinite((v[0] + v[1]) + (v[2] + v[3]));
+    // Non-negative floats order like their bit patterns: integer max.
+    uint32_t mb = max(max(__float_as_uint(fabsf(v[0])), __float_as_uint(fabsf(v[1]))),
+                      max(__float_as_uint(fabsf(v[2])), __float_as_uint(fabsf(v[3]))));
+    mb = row16_reduce(mb, [](uint32_t x, uint32_t y) { return max(x, y); });
+    const float mx = __uint_as_float(mb);
+    const int badi = row16_reduce((int)bad, [](int x, int y) { return x | y; });
+    int ex = 0;
+    if (mx > 0.0f) frexpf(mx, &ex);
+    // X = rint(v * 2^(22 - e)): one fma against 1.5 * 2^23 rounds to the
+    // nearest integer (ties to even) in the low mantissa bits (|X| <= 2^22).
+    const bool live = mx > 0.0f && !badi;
+    const float p2 = live ? ldexpf(1.0f, CTOX_XFRAC_BITS - ex) : 0.0f;
+    int X[4];
+    int sx = 0;
 #pragma unroll
-    for (int G = 0; G < 4; G++)
+    for (int i = 0; i < 4; i++) {
+        X[i] = __float_as_int(fmaf(v[i], p2, 12582912.0f)) - 0x4b400000;
+        sx += X[i];
+    }
+    sx = row16_reduce(sx, [](int x, int y) { return x + y; });
+    const float q = badi ? __builtin_nanf("") : (mx > 0.0f ? ldexpf(1.0f, ex - CTOX_XFRAC_BITS) : 0.0f);
+    const long long off = DT ? 15 : 3;
+    // Balanced limbs X = X0 + 256 X1 + 65536 X2 (X0, X1 in [-128, 127]):
+    // X0 is byte 0 of X, X1 byte 1 of X + 0x80, X2 byte 2 of X + 0x8080.
+    // Element 4m + i of block g goes to quarter m / 4, element 4 (m % 4) + i.
+    int8_t *blkp = frag + g * 192 + (m >> 2) * 16;
 #pragma unroll
-        for (int q = 0; q < 4; q++)
-            af[G][q] = aok ? *(const v4i *)(mys + (4 * G + g) * 192 + limb * 64 + q * 16) : (v4i){0, 0, 0, 0};
+    for (int i = 0; i < 4; i++) {
+        const int pos = frag_pos(DT, (int)(4 * (m & 3) + i));
+        blkp[0 * 64 + pos] = (int8_t)X[i];
+        blkp[1 * 64 + pos] = (int8_t)((X[i] + 0x80) >> 8);
+        blkp[2 * 64 + pos] = (int8_t)((X[i] + 0x8080) >> 16);
+    }
+    return make_float4(2.0f * q, 512.0f * q, 131072.0f * q, (float)(-off * (long long)sx) * q);
 }
 
 template <int DT, int U, int AB>
@@ -176,7 +175,10 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
         }
     }
     v4i xv[4], sv[4];
-    if (AB) tile_fragment_loads(a, c, lane, xv, sv);
+    if (AB)
+#pragma unroll
+        for (int G = 0; G < 4; G++) frag_group_loads(a, c * 4 + G, lane, xv[G], sv[G]);
+    __builtin_amdgcn_sched_barrier(0);  // activation loads stay ahead of the weight loads
     TileUnit<DT> u[U];
 #pragma unroll
     for (int k = 0; k < U; k++) {
@@ -185,7 +187,19 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
             u[k].w[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, lane * 16, k * C::UB + i * 1024, CTOX_LOAD_NT);
         u[k].s = __builtin_amdgcn_raw_buffer_load_b64(wr, C::CB + lane * 8, k * C::UB, CTOX_LOAD_NT);
     }
-    if (AB) tile_build_fragments<DT>(a, lane, xv, sv, af, kq);
+    if (AB) {
+        __shared__ __align__(16) int8_t xs[4][CTOX_TILE_BLOCKS * 192];
+        int8_t *mys = xs[threadIdx.x >> 6];
+#pragma unroll
+        for (int G = 0; G < 4; G++) kq[G] = frag_group_build<DT>(a, lane, xv[G], sv[G], mys + G * 768);
+        // LDS operations of one wave complete in issue order.
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+        for (int G = 0; G < 4; G++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                af[G][q] = aok ? *(const v4i *)(mys + G * 768 + g * 192 + limb * 64 + q * 16) : (v4i){0, 0, 0, 0};
+    }
 
     float part[U];
 #pragma unroll
@@ -281,6 +295,7 @@ CTOX_TILE_KERNEL(ctox_q4_mv_tile1x_gfx950, 1, 1, 1)
 CTOX_TILE_KERNEL(ctox_q4_mv_tile2x_gfx950, 1, 2, 1)
 CTOX_TILE_KERNEL(ctox_q4_mv_tile3x_gfx950, 1, 3, 1)
 CTOX_TILE_KERNEL(ctox_q4_mv_tile4x_gfx950, 1, 4, 1)
+
 
 // Rewrites crate rows (Q/src/quant.rs:20-29 block layout, rows dense) into
 // the tiled layout; one workgroup per unit, lane (g, j) moves its fragment
