@@ -10,8 +10,9 @@
 //  * A wave owns one 16-block column chunk for all its row tiles: the
 //    chunk's activation fragments (4 groups x 4 quarters) and epilogue
 //    constants sit in registers. They are either loaded from a prep
-//    kernel's output or (AB = 1) built by the wave itself from x and s_in,
-//    so a batch-1 dispatch is a single launch.
+//    kernel's output or (AB = 1) built from x and s_in by the workgroup's
+//    four waves (one group each, exchanged through LDS), so a batch-1
+//    dispatch is a single launch.
 //  * Each wave takes up to U row tiles of its chunk; every
 //    load of all of them is issued before the first MFMA (straight-line
 //    code, loads past the wave's tiles fall outside the buffer range and
@@ -150,9 +151,12 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
     const uint32_t v = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
     const uint32_t c = v / a.segs, s = v - c * a.segs;
     const uint32_t t0 = s * U;
-    if (c >= a.chunks || t0 >= a.tiles) return;
-    const uint32_t n = min((uint32_t)U, a.tiles - t0);
-    const uint8_t *base = a.weights + ((size_t)c * a.tiles + t0) * C::UB;
+    // With AB the host makes segs a multiple of the workgroup's wave count,
+    // so c is uniform over the workgroup and every wave of it reaches the
+    // barrier of the shared fragment build (waves without tiles leave after).
+    if (c >= a.chunks || (!AB && t0 >= a.tiles)) return;
+    const uint32_t n = t0 < a.tiles ? min((uint32_t)U, a.tiles - t0) : 0u;
+    const uint8_t *base = a.weights + ((size_t)c * a.tiles + min(t0, a.tiles - 1)) * C::UB;
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)(n * C::UB), 0x00020000);
     const __amdgpu_buffer_rsrc_t fr = __builtin_amdgcn_make_buffer_rsrc((void *)a.xa, (short)0, (int)(a.blocks * 192), 0x00020000);
     const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc((void *)a.xc, (short)0, (int)(a.blocks * 16), 0x00020000);
@@ -174,10 +178,10 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
             kq[G] = make_float4(__int_as_float(k4[0]), __int_as_float(k4[1]), __int_as_float(k4[2]), __int_as_float(k4[3]));
         }
     }
-    v4i xv[4], sv[4];
-    if (AB)
-#pragma unroll
-        for (int G = 0; G < 4; G++) frag_group_loads(a, c * 4 + G, lane, xv[G], sv[G]);
+    // AB: wave w of the workgroup builds group w of the chunk.
+    const uint32_t wg_wave = threadIdx.x >> 6;
+    v4i xv, sv;
+    if (AB) frag_group_loads(a, c * 4 + wg_wave, lane, xv, sv);
     __builtin_amdgcn_sched_barrier(0);  // activation loads stay ahead of the weight loads
     TileUnit<DT> u[U];
 #pragma unroll
@@ -188,17 +192,19 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
         u[k].s = __builtin_amdgcn_raw_buffer_load_b64(wr, C::CB + lane * 8, k * C::UB, CTOX_LOAD_NT);
     }
     if (AB) {
-        __shared__ __align__(16) int8_t xs[4][CTOX_TILE_BLOCKS * 192];
-        int8_t *mys = xs[threadIdx.x >> 6];
+        __shared__ __align__(16) int8_t xs[CTOX_TILE_BLOCKS * 192];
+        __shared__ float4 kqs[CTOX_TILE_BLOCKS];
+        const float4 k = frag_group_build<DT>(a, lane, xv, sv, xs + wg_wave * 768);
+        if (j == 0) kqs[4 * wg_wave + g] = k;
+        lds_barrier();  // orders LDS only: the weight loads stay in flight
+        if (t0 >= a.tiles) return;
 #pragma unroll
-        for (int G = 0; G < 4; G++) kq[G] = frag_group_build<DT>(a, lane, xv[G], sv[G], mys + G * 768);
-        // LDS operations of one wave complete in issue order.
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-#pragma unroll
-        for (int G = 0; G < 4; G++)
+        for (int G = 0; G < 4; G++) {
+            kq[G] = kqs[4 * G + g];
 #pragma unroll
             for (int q = 0; q < 4; q++)
-                af[G][q] = aok ? *(const v4i *)(mys + G * 768 + g * 192 + limb * 64 + q * 16) : (v4i){0, 0, 0, 0};
+                af[G][q] = aok ? *(const v4i *)(xs + G * 768 + g * 192 + limb * 64 + q * 16) : (v4i){0, 0, 0, 0};
+        }
     }
 
     float part[U];
@@ -225,9 +231,16 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
                 }
                 const uint32_t sw = u[k].s[G >> 1];
                 const float scale = half_bits_to_float((G & 1) ? (sw >> 16) : (sw & 0xffffu));
-                float f = fmaf((float)cc[0], kq[G].x, kq[G].w);
-                f = fmaf((float)cc[1], kq[G].y, f);
-                f = fmaf((float)cc[2], kq[G].z, f);
+                float f;
+                if (DT) {
+                    f = fmaf((float)cc[0], kq[G].x, kq[G].w);
+                    f = fmaf((float)cc[1], kq[G].y, f);
+                    f = fmaf((float)cc[2], kq[G].z, f);
+                } else {
+                    // Q2: sum(c X) = C0 + 256 C1 + 65536 C2 is exact in int32
+                    // (|sum| <= 64 * 3 * 2^22 < 2^30): one conversion.
+                    f = fmaf((float)(cc[0] + (cc[1] << 8) + (cc[2] << 16)), kq[G].x, kq[G].w);
+                }
                 acc = fmaf(f, scale, acc);
             }
         }

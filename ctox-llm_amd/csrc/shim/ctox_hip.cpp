@@ -387,7 +387,7 @@ ctox_status run_matvec(ctox_hip_backend *b, int layout, int32_t dtype, const voi
 }
 
 // One launch of the tiled batch-1 matvec over a prepared segment. Plan: the
-// chunks x tiles units are spread so that one pass of about eight waves per
+// chunks x tiles units are spread so that one pass of about twelve waves per
 // CU covers them, at most CTOX_TILE_MAXU row tiles per wave. With d_input
 // set the kernel builds the activation fragments itself (no prep launch);
 // otherwise it reads the ones staged in the backend's xa/xc.
@@ -397,9 +397,11 @@ ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const ctox_hip_m
                             const void *d_s_in = nullptr, uint32_t s_in_kind = CTOX_KSCALE_NONE) {
     const int q4 = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
     const size_t units = (size_t)t.tiles * t.chunks;
-    const size_t slots = (size_t)(b->cus > 0 ? b->cus : 256) * 8;
+    const size_t slots = (size_t)(b->cus > 0 ? b->cus : 256) * 12;
     uint32_t u = b->tile_u ? b->tile_u : (uint32_t)std::min<size_t>(CTOX_TILE_MAXU, std::max<size_t>(1, (units + slots - 1) / slots));
-    const uint32_t segs = (t.tiles + u - 1) / u;
+    uint32_t segs = (t.tiles + u - 1) / u;
+    // The in-kernel fragment build shares one chunk per workgroup of four waves.
+    if (d_input) segs = (segs + 3) & ~3u;
     const size_t waves = (size_t)segs * t.chunks;
     if ((waves + 3) / 4 > 0x7fffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
     if (t.chunks > 1) {
