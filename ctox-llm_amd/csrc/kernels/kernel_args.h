@@ -148,6 +148,27 @@ struct TileMatvecArgs {
     uint32_t activation;
     uint32_t s_in_kind;
     uint32_t pad;
+    // In-kernel fragment build (the _x kernels): the activation is computed
+    // from its producer's outputs (`input` is `a` below). xmode:
+    //   0 plain:       x = a[c]
+    //   1 residual norm (Q/src/reference.rs:38-62): h = a[c] + delta[c] (delta
+    //                  may be NULL), x = h * rsqrt(mean(h^2) + eps) * (1 + w[c]);
+    //                  h goes to x_out and x to norm_out (each when set) for
+    //                  the columns of the chunk, by the workgroup of segment 0
+    //   2 swiglu (Q/src/reference.rs:96-112): x = silu(a[c]) * a[off + c]
+    //   3 gated norm per head (Q/src/reference.rs:66-93):
+    //                  x = a[c] * rsqrt(mean_head(a^2) + eps) * w[c % head_dim] * silu(b[c])
+    //   4 attention gate (Q/src/decoder.rs:727-737): x = a[c] * sigmoid(b[h * 2 hd + hd + d])
+    // then x * s_in.
+    const float *xb;
+    const float *xw;
+    const float *delta;
+    float *x_out;
+    float *norm_out;
+    uint32_t xmode;
+    uint32_t off;
+    uint32_t head_dim;
+    float eps;
 };
 
 struct RecoveredRowArgs {

@@ -68,42 +68,101 @@ __device__ __forceinline__ T row16_reduce(T v, F op) {
     return v;
 }
 
-// Loads of one 4-block group's activation (x and s_in) for the fragment
-// builder; branch-free (out-of-range offsets read zeros), so no wait lands
-// in a divergent block ahead of weight loads already in flight. Lane
-// 16 t + m takes elements 4m .. 4m + 3 of block 4 grp + t.
-__device__ __forceinline__ void frag_group_loads(const TileMatvecArgs &a, uint32_t grp, uint32_t lane, v4i &xv,
-                                                 v4i &sv) {
-    const uint32_t sbytes = a.s_in_kind == CTOX_KSCALE_F32 ? 4u : 2u;
-    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void *)a.input, (short)0, (int)(a.blocks * 256), 0x00020000);
-    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)a.s_in, (short)0, a.s_in_kind == CTOX_KSCALE_NONE ? 0 : (int)(a.blocks * 64 * sbytes), 0x00020000);
-    const uint32_t col = (4 * grp + (lane >> 4)) * CTOX_BLOCK_LEN + 4 * (lane & 15);
-    xv = __builtin_amdgcn_raw_buffer_load_b128(xr, col * 4, 0, 0);
-    sv = __builtin_amdgcn_raw_buffer_load_b128(sr, col * sbytes, 0, 0);
+// Raw inputs of one 4-block group of the in-kernel fragment build.
+struct GroupIn {
+    v4i a, b, w, s;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t f32_rsrc(const void *p, uint32_t floats) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, p ? (int)(floats * 4) : 0, 0x00020000);
 }
+
+// Loads of one 4-block group's activation inputs (TileMatvecArgs::xmode);
+// branch-free: an unused or absent input has an empty range and reads zeros,
+// so no wait lands in a divergent block ahead of weight loads in flight.
+// Lane 16 t + m takes columns 4m .. 4m + 3 of block 4 grp + t.
+__device__ __forceinline__ void frag_group_loads(const TileMatvecArgs &a, uint32_t grp, uint32_t lane, GroupIn &in) {
+    const uint32_t cols = a.blocks * CTOX_BLOCK_LEN, xm = a.xmode, dh = a.head_dim;
+    const uint32_t col = (4 * grp + (lane >> 4)) * CTOX_BLOCK_LEN + 4 * (lane & 15);
+    const uint32_t sbytes = a.s_in_kind == CTOX_KSCALE_F32 ? 4u : 2u;
+    const __amdgpu_buffer_rsrc_t ar = f32_rsrc(a.input, xm == 2 ? a.off + cols : cols);
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)a.s_in, (short)0, a.s_in_kind == CTOX_KSCALE_NONE ? 0 : (int)(cols * sbytes), 0x00020000);
+    const void *bp = xm == 1 ? (const void *)a.delta : (xm == 2 ? (const void *)a.input : (const void *)a.xb);
+    const uint32_t bn = xm == 1 || xm == 3 ? cols : (xm == 2 ? a.off + cols : (xm == 4 ? 2 * cols : 0u));
+    const uint32_t bo = xm == 2 ? a.off + col : (xm == 4 ? (col / dh) * 2 * dh + dh + col % dh : col);
+    const __amdgpu_buffer_rsrc_t br = f32_rsrc(xm == 0 ? nullptr : bp, bn);
+    const __amdgpu_buffer_rsrc_t wr = f32_rsrc(xm == 1 || xm == 3 ? a.xw : nullptr, xm == 1 ? cols : dh);
+    in.a = __builtin_amdgcn_raw_buffer_load_b128(ar, col * 4, 0, 0);
+    in.b = __builtin_amdgcn_raw_buffer_load_b128(br, bo * 4, 0, 0);
+    in.w = __builtin_amdgcn_raw_buffer_load_b128(wr, (xm == 3 ? col % (dh ? dh : 1) : col) * 4, 0, 0);
+    in.s = __builtin_amdgcn_raw_buffer_load_b128(sr, col * sbytes, 0, 0);
+}
+
+__device__ __forceinline__ float tl_silu(float v) { return v / (1.0f + expf(-v)); }
 
 // Builds one group's activation fragments with exactly the arithmetic of
 // prep_block in qmatvec.hip: per 64-column block the fixed point
 // X = rint(x' * 2^(22 - e)) (|x'| < 2^e), three balanced int8 limbs, and the
 // epilogue constants {2q, 512q, 131072q, -off * sum(X) * q}, q = 2^(e - 22);
-// a block holding a non-finite value gets q = NaN. A block is one 16-lane
-// row, so every reduction stays inside it (DPP). The limbs are written to
-// `frag` (4 blocks x 192 bytes, the prep kernel's xa order); lane (g, j)
-// receives the constants of block g.
+// a block holding a non-finite value gets q = NaN. x' is the transformed
+// input (xmode, with the row's inverse RMS `inv` for the residual norm)
+// times s_in. A block is one 16-lane row, so the block reductions stay
+// inside it (DPP). The limbs are written to `frag` (4 blocks x 192 bytes,
+// the prep kernel's xa order); lane (g, j) receives the constants of
+// block g. With `keep` the residual and normalized values of the lane's
+// columns are stored (residual norm, segment-0 workgroup).
 template <int DT>
-__device__ __forceinline__ float4 frag_group_build(const TileMatvecArgs &a, uint32_t lane, const v4i &xv,
-                                                   const v4i &sv, int8_t *frag) {
-    const uint32_t g = lane >> 4, m = lane & 15;
-    float v[4] = {__int_as_float(xv[0]), __int_as_float(xv[1]), __int_as_float(xv[2]), __int_as_float(xv[3])};
+__device__ __forceinline__ float4 frag_group_build(const TileMatvecArgs &a, uint32_t grp, uint32_t lane,
+                                                   const GroupIn &in, float inv, bool keep, int8_t *frag) {
+    const uint32_t g = lane >> 4, m = lane & 15, xm = a.xmode;
+    float xa[4], yb[4], wv[4], v[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        xa[i] = __int_as_float(in.a[i]);
+        yb[i] = __int_as_float(in.b[i]);
+        wv[i] = __int_as_float(in.w[i]);
+    }
+    // One uniform branch per transform, each straight-line over the lane's
+    // four columns.
+    if (xm == 1) {
+        const uint32_t col = (4 * grp + g) * CTOX_BLOCK_LEN + 4 * m;
+        const bool inside = col < a.blocks * CTOX_BLOCK_LEN;
+        float h[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) h[i] = xa[i] + yb[i];
+        if (keep && inside && a.x_out) *(float4 *)(a.x_out + col) = make_float4(h[0], h[1], h[2], h[3]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = h[i] * inv * (1.0f + wv[i]);
+        if (keep && inside && a.norm_out) *(float4 *)(a.norm_out + col) = make_float4(v[0], v[1], v[2], v[3]);
+    } else if (xm == 2) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = tl_silu(xa[i]) * yb[i];
+    } else if (xm == 3) {
+        // Per-head mean of squares: a head of head_dim columns is head_dim / 4
+        // consecutive lanes (head_dim 64, 128 or 256).
+        float ss = (xa[0] * xa[0] + xa[1] * xa[1]) + (xa[2] * xa[2] + xa[3] * xa[3]);
+        ss = row16_reduce(ss, [](float x, float y) { return x + y; });
+        if (a.head_dim >= 128) ss += __shfl_xor(ss, 16);
+        if (a.head_dim >= 256) ss += __shfl_xor(ss, 32);
+        const float hinv = 1.0f / sqrtf(ss / (float)a.head_dim + a.eps);
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = xa[i] * hinv * wv[i] * tl_silu(yb[i]);
+    } else if (xm == 4) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = xa[i] * (1.0f / (1.0f + expf(-yb[i])));
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = xa[i];
+    }
     if (a.s_in_kind == CTOX_KSCALE_F16) {
-        v[0] *= half_bits_to_float((uint32_t)sv[0] & 0xffffu);
-        v[1] *= half_bits_to_float((uint32_t)sv[0] >> 16);
-        v[2] *= half_bits_to_float((uint32_t)sv[1] & 0xffffu);
-        v[3] *= half_bits_to_float((uint32_t)sv[1] >> 16);
+        v[0] *= half_bits_to_float((uint32_t)in.s[0] & 0xffffu);
+        v[1] *= half_bits_to_float((uint32_t)in.s[0] >> 16);
+        v[2] *= half_bits_to_float((uint32_t)in.s[1] & 0xffffu);
+        v[3] *= half_bits_to_float((uint32_t)in.s[1] >> 16);
     } else if (a.s_in_kind == CTOX_KSCALE_F32) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) v[i] *= __int_as_float(sv[i]);
+        for (int i = 0; i < 4; i++) v[i] *= __int_as_float(in.s[i]);
     }
     // A non-finite value anywhere in the block makes its quantum NaN (the
     // lane sum of a finite row can only overflow for |x'| near 2^128).
@@ -178,10 +237,23 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
             kq[G] = make_float4(__int_as_float(k4[0]), __int_as_float(k4[1]), __int_as_float(k4[2]), __int_as_float(k4[3]));
         }
     }
-    // AB: wave w of the workgroup builds group w of the chunk.
+    // AB: wave w of the workgroup builds group w of the chunk. The residual
+    // norm first needs the whole row's sum of squares: every workgroup
+    // reduces it (the row is at most 8192 floats and L2-resident) in the same
+    // thread order, so all workgroups agree on it.
     const uint32_t wg_wave = threadIdx.x >> 6;
-    v4i xv, sv;
-    if (AB) frag_group_loads(a, c * 4 + wg_wave, lane, xv, sv);
+    GroupIn gin;
+    v4i hx[8], hd[8];
+    if (AB && a.xmode == 1) {
+        const uint32_t cols = a.blocks * CTOX_BLOCK_LEN;
+        const __amdgpu_buffer_rsrc_t xr = f32_rsrc(a.input, cols), dr = f32_rsrc(a.delta, cols);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            hx[k] = __builtin_amdgcn_raw_buffer_load_b128(xr, (threadIdx.x + 256 * k) * 16, 0, 0);
+            hd[k] = __builtin_amdgcn_raw_buffer_load_b128(dr, (threadIdx.x + 256 * k) * 16, 0, 0);
+        }
+    }
+    if (AB) frag_group_loads(a, c * 4 + wg_wave, lane, gin);
     __builtin_amdgcn_sched_barrier(0);  // activation loads stay ahead of the weight loads
     TileUnit<DT> u[U];
 #pragma unroll
@@ -194,7 +266,27 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
     if (AB) {
         __shared__ __align__(16) int8_t xs[CTOX_TILE_BLOCKS * 192];
         __shared__ float4 kqs[CTOX_TILE_BLOCKS];
-        const float4 k = frag_group_build<DT>(a, lane, xv, sv, xs + wg_wave * 768);
+        __shared__ float wss[4];
+        float inv = 0.0f;
+        if (a.xmode == 1) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float h = __int_as_float(hx[k][i]) + __int_as_float(hd[k][i]);
+                    ss = fmaf(h, h, ss);
+                }
+            }
+            ss = row16_reduce(ss, [](float x, float y) { return x + y; });
+            ss += __shfl_xor(ss, 16);
+            ss += __shfl_xor(ss, 32);
+            if (lane == 0) wss[wg_wave] = ss;
+            lds_barrier();
+            inv = 1.0f / sqrtf(((wss[0] + wss[1]) + (wss[2] + wss[3])) / (float)(a.blocks * CTOX_BLOCK_LEN) + a.eps);
+        }
+        const bool keep = ((blockIdx.x * (blockDim.x >> 6)) % a.segs) == 0;  // segment 0 of the chunk
+        const float4 k = frag_group_build<DT>(a, c * 4 + wg_wave, lane, gin, inv, keep, xs + wg_wave * 768);
         if (j == 0) kqs[4 * wg_wave + g] = k;
         lds_barrier();  // orders LDS only: the weight loads stay in flight
         if (t0 >= a.tiles) return;

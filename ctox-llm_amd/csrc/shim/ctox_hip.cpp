@@ -23,6 +23,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "../kernels/kernel_args.h"
@@ -125,6 +126,12 @@ struct DevBuf {
 
 }  // namespace
 
+// A matrix segment rewritten into the tiled layout (kernel_args.h).
+struct TiledCopy {
+    void *d = nullptr;
+    uint32_t tiles = 0, chunks = 0, rows = 0, columns = 0;
+};
+
 struct ctox_hip_backend {
     int device = 0;
     char arch[64] = {0};
@@ -155,6 +162,8 @@ struct ctox_hip_backend {
     uint32_t tile_u = 0;  // CTOX_TILE_U: fixed row tiles per wave (0 = planned)
     // Tiled matvec chunk partials and per-tile arrival counts (zero between launches).
     DevBuf tpart, tcnt;
+    // Tiled copies of raw device weights (ctox_hip_register_tiled_weights).
+    std::unordered_map<const void *, TiledCopy> raw_tiled;
     // Activation staging (two layouts: [0] Q2, [1] Q4) and gated-delta norms.
     DevBuf xa[2], xc[2], norms;
     // Token selection scratch: per-part partials, pick sums and state.
@@ -178,10 +187,7 @@ struct ctox_hip_matrix {
     uint32_t activation = 0;
     std::vector<uint8_t> s_in_host;  // exact s_in bytes, for fan-out sharing checks
     // Per segment: the same rows rewritten into the tiled layout (kernel_args.h).
-    struct Tiled {
-        void *d = nullptr;
-        uint32_t tiles = 0, chunks = 0;
-    };
+    using Tiled = TiledCopy;
     std::vector<Tiled> tiled;
 };
 
@@ -333,6 +339,20 @@ ctox_status run_prep(ctox_hip_backend *b, int layout, const float *d_input, size
                   "ctox_prep_activation_gfx950");
 }
 
+// Input transform of the in-kernel fragment build (TileMatvecArgs::xmode).
+struct TileXform {
+    uint32_t xmode = 0;
+    const float *b = nullptr, *w = nullptr, *delta = nullptr;
+    float *x_out = nullptr, *norm_out = nullptr;
+    uint32_t off = 0, head_dim = 0;
+    float eps = 0.0f;
+};
+
+ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows, size_t columns,
+                            const void *d_s_out, uint32_t s_out_kind, const float *d_bias, float *d_output, uint32_t act,
+                            hipStream_t s, const float *d_input = nullptr, const void *d_s_in = nullptr,
+                            uint32_t s_in_kind = CTOX_KSCALE_NONE, const TileXform *xf = nullptr);
+
 // One launch over `rows` packed rows of one dtype (a pure matrix or one
 // mixed segment), output rows written at d_output[m*out_stride + r], with
 // the activation already staged in `layout`.
@@ -361,6 +381,12 @@ ctox_status run_matvec(ctox_hip_backend *b, int layout, int32_t dtype, const voi
     a.s_out_kind = s_out_kind;
     a.activation = act;
     const bool q4 = dtype == CTOX_DTYPE_Q4B64;
+    // Batch 1 on registered raw weights: the tiled kernel over the staged activation.
+    if (batch == 1 && !b->raw_tiled.empty()) {
+        auto it = b->raw_tiled.find(d_weights);
+        if (it != b->raw_tiled.end() && it->second.rows == rows && it->second.columns == columns)
+            return run_tile_matvec(b, dtype, it->second, rows, columns, d_s_out, s_out_kind, d_bias, d_output, act, s);
+    }
     // Batch 1 on rows of whole 16-byte units: the slice kernels (all slices
     // requested up front when there are at most three, else walked).
     const size_t rb = packed_row_bytes(dtype, columns);
@@ -391,10 +417,10 @@ ctox_status run_matvec(ctox_hip_backend *b, int layout, int32_t dtype, const voi
 // CU covers them, at most CTOX_TILE_MAXU row tiles per wave. With d_input
 // set the kernel builds the activation fragments itself (no prep launch);
 // otherwise it reads the ones staged in the backend's xa/xc.
-ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const ctox_hip_matrix::Tiled &t, size_t rows,
+ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows,
                             size_t columns, const void *d_s_out, uint32_t s_out_kind, const float *d_bias,
-                            float *d_output, uint32_t act, hipStream_t s, const float *d_input = nullptr,
-                            const void *d_s_in = nullptr, uint32_t s_in_kind = CTOX_KSCALE_NONE) {
+                            float *d_output, uint32_t act, hipStream_t s, const float *d_input,
+                            const void *d_s_in, uint32_t s_in_kind, const TileXform *xf) {
     const int q4 = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
     const size_t units = (size_t)t.tiles * t.chunks;
     const size_t slots = (size_t)(b->cus > 0 ? b->cus : 256) * 12;
@@ -429,8 +455,27 @@ ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const ctox_hip_m
     a.input = d_input;
     a.s_in = d_s_in;
     a.s_in_kind = s_in_kind;
+    if (xf) {
+        a.xmode = xf->xmode;
+        a.xb = xf->b;
+        a.xw = xf->w;
+        a.delta = xf->delta;
+        a.x_out = xf->x_out;
+        a.norm_out = xf->norm_out;
+        a.off = xf->off;
+        a.head_dim = xf->head_dim;
+        a.eps = xf->eps;
+    }
     hipFunction_t f = d_input ? b->tilex[q4][u - 1] : b->tile[q4][u - 1];
     return launch(f, dim3((unsigned)((waves + 3) / 4)), dim3(256), s, a, "ctox_q*_mv_tile*_gfx950");
+}
+
+// The registered tiled copy of raw weights, or NULL.
+const TiledCopy *registered(ctox_hip_backend *b, const void *d_weights, size_t rows, size_t columns) {
+    if (b->raw_tiled.empty()) return nullptr;
+    auto it = b->raw_tiled.find(d_weights);
+    if (it == b->raw_tiled.end() || it->second.rows != rows || it->second.columns != columns) return nullptr;
+    return &it->second;
 }
 
 // `prepped` marks the layouts already staged for this input in this call
@@ -575,6 +620,8 @@ extern "C" void ctox_hip_backend_destroy(ctox_hip_backend *b) {
     (void)hipDeviceSynchronize();
     DevBuf *bufs[] = {&b->xa[0], &b->xa[1], &b->xc[0], &b->xc[1], &b->norms, &b->tok, &b->stats, &b->attn,
                       &b->tpart, &b->tcnt};
+    for (auto &kv : b->raw_tiled)
+        if (kv.second.d) (void)hipFree(kv.second.d);
     for (DevBuf *d : bufs)
         if (d->ptr) (void)hipFree(d->ptr);
     if (b->stream) (void)hipStreamDestroy(b->stream);
@@ -602,27 +649,37 @@ extern "C" ctox_status ctox_hip_synchronize(ctox_hip_backend *b) {
 namespace {
 // Rewrites every segment of a resident matrix into the tiled layout on the
 // device (one pass at prepare time; the crate-layout copy stays for batch > 1).
+ctox_status tile_copy(ctox_hip_backend *b, int32_t dtype, const void *d_src, size_t rows, size_t columns,
+                      hipStream_t s, TiledCopy &t) {
+    const uint32_t blocks = (uint32_t)(columns / kBlockLen);
+    t.rows = (uint32_t)rows;
+    t.columns = (uint32_t)columns;
+    t.tiles = (uint32_t)((rows + CTOX_TILE_ROWS - 1) / CTOX_TILE_ROWS);
+    t.chunks = (blocks + CTOX_TILE_BLOCKS - 1) / CTOX_TILE_BLOCKS;
+    const uint32_t q4 = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
+    const size_t units = (size_t)t.tiles * t.chunks;
+    if (units > 0x7fffffffu || units * ctox_tile_unit_bytes(q4) > 0x7ffffff0u)
+        return fail(CTOX_ERR_SHAPE, "matrix too large to tile");
+    HIP_TRY(hipMalloc(&t.d, units * ctox_tile_unit_bytes(q4)));
+    TileRepackArgs a{};
+    a.src = (const uint8_t *)d_src;
+    a.dst = (uint8_t *)t.d;
+    a.rows = (uint32_t)rows;
+    a.blocks = blocks;
+    a.tiles = t.tiles;
+    a.chunks = t.chunks;
+    a.dtype = q4;
+    return launch(b->repack, dim3((unsigned)units), dim3(64), s, a, "ctox_tile_repack_gfx950");
+}
+
+// Rewrites every segment of a resident matrix into the tiled layout on the
+// device (one pass at prepare time; the crate-layout copy stays for batch > 1).
 ctox_status tile_segments(ctox_hip_backend *b, ctox_hip_matrix *m) {
-    const uint32_t blocks = (uint32_t)(m->columns / kBlockLen);
     for (const ctox_quant_segment &seg : m->segments) {
-        ctox_hip_matrix::Tiled t;
-        const size_t rows = seg.row_end - seg.row_start;
-        t.tiles = (uint32_t)((rows + CTOX_TILE_ROWS - 1) / CTOX_TILE_ROWS);
-        t.chunks = (blocks + CTOX_TILE_BLOCKS - 1) / CTOX_TILE_BLOCKS;
-        const uint32_t q4 = seg.dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
-        const size_t units = (size_t)t.tiles * t.chunks;
-        if (units > 0x7fffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large to tile");
-        HIP_TRY(hipMalloc(&t.d, units * ctox_tile_unit_bytes(q4)));
-        m->tiled.push_back(t);
-        TileRepackArgs a{};
-        a.src = (const uint8_t *)m->d_weights + seg.offset;
-        a.dst = (uint8_t *)t.d;
-        a.rows = (uint32_t)rows;
-        a.blocks = blocks;
-        a.tiles = t.tiles;
-        a.chunks = t.chunks;
-        a.dtype = q4;
-        ctox_status st = launch(b->repack, dim3((unsigned)units), dim3(64), b->stream, a, "ctox_tile_repack_gfx950");
+        TiledCopy t;
+        ctox_status st = tile_copy(b, seg.dtype, (const uint8_t *)m->d_weights + seg.offset,
+                                   seg.row_end - seg.row_start, m->columns, b->stream, t);
+        if (t.d) m->tiled.push_back(t);
         if (st) return st;
     }
     HIP_TRY(hipStreamSynchronize(b->stream));
@@ -743,11 +800,46 @@ extern "C" ctox_status ctox_hip_launch_fused_matvec(ctox_hip_backend *b, int32_t
     if (activation > 1) return fail(CTOX_ERR_SHAPE, "activation %u is not identity (0) or SiLU (1)", activation);
     hipStream_t s = pick_stream(b, stream);
     const int layout = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
+    if (batch == 1)
+        if (const TiledCopy *t = registered(b, d_weights, rows, columns))
+            return run_tile_matvec(b, dtype, *t, rows, columns, d_s_out, d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE,
+                                   d_bias, d_output, activation, s, d_input, d_s_in,
+                                   d_s_in ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE);
     ctox_status st = run_prep(b, layout, d_input, columns, batch, d_s_in,
                               d_s_in ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, s);
     if (st) return st;
     return run_matvec(b, layout, dtype, d_weights, rows, columns, batch, d_s_out,
                       d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, d_bias, d_output, rows, activation, s);
+}
+
+extern "C" ctox_status ctox_hip_register_tiled_weights(ctox_hip_backend *b, int32_t dtype, const void *d_weights,
+                                                       uint32_t rows, uint32_t columns, void *stream) {
+    if (!b || !d_weights) return fail(CTOX_ERR_SHAPE, "null argument");
+    if (dtype != CTOX_DTYPE_Q2B64 && dtype != CTOX_DTYPE_Q4B64)
+        return fail(CTOX_ERR_UNSUPPORTED_DTYPE, "tiled registration takes pure Q2_B64 or Q4_B64 weights");
+    if (rows == 0 || columns == 0 || columns % kBlockLen)
+        return fail(CTOX_ERR_SHAPE, "Q2/Q4 fused matvec dimensions must be non-zero and columns divisible by 64");
+    ctox_hip_unregister_tiled_weights(b, d_weights);
+    TiledCopy t;
+    ctox_status st = tile_copy(b, dtype, d_weights, rows, columns, pick_stream(b, stream), t);
+    if (st) {
+        if (t.d) {
+            (void)hipStreamSynchronize(pick_stream(b, stream));
+            (void)hipFree(t.d);
+        }
+        return st;
+    }
+    b->raw_tiled[d_weights] = t;
+    return CTOX_OK;
+}
+
+extern "C" void ctox_hip_unregister_tiled_weights(ctox_hip_backend *b, const void *d_weights) {
+    if (!b) return;
+    auto it = b->raw_tiled.find(d_weights);
+    if (it == b->raw_tiled.end()) return;
+    (void)hipDeviceSynchronize();  // launches queued on any stream may still read the copy
+    if (it->second.d) (void)hipFree(it->second.d);
+    b->raw_tiled.erase(it);
 }
 
 // ======================================================================
@@ -775,6 +867,21 @@ extern "C" ctox_status ctox_hip_norm_matvec_device(ctox_hip_backend *b, const fl
     hipStream_t s = pick_stream(b, stream);
     const int layout = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
     const size_t blocks = columns / kBlockLen;
+    // Registered weights, batch 1, at most one delta part: the residual add
+    // and norm are computed inside the tiled matvec (one launch).
+    if (batch == 1 && (!d_delta || delta_parts == 1)) {
+        if (const TiledCopy *t = registered(b, d_weights, rows, columns)) {
+            TileXform xf;
+            xf.xmode = 1;
+            xf.w = d_norm_w;
+            xf.delta = d_delta;
+            xf.x_out = d_delta ? d_x_out : nullptr;
+            xf.norm_out = d_norm_out;
+            xf.eps = eps;
+            return run_tile_matvec(b, dtype, *t, rows, columns, d_s_out, d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE,
+                                   nullptr, d_output, 0, s, d_x, d_s_in, d_s_in ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, &xf);
+        }
+    }
     ctox_status st = ensure(b, b->xa[layout], blocks * batch * 192, false);
     if (!st) st = ensure(b, b->xc[layout], blocks * batch * 4 * sizeof(float), false);
     if (st) return st;
@@ -823,6 +930,21 @@ extern "C" ctox_status ctox_hip_transform_matvec_device(ctox_hip_backend *b, con
     hipStream_t s = pick_stream(b, stream);
     const int layout = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
     const size_t blocks = columns / kBlockLen;
+    // Registered weights, batch 1: the producer runs inside the tiled matvec.
+    if (batch == 1 && (x->mode != 2 || x->head_dim == 64 || x->head_dim == 128 || x->head_dim == 256) &&
+        (x->mode != 3 || x->head_dim % 4 == 0)) {
+        if (const TiledCopy *t = registered(b, d_weights, rows, columns)) {
+            TileXform xf;
+            xf.xmode = x->mode + 1;
+            xf.b = x->b;
+            xf.w = x->w;
+            xf.off = x->off;
+            xf.head_dim = x->head_dim;
+            xf.eps = x->eps;
+            return run_tile_matvec(b, dtype, *t, rows, columns, d_s_out, d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE,
+                                   nullptr, d_output, 0, s, x->a, d_s_in, d_s_in ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, &xf);
+        }
+    }
     ctox_status st = ensure(b, b->xa[layout], blocks * batch * 192, false);
     if (!st) st = ensure(b, b->xc[layout], blocks * batch * 4 * sizeof(float), false);
     if (st) return st;

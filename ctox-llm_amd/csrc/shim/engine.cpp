@@ -94,6 +94,7 @@ struct ctox_hip_engine {
     ctox_engine_config c{};
     hipStream_t s = nullptr;
     std::vector<void *> allocs;
+    std::vector<const void *> tiled;  // weights with a registered tiled copy
     std::vector<Layer> layers;
     Mat embed, lm_head;
     float *final_norm = nullptr;
@@ -158,7 +159,7 @@ ctox_status fill(ctox_hip_engine *e, void *p, uint64_t n, uint32_t kind, uint64_
 
 // A quantized matrix with fp16 s_in / s_out in U(0.75, 1.25) and block scales |N(0, 0.02)|.
 ctox_status make_mat(ctox_hip_engine *e, Mat &m, int32_t dtype, uint32_t rows, uint32_t cols, uint64_t &seed,
-                     uint16_t *shared_s_in = nullptr) {
+                     uint16_t *shared_s_in = nullptr, bool projection = true) {
     m.dtype = dtype;
     m.rows = rows;
     m.cols = cols;
@@ -172,6 +173,12 @@ ctox_status make_mat(ctox_hip_engine *e, Mat &m, int32_t dtype, uint32_t rows, u
     }
     TRY(dalloc_t(e, &m.s_out, rows));
     TRY(fill(e, m.s_out, rows, 3, seed++, 0.75f, 1.25f));
+    if (projection) {
+        // Batch-1 projections stream the tiled copy; the crate-layout rows stay
+        // for the small-M verify kernels.
+        TRY(ctox_hip_register_tiled_weights(e->b, dtype, m.w, rows, cols, e->s));
+        e->tiled.push_back(m.w);
+    }
     return CTOX_OK;
 }
 
@@ -504,7 +511,7 @@ extern "C" ctox_status ctox_hip_engine_create(ctox_hip_backend *b, const ctox_en
     if (hipStreamCreate(&e->s) != hipSuccess) return cleanup(efail(CTOX_ERR_INVALID_STATE, "stream creation failed"));
     ctox_status st;
     uint64_t sd = seed * 1000003ull + 17;
-    if ((st = make_mat(e, e->embed, CTOX_DTYPE_Q4B64, e->V, e->H, sd))) return cleanup(st);
+    if ((st = make_mat(e, e->embed, CTOX_DTYPE_Q4B64, e->V, e->H, sd, nullptr, false))) return cleanup(st);
     if ((st = make_mat(e, e->lm_head, CTOX_DTYPE_Q4B64, e->V, e->H, sd))) return cleanup(st);
     if ((st = make_vec(e, &e->final_norm, e->H, sd, 0.0f, 0.1f))) return cleanup(st);
     uint32_t n_gdn = 0;
@@ -575,6 +582,7 @@ extern "C" ctox_status ctox_hip_engine_create(ctox_hip_backend *b, const ctox_en
 extern "C" void ctox_hip_engine_destroy(ctox_hip_engine *e) {
     if (!e) return;
     if (e->s) hipStreamSynchronize(e->s);
+    for (const void *p : e->tiled) ctox_hip_unregister_tiled_weights(e->b, p);
     for (void *p : e->allocs) hipFree(p);
     if (e->s) hipStreamDestroy(e->s);
     delete e;

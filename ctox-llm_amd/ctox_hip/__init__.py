@@ -224,6 +224,8 @@ SIGNATURES = {
     "ctox_hip_matrix_dispatch": (_I32, [_P, _P, _P, _SZ, _P, _P]),
     "ctox_hip_matrix_dispatch_fanout": (_I32, [_P, ctypes.POINTER(_P), _SZ, _P, _SZ, ctypes.POINTER(_P), _P]),
     "ctox_hip_launch_fused_matvec": (_I32, [_P, _I32, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _P]),
+    "ctox_hip_register_tiled_weights": (_I32, [_P, _I32, _P, _U32, _U32, _P]),
+    "ctox_hip_unregister_tiled_weights": (None, [_P, _P]),
     "ctox_hip_gated_delta_step": (_I32, [_P, _P, _P, _P, _P, _P, _P, _SZ, _SZ, _SZ, _P]),
     "ctox_hip_gated_delta_sequence": (_I32, [_P, _P, _P, _P, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P]),
     "ctox_hip_gated_delta_step_device": (_I32, [_P, _P, _P, _P, _P, _P, _P, _SZ, _SZ, _SZ, _P, _P]),
@@ -441,6 +443,15 @@ class HipBackend:
         _check(load_library().ctox_hip_launch_fused_matvec(
             self.handle, int(dtype), d_weights, d_input, d_s_in, d_s_out, d_bias, d_output, rows, columns,
             int(activation), batch, stream))
+
+    def register_tiled_weights(self, dtype: TensorDType, d_weights: int, rows: int, columns: int,
+                               stream: Optional[int] = None) -> None:
+        """Batch-1 raw launches on d_weights use a tiled copy made now."""
+        _check(load_library().ctox_hip_register_tiled_weights(self.handle, int(dtype), d_weights, rows, columns,
+                                                              stream))
+
+    def unregister_tiled_weights(self, d_weights: int) -> None:
+        load_library().ctox_hip_unregister_tiled_weights(self.handle, d_weights)
 
     # -- gated delta (Q/src/reference.rs:230-415)
     def gated_delta_step(self, q, k, v, log_decay, beta, state: np.ndarray, heads: int, key_dim: int,

@@ -195,6 +195,21 @@ ctox_status ctox_hip_launch_fused_matvec(ctox_hip_backend *backend, int32_t dtyp
                                          uint32_t columns, uint32_t activation, uint32_t batch,
                                          void *stream);
 
+/* Registers a tiled copy of raw packed weights already on the device
+ * (pure Q2_B64 / Q4_B64, `rows` x `columns`, the crate's row layout at
+ * d_weights). Batch-1 launches of the raw device entry points
+ * (ctox_hip_launch_fused_matvec, ctox_hip_norm_matvec_device,
+ * ctox_hip_transform_matvec_device) whose d_weights, rows and columns match a
+ * registration then run the tiled-layout kernel, as resident matrices do
+ * (the device-side counterpart of the CUDA runtime's prepare step,
+ * Q/src/backend/cuda_runtime.rs:8341-8386). The copy is made in stream order
+ * on `stream` and reflects the weights at that point; re-register after
+ * changing them. Registering the same pointer again replaces the copy. */
+ctox_status ctox_hip_register_tiled_weights(ctox_hip_backend *backend, int32_t dtype, const void *d_weights,
+                                            uint32_t rows, uint32_t columns, void *stream);
+/* Drops the tiled copy registered for d_weights (no-op when none is). */
+void ctox_hip_unregister_tiled_weights(ctox_hip_backend *backend, const void *d_weights);
+
 /* Residual add + (1 + w) RMS norm (Q/src/reference.rs:38-62) of `batch`
  * dense rows: h = d_x + d_delta (d_delta may be NULL: h = d_x), written to
  * d_x_out (required with d_delta, must not alias d_x); then the fused matvec

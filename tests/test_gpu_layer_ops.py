@@ -15,6 +15,8 @@
 """
 import sys
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -156,14 +158,17 @@ def test_strided_gates_and_conv_rows(hip, orc):
     assert np.array_equal(ds.cpu().numpy().reshape(-1), ref_state)
 
 
-@pytest.mark.parametrize("batch,with_delta,dtype", [(1, True, 1), (3, False, 1), (5, True, 0)])
-def test_norm_matvec(hip, orc, batch, with_delta, dtype):
+@pytest.mark.parametrize("batch,with_delta,dtype,registered,rows,cols", [
+    (1, True, 1, False, 300, 5120), (3, False, 1, False, 300, 5120), (5, True, 0, False, 300, 5120),
+    (1, True, 1, True, 300, 5120), (1, False, 0, True, 300, 5120), (1, True, 0, True, 300, 5120),
+    (1, True, 1, True, 1024, 256), (1, False, 1, True, 512, 256), (1, True, 0, True, 40, 1088)])
+def test_norm_matvec(hip, orc, batch, with_delta, dtype, registered, rows, cols):
     """Residual add + (1 + w) RMS norm fused with the projection's activation
-    staging, against the oracle norm followed by the oracle fused matvec."""
-    say(f"case norm_matvec batch={batch} delta={with_delta} dtype={dtype}")
+    staging (registered weights: inside the tiled matvec), against the oracle
+    norm followed by the oracle fused matvec."""
+    say(f"case norm_matvec batch={batch} delta={with_delta} dtype={dtype} registered={registered}")
     from ctox_hip import synth  # noqa: F401  (weights built here directly)
     rng = np.random.default_rng(batch * 10 + dtype)
-    rows, cols = 300, 5120
     bb = 34 if dtype == 1 else 18
     blocks = rng.integers(0, 256, size=(rows, cols // 64, bb), dtype=np.uint8)
     scales = (np.abs(rng.standard_normal((rows, cols // 64))) * 0.02).astype(np.float16)
@@ -182,6 +187,8 @@ def test_norm_matvec(hip, orc, batch, with_delta, dtype):
     no = torch.empty(batch, cols, device="cuda")
     out = torch.empty(batch, rows, device="cuda")
     hip_lib = __import__("ctox_hip").load_library()
+    if registered:
+        hip.register_tiled_weights(__import__("ctox_hip").TensorDType(dtype), dwt.data_ptr(), rows, cols)
     st = hip_lib.ctox_hip_norm_matvec_device(hip.handle, dx.data_ptr(), dd.data_ptr() if with_delta else None, 1, 0,
                                              xo.data_ptr() if with_delta else None, dw.data_ptr(), 1e-6,
                                              no.data_ptr(), dtype, dwt.data_ptr(), dsi.data_ptr(), dso.data_ptr(),
@@ -197,3 +204,75 @@ def test_norm_matvec(hip, orc, batch, with_delta, dtype):
         ref = orc.fused_matvec(dtype, w_bytes, rows, cols, y, s_in=("f16le", s_in.view(np.uint8)),
                                s_out=("f16le", s_out.view(np.uint8)))
         np.testing.assert_allclose(out[t].cpu().numpy(), ref, rtol=1e-3, atol=1e-4 * float(np.abs(ref).max()))
+    if registered:
+        hip.unregister_tiled_weights(dwt.data_ptr())
+
+
+class _Transform(ctypes.Structure):
+    _fields_ = [("a", ctypes.c_void_p), ("b", ctypes.c_void_p), ("w", ctypes.c_void_p), ("mode", ctypes.c_uint32),
+                ("a_stride", ctypes.c_uint32), ("b_stride", ctypes.c_uint32), ("off", ctypes.c_uint32),
+                ("head_dim", ctypes.c_uint32), ("eps", ctypes.c_float)]
+
+
+@pytest.mark.parametrize("mode,dtype,registered,hd,heads", [
+    (1, 0, True, 128, 12), (2, 1, True, 128, 12), (3, 1, True, 128, 12), (1, 0, False, 128, 12),
+    (2, 1, False, 128, 12), (3, 1, False, 128, 12), (2, 1, True, 64, 4), (3, 1, True, 256, 4), (1, 0, True, 64, 4)])
+def test_transform_matvec(hip, orc, mode, dtype, registered, hd, heads):
+    """Producer fused into a projection (swiglu -> down, gated norm ->
+    out_proj, attention gate -> o_proj), batch 1, with the staging kernel or
+    (registered weights) inside the tiled matvec, against the oracle producer
+    followed by the oracle fused matvec."""
+    import ctox_hip
+    say(f"case transform_matvec mode={mode} dtype={dtype} registered={registered}")
+    rng = np.random.default_rng(40 + mode)
+    rows = 192
+    cols = {1: 2048 if heads == 12 else 512, 2: heads * hd, 3: heads * hd}[mode]
+    bb = 34 if dtype == 1 else 18
+    blocks = rng.integers(0, 256, size=(rows, cols // 64, bb), dtype=np.uint8)
+    blocks[:, :, :2] = (np.abs(rng.standard_normal((rows, cols // 64))) * 0.02).astype(np.float16).view(
+        np.uint8).reshape(rows, cols // 64, 2)
+    w_bytes = blocks.tobytes()
+    s_in = rng.uniform(0.75, 1.25, cols).astype(np.float16)
+    s_out = rng.uniform(0.75, 1.25, rows).astype(np.float16)
+    nw = (rng.standard_normal(hd) * 0.1 + 1.0).astype(np.float32)
+    if mode == 1:
+        a = rng.standard_normal(2 * cols).astype(np.float32)
+        b = None
+        x = orc.swiglu(a[:cols], a[cols:])
+        tr = _Transform(0, 0, 0, 1, 2 * cols, 0, cols, 0, 0.0)
+    elif mode == 2:
+        a = rng.standard_normal(cols).astype(np.float32)
+        b = rng.standard_normal(cols).astype(np.float32)
+        x = orc.rms_norm_gated(a, b, heads, hd, nw, 1e-6)
+        tr = _Transform(0, 0, 0, 2, cols, cols, 0, hd, 1e-6)
+    else:
+        a = rng.standard_normal(cols).astype(np.float32)
+        b = rng.standard_normal(2 * cols).astype(np.float32)
+        x = a.copy()
+        orc.sigmoid_gate(x, b.reshape(heads, 2 * hd)[:, hd:].reshape(-1))
+        tr = _Transform(0, 0, 0, 3, cols, 2 * cols, 0, hd, 0.0)
+    da, dw_norm = dev(a), dev(nw)
+    db = dev(b) if b is not None else None
+    tr.a = da.data_ptr()
+    tr.b = db.data_ptr() if db is not None else None
+    tr.w = dw_norm.data_ptr() if mode == 2 else None
+    dwt = torch.from_numpy(np.frombuffer(w_bytes, np.uint8).copy()).cuda()
+    dsi = torch.from_numpy(s_in.view(np.int16).copy()).cuda()
+    dso = torch.from_numpy(s_out.view(np.int16).copy()).cuda()
+    out = torch.full((1, rows), float("nan"), device="cuda")
+    lib = ctox_hip.load_library()
+    if registered:
+        hip.register_tiled_weights(ctox_hip.TensorDType(dtype), dwt.data_ptr(), rows, cols)
+    parts = ctypes.c_uint32(0)
+    st = lib.ctox_hip_transform_matvec_device(hip.handle, ctypes.byref(tr), dtype, dwt.data_ptr(), dsi.data_ptr(),
+                                              dso.data_ptr(), out.data_ptr(), rows, cols, 1, 0,
+                                              ctypes.byref(parts), None)
+    assert st == 0, lib.ctox_hip_last_error()
+    torch.cuda.synchronize()
+    if registered:
+        hip.unregister_tiled_weights(dwt.data_ptr())
+    ref = orc.fused_matvec(dtype, w_bytes, rows, cols, x, s_in=("f16le", s_in.view(np.uint8)),
+                           s_out=("f16le", s_out.view(np.uint8)))
+    got = out[0].cpu().numpy()
+    rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
+    assert np.all(np.abs(got - ref) <= 1e-3 * (np.abs(ref) + rms)), float(np.abs(got - ref).max())

@@ -325,3 +325,39 @@ def test_recovered_row_bit_exact(hip, orc, dtype):
     got = hip.recovered_row_matvec(ctox_hip.RecoveredRowMatVec(ctox_hip.TensorDType(dtype), w, x, 0.5))
     ref = orc.recovered_row_matvec(dtype, w.tobytes(), x, 0.5)
     assert abs(got - ref) <= 1e-4 * (abs(ref) + 1.0)
+
+
+@pytest.mark.parametrize("dtype,rows,cols", [(1, 1000, 5120), (0, 333, 17408), (1, 17, 192)])
+def test_registered_tiled_raw_launch(hip, orc, dtype, rows, cols):
+    """Batch-1 raw launches on registered weights run the tiled kernel and
+    agree with the oracle; after unregistering, the crate-layout kernels
+    give the same rows to the stated tolerance."""
+    torch = _torch()
+    say(f"case registered tiled dtype={dtype} {rows}x{cols}")
+    w = synth.random_matrix(dtype, rows, cols, 91)
+    x = synth.activation("normal", cols, 92, 1)
+    s_in = np.linspace(0.9, 1.1, cols).astype(np.float16)
+    s_out = np.linspace(1.1, 0.9, rows).astype(np.float16)
+    ref = orc.fused_matvec(dtype, w, rows, cols, x[0], ("f16le", s_in.view(np.uint8)), ("f16le", s_out.view(np.uint8)),
+                           None, 0)
+    dw = torch.from_numpy(w).cuda()
+    dx = torch.from_numpy(x).cuda()
+    dsi = torch.from_numpy(s_in.view(np.int16)).cuda()
+    dso = torch.from_numpy(s_out.view(np.int16)).cuda()
+    stream = torch.cuda.current_stream().cuda_stream
+    hip.register_tiled_weights(ctox_hip.TensorDType(dtype), dw.data_ptr(), rows, cols, stream)
+    outs = []
+    for _ in range(2):
+        dy = torch.full((1, rows), float("nan"), device="cuda")
+        hip.launch_fused_matvec(ctox_hip.TensorDType(dtype), dw.data_ptr(), dx.data_ptr(), dsi.data_ptr(),
+                                dso.data_ptr(), None, dy.data_ptr(), rows, cols, ctox_hip.Activation.Identity, 1, stream)
+        torch.cuda.synchronize()
+        outs.append(dy.cpu().numpy()[0])
+    assert np.array_equal(outs[0], outs[1])
+    check(outs[0], ref, "registered tiled")
+    hip.unregister_tiled_weights(dw.data_ptr())
+    dy = torch.empty((1, rows), device="cuda")
+    hip.launch_fused_matvec(ctox_hip.TensorDType(dtype), dw.data_ptr(), dx.data_ptr(), dsi.data_ptr(), dso.data_ptr(),
+                            None, dy.data_ptr(), rows, cols, ctox_hip.Activation.Identity, 1, stream)
+    torch.cuda.synchronize()
+    check(dy.cpu().numpy()[0], ref, "crate layout after unregister")
