@@ -5,8 +5,8 @@
 Headline (BASELINE.json metric "Q4/Q2 matvec GB/s"): BASELINE config 2, the
 Q2_B64 fused dequant-matvec of the FFN down-projection, 5120 x 17408, batch
 1, fp16 s_in/s_out as production loads them. One step = one
-ctox_hip_matrix_dispatch (activation staging + matvec) on a resident
-weight copy; copies rotate over > 512 MB so the 256 MB Infinity Cache
+ctox_hip_matrix_dispatch (one launch of the tiled matvec, which stages the
+activation itself) on a resident weight copy; copies rotate over > 512 MB so the 256 MB Infinity Cache
 cannot serve repeats. `value` = algorithmic bytes per step / step time.
 
 Also reported under "extra": config 1 (Q4 17408 x 5120), config 3 (one
@@ -29,8 +29,8 @@ sys.path.insert(0, os.path.join(ROOT, "ctox-llm_amd"))
 
 HBM_PEAK_GBS = 8000.0
 INFINITY_CACHE = 256 << 20
-HEAD_KERNEL = "ctox_q2_matvec_sl_gfx950"
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "ctox_q2_matvec_sl_gfx950.config2.traffic.txt")
+HEAD_KERNEL = "ctox_q2_mv_tile2x_gfx950"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "ctox_q2_mv_tile2x_gfx950.config2.traffic.txt")
 
 
 def log(*a):
@@ -89,8 +89,8 @@ def bench_matvec(torch, hip, ctox_hip, synth, dtype, rows, cols, xkind, steps, w
         for i in range(steps):
             mats[i % copies].dispatch(x.data_ptr(), batch, y.data_ptr(), stream)
     step_ms = t.ms / steps
-    # Dominant kernel alone: one fan-out call stages the activation once and
-    # runs the matvec kernel on every copy back to back.
+    # Dominant kernel alone: one fan-out call runs the matvec kernel on every
+    # copy back to back (batch 1 is a single kernel per matrix).
     reps = max(1, 240 // copies)
     seq = mats * reps
     outs = [y.data_ptr()] * len(seq)
