@@ -169,6 +169,10 @@ struct TileMatvecArgs {
     uint32_t off;
     uint32_t head_dim;
     float eps;
+    // Small-M kernels (ctox_q*_mv_tilem*): activation rows (2..8, staged in
+    // xa/xc by a prep kernel) and the output row stride.
+    uint32_t batch;
+    uint32_t out_stride;
 };
 
 struct RecoveredRowArgs {

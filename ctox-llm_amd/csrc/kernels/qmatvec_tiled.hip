@@ -402,6 +402,195 @@ CTOX_TILE_KERNEL(ctox_q4_mv_tile3x_gfx950, 1, 3, 1)
 CTOX_TILE_KERNEL(ctox_q4_mv_tile4x_gfx950, 1, 4, 1)
 
 
+
+// ---------------------------------------------------------------------------
+// Small-M (2..8 activation rows) tiled matvec: the MTP verify projections.
+// Same waves, chunks and last-arrival combine as the batch-1 kernel, with
+// token-stacked MFMAs: A rows 4t + l carry token t's limb l of one block (the
+// prep kernels' xa rows, loaded into registers once per wave), B lane (g, j)
+// carries quarter g of that block for row j, and C lane (g, j) accumulates
+// (token 4 tg + g, row j). The tiled units give lane (g, j) all four
+// quarters of block 4G + g; two permlane swap stages transpose each group's
+// 4 x 4 (lane row x dword) layout into quarter g of blocks 4G .. 4G + 3.
+// A wave covers all 16 blocks of its chunk for every token, so no
+// cross-lane reduction is needed before the combine.
+__device__ __forceinline__ void transpose4(uint32_t &r0, uint32_t &r1, uint32_t &r2, uint32_t &r3) {
+    auto s02 = __builtin_amdgcn_permlane32_swap(r0, r2, false, false);
+    auto s13 = __builtin_amdgcn_permlane32_swap(r1, r3, false, false);
+    auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+    auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+    r0 = s01[0];
+    r1 = s01[1];
+    r2 = s23[0];
+    r3 = s23[1];
+}
+
+template <int DT, int U, int TG>
+__device__ __forceinline__ void tile_matvec_m(const TileMatvecArgs &a) {
+    using C = TlCfg<DT>;
+    constexpr uint32_t MAXM = 4 * TG;
+    // The chunk's staged activation rows (xa order: [block][token][192]) and
+    // epilogue constants, shared by the workgroup's four waves (same chunk),
+    // plus a zero line for the A lanes outside the token/limb range.
+    __shared__ __align__(16) int8_t xas[CTOX_TILE_BLOCKS * MAXM * 192 + 16];
+    __shared__ float4 kqs[CTOX_TILE_BLOCKS * MAXM];
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t v = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
+    const uint32_t c = v / a.segs, s = v - c * a.segs;
+    const uint32_t t0 = s * U, M = a.batch;
+    if (c >= a.chunks) return;  // uniform over the workgroup (segs is a multiple of 4)
+    const uint32_t n = t0 < a.tiles ? min((uint32_t)U, a.tiles - t0) : 0u;
+    const uint8_t *base = a.weights + ((size_t)c * a.tiles + min(t0, a.tiles - 1)) * C::UB;
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)(n * C::UB), 0x00020000);
+    const uint32_t g = lane >> 4, j = lane & 15, limb = j & 3;
+
+    // Workgroup copy of the chunk's xa rows (contiguous: 16 blocks x M x 192
+    // bytes) and xc constants, issued before the weight loads, branch-free.
+    const uint32_t xbytes = min(CTOX_TILE_BLOCKS, a.blocks - c * CTOX_TILE_BLOCKS) * M * 192;
+    const __amdgpu_buffer_rsrc_t fr = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(a.xa + (size_t)c * CTOX_TILE_BLOCKS * M * 192), (short)0, (int)xbytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(a.xc + (size_t)c * CTOX_TILE_BLOCKS * M * 4), (short)0, (int)(xbytes / 12), 0x00020000);
+    constexpr uint32_t XL = (CTOX_TILE_BLOCKS * MAXM * 192 + 4095) / 4096;  // 16-byte loads per thread
+    v4i xl[XL];
+#pragma unroll
+    for (int i = 0; i < (int)XL; i++) xl[i] = __builtin_amdgcn_raw_buffer_load_b128(fr, (threadIdx.x + 256 * i) * 16, 0, 0);
+    const v4i kv = __builtin_amdgcn_raw_buffer_load_b128(cr, threadIdx.x * 16, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    TileUnit<DT> u[U];
+    v2u sc[U][4];
+#pragma unroll
+    for (int k = 0; k < U; k++) {
+#pragma unroll
+        for (int i = 0; i < (int)C::LPU; i++)
+            u[k].w[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, lane * 16, k * C::UB + i * 1024, CTOX_LOAD_NT);
+        // Scales of row j for all 16 blocks: entries (g', j), g' = 0..3.
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            sc[k][q] = __builtin_amdgcn_raw_buffer_load_b64(wr, C::CB + (q * 16 + j) * 8, k * C::UB, CTOX_LOAD_NT);
+    }
+#pragma unroll
+    for (int i = 0; i < (int)XL; i++)
+        if ((threadIdx.x + 256 * i) * 16 < CTOX_TILE_BLOCKS * MAXM * 192) *(v4i *)(xas + (threadIdx.x + 256 * i) * 16) = xl[i];
+    if (threadIdx.x < CTOX_TILE_BLOCKS * MAXM)
+        kqs[threadIdx.x] = make_float4(__int_as_float(kv[0]), __int_as_float(kv[1]), __int_as_float(kv[2]), __int_as_float(kv[3]));
+    if (threadIdx.x == 0) *(v4i *)(xas + CTOX_TILE_BLOCKS * MAXM * 192) = (v4i){0, 0, 0, 0};
+    lds_barrier();
+    if (t0 >= a.tiles) return;
+
+    // Tiles in load order (the compute of tile k needs only its own loads);
+    // the A fragments are re-read from LDS per tile.
+    float acc[U][TG];
+#pragma unroll
+    for (int k = 0; k < U; k++) {
+#pragma unroll
+        for (int tg = 0; tg < TG; tg++) acc[k][tg] = 0.0f;
+#pragma unroll
+        for (int G = 0; G < 4; G++) {
+            uint32_t e[4], o[4];
+            if (DT) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const v4i W = u[k].w[2 * G + (q >> 1)];
+                    e[q] = (uint32_t)W[2 * (q & 1)];
+                    o[q] = (uint32_t)W[2 * (q & 1) + 1];
+                }
+                transpose4(e[0], e[1], e[2], e[3]);
+                transpose4(o[0], o[1], o[2], o[3]);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; q++) e[q] = (uint32_t)u[k].w[G][q];
+                transpose4(e[0], e[1], e[2], e[3]);
+            }
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const v4i bf = DT ? unpack_quarter<DT>(e[b], o[b]) : unpack_quarter<DT>(e[b], 0);
+                const uint32_t sw = sc[k][b][G >> 1];
+                const float scale = half_bits_to_float((G & 1) ? (sw >> 16) : (sw & 0xffffu));
+#pragma unroll
+                for (int tg = 0; tg < TG; tg++) {
+                    // A lane (g, i): token 4 tg + i / 4, limb i % 4, quarter g
+                    // (the zero line outside the token / limb range).
+                    const uint32_t tok = 4 * tg + (j >> 2);
+                    const bool ok = limb < 3 && tok < M;
+                    const v4i af = *(const v4i *)(xas + (ok ? ((4 * G + b) * M + tok) * 192 + limb * 64 + g * 16
+                                                            : CTOX_TILE_BLOCKS * MAXM * 192));
+                    const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf, (v4i){0, 0, 0, 0}, 0, 0, 0);
+                    const float4 kq = kqs[(4 * G + b) * M + min(4 * tg + g, M - 1)];
+                    float f;
+                    if (DT) {
+                        f = fmaf((float)cc[0], kq.x, kq.w);
+                        f = fmaf((float)cc[1], kq.y, f);
+                        f = fmaf((float)cc[2], kq.z, f);
+                    } else {
+                        f = fmaf((float)(cc[0] + (cc[1] << 8) + (cc[2] << 16)), kq.x, kq.w);
+                    }
+                    acc[k][tg] = fmaf(f, scale, acc[k][tg]);
+                }
+            }
+        }
+    }
+    // Lane (g, j) of unit k and token group tg holds (token 4 tg + g, row j).
+    if (a.chunks == 1) {
+#pragma unroll
+        for (int k = 0; k < U; k++)
+#pragma unroll
+            for (int tg = 0; tg < TG; tg++) {
+                const uint32_t tok = 4 * tg + g, row = (t0 + k) * CTOX_TILE_ROWS + j;
+                if ((uint32_t)k < n && tok < M && row < a.rows)
+                    a.output[(size_t)tok * a.out_stride + row] = tile_epilogue(acc[k][tg] / C::DEN, row, a);
+            }
+        return;
+    }
+    // Partials [chunk][token][tiles * 16], combined as in the batch-1 kernel.
+    const size_t tstride = (size_t)a.tiles * CTOX_TILE_ROWS, cstride = tstride * M;
+#pragma unroll
+    for (int k = 0; k < U; k++)
+#pragma unroll
+        for (int tg = 0; tg < TG; tg++) {
+            const uint32_t tok = 4 * tg + g, row = (t0 + k) * CTOX_TILE_ROWS + j;
+            if ((uint32_t)k < n && tok < M)
+                __hip_atomic_store(&a.partial[c * cstride + tok * tstride + row], acc[k][tg], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+    __builtin_amdgcn_s_waitcnt(0);
+    uint32_t old = 0;
+    if (lane < n) old = __hip_atomic_fetch_add(&a.counts[t0 + lane], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int k = 0; k < U; k++) {
+        const uint32_t ok = __shfl(old, k);
+        if ((uint32_t)k < n && ok == a.chunks - 1) {
+            const uint32_t row = (t0 + k) * CTOX_TILE_ROWS + j;
+#pragma unroll
+            for (int tg = 0; tg < TG; tg++) {
+                const uint32_t tok = 4 * tg + g;
+                if (tok < M) {
+                    float sum = 0.0f;
+                    for (uint32_t c0 = 0; c0 < a.chunks; c0 += 32) {
+                        float pv[32];
+#pragma unroll
+                        for (int i = 0; i < 32; i++)
+                            pv[i] = __hip_atomic_load(&a.partial[min(c0 + i, a.chunks - 1) * cstride + tok * tstride + row],
+                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                        for (int i = 0; i < 32; i++)
+                            if (c0 + i < a.chunks) sum += pv[i];
+                    }
+                    if (row < a.rows) a.output[(size_t)tok * a.out_stride + row] = tile_epilogue(sum / C::DEN, row, a);
+                }
+            }
+            if (lane == 0) __hip_atomic_store(&a.counts[t0 + k], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+#define CTOX_TILE_M_KERNEL(name, dt, u, tg) \
+    extern "C" __global__ __launch_bounds__(256) void name(TileMatvecArgs a) { tile_matvec_m<dt, u, tg>(a); }
+CTOX_TILE_M_KERNEL(ctox_q2_mv_tilem1_gfx950, 0, 2, 1)
+CTOX_TILE_M_KERNEL(ctox_q2_mv_tilem2_gfx950, 0, 2, 2)
+CTOX_TILE_M_KERNEL(ctox_q4_mv_tilem1_gfx950, 1, 2, 1)
+CTOX_TILE_M_KERNEL(ctox_q4_mv_tilem2_gfx950, 1, 2, 2)
+
 // Rewrites crate rows (Q/src/quant.rs:20-29 block layout, rows dense) into
 // the tiled layout; one workgroup per unit, lane (g, j) moves its fragment
 // of each of the unit's four groups. Runs once per matrix at prepare time.

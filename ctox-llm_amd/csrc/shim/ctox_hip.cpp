@@ -157,6 +157,8 @@ struct ctox_hip_backend {
     hipFunction_t tile[2][CTOX_TILE_MAXU] = {};
     // The same with the activation fragments built inside the kernel.
     hipFunction_t tilex[2][CTOX_TILE_MAXU] = {};
+    // Small-M tiled kernels per dtype: [0] 2..4 rows, [1] 5..8 rows (2 row tiles per wave).
+    hipFunction_t tilem[2][2] = {};
     hipFunction_t repack = nullptr;
     int cus = 0;
     uint32_t tile_u = 0;  // CTOX_TILE_U: fixed row tiles per wave (0 = planned)
@@ -353,6 +355,10 @@ ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy 
                             hipStream_t s, const float *d_input = nullptr, const void *d_s_in = nullptr,
                             uint32_t s_in_kind = CTOX_KSCALE_NONE, const TileXform *xf = nullptr);
 
+ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows, size_t columns,
+                              size_t batch, const void *d_s_out, uint32_t s_out_kind, const float *d_bias,
+                              float *d_output, size_t out_stride, uint32_t act, hipStream_t s);
+
 // One launch over `rows` packed rows of one dtype (a pure matrix or one
 // mixed segment), output rows written at d_output[m*out_stride + r], with
 // the activation already staged in `layout`.
@@ -381,11 +387,14 @@ ctox_status run_matvec(ctox_hip_backend *b, int layout, int32_t dtype, const voi
     a.s_out_kind = s_out_kind;
     a.activation = act;
     const bool q4 = dtype == CTOX_DTYPE_Q4B64;
-    // Batch 1 on registered raw weights: the tiled kernel over the staged activation.
-    if (batch == 1 && !b->raw_tiled.empty()) {
+    // Registered raw weights: the tiled kernels over the staged activation.
+    if (!b->raw_tiled.empty()) {
         auto it = b->raw_tiled.find(d_weights);
         if (it != b->raw_tiled.end() && it->second.rows == rows && it->second.columns == columns)
-            return run_tile_matvec(b, dtype, it->second, rows, columns, d_s_out, s_out_kind, d_bias, d_output, act, s);
+            return batch == 1 ? run_tile_matvec(b, dtype, it->second, rows, columns, d_s_out, s_out_kind, d_bias,
+                                                d_output, act, s)
+                              : run_tile_matvec_m(b, dtype, it->second, rows, columns, batch, d_s_out, s_out_kind,
+                                                  d_bias, d_output, out_stride, act, s);
     }
     // Batch 1 on rows of whole 16-byte units: the slice kernels (all slices
     // requested up front when there are at most three, else walked).
@@ -470,6 +479,43 @@ ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy 
     return launch(f, dim3((unsigned)((waves + 3) / 4)), dim3(256), s, a, "ctox_q*_mv_tile*_gfx950");
 }
 
+// One launch of the small-M tiled matvec (2..8 rows staged in xa/xc).
+ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows, size_t columns,
+                              size_t batch, const void *d_s_out, uint32_t s_out_kind, const float *d_bias,
+                              float *d_output, size_t out_stride, uint32_t act, hipStream_t s) {
+    const int q4 = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
+    const uint32_t tg = batch > 4 ? 2 : 1;
+    const uint32_t u = 2;
+    const uint32_t segs = (((t.tiles + u - 1) / u) + 3) & ~3u;
+    const size_t waves = (size_t)segs * t.chunks;
+    if (waves / 4 > 0x7fffffffu || out_stride > 0xffffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
+    if (t.chunks > 1) {
+        ctox_status st = ensure(b, b->tpart, (size_t)t.chunks * batch * t.tiles * CTOX_TILE_ROWS * sizeof(float), false);
+        if (!st) st = ensure(b, b->tcnt, (size_t)t.tiles * sizeof(uint32_t), true);
+        if (st) return st;
+    }
+    TileMatvecArgs a{};
+    a.weights = (const uint8_t *)t.d;
+    a.xa = (const int8_t *)b->xa[q4].ptr;
+    a.xc = (const float *)b->xc[q4].ptr;
+    a.s_out = d_s_out;
+    a.bias = d_bias;
+    a.output = d_output;
+    a.partial = (float *)b->tpart.ptr;
+    a.counts = (uint32_t *)b->tcnt.ptr;
+    a.rows = (uint32_t)rows;
+    a.blocks = (uint32_t)(columns / kBlockLen);
+    a.tiles = t.tiles;
+    a.chunks = t.chunks;
+    a.segs = segs;
+    a.tpw = u;
+    a.s_out_kind = s_out_kind;
+    a.activation = act;
+    a.batch = (uint32_t)batch;
+    a.out_stride = (uint32_t)out_stride;
+    return launch(b->tilem[q4][tg - 1], dim3((unsigned)(waves / 4)), dim3(256), s, a, "ctox_q*_mv_tilem*_gfx950");
+}
+
 // The registered tiled copy of raw weights, or NULL.
 const TiledCopy *registered(ctox_hip_backend *b, const void *d_weights, size_t rows, size_t columns) {
     if (b->raw_tiled.empty()) return nullptr;
@@ -509,6 +555,13 @@ ctox_status dispatch_matrix(ctox_hip_backend *b, const ctox_hip_matrix *m, const
         const void *so = nullptr;
         if (m->s_out_kind == CTOX_KSCALE_F32) so = (const float *)m->d_s_out + r0;
         if (m->s_out_kind == CTOX_KSCALE_F16) so = (const uint16_t *)m->d_s_out + r0;
+        if (si < m->tiled.size()) {
+            ctox_status st = run_tile_matvec_m(b, seg.dtype, m->tiled[si], nrows, m->columns, batch, so, m->s_out_kind,
+                                               m->d_bias ? m->d_bias + r0 : nullptr, d_output + r0, m->rows, act, s);
+            if (st) return st;
+            si++;
+            continue;
+        }
         si++;
         ctox_status st = run_matvec(b, layout, seg.dtype, w, nrows, m->columns, batch, so, m->s_out_kind,
                                     m->d_bias ? m->d_bias + r0 : nullptr, d_output + r0, m->rows, act, s);
@@ -591,6 +644,8 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->tilex[0][2], "ctox_q2_mv_tile3x_gfx950"}, {&b->tilex[0][3], "ctox_q2_mv_tile4x_gfx950"},
                {&b->tilex[1][0], "ctox_q4_mv_tile1x_gfx950"}, {&b->tilex[1][1], "ctox_q4_mv_tile2x_gfx950"},
                {&b->tilex[1][2], "ctox_q4_mv_tile3x_gfx950"}, {&b->tilex[1][3], "ctox_q4_mv_tile4x_gfx950"},
+               {&b->tilem[0][0], "ctox_q2_mv_tilem1_gfx950"}, {&b->tilem[0][1], "ctox_q2_mv_tilem2_gfx950"},
+               {&b->tilem[1][0], "ctox_q4_mv_tilem1_gfx950"}, {&b->tilem[1][1], "ctox_q4_mv_tilem2_gfx950"},
                {&b->repack, "ctox_tile_repack_gfx950"}};
     for (auto &f : fns) {
         if (le != hipSuccess) break;
