@@ -111,3 +111,187 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_scan_gfx950(GdnArgs a
         if ((uint32_t)r < nrows && i < a.key_dim && colok) S[(size_t)i * a.value_dim + j] = s[r];
     }
 }
+
+// Fused token mixer core (GdnFusedArgs): one workgroup per (head, 16-column
+// slice), 256 threads, tokens in order. Per token, threads 0 .. 2 dk - 1 run
+// the causal conv + SiLU (Q/src/reference.rs:159-187) of the head's q and k
+// channels (key head h / rep, Q/src/decoder.rs:868-880) and threads 0..15 the
+// slice's v channels, each keeping its channel's window in registers; the
+// gates (Q/src/decoder.rs:29-35, 881-902) are computed by one thread (or read
+// when given); then the recurrence step of ctox_gdn_scan_gfx950 on those
+// values from LDS. The conv windows are read from conv_in and the final ones
+// written to conv_out: a key head's q/k windows by its first value head's
+// slice-0 workgroup, v windows by the workgroup that owns the columns. The
+// conv arithmetic is that of ctox_conv_update_gfx950, the gates that of
+// ctox_gdn_gates_gfx950 (same operation order).
+#define GDN_MAX_KERNEL 8
+extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_gfx950(GdnFusedArgs a) {
+    __shared__ float red_mem[GDN_GROUPS][GDN_COLS];
+    __shared__ float red_out[GDN_GROUPS][GDN_COLS];
+    __shared__ float red_nrm[2][GDN_GROUPS];
+    __shared__ float qs[256], ks[256], vs[GDN_COLS], gsc[2];
+
+    const uint32_t slices = (a.value_dim + GDN_COLS - 1) / GDN_COLS;
+    const uint32_t h = blockIdx.x / slices, slice = blockIdx.x % slices;
+    const uint32_t tid = threadIdx.x, jj = tid % GDN_COLS, ig = tid / GDN_COLS;
+    const uint32_t j = slice * GDN_COLS + jj;
+    const bool colok = j < a.value_dim;
+    const uint32_t dk = a.key_dim, rep = a.heads / a.key_heads, kh = h / rep;
+    const uint32_t kw = a.key_heads * dk, K = a.kernel;
+    const uint32_t nrows = (dk + GDN_GROUPS - 1) / GDN_GROUPS;
+    const float qscale = 1.0f / sqrtf((float)dk);
+
+    // Conv channels of this thread: one q/k channel (tid < 2 dk) and, for
+    // tid < 16, the slice's v channel.
+    const bool qk_thr = tid < 2 * dk;
+    const uint32_t qk_ch = tid < dk ? kh * dk + tid : kw + kh * dk + (tid - dk);
+    const uint32_t vj = slice * GDN_COLS + tid;
+    const bool v_thr = tid < GDN_COLS && vj < a.value_dim;
+    const uint32_t v_ch = 2 * kw + h * a.value_dim + vj;
+    float wq[GDN_MAX_KERNEL], sq_[GDN_MAX_KERNEL], wv[GDN_MAX_KERNEL], sv_[GDN_MAX_KERNEL];
+#pragma unroll
+    for (int i = 0; i < GDN_MAX_KERNEL; i++) {
+        const bool ok = (uint32_t)i < K;
+        wq[i] = qk_thr && ok ? a.conv_w[(size_t)qk_ch * K + i] : 0.0f;
+        sq_[i] = qk_thr && ok ? a.conv_in[(size_t)qk_ch * K + i] : 0.0f;
+        wv[i] = v_thr && ok ? a.conv_w[(size_t)v_ch * K + i] : 0.0f;
+        sv_[i] = v_thr && ok ? a.conv_in[(size_t)v_ch * K + i] : 0.0f;
+    }
+
+    float *S = a.state + (size_t)h * dk * a.value_dim;
+    float s[GDN_MAX_ROWS];
+#pragma unroll
+    for (int r = 0; r < GDN_MAX_ROWS; r++) {
+        const uint32_t i = ig + GDN_GROUPS * r;
+        s[r] = ((uint32_t)r < nrows && i < dk && colok) ? S[(size_t)i * a.value_dim + j] : 0.0f;
+    }
+
+    for (uint32_t t = 0; t < a.tokens; t++) {
+        const float *row = a.proj + (size_t)t * a.proj_stride;
+        // Conv step: shift the window left by one, append the input.
+        if (qk_thr) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int i = 0; i + 1 < GDN_MAX_KERNEL; i++)
+                if ((uint32_t)i + 1 < K) {
+                    const float v = sq_[i + 1];
+                    sq_[i] = v;
+                    sum += v * wq[i];
+                }
+            const float x = row[qk_ch];
+#pragma unroll
+            for (int i = 0; i < GDN_MAX_KERNEL; i++)
+                if ((uint32_t)i == K - 1) sq_[i] = x;
+            float wl = 0.0f;
+#pragma unroll
+            for (int i = 0; i < GDN_MAX_KERNEL; i++)
+                if ((uint32_t)i == K - 1) wl = wq[i];
+            sum += x * wl;
+            const float y = sum / (1.0f + expf(-sum));
+            if (tid < dk) qs[tid] = y;
+            else ks[tid - dk] = y;
+        }
+        if (v_thr) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int i = 0; i + 1 < GDN_MAX_KERNEL; i++)
+                if ((uint32_t)i + 1 < K) {
+                    const float v = sv_[i + 1];
+                    sv_[i] = v;
+                    sum += v * wv[i];
+                }
+            const float x = row[v_ch];
+            float wl = 0.0f;
+#pragma unroll
+            for (int i = 0; i < GDN_MAX_KERNEL; i++)
+                if ((uint32_t)i == K - 1) {
+                    sv_[i] = x;
+                    wl = wv[i];
+                }
+            sum += x * wl;
+            vs[tid] = sum / (1.0f + expf(-sum));
+        }
+        if (tid == 255) {
+            const size_t th = (size_t)t * a.heads + h;
+            float be, ld;
+            if (a.gates_given) {
+                be = a.beta[th];
+                ld = a.log_decay[th];
+            } else {
+                be = 1.0f / (1.0f + expf(-row[a.b_off + h]));
+                const float x = row[a.a_off + h] + a.dt_bias[h];
+                const float sp = x > 20.0f ? x : log1pf(expf(x));
+                ld = -expf(a.a_log[h]) * sp;
+                if (slice == 0) {
+                    a.beta[th] = be;
+                    a.log_decay[th] = ld;
+                }
+            }
+            gsc[0] = expf(ld);
+            gsc[1] = be;
+        }
+        __syncthreads();
+        const float decay = gsc[0], beta = gsc[1];
+        const float vjv = colok ? vs[jj] : 0.0f;
+        float kk[GDN_MAX_ROWS], qq[GDN_MAX_ROWS];
+        float mem = 0.0f, sk = 0.0f, sqq = 0.0f;
+#pragma unroll
+        for (int r = 0; r < GDN_MAX_ROWS; r++) {
+            const uint32_t i = ig + GDN_GROUPS * r;
+            const bool ok = (uint32_t)r < nrows && i < dk;
+            kk[r] = ok ? ks[i] : 0.0f;
+            qq[r] = ok ? qs[i] : 0.0f;
+            sk += kk[r] * kk[r];
+            sqq += qq[r] * qq[r];
+            s[r] = s[r] * decay;
+            mem += s[r] * kk[r];
+        }
+        red_mem[ig][jj] = mem;
+        if (jj == 0) {
+            red_nrm[0][ig] = sk;
+            red_nrm[1][ig] = sqq;
+        }
+        __syncthreads();
+        float memj = 0.0f, ssk = 0.0f, ssq = 0.0f;
+#pragma unroll
+        for (int gi = 0; gi < GDN_GROUPS; gi++) {
+            memj += red_mem[gi][jj];
+            ssk += red_nrm[0][gi];
+            ssq += red_nrm[1][gi];
+        }
+        const float kinv = 1.0f / sqrtf(ssk + 1e-6f), qinv = 1.0f / sqrtf(ssq + 1e-6f);
+        const float delta = (vjv - memj * kinv) * beta;
+        float o = 0.0f;
+#pragma unroll
+        for (int r = 0; r < GDN_MAX_ROWS; r++) {
+            s[r] += kk[r] * kinv * delta;
+            o += s[r] * qq[r];
+        }
+        red_out[ig][jj] = o;
+        __syncthreads();
+        if (ig == 0 && colok) {
+            float oj = 0.0f;
+#pragma unroll
+            for (int gi = 0; gi < GDN_GROUPS; gi++) oj += red_out[gi][jj];
+            a.out[((size_t)t * a.heads + h) * a.value_dim + j] = oj * qinv * qscale;
+        }
+        // qs/ks/vs/gsc and red_* are rewritten next token only after every
+        // thread has passed this barrier.
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int r = 0; r < GDN_MAX_ROWS; r++) {
+        const uint32_t i = ig + GDN_GROUPS * r;
+        if ((uint32_t)r < nrows && i < dk && colok) S[(size_t)i * a.value_dim + j] = s[r];
+    }
+    // Final conv windows, each written once.
+    if (qk_thr && h % rep == 0 && slice == 0)
+#pragma unroll
+        for (int i = 0; i < GDN_MAX_KERNEL; i++)
+            if ((uint32_t)i < K) a.conv_out[(size_t)qk_ch * K + i] = sq_[i];
+    if (v_thr)
+#pragma unroll
+        for (int i = 0; i < GDN_MAX_KERNEL; i++)
+            if ((uint32_t)i < K) a.conv_out[(size_t)v_ch * K + i] = sv_[i];
+}

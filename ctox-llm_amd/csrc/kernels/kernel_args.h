@@ -216,6 +216,36 @@ struct GdnArgs {
     uint32_t pad;
 };
 
+// GatedDeltaNet token mixer core in one launch (gated_delta.hip,
+// ctox_gdn_fused_gfx950): causal conv + SiLU of the q, k, v channels of the
+// projected rows, the gates, and the recurrence. Projected rows are
+// [tokens][proj_stride] holding [q (key_heads*key_dim) | k | v (heads*value_dim)]
+// at 0, a at a_off and b at b_off. The conv window goes from conv_in to
+// conv_out ([channels][kernel], channels = 2 key_heads key_dim + heads
+// value_dim; the buffers must not alias).
+struct GdnFusedArgs {
+    const float *proj;
+    const float *conv_w;     // [channels][kernel]
+    const float *conv_in;
+    float *conv_out;
+    const float *a_log;      // [heads]
+    const float *dt_bias;    // [heads]
+    float *log_decay;        // [tokens][heads]: written, or read when gates_given
+    float *beta;             // [tokens][heads]: likewise
+    float *state;            // [heads][key_dim][value_dim]
+    float *out;              // [tokens][heads][value_dim]
+    uint32_t tokens;
+    uint32_t heads;
+    uint32_t key_heads;
+    uint32_t key_dim;
+    uint32_t value_dim;
+    uint32_t kernel;
+    uint32_t proj_stride;
+    uint32_t a_off;
+    uint32_t b_off;
+    uint32_t gates_given;
+};
+
 // Decode-step glue and token selection (decode_ops.hip).
 struct GateArgs {
     const float *a;          // [tokens][heads]

@@ -160,6 +160,7 @@ struct ctox_hip_backend {
     // Small-M tiled kernels per dtype: [0] 2..4 rows, [1] 5..8 rows (2 row tiles per wave).
     hipFunction_t tilem[2][2] = {};
     hipFunction_t repack = nullptr;
+    hipFunction_t gdn_fused = nullptr;
     int cus = 0;
     uint32_t tile_u = 0;  // CTOX_TILE_U: fixed row tiles per wave (0 = planned)
     // Tiled matvec chunk partials and per-tile arrival counts (zero between launches).
@@ -646,7 +647,7 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->tilex[1][2], "ctox_q4_mv_tile3x_gfx950"}, {&b->tilex[1][3], "ctox_q4_mv_tile4x_gfx950"},
                {&b->tilem[0][0], "ctox_q2_mv_tilem1_gfx950"}, {&b->tilem[0][1], "ctox_q2_mv_tilem2_gfx950"},
                {&b->tilem[1][0], "ctox_q4_mv_tilem1_gfx950"}, {&b->tilem[1][1], "ctox_q4_mv_tilem2_gfx950"},
-               {&b->repack, "ctox_tile_repack_gfx950"}};
+               {&b->repack, "ctox_tile_repack_gfx950"}, {&b->gdn_fused, "ctox_gdn_fused_gfx950"}};
     for (auto &f : fns) {
         if (le != hipSuccess) break;
         le = hipModuleGetFunction(f.f, b->module, f.name);
@@ -1315,6 +1316,50 @@ extern "C" ctox_status ctox_hip_gated_delta_strided_device(ctox_hip_backend *b, 
     if (key_heads == 0) return fail(CTOX_ERR_SHAPE, "delta key heads must be non-zero");
     return gdn_device(b, q, k, v, log_decay, beta, state, tokens, heads, key_dim, value_dim, chunk, out,
                       pick_stream(b, stream), key_heads, qk_stride, v_stride);
+}
+
+extern "C" ctox_status ctox_hip_gdn_fused_device(ctox_hip_backend *b, const float *d_proj, size_t proj_stride,
+                                                 size_t a_off, size_t b_off, const float *d_conv_w,
+                                                 const float *d_conv_in, float *d_conv_out, size_t kernel,
+                                                 const float *d_a_log, const float *d_dt_bias, float *d_log_decay,
+                                                 float *d_beta, int gates_given, float *d_state, size_t tokens,
+                                                 size_t heads, size_t key_heads, size_t key_dim, size_t value_dim,
+                                                 float *d_out, void *stream) {
+    if (!b || !d_proj || !d_conv_w || !d_conv_in || !d_conv_out || !d_log_decay || !d_beta || !d_state || !d_out ||
+        (!gates_given && (!d_a_log || !d_dt_bias)))
+        return fail(CTOX_ERR_SHAPE, "null argument");
+    if (d_conv_in == d_conv_out) return fail(CTOX_ERR_SHAPE, "fused gated delta conv windows must not alias");
+    ctox_status st = gdn_shape(tokens, heads, key_dim, value_dim);
+    if (st) return st;
+    const size_t channels = 2 * key_heads * key_dim + heads * value_dim;
+    if (key_heads == 0 || heads % key_heads || key_dim > 128 || kernel == 0 || kernel > 8 ||
+        proj_stride < channels || a_off + heads > proj_stride || b_off + heads > proj_stride ||
+        proj_stride > 0x7fffffffu || tokens > 65536)
+        return fail(CTOX_ERR_SHAPE, "fused gated delta shapes");
+    GdnFusedArgs a{};
+    a.proj = d_proj;
+    a.conv_w = d_conv_w;
+    a.conv_in = d_conv_in;
+    a.conv_out = d_conv_out;
+    a.a_log = d_a_log;
+    a.dt_bias = d_dt_bias;
+    a.log_decay = d_log_decay;
+    a.beta = d_beta;
+    a.state = d_state;
+    a.out = d_out;
+    a.tokens = (uint32_t)tokens;
+    a.heads = (uint32_t)heads;
+    a.key_heads = (uint32_t)key_heads;
+    a.key_dim = (uint32_t)key_dim;
+    a.value_dim = (uint32_t)value_dim;
+    a.kernel = (uint32_t)kernel;
+    a.proj_stride = (uint32_t)proj_stride;
+    a.a_off = (uint32_t)a_off;
+    a.b_off = (uint32_t)b_off;
+    a.gates_given = gates_given ? 1u : 0u;
+    const size_t slices = (value_dim + 15) / 16;
+    return launch(b->gdn_fused, dim3((unsigned)(heads * slices)), dim3(256), pick_stream(b, stream), a,
+                  "ctox_gdn_fused_gfx950");
 }
 
 // ======================================================================

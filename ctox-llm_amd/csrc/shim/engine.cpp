@@ -58,7 +58,8 @@ struct GdnLayer {
     Mat in;                 // [qkv | z | a | b]
     float *conv_w = nullptr, *a_log = nullptr, *dt_bias = nullptr, *gnorm = nullptr;
     Mat out;
-    float *state = nullptr, *conv = nullptr;  // views into the engine's state blocks
+    float *state = nullptr;  // view into the engine's state block
+    size_t conv_off = 0;     // offset of the layer's conv windows in each conv block
     float *proj = nullptr, *ld = nullptr, *beta = nullptr;  // per-layer rows kept for the commit replay
 };
 
@@ -109,6 +110,11 @@ struct ctox_hip_engine {
     uint32_t q4_token_bytes = 0, q2_token_bytes = 0, q4_page_bytes = 0, q2_page_bytes = 0;
     // state blocks
     float *gdn_state = nullptr, *gdn_ckpt = nullptr, *conv_state = nullptr, *conv_ckpt = nullptr;
+    // Conv windows ping-pong between conv_state and conv_state2: a target
+    // pass reads the current block and writes the other one (the fused
+    // GatedDeltaNet kernel must not update the windows in place).
+    float *conv_state2 = nullptr;
+    uint32_t conv_par = 0;
     size_t gdn_floats = 0, conv_floats = 0;
     // activations (sized for R rows)
     float *hid = nullptr, *hid2 = nullptr, *xn = nullptr, *proj = nullptr, *convo = nullptr, *core = nullptr, *coren = nullptr,
@@ -382,17 +388,26 @@ ctox_status attn_forward(ctox_hip_engine *e, AttnLayer &a, uint32_t R, uint32_t 
                                             1, &e->delta_parts, e->s);
 }
 
-ctox_status gdn_forward(ctox_hip_engine *e, GdnLayer &g, uint32_t R, float *delta, bool keep_rows) {
+float *conv_cur(ctox_hip_engine *e) { return e->conv_par ? e->conv_state2 : e->conv_state; }
+float *conv_next(ctox_hip_engine *e) { return e->conv_par ? e->conv_state : e->conv_state2; }
+
+// Causal conv, gates and recurrence of one GatedDeltaNet layer over R
+// projected rows (one launch); gates_given replays kept gate rows.
+ctox_status gdn_core(ctox_hip_engine *e, GdnLayer &g, const float *proj, uint32_t R, float *ld, float *beta,
+                     bool gates_given) {
     const uint32_t Hv = e->c.linear_num_value_heads, Hk = e->c.linear_num_key_heads;
-    const uint32_t dk = e->c.linear_key_head_dim, dv = e->c.linear_value_head_dim;
+    return ctox_hip_gdn_fused_device(e->b, proj, e->Rin, e->C + e->Vw, e->C + e->Vw + Hv, g.conv_w,
+                                     conv_cur(e) + g.conv_off, conv_next(e) + g.conv_off,
+                                     e->c.linear_conv_kernel_dim, g.a_log, g.dt_bias, ld, beta, gates_given ? 1 : 0,
+                                     g.state, R, Hv, Hk, e->c.linear_key_head_dim, e->c.linear_value_head_dim, e->core,
+                                     e->s);
+}
+
+ctox_status gdn_forward(ctox_hip_engine *e, GdnLayer &g, uint32_t R, float *delta, bool keep_rows) {
+    const uint32_t dv = e->c.linear_value_head_dim;
     float *proj = keep_rows ? g.proj : e->proj;  // the in-projection, already computed (norm_mv)
     float *ld = keep_rows ? g.ld : e->ld, *beta = keep_rows ? g.beta : e->beta;
-    TRY(ctox_hip_causal_conv_rows_device(e->b, proj, e->Rin, g.conv, g.conv_w, e->C, e->c.linear_conv_kernel_dim, R,
-                                         e->convo, e->s));
-    TRY(ctox_hip_gdn_gates_strided_device(e->b, proj + e->C + e->Vw, proj + e->C + e->Vw + Hv, e->Rin, g.a_log,
-                                          g.dt_bias, R, Hv, ld, beta, e->s));
-    TRY(ctox_hip_gated_delta_strided_device(e->b, e->convo, e->convo + e->Kw, e->convo + 2 * e->Kw, e->C, e->C, ld,
-                                            beta, g.state, R, Hv, Hk, dk, dv, 0, e->core, e->s));
+    TRY(gdn_core(e, g, proj, R, ld, beta, false));
     ctox_input_transform x{e->core, proj + e->C, g.gnorm, 2, e->Vw, e->Rin, 0, dv, e->c.rms_norm_epsilon};
     return ctox_hip_transform_matvec_device(e->b, &x, g.out.dtype, g.out.w, g.out.s_in, g.out.s_out, delta, g.out.rows,
                                             g.out.cols, R, 1, &e->delta_parts, e->s);
@@ -423,6 +438,7 @@ ctox_status target_forward(ctox_hip_engine *e, const uint32_t *d_tok, uint32_t R
         TRY(mlp_forward(e, L.mlp, R, e->delta, e->delta));
         pending = true;
     }
+    e->conv_par ^= 1u;  // every GatedDeltaNet layer wrote its windows to the other block
     return norm_mv(e, e->delta, e->final_norm, R, e->lm_head, e->logits, e->fin);
 }
 
@@ -519,12 +535,14 @@ extern "C" ctox_status ctox_hip_engine_create(ctox_hip_backend *b, const ctox_en
     const uint32_t Hv = c.linear_num_value_heads;
     e->gdn_floats = (size_t)n_gdn * Hv * c.linear_key_head_dim * c.linear_value_head_dim;
     e->conv_floats = (size_t)n_gdn * e->C * c.linear_conv_kernel_dim;
-    if ((st = dalloc_t(e, &e->gdn_state, e->gdn_floats)) || (st = dalloc_t(e, &e->conv_state, e->conv_floats)))
+    if ((st = dalloc_t(e, &e->gdn_state, e->gdn_floats)) || (st = dalloc_t(e, &e->conv_state, e->conv_floats)) ||
+        (st = dalloc_t(e, &e->conv_state2, e->conv_floats)))
         return cleanup(st);
     if (e->mtp && ((st = dalloc_t(e, &e->gdn_ckpt, e->gdn_floats)) || (st = dalloc_t(e, &e->conv_ckpt, e->conv_floats))))
         return cleanup(st);
     hipMemsetAsync(e->gdn_state, 0, e->gdn_floats * 4, e->s);
     hipMemsetAsync(e->conv_state, 0, e->conv_floats * 4, e->s);
+    hipMemsetAsync(e->conv_state2, 0, e->conv_floats * 4, e->s);
     e->layers.resize(c.num_hidden_layers);
     uint32_t gi = 0;
     for (uint32_t l = 0; l < c.num_hidden_layers; l++) {
@@ -542,7 +560,7 @@ extern "C" ctox_status ctox_hip_engine_create(ctox_hip_backend *b, const ctox_en
             if ((st = make_vec(e, &g.gnorm, c.linear_value_head_dim, sd, 1.0f, 0.1f))) return cleanup(st);
             if ((st = make_mat(e, g.out, CTOX_DTYPE_Q4B64, e->H, e->Vw, sd))) return cleanup(st);
             g.state = e->gdn_state + (size_t)gi * Hv * c.linear_key_head_dim * c.linear_value_head_dim;
-            g.conv = e->conv_state + (size_t)gi * e->C * c.linear_conv_kernel_dim;
+            g.conv_off = (size_t)gi * e->C * c.linear_conv_kernel_dim;
             if (e->mtp && ((st = dalloc_t(e, &g.proj, (size_t)e->R * e->Rin)) || (st = dalloc_t(e, &g.ld, (size_t)e->R * Hv)) ||
                            (st = dalloc_t(e, &g.beta, (size_t)e->R * Hv))))
                 return cleanup(st);
@@ -644,7 +662,7 @@ extern "C" ctox_status ctox_hip_engine_mtp_step(ctox_hip_engine *e, uint32_t tok
     }
     // Checkpoint the recurrent states, then verify [token, d1..dk] in one pass.
     TRY(copy_d2d(e, e->gdn_ckpt, e->gdn_state, e->gdn_floats * 4));
-    TRY(copy_d2d(e, e->conv_ckpt, e->conv_state, e->conv_floats * 4));
+    TRY(copy_d2d(e, e->conv_ckpt, conv_cur(e), e->conv_floats * 4));
     TRY(target_forward(e, e->d_drafts, R, true));
     TRY(ctox_hip_mtp_accept_device(e->b, e->draft_logits, e->logits, e->logits + (size_t)k * e->V, e->d_drafts + 1, k,
                                    e->V, temperature, e->d_rng, e->d_result, e->s));
@@ -660,18 +678,10 @@ extern "C" ctox_status ctox_hip_engine_mtp_step(ctox_hip_engine *e, uint32_t tok
         if (L.full) cache_truncate(L.f.cache, k - n);
     if (n < k) {
         TRY(copy_d2d(e, e->gdn_state, e->gdn_ckpt, e->gdn_floats * 4));
-        TRY(copy_d2d(e, e->conv_state, e->conv_ckpt, e->conv_floats * 4));
-        const uint32_t Hv = e->c.linear_num_value_heads;
-        for (Layer &L : e->layers) {
-            if (L.full) continue;
-            GdnLayer &g = L.g;
-            TRY(ctox_hip_causal_conv_rows_device(e->b, g.proj, e->Rin, g.conv, g.conv_w, e->C,
-                                                 e->c.linear_conv_kernel_dim, n + 1, e->convo, e->s));
-            TRY(ctox_hip_gated_delta_strided_device(e->b, e->convo, e->convo + e->Kw, e->convo + 2 * e->Kw, e->C, e->C,
-                                                    g.ld, g.beta, g.state, n + 1, Hv, e->c.linear_num_key_heads,
-                                                    e->c.linear_key_head_dim, e->c.linear_value_head_dim, 0, e->core,
-                                                    e->s));
-        }
+        TRY(copy_d2d(e, conv_cur(e), e->conv_ckpt, e->conv_floats * 4));
+        for (Layer &L : e->layers)
+            if (!L.full) TRY(gdn_core(e, L.g, L.g.proj, n + 1, L.g.ld, L.g.beta, true));
+        e->conv_par ^= 1u;
     }
     // Final hiddens of the committed rows: h_p .. h_{p+n}.
     TRY(copy_d2d(e, e->target_hidden + e->H, e->fin, (size_t)(n + 1) * e->H * 4));
@@ -742,7 +752,7 @@ extern "C" ctox_status ctox_hip_engine_buffer(ctox_hip_engine *e, uint32_t which
     case 1: *ptr = e->fin; *bytes = (size_t)e->R * e->H * 4; break;
     case 2: *ptr = e->prev_hidden; *bytes = (size_t)e->H * 4; break;
     case 3: *ptr = e->gdn_state; *bytes = e->gdn_floats * 4; break;
-    case 4: *ptr = e->conv_state; *bytes = e->conv_floats * 4; break;
+    case 4: *ptr = conv_cur(e); *bytes = e->conv_floats * 4; break;
     case 5: *ptr = e->draft_logits; *bytes = (size_t)std::max(1u, e->c.draft_tokens) * e->V * 4; break;
     default: return efail(CTOX_ERR_SHAPE, "unknown engine buffer");
     }

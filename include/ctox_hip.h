@@ -294,6 +294,22 @@ ctox_status ctox_hip_gated_delta_strided_device(ctox_hip_backend *backend, const
                                                 const float *d_log_decay, const float *d_beta, float *d_state,
                                                 size_t tokens, size_t heads, size_t key_heads, size_t key_dim,
                                                 size_t value_dim, size_t chunk, float *d_out, void *stream);
+/* The GatedDeltaNet token mixer core of Q/src/decoder.rs:863-913 in one
+ * launch over `tokens` projected rows (row t at d_proj + t * proj_stride:
+ * [q (key_heads * key_dim) | k | v (heads * value_dim)] at 0, a at a_off, b at
+ * b_off): causal conv + SiLU of the q, k, v channels (reference.rs:159-187)
+ * from the windows in d_conv_in to d_conv_out ([channels][kernel], channels =
+ * 2 key_heads key_dim + heads value_dim; must not alias d_conv_in), the gates
+ * (decoder.rs:29-35, 881-902; written to d_log_decay / d_beta
+ * [tokens][heads], or read from them when gates_given), and the recurrence of
+ * ctox_hip_gated_delta_strided_device into d_state and d_out
+ * [tokens][heads][value_dim]. key_dim <= 128, kernel <= 8. */
+ctox_status ctox_hip_gdn_fused_device(ctox_hip_backend *backend, const float *d_proj, size_t proj_stride,
+                                      size_t a_off, size_t b_off, const float *d_conv_w, const float *d_conv_in,
+                                      float *d_conv_out, size_t kernel, const float *d_a_log, const float *d_dt_bias,
+                                      float *d_log_decay, float *d_beta, int gates_given, float *d_state,
+                                      size_t tokens, size_t heads, size_t key_heads, size_t key_dim,
+                                      size_t value_dim, float *d_out, void *stream);
 
 /* ---- decode-step glue and token selection (device buffers) ---- */
 /* GatedDeltaNet gates, Q/src/decoder.rs:881-902 (softplus :29-35):

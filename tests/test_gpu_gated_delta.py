@@ -177,3 +177,64 @@ def test_strided_repeated_key_heads(hip, orc, tokens, chunk):
     torch.cuda.synchronize()
     np.testing.assert_allclose(out.cpu().numpy().reshape(-1), ref, rtol=1e-3, atol=1e-4 * float(np.abs(ref).max()))
     np.testing.assert_allclose(dstate.cpu().numpy().reshape(-1), ref_state, rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("tokens,heads,key_heads,dk,dv,given", [(1, 48, 16, 128, 128, False), (5, 48, 16, 128, 128, False),
+                                                               (3, 4, 2, 64, 64, True), (2, 8, 8, 128, 48, False)])
+def test_fused_mixer_core_matches_separate(hip, tokens, heads, key_heads, dk, dv, given):
+    """ctox_hip_gdn_fused_device (conv + gates + recurrence in one launch) against
+    the separate conv, gates and strided recurrence entry points (each pinned
+    to the oracle by the tests above and test_gpu_layer_ops): outputs, states,
+    conv windows and gates."""
+    import ctypes
+    import torch
+    import ctox_hip
+    say(f"case fused mixer tokens={tokens} heads={heads}/{key_heads} dk={dk} dv={dv} given={given}")
+    lib = ctox_hip.load_library()
+    rng = np.random.default_rng(tokens * 100 + heads)
+    K = 4
+    kw, vw = key_heads * dk, heads * dv
+    C = 2 * kw + vw
+    a_off, b_off = C + vw, C + vw + heads
+    stride = b_off + heads + 3
+    dev = lambda x: torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+    proj = dev(rng.standard_normal((tokens, stride)))
+    conv_w = dev(rng.standard_normal((C, K)) * 0.5)
+    conv0 = rng.standard_normal((C, K)).astype(np.float32)
+    a_log = dev(rng.standard_normal(heads) * 0.3)
+    dt_bias = dev(rng.standard_normal(heads) * 0.3)
+    state0 = (rng.standard_normal((heads, dk, dv)) * 0.1).astype(np.float32)
+    ld_g = rng.uniform(-1.0, -0.05, (tokens, heads)).astype(np.float32)
+    be_g = rng.uniform(0.1, 0.9, (tokens, heads)).astype(np.float32)
+    # separate path
+    conv_a, st_a = dev(conv0), dev(state0)
+    convo = torch.empty(tokens, C, device="cuda")
+    ld_a, be_a = (dev(ld_g), dev(be_g)) if given else (torch.empty(tokens, heads, device="cuda"),
+                                                        torch.empty(tokens, heads, device="cuda"))
+    out_a = torch.empty(tokens, heads, dv, device="cuda")
+    p = lambda t: t.data_ptr()
+    assert lib.ctox_hip_causal_conv_rows_device(hip.handle, p(proj), stride, p(conv_a), p(conv_w), C, K, tokens,
+                                                p(convo), None) == 0
+    if not given:
+        assert lib.ctox_hip_gdn_gates_strided_device(hip.handle, p(proj) + 4 * a_off, p(proj) + 4 * b_off, stride,
+                                                     p(a_log), p(dt_bias), tokens, heads, p(ld_a), p(be_a), None) == 0
+    assert lib.ctox_hip_gated_delta_strided_device(hip.handle, p(convo), p(convo) + 4 * kw, p(convo) + 8 * kw, C, C,
+                                                   p(ld_a), p(be_a), p(st_a), tokens, heads, key_heads, dk, dv, 0,
+                                                   p(out_a), None) == 0
+    # fused path
+    conv_in, conv_out, st_b = dev(conv0), torch.zeros(C, K, device="cuda"), dev(state0)
+    ld_b, be_b = (dev(ld_g), dev(be_g)) if given else (torch.empty(tokens, heads, device="cuda"),
+                                                        torch.empty(tokens, heads, device="cuda"))
+    out_b = torch.empty(tokens, heads, dv, device="cuda")
+    st = lib.ctox_hip_gdn_fused_device(hip.handle, p(proj), stride, a_off, b_off, p(conv_w), p(conv_in), p(conv_out), K,
+                                       p(a_log), p(dt_bias), p(ld_b), p(be_b), 1 if given else 0, p(st_b), tokens,
+                                       heads, key_heads, dk, dv, p(out_b), None)
+    assert st == 0, lib.ctox_hip_last_error()
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(conv_out.cpu().numpy(), conv_a.cpu().numpy(), rtol=0, atol=0)
+    assert np.array_equal(conv_in.cpu().numpy(), conv0)
+    np.testing.assert_allclose(ld_b.cpu().numpy(), ld_a.cpu().numpy(), rtol=1e-6, atol=0)
+    np.testing.assert_allclose(be_b.cpu().numpy(), be_a.cpu().numpy(), rtol=1e-6, atol=0)
+    ref_o, ref_s = out_a.cpu().numpy(), st_a.cpu().numpy()
+    np.testing.assert_allclose(out_b.cpu().numpy(), ref_o, rtol=1e-4, atol=1e-5 * float(np.abs(ref_o).max()))
+    np.testing.assert_allclose(st_b.cpu().numpy(), ref_s, rtol=1e-4, atol=1e-5 * float(np.abs(ref_s).max()))
