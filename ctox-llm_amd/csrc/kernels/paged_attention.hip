@@ -306,6 +306,7 @@ __device__ __forceinline__ void pa_merge(float &m, float &d, float m2, float d2,
     m = mm;
 }
 
+#define PA_SROW 69  // stage row of one token (dwords): K run at 0, V run at 34, one pad
 #define PA_QS 260   // merge-area row of one query (floats)
 #define PA_QB 272   // LDS row of one query limb (int8): 256 + 16 spreads the b128 reads over banks
 
@@ -315,6 +316,8 @@ struct PaState {
     int32_t lim[R];
     float qscale[R][4];   // per 64-dim block: 2^-E of the query's fixed point
     int32_t xsum[R][4][3];  // per block and limb: sum of the limb over the block
+    int32_t xst[R][4];      // per block: sum of X (xsum combined)
+    float corr[R][4];       // f16 path: sum over tokens of P * (block scale), per value block
     pa_v4f o[R][16];
 };
 
@@ -425,15 +428,353 @@ __device__ __forceinline__ void pa_tile(const GqaArgs &a, PaLds<R> &L, uint32_t 
     }
 }
 
-// grid (splits, kv heads), 256 threads; four waves take contiguous runs of
-// tiles_per_wave tiles. R = 16-query tiles (queries = group * rows <= 16 R).
-template <int R>
-__device__ __forceinline__ void paged_gqa_partial(const GqaArgs &a) {
-    __shared__ PaLds<R> L;
-    const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t li = lane & 15, lg = lane >> 4;
-    const uint32_t h = blockIdx.y, split = blockIdx.x;
 
+// ---------------------------------------------------------------------------
+// Page-aligned tiles (page_tokens % 16 == 0): P.V on f16 MFMA 16x16x16.
+//
+// O^T (dims x queries) += V^T P^T with k = the tile's 16 tokens. The score
+// accumulator already leaves lane (li, lg) the probabilities of tokens
+// 4 lg .. 4 lg + 3 for query li, which is exactly its B operand. Per value
+// block b and chunk c the A operand row m is dim 64 b + 4 m + c, so lane
+// (li, lg) needs one code byte (Q2) or two (Q4) per (token, block) and its
+// C rows are dims 64 b + 16 lg + 4 i + c.
+//
+// A value is v = s (2 code - K) / K = (2 s / K) code - s (K = 3 Q2, 15 Q4).
+// A holds the raw codes, exact in f16: the code field (placed at bit 2 c of
+// each half, i.e. times 4^c) is ORed under the exponent field E and the
+// implicit one is subtracted, giving code * 4^c * 2^(E - 25) exactly. B holds
+// P * (2 s / K) * 2^(25 - E) as an f16 hi + lo pair (relative error ~2^-21),
+// with E chosen per tile and block from the largest 2 s / K so that B stays
+// in f16's normal range. The products are P (2 s / K) code 4^c whatever E
+// is; the 4^c is removed at the end and the "- s" part is summed per
+// (query, block) on the VALU (corr).
+// ---------------------------------------------------------------------------
+typedef _Float16 pa_h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 pa_h4 __attribute__((ext_vector_type(4)));
+
+// One tile's K and V head runs (4 blocks each: 18 dwords Q2, 34 Q4) of the
+// 16 tokens, moved through a per-wave LDS stage: lane (t = lane / 4, q =
+// lane % 4) loads dwords q, q + 4, ... of token t's runs, so each quad of
+// lanes reads 16 contiguous bytes. Absent tokens read a valid dummy address;
+// presence is applied where the tile is computed, and no loaded value is
+// used before then, so the wait before each tile's compute stays exact.
+
+struct PaStage {
+    uint32_t k[9], v[9];
+};
+
+__device__ __forceinline__ bool pa_present(const GqaArgs &a, const PaTile &T, uint32_t j) {
+    return T.base != nullptr && j < a.tokens && j >= T.first && j - T.first < T.count;
+}
+
+
+__device__ __forceinline__ void pa_issue_stage(const GqaArgs &a, const PaTile &T, uint32_t tb, uint32_t h,
+                                               uint32_t lane, PaStage &r) {
+    // Buffer loads against the tile's page: one 32-bit lane offset, the
+    // dword steps in the instructions' immediate offsets. Absent tokens use
+    // an offset past the page, which returns zeros without memory traffic.
+    // Loads past a run's end (up to 15 bytes) are never staged.
+    const uint32_t t = lane >> 2, q = lane & 3, j = tb + t;
+    const bool p = pa_present(a, T, j);
+    const uint32_t bs = T.q4 ? 34u : 18u;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)T.base, (short)0, (int)(T.q4 ? a.q4_page_bytes : a.q2_page_bytes), 0x00020000);
+    const uint32_t ko = p ? (j - T.first) * T.token_bytes + h * 4 * bs + 4 * q : 0x7fff0000u;
+    const uint32_t vo = p ? ko + (a.component_values / 64) * bs : 0x7fff0000u;
+    if (T.q4) {
+#pragma unroll
+        for (int m = 0; m < 9; m++) {
+            r.k[m] = __builtin_amdgcn_raw_buffer_load_b32(rs, ko + 16 * m, 0, 0);
+            r.v[m] = __builtin_amdgcn_raw_buffer_load_b32(rs, vo + 16 * m, 0, 0);
+        }
+    } else {
+#pragma unroll
+        for (int m = 0; m < 5; m++) {
+            r.k[m] = __builtin_amdgcn_raw_buffer_load_b32(rs, ko + 16 * m, 0, 0);
+            r.v[m] = __builtin_amdgcn_raw_buffer_load_b32(rs, vo + 16 * m, 0, 0);
+        }
+    }
+}
+
+// v_and_or_b32: (x & m) | o in one instruction (m a wave-uniform mask, o in a VGPR).
+__device__ __forceinline__ uint32_t pa_and_or(uint32_t x, uint32_t m, uint32_t o) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(m), "v"(o));
+    return r;
+}
+
+__device__ __forceinline__ void pa_stage_write(uint32_t *stage, uint32_t lane, bool q4, const PaStage &r) {
+    const uint32_t t = lane >> 2, q = lane & 3, nd = q4 ? 34u : 18u;
+    uint32_t *row = stage + t * PA_SROW;
+#pragma unroll
+    for (int m = 0; m < 9; m++) {
+        const uint32_t d = q + 4 * m;
+        if ((m < 5 || q4) && d < nd) {
+            row[d] = r.k[m];
+            row[34 + d] = r.v[m];
+        }
+    }
+}
+
+// Stage reads: dword-aligned byte offset o of a run; the fp16 at even offset o.
+__device__ __forceinline__ uint32_t pa_s32(const uint32_t *run, uint32_t o) { return run[o >> 2]; }
+__device__ __forceinline__ uint32_t pa_s16(const uint32_t *run, uint32_t o) {
+    return (run[o >> 2] >> (8 * (o & 2))) & 0xffffu;
+}
+
+// K operand words of token li (dims 16 lg .. of each block) from the stage,
+// in pa_issue_k's layout.
+__device__ __forceinline__ void pa_k_from_stage(const uint32_t *kr, uint32_t lg, bool q4, bool present, PaK &r) {
+#pragma unroll
+    for (int i = 0; i < 12; i++) r.w[i] = 0;
+    if (q4) {
+        r.meta = (present ? 2u << 20 : 0u) | pa_s16(kr, lg * 34);
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const uint32_t o = b * 34 + 8 * lg;
+            if (b & 1) {
+                r.w[3 * b] = pa_s32(kr, o + 2);
+                r.w[3 * b + 1] = pa_s32(kr, o + 6);
+            } else {
+                r.w[3 * b] = pa_s32(kr, o);
+                r.w[3 * b + 1] = pa_s32(kr, o + 4);
+                r.w[3 * b + 2] = pa_s32(kr, o + 8);
+            }
+        }
+    } else {
+        r.meta = (present ? 1u << 20 : 0u) | pa_s16(kr, lg * 18);
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const uint32_t o = b * 18 + 4 * lg;
+            if (b & 1) {
+                r.w[3 * b] = pa_s32(kr, o + 2);
+            } else {
+                r.w[3 * b] = pa_s32(kr, o);
+                r.w[3 * b + 1] = pa_s32(kr, o + 4);
+            }
+        }
+    }
+}
+
+// Lane i holds the page descriptor of tile t0 + i (all zeros, i.e. no
+// tokens, past t1 or past the page table). Tiles lie in one page here.
+__device__ __forceinline__ uint4 pa_load_descs(const GqaArgs &a, uint32_t t0, uint32_t t1, uint32_t lane) {
+    const uint32_t t = t0 + lane;
+    const uint32_t p = t < t1 ? t * 16 / a.page_tokens : a.page_count;
+    const uint4 d = ((const uint4 *)a.desc)[p < a.page_count ? p : 0];
+    return p < a.page_count ? d : make_uint4(0, 0, 0, 0);
+}
+
+// Tile k of the wave's range (k wave-uniform) from the descriptor registers.
+__device__ __forceinline__ PaTile pa_tile_of(const GqaArgs &a, const uint4 &d, uint32_t k) {
+    const uint32_t kk = k < 64 ? k : 0;
+    const uint32_t prec = __builtin_amdgcn_readlane(d.x, kk), slot = __builtin_amdgcn_readlane(d.y, kk);
+    const uint32_t cnt = __builtin_amdgcn_readlane(d.z, kk), first = __builtin_amdgcn_readlane(d.w, kk);
+    PaTile T;
+    T.first = first;
+    T.count = k < 64 ? cnt : 0u;
+    T.q4 = prec != 0;
+    T.token_bytes = T.q4 ? a.q4_token_bytes : a.q2_token_bytes;
+    T.base = T.q4 ? a.q4 + (size_t)slot * a.q4_page_bytes : a.q2 + (size_t)slot * a.q2_page_bytes;
+    return T;
+}
+
+// Max over lanes l and l ^ 16 / l ^ 32 with permlane swaps (VALU, no LDS trip).
+__device__ __forceinline__ float pa_max_x16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                    false, false);
+    return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+__device__ __forceinline__ float pa_max_x32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                    false, false);
+    return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+// Max over the four lanes of a 16-lane row that share lane % 4 (DPP row rotations by 4 and 8).
+__device__ __forceinline__ float pa_max_rot48(float v) {
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false)));
+    return v;
+}
+
+__device__ __forceinline__ pa_h2 pa_as_h2(uint32_t x) { return __builtin_bit_cast(pa_h2, x); }
+__device__ __forceinline__ uint32_t pa_pk(float x, float y) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x, y));
+}
+
+template <int R, class LDS>
+__device__ __forceinline__ void pa_tile16(const GqaArgs &a, LDS &L, const int8_t *qb, uint32_t wave, uint32_t tb, uint32_t h,
+                                          uint32_t li, uint32_t lg, const PaTile &T, const uint32_t *stage,
+                                          PaState<R> &st) {
+    const uint32_t lane = 16 * lg + li;
+    const bool q4 = T.q4 != 0;
+    bool present[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) present[c] = pa_present(a, T, tb + 4 * lg + c);
+    // Operands from the stage (rows: tokens; K run at dword 0, V run at 34).
+    const uint32_t bs = q4 ? 34u : 18u;
+    PaK rk;
+    pa_k_from_stage(stage + li * PA_SROW, lg, q4, pa_present(a, T, tb + li), rk);
+    uint32_t vw[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t *vr = stage + (4 * lg + i) * PA_SROW + 34;
+#pragma unroll
+        for (int b = 0; b < 4; b++) vw[b][i] = pa_s32(vr, (b * bs + 2 + (q4 ? 2 * li : li)) & ~3u);
+    }
+    // (absent tokens were staged as zeros: zero codes and scales)
+    const uint32_t vsb = pa_s16(stage + (4 * lg + (li >> 2)) * PA_SROW + 34, (li & 3) * bs);
+    {   // K block scale of (token li, block lg) for the score epilogue
+        const uint32_t kind = pa_kind(rk.meta);
+        const float sc = pa_half(rk.meta & 0xffffu);
+        L.scl[wave][li][lg] = kind == 2 ? sc * (1.0f / 15.0f) : (kind == 1 ? sc * (1.0f / 3.0f) : 0.0f);
+    }
+    int32_t Eb[4];  // the tile's exponent field per V block
+    {   // V: 2 s / K of (token 4 lg + (li >> 2), block li & 3), staged unscaled;
+        // the block maxima reduce on the VALU meanwhile.
+        const float ws = pa_half(vsb) * (q4 ? 2.0f / 15.0f : 2.0f / 3.0f);
+        L.vws[wave][4 * lg + (li >> 2)][li & 3] = ws;
+        const float mx = pa_max_x32(pa_max_x16(pa_max_rot48(ws)));
+        int ex = 0;
+        frexpf(mx, &ex);  // mx < 2^ex: B = P * ws * 2^(25 - E) < 2^14
+        const int E = min(30, max(1, 11 + ex));
+#pragma unroll
+        for (int b = 0; b < 4; b++) Eb[b] = __builtin_amdgcn_readlane(E, b);  // lane b holds block b's
+    }
+    pa_i4 ak[4];
+    {   // absent tokens staged as zeros: unpack with the tile-uniform precision
+        PaK ku = rk;
+        ku.meta = (rk.meta & 0xfffffu) | ((q4 ? 2u : 1u) << 20);
+        pa_k_operands(ku, ak);
+    }
+    __builtin_amdgcn_wave_barrier();
+    float4 f[4];   // K block scales of tokens tb + 4 lg + c
+    float4 wv[4];  // V: 2 s / K * 2^(25 - E) of tokens tb + 4 lg + c, per block
+    float fe[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) fe[b] = ldexpf(1.0f, 25 - Eb[b]);
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        f[c] = *(const float4 *)&L.scl[wave][4 * lg + c][0];
+        const float4 w = *(const float4 *)&L.vws[wave][4 * lg + c][0];
+        wv[c] = make_float4(w.x * fe[0], w.y * fe[1], w.z * fe[2], w.w * fe[3]);
+    }
+    // Scores, one block at a time: T = sum X (2c - K) = 2 sum(X c) - K sum X,
+    // exact in 32-bit modular arithmetic (|T| < 2^31 although 2 sum(X c) may wrap).
+    const uint32_t kq = T.q4 ? 15u : 3u;
+    float s[R][4];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        uint32_t off = (16 * r + li) * PA_QB + lg * 16;
+        asm volatile("" : "+v"(off));
+#pragma unroll
+        for (int c = 0; c < 4; c++) s[r][c] = 0.0f;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            pa_i4 acc[3];
+#pragma unroll
+            for (int limb = 0; limb < 3; limb++) {
+                const pa_i4 qv = *(const pa_i4 *)(qb + limb * R * 16 * PA_QB + off + 64 * b);
+                acc[limb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ak[b], qv, pa_i4{0, 0, 0, 0}, 0, 0, 0);
+            }
+            const uint32_t kx = kq * (uint32_t)st.xst[r][b];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const uint32_t U = (uint32_t)acc[0][c] + ((uint32_t)acc[1][c] << 8) + ((uint32_t)acc[2][c] << 16);
+                const int32_t t = (int32_t)(2u * U - kx);
+                const float fb = b == 0 ? f[c].x : b == 1 ? f[c].y : b == 2 ? f[c].z : f[c].w;
+                s[r][c] = fmaf(fb * st.qscale[r][b], (float)t, s[r][c]);
+            }
+        }
+    }
+    float p[R][4];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        float sc[4];
+        float mt = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int32_t j = (int32_t)(tb + 4 * lg + c);
+            sc[c] = present[c] && j <= st.lim[r] ? s[r][c] * a.scale : -INFINITY;
+            mt = fmaxf(mt, sc[c]);
+        }
+        mt = pa_max_x32(pa_max_x16(mt));
+        const float mn = fmaxf(st.m[r], mt);
+        float alpha = 1.0f;
+        if (mn == -INFINITY) {
+            p[r][0] = p[r][1] = p[r][2] = p[r][3] = 0.0f;
+        } else {
+            alpha = expf(st.m[r] - mn);
+#pragma unroll
+            for (int c = 0; c < 4; c++) p[r][c] = expf(sc[c] - mn);
+        }
+        st.den[r] = st.den[r] * alpha + ((p[r][0] + p[r][1]) + (p[r][2] + p[r][3]));
+        st.m[r] = mn;
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+            for (int j = 0; j < 16; j++) st.o[r][j] *= alpha;
+#pragma unroll
+            for (int b = 0; b < 4; b++) st.corr[r][b] *= alpha;
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        // B operands (hi, lo) for block b, and the "- s" sums.
+        pa_h4 bh[R], bl[R];
+        const float kh = ldexpf(q4 ? 7.5f : 1.5f, Eb[b] - 25);  // K / 2 * 2^(E - 25): B back to P * s
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            float pb[4];
+            pb[0] = p[r][0] * wv[0][b];
+            pb[1] = p[r][1] * wv[1][b];
+            pb[2] = p[r][2] * wv[2][b];
+            pb[3] = p[r][3] * wv[3][b];
+            const uint32_t h01 = pa_pk(pb[0], pb[1]), h23 = pa_pk(pb[2], pb[3]);
+            const pa_h2 H01 = pa_as_h2(h01), H23 = pa_as_h2(h23);
+            const uint32_t l01 = pa_pk(pb[0] - (float)H01[0], pb[1] - (float)H01[1]);
+            const uint32_t l23 = pa_pk(pb[2] - (float)H23[0], pb[3] - (float)H23[1]);
+            bh[r] = __builtin_bit_cast(pa_h4, (uint64_t)h01 | ((uint64_t)h23 << 32));
+            bl[r] = __builtin_bit_cast(pa_h4, (uint64_t)l01 | ((uint64_t)l23 << 32));
+            st.corr[r][b] = fmaf((pb[0] + pb[1]) + (pb[2] + pb[3]), kh, st.corr[r][b]);
+        }
+        // A operands: codes of tokens (0, 1) and (2, 3) side by side in the two halves.
+        const uint32_t o = (b * bs + 2 + (q4 ? 2 * li : li)) & 3u;
+        const uint32_t sel = q4 ? (o | ((o + 1) << 8) | ((o + 4) << 16) | ((o + 5) << 24))
+                                : (o | (0x0cu << 8) | ((o + 4) << 16) | (0x0cu << 24));
+        const uint32_t y01 = __builtin_amdgcn_perm(vw[b][1], vw[b][0], sel);
+        const uint32_t y23 = __builtin_amdgcn_perm(vw[b][3], vw[b][2], sel);
+        const uint32_t E = (uint32_t)Eb[b];
+        uint32_t magic = (E << 10) | (E << 26);
+        asm volatile("" : "+v"(magic));  // a VGPR operand of v_and_or_b32
+        const _Float16 one = (_Float16)ldexpf(1.0f, (int)E - 15);
+        const pa_h2 bias = pa_h2{-one, -one};
+        pa_h4 av[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            // Q4 nibble c sits at bit 4c: shifted to bit 2c like the Q2 crumb.
+            const uint32_t x01 = q4 ? y01 >> (2 * c) : y01, x23 = q4 ? y23 >> (2 * c) : y23;
+            const uint32_t m = (q4 ? 0x000F000Fu : 0x00030003u) << (2 * c);
+            const pa_h2 a01 = pa_as_h2(pa_and_or(x01, m, magic)) + bias;
+            const pa_h2 a23 = pa_as_h2(pa_and_or(x23, m, magic)) + bias;
+            av[c] = pa_h4{a01[0], a01[1], a23[0], a23[1]};
+        }
+        // hi parts of the four chunks, then the lo parts: no MFMA waits on the one before.
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                st.o[r][4 * b + c] = __builtin_amdgcn_mfma_f32_16x16x16f16(av[c], bh[r], st.o[r][4 * b + c], 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                st.o[r][4 * b + c] = __builtin_amdgcn_mfma_f32_16x16x16f16(av[c], bl[r], st.o[r][4 * b + c], 0, 0, 0);
+    }
+}
+
+template <int R>
+__device__ __forceinline__ void pa_prep_queries(const GqaArgs &a, uint32_t h, int8_t *qb, float (*qsc)[4],
+                                                int32_t (*xs)[4][3]) {
     // Query fixed point per 64-dim block: X = rint(q 2^E) with |X| <= 2^21
     // (2^E from the block's max |q|), split into three balanced int8 limbs
     // X = l0 + 256 l1 + 65536 l2, dims reordered to the K operand's order
@@ -441,49 +782,226 @@ __device__ __forceinline__ void paged_gqa_partial(const GqaArgs &a) {
     // the limb sums for the score epilogue.
     for (uint32_t i = threadIdx.x; i < R * 16 * 16; i += 256) {
         // Four consecutive lanes share one (query, block), a quarter of it each.
-        int8_t *qb = (int8_t *)L.main;
         const uint32_t qi = i / 16, b = (i / 4) % 4, part = i % 4;
-        const float *q = nullptr;
-        float mx = 0.0f;
-        if (qi < a.queries) {
-            const uint32_t t = qi / a.group, g = qi - t * a.group;
-            q = a.query + ((size_t)t * a.query_heads + h * a.group + g) * PA_HD + 64 * b;
-            for (int d = 0; d < 16; d++) mx = fmaxf(mx, fabsf(q[16 * part + d]));
+        // The quarter's 16 values in registers (one load each; zeros past the queries).
+        const bool valid = qi < a.queries;
+        const uint32_t t = valid ? qi / a.group : 0, g = valid ? qi - t * a.group : 0;
+        const float4 *qp = (const float4 *)(a.query + ((size_t)t * a.query_heads + h * a.group + g) * PA_HD + 64 * b +
+                                            16 * part);
+        float qv[16];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float4 v4 = qp[k];
+            qv[4 * k] = valid ? v4.x : 0.0f;
+            qv[4 * k + 1] = valid ? v4.y : 0.0f;
+            qv[4 * k + 2] = valid ? v4.z : 0.0f;
+            qv[4 * k + 3] = valid ? v4.w : 0.0f;
         }
+        float mx = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 16; d++) mx = fmaxf(mx, fabsf(qv[d]));
         mx = fmaxf(mx, __shfl_xor(mx, 1));
         mx = fmaxf(mx, __shfl_xor(mx, 2));
         int ex = 0;
         frexpf(mx, &ex);  // mx < 2^ex
         const float e = mx > 0.0f ? ldexpf(1.0f, 21 - ex) : 0.0f;
         int32_t sums[3] = {0, 0, 0};
+        // The quarter's dims land in 16 consecutive bytes of each limb row
+        // (dims reordered within each 8 as 0,2,4,6,1,3,5,7): one 16-byte store per limb.
+        uint32_t packed[3][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
         for (int dd = 0; dd < 16; dd++) {
-            const int d = 16 * part + dd;
-            const int32_t X = q ? (int32_t)rintf(q[d] * e) : 0;
+            const int32_t X = (int32_t)rintf(qv[dd] * e);
             const int32_t l0 = ((X + 128) & 255) - 128;
             const int32_t X1 = (X - l0) >> 8;
             const int32_t l1 = ((X1 + 128) & 255) - 128;
             const int32_t l2 = (X1 - l1) >> 8;
-            const uint32_t w = d % 8, pos = 64 * b + (d / 8) * 8 + (w % 2) * 4 + w / 2;
-            qb[(0 * R * 16 + qi) * PA_QB + pos] = (int8_t)l0;
-            qb[(1 * R * 16 + qi) * PA_QB + pos] = (int8_t)l1;
-            qb[(2 * R * 16 + qi) * PA_QB + pos] = (int8_t)l2;
+            const uint32_t w = dd % 8, local = (dd / 8) * 8 + (w % 2) * 4 + w / 2;
+            packed[0][local / 4] |= (uint32_t)(l0 & 255) << (8 * (local % 4));
+            packed[1][local / 4] |= (uint32_t)(l1 & 255) << (8 * (local % 4));
+            packed[2][local / 4] |= (uint32_t)(l2 & 255) << (8 * (local % 4));
             sums[0] += l0;
             sums[1] += l1;
             sums[2] += l2;
         }
+#pragma unroll
+        for (int l = 0; l < 3; l++)
+            *(uint4 *)(qb + (l * R * 16 + qi) * PA_QB + 64 * b + 16 * part) =
+                make_uint4(packed[l][0], packed[l][1], packed[l][2], packed[l][3]);
 #pragma unroll
         for (int l = 0; l < 3; l++) {
             sums[l] += __shfl_xor(sums[l], 1);
             sums[l] += __shfl_xor(sums[l], 2);
         }
         if (part == 0) {
-            L.qsc[qi][b] = mx > 0.0f ? ldexpf(1.0f, ex - 21) : 0.0f;
-            L.xs[qi][b][0] = sums[0];
-            L.xs[qi][b][1] = sums[1];
-            L.xs[qi][b][2] = sums[2];
+            qsc[qi][b] = mx > 0.0f ? ldexpf(1.0f, ex - 21) : 0.0f;
+            xs[qi][b][0] = sums[0];
+            xs[qi][b][1] = sums[1];
+            xs[qi][b][2] = sums[2];
         }
     }
+}
+
+
+// LDS of the page-aligned kernel: query limbs and the per-wave K/V stages
+// while tiles run, overlaid afterwards by the merge area of waves 1..3.
+template <int R>
+struct PaLds16 {
+    static constexpr uint32_t limb_bytes = 3 * R * 16 * PA_QB;
+    static constexpr uint32_t merge_floats = 3 * R * 16 * PA_QS + 6 * R * 16;
+    union {
+        struct {
+            int8_t limbs[limb_bytes];
+            uint32_t stage[4][16 * PA_SROW];
+        } run;
+        float merge[merge_floats];
+    } u;
+    float scl[4][16][4];       // [wave][token of tile][block]: K scale / 15 (Q4) or / 3 (Q2)
+    float vws[4][16][4];       // [wave][token][V block]: 2 V scale / K
+    float qsc[R * 16][4];      // [query][block]: 2^-E of the query's fixed point
+    int32_t xs[R * 16][4][3];  // [query][block][limb]: limb sums
+};
+
+// grid (splits, kv heads), 256 threads; four waves take contiguous runs of
+// tiles_per_wave (<= 64) page-aligned tiles. Lane (li, lg) ends with O^T of
+// query 16 r + li at dims 64 b + 16 lg + 4 i + c in o[r][4 b + c][i].
+template <int R>
+__device__ __forceinline__ void paged_gqa_partial16(const GqaArgs &a) {
+    __shared__ PaLds16<R> L;
+    const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t li = lane & 15, lg = lane >> 4;
+    const uint32_t h = blockIdx.y, split = blockIdx.x;
+    const uint32_t gw = split * 4 + wave;
+    const uint32_t t0 = gw * a.tiles_per_wave;
+    const uint32_t t1 = min(t0 + a.tiles_per_wave, a.tiles);
+    // The wave's page descriptors load together with the queries.
+    const uint4 dsc = pa_load_descs(a, t0, t1, lane);
+    pa_prep_queries<R>(a, h, L.u.run.limbs, L.qsc, L.xs);
+    PaState<R> st;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const uint32_t qi = 16 * r + li;
+        st.lim[r] = qi < a.queries ? (int32_t)(a.tokens - a.rows + qi / a.group) : -1;
+        st.m[r] = -INFINITY;
+        st.den[r] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) st.o[r][j] = pa_v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    // The first tile's loads stay in flight across the (LDS-only) barrier.
+    PaStage sg;
+    PaTile PA = pa_tile_of(a, dsc, 0);
+    uint32_t *stage = L.u.run.stage[wave];
+    pa_issue_stage(a, PA, t0 * 16, h, lane, sg);
+    lds_barrier();
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            st.qscale[r][b] = L.qsc[16 * r + li][b];
+            st.xst[r][b] = L.xs[16 * r + li][b][0] + 256 * L.xs[16 * r + li][b][1] + 65536 * L.xs[16 * r + li][b][2];
+            st.corr[r][b] = 0.0f;
+        }
+    // Tile k computes from the stage while tile k + 1's loads are in flight.
+    for (uint32_t tile = t0; tile < t1; tile++) {
+        pa_stage_write(stage, lane, PA.q4 != 0, sg);
+        const PaTile PN = pa_tile_of(a, dsc, tile + 1 - t0);
+        pa_issue_stage(a, PN, (tile + 1) * 16, h, lane, sg);
+        pa_tile16<R>(a, L, L.u.run.limbs, wave, tile * 16, h, li, lg, PA, stage, st);
+        PA = PN;
+    }
+    // O = C 4^-c - sum P s (the latter summed over the four lane groups' tokens);
+    // denominators likewise.
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            float cs = st.corr[r][b];
+            cs += __shfl_xor(cs, 16);
+            cs += __shfl_xor(cs, 32);
+#pragma unroll
+            for (int c = 0; c < 4; c++) st.o[r][4 * b + c] = st.o[r][4 * b + c] * (1.0f / (float)(1u << (2 * c))) - cs;
+        }
+        st.den[r] += __shfl_xor(st.den[r], 16);
+        st.den[r] += __shfl_xor(st.den[r], 32);
+    }
+    __syncthreads();  // the stages and limbs are dead: the LDS becomes the merge area
+
+    // One merge stage: waves 1..3 publish, wave 0 absorbs them in wave order.
+    float *xo = L.u.merge;                      // [3][R * 16][PA_QS]
+    float *xm = L.u.merge + 3 * R * 16 * PA_QS;  // [3][R * 16]
+    float *xd = xm + 3 * R * 16;                 // [3][R * 16]
+    if (wave != 0) {
+        const uint32_t slot = wave - 1;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t row = slot * R * 16 + 16 * r + li;
+            if (lg == 0) {
+                xm[row] = st.m[r];
+                xd[row] = st.den[r];
+            }
+#pragma unroll
+            for (int b = 0; b < 4; b++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    *(float4 *)&xo[row * PA_QS + 64 * b + 16 * lg + 4 * i] =
+                        make_float4(st.o[r][4 * b][i], st.o[r][4 * b + 1][i], st.o[r][4 * b + 2][i], st.o[r][4 * b + 3][i]);
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    // Partial layout: [kv head][split][query][PA_HD]; stats [kv head][split][query][2].
+    const size_t base = ((size_t)h * a.splits + split) * a.queries;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const uint32_t qi = 16 * r + li;
+        float mm = st.m[r];
+#pragma unroll
+        for (int w = 0; w < 3; w++) mm = fmaxf(mm, xm[w * R * 16 + 16 * r + li]);
+        float f[4];
+        f[0] = mm == -INFINITY ? 0.0f : expf(st.m[r] - mm);
+        float den = st.den[r] * f[0];
+#pragma unroll
+        for (int w = 0; w < 3; w++) {
+            const uint32_t row = w * R * 16 + 16 * r + li;
+            f[w + 1] = mm == -INFINITY ? 0.0f : expf(xm[row] - mm);
+            den += xd[row] * f[w + 1];
+        }
+        float *dst = a.part_out + (base + qi) * PA_HD;
+#pragma unroll
+        for (int b = 0; b < 4; b++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t d = 64 * b + 16 * lg + 4 * i;
+                float4 v = make_float4(st.o[r][4 * b][i] * f[0], st.o[r][4 * b + 1][i] * f[0],
+                                       st.o[r][4 * b + 2][i] * f[0], st.o[r][4 * b + 3][i] * f[0]);
+#pragma unroll
+                for (int w = 0; w < 3; w++) {
+                    const float4 x = *(const float4 *)&xo[(w * R * 16 + 16 * r + li) * PA_QS + d];
+                    v.x += x.x * f[w + 1];
+                    v.y += x.y * f[w + 1];
+                    v.z += x.z * f[w + 1];
+                    v.w += x.w * f[w + 1];
+                }
+                if (qi < a.queries) *(float4 *)&dst[d] = v;
+            }
+        if (qi < a.queries && lg == 0) {
+            a.part_stats[2 * (base + qi)] = mm;
+            a.part_stats[2 * (base + qi) + 1] = den;
+        }
+    }
+}
+
+
+template <int R>
+__device__ __forceinline__ void paged_gqa_partial(const GqaArgs &a) {
+    __shared__ PaLds<R> L;
+    const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t li = lane & 15, lg = lane >> 4;
+    const uint32_t h = blockIdx.y, split = blockIdx.x;
+    const uint32_t gw = split * 4 + wave;
+    const uint32_t t0 = gw * a.tiles_per_wave;
+    const uint32_t t1 = min(t0 + a.tiles_per_wave, a.tiles);
+    pa_prep_queries<R>(a, h, (int8_t *)L.main, L.qsc, L.xs);
     PaState<R> st;
 #pragma unroll
     for (int r = 0; r < R; r++) {
@@ -502,11 +1020,10 @@ __device__ __forceinline__ void paged_gqa_partial(const GqaArgs &a) {
             st.qscale[r][b] = L.qsc[16 * r + li][b];
 #pragma unroll
             for (int limb = 0; limb < 3; limb++) st.xsum[r][b][limb] = L.xs[16 * r + li][b][limb];
+            st.xst[r][b] = st.xsum[r][b][0] + 256 * st.xsum[r][b][1] + 65536 * st.xsum[r][b][2];
+            st.corr[r][b] = 0.0f;
         }
 
-    const uint32_t gw = split * 4 + wave;
-    const uint32_t t0 = gw * a.tiles_per_wave;
-    const uint32_t t1 = min(t0 + a.tiles_per_wave, a.tiles);
     if constexpr (R == 1) {
         // Two tiles per iteration: the second tile's loads are in flight while
         // the first computes (R = 2 has no registers to spare for it).
@@ -609,18 +1126,26 @@ extern "C" __global__ __launch_bounds__(256, 2) void ctox_paged_gqa_partial_r1_g
 extern "C" __global__ __launch_bounds__(256, 1) void ctox_paged_gqa_partial_r2_gfx950(GqaArgs a) {
     paged_gqa_partial<2>(a);
 }
+// Page-aligned tiles (page_tokens % 16 == 0): P.V on f16 MFMA.
+extern "C" __global__ __launch_bounds__(256, 2) void ctox_paged_gqa_partial16_r1_gfx950(GqaArgs a) {
+    paged_gqa_partial16<1>(a);
+}
+extern "C" __global__ __launch_bounds__(256, 1) void ctox_paged_gqa_partial16_r2_gfx950(GqaArgs a) {
+    paged_gqa_partial16<2>(a);
+}
 
 #define PA_MAX_SPLITS 1024
 
-// grid (queries, kv heads), 256 threads. Split weights exp(m_s - M) are formed
-// once in LDS; each wave then sums every fourth split over all 256 dims
-// (a float4 per lane) and the four wave sums are added in a fixed order.
+// grid (queries, kv heads, 4 dim quarters), 256 threads. Split weights
+// exp(m_s - M) are formed once in LDS; thread (g = tid / 16, c = tid % 16)
+// sums the float4 at dims 64 quarter + 4 c over splits g, g + 16, ..., and
+// the 16 split groups are added in a fixed order.
 // out[row][q head][dim] with q head = kv head * group + member.
 extern "C" __global__ __launch_bounds__(256) void ctox_paged_gqa_combine_gfx950(GqaArgs a) {
     __shared__ float wgt[PA_MAX_SPLITS];
     __shared__ float red[4];
-    __shared__ float4 acc4[4][64];
-    const uint32_t qi = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    __shared__ float4 acc4[16][16];
+    const uint32_t qi = blockIdx.x, h = blockIdx.y, quarter = blockIdx.z, tid = threadIdx.x;
     const uint32_t lane = tid & 63, wave = tid >> 6;
     const size_t base = (size_t)h * a.splits * a.queries + qi;  // + s * queries
     float mx = -INFINITY;
@@ -644,23 +1169,31 @@ extern "C" __global__ __launch_bounds__(256) void ctox_paged_gqa_combine_gfx950(
     if (lane == 0) red[wave] = den;
     __syncthreads();
     den = (red[0] + red[1]) + (red[2] + red[3]);
+    const uint32_t g = tid >> 4, c = tid & 15;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll 4
-    for (uint32_t s = wave; s < a.splits; s += 4) {
+#pragma unroll 8
+    for (uint32_t s = g; s < a.splits; s += 16) {
         const float f = wgt[s];
-        const float4 v = ((const float4 *)(a.part_out + (base + (size_t)s * a.queries) * PA_HD))[lane];
+        const float4 v = ((const float4 *)(a.part_out + (base + (size_t)s * a.queries) * PA_HD + 64 * quarter))[c];
         acc.x += v.x * f;
         acc.y += v.y * f;
         acc.z += v.z * f;
         acc.w += v.w * f;
     }
-    acc4[wave][lane] = acc;
+    acc4[g][c] = acc;
     __syncthreads();
-    if (wave != 0) return;
-    const float4 a0 = acc4[0][lane], a1 = acc4[1][lane], a2 = acc4[2][lane], a3 = acc4[3][lane];
+    if (tid >= 16) return;
+    float4 sum = acc4[0][tid];
+#pragma unroll
+    for (int k = 1; k < 16; k++) {
+        const float4 v = acc4[k][tid];
+        sum.x += v.x;
+        sum.y += v.y;
+        sum.z += v.z;
+        sum.w += v.w;
+    }
     const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-    const uint32_t t = qi / a.group, g = qi - t * a.group;
-    float4 *out = (float4 *)(a.out + ((size_t)t * a.query_heads + h * a.group + g) * PA_HD);
-    out[lane] = make_float4(((a0.x + a1.x) + (a2.x + a3.x)) * inv, ((a0.y + a1.y) + (a2.y + a3.y)) * inv,
-                            ((a0.z + a1.z) + (a2.z + a3.z)) * inv, ((a0.w + a1.w) + (a2.w + a3.w)) * inv);
+    const uint32_t t = qi / a.group, gm = qi - t * a.group;
+    float4 *out = (float4 *)(a.out + ((size_t)t * a.query_heads + h * a.group + gm) * PA_HD + 64 * quarter);
+    out[tid] = make_float4(sum.x * inv, sum.y * inv, sum.z * inv, sum.w * inv);
 }

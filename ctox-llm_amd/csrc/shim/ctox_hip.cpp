@@ -142,7 +142,7 @@ struct ctox_hip_backend {
                   gdn_scan = nullptr, gdn_chunk_prep = nullptr, gdn_chunk_scan = nullptr, gates = nullptr,
                   repeat = nullptr, partials = nullptr, argmax_final = nullptr, verify = nullptr, decide = nullptr,
                   pick_sums = nullptr, pick_final = nullptr, rms = nullptr, swiglu = nullptr, sgate = nullptr,
-                  conv = nullptr, rope = nullptr, kv_pack = nullptr, kv_demote = nullptr, gqa_part[2] = {},
+                  conv = nullptr, rope = nullptr, kv_pack = nullptr, kv_demote = nullptr, gqa_part[2] = {}, gqa_part16[2] = {},
                   gqa_combine = nullptr, fill = nullptr, embed = nullptr, norm_rows = nullptr, attn_gate = nullptr,
                   swiglu_rows = nullptr, copy_rows = nullptr, write_words = nullptr, norm_prep = nullptr,
                   prep_x = nullptr;
@@ -625,6 +625,8 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->kv_pack, "ctox_kv_pack_q4_gfx950"},    {&b->kv_demote, "ctox_kv_demote_gfx950"},
                {&b->gqa_part[0], "ctox_paged_gqa_partial_r1_gfx950"},
                {&b->gqa_part[1], "ctox_paged_gqa_partial_r2_gfx950"},
+               {&b->gqa_part16[0], "ctox_paged_gqa_partial16_r1_gfx950"},
+               {&b->gqa_part16[1], "ctox_paged_gqa_partial16_r2_gfx950"},
                {&b->gqa_combine, "ctox_paged_gqa_combine_gfx950"},
                {&b->fill, "ctox_fill_random_gfx950"},      {&b->embed, "ctox_embed_rows_gfx950"},
                {&b->norm_rows, "ctox_norm_rows_gfx950"},   {&b->attn_gate, "ctox_attn_gate_gfx950"},
@@ -1614,10 +1616,14 @@ extern "C" ctox_status ctox_hip_paged_gqa_device(ctox_hip_backend *b, const floa
               p->page_tokens, p->page_count, (uint32_t)cv, p->q2_token_bytes, p->q4_token_bytes, tiles, tpw, splits,
               p->scale, p->page_tokens % 16 == 0 ? 1u : 0u, 0};
     hipStream_t s = pick_stream(b, stream);
-    st = launch(b->gqa_part[queries > 16 ? 1 : 0], dim3(splits, p->key_value_heads), dim3(256), s, a,
+    // Page-aligned 16-token tiles run P.V on f16 MFMA; other page sizes on the fp32-MFMA kernel.
+    // (its waves hold up to 64 tiles' page descriptors in registers).
+    const bool f16 = p->page_tokens % 16 == 0 && tpw <= 64;
+    hipFunction_t part_fn = f16 ? b->gqa_part16[queries > 16 ? 1 : 0] : b->gqa_part[queries > 16 ? 1 : 0];
+    st = launch(part_fn, dim3(splits, p->key_value_heads), dim3(256), s, a,
                 "ctox_paged_gqa_partial_gfx950");
     if (st) return st;
-    return launch(b->gqa_combine, dim3(queries, p->key_value_heads), dim3(256), s, a, "ctox_paged_gqa_combine_gfx950");
+    return launch(b->gqa_combine, dim3(queries, p->key_value_heads, 4), dim3(256), s, a, "ctox_paged_gqa_combine_gfx950");
 }
 static_assert(sizeof(ctox_paged_kv_descriptor) == sizeof(PagedKvDesc), "page descriptor layout");
 

@@ -111,6 +111,26 @@ def test_paged_attention_matches_oracle(hip, tokens, rows, page, sink, recent):
     attention_case(hip, tokens, rows, page, sink, recent, seed=tokens * 7 + rows)
 
 
+@pytest.mark.parametrize("page", [16, 24])
+def test_paged_attention_value_scale_range(hip, page):
+    say(f"case paged attention value scales 1e-3..1e3 page={page}")
+    # Value blocks whose magnitudes differ by six orders across tokens: the
+    # page-aligned kernel rescales its f16 probability operands per tile.
+    rng = np.random.default_rng(11)
+    tokens, rows = 700, 5
+    dev, ref = make_caches(hip, 720, page, 48, 96)
+    cv = KVH * HD
+    k = rng.standard_normal((tokens, cv)).astype(np.float32)
+    mag = 10.0 ** rng.uniform(-3, 3, (tokens, cv // 64))
+    v = (rng.standard_normal((tokens, cv)) * np.repeat(mag, 64, axis=1)).astype(np.float32)
+    push_both(dev, ref, k, v)
+    q = rng.standard_normal((rows, QH, HD)).astype(np.float32)
+    out = dev.attention(torch.from_numpy(q).cuda(), rows, QH)
+    torch.cuda.synchronize()
+    want = pk.paged_attention(ref, q, rows, QH, KVH, HD).reshape(rows, QH, HD)
+    np.testing.assert_allclose(out.cpu().numpy(), want, rtol=1e-3, atol=1e-4 * float(np.abs(want).max()))
+
+
 def test_paged_attention_peaked_scores(hip):
     say("case paged attention peaked")
     # Large logits make the softmax nearly one-hot; the online max must track it.
