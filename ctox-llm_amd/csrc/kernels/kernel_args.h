@@ -382,6 +382,29 @@ struct KvPackArgs {
     uint64_t q4_page_bytes;
 };
 
+// Fused attention-layer prep (ctox_attn_prep_gfx950): per-head q/k RMS norm,
+// partial RoPE and the Q4 page append of the new K/V rows.
+#define CTOX_ATTN_PREP_ROWS 8
+struct AttnPrepArgs {
+    const float *proj;       // [rows][proj_stride]: per q head [q, gate] (2 hd), then k [kh hd], v [kh hd]
+    const float *q_norm;     // [hd]
+    const float *k_norm;     // [hd]
+    float *q_out;            // [rows][qh][hd]
+    uint8_t *q4_pages;
+    uint64_t q4_page_bytes;
+    uint64_t position;       // rope position of row 0
+    uint32_t proj_stride;
+    uint32_t qh;
+    uint32_t kh;
+    uint32_t hd;             // 256
+    uint32_t rd;             // rotary dims (even, <= hd)
+    uint32_t q4_token_bytes;
+    float eps;
+    float theta;
+    uint32_t slot[CTOX_ATTN_PREP_ROWS];  // Q4 page slot of row t
+    uint32_t pos[CTOX_ATTN_PREP_ROWS];   // token index of row t inside that page
+};
+
 struct KvDemoteArgs {
     const uint8_t *q4_page;
     uint8_t *q2_page;

@@ -49,11 +49,8 @@ __device__ __forceinline__ float pa_half(uint32_t h) {
 // pack
 // ---------------------------------------------------------------------------
 #pragma clang fp contract(off)
-extern "C" __global__ __launch_bounds__(64) void ctox_kv_pack_q4_gfx950(KvPackArgs a) {
-    const uint32_t lane = threadIdx.x, blk = blockIdx.x, tok = blockIdx.y;
-    const uint32_t idx = blk * 64 + lane;
-    const size_t row = (size_t)tok * a.component_values;
-    const float v = idx < a.component_values ? a.keys[row + idx] : a.values[row + idx - a.component_values];
+// One 64-value block held one value per lane: Q4 codes and fp16 scale at dst.
+__device__ __forceinline__ void pa_pack_q4_block(float v, uint32_t lane, uint8_t *dst) {
     float m = fabsf(v);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
@@ -61,18 +58,25 @@ extern "C" __global__ __launch_bounds__(64) void ctox_kv_pack_q4_gfx950(KvPackAr
     if (m != 0.0f) {
         float n = v / m;  // correctly rounded division (HIP's default for f32)
         n = fminf(1.0f, fmaxf(-1.0f, n));
-        const float sel = n * 7.5f + 7.5f;  // contraction is off in this file: two roundings
+        const float sel = n * 7.5f + 7.5f;  // contraction is off in this region: two roundings
         code = (uint32_t)fminf(15.0f, fmaxf(0.0f, roundf(sel)));
     }
     const uint32_t hi = __shfl_down(code, 1);
-    uint8_t *dst = a.q4_pages + (size_t)a.physical_slot * a.q4_page_bytes +
-                   (size_t)(a.first_token_in_page + tok) * a.q4_token_bytes + (size_t)blk * 34;
     if ((lane & 1) == 0) dst[2 + lane / 2] = (uint8_t)(code | (hi << 4));
     if (lane == 0) {
         const uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)m);  // round to nearest even
         dst[0] = (uint8_t)h;
         dst[1] = (uint8_t)(h >> 8);
     }
+}
+
+extern "C" __global__ __launch_bounds__(64) void ctox_kv_pack_q4_gfx950(KvPackArgs a) {
+    const uint32_t lane = threadIdx.x, blk = blockIdx.x, tok = blockIdx.y;
+    const uint32_t idx = blk * 64 + lane;
+    const size_t row = (size_t)tok * a.component_values;
+    const float v = idx < a.component_values ? a.keys[row + idx] : a.values[row + idx - a.component_values];
+    pa_pack_q4_block(v, lane, a.q4_pages + (size_t)a.physical_slot * a.q4_page_bytes +
+                                  (size_t)(a.first_token_in_page + tok) * a.q4_token_bytes + (size_t)blk * 34);
 }
 #pragma clang fp contract(fast)
 
@@ -1196,4 +1200,66 @@ extern "C" __global__ __launch_bounds__(256) void ctox_paged_gqa_combine_gfx950(
     const uint32_t t = qi / a.group, gm = qi - t * a.group;
     float4 *out = (float4 *)(a.out + ((size_t)t * a.query_heads + h * a.group + gm) * PA_HD + 64 * quarter);
     out[tid] = make_float4(sum.x * inv, sum.y * inv, sum.z * inv, sum.w * inv);
+}
+
+// ---------------------------------------------------------------------------
+// Fused attention-layer prep: grid (qh + 2 kh, rows), one wave per (head, row).
+//   q head: RMS norm with q_norm ((1 + w), Q/src/reference.rs:38-62, as
+//           ctox_norm_rows_gfx950 sums it for a 256-wide row), partial RoPE
+//           (Q/src/reference.rs:115-155, as ctox_rope_gfx950), written to q_out;
+//   k head: the same with k_norm, then its four 64-value blocks packed into
+//           the row's Q4 page slot (as ctox_kv_pack_q4_gfx950);
+//   v head: packed as it is.
+// Replaces the norm, norm, rope, copy and pack launches of an attention
+// layer's K/V append (Q/src/decoder.rs:687-800, Q/src/kv_cache.rs:200-206).
+// ---------------------------------------------------------------------------
+extern "C" __global__ __launch_bounds__(64) void ctox_attn_prep_gfx950(AttnPrepArgs a) {
+    __shared__ float hs[PA_HD];
+    const uint32_t job = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    const bool is_q = job < a.qh, is_k = !is_q && job < a.qh + a.kh;
+    const uint32_t kk = is_q ? job : is_k ? job - a.qh : job - a.qh - a.kh;
+    const float *row = a.proj + (size_t)t * a.proj_stride;
+    const float *x = is_q ? row + (size_t)kk * 2 * a.hd
+                          : row + (size_t)2 * a.qh * a.hd + (is_k ? 0 : (size_t)a.kh * a.hd) + (size_t)kk * a.hd;
+    float v[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) v[k] = x[lane + 64 * k];
+    if (is_q || is_k) {
+        float s = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) s += v[k] * v[k];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+        const float inv = 1.0f / sqrtf(s / (float)a.hd + a.eps);
+        const float *w = is_q ? a.q_norm : a.k_norm;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float n = v[k] * inv;
+            hs[lane + 64 * k] = n * (1.0f + w[lane + 64 * k]);
+        }
+        __syncthreads();
+        const uint32_t half = a.rd / 2;
+        for (uint32_t i = lane; i < half; i += 64) {
+            const float invf = powf(a.theta, -((float)(2 * i)) / (float)a.rd);
+            const float angle = (float)(a.position + t) * invf;  // u64 -> f32, as `position as f32`
+            const float cs = cosf(angle), sn = sinf(angle);
+            const float l = hs[i], r = hs[i + half];
+            hs[i] = l * cs - r * sn;
+            hs[i + half] = r * cs + l * sn;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] = hs[lane + 64 * k];
+        if (is_q) {
+            float *q = a.q_out + ((size_t)t * a.qh + kk) * a.hd;
+#pragma unroll
+            for (int k = 0; k < 4; k++) q[lane + 64 * k] = v[k];
+            return;
+        }
+    }
+    // Blocks of this head inside the token: K blocks [0, 4 kh), V blocks after.
+    uint8_t *tok = a.q4_pages + (size_t)a.slot[t] * a.q4_page_bytes + (size_t)a.pos[t] * a.q4_token_bytes;
+    const uint32_t blk0 = (is_k ? 0u : 4u * a.kh) + 4 * kk;
+#pragma unroll
+    for (int k = 0; k < 4; k++) pa_pack_q4_block(v[k], lane, tok + (size_t)(blk0 + k) * 34);
 }

@@ -142,7 +142,7 @@ struct ctox_hip_backend {
                   gdn_scan = nullptr, gdn_chunk_prep = nullptr, gdn_chunk_scan = nullptr, gates = nullptr,
                   repeat = nullptr, partials = nullptr, argmax_final = nullptr, verify = nullptr, decide = nullptr,
                   pick_sums = nullptr, pick_final = nullptr, rms = nullptr, swiglu = nullptr, sgate = nullptr,
-                  conv = nullptr, rope = nullptr, kv_pack = nullptr, kv_demote = nullptr, gqa_part[2] = {}, gqa_part16[2] = {},
+                  conv = nullptr, rope = nullptr, kv_pack = nullptr, attn_prep = nullptr, kv_demote = nullptr, gqa_part[2] = {}, gqa_part16[2] = {},
                   gqa_combine = nullptr, fill = nullptr, embed = nullptr, norm_rows = nullptr, attn_gate = nullptr,
                   swiglu_rows = nullptr, copy_rows = nullptr, write_words = nullptr, norm_prep = nullptr,
                   prep_x = nullptr;
@@ -622,7 +622,7 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->pick_final, "ctox_pick_final_gfx950"},  {&b->rms, "ctox_rms_norm_gfx950"},
                {&b->swiglu, "ctox_swiglu_gfx950"},         {&b->sgate, "ctox_sigmoid_gate_gfx950"},
                {&b->conv, "ctox_conv_update_gfx950"},      {&b->rope, "ctox_rope_gfx950"},
-               {&b->kv_pack, "ctox_kv_pack_q4_gfx950"},    {&b->kv_demote, "ctox_kv_demote_gfx950"},
+               {&b->kv_pack, "ctox_kv_pack_q4_gfx950"}, {&b->attn_prep, "ctox_attn_prep_gfx950"},    {&b->kv_demote, "ctox_kv_demote_gfx950"},
                {&b->gqa_part[0], "ctox_paged_gqa_partial_r1_gfx950"},
                {&b->gqa_part[1], "ctox_paged_gqa_partial_r2_gfx950"},
                {&b->gqa_part16[0], "ctox_paged_gqa_partial16_r1_gfx950"},
@@ -1565,6 +1565,46 @@ extern "C" ctox_status ctox_hip_kv_pack_q4_device(ctox_hip_backend *b, uint8_t *
                  (uint32_t)token_bytes, q4_page_bytes};
     return launch(b->kv_pack, dim3((unsigned)(component_values * 2 / 64), (unsigned)token_count), dim3(64),
                   pick_stream(b, stream), a, "ctox_kv_pack_q4_gfx950");
+}
+
+extern "C" ctox_status ctox_hip_attn_prep_device(ctox_hip_backend *b, const float *d_proj, size_t proj_stride,
+                                                const float *d_q_norm, const float *d_k_norm, size_t rows,
+                                                size_t q_heads, size_t kv_heads, size_t head_dim, size_t rotary_dim,
+                                                uint64_t position, float theta, float eps, uint8_t *d_q4_pages,
+                                                uint32_t q4_page_bytes, const uint32_t *slots,
+                                                const uint32_t *positions_in_page, float *d_q_out, void *stream) {
+    if (!b || !d_proj || !d_q_norm || !d_k_norm || !d_q4_pages || !slots || !positions_in_page || !d_q_out)
+        return fail(CTOX_ERR_SHAPE, "null argument");
+    if (head_dim != 256 || rows == 0 || rows > CTOX_ATTN_PREP_ROWS || q_heads == 0 || kv_heads == 0 ||
+        q_heads + 2 * kv_heads > 65535 || rotary_dim == 0 || rotary_dim % 2 || rotary_dim > head_dim ||
+        proj_stride < 2 * (q_heads + kv_heads) * head_dim || proj_stride > 0xffffffffu || !std::isfinite(theta) ||
+        !(theta > 0.0f) || !std::isfinite(eps) || !(eps > 0.0f))
+        return fail(CTOX_ERR_SHAPE, "attention prep shapes");
+    const uint64_t token_bytes = 2 * kv_heads * head_dim / 64 * 34;
+    AttnPrepArgs a{};
+    for (size_t t = 0; t < rows; t++) {
+        if ((uint64_t)(positions_in_page[t] + 1) * token_bytes > q4_page_bytes)
+            return fail(CTOX_ERR_SHAPE, "attention prep row does not fit its Q4 page");
+        a.slot[t] = slots[t];
+        a.pos[t] = positions_in_page[t];
+    }
+    a.proj = d_proj;
+    a.q_norm = d_q_norm;
+    a.k_norm = d_k_norm;
+    a.q_out = d_q_out;
+    a.q4_pages = d_q4_pages;
+    a.q4_page_bytes = q4_page_bytes;
+    a.position = position;
+    a.proj_stride = (uint32_t)proj_stride;
+    a.qh = (uint32_t)q_heads;
+    a.kh = (uint32_t)kv_heads;
+    a.hd = (uint32_t)head_dim;
+    a.rd = (uint32_t)rotary_dim;
+    a.q4_token_bytes = (uint32_t)token_bytes;
+    a.eps = eps;
+    a.theta = theta;
+    return launch(b->attn_prep, dim3((unsigned)(q_heads + 2 * kv_heads), (unsigned)rows), dim3(64),
+                  pick_stream(b, stream), a, "ctox_attn_prep_gfx950");
 }
 
 extern "C" ctox_status ctox_hip_kv_demote_device(ctox_hip_backend *b, const uint8_t *d_q4_page, uint8_t *d_q2_page,

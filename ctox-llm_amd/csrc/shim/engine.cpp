@@ -256,11 +256,11 @@ ctox_status cache_upload(ctox_hip_engine *e, Cache &c) {
     return CTOX_OK;
 }
 
-// Append `rows` tokens (k, v: [rows][cv] dense) into Q4 pages.
-ctox_status cache_push(ctox_hip_engine *e, Cache &c, const float *k, const float *v, uint32_t rows) {
+// Reserve Q4 page slots for `rows` new tokens: row t goes to slot slots[t] at
+// token index pos[t] of that page (descriptors updated, device copy dirty).
+ctox_status cache_reserve(ctox_hip_engine *e, Cache &c, uint32_t rows, uint32_t *slots, uint32_t *pos) {
     if (c.tokens + rows > e->c.max_tokens) return efail(CTOX_ERR_MEMORY_BUDGET, "paged KV cache is full");
-    uint32_t done = 0;
-    while (done < rows) {
+    for (uint32_t t = 0; t < rows; t++) {
         if (c.pages == 0 || c.desc[c.pages - 1].tokens == e->c.page_tokens) {
             if (c.free_q4.empty()) return efail(CTOX_ERR_MEMORY_BUDGET, "no free Q4 page slot");
             c.desc[c.pages] = ctox_paged_kv_descriptor{1, c.free_q4.back(), 0, c.pages * e->c.page_tokens};
@@ -269,12 +269,24 @@ ctox_status cache_push(ctox_hip_engine *e, Cache &c, const float *k, const float
         }
         ctox_paged_kv_descriptor &d = c.desc[c.pages - 1];
         c.dirty = std::min(c.dirty, c.pages - 1);
-        const uint32_t take = std::min(rows - done, e->c.page_tokens - d.tokens);
-        TRY(ctox_hip_kv_pack_q4_device(e->b, c.q4, k + (size_t)done * e->kvw, v + (size_t)done * e->kvw, take, e->kvw,
-                                       d.physical_slot, d.tokens, e->q4_page_bytes, e->s));
-        d.tokens += take;
-        done += take;
-        c.tokens += take;
+        slots[t] = d.physical_slot;
+        pos[t] = d.tokens;
+        d.tokens++;
+        c.tokens++;
+    }
+    return CTOX_OK;
+}
+
+// Append `rows` tokens (k, v: [rows][cv] dense) into Q4 pages, one pack per page run.
+ctox_status cache_push(ctox_hip_engine *e, Cache &c, const float *k, const float *v, uint32_t rows) {
+    std::vector<uint32_t> slots(rows), pos(rows);
+    TRY(cache_reserve(e, c, rows, slots.data(), pos.data()));
+    for (uint32_t t = 0; t < rows;) {
+        uint32_t n = 1;
+        while (t + n < rows && slots[t + n] == slots[t] && pos[t + n] == pos[t] + n) n++;
+        TRY(ctox_hip_kv_pack_q4_device(e->b, c.q4, k + (size_t)t * e->kvw, v + (size_t)t * e->kvw, n, e->kvw, slots[t],
+                                       pos[t], e->q4_page_bytes, e->s));
+        t += n;
     }
     return CTOX_OK;
 }
@@ -356,29 +368,14 @@ ctox_status make_mlp(ctox_hip_engine *e, Mlp &m, uint64_t &seed) {
 // FullAttentionState::append does (decoder.rs:774).
 ctox_status attn_forward(ctox_hip_engine *e, AttnLayer &a, uint32_t R, uint32_t rope0, float *delta, bool retain) {
     const uint32_t qh = e->c.num_attention_heads, kvh = e->c.num_key_value_heads, hd = e->c.head_dim;
-    // the q|k|v projection is already in e->proj (norm_mv)
-    ctox_norm_rows d{};
-    d.x = e->proj;
-    d.w = a.q_norm;
-    d.out = e->q;
-    d.rows = R * qh;
-    d.cols = hd;
-    d.inner = qh;
-    d.eps = e->c.rms_norm_epsilon;
-    d.x_inner = 2 * hd;
-    d.x_outer = e->Rq;
-    d.out_stride = hd;
-    TRY(ctox_hip_norm_rows_device(e->b, &d, e->s));
-    d.x = e->proj + 2 * qh * hd;
-    d.w = a.k_norm;
-    d.out = e->k;
-    d.rows = R * kvh;
-    d.inner = kvh;
-    d.x_inner = hd;
-    TRY(ctox_hip_norm_rows_device(e->b, &d, e->s));
-    TRY(ctox_hip_partial_rope_device(e->b, e->q, e->k, R, qh, kvh, hd, e->c.rotary_dim, rope0, e->c.rope_theta, e->s));
-    TRY(ctox_hip_copy_rows_device(e->b, e->proj, e->Rq, 2 * qh * hd + e->kvw, R, e->kvw, e->v, e->kvw, e->s));
-    TRY(cache_push(e, a.cache, e->k, e->v, R));
+    // the q|k|v projection is already in e->proj (norm_mv): q/k norms, RoPE
+    // and the K/V append in one launch
+    uint32_t slots[8], pos[8];
+    if (R > 8) return efail(CTOX_ERR_SHAPE, "attention rows exceed 8");
+    TRY(cache_reserve(e, a.cache, R, slots, pos));
+    TRY(ctox_hip_attn_prep_device(e->b, e->proj, e->Rq, a.q_norm, a.k_norm, R, qh, kvh, hd, e->c.rotary_dim, rope0,
+                                  e->c.rope_theta, e->c.rms_norm_epsilon, a.cache.q4, e->q4_page_bytes, slots, pos,
+                                  e->q, e->s));
     if (!retain) TRY(cache_demote(e, a.cache));
     TRY(cache_upload(e, a.cache));
     const ctox_paged_gqa_params p = gqa_params(e, a.cache);

@@ -248,6 +248,8 @@ SIGNATURES = {
     "ctox_hip_gdn_gates_strided_device": (_I32, [_P, _P, _P, _SZ, _P, _P, _SZ, _SZ, _P, _P, _P]),
     "ctox_hip_causal_conv_rows_device": (_I32, [_P, _P, _SZ, _P, _P, _SZ, _SZ, _SZ, _P, _P]),
     "ctox_hip_kv_pack_q4_device": (_I32, [_P, _P, _P, _P, _SZ, _SZ, _U32, _U32, _U32, _P]),
+    "ctox_hip_attn_prep_device": (_I32, [_P, _P, _SZ, _P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_uint64, ctypes.c_float,
+                                         ctypes.c_float, _P, _U32, _P, _P, _P, _P]),
     "ctox_hip_kv_demote_device": (_I32, [_P, _P, _P, _SZ, _SZ, _P]),
     "ctox_hip_paged_gqa_device": (_I32, [_P, _P, _P, _P, _P, ctypes.POINTER(PagedGqaParams), _SZ, _P, _P]),
     "ctox_hip_fill_random_device": (_I32, [_P, _P, ctypes.c_uint64, _U32, ctypes.c_uint64, ctypes.c_float,
@@ -583,6 +585,17 @@ class HipBackend:
         _check(load_library().ctox_hip_kv_pack_q4_device(self.handle, d_q4_pages, d_keys, d_values, token_count,
                                                          component_values, physical_slot, first_token_in_page,
                                                          q4_page_bytes, stream))
+
+    def attn_prep_device(self, d_proj: int, proj_stride: int, d_q_norm: int, d_k_norm: int, rows: int, q_heads: int,
+                         kv_heads: int, head_dim: int, rotary_dim: int, position: int, theta: float, eps: float,
+                         d_q4_pages: int, q4_page_bytes: int, slots, positions_in_page, d_q_out: int,
+                         stream: Optional[int] = None) -> None:
+        """Fused q/k norm + partial RoPE + Q4 K/V append (Q/src/decoder.rs:687-800, Q/src/kv_cache.rs:200-206)."""
+        sl = (ctypes.c_uint32 * len(slots))(*slots)
+        ps = (ctypes.c_uint32 * len(positions_in_page))(*positions_in_page)
+        _check(load_library().ctox_hip_attn_prep_device(self.handle, d_proj, proj_stride, d_q_norm, d_k_norm, rows,
+                                                        q_heads, kv_heads, head_dim, rotary_dim, position, theta, eps,
+                                                        d_q4_pages, q4_page_bytes, sl, ps, d_q_out, stream))
 
     def kv_demote_device(self, d_q4_page: int, d_q2_page: int, tokens: int, blocks_per_token: int,
                          stream: Optional[int] = None) -> None:

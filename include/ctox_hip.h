@@ -410,6 +410,23 @@ ctox_status ctox_hip_kv_pack_q4_device(ctox_hip_backend *backend, uint8_t *d_q4_
                                        const float *d_values, size_t token_count, size_t component_values,
                                        uint32_t physical_slot, uint32_t first_token_in_page,
                                        uint32_t q4_page_bytes, void *stream);
+/* An attention layer's K/V append for `rows` (<= 8) projected rows, fused:
+ * per q head RMS norm with q_norm ((1 + w), Q/src/reference.rs:38-62) and
+ * partial RoPE (:115-155) into d_q_out [rows][q_heads][head_dim]; per k head
+ * the same with k_norm, then K and V (the v part of the row as it is)
+ * quantized into Q4 page slot slots[t] at token positions_in_page[t], as
+ * ctox_hip_kv_pack_q4_device does. d_proj rows: per q head [q, gate] (2 *
+ * head_dim), then k [kv_heads * head_dim], then v. Replaces the q/k norm,
+ * RoPE and KV-append steps of FullAttentionState::append
+ * (Q/src/decoder.rs:687-800, Q/src/kv_cache.rs:200-206) and the CUDA
+ * runtime's query-gate-norm-rope + pack pair (q2q4_fused_matvec_sm86.cu:1491-1546,
+ * :1734-1799). head_dim 256. */
+ctox_status ctox_hip_attn_prep_device(ctox_hip_backend *backend, const float *d_proj, size_t proj_stride,
+                                      const float *d_q_norm, const float *d_k_norm, size_t rows, size_t q_heads,
+                                      size_t kv_heads, size_t head_dim, size_t rotary_dim, uint64_t position,
+                                      float theta, float eps, uint8_t *d_q4_pages, uint32_t q4_page_bytes,
+                                      const uint32_t *slots, const uint32_t *positions_in_page, float *d_q_out,
+                                      void *stream);
 /* Rewrite one Q4 page as Q2, byte-identical to QuantizedKvPage::requantize
  * (Q/src/kv_cache.rs:216-236). Replaces ctox_demote_paged_kv_q4_to_q2_sm86
  * (q2q4_fused_matvec_sm86.cu:1801-1834). */

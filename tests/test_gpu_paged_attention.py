@@ -161,3 +161,59 @@ def test_paged_attention_errors(hip):
     with pytest.raises(ctox_hip.UnsupportedOperation):
         hip.paged_gqa_device(q.data_ptr(), dev.q2_pool.data_ptr(), dev.q4_pool.data_ptr(), dev.d_desc.data_ptr(), p, 1,
                              q.data_ptr())
+
+
+@pytest.mark.parametrize("rows,pos0,slot_of", [(1, 4093, [3]), (5, 30, [1, 1, 0, 0, 0]), (8, 70000, [2] * 8)])
+def test_attn_prep_fused(hip, rows, pos0, slot_of):
+    """Fused q/k norm + partial RoPE + Q4 append against the oracle: q within
+    the RoPE/norm tolerances of test_gpu_layer_ops; V blocks byte-exact with
+    Q4Block64::quantize of the raw rows; K blocks byte-exact with the
+    quantize of the oracle's normed, rotated keys except where that value lies
+    within 1e-5 (relative) of a code boundary."""
+    from oracle import oracle as orc
+    say(f"case attn prep rows={rows} pos0={pos0}")
+    qh, kvh, hd, rd, theta, eps = 24, 4, 256, 64, 1e7, 1e-6
+    rng = np.random.default_rng(rows * 31 + pos0)
+    rq = 2 * (qh + kvh) * hd + 8                       # q|gate per head, k, v, slack
+    proj = (rng.standard_normal((rows, rq)) * 1.7).astype(np.float32)
+    qn = (rng.standard_normal(hd) * 0.3).astype(np.float32)
+    kn = (rng.standard_normal(hd) * 0.3).astype(np.float32)
+    page_tokens = 16
+    tb = 2 * kvh * hd // 64 * 34
+    page_bytes = page_tokens * tb
+    pages = torch.zeros(4 * page_bytes, dtype=torch.uint8, device="cuda")
+    pos_in = [(7 + t) % page_tokens for t in range(rows)]
+    pos_in = [pos_in[t] if slot_of.count(slot_of[t]) == 1 else t % page_tokens for t in range(rows)]
+    q_out = torch.empty(rows * qh * hd, dtype=torch.float32, device="cuda")
+    dproj, dqn, dkn = (torch.from_numpy(x).cuda() for x in (proj, qn, kn))
+    hip.attn_prep_device(dproj.data_ptr(), rq, dqn.data_ptr(), dkn.data_ptr(), rows, qh, kvh, hd, rd, pos0, theta, eps,
+                         pages.data_ptr(), page_bytes, slot_of, pos_in, q_out.data_ptr())
+    torch.cuda.synchronize()
+    got_q = q_out.cpu().numpy().reshape(rows, qh, hd)
+    raw = pages.cpu().numpy()
+    for t in range(rows):
+        q = np.stack([proj[t, h * 2 * hd:h * 2 * hd + hd] for h in range(qh)])
+        k = proj[t, 2 * qh * hd:2 * qh * hd + kvh * hd].reshape(kvh, hd)
+        v = proj[t, 2 * qh * hd + kvh * hd:2 * (qh + kvh) * hd].reshape(kvh, hd)
+        nq = orc.rms_norm_1p_weight(q.reshape(-1), qh, hd, qn, eps).reshape(qh, hd).copy()
+        nk = orc.rms_norm_1p_weight(k.reshape(-1), kvh, hd, kn, eps).reshape(kvh, hd).copy()
+        fq, fk = nq.reshape(-1).copy(), nk.reshape(-1).copy()
+        orc.apply_partial_rope(fq, fk, qh, kvh, hd, rd, pos0 + t, theta)
+        tol = 4 * float(np.spacing(np.float32(max(pos0 + t, 1)))) * 2 * 4.5 * np.abs(nq).max() + 1e-5
+        np.testing.assert_allclose(got_q[t], fq.reshape(qh, hd), rtol=1e-5, atol=tol)
+        off = slot_of[t] * page_bytes + pos_in[t] * tb
+        tok = raw[off:off + tb].tobytes()
+        assert tok[kvh * 4 * 34:] == pk.quantize_values(v.reshape(-1), pk.Q4)
+        want_k = pk.quantize_values(fk, pk.Q4)
+        if tok[:kvh * 4 * 34] != want_k:
+            fkb = fk.reshape(-1, 64)
+            for b in range(fkb.shape[0]):
+                g, w = tok[b * 34:(b + 1) * 34], want_k[b * 34:(b + 1) * 34]
+                if g == w:
+                    continue
+                m = np.abs(fkb[b]).max()
+                sel = np.clip(fkb[b] / m, -1, 1) * 7.5 + 7.5
+                near = np.abs(sel - np.floor(sel) - 0.5) < 1e-5 * 16
+                gc = np.array([(g[2 + i // 2] >> (4 * (i % 2))) & 15 for i in range(64)])
+                wc = np.array([(w[2 + i // 2] >> (4 * (i % 2))) & 15 for i in range(64)])
+                assert np.all((gc == wc) | near), f"row {t} K block {b} codes differ away from a rounding boundary"
