@@ -136,8 +136,9 @@ struct TileMatvecArgs {
     const void *s_out;      // NULL, f32[rows] or f16[rows]
     const float *bias;      // NULL or f32[rows]
     float *output;          // [rows]
-    float *partial;         // [chunks][tiles * 16] when chunks > 1
-    uint32_t *counts;       // [tiles], zero between launches
+    uint64_t *partial;      // [chunks - 1][tiles * 16] when chunks > 1: f32 bits | seq << 32
+    uint32_t seq;           // this launch's tag in the partial slots (never 0)
+    uint32_t pad0;
     uint32_t rows;
     uint32_t blocks;
     uint32_t tiles;

@@ -203,6 +203,59 @@ __device__ __forceinline__ float4 frag_group_build(const TileMatvecArgs &a, uint
     return make_float4(2.0f * q, 512.0f * q, 131072.0f * q, (float)(-off * (long long)sx) * q);
 }
 
+
+// Cross-chunk combine. The waves of the last chunk are dispatched after every
+// other chunk's waves (wave index = chunk * segs + segment), so they combine:
+// the other chunks store their row partials, tagged with the launch's
+// sequence number, as single 64-bit agent-scope atomic stores (coherent
+// across the XCDs' L2s without cache maintenance) and leave; the combining
+// lane polls its row's slots until every tag is this launch's and adds the
+// partials in chunk order (deterministic). Producers never wait, so the
+// polls always end; a poll count past CTOX_COMBINE_POLLS (only a broken
+// invariant) yields NaN, which the host reports, instead of a hang.
+#define CTOX_COMBINE_POLLS (1u << 16)
+__device__ __forceinline__ void combine_store(uint64_t *slot, float v, uint32_t seq) {
+    __hip_atomic_store(slot, (uint64_t)__float_as_uint(v) | ((uint64_t)seq << 32), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Sum of slots[k * stride], k < n (n = chunks - 1), in order, then + own.
+// `want` false (no row for this lane) returns at once with 0.
+__device__ __forceinline__ float combine_poll(const uint64_t *slots, size_t stride, uint32_t n, uint32_t seq, float own,
+                                              bool want) {
+    float sum = 0.0f;
+    bool done = !want;
+    for (uint32_t poll = 0; __builtin_amdgcn_ballot_w64(!done) != 0; poll++) {
+        if (poll >= CTOX_COMBINE_POLLS) {
+            if (!done) sum = __builtin_nanf("");
+            break;
+        }
+        if (poll) __builtin_amdgcn_s_sleep(2);
+        if (!done) {
+            float s = 0.0f;
+            bool all = true;
+            for (uint32_t c0 = 0; c0 < n; c0 += 16) {
+                uint64_t pv[16];
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    pv[i] = __hip_atomic_load(&slots[(size_t)min(c0 + i, n - 1) * stride], __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    if (c0 + i < n) {
+                        all = all && (uint32_t)(pv[i] >> 32) == seq;
+                        s += __uint_as_float((uint32_t)pv[i]);
+                    }
+            }
+            if (all) {
+                sum = s;
+                done = true;
+            }
+        }
+    }
+    return sum + own;
+}
+
 template <int DT, int U, int AB>
 __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
     using C = TlCfg<DT>;
@@ -351,33 +404,13 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
         if (mine && row < a.rows) a.output[row] = tile_epilogue(val / C::DEN, row, a);
         return;
     }
-    // Cross-chunk combine without cache maintenance: the partials are
-    // written and read with agent-scope atomic stores/loads (coherent across
-    // the XCDs' L2s by themselves), the stores are complete before the
-    // arrival count is raised, and the last arrival's reads depend on the
-    // count it got back.
     const size_t cstride = (size_t)a.tiles * CTOX_TILE_ROWS;
-    if (mine) __hip_atomic_store(&a.partial[(size_t)c * cstride + row], val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);
-    uint32_t old = 0;
-    if (mine && j == 0) old = __hip_atomic_fetch_add(&a.counts[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    old = __shfl(old, lane & 0x30);
-    if (mine && old == a.chunks - 1) {
-        // Up to 32 partial loads in flight at a time, added in chunk order.
-        float sum = 0.0f;
-        for (uint32_t c0 = 0; c0 < a.chunks; c0 += 32) {
-            float pv[32];
-#pragma unroll
-            for (int i = 0; i < 32; i++)
-                pv[i] = __hip_atomic_load(&a.partial[(size_t)min(c0 + i, a.chunks - 1) * cstride + row],
-                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-            for (int i = 0; i < 32; i++)
-                if (c0 + i < a.chunks) sum += pv[i];
-        }
-        if (row < a.rows) a.output[row] = tile_epilogue(sum / C::DEN, row, a);
-        if (j == 0) __hip_atomic_store(&a.counts[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (c + 1 < a.chunks) {
+        if (mine) combine_store(&a.partial[(size_t)c * cstride + row], val, a.seq);
+        return;
     }
+    const float sum = combine_poll(&a.partial[row], cstride, a.chunks - 1, a.seq, val, mine);
+    if (mine && row < a.rows) a.output[row] = tile_epilogue(sum / C::DEN, row, a);
 }
 
 // ctox_q{2,4}_mv_tile{U}_gfx950 take prep-staged fragments; the _x
@@ -544,44 +577,25 @@ __device__ __forceinline__ void tile_matvec_m(const TileMatvecArgs &a) {
     }
     // Partials [chunk][token][tiles * 16], combined as in the batch-1 kernel.
     const size_t tstride = (size_t)a.tiles * CTOX_TILE_ROWS, cstride = tstride * M;
+    if (c + 1 < a.chunks) {
+#pragma unroll
+        for (int k = 0; k < U; k++)
+#pragma unroll
+            for (int tg = 0; tg < TG; tg++) {
+                const uint32_t tok = 4 * tg + g, row = (t0 + k) * CTOX_TILE_ROWS + j;
+                if ((uint32_t)k < n && tok < M) combine_store(&a.partial[c * cstride + tok * tstride + row], acc[k][tg], a.seq);
+            }
+        return;
+    }
 #pragma unroll
     for (int k = 0; k < U; k++)
 #pragma unroll
         for (int tg = 0; tg < TG; tg++) {
             const uint32_t tok = 4 * tg + g, row = (t0 + k) * CTOX_TILE_ROWS + j;
-            if ((uint32_t)k < n && tok < M)
-                __hip_atomic_store(&a.partial[c * cstride + tok * tstride + row], acc[k][tg], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+            const bool want = (uint32_t)k < n && tok < M;
+            const float sum = combine_poll(&a.partial[tok * tstride + row], cstride, a.chunks - 1, a.seq, acc[k][tg], want);
+            if (want && row < a.rows) a.output[(size_t)tok * a.out_stride + row] = tile_epilogue(sum / C::DEN, row, a);
         }
-    __builtin_amdgcn_s_waitcnt(0);
-    uint32_t old = 0;
-    if (lane < n) old = __hip_atomic_fetch_add(&a.counts[t0 + lane], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-    for (int k = 0; k < U; k++) {
-        const uint32_t ok = __shfl(old, k);
-        if ((uint32_t)k < n && ok == a.chunks - 1) {
-            const uint32_t row = (t0 + k) * CTOX_TILE_ROWS + j;
-#pragma unroll
-            for (int tg = 0; tg < TG; tg++) {
-                const uint32_t tok = 4 * tg + g;
-                if (tok < M) {
-                    float sum = 0.0f;
-                    for (uint32_t c0 = 0; c0 < a.chunks; c0 += 32) {
-                        float pv[32];
-#pragma unroll
-                        for (int i = 0; i < 32; i++)
-                            pv[i] = __hip_atomic_load(&a.partial[min(c0 + i, a.chunks - 1) * cstride + tok * tstride + row],
-                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-                        for (int i = 0; i < 32; i++)
-                            if (c0 + i < a.chunks) sum += pv[i];
-                    }
-                    if (row < a.rows) a.output[(size_t)tok * a.out_stride + row] = tile_epilogue(sum / C::DEN, row, a);
-                }
-            }
-            if (lane == 0) __hip_atomic_store(&a.counts[t0 + k], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
 }
 
 #define CTOX_TILE_M_KERNEL(name, dt, u, tg) \

@@ -163,8 +163,10 @@ struct ctox_hip_backend {
     hipFunction_t gdn_fused = nullptr;
     int cus = 0;
     uint32_t tile_u = 0;  // CTOX_TILE_U: fixed row tiles per wave (0 = planned)
-    // Tiled matvec chunk partials and per-tile arrival counts (zero between launches).
-    DevBuf tpart, tcnt;
+    // Tiled matvec chunk partials (64-bit slots tagged with a launch sequence
+    // number; zeroed when allocated) and the last sequence number used.
+    DevBuf tpart;
+    uint32_t tile_seq = 0;
     // Tiled copies of raw device weights (ctox_hip_register_tiled_weights).
     std::unordered_map<const void *, TiledCopy> raw_tiled;
     // Activation staging (two layouts: [0] Q2, [1] Q4) and gated-delta norms.
@@ -422,6 +424,21 @@ ctox_status run_matvec(ctox_hip_backend *b, int layout, int32_t dtype, const voi
     return launch(f, dim3((unsigned)groups), dim3(256), s, a, "ctox_q*_matvec_gfx950");
 }
 
+// Tag of the next tiled launch's partial slots: never 0 (the value of a
+// freshly zeroed slot) and never one still present in the buffer (on wrap
+// the slots are zeroed again).
+uint32_t next_tile_seq(ctox_hip_backend *b) {
+    if (++b->tile_seq == 0) {
+        if (b->tpart.ptr) {
+            (void)hipDeviceSynchronize();
+            (void)hipMemset(b->tpart.ptr, 0, b->tpart.bytes);
+            (void)hipDeviceSynchronize();
+        }
+        b->tile_seq = 1;
+    }
+    return b->tile_seq;
+}
+
 // One launch of the tiled batch-1 matvec over a prepared segment. Plan: the
 // chunks x tiles units are spread so that one pass of about twelve waves per
 // CU covers them, at most CTOX_TILE_MAXU row tiles per wave. With d_input
@@ -441,8 +458,7 @@ ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy 
     const size_t waves = (size_t)segs * t.chunks;
     if ((waves + 3) / 4 > 0x7fffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
     if (t.chunks > 1) {
-        ctox_status st = ensure(b, b->tpart, (size_t)t.chunks * t.tiles * CTOX_TILE_ROWS * sizeof(float), false);
-        if (!st) st = ensure(b, b->tcnt, (size_t)t.tiles * sizeof(uint32_t), true);
+        ctox_status st = ensure(b, b->tpart, (size_t)(t.chunks - 1) * t.tiles * CTOX_TILE_ROWS * sizeof(uint64_t), true);
         if (st) return st;
     }
     TileMatvecArgs a{};
@@ -452,8 +468,8 @@ ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy 
     a.s_out = d_s_out;
     a.bias = d_bias;
     a.output = d_output;
-    a.partial = (float *)b->tpart.ptr;
-    a.counts = (uint32_t *)b->tcnt.ptr;
+    a.partial = (uint64_t *)b->tpart.ptr;
+    a.seq = next_tile_seq(b);
     a.rows = (uint32_t)rows;
     a.blocks = (uint32_t)(columns / kBlockLen);
     a.tiles = t.tiles;
@@ -491,8 +507,8 @@ ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCop
     const size_t waves = (size_t)segs * t.chunks;
     if (waves / 4 > 0x7fffffffu || out_stride > 0xffffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
     if (t.chunks > 1) {
-        ctox_status st = ensure(b, b->tpart, (size_t)t.chunks * batch * t.tiles * CTOX_TILE_ROWS * sizeof(float), false);
-        if (!st) st = ensure(b, b->tcnt, (size_t)t.tiles * sizeof(uint32_t), true);
+        ctox_status st =
+            ensure(b, b->tpart, (size_t)(t.chunks - 1) * batch * t.tiles * CTOX_TILE_ROWS * sizeof(uint64_t), true);
         if (st) return st;
     }
     TileMatvecArgs a{};
@@ -502,8 +518,8 @@ ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCop
     a.s_out = d_s_out;
     a.bias = d_bias;
     a.output = d_output;
-    a.partial = (float *)b->tpart.ptr;
-    a.counts = (uint32_t *)b->tcnt.ptr;
+    a.partial = (uint64_t *)b->tpart.ptr;
+    a.seq = next_tile_seq(b);
     a.rows = (uint32_t)rows;
     a.blocks = (uint32_t)(columns / kBlockLen);
     a.tiles = t.tiles;
@@ -677,7 +693,7 @@ extern "C" void ctox_hip_backend_destroy(ctox_hip_backend *b) {
     (void)hipSetDevice(b->device);
     (void)hipDeviceSynchronize();
     DevBuf *bufs[] = {&b->xa[0], &b->xa[1], &b->xc[0], &b->xc[1], &b->norms, &b->tok, &b->stats, &b->attn,
-                      &b->tpart, &b->tcnt};
+                      &b->tpart};
     for (auto &kv : b->raw_tiled)
         if (kv.second.d) (void)hipFree(kv.second.d);
     for (DevBuf *d : bufs)
