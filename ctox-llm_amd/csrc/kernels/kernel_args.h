@@ -138,7 +138,10 @@ struct TileMatvecArgs {
     float *output;          // [rows]
     uint64_t *partial;      // [chunks - 1][tiles * 16] when chunks > 1: f32 bits | seq << 32
     uint32_t seq;           // this launch's tag in the partial slots (never 0)
-    uint32_t pad0;
+    uint32_t sq_n;          // xmode 1: entries of sq_in (0: reduce the row itself)
+    const float *res_h;     // res_sq set: the residual the output is added to [rows]
+    float *res_sq;          // NULL or [tiles]: sum over the tile's rows of (res_h + out)^2
+    const float *sq_in;     // xmode 1: per-tile sums of squares of the residual row, or NULL
     uint32_t rows;
     uint32_t blocks;
     uint32_t tiles;

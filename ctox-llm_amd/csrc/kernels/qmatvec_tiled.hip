@@ -256,6 +256,17 @@ __device__ __forceinline__ float combine_poll(const uint64_t *slots, size_t stri
     return sum + own;
 }
 
+
+// Producer side of the residual sums: per 16-row tile, sum of (res_h + y)^2
+// over its rows (the 16 lanes of one row group, DPP within the row).
+__device__ __forceinline__ void residual_tile_sum(const TileMatvecArgs &a, uint32_t tile, uint32_t row, bool mine,
+                                                  float y, uint32_t j) {
+    if (!a.res_sq) return;
+    const float h = mine && row < a.rows ? a.res_h[row] + y : 0.0f;
+    const float s = row16_reduce(h * h, [](float x, float z) { return x + z; });
+    if (mine && j == 0) a.res_sq[tile] = s;
+}
+
 template <int DT, int U, int AB>
 __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
     using C = TlCfg<DT>;
@@ -297,7 +308,15 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
     const uint32_t wg_wave = threadIdx.x >> 6;
     GroupIn gin;
     v4i hx[8], hd[8];
-    if (AB && a.xmode == 1) {
+    float sqv[2] = {0.0f, 0.0f};
+    if (AB && a.xmode == 1 && a.sq_n) {
+        // The producer's per-tile sums of squares (at most 512).
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const uint32_t t = threadIdx.x + 256 * k;
+            sqv[k] = t < a.sq_n ? a.sq_in[t] : 0.0f;
+        }
+    } else if (AB && a.xmode == 1) {
         const uint32_t cols = a.blocks * CTOX_BLOCK_LEN;
         const __amdgpu_buffer_rsrc_t xr = f32_rsrc(a.input, cols), dr = f32_rsrc(a.delta, cols);
 #pragma unroll
@@ -316,19 +335,26 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
             u[k].w[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, lane * 16, k * C::UB + i * 1024, CTOX_LOAD_NT);
         u[k].s = __builtin_amdgcn_raw_buffer_load_b64(wr, C::CB + lane * 8, k * C::UB, CTOX_LOAD_NT);
     }
+    // AB: the chunk's fragments and constants stay in LDS and are read per
+    // group where they are used, which leaves the wave's registers to the
+    // weight loads in flight (more waves per CU).
+    __shared__ __align__(16) int8_t xs[CTOX_TILE_BLOCKS * 192];
+    __shared__ float4 kqs[CTOX_TILE_BLOCKS];
     if (AB) {
-        __shared__ __align__(16) int8_t xs[CTOX_TILE_BLOCKS * 192];
-        __shared__ float4 kqs[CTOX_TILE_BLOCKS];
         __shared__ float wss[4];
         float inv = 0.0f;
         if (a.xmode == 1) {
             float ss = 0.0f;
+            if (a.sq_n) {
+                ss = sqv[0] + sqv[1];
+            } else {
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
+                for (int k = 0; k < 8; k++) {
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float h = __int_as_float(hx[k][i]) + __int_as_float(hd[k][i]);
-                    ss = fmaf(h, h, ss);
+                    for (int i = 0; i < 4; i++) {
+                        const float h = __int_as_float(hx[k][i]) + __int_as_float(hd[k][i]);
+                        ss = fmaf(h, h, ss);
+                    }
                 }
             }
             ss = row16_reduce(ss, [](float x, float y) { return x + y; });
@@ -343,55 +369,62 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
         if (j == 0) kqs[4 * wg_wave + g] = k;
         lds_barrier();  // orders LDS only: the weight loads stay in flight
         if (t0 >= a.tiles) return;
-#pragma unroll
-        for (int G = 0; G < 4; G++) {
-            kq[G] = kqs[4 * G + g];
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-                af[G][q] = aok ? *(const v4i *)(xs + G * 768 + g * 192 + limb * 64 + q * 16) : (v4i){0, 0, 0, 0};
-        }
     }
 
+    // Every unit is computed (a unit past the wave's tiles reads zeros): a
+    // branch here would let the compiler sink its loads behind it. Per unit
+    // the groups are added in order G = 0..3.
     float part[U];
 #pragma unroll
-    for (int k = 0; k < U; k++) {
-        // Every unit is computed (a unit past the wave's tiles reads zeros):
-        // a branch here would let the compiler sink its loads behind it.
-        float acc = 0.0f;
-        {
+    for (int k = 0; k < U; k++) part[k] = 0.0f;
 #pragma unroll
-            for (int G = 0; G < 4; G++) {
-                v4i cc = (v4i){0, 0, 0, 0};
+    for (int G = 0; G < 4; G++) {
+        v4i fg[4];
+        float4 kg;
+        if (AB) {
+            kg = kqs[4 * G + g];
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    uint32_t w0, w1 = 0;
-                    if (DT) {
-                        const v4i W = u[k].w[2 * G + (q >> 1)];
-                        w0 = (uint32_t)W[2 * (q & 1)];
-                        w1 = (uint32_t)W[2 * (q & 1) + 1];
-                    } else {
-                        w0 = (uint32_t)u[k].w[G][q];
-                    }
-                    cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[G][q], unpack_quarter<DT>(w0, w1), cc, 0, 0, 0);
-                }
-                const uint32_t sw = u[k].s[G >> 1];
-                const float scale = half_bits_to_float((G & 1) ? (sw >> 16) : (sw & 0xffffu));
-                float f;
-                if (DT) {
-                    f = fmaf((float)cc[0], kq[G].x, kq[G].w);
-                    f = fmaf((float)cc[1], kq[G].y, f);
-                    f = fmaf((float)cc[2], kq[G].z, f);
-                } else {
-                    // Q2: sum(c X) = C0 + 256 C1 + 65536 C2 is exact in int32
-                    // (|sum| <= 64 * 3 * 2^22 < 2^30): one conversion.
-                    f = fmaf((float)(cc[0] + (cc[1] << 8) + (cc[2] << 16)), kq[G].x, kq[G].w);
-                }
-                acc = fmaf(f, scale, acc);
-            }
+            for (int q = 0; q < 4; q++)
+                fg[q] = aok ? *(const v4i *)(xs + G * 768 + g * 192 + limb * 64 + q * 16) : (v4i){0, 0, 0, 0};
+        } else {
+            kg = kq[G];
+#pragma unroll
+            for (int q = 0; q < 4; q++) fg[q] = af[G][q];
         }
-        acc += __shfl_xor(acc, 16);
-        acc += __shfl_xor(acc, 32);
-        part[k] = acc;
+#pragma unroll
+        for (int k = 0; k < U; k++) {
+            v4i cc = (v4i){0, 0, 0, 0};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                uint32_t w0, w1 = 0;
+                if (DT) {
+                    const v4i W = u[k].w[2 * G + (q >> 1)];
+                    w0 = (uint32_t)W[2 * (q & 1)];
+                    w1 = (uint32_t)W[2 * (q & 1) + 1];
+                } else {
+                    w0 = (uint32_t)u[k].w[G][q];
+                }
+                cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(fg[q], unpack_quarter<DT>(w0, w1), cc, 0, 0, 0);
+            }
+            const uint32_t sw = u[k].s[G >> 1];
+            const float scale = half_bits_to_float((G & 1) ? (sw >> 16) : (sw & 0xffffu));
+            float f;
+            if (DT) {
+                f = fmaf((float)cc[0], kg.x, kg.w);
+                f = fmaf((float)cc[1], kg.y, f);
+                f = fmaf((float)cc[2], kg.z, f);
+            } else {
+                // Q2: sum(c X) = C0 + 256 C1 + 65536 C2 is exact in int32
+                // (|sum| <= 64 * 3 * 2^22 < 2^30): one conversion.
+                f = fmaf((float)(cc[0] + (cc[1] << 8) + (cc[2] << 16)), kg.x, kg.w);
+            }
+            part[k] = fmaf(f, scale, part[k]);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < U; k++) {
+        part[k] += __shfl_xor(part[k], 16);
+        part[k] += __shfl_xor(part[k], 32);
     }
     // Lane (g, j) reports row j of the wave's tile g.
     float val = part[0];
@@ -401,7 +434,9 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
     const uint32_t tile = t0 + g, row = tile * CTOX_TILE_ROWS + j;
     const bool mine = g < n;
     if (a.chunks == 1) {
-        if (mine && row < a.rows) a.output[row] = tile_epilogue(val / C::DEN, row, a);
+        const float y = mine && row < a.rows ? tile_epilogue(val / C::DEN, row, a) : 0.0f;
+        if (mine && row < a.rows) a.output[row] = y;
+        residual_tile_sum(a, tile, row, mine, y, j);
         return;
     }
     const size_t cstride = (size_t)a.tiles * CTOX_TILE_ROWS;
@@ -410,7 +445,9 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
         return;
     }
     const float sum = combine_poll(&a.partial[row], cstride, a.chunks - 1, a.seq, val, mine);
-    if (mine && row < a.rows) a.output[row] = tile_epilogue(sum / C::DEN, row, a);
+    const float y = mine && row < a.rows ? tile_epilogue(sum / C::DEN, row, a) : 0.0f;
+    if (mine && row < a.rows) a.output[row] = y;
+    residual_tile_sum(a, tile, row, mine, y, j);
 }
 
 // ctox_q{2,4}_mv_tile{U}_gfx950 take prep-staged fragments; the _x

@@ -351,6 +351,10 @@ struct TileXform {
     float *x_out = nullptr, *norm_out = nullptr;
     uint32_t off = 0, head_dim = 0;
     float eps = 0.0f;
+    const float *res_h = nullptr;  // producer: residual the output is added to
+    float *res_sq = nullptr;       // producer: per-tile sums of (res_h + out)^2
+    const float *sq_in = nullptr;  // consumer (xmode 1): those sums
+    uint32_t sq_n = 0;
 };
 
 ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows, size_t columns,
@@ -491,6 +495,10 @@ ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy 
         a.off = xf->off;
         a.head_dim = xf->head_dim;
         a.eps = xf->eps;
+        a.res_h = xf->res_h;
+        a.res_sq = xf->res_sq;
+        a.sq_in = xf->sq_in;
+        a.sq_n = xf->sq_in ? xf->sq_n : 0u;
     }
     hipFunction_t f = d_input ? b->tilex[q4][u - 1] : b->tile[q4][u - 1];
     return launch(f, dim3((unsigned)((waves + 3) / 4)), dim3(256), s, a, "ctox_q*_mv_tile*_gfx950");
@@ -926,6 +934,21 @@ extern "C" ctox_status ctox_hip_norm_matvec_device(ctox_hip_backend *b, const fl
                                                   const void *d_weights, const uint16_t *d_s_in,
                                                   const uint16_t *d_s_out, float *d_output, uint32_t rows,
                                                   uint32_t columns, uint32_t batch, void *stream) {
+    return ctox_hip_norm_matvec_sums_device(b, d_x, d_delta, delta_parts, delta_part_stride, d_x_out, d_norm_w, eps,
+                                            d_norm_out, dtype, d_weights, d_s_in, d_s_out, d_output, rows, columns,
+                                            batch, nullptr, 0, stream);
+}
+
+extern "C" ctox_status ctox_hip_norm_matvec_sums_device(ctox_hip_backend *b, const float *d_x, const float *d_delta,
+                                                       uint32_t delta_parts, size_t delta_part_stride,
+                                                       float *d_x_out, const float *d_norm_w, float eps,
+                                                       float *d_norm_out, int32_t dtype, const void *d_weights,
+                                                       const uint16_t *d_s_in, const uint16_t *d_s_out,
+                                                       float *d_output, uint32_t rows, uint32_t columns,
+                                                       uint32_t batch, const float *d_sums, uint32_t sum_count,
+                                                       void *stream) {
+    if (d_sums && (sum_count != (columns + CTOX_TILE_ROWS - 1) / CTOX_TILE_ROWS || sum_count > 512))
+        return fail(CTOX_ERR_SHAPE, "residual sums: one per 16 columns of the row, at most 512");
     if (!b || !d_x || !d_norm_w || !d_weights || !d_output || (d_delta && !d_x_out))
         return fail(CTOX_ERR_SHAPE, "null argument");
     if (d_delta && d_x_out == d_x) return fail(CTOX_ERR_SHAPE, "norm-matvec residual output must not alias its input");
@@ -952,6 +975,8 @@ extern "C" ctox_status ctox_hip_norm_matvec_device(ctox_hip_backend *b, const fl
             xf.x_out = d_delta ? d_x_out : nullptr;
             xf.norm_out = d_norm_out;
             xf.eps = eps;
+            xf.sq_in = d_sums;
+            xf.sq_n = sum_count;
             return run_tile_matvec(b, dtype, *t, rows, columns, d_s_out, d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE,
                                    nullptr, d_output, 0, s, d_x, d_s_in, d_s_in ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, &xf);
         }
@@ -989,7 +1014,7 @@ extern "C" ctox_status ctox_hip_transform_matvec_device(ctox_hip_backend *b, con
                                                        uint32_t *parts, void *stream) {
     if (parts) *parts = 1;
     if (!b || !x || !x->a || !d_weights || !d_output || ((x->mode == 2 || x->mode == 3) && !x->b) ||
-        (x->mode == 2 && !x->w))
+        (x->mode == 2 && !x->w) || (x->res_sums && !x->res_h))
         return fail(CTOX_ERR_SHAPE, "null argument");
     if (x->mode < 1 || x->mode > 3) return fail(CTOX_ERR_SHAPE, "unknown input transform %u", x->mode);
     if (dtype != CTOX_DTYPE_Q2B64 && dtype != CTOX_DTYPE_Q4B64)
@@ -1015,10 +1040,14 @@ extern "C" ctox_status ctox_hip_transform_matvec_device(ctox_hip_backend *b, con
             xf.off = x->off;
             xf.head_dim = x->head_dim;
             xf.eps = x->eps;
+            xf.res_h = x->res_h;
+            xf.res_sq = x->res_sums;
             return run_tile_matvec(b, dtype, *t, rows, columns, d_s_out, d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE,
                                    nullptr, d_output, 0, s, x->a, d_s_in, d_s_in ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, &xf);
         }
     }
+    if (x->res_sums)
+        return fail(CTOX_ERR_UNSUPPORTED_OPERATION, "residual sums need batch 1 on registered weights");
     ctox_status st = ensure(b, b->xa[layout], blocks * batch * 192, false);
     if (!st) st = ensure(b, b->xc[layout], blocks * batch * 4 * sizeof(float), false);
     if (st) return st;

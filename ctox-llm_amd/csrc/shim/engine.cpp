@@ -124,6 +124,11 @@ struct ctox_hip_engine {
     uint32_t *d_tokens = nullptr, *d_drafts = nullptr, *d_result = nullptr;
     uint64_t *d_rng = nullptr;
     uint32_t delta_parts = 1;  // partial sums held in delta (split-K producers)
+    // Per-16-row sums of (hid + delta)^2 written by the last single-row
+    // producer of `rsq_delta` against residual `rsq_hid` (the next norm's
+    // sum of squares); valid until that norm consumes them.
+    float *rsq = nullptr;
+    const float *rsq_delta = nullptr, *rsq_hid = nullptr;
     uint32_t position = 0;   // tokens processed by the target model
     uint32_t mtp_tokens = 0; // entries in the MTP cache
     bool have_prev = false;  // prev_hidden holds the last target final hidden
@@ -204,10 +209,29 @@ ctox_status matvec(ctox_hip_engine *e, const Mat &m, const float *in, float *out
 // sum goes to the other buffer, which becomes the stream.
 ctox_status norm_mv(ctox_hip_engine *e, const float *delta, const float *w, uint32_t rows, const Mat &m, float *out,
                     float *norm_out = nullptr) {
-    TRY(ctox_hip_norm_matvec_device(e->b, e->hid, delta, e->delta_parts, (size_t)rows * e->H, delta ? e->hid2 : nullptr,
+    const bool sums = delta && rows == 1 && e->rsq_delta == delta && e->rsq_hid == e->hid && e->delta_parts == 1;
+    e->rsq_delta = e->rsq_hid = nullptr;
+    TRY(ctox_hip_norm_matvec_sums_device(e->b, e->hid, delta, e->delta_parts, (size_t)rows * e->H, delta ? e->hid2 : nullptr,
                                     w, e->c.rms_norm_epsilon, norm_out, m.dtype, m.w, m.s_in, m.s_out, out, m.rows,
-                                    m.cols, rows, e->s));
+                                    m.cols, rows, sums ? e->rsq : nullptr, sums ? (e->H + 15) / 16 : 0, e->s));
     if (delta) std::swap(e->hid, e->hid2);
+    return CTOX_OK;
+}
+
+// A single-row producer of residual delta `out` also leaves the next norm's
+// per-tile sums of squares (ctox_input_transform::res_sums).
+ctox_status delta_mv(ctox_hip_engine *e, ctox_input_transform &x, const Mat &m, float *out, uint32_t R) {
+    if (R == 1) {
+        x.res_h = e->hid;
+        x.res_sums = e->rsq;
+    }
+    e->rsq_delta = e->rsq_hid = nullptr;
+    TRY(ctox_hip_transform_matvec_device(e->b, &x, m.dtype, m.w, m.s_in, m.s_out, out, m.rows, m.cols, R, 1,
+                                         &e->delta_parts, e->s));
+    if (R == 1) {
+        e->rsq_delta = out;
+        e->rsq_hid = e->hid;
+    }
     return CTOX_OK;
 }
 
@@ -380,9 +404,8 @@ ctox_status attn_forward(ctox_hip_engine *e, AttnLayer &a, uint32_t R, uint32_t 
     TRY(cache_upload(e, a.cache));
     const ctox_paged_gqa_params p = gqa_params(e, a.cache);
     TRY(ctox_hip_paged_gqa_device(e->b, e->q, a.cache.q2, a.cache.q4, a.cache.d_desc, &p, R, e->attn, e->s));
-    ctox_input_transform x{e->attn, e->proj, nullptr, 3, qh * hd, e->Rq, 0, hd, 0.0f};
-    return ctox_hip_transform_matvec_device(e->b, &x, a.o.dtype, a.o.w, a.o.s_in, a.o.s_out, delta, a.o.rows, a.o.cols, R,
-                                            1, &e->delta_parts, e->s);
+    ctox_input_transform x{e->attn, e->proj, nullptr, 3, qh * hd, e->Rq, 0, hd, 0.0f, nullptr, nullptr};
+    return delta_mv(e, x, a.o, delta, R);
 }
 
 float *conv_cur(ctox_hip_engine *e) { return e->conv_par ? e->conv_state2 : e->conv_state; }
@@ -405,16 +428,14 @@ ctox_status gdn_forward(ctox_hip_engine *e, GdnLayer &g, uint32_t R, float *delt
     float *proj = keep_rows ? g.proj : e->proj;  // the in-projection, already computed (norm_mv)
     float *ld = keep_rows ? g.ld : e->ld, *beta = keep_rows ? g.beta : e->beta;
     TRY(gdn_core(e, g, proj, R, ld, beta, false));
-    ctox_input_transform x{e->core, proj + e->C, g.gnorm, 2, e->Vw, e->Rin, 0, dv, e->c.rms_norm_epsilon};
-    return ctox_hip_transform_matvec_device(e->b, &x, g.out.dtype, g.out.w, g.out.s_in, g.out.s_out, delta, g.out.rows,
-                                            g.out.cols, R, 1, &e->delta_parts, e->s);
+    ctox_input_transform x{e->core, proj + e->C, g.gnorm, 2, e->Vw, e->Rin, 0, dv, e->c.rms_norm_epsilon, nullptr, nullptr};
+    return delta_mv(e, x, g.out, delta, R);
 }
 
 ctox_status mlp_forward(ctox_hip_engine *e, Mlp &m, uint32_t R, const float *delta_in, float *delta_out) {
     TRY(norm_mv(e, delta_in, m.norm, R, m.gate_up, e->gu));
-    ctox_input_transform x{e->gu, nullptr, nullptr, 1, 2 * e->I, 0, e->I, 0, 0.0f};
-    return ctox_hip_transform_matvec_device(e->b, &x, m.down.dtype, m.down.w, m.down.s_in, m.down.s_out, delta_out,
-                                            m.down.rows, m.down.cols, R, 1, &e->delta_parts, e->s);
+    ctox_input_transform x{e->gu, nullptr, nullptr, 1, 2 * e->I, 0, e->I, 0, 0.0f, nullptr, nullptr};
+    return delta_mv(e, x, m.down, delta_out, R);
 }
 
 // Target model over R rows (tokens in d_tok, positions position..position+R-1).
@@ -587,7 +608,8 @@ extern "C" ctox_status ctox_hip_engine_create(ctox_hip_backend *b, const ctox_en
         (st = dalloc_t(e, &e->draft_logits, (size_t)std::max(1u, c.draft_tokens) * e->V)) ||
         (st = dalloc_t(e, &e->mtp_hidden, R * e->H)) || (st = dalloc_t(e, &e->prev_hidden, R * e->H)) ||
         (st = dalloc_t(e, &e->target_hidden, (R + 1) * e->H)) || (st = dalloc_t(e, &e->d_tokens, 16)) ||
-        (st = dalloc_t(e, &e->d_drafts, 16)) || (st = dalloc_t(e, &e->d_result, 16)) || (st = dalloc_t(e, &e->d_rng, 1)))
+        (st = dalloc_t(e, &e->d_drafts, 16)) || (st = dalloc_t(e, &e->d_result, 16)) || (st = dalloc_t(e, &e->d_rng, 1)) ||
+        (st = dalloc_t(e, &e->rsq, 512)))
         return cleanup(st);
     if ((st = sync(e))) return cleanup(st);
     *out = e;

@@ -226,6 +226,18 @@ ctox_status ctox_hip_norm_matvec_device(ctox_hip_backend *backend, const float *
                                         float *d_output, uint32_t rows, uint32_t columns, uint32_t batch,
                                         void *stream);
 
+/* ctox_hip_norm_matvec_device with the residual's sum of squares given as
+ * d_sums[sum_count] per-16-row-tile partials (a producing
+ * ctox_hip_transform_matvec_device's res_sums over d_x + d_delta); they are
+ * added in tile order. Used on the batch-1 registered-weights path only
+ * (otherwise the sum is computed from the rows as before). */
+ctox_status ctox_hip_norm_matvec_sums_device(ctox_hip_backend *backend, const float *d_x, const float *d_delta,
+                                             uint32_t delta_parts, size_t delta_part_stride, float *d_x_out,
+                                             const float *d_norm_w, float eps, float *d_norm_out, int32_t dtype,
+                                             const void *d_weights, const uint16_t *d_s_in, const uint16_t *d_s_out,
+                                             float *d_output, uint32_t rows, uint32_t columns, uint32_t batch,
+                                             const float *d_sums, uint32_t sum_count, void *stream);
+
 /* The projection of a value computed on the fly from its producer's output,
  * staged in the same pass (rows of a at t * a_stride, of b at t * b_stride):
  *   mode 1 swiglu (Q/src/reference.rs:96-112): silu(a[c]) * a[off + c];
@@ -237,6 +249,16 @@ typedef struct {
     const float *a, *b, *w;
     uint32_t mode, a_stride, b_stride, off, head_dim;
     float eps;
+    /* Optional (both NULL: off). When the output is a residual delta that
+     * will be added to res_h [rows], res_sums receives, per 16-row tile t,
+     * the sum over its rows r of (res_h[r] + out[r])^2: the sum of squares a
+     * following ctox_hip_norm_matvec_sums_device needs (Q/src/reference.rs:38-62),
+     * so that it need not re-read the whole residual row in every workgroup.
+     * Batch 1 on registered weights only; otherwise the call fails with
+     * CTOX_ERR_UNSUPPORTED_OPERATION. No crate counterpart (the CPU decoder
+     * adds and normalizes in one pass, Q/src/decoder.rs:636-680). */
+    const float *res_h;
+    float *res_sums;
 } ctox_input_transform;
 /* split_k != 0 lets a batch-1 projection split its K range into one partial
  * per 1 KiB slice of a row (balancing few-row, long-K matrices over the

@@ -211,7 +211,8 @@ def test_norm_matvec(hip, orc, batch, with_delta, dtype, registered, rows, cols)
 class _Transform(ctypes.Structure):
     _fields_ = [("a", ctypes.c_void_p), ("b", ctypes.c_void_p), ("w", ctypes.c_void_p), ("mode", ctypes.c_uint32),
                 ("a_stride", ctypes.c_uint32), ("b_stride", ctypes.c_uint32), ("off", ctypes.c_uint32),
-                ("head_dim", ctypes.c_uint32), ("eps", ctypes.c_float)]
+                ("head_dim", ctypes.c_uint32), ("eps", ctypes.c_float), ("res_h", ctypes.c_void_p),
+                ("res_sums", ctypes.c_void_p)]
 
 
 @pytest.mark.parametrize("mode,dtype,registered,hd,heads", [
@@ -276,3 +277,68 @@ def test_transform_matvec(hip, orc, mode, dtype, registered, hd, heads):
     got = out[0].cpu().numpy()
     rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
     assert np.all(np.abs(got - ref) <= 1e-3 * (np.abs(ref) + rms)), float(np.abs(got - ref).max())
+
+
+@pytest.mark.parametrize("rows,cols", [(5120, 2048), (320, 512)])
+def test_residual_sums_chain(hip, orc, rows, cols):
+    """A projection producing a residual delta (swiglu -> down, registered
+    weights, batch 1) also writes per-16-row sums of (h + delta)^2, checked
+    against float64; the next norm-matvec given those sums matches the one
+    that reduces the row itself (both against the oracle norm + matvec)."""
+    import ctox_hip
+    say(f"case residual sums rows={rows} cols={cols}")
+    rng = np.random.default_rng(rows + cols)
+    lib = ctox_hip.load_library()
+
+    def qmat(r, c, dtype):
+        bb = 34 if dtype == 1 else 18
+        blocks = rng.integers(0, 256, size=(r, c // 64, bb), dtype=np.uint8)
+        blocks[:, :, :2] = (np.abs(rng.standard_normal((r, c // 64))) * 0.02).astype(np.float16).view(
+            np.uint8).reshape(r, c // 64, 2)
+        return blocks.tobytes()
+
+    w1 = qmat(rows, cols, 0)                      # producer: down-like, out [rows]
+    w2 = qmat(256, rows, 1)                       # consumer: reads the rows-wide residual
+    a = rng.standard_normal(2 * cols).astype(np.float32)
+    hres = rng.standard_normal(rows).astype(np.float32)
+    nw = (rng.standard_normal(rows) * 0.1).astype(np.float32)
+    d1 = torch.from_numpy(np.frombuffer(w1, np.uint8).copy()).cuda()
+    d2 = torch.from_numpy(np.frombuffer(w2, np.uint8).copy()).cuda()
+    hip.register_tiled_weights(ctox_hip.TensorDType(0), d1.data_ptr(), rows, cols)
+    hip.register_tiled_weights(ctox_hip.TensorDType(1), d2.data_ptr(), 256, rows)
+    da, dh, dw = dev(a), dev(hres), dev(nw)
+    delta = torch.empty(rows, device="cuda")
+    tiles = (rows + 15) // 16
+    sums = torch.full((tiles,), float("nan"), device="cuda")
+    tr = _Transform(da.data_ptr(), None, None, 1, 2 * cols, 0, cols, 0, 0.0, dh.data_ptr(), sums.data_ptr())
+    parts = ctypes.c_uint32(0)
+    st = lib.ctox_hip_transform_matvec_device(hip.handle, ctypes.byref(tr), 0, d1.data_ptr(), None, None,
+                                              delta.data_ptr(), rows, cols, 1, 1, ctypes.byref(parts), None)
+    assert st == 0, lib.ctox_hip_last_error()
+    torch.cuda.synchronize()
+    h = (hres + delta.cpu().numpy()).astype(np.float32)
+    want = np.array([np.sum(h[t * 16:(t + 1) * 16].astype(np.float64) ** 2) for t in range(tiles)])
+    np.testing.assert_allclose(sums.cpu().numpy(), want, rtol=1e-5)
+    outs = []
+    for use in (False, True):
+        xo = torch.empty(rows, device="cuda")
+        out = torch.empty(256, device="cuda")
+        st = lib.ctox_hip_norm_matvec_sums_device(hip.handle, dh.data_ptr(), delta.data_ptr(), 1, 0, xo.data_ptr(),
+                                                  dw.data_ptr(), 1e-6, None, 1, d2.data_ptr(), None, None,
+                                                  out.data_ptr(), 256, rows, 1,
+                                                  sums.data_ptr() if use else None, tiles if use else 0, None)
+        assert st == 0, lib.ctox_hip_last_error()
+        torch.cuda.synchronize()
+        assert np.array_equal(xo.cpu().numpy(), h)
+        outs.append(out.cpu().numpy())
+    y = orc.rms_norm_1p_weight(h, 1, rows, nw, 1e-6)
+    ref = orc.fused_matvec(1, w2, 256, rows, y)
+    for got in outs:
+        np.testing.assert_allclose(got, ref, rtol=1e-3, atol=1e-4 * float(np.abs(ref).max()))
+    np.testing.assert_allclose(outs[1], outs[0], rtol=1e-5, atol=1e-6 * float(np.abs(ref).max()))
+    # Unregistered weights cannot produce the sums: fails closed.
+    hip.unregister_tiled_weights(d1.data_ptr())
+    st = lib.ctox_hip_transform_matvec_device(hip.handle, ctypes.byref(tr), 0, d1.data_ptr(), None, None,
+                                              delta.data_ptr(), rows, cols, 1, 1, ctypes.byref(parts), None)
+    assert st == 5, st  # CTOX_ERR_UNSUPPORTED_OPERATION
+    hip.unregister_tiled_weights(d2.data_ptr())
