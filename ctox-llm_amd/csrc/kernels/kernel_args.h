@@ -389,6 +389,7 @@ struct KvPackArgs {
 // Fused attention-layer prep (ctox_attn_prep_gfx950): per-head q/k RMS norm,
 // partial RoPE and the Q4 page append of the new K/V rows.
 #define CTOX_ATTN_PREP_ROWS 8
+#define CTOX_ATTN_PREP_DESC_WORDS 32
 struct AttnPrepArgs {
     const float *proj;       // [rows][proj_stride]: per q head [q, gate] (2 hd), then k [kh hd], v [kh hd]
     const float *q_norm;     // [hd]
@@ -407,6 +408,9 @@ struct AttnPrepArgs {
     float theta;
     uint32_t slot[CTOX_ATTN_PREP_ROWS];  // Q4 page slot of row t
     uint32_t pos[CTOX_ATTN_PREP_ROWS];   // token index of row t inside that page
+    uint32_t *desc_dst;                  // page descriptor words to store (NULL: none)
+    uint32_t desc_words;                 // <= CTOX_ATTN_PREP_DESC_WORDS
+    uint32_t desc[CTOX_ATTN_PREP_DESC_WORDS];
 };
 
 struct KvDemoteArgs {

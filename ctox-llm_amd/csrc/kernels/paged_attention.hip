@@ -1210,12 +1210,15 @@ extern "C" __global__ __launch_bounds__(256) void ctox_paged_gqa_combine_gfx950(
 //   k head: the same with k_norm, then its four 64-value blocks packed into
 //           the row's Q4 page slot (as ctox_kv_pack_q4_gfx950);
 //   v head: packed as it is.
-// Replaces the norm, norm, rope, copy and pack launches of an attention
-// layer's K/V append (Q/src/decoder.rs:687-800, Q/src/kv_cache.rs:200-206).
+// Replaces the norm, norm, rope, copy, pack and descriptor-write launches of
+// an attention layer's K/V append (Q/src/decoder.rs:687-800,
+// Q/src/kv_cache.rs:200-206).
 // ---------------------------------------------------------------------------
 extern "C" __global__ __launch_bounds__(64) void ctox_attn_prep_gfx950(AttnPrepArgs a) {
     __shared__ float hs[PA_HD];
     const uint32_t job = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    // The cache's changed page descriptors, carried in the arguments.
+    if (job == 0 && t == 0 && a.desc_dst && lane < a.desc_words) a.desc_dst[lane] = a.desc[lane];
     const bool is_q = job < a.qh, is_k = !is_q && job < a.qh + a.kh;
     const uint32_t kk = is_q ? job : is_k ? job - a.qh : job - a.qh - a.kh;
     const float *row = a.proj + (size_t)t * a.proj_stride;

@@ -1617,9 +1617,13 @@ extern "C" ctox_status ctox_hip_attn_prep_device(ctox_hip_backend *b, const floa
                                                 size_t q_heads, size_t kv_heads, size_t head_dim, size_t rotary_dim,
                                                 uint64_t position, float theta, float eps, uint8_t *d_q4_pages,
                                                 uint32_t q4_page_bytes, const uint32_t *slots,
-                                                const uint32_t *positions_in_page, float *d_q_out, void *stream) {
-    if (!b || !d_proj || !d_q_norm || !d_k_norm || !d_q4_pages || !slots || !positions_in_page || !d_q_out)
+                                                const uint32_t *positions_in_page, float *d_q_out,
+                                                uint32_t *d_words_dst, const uint32_t *words, size_t word_count,
+                                                void *stream) {
+    if (!b || !d_proj || !d_q_norm || !d_k_norm || !d_q4_pages || !slots || !positions_in_page || !d_q_out ||
+        (word_count && (!d_words_dst || !words)))
         return fail(CTOX_ERR_SHAPE, "null argument");
+    if (word_count > CTOX_ATTN_PREP_DESC_WORDS) return fail(CTOX_ERR_SHAPE, "attention prep carries at most 32 words");
     if (head_dim != 256 || rows == 0 || rows > CTOX_ATTN_PREP_ROWS || q_heads == 0 || kv_heads == 0 ||
         q_heads + 2 * kv_heads > 65535 || rotary_dim == 0 || rotary_dim % 2 || rotary_dim > head_dim ||
         proj_stride < 2 * (q_heads + kv_heads) * head_dim || proj_stride > 0xffffffffu || !std::isfinite(theta) ||
@@ -1648,6 +1652,9 @@ extern "C" ctox_status ctox_hip_attn_prep_device(ctox_hip_backend *b, const floa
     a.q4_token_bytes = (uint32_t)token_bytes;
     a.eps = eps;
     a.theta = theta;
+    a.desc_dst = word_count ? d_words_dst : nullptr;
+    a.desc_words = (uint32_t)word_count;
+    for (size_t i = 0; i < word_count; i++) a.desc[i] = words[i];
     return launch(b->attn_prep, dim3((unsigned)(q_heads + 2 * kv_heads), (unsigned)rows), dim3(64),
                   pick_stream(b, stream), a, "ctox_attn_prep_gfx950");
 }

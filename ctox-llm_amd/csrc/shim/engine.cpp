@@ -397,11 +397,20 @@ ctox_status attn_forward(ctox_hip_engine *e, AttnLayer &a, uint32_t R, uint32_t 
     uint32_t slots[8], pos[8];
     if (R > 8) return efail(CTOX_ERR_SHAPE, "attention rows exceed 8");
     TRY(cache_reserve(e, a.cache, R, slots, pos));
-    TRY(ctox_hip_attn_prep_device(e->b, e->proj, e->Rq, a.q_norm, a.k_norm, R, qh, kvh, hd, e->c.rotary_dim, rope0,
-                                  e->c.rope_theta, e->c.rms_norm_epsilon, a.cache.q4, e->q4_page_bytes, slots, pos,
-                                  e->q, e->s));
+    // Demotion reads only pages older than the recent window, never the rows
+    // appended here, so it may precede the append; the changed descriptors
+    // then travel with the append's launch.
     if (!retain) TRY(cache_demote(e, a.cache));
-    TRY(cache_upload(e, a.cache));
+    Cache &c = a.cache;
+    const size_t words = (size_t)(c.pages - std::min(c.dirty, c.pages)) * 4;
+    const bool carry = words > 0 && words <= 32;
+    if (!carry) TRY(cache_upload(e, c));
+    TRY(ctox_hip_attn_prep_device(e->b, e->proj, e->Rq, a.q_norm, a.k_norm, R, qh, kvh, hd, e->c.rotary_dim, rope0,
+                                  e->c.rope_theta, e->c.rms_norm_epsilon, c.q4, e->q4_page_bytes, slots, pos, e->q,
+                                  carry ? (uint32_t *)(c.d_desc + c.dirty) : nullptr,
+                                  carry ? (const uint32_t *)(c.desc.data() + c.dirty) : nullptr, carry ? words : 0,
+                                  e->s));
+    if (carry) c.dirty = c.pages;
     const ctox_paged_gqa_params p = gqa_params(e, a.cache);
     TRY(ctox_hip_paged_gqa_device(e->b, e->q, a.cache.q2, a.cache.q4, a.cache.d_desc, &p, R, e->attn, e->s));
     ctox_input_transform x{e->attn, e->proj, nullptr, 3, qh * hd, e->Rq, 0, hd, 0.0f, nullptr, nullptr};

@@ -249,7 +249,7 @@ SIGNATURES = {
     "ctox_hip_causal_conv_rows_device": (_I32, [_P, _P, _SZ, _P, _P, _SZ, _SZ, _SZ, _P, _P]),
     "ctox_hip_kv_pack_q4_device": (_I32, [_P, _P, _P, _P, _SZ, _SZ, _U32, _U32, _U32, _P]),
     "ctox_hip_attn_prep_device": (_I32, [_P, _P, _SZ, _P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_uint64, ctypes.c_float,
-                                         ctypes.c_float, _P, _U32, _P, _P, _P, _P]),
+                                         ctypes.c_float, _P, _U32, _P, _P, _P, _P, _P, _SZ, _P]),
     "ctox_hip_kv_demote_device": (_I32, [_P, _P, _P, _SZ, _SZ, _P]),
     "ctox_hip_paged_gqa_device": (_I32, [_P, _P, _P, _P, _P, ctypes.POINTER(PagedGqaParams), _SZ, _P, _P]),
     "ctox_hip_fill_random_device": (_I32, [_P, _P, ctypes.c_uint64, _U32, ctypes.c_uint64, ctypes.c_float,
@@ -597,7 +597,8 @@ class HipBackend:
         ps = (ctypes.c_uint32 * len(positions_in_page))(*positions_in_page)
         _check(load_library().ctox_hip_attn_prep_device(self.handle, d_proj, proj_stride, d_q_norm, d_k_norm, rows,
                                                         q_heads, kv_heads, head_dim, rotary_dim, position, theta, eps,
-                                                        d_q4_pages, q4_page_bytes, sl, ps, d_q_out, stream))
+                                                        d_q4_pages, q4_page_bytes, sl, ps, d_q_out, None, None, 0,
+                                                        stream))
 
     def kv_demote_device(self, d_q4_page: int, d_q2_page: int, tokens: int, blocks_per_token: int,
                          stream: Optional[int] = None) -> None:

@@ -442,12 +442,15 @@ ctox_status ctox_hip_kv_pack_q4_device(ctox_hip_backend *backend, uint8_t *d_q4_
  * RoPE and KV-append steps of FullAttentionState::append
  * (Q/src/decoder.rs:687-800, Q/src/kv_cache.rs:200-206) and the CUDA
  * runtime's query-gate-norm-rope + pack pair (q2q4_fused_matvec_sm86.cu:1491-1546,
- * :1734-1799). head_dim 256. */
+ * :1734-1799). head_dim 256. Up to 32 further words (words[word_count],
+ * e.g. changed page descriptors) are stored to d_words_dst in the same
+ * launch, as ctox_hip_write_words_device would. */
 ctox_status ctox_hip_attn_prep_device(ctox_hip_backend *backend, const float *d_proj, size_t proj_stride,
                                       const float *d_q_norm, const float *d_k_norm, size_t rows, size_t q_heads,
                                       size_t kv_heads, size_t head_dim, size_t rotary_dim, uint64_t position,
                                       float theta, float eps, uint8_t *d_q4_pages, uint32_t q4_page_bytes,
                                       const uint32_t *slots, const uint32_t *positions_in_page, float *d_q_out,
+                                      uint32_t *d_words_dst, const uint32_t *words, size_t word_count,
                                       void *stream);
 /* Rewrite one Q4 page as Q2, byte-identical to QuantizedKvPage::requantize
  * (Q/src/kv_cache.rs:216-236). Replaces ctox_demote_paged_kv_q4_to_q2_sm86
