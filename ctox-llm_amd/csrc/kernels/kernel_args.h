@@ -139,6 +139,10 @@ struct TileMatvecArgs {
     uint64_t *partial;      // [chunks - 1][tiles * 16] when chunks > 1: f32 bits | seq << 32
     uint32_t seq;           // this launch's tag in the partial slots (never 0)
     uint32_t sq_n;          // xmode 1: entries of sq_in (0: reduce the row itself)
+    uint32_t parts_out;     // batch 1: write each chunk's s_out-scaled sum to output[chunk * out_stride + row]
+    uint32_t a_parts;       // xmode 2: input holds a_parts partial rows a_pstride floats apart (summed in order)
+    uint32_t a_pstride;
+    uint32_t pad3;
     const float *res_h;     // res_sq set: the residual the output is added to [rows]
     float *res_sq;          // NULL or [tiles]: sum over the tile's rows of (res_h + out)^2
     const float *sq_in;     // xmode 1: per-tile sums of squares of the residual row, or NULL

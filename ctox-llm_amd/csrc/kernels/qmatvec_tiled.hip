@@ -24,6 +24,8 @@
 
 // Cache policy of streamed weight loads: non-temporal.
 #define CTOX_LOAD_NT 2
+// Most producer chunk partials an in-kernel SwiGLU build sums.
+#define CTOX_MAX_IN_PARTS 6
 
 typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 
@@ -93,8 +95,32 @@ __device__ __forceinline__ void frag_group_loads(const TileMatvecArgs &a, uint32
     const uint32_t bo = xm == 2 ? a.off + col : (xm == 4 ? (col / dh) * 2 * dh + dh + col % dh : col);
     const __amdgpu_buffer_rsrc_t br = f32_rsrc(xm == 0 ? nullptr : bp, bn);
     const __amdgpu_buffer_rsrc_t wr = f32_rsrc(xm == 1 || xm == 3 ? a.xw : nullptr, xm == 1 ? cols : dh);
-    in.a = __builtin_amdgcn_raw_buffer_load_b128(ar, col * 4, 0, 0);
-    in.b = __builtin_amdgcn_raw_buffer_load_b128(br, bo * 4, 0, 0);
+    if (xm == 2 && a.a_parts > 1) {
+        // SwiGLU over a producer's chunk partials: a = sum_k part_k[c],
+        // b = sum_k part_k[off + c], in part order.
+        const __amdgpu_buffer_rsrc_t pr = f32_rsrc(a.input, (a.a_parts - 1) * a.a_pstride + a.off + cols);
+        v4i pa[CTOX_MAX_IN_PARTS], pb[CTOX_MAX_IN_PARTS];
+#pragma unroll
+        for (int k = 0; k < CTOX_MAX_IN_PARTS; k++) {
+            const uint32_t o = (uint32_t)k < a.a_parts ? k * a.a_pstride : 0x10000000u;
+            pa[k] = __builtin_amdgcn_raw_buffer_load_b128(pr, (o + col) * 4, 0, 0);
+            pb[k] = __builtin_amdgcn_raw_buffer_load_b128(pr, (o + a.off + col) * 4, 0, 0);
+        }
+        v4i sa = pa[0], sb = pb[0];
+#pragma unroll
+        for (int k = 1; k < CTOX_MAX_IN_PARTS; k++)
+            if ((uint32_t)k < a.a_parts)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    sa[i] = __float_as_int(__int_as_float(sa[i]) + __int_as_float(pa[k][i]));
+                    sb[i] = __float_as_int(__int_as_float(sb[i]) + __int_as_float(pb[k][i]));
+                }
+        in.a = sa;
+        in.b = sb;
+    } else {
+        in.a = __builtin_amdgcn_raw_buffer_load_b128(ar, col * 4, 0, 0);
+        in.b = __builtin_amdgcn_raw_buffer_load_b128(br, bo * 4, 0, 0);
+    }
     in.w = __builtin_amdgcn_raw_buffer_load_b128(wr, (xm == 3 ? col % (dh ? dh : 1) : col) * 4, 0, 0);
     in.s = __builtin_amdgcn_raw_buffer_load_b128(sr, col * sbytes, 0, 0);
 }
@@ -437,6 +463,11 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
         const float y = mine && row < a.rows ? tile_epilogue(val / C::DEN, row, a) : 0.0f;
         if (mine && row < a.rows) a.output[row] = y;
         residual_tile_sum(a, tile, row, mine, y, j);
+        return;
+    }
+    if (a.parts_out) {
+        // Chunk partials for a consumer that adds them (no combine here).
+        if (mine && row < a.rows) a.output[(size_t)c * a.out_stride + row] = tile_epilogue(val / C::DEN, row, a);
         return;
     }
     const size_t cstride = (size_t)a.tiles * CTOX_TILE_ROWS;

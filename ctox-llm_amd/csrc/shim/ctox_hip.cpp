@@ -355,6 +355,8 @@ struct TileXform {
     float *res_sq = nullptr;       // producer: per-tile sums of (res_h + out)^2
     const float *sq_in = nullptr;  // consumer (xmode 1): those sums
     uint32_t sq_n = 0;
+    bool parts_out = false;        // batch 1: chunk partials to output [chunks][rows]
+    uint32_t a_parts = 0, a_pstride = 0;  // xmode 2: input as producer chunk partials
 };
 
 ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows, size_t columns,
@@ -499,6 +501,10 @@ ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy 
         a.res_sq = xf->res_sq;
         a.sq_in = xf->sq_in;
         a.sq_n = xf->sq_in ? xf->sq_n : 0u;
+        a.parts_out = xf->parts_out && t.chunks > 1 ? 1u : 0u;
+        a.out_stride = (uint32_t)rows;  // part stride of parts_out
+        a.a_parts = xf->a_parts;
+        a.a_pstride = xf->a_pstride;
     }
     hipFunction_t f = d_input ? b->tilex[q4][u - 1] : b->tile[q4][u - 1];
     return launch(f, dim3((unsigned)((waves + 3) / 4)), dim3(256), s, a, "ctox_q*_mv_tile*_gfx950");
@@ -947,6 +953,20 @@ extern "C" ctox_status ctox_hip_norm_matvec_sums_device(ctox_hip_backend *b, con
                                                        float *d_output, uint32_t rows, uint32_t columns,
                                                        uint32_t batch, const float *d_sums, uint32_t sum_count,
                                                        void *stream) {
+    return ctox_hip_norm_matvec_parts_device(b, d_x, d_delta, delta_parts, delta_part_stride, d_x_out, d_norm_w, eps,
+                                             d_norm_out, dtype, d_weights, d_s_in, d_s_out, d_output, rows, columns,
+                                             batch, d_sums, sum_count, 1, nullptr, stream);
+}
+
+extern "C" ctox_status ctox_hip_norm_matvec_parts_device(ctox_hip_backend *b, const float *d_x, const float *d_delta,
+                                                        uint32_t delta_parts, size_t delta_part_stride,
+                                                        float *d_x_out, const float *d_norm_w, float eps,
+                                                        float *d_norm_out, int32_t dtype, const void *d_weights,
+                                                        const uint16_t *d_s_in, const uint16_t *d_s_out,
+                                                        float *d_output, uint32_t rows, uint32_t columns,
+                                                        uint32_t batch, const float *d_sums, uint32_t sum_count,
+                                                        uint32_t max_parts, uint32_t *parts, void *stream) {
+    if (parts) *parts = 1;
     if (d_sums && (sum_count != (columns + CTOX_TILE_ROWS - 1) / CTOX_TILE_ROWS || sum_count > 512))
         return fail(CTOX_ERR_SHAPE, "residual sums: one per 16 columns of the row, at most 512");
     if (!b || !d_x || !d_norm_w || !d_weights || !d_output || (d_delta && !d_x_out))
@@ -977,6 +997,11 @@ extern "C" ctox_status ctox_hip_norm_matvec_sums_device(ctox_hip_backend *b, con
             xf.eps = eps;
             xf.sq_in = d_sums;
             xf.sq_n = sum_count;
+            // Chunk partials for a consumer that adds them, when it takes that many.
+            if (parts && max_parts > 1 && t->chunks <= max_parts) {
+                xf.parts_out = true;
+                *parts = t->chunks;
+            }
             return run_tile_matvec(b, dtype, *t, rows, columns, d_s_out, d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE,
                                    nullptr, d_output, 0, s, d_x, d_s_in, d_s_in ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, &xf);
         }
@@ -1017,6 +1042,8 @@ extern "C" ctox_status ctox_hip_transform_matvec_device(ctox_hip_backend *b, con
         (x->mode == 2 && !x->w) || (x->res_sums && !x->res_h))
         return fail(CTOX_ERR_SHAPE, "null argument");
     if (x->mode < 1 || x->mode > 3) return fail(CTOX_ERR_SHAPE, "unknown input transform %u", x->mode);
+    if (x->a_parts > 1 && (x->mode != 1 || x->a_parts > 6 || x->a_part_stride < x->off + columns))
+        return fail(CTOX_ERR_SHAPE, "input partials: swiglu only, at most 6, a_part_stride covering a row");
     if (dtype != CTOX_DTYPE_Q2B64 && dtype != CTOX_DTYPE_Q4B64)
         return fail(CTOX_ERR_UNSUPPORTED_DTYPE, "transform-matvec takes pure Q2_B64 or Q4_B64 weights");
     if (rows == 0 || columns == 0 || columns % kBlockLen) return fail(CTOX_ERR_SHAPE, "transform-matvec dimensions");
@@ -1042,12 +1069,14 @@ extern "C" ctox_status ctox_hip_transform_matvec_device(ctox_hip_backend *b, con
             xf.eps = x->eps;
             xf.res_h = x->res_h;
             xf.res_sq = x->res_sums;
+            xf.a_parts = x->a_parts > 1 ? x->a_parts : 0;
+            xf.a_pstride = x->a_part_stride;
             return run_tile_matvec(b, dtype, *t, rows, columns, d_s_out, d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE,
                                    nullptr, d_output, 0, s, x->a, d_s_in, d_s_in ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, &xf);
         }
     }
-    if (x->res_sums)
-        return fail(CTOX_ERR_UNSUPPORTED_OPERATION, "residual sums need batch 1 on registered weights");
+    if (x->res_sums || x->a_parts > 1)
+        return fail(CTOX_ERR_UNSUPPORTED_OPERATION, "residual sums and input partials need batch 1 on registered weights");
     ctox_status st = ensure(b, b->xa[layout], blocks * batch * 192, false);
     if (!st) st = ensure(b, b->xc[layout], blocks * batch * 4 * sizeof(float), false);
     if (st) return st;

@@ -208,12 +208,12 @@ ctox_status matvec(ctox_hip_engine *e, const Mat &m, const float *in, float *out
 // The residual stream ping-pongs between e->hid and e->hid2: with a delta the
 // sum goes to the other buffer, which becomes the stream.
 ctox_status norm_mv(ctox_hip_engine *e, const float *delta, const float *w, uint32_t rows, const Mat &m, float *out,
-                    float *norm_out = nullptr) {
+                    float *norm_out = nullptr, uint32_t max_parts = 1, uint32_t *parts = nullptr) {
     const bool sums = delta && rows == 1 && e->rsq_delta == delta && e->rsq_hid == e->hid && e->delta_parts == 1;
     e->rsq_delta = e->rsq_hid = nullptr;
-    TRY(ctox_hip_norm_matvec_sums_device(e->b, e->hid, delta, e->delta_parts, (size_t)rows * e->H, delta ? e->hid2 : nullptr,
+    TRY(ctox_hip_norm_matvec_parts_device(e->b, e->hid, delta, e->delta_parts, (size_t)rows * e->H, delta ? e->hid2 : nullptr,
                                     w, e->c.rms_norm_epsilon, norm_out, m.dtype, m.w, m.s_in, m.s_out, out, m.rows,
-                                    m.cols, rows, sums ? e->rsq : nullptr, sums ? (e->H + 15) / 16 : 0, e->s));
+                                    m.cols, rows, sums ? e->rsq : nullptr, sums ? (e->H + 15) / 16 : 0, max_parts, parts, e->s));
     if (delta) std::swap(e->hid, e->hid2);
     return CTOX_OK;
 }
@@ -413,7 +413,7 @@ ctox_status attn_forward(ctox_hip_engine *e, AttnLayer &a, uint32_t R, uint32_t 
     if (carry) c.dirty = c.pages;
     const ctox_paged_gqa_params p = gqa_params(e, a.cache);
     TRY(ctox_hip_paged_gqa_device(e->b, e->q, a.cache.q2, a.cache.q4, a.cache.d_desc, &p, R, e->attn, e->s));
-    ctox_input_transform x{e->attn, e->proj, nullptr, 3, qh * hd, e->Rq, 0, hd, 0.0f, nullptr, nullptr};
+    ctox_input_transform x{e->attn, e->proj, nullptr, 3, qh * hd, e->Rq, 0, hd, 0.0f, nullptr, nullptr, 0, 0};
     return delta_mv(e, x, a.o, delta, R);
 }
 
@@ -437,13 +437,15 @@ ctox_status gdn_forward(ctox_hip_engine *e, GdnLayer &g, uint32_t R, float *delt
     float *proj = keep_rows ? g.proj : e->proj;  // the in-projection, already computed (norm_mv)
     float *ld = keep_rows ? g.ld : e->ld, *beta = keep_rows ? g.beta : e->beta;
     TRY(gdn_core(e, g, proj, R, ld, beta, false));
-    ctox_input_transform x{e->core, proj + e->C, g.gnorm, 2, e->Vw, e->Rin, 0, dv, e->c.rms_norm_epsilon, nullptr, nullptr};
+    ctox_input_transform x{e->core, proj + e->C, g.gnorm, 2, e->Vw, e->Rin, 0, dv, e->c.rms_norm_epsilon, nullptr, nullptr, 0, 0};
     return delta_mv(e, x, g.out, delta, R);
 }
 
 ctox_status mlp_forward(ctox_hip_engine *e, Mlp &m, uint32_t R, const float *delta_in, float *delta_out) {
-    TRY(norm_mv(e, delta_in, m.norm, R, m.gate_up, e->gu));
-    ctox_input_transform x{e->gu, nullptr, nullptr, 1, 2 * e->I, 0, e->I, 0, 0.0f, nullptr, nullptr};
+    // Single row: gate|up leaves its chunk partials and down's SwiGLU build adds them.
+    uint32_t parts = 1;
+    TRY(norm_mv(e, delta_in, m.norm, R, m.gate_up, e->gu, nullptr, R == 1 ? 6 : 1, &parts));
+    ctox_input_transform x{e->gu, nullptr, nullptr, 1, 2 * e->I, 0, e->I, 0, 0.0f, nullptr, nullptr, parts, 2 * e->I};
     return delta_mv(e, x, m.down, delta_out, R);
 }
 
@@ -610,7 +612,7 @@ extern "C" ctox_status ctox_hip_engine_create(ctox_hip_backend *b, const ctox_en
         (st = dalloc_t(e, &e->core, R * e->Vw)) || (st = dalloc_t(e, &e->coren, R * e->Vw)) ||
         (st = dalloc_t(e, &e->delta, 16 * R * e->H)) || (st = dalloc_t(e, &e->q, R * qh * hd)) ||
         (st = dalloc_t(e, &e->k, R * e->kvw)) || (st = dalloc_t(e, &e->v, R * e->kvw)) ||
-        (st = dalloc_t(e, &e->attn, R * qh * hd)) || (st = dalloc_t(e, &e->gu, R * 2 * e->I)) ||
+        (st = dalloc_t(e, &e->attn, R * qh * hd)) || (st = dalloc_t(e, &e->gu, std::max<size_t>(R, 6) * 2 * e->I)) ||
         (st = dalloc_t(e, &e->act, R * e->I)) || (st = dalloc_t(e, &e->fin, R * e->H)) ||
         (st = dalloc_t(e, &e->logits, R * e->V)) || (st = dalloc_t(e, &e->ld, R * Hv)) ||
         (st = dalloc_t(e, &e->beta, R * Hv)) || (st = dalloc_t(e, &e->fcin, R * 2 * e->H)) ||

@@ -265,6 +265,8 @@ SIGNATURES = {
     "ctox_hip_transform_matvec_device": (_I32, [_P, _P, _I32, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _P, _P]),
     "ctox_hip_norm_matvec_sums_device": (_I32, [_P, _P, _P, _U32, _SZ, _P, _P, ctypes.c_float, _P, _I32, _P, _P, _P, _P,
                                                 _U32, _U32, _U32, _P, _U32, _P]),
+    "ctox_hip_norm_matvec_parts_device": (_I32, [_P, _P, _P, _U32, _SZ, _P, _P, ctypes.c_float, _P, _I32, _P, _P, _P,
+                                                 _P, _U32, _U32, _U32, _P, _U32, _U32, _P, _P]),
     # decode engine (struct arguments passed by reference)
     "ctox_hip_engine_create": (_I32, [_P, _P, ctypes.c_uint64, ctypes.POINTER(_P)]),
     "ctox_hip_engine_destroy": (None, [_P]),

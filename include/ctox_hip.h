@@ -238,6 +238,22 @@ ctox_status ctox_hip_norm_matvec_sums_device(ctox_hip_backend *backend, const fl
                                              float *d_output, uint32_t rows, uint32_t columns, uint32_t batch,
                                              const float *d_sums, uint32_t sum_count, void *stream);
 
+/* ctox_hip_norm_matvec_sums_device whose output may be left as partial
+ * rows: on the batch-1 registered-weights path, when the K range is split
+ * into n <= max_parts chunks, d_output receives n rows [n][rows] (each
+ * chunk's sum times s_out) whose sum in order is the projection, *parts = n,
+ * and the cross-chunk combine is skipped; otherwise the result itself and
+ * *parts = 1. For a consumer that adds them (ctox_input_transform::a_parts).
+ * No crate counterpart (the crate's projection returns finished rows,
+ * Q/src/backend/mod.rs:153-169). */
+ctox_status ctox_hip_norm_matvec_parts_device(ctox_hip_backend *backend, const float *d_x, const float *d_delta,
+                                              uint32_t delta_parts, size_t delta_part_stride, float *d_x_out,
+                                              const float *d_norm_w, float eps, float *d_norm_out, int32_t dtype,
+                                              const void *d_weights, const uint16_t *d_s_in, const uint16_t *d_s_out,
+                                              float *d_output, uint32_t rows, uint32_t columns, uint32_t batch,
+                                              const float *d_sums, uint32_t sum_count, uint32_t max_parts,
+                                              uint32_t *parts, void *stream);
+
 /* The projection of a value computed on the fly from its producer's output,
  * staged in the same pass (rows of a at t * a_stride, of b at t * b_stride):
  *   mode 1 swiglu (Q/src/reference.rs:96-112): silu(a[c]) * a[off + c];
@@ -259,6 +275,11 @@ typedef struct {
      * adds and normalizes in one pass, Q/src/decoder.rs:636-680). */
     const float *res_h;
     float *res_sums;
+    /* Mode 1 only, batch 1 on registered weights: a holds a_parts (2..6)
+     * partial rows a_part_stride floats apart whose sum (in order) is the
+     * gate|up row, as ctox_hip_norm_matvec_parts_device leaves them (0 or 1:
+     * a is the row itself). */
+    uint32_t a_parts, a_part_stride;
 } ctox_input_transform;
 /* split_k != 0 lets a batch-1 projection split its K range into one partial
  * per 1 KiB slice of a row (balancing few-row, long-K matrices over the
