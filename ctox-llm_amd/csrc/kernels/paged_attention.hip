@@ -776,31 +776,45 @@ __device__ __forceinline__ void pa_tile16(const GqaArgs &a, LDS &L, const int8_t
     }
 }
 
+// The query values one thread of pa_prep_queries works on: iteration r is
+// (query, block, quarter) i = threadIdx.x + 256 r, its 16 values (zeros past
+// the queries). Loaded apart from the computation so that callers can issue
+// other loads in between.
 template <int R>
-__device__ __forceinline__ void pa_prep_queries(const GqaArgs &a, uint32_t h, int8_t *qb, float (*qsc)[4],
-                                                int32_t (*xs)[4][3]) {
-    // Query fixed point per 64-dim block: X = rint(q 2^E) with |X| <= 2^21
-    // (2^E from the block's max |q|), split into three balanced int8 limbs
-    // X = l0 + 256 l1 + 65536 l2, dims reordered to the K operand's order
-    // within each 16. One thread per (query, block); it also leaves 2^-E and
-    // the limb sums for the score epilogue.
-    for (uint32_t i = threadIdx.x; i < R * 16 * 16; i += 256) {
-        // Four consecutive lanes share one (query, block), a quarter of it each.
+__device__ __forceinline__ void pa_prep_load(const GqaArgs &a, uint32_t h, float (&qv)[R][16]) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const uint32_t i = threadIdx.x + 256 * r;
         const uint32_t qi = i / 16, b = (i / 4) % 4, part = i % 4;
-        // The quarter's 16 values in registers (one load each; zeros past the queries).
         const bool valid = qi < a.queries;
         const uint32_t t = valid ? qi / a.group : 0, g = valid ? qi - t * a.group : 0;
         const float4 *qp = (const float4 *)(a.query + ((size_t)t * a.query_heads + h * a.group + g) * PA_HD + 64 * b +
                                             16 * part);
-        float qv[16];
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const float4 v4 = qp[k];
-            qv[4 * k] = valid ? v4.x : 0.0f;
-            qv[4 * k + 1] = valid ? v4.y : 0.0f;
-            qv[4 * k + 2] = valid ? v4.z : 0.0f;
-            qv[4 * k + 3] = valid ? v4.w : 0.0f;
+            qv[r][4 * k] = valid ? v4.x : 0.0f;
+            qv[r][4 * k + 1] = valid ? v4.y : 0.0f;
+            qv[r][4 * k + 2] = valid ? v4.z : 0.0f;
+            qv[r][4 * k + 3] = valid ? v4.w : 0.0f;
         }
+    }
+}
+
+// Query fixed point per 64-dim block: X = rint(q 2^E) with |X| <= 2^21
+// (2^E from the block's max |q|), split into three balanced int8 limbs
+// X = l0 + 256 l1 + 65536 l2, dims reordered to the K operand's order
+// within each 16. One thread per (query, block, quarter); it also leaves 2^-E
+// and the limb sums for the score epilogue.
+template <int R>
+__device__ __forceinline__ void pa_prep_compute(const GqaArgs &a, const float (&q)[R][16], int8_t *qb,
+                                                float (*qsc)[4], int32_t (*xs)[4][3]) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const uint32_t i = threadIdx.x + 256 * r;
+        // Four consecutive lanes share one (query, block), a quarter of it each.
+        const uint32_t qi = i / 16, b = (i / 4) % 4, part = i % 4;
+        const float *qv = q[r];
         float mx = 0.0f;
 #pragma unroll
         for (int d = 0; d < 16; d++) mx = fmaxf(mx, fabsf(qv[d]));
@@ -846,6 +860,13 @@ __device__ __forceinline__ void pa_prep_queries(const GqaArgs &a, uint32_t h, in
     }
 }
 
+template <int R>
+__device__ __forceinline__ void pa_prep_queries(const GqaArgs &a, uint32_t h, int8_t *qb, float (*qsc)[4],
+                                                int32_t (*xs)[4][3]) {
+    float q[R][16];
+    pa_prep_load<R>(a, h, q);
+    pa_prep_compute<R>(a, q, qb, qsc, xs);
+}
 
 // LDS of the page-aligned kernel: query limbs and the per-wave K/V stages
 // while tiles run, overlaid afterwards by the merge area of waves 1..3.
@@ -878,9 +899,16 @@ __device__ __forceinline__ void paged_gqa_partial16(const GqaArgs &a) {
     const uint32_t gw = split * 4 + wave;
     const uint32_t t0 = gw * a.tiles_per_wave;
     const uint32_t t1 = min(t0 + a.tiles_per_wave, a.tiles);
-    // The wave's page descriptors load together with the queries.
+    // The wave's page descriptors load together with the queries; the first
+    // tile's loads go out (they need only the descriptors) before the query
+    // limbs are computed.
     const uint4 dsc = pa_load_descs(a, t0, t1, lane);
-    pa_prep_queries<R>(a, h, L.u.run.limbs, L.qsc, L.xs);
+    float qv[R][16];
+    pa_prep_load<R>(a, h, qv);
+    PaStage sg;
+    PaTile PA = pa_tile_of(a, dsc, 0);
+    pa_issue_stage(a, PA, t0 * 16, h, lane, sg);
+    pa_prep_compute<R>(a, qv, L.u.run.limbs, L.qsc, L.xs);
     PaState<R> st;
 #pragma unroll
     for (int r = 0; r < R; r++) {
@@ -892,10 +920,7 @@ __device__ __forceinline__ void paged_gqa_partial16(const GqaArgs &a) {
         for (int j = 0; j < 16; j++) st.o[r][j] = pa_v4f{0.0f, 0.0f, 0.0f, 0.0f};
     }
     // The first tile's loads stay in flight across the (LDS-only) barrier.
-    PaStage sg;
-    PaTile PA = pa_tile_of(a, dsc, 0);
     uint32_t *stage = L.u.run.stage[wave];
-    pa_issue_stage(a, PA, t0 * 16, h, lane, sg);
     lds_barrier();
 #pragma unroll
     for (int r = 0; r < R; r++)
