@@ -368,3 +368,42 @@ def test_registered_tiled_raw_launch(hip, orc, dtype, rows, cols):
                             None, dy.data_ptr(), rows, cols, ctox_hip.Activation.Identity, 1, stream)
     torch.cuda.synchronize()
     check(dy.cpu().numpy()[0], ref, "crate layout after unregister")
+
+
+@pytest.mark.gpu
+def test_artifact_mixed_recovered_upload(hip, orc, tmp_path):
+    """A v2 `.ctoxq` mixed tensor with FP16 recovery scales, mapped and uploaded to HBM
+    (models/qwen38_27b/src/loader.rs:362-402), equals the oracle on the same bytes."""
+    from ctox_hip import artifact as A
+    say("case artifact mixed recovered upload")
+    torch = _torch()
+    T = ctox_hip.TensorDType
+    cols, r2, r4 = 1024, 48, 80
+    q2 = synth.random_matrix(0, r2, cols, 11)
+    q4 = synth.random_matrix(1, r4, cols, 12)
+    rng = np.random.default_rng(13)
+    s_in = (0.5 + rng.random(cols)).astype("<f2")
+    s_out = (0.5 + rng.random(r2 + r4)).astype("<f2")
+    segs = [ctox_hip.QuantSegment(0, 0, r2, T.Q2B64, 0, q2.size),
+            ctox_hip.QuantSegment(1, r2, r2 + r4, T.Q4B64, q2.size, q4.size)]
+    path = tmp_path / "mixed.ctoxq"
+    A.ArtifactBuilder("test/qwen", "0123456789abcdef", "gfx950", 256, [
+        A.PackedTensor("w", T.MixedQ2Q4B64, [r2 + r4, cols], np.concatenate([q2, q4]).tobytes(), segs),
+        A.PackedTensor("w.s_in", T.F16, [cols], s_in.tobytes()),
+        A.PackedTensor("w.s_out", T.F16, [r2 + r4], s_out.tobytes()),
+    ]).write_new(path)
+    art = A.ModelArtifact.open(path, A.ChecksumPolicy.AllTensors)
+    m = A.upload_matrix(hip, art, "w")
+    xs = synth.activation("normal", cols, 14, batch=2)
+    dx = torch.from_numpy(np.ascontiguousarray(xs)).cuda()
+    dy = torch.empty((xs.shape[0], r2 + r4), dtype=torch.float32, device="cuda")
+    m.dispatch(dx.data_ptr(), xs.shape[0], dy.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got = dy.cpu().numpy()
+    m.close()
+    raw = np.concatenate([q2, q4]).tobytes()
+    for b in range(xs.shape[0]):
+        ref = orc.fused_matvec(2, raw, r2 + r4, cols, xs[b], s_in=("f16le", s_in.view(np.uint8)),
+                               s_out=("f16le", s_out.view(np.uint8)),
+                               segments=[(0, 0, r2, 0, 0, q2.size), (1, r2, r2 + r4, 1, q2.size, q4.size)])
+        check(got[b], ref, f"artifact mixed batch row {b}")
