@@ -30,7 +30,8 @@ def test_f16_narrowing_is_round_to_nearest_even(orc):
         (np.arange(1, 500, dtype=np.float32) + 0.5) * 2.0 ** -24,  # subnormal ties
         np.array([65504.0, 65519.0, 65520.0, 1e6, -1e6, 0.0, -0.0, 2.0 ** -25, 2.0 ** -26], dtype=np.float32),
     ]).astype(np.float32)
-    ref = xs.astype(np.float16).view(np.uint16)
+    with np.errstate(over="ignore"):  # 65520 and 1e6 round to infinity on purpose
+        ref = xs.astype(np.float16).view(np.uint16)
     got = np.array([orc.f32_to_f16(float(x)) for x in xs], dtype=np.uint16)
     assert np.array_equal(got, ref)
 
