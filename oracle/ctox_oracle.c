@@ -1003,19 +1003,42 @@ static size_t cumulative_pick(const float *w, size_t n, float draw) {
 int orc_mtp_accept_sample(const float *draft, const float *target, const float *bonus,
                           const uint32_t *tokens, size_t drafts, size_t vocab, float temperature,
                           orc_pcg32 *rng, uint32_t *next_token, uint32_t *n_accepted) {
+    return orc_mtp_accept_sample_restricted(draft, NULL, vocab, target, bonus, tokens, drafts, vocab,
+                                            temperature, rng, next_token, n_accepted);
+}
+
+/* The same with restricted draft rows (DraftDistribution::Restricted,
+ * Q/src/engine.rs:151-200): draft row i holds `draft_n` scores for the
+ * strictly increasing token IDs `draft_ids` (Q/src/decoder.rs:597-608 rules);
+ * q is their temperature softmax and 0 for every other token. draft_ids NULL
+ * means a full draft row (draft_n == vocab). */
+int orc_mtp_accept_sample_restricted(const float *draft, const uint32_t *draft_ids, size_t draft_n,
+                                     const float *target, const float *bonus, const uint32_t *tokens,
+                                     size_t drafts, size_t vocab, float temperature, orc_pcg32 *rng,
+                                     uint32_t *next_token, uint32_t *n_accepted) {
     if (!(temperature > 0.0f) || !finite_f(temperature) || vocab == 0) return ORC_ERR_INVALID_ARTIFACT;
+    if (draft_n == 0 || (!draft_ids && draft_n != vocab)) return ORC_ERR_SHAPE;
+    if (draft_ids)
+        for (size_t j = 0; j < draft_n; j++)
+            if (draft_ids[j] >= vocab || (j && draft_ids[j - 1] >= draft_ids[j])) return ORC_ERR_SHAPE;
     float invt = 1.0f / temperature;
     float *p = (float *)malloc(vocab * sizeof(float));
-    float *q = (float *)malloc(vocab * sizeof(float));
+    float *q = (float *)calloc(vocab, sizeof(float));
+    float *qr = (float *)malloc(draft_n * sizeof(float));
     int st = ORC_OK;
     uint32_t acc = 0;
     for (size_t i = 0; i < drafts; i++) {
         if ((st = softmax_t(target + i * vocab, vocab, invt, p))) goto done;
-        if ((st = softmax_t(draft + i * vocab, vocab, invt, q))) goto done;
+        if ((st = softmax_t(draft + i * draft_n, draft_n, invt, qr))) goto done;
+        for (size_t j = 0; j < draft_n; j++) q[draft_ids ? draft_ids[j] : j] = qr[j];
         uint32_t d = tokens[i];
         if (d >= vocab) { st = ORC_ERR_SHAPE; goto done; }
         float u = orc_pcg32_next_f32(rng);
-        if (u * q[d] < p[d]) { acc++; continue; }
+        if (u * q[d] < p[d]) {
+            acc++;
+            for (size_t j = 0; j < draft_n; j++) q[draft_ids ? draft_ids[j] : j] = 0.0f;
+            continue;
+        }
         for (size_t t = 0; t < vocab; t++) { float r = p[t] - q[t]; p[t] = r > 0.0f ? r : 0.0f; }
         float u2 = orc_pcg32_next_f32(rng);
         *next_token = (uint32_t)cumulative_pick(p, vocab, u2);
@@ -1032,5 +1055,6 @@ int orc_mtp_accept_sample(const float *draft, const float *target, const float *
 done:
     free(p);
     free(q);
+    free(qr);
     return st;
 }

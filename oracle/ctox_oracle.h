@@ -152,6 +152,12 @@ int orc_mtp_accept_sample(const float *draft_logits, const float *target_logits,
                           const float *bonus_logits, const uint32_t *draft_tokens,
                           size_t drafts, size_t vocab, float temperature, orc_pcg32 *rng,
                           uint32_t *next_token, uint32_t *n_accepted);
+/* The same with restricted draft rows of draft_n scores over draft_ids. */
+int orc_mtp_accept_sample_restricted(const float *draft_logits, const uint32_t *draft_ids, size_t draft_n,
+                                     const float *target_logits, const float *bonus_logits,
+                                     const uint32_t *draft_tokens, size_t drafts, size_t vocab,
+                                     float temperature, orc_pcg32 *rng, uint32_t *next_token,
+                                     uint32_t *n_accepted);
 
 #ifdef __cplusplus
 }

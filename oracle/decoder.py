@@ -10,9 +10,13 @@ Follows Q/src/decoder.rs (Q = models/qwen38_27b):
     (:687-800), decoder_mlp_residual (:636-670), final norm, LM head;
   * mtp_final_hidden (:1009-1046) and the prefill-time MTP advance
     (:1248-1261);
+  * restricted_logits_from_final_hidden (:589-627): the draft head over the
+    release-bound draft token IDs, one recovered_row_matvec per ID;
   * the speculative step the engine runs (the crate's executor is greedy
     only, so this is the build's specification, stated once here): k drafts
-    where draft i + 1 is sampled at temperature T from MTP(x_i, g_i) with
+    where draft i + 1 is sampled at temperature T from MTP(x_i, g_i) (over
+    the draft vocabulary when one is bound, as the CUDA MTP4 flow drafts,
+    Q/src/backend/cuda_graph.rs:4501-4509) with
     x_0 = token, g_0 = the previous target hidden, x_i = d_i and g_i the MTP
     hidden of step i; one target pass over [token, d1..dk] with KV pushes
     that retain Q4 pages (push_retaining_q4, kv_cache.rs:372-381); the
@@ -37,10 +41,21 @@ from . import oracle as orc
 from . import paged_kv as pk
 
 
+def check_draft_ids(ids, vocab: int) -> np.ndarray:
+    """The canonical draft vocabulary: non-empty, strictly increasing, inside
+    the vocabulary (Q/src/decoder.rs:597-608, Q/src/release.rs:414-431)."""
+    ids = np.asarray(ids, dtype=np.int64).reshape(-1)
+    if ids.size == 0 or np.any(ids[1:] <= ids[:-1]) or ids[0] < 0 or ids[-1] >= vocab:
+        raise orc.OracleError(1)
+    return ids.astype(np.uint32)
+
+
 class OracleDecoder:
-    def __init__(self, cfg: dict, tensor):
-        """cfg: EngineConfig.as_dict(); tensor(name) -> the engine tensor dict."""
+    def __init__(self, cfg: dict, tensor, draft_ids=None):
+        """cfg: EngineConfig.as_dict(); tensor(name) -> the engine tensor dict;
+        draft_ids: the release-bound MTP draft vocabulary (None: full head)."""
         self.c = cfg
+        self.draft_ids = None if draft_ids is None else check_draft_ids(draft_ids, cfg["vocab_size"])
         self.t = {}
         self.fetch = tensor
         c = cfg
@@ -63,6 +78,8 @@ class OracleDecoder:
 
     def _cache(self):
         c = self.c
+        if (self.kvh * self.hd) % orc.BLOCK_LEN:  # FullAttentionState::new (decoder.rs:171-195)
+            return pk.DenseKvCache(c["max_tokens"], self.kvh * self.hd)
         return pk.PagedKvCache(c["max_tokens"], self.kvh * self.hd, c["page_tokens"], c["sink_tokens"],
                                c["recent_tokens"])
 
@@ -83,6 +100,8 @@ class OracleDecoder:
 
     def embedding(self, token):
         m = self.w("embed")
+        if not 0 <= token < m["rows"]:
+            raise orc.OracleError(1)
         rb = m["cols"] // 64 * (34 if m["dtype"] == orc.Q4B64 else 18)
         s_out = float(np.frombuffer(m["s_out"].tobytes(), np.float16)[token])
         return orc.recovered_row(m["dtype"], m["data"][token * rb:(token + 1) * rb], m["cols"],
@@ -139,15 +158,41 @@ class OracleDecoder:
         self.position += 1
         return self.matvec("lm_head", fin), fin
 
+    def restricted_logits(self, fin, ids):
+        """restricted_logits_from_final_hidden (Q/src/decoder.rs:589-627):
+        x' = fin * s_in once, then one recovered_row_matvec per token ID."""
+        m = self.w("lm_head")
+        ids = check_draft_ids(ids, m["rows"])
+        s_in = np.frombuffer(m["s_in"].tobytes(), np.float16).astype(np.float32)
+        s_out = np.frombuffer(m["s_out"].tobytes(), np.float16).astype(np.float32)
+        x = (np.asarray(fin, np.float32) * s_in).astype(np.float32)
+        rb = m["cols"] // 64 * (34 if m["dtype"] == orc.Q4B64 else 18)
+        return np.array([orc.recovered_row_matvec(m["dtype"], m["data"][int(t) * rb:(int(t) + 1) * rb], x,
+                                                  float(s_out[t])) for t in ids], np.float32)
+
+    def attention_residual(self, prefix, h, position, cache):
+        """full_attention_residual (Q/src/decoder.rs:676-800): the position
+        must be the cache's next token."""
+        if position != cache.tokens():
+            raise orc.OracleError(1)
+        return h + self.attention(prefix, self.norm(h, f"{prefix}.norm"), position, cache, False)
+
     def mtp(self, token, prev, rope_pos, retain, logits=True):
-        """mtp_final_hidden (Q/src/decoder.rs:1009-1046) (+ the shared LM head)."""
+        """mtp_final_hidden (Q/src/decoder.rs:1009-1046) (+ the shared LM head,
+        restricted to the draft vocabulary when one is bound)."""
+        if rope_pos != self.mtp_cache.tokens() + 1:  # decoder.rs:1017-1024
+            raise orc.OracleError(1)
         e = self.norm(self.embedding(token), "mtp.norm_emb")
         hn = self.norm(prev, "mtp.norm_hid")
         h = self.matvec("mtp.fc", np.concatenate([e, hn]))
         x = self.norm(h, "mtp.attn_norm")
         h = self.mlp("mtp", h + self.attention("mtp", x, rope_pos, self.mtp_cache, retain))
         fin = self.norm(h, "mtp.norm")
-        return fin, (self.matvec("lm_head", fin) if logits else None)
+        if not logits:
+            return fin, None
+        if self.draft_ids is not None:
+            return fin, self.restricted_logits(fin, self.draft_ids)
+        return fin, self.matvec("lm_head", fin)
 
     def decode(self, token):
         """One target step with the prefill-time MTP advance (:1248-1261)."""
@@ -175,7 +220,7 @@ class OracleDecoder:
             draft_logits.append(lg)
             empty = np.zeros((0, lg.size), np.float32)
             d, _ = orc.mtp_accept_sample(empty, empty, lg, np.zeros(0, np.uint32), temperature, rng)
-            xs.append(d)
+            xs.append(int(self.draft_ids[d]) if self.draft_ids is not None else d)
         saved = (copy.deepcopy(self.gdn_state), copy.deepcopy(self.conv_state), copy.deepcopy(self.caches),
                  self.position)
         target, hiddens = [], []
@@ -184,7 +229,7 @@ class OracleDecoder:
             target.append(lg)
             hiddens.append(fin)
         nxt, n = orc.mtp_accept_sample(np.stack(draft_logits), np.stack(target[:drafts]), target[drafts],
-                                       np.array(xs[1:], np.uint32), temperature, rng)
+                                       np.array(xs[1:], np.uint32), temperature, rng, draft_ids=self.draft_ids)
         # commit n + 1 target tokens
         self.gdn_state, self.conv_state, self.caches, self.position = saved
         for x in xs[:n + 1]:

@@ -98,6 +98,9 @@ def lib() -> ctypes.CDLL:
         L.orc_verify_greedy_mtp.argtypes = [P, P, P, SZ, SZ] + [ctypes.POINTER(ctypes.c_uint32)] * 2 + [P, ctypes.POINTER(ctypes.c_uint32)]
         L.orc_mtp_accept_sample.argtypes = [P, P, P, P, SZ, SZ, F, ctypes.POINTER(_Pcg),
                                             ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32)]
+        L.orc_mtp_accept_sample_restricted.argtypes = [P, P, SZ, P, P, P, SZ, SZ, F, ctypes.POINTER(_Pcg),
+                                                       ctypes.POINTER(ctypes.c_uint32),
+                                                       ctypes.POINTER(ctypes.c_uint32)]
         L.orc_fused_matvec.argtypes = [ctypes.c_int, ctypes.POINTER(_Op), P]
         L.orc_fused_matvec_threads.argtypes = [ctypes.c_int, ctypes.POINTER(_Op), P, ctypes.c_int]
         L.orc_fused_matvec_fanout.argtypes = [ctypes.c_int, ctypes.POINTER(_Op), SZ, ctypes.POINTER(P)]
@@ -375,11 +378,20 @@ def verify_greedy_mtp(draft, target, bonus):
     return nxt.value, ver.value, list(acc[: nacc.value])
 
 
-def mtp_accept_sample(draft, target, bonus, draft_tokens, temperature, rng: Pcg32):
+def mtp_accept_sample(draft, target, bonus, draft_tokens, temperature, rng: Pcg32, draft_ids=None):
+    """Rejection-sampling acceptance; with `draft_ids` the draft rows are
+    restricted distributions over those strictly increasing token IDs."""
     d, t, b = _f32(draft), _f32(target), _f32(bonus)
     toks = np.ascontiguousarray(draft_tokens, dtype=np.uint32)
     nxt, nacc = ctypes.c_uint32(), ctypes.c_uint32()
-    _ok(lib().orc_mtp_accept_sample(d.ctypes.data, t.ctypes.data, b.ctypes.data, toks.ctypes.data, d.shape[0],
-                                    d.shape[1], temperature, ctypes.byref(rng.c), ctypes.byref(nxt),
-                                    ctypes.byref(nacc)))
+    drafts = toks.size
+    vocab = b.size
+    ids = None if draft_ids is None else np.ascontiguousarray(draft_ids, dtype=np.uint32)
+    dn = vocab if ids is None else ids.size
+    if drafts and (d.size != drafts * dn or t.size != drafts * vocab):
+        raise OracleError(1)
+    _ok(lib().orc_mtp_accept_sample_restricted(
+        d.ctypes.data if d.size else None, None if ids is None else ids.ctypes.data, dn,
+        t.ctypes.data if t.size else None, b.ctypes.data, toks.ctypes.data, drafts, vocab, temperature,
+        ctypes.byref(rng.c), ctypes.byref(nxt), ctypes.byref(nacc)))
     return nxt.value, nacc.value

@@ -178,6 +178,47 @@ class PagedKvCache:
         return self.flattened(self.component_values, heads, head_dim)
 
 
+class DenseKvCache:
+    """FullAttentionStorage::Dense (Q/src/decoder.rs:171-265): exact f32 K/V
+    rows, chosen by FullAttentionState::new when the KV width is not a whole
+    number of 64-value blocks."""
+
+    def __init__(self, maximum_tokens, component_values):
+        if maximum_tokens == 0 or component_values == 0:
+            raise orc.OracleError(1)
+        self.maximum_tokens, self.component_values = maximum_tokens, component_values
+        self.keys, self.values = [], []
+
+    def push(self, key, value, demote: bool = True):
+        if len(self.keys) >= self.maximum_tokens or len(key) != self.component_values \
+                or len(value) != self.component_values:
+            raise orc.OracleError(1)
+        self.keys.append(np.asarray(key, np.float32).copy())
+        self.values.append(np.asarray(value, np.float32).copy())
+        return len(self.keys) - 1, 0, []
+
+    def demote_old_pages(self) -> List[int]:
+        return []
+
+    def tokens(self) -> int:
+        return len(self.keys)
+
+    def q2_tokens(self) -> int:
+        return 0
+
+    def _flat(self, rows, heads, head_dim):
+        if heads * head_dim != self.component_values:
+            raise orc.OracleError(1)
+        a = np.stack(rows).reshape(len(rows), heads, head_dim) if rows else np.zeros((0, heads, head_dim), np.float32)
+        return a.transpose(1, 0, 2).reshape(-1).copy()
+
+    def flattened_key(self, heads, head_dim):
+        return self._flat(self.keys, heads, head_dim)
+
+    def flattened_value(self, heads, head_dim):
+        return self._flat(self.values, heads, head_dim)
+
+
 def paged_attention(cache: PagedKvCache, query, rows: int, query_heads: int, kv_heads: int,
                     head_dim: int) -> np.ndarray:
     """Attention of the last `rows` cached tokens' queries (query

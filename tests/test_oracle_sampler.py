@@ -11,6 +11,7 @@ import json
 import os
 
 import numpy as np
+import pytest
 
 GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "crate_goldens.json")))
 
@@ -106,3 +107,52 @@ def test_mtp_accept_output_law_equals_target(orc):
         nxt, nacc = orc.mtp_accept_sample(q_log, p_log, bonus, [d], t, g)
         counts[d if nacc == 1 else nxt] += 1
     assert np.max(np.abs(counts / n - p)) < 0.015
+
+
+def test_mtp_accept_restricted_equals_padded_full_row(orc):
+    # A restricted draft row (Q/src/engine.rs:151-200) is the full row with
+    # every other token at -inf: the same draws give the same decisions.
+    rng = np.random.default_rng(3)
+    vocab, k = 40, 4
+    ids = np.sort(rng.choice(vocab, 12, replace=False)).astype(np.uint32)
+    for trial in range(30):
+        dr = rng.standard_normal((k, ids.size)).astype(np.float32) * 2
+        full = np.full((k, vocab), -np.inf, np.float32)
+        full[:, ids] = dr
+        tg = rng.standard_normal((k, vocab)).astype(np.float32) * 2
+        bonus = rng.standard_normal(vocab).astype(np.float32)
+        toks = ids[rng.integers(0, ids.size, k)]
+        g1, g2 = orc.Pcg32(trial), orc.Pcg32(trial)
+        a = orc.mtp_accept_sample(dr, tg, bonus, toks, 0.7, g1, draft_ids=ids)
+        b = orc.mtp_accept_sample(full, tg, bonus, toks, 0.7, g2)
+        assert a == b and g1.c.state == g2.c.state
+
+
+def test_mtp_accept_restricted_output_law_equals_target(orc):
+    # Drafts drawn from a restricted q still emit exactly the target law p.
+    p_log = np.array([[1.0, 0.2, -0.3, 0.5, 0.1]], np.float32)
+    ids = np.array([1, 3], np.uint32)
+    q_log = np.array([[0.4, -0.2]], np.float32)
+    t = 0.7
+    p = np.exp(p_log[0] / t); p /= p.sum()
+    q = np.exp(q_log[0] / t); q /= q.sum()
+    rng = np.random.default_rng(2)
+    g = orc.Pcg32(11)
+    counts = np.zeros(5)
+    n = 20000
+    bonus = np.zeros(5, np.float32)
+    for _ in range(n):
+        d = ids[rng.choice(2, p=q)]
+        nxt, nacc = orc.mtp_accept_sample(q_log, p_log, bonus, [d], t, g, draft_ids=ids)
+        counts[d if nacc == 1 else nxt] += 1
+    assert np.max(np.abs(counts / n - p)) < 0.015
+
+
+def test_mtp_accept_restricted_rejects_noncanonical_ids(orc):
+    # Q/src/decoder.rs:597-608 and Q/src/engine.rs:1387-1412: IDs must be
+    # strictly increasing and inside the vocabulary.
+    tg = np.zeros((1, 6), np.float32)
+    for ids in ([4, 1], [1, 1], [1, 6]):
+        with pytest.raises(orc.OracleError):
+            orc.mtp_accept_sample(np.zeros((1, len(ids)), np.float32), tg, tg[0], [1], 0.7, orc.Pcg32(0),
+                                  draft_ids=ids)
