@@ -65,7 +65,7 @@ __device__ __forceinline__ void take_max(int32_t &k, uint32_t &i, int32_t k2, ui
 }
 
 __device__ __forceinline__ const float *logits_row(const PartialArgs &a, uint32_t r) {
-    return r < a.drafts ? a.draft + (size_t)r * a.vocab
+    return r < a.drafts ? a.draft + (size_t)r * a.draft_vocab
                         : (r < 2 * a.drafts ? a.target + (size_t)(r - a.drafts) * a.vocab : a.bonus);
 }
 
@@ -74,8 +74,9 @@ extern "C" __global__ __launch_bounds__(256) void ctox_row_partials_gfx950(Parti
     __shared__ float s0[4], s1[4];
     const uint32_t r = blockIdx.x, part = blockIdx.y;
     const float *row = logits_row(a, r);
-    const uint32_t per = (a.vocab + a.parts - 1) / a.parts;
-    const uint32_t b = part * per, e = min(a.vocab, b + per);
+    const uint32_t len = r < a.drafts ? a.draft_vocab : a.vocab;
+    const uint32_t per = (len + a.parts - 1) / a.parts;
+    const uint32_t b = part * per, e = min(len, b + per);
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     float *o = a.out + ((size_t)r * a.parts + part) * 2;
     if (a.mode == 0) {
@@ -230,7 +231,8 @@ extern "C" __global__ __launch_bounds__(64) void ctox_mtp_decide_gfx950(AcceptAr
             return;
         }
         const float p = expf(a.target[(size_t)i * a.vocab + d] * invt - tm) / tz;
-        const float q = expf(a.draft[(size_t)i * a.vocab + d] * invt - dm) / dz;
+        const uint32_t di = a.draft_inv ? a.draft_inv[d] : d;
+        const float q = di < a.draft_vocab ? expf(a.draft[(size_t)i * a.draft_vocab + di] * invt - dm) / dz : 0.0f;
         const float u = pcg32_f32(s);
         if (u * q < p) {
             acc++;
@@ -264,7 +266,9 @@ extern "C" __global__ __launch_bounds__(64) void ctox_mtp_decide_gfx950(AcceptAr
 __device__ __forceinline__ float pick_weight(const AcceptArgs &a, const PickState &st, uint32_t t, float invt) {
     if (st.mode == 1) return expf(a.bonus[t] * invt - st.m_t) / st.z_t;
     const float p = expf(a.target[(size_t)st.row * a.vocab + t] * invt - st.m_t) / st.z_t;
-    const float q = expf(a.draft[(size_t)st.row * a.vocab + t] * invt - st.m_d) / st.z_d;
+    const uint32_t di = a.draft_inv ? a.draft_inv[t] : t;
+    const float q = di < a.draft_vocab ? expf(a.draft[(size_t)st.row * a.draft_vocab + di] * invt - st.m_d) / st.z_d
+                                       : 0.0f;
     const float r = p - q;
     return r > 0.0f ? r : 0.0f;
 }
@@ -353,7 +357,8 @@ extern "C" __global__ __launch_bounds__(1024) void ctox_pick_final_gfx950(Accept
         __syncthreads();
     }
     if (tid == 0) {
-        a.out[0] = res[1] != 0xffffffffu ? res[1] : res[2];
+        const uint32_t t = res[1] != 0xffffffffu ? res[1] : res[2];
+        a.out[0] = st.mode == 1 && a.bonus_ids ? a.bonus_ids[t] : t;
         a.out[1] = st.accepted;
     }
 }

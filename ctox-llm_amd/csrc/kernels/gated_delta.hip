@@ -275,15 +275,35 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_gfx950(GdnFused
             for (int gi = 0; gi < GDN_GROUPS; gi++) oj += red_out[gi][jj];
             a.out[((size_t)t * a.heads + h) * a.value_dim + j] = oj * qinv * qscale;
         }
+        if (a.snap_stride) {
+            // Row snapshot: the state and conv windows after token t.
+            float *So = a.state_out + (size_t)t * a.snap_stride + (size_t)h * dk * a.value_dim;
+#pragma unroll
+            for (int r = 0; r < GDN_MAX_ROWS; r++) {
+                const uint32_t i = ig + GDN_GROUPS * r;
+                if ((uint32_t)r < nrows && i < dk && colok) So[(size_t)i * a.value_dim + j] = s[r];
+            }
+            float *co = a.conv_out + (size_t)t * a.conv_snap_stride;
+            if (qk_thr && h % rep == 0 && slice == 0)
+#pragma unroll
+                for (int i = 0; i < GDN_MAX_KERNEL; i++)
+                    if ((uint32_t)i < K) co[(size_t)qk_ch * K + i] = sq_[i];
+            if (v_thr)
+#pragma unroll
+                for (int i = 0; i < GDN_MAX_KERNEL; i++)
+                    if ((uint32_t)i < K) co[(size_t)v_ch * K + i] = sv_[i];
+        }
         // qs/ks/vs/gsc and red_* are rewritten next token only after every
         // thread has passed this barrier.
         __syncthreads();
     }
+    if (a.snap_stride) return;
 
+    float *So = a.state_out + (size_t)h * dk * a.value_dim;
 #pragma unroll
     for (int r = 0; r < GDN_MAX_ROWS; r++) {
         const uint32_t i = ig + GDN_GROUPS * r;
-        if ((uint32_t)r < nrows && i < dk && colok) S[(size_t)i * a.value_dim + j] = s[r];
+        if ((uint32_t)r < nrows && i < dk && colok) So[(size_t)i * a.value_dim + j] = s[r];
     }
     // Final conv windows, each written once.
     if (qk_thr && h % rep == 0 && slice == 0)

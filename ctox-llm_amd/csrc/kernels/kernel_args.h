@@ -240,8 +240,16 @@ struct GdnFusedArgs {
     const float *dt_bias;    // [heads]
     float *log_decay;        // [tokens][heads]: written, or read when gates_given
     float *beta;             // [tokens][heads]: likewise
-    float *state;            // [heads][key_dim][value_dim]
+    float *state;            // [heads][key_dim][value_dim] read at the start
     float *out;              // [tokens][heads][value_dim]
+    // Where the state goes: state_out (may equal state: every workgroup has
+    // read its slice before it writes it). snap_stride != 0: the state after
+    // token t is written at state_out + t * snap_stride for every t, and the
+    // conv windows after token t at conv_out + t * conv_snap_stride (the
+    // speculative verify keeps every row's state; commit picks one).
+    float *state_out;
+    uint64_t snap_stride;    // floats; 0: only the final state
+    uint64_t conv_snap_stride;
     uint32_t tokens;
     uint32_t heads;
     uint32_t key_heads;
@@ -282,7 +290,7 @@ struct RepeatArgs {
 // 2 drafts is `bonus`. mode 0: {total-order key, index} of the maximum;
 // mode 1: {max(x / T), sum exp(x / T - max)}.
 struct PartialArgs {
-    const float *draft;
+    const float *draft;      // [drafts][draft_vocab]
     const float *target;
     const float *bonus;
     float *out;              // [rows][parts][2] (mode 0: key and index bit patterns)
@@ -291,7 +299,7 @@ struct PartialArgs {
     uint32_t parts;
     uint32_t mode;
     float temperature;
-    uint32_t pad;
+    uint32_t draft_vocab;    // length of a draft row (restricted drafts: the draft vocabulary)
 };
 
 // Token-selection decision state shared by the accept kernels.
@@ -321,12 +329,19 @@ struct AcceptArgs {
     PickState *state;
     uint64_t *rng;           // Pcg32 state, advanced in place
     uint32_t *out;           // [2]: next token, accepted count
+    // Restricted drafts (Q/src/engine.rs:151-200): draft rows hold
+    // draft_vocab scores; draft_inv[t] is token t's index in them
+    // (0xffffffff: outside the draft vocabulary, q = 0). NULL: full rows.
+    const uint32_t *draft_inv;
+    // Token of each bonus-row index (a restricted row sampled as the bonus
+    // row); NULL: the index is the token.
+    const uint32_t *bonus_ids;
     uint32_t drafts;
     uint32_t vocab;
     uint32_t parts;          // partials per row
     uint32_t parts2;         // parts of the cumulative search
     float temperature;
-    uint32_t pad;
+    uint32_t draft_vocab;
 };
 
 // Layer glue (layer_ops.hip).
@@ -507,6 +522,21 @@ struct RowsArgs {
     uint32_t in_stride;
     uint32_t out_stride;
     uint32_t offset;         // swiglu: offset of up within an input row; copy: offset of the copied columns
+    uint32_t pad;
+};
+
+struct FiniteArgs {          // ctox_finite_check_gfx950
+    const float *x;
+    uint32_t *flag;          // written: 1 if any of the n values is not finite, else 0
+    uint64_t n;
+};
+
+struct GatherRowsArgs {      // ctox_gather_rows_gfx950: dst row r = src row ids[r] (bytes)
+    const uint8_t *src;
+    uint8_t *dst;
+    const uint32_t *ids;
+    uint64_t row_bytes;
+    uint32_t rows;
     uint32_t pad;
 };
 

@@ -145,7 +145,7 @@ struct ctox_hip_backend {
                   conv = nullptr, rope = nullptr, kv_pack = nullptr, attn_prep = nullptr, kv_demote = nullptr, gqa_part[2] = {}, gqa_part16[2] = {},
                   gqa_combine = nullptr, fill = nullptr, embed = nullptr, norm_rows = nullptr, attn_gate = nullptr,
                   swiglu_rows = nullptr, copy_rows = nullptr, write_words = nullptr, norm_prep = nullptr,
-                  prep_x = nullptr;
+                  prep_x = nullptr, finite = nullptr, gather = nullptr;
     // Batch-1 slice kernels per dtype [Q2, Q4]: [0] walks the slices, [n]
     // requests all n slices up front (n <= 3: more slices up front measured
     // slower than walking them).
@@ -175,6 +175,10 @@ struct ctox_hip_backend {
     DevBuf tok, stats;
     // Split-attention partials.
     DevBuf attn;
+    // The scratch above is one set per backend: the stream of the previous
+    // call (compared, never used), see pick_stream.
+    hipStream_t last = nullptr;
+    bool used = false;
 };
 
 struct ctox_hip_matrix {
@@ -228,8 +232,20 @@ ctox_status launch(hipFunction_t f, dim3 grid, dim3 block, hipStream_t s, Args a
 }
 
 // Device entry points run on the caller's stream exactly as given; NULL is
-// HIP's null stream, as everywhere in the HIP API.
-hipStream_t pick_stream(ctox_hip_backend *, void *s) { return (hipStream_t)s; }
+// HIP's null stream, as everywhere in the HIP API. The backend's scratch
+// (activation staging, combine slots, selection statistics) is one set per
+// backend, so a call on a stream other than the previous call's first waits
+// on the host until the device has drained: the previous stream may already
+// be destroyed, so its handle is never used again. Calls that stay on one
+// stream (the decode engine, a serving loop) never wait.
+hipStream_t pick_stream(ctox_hip_backend *b, void *sv) {
+    hipStream_t s = (hipStream_t)sv;
+    if (!b) return s;
+    if (b->used && s != b->last) (void)hipDeviceSynchronize();
+    b->last = s;
+    b->used = true;
+    return s;
+}
 
 // Q/src/backend/cpu.rs:41-173 (same order of checks and error kinds).
 ctox_status validate_matvec(const ctox_fused_matvec *op, bool need_input, size_t *bpr) {
@@ -679,7 +695,8 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->tilex[1][2], "ctox_q4_mv_tile3x_gfx950"}, {&b->tilex[1][3], "ctox_q4_mv_tile4x_gfx950"},
                {&b->tilem[0][0], "ctox_q2_mv_tilem1_gfx950"}, {&b->tilem[0][1], "ctox_q2_mv_tilem2_gfx950"},
                {&b->tilem[1][0], "ctox_q4_mv_tilem1_gfx950"}, {&b->tilem[1][1], "ctox_q4_mv_tilem2_gfx950"},
-               {&b->repack, "ctox_tile_repack_gfx950"}, {&b->gdn_fused, "ctox_gdn_fused_gfx950"}};
+               {&b->repack, "ctox_tile_repack_gfx950"}, {&b->gdn_fused, "ctox_gdn_fused_gfx950"},
+               {&b->finite, "ctox_finite_check_gfx950"}, {&b->gather, "ctox_gather_rows_gfx950"}};
     for (auto &f : fns) {
         if (le != hipSuccess) break;
         le = hipModuleGetFunction(f.f, b->module, f.name);
@@ -766,7 +783,7 @@ ctox_status tile_segments(ctox_hip_backend *b, ctox_hip_matrix *m) {
     for (const ctox_quant_segment &seg : m->segments) {
         TiledCopy t;
         ctox_status st = tile_copy(b, seg.dtype, (const uint8_t *)m->d_weights + seg.offset,
-                                   seg.row_end - seg.row_start, m->columns, b->stream, t);
+                                   seg.row_end - seg.row_start, m->columns, pick_stream(b, b->stream), t);
         if (t.d) m->tiled.push_back(t);
         if (st) return st;
     }
@@ -1117,7 +1134,7 @@ extern "C" ctox_status ctox_hip_fused_matvec(ctox_hip_backend *b, const ctox_fus
     hipError_t e = hipMalloc((void **)&d_in, op->columns * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void **)&d_out, op->rows * sizeof(float));
     if (e == hipSuccess)
-        e = hipMemcpyAsync(d_in, op->input, op->columns * sizeof(float), hipMemcpyHostToDevice, b->stream);
+        e = hipMemcpyAsync(d_in, op->input, op->columns * sizeof(float), hipMemcpyHostToDevice, pick_stream(b, b->stream));
     if (e == hipSuccess) {
         bool prepped[2] = {false, false};
         st = dispatch_matrix(b, m, d_in, 1, d_out, b->stream, prepped, (uint32_t)op->activation);
@@ -1180,7 +1197,7 @@ extern "C" ctox_status ctox_hip_recovered_row(ctox_hip_backend *b, const ctox_re
         a.dtype = op->dtype == CTOX_DTYPE_Q4B64 ? 1u : 0u;
         a.s_in_kind = kernel_scale_kind(op->s_in.kind);
         a.s_out = op->s_out;
-        st = launch(b->rec_row, dim3((unsigned)((op->columns + 255) / 256)), dim3(256), b->stream, a,
+        st = launch(b->rec_row, dim3((unsigned)((op->columns + 255) / 256)), dim3(256), pick_stream(b, b->stream), a,
                     "ctox_recovered_row_gfx950");
         if (!st && (hipMemcpyAsync(output, d_o, op->columns * sizeof(float), hipMemcpyDeviceToHost, b->stream) !=
                         hipSuccess ||
@@ -1221,7 +1238,7 @@ extern "C" ctox_status ctox_hip_recovered_row_matvec(ctox_hip_backend *b, const 
         a.len = (uint32_t)op->len;
         a.dtype = op->dtype == CTOX_DTYPE_Q4B64 ? 1u : 0u;
         a.s_out = op->s_out;
-        st = launch(b->row_dot, dim3(1), dim3(64), b->stream, a, "ctox_row_dot_gfx950");
+        st = launch(b->row_dot, dim3(1), dim3(64), pick_stream(b, b->stream), a, "ctox_row_dot_gfx950");
         if (!st && (hipMemcpyAsync(result, d_r, sizeof(float), hipMemcpyDeviceToHost, b->stream) != hipSuccess ||
                     hipStreamSynchronize(b->stream) != hipSuccess))
             st = fail(CTOX_ERR_INVALID_STATE, "row matvec readback failed");
@@ -1334,7 +1351,7 @@ ctox_status gdn_host(ctox_hip_backend *b, const float *q, const float *k, const 
     if (!st && hipMalloc(&dout, nv * 4) != hipSuccess) st = fail(CTOX_ERR_INVALID_STATE, "hipMalloc failed");
     if (!st)
         st = gdn_device(b, (float *)dq, (float *)dk, (float *)dv, (float *)dl, (float *)db, (float *)ds, tokens,
-                        heads, kd, vd, chunk, (float *)dout, b->stream);
+                        heads, kd, vd, chunk, (float *)dout, pick_stream(b, b->stream));
     if (!st && (hipMemcpyAsync(out, dout, nv * 4, hipMemcpyDeviceToHost, b->stream) != hipSuccess ||
                 hipMemcpyAsync(state, ds, ns * 4, hipMemcpyDeviceToHost, b->stream) != hipSuccess ||
                 hipStreamSynchronize(b->stream) != hipSuccess))
@@ -1394,17 +1411,16 @@ extern "C" ctox_status ctox_hip_gated_delta_strided_device(ctox_hip_backend *b, 
                       pick_stream(b, stream), key_heads, qk_stride, v_stride);
 }
 
-extern "C" ctox_status ctox_hip_gdn_fused_device(ctox_hip_backend *b, const float *d_proj, size_t proj_stride,
-                                                 size_t a_off, size_t b_off, const float *d_conv_w,
-                                                 const float *d_conv_in, float *d_conv_out, size_t kernel,
-                                                 const float *d_a_log, const float *d_dt_bias, float *d_log_decay,
-                                                 float *d_beta, int gates_given, float *d_state, size_t tokens,
-                                                 size_t heads, size_t key_heads, size_t key_dim, size_t value_dim,
-                                                 float *d_out, void *stream) {
-    if (!b || !d_proj || !d_conv_w || !d_conv_in || !d_conv_out || !d_log_decay || !d_beta || !d_state || !d_out ||
-        (!gates_given && (!d_a_log || !d_dt_bias)))
+namespace {
+ctox_status gdn_fused_impl(ctox_hip_backend *b, const float *d_proj, size_t proj_stride, size_t a_off, size_t b_off,
+                           const float *d_conv_w, const float *d_conv_in, float *d_conv_out, size_t kernel,
+                           const float *d_a_log, const float *d_dt_bias, float *d_log_decay, float *d_beta,
+                           int gates_given, const float *d_state_in, float *d_state_out, size_t snap_stride,
+                           size_t conv_snap_stride, size_t tokens, size_t heads, size_t key_heads, size_t key_dim,
+                           size_t value_dim, float *d_out, void *stream) {
+    if (!b || !d_proj || !d_conv_w || !d_conv_in || !d_conv_out || !d_log_decay || !d_beta || !d_state_in ||
+        !d_state_out || !d_out || (!gates_given && (!d_a_log || !d_dt_bias)))
         return fail(CTOX_ERR_SHAPE, "null argument");
-    if (d_conv_in == d_conv_out) return fail(CTOX_ERR_SHAPE, "fused gated delta conv windows must not alias");
     ctox_status st = gdn_shape(tokens, heads, key_dim, value_dim);
     if (st) return st;
     const size_t channels = 2 * key_heads * key_dim + heads * value_dim;
@@ -1412,6 +1428,17 @@ extern "C" ctox_status ctox_hip_gdn_fused_device(ctox_hip_backend *b, const floa
         proj_stride < channels || a_off + heads > proj_stride || b_off + heads > proj_stride ||
         proj_stride > 0x7fffffffu || tokens > 65536)
         return fail(CTOX_ERR_SHAPE, "fused gated delta shapes");
+    // The conv windows written (every snapshot, or the final one) never
+    // overlap the ones read: other workgroups still read them.
+    const size_t cw = channels * kernel, sw = heads * key_dim * value_dim;
+    const size_t nsnap = snap_stride ? tokens : 1;
+    if ((snap_stride && (snap_stride < sw || conv_snap_stride < cw)) || (!snap_stride && conv_snap_stride))
+        return fail(CTOX_ERR_SHAPE, "fused gated delta snapshot strides");
+    for (size_t t = 0; t < nsnap; t++) {
+        const float *o = d_conv_out + t * conv_snap_stride;
+        if (o < d_conv_in + cw && d_conv_in < o + cw)
+            return fail(CTOX_ERR_SHAPE, "fused gated delta conv windows must not alias");
+    }
     GdnFusedArgs a{};
     a.proj = d_proj;
     a.conv_w = d_conv_w;
@@ -1421,7 +1448,10 @@ extern "C" ctox_status ctox_hip_gdn_fused_device(ctox_hip_backend *b, const floa
     a.dt_bias = d_dt_bias;
     a.log_decay = d_log_decay;
     a.beta = d_beta;
-    a.state = d_state;
+    a.state = (float *)d_state_in;
+    a.state_out = d_state_out;
+    a.snap_stride = snap_stride;
+    a.conv_snap_stride = conv_snap_stride;
     a.out = d_out;
     a.tokens = (uint32_t)tokens;
     a.heads = (uint32_t)heads;
@@ -1436,6 +1466,34 @@ extern "C" ctox_status ctox_hip_gdn_fused_device(ctox_hip_backend *b, const floa
     const size_t slices = (value_dim + 15) / 16;
     return launch(b->gdn_fused, dim3((unsigned)(heads * slices)), dim3(256), pick_stream(b, stream), a,
                   "ctox_gdn_fused_gfx950");
+}
+}  // namespace
+
+extern "C" ctox_status ctox_hip_gdn_fused_device(ctox_hip_backend *b, const float *d_proj, size_t proj_stride,
+                                                 size_t a_off, size_t b_off, const float *d_conv_w,
+                                                 const float *d_conv_in, float *d_conv_out, size_t kernel,
+                                                 const float *d_a_log, const float *d_dt_bias, float *d_log_decay,
+                                                 float *d_beta, int gates_given, float *d_state, size_t tokens,
+                                                 size_t heads, size_t key_heads, size_t key_dim, size_t value_dim,
+                                                 float *d_out, void *stream) {
+    return gdn_fused_impl(b, d_proj, proj_stride, a_off, b_off, d_conv_w, d_conv_in, d_conv_out, kernel, d_a_log,
+                          d_dt_bias, d_log_decay, d_beta, gates_given, d_state, d_state, 0, 0, tokens, heads,
+                          key_heads, key_dim, value_dim, d_out, stream);
+}
+
+extern "C" ctox_status ctox_hip_gdn_fused_snap_device(ctox_hip_backend *b, const float *d_proj, size_t proj_stride,
+                                                      size_t a_off, size_t b_off, const float *d_conv_w,
+                                                      const float *d_conv_in, float *d_conv_out,
+                                                      size_t conv_snap_stride, size_t kernel, const float *d_a_log,
+                                                      const float *d_dt_bias, float *d_log_decay, float *d_beta,
+                                                      const float *d_state_in, float *d_state_out,
+                                                      size_t snap_stride, size_t tokens, size_t heads,
+                                                      size_t key_heads, size_t key_dim, size_t value_dim,
+                                                      float *d_out, void *stream) {
+    if (snap_stride == 0) return fail(CTOX_ERR_SHAPE, "snapshot stride must be non-zero");
+    return gdn_fused_impl(b, d_proj, proj_stride, a_off, b_off, d_conv_w, d_conv_in, d_conv_out, kernel, d_a_log,
+                          d_dt_bias, d_log_decay, d_beta, 0, d_state_in, d_state_out, snap_stride, conv_snap_stride,
+                          tokens, heads, key_heads, key_dim, value_dim, d_out, stream);
 }
 
 // ======================================================================
@@ -1497,7 +1555,8 @@ extern "C" ctox_status ctox_hip_greedy_tokens_device(ctox_hip_backend *b, const 
     const uint32_t parts = row_parts(vocab);
     ctox_status st = ensure(b, b->tok, rows * parts * 2 * sizeof(float), false);
     if (st) return st;
-    PartialArgs p{d_logits, d_logits, d_logits, (float *)b->tok.ptr, (uint32_t)rows, (uint32_t)vocab, parts, 0, 1.0f, 0};
+    PartialArgs p{d_logits, d_logits, d_logits, (float *)b->tok.ptr, (uint32_t)rows, (uint32_t)vocab, parts, 0, 1.0f,
+                  (uint32_t)vocab};
     if ((st = launch(b->partials, dim3((unsigned)rows, parts), dim3(256), s, p, "ctox_row_partials_gfx950"))) return st;
     VerifyArgs v{(const float *)b->tok.ptr, d_tokens, (uint32_t)rows, parts};
     return launch(b->argmax_final, dim3((unsigned)rows), dim3(64), s, v, "ctox_argmax_final_gfx950");
@@ -1514,23 +1573,26 @@ extern "C" ctox_status ctox_hip_verify_greedy_mtp_device(ctox_hip_backend *b, co
     const size_t rows = 2 * drafts + 1;
     ctox_status st = ensure(b, b->tok, rows * parts * 2 * sizeof(float), false);
     if (st) return st;
-    PartialArgs p{d_draft, d_target, d_bonus, (float *)b->tok.ptr, (uint32_t)drafts, (uint32_t)vocab, parts, 0, 1.0f, 0};
+    PartialArgs p{d_draft, d_target, d_bonus, (float *)b->tok.ptr, (uint32_t)drafts, (uint32_t)vocab, parts, 0, 1.0f,
+                  (uint32_t)vocab};
     if ((st = launch(b->partials, dim3((unsigned)rows, parts), dim3(256), s, p, "ctox_row_partials_gfx950"))) return st;
     VerifyArgs v{(const float *)b->tok.ptr, d_out, (uint32_t)drafts, parts};
     return launch(b->verify, dim3(1), dim3(64), s, v, "ctox_verify_greedy_gfx950");
 }
 
-extern "C" ctox_status ctox_hip_mtp_accept_device(ctox_hip_backend *b, const float *d_draft, const float *d_target,
-                                                  const float *d_bonus, const uint32_t *d_tokens, size_t drafts,
-                                                  size_t vocab, float temperature, uint64_t *d_rng, uint32_t *d_out,
-                                                  void *stream) {
-    if (!b || !d_draft || !d_target || !d_bonus || !d_tokens || !d_rng || !d_out)
+extern "C" ctox_status ctox_hip_mtp_accept_restricted_device(
+    ctox_hip_backend *b, const float *d_draft, size_t draft_vocab, const uint32_t *d_draft_inv, const float *d_target,
+    const float *d_bonus, const uint32_t *d_bonus_ids, const uint32_t *d_tokens, size_t drafts, size_t vocab,
+    float temperature, uint64_t *d_rng, uint32_t *d_out, void *stream) {
+    if (!b || !d_bonus || !d_tokens || !d_rng || !d_out || (drafts && (!d_draft || !d_target)))
         return fail(CTOX_ERR_SHAPE, "null argument");
     if (!(temperature > 0.0f) || !std::isfinite(temperature) || !std::isfinite(1.0f / temperature))
         return fail(CTOX_ERR_INVALID_ARTIFACT, "sampling temperature must be finite and positive");
     if (vocab == 0) return fail(CTOX_ERR_INVALID_ARTIFACT, "cannot sample from empty logits");
     // The final search scans one part per pass with 1024 threads.
     if (drafts > kMaxDrafts || vocab > (size_t)1024 * 1024) return fail(CTOX_ERR_SHAPE, "drafts outside 0..64 or vocab above 2^20");
+    if (draft_vocab == 0 || draft_vocab > vocab || (draft_vocab < vocab && drafts && !d_draft_inv))
+        return fail(CTOX_ERR_SHAPE, "restricted draft rows need 1..vocab scores and the token-to-index map");
     hipStream_t s = pick_stream(b, stream);
     const uint32_t parts = row_parts(vocab);
     const uint32_t parts2 = (uint32_t)std::max<size_t>(256, (vocab + 1023) / 1024);
@@ -1539,14 +1601,69 @@ extern "C" ctox_status ctox_hip_mtp_accept_device(ctox_hip_backend *b, const flo
     ctox_status st = ensure(b, b->stats, state_off + sizeof(PickState), false);
     if (st) return st;
     float *partials = (float *)b->stats.ptr;
-    AcceptArgs a{d_draft, d_target, d_bonus, d_tokens, partials, partials + rows * parts * 2,
-                 (PickState *)((char *)b->stats.ptr + state_off), d_rng, d_out, (uint32_t)drafts, (uint32_t)vocab,
-                 parts, parts2, temperature, 0};
-    PartialArgs p{d_draft, d_target, d_bonus, partials, (uint32_t)drafts, (uint32_t)vocab, parts, 1, temperature, 0};
+    AcceptArgs a{};
+    a.draft = d_draft;
+    a.target = d_target;
+    a.bonus = d_bonus;
+    a.tokens = d_tokens;
+    a.partials = partials;
+    a.sums = partials + rows * parts * 2;
+    a.state = (PickState *)((char *)b->stats.ptr + state_off);
+    a.rng = d_rng;
+    a.out = d_out;
+    a.draft_inv = draft_vocab < vocab ? d_draft_inv : nullptr;
+    a.bonus_ids = d_bonus_ids;
+    a.drafts = (uint32_t)drafts;
+    a.vocab = (uint32_t)vocab;
+    a.parts = parts;
+    a.parts2 = parts2;
+    a.temperature = temperature;
+    a.draft_vocab = (uint32_t)draft_vocab;
+    PartialArgs p{d_draft, d_target, d_bonus, partials, (uint32_t)drafts, (uint32_t)vocab, parts, 1, temperature,
+                  (uint32_t)draft_vocab};
     if ((st = launch(b->partials, dim3((unsigned)rows, parts), dim3(256), s, p, "ctox_row_partials_gfx950"))) return st;
     if ((st = launch(b->decide, dim3(1), dim3(64), s, a, "ctox_mtp_decide_gfx950"))) return st;
     if ((st = launch(b->pick_sums, dim3(parts2), dim3(256), s, a, "ctox_pick_sums_gfx950"))) return st;
     return launch(b->pick_final, dim3(1), dim3(1024), s, a, "ctox_pick_final_gfx950");
+}
+
+extern "C" ctox_status ctox_hip_mtp_accept_device(ctox_hip_backend *b, const float *d_draft, const float *d_target,
+                                                  const float *d_bonus, const uint32_t *d_tokens, size_t drafts,
+                                                  size_t vocab, float temperature, uint64_t *d_rng, uint32_t *d_out,
+                                                  void *stream) {
+    if (!b || !d_draft || !d_target || !d_bonus || !d_tokens || !d_rng || !d_out)
+        return fail(CTOX_ERR_SHAPE, "null argument");
+    return ctox_hip_mtp_accept_restricted_device(b, d_draft, vocab, nullptr, d_target, d_bonus, nullptr, d_tokens,
+                                                 drafts, vocab, temperature, d_rng, d_out, stream);
+}
+
+extern "C" ctox_status ctox_hip_check_finite_device(ctox_hip_backend *b, const float *d_x, size_t n,
+                                                    uint32_t *d_flag, void *stream) {
+    if (!b || !d_x || !d_flag) return fail(CTOX_ERR_SHAPE, "null argument");
+    if ((uintptr_t)d_x % 16) return fail(CTOX_ERR_SHAPE, "finite check needs a 16-byte aligned buffer");
+    FiniteArgs a{d_x, d_flag, (uint64_t)n};
+    return launch(b->finite, dim3(1), dim3(1024), pick_stream(b, stream), a, "ctox_finite_check_gfx950");
+}
+
+extern "C" ctox_status ctox_hip_gather_rows_device(ctox_hip_backend *b, const void *d_src, size_t src_rows,
+                                                   size_t row_bytes, const uint32_t *ids, size_t rows, void *d_dst,
+                                                   void *stream) {
+    if (!b || !d_src || !ids || !d_dst) return fail(CTOX_ERR_SHAPE, "null argument");
+    if (rows == 0 || rows > 0x7fffffffu || row_bytes == 0) return fail(CTOX_ERR_SHAPE, "gather rows geometry");
+    // ids are host values: checked here, then carried to the device.
+    for (size_t r = 0; r < rows; r++)
+        if (ids[r] >= src_rows) return fail(CTOX_ERR_SHAPE, "gathered row %u outside %zu rows", ids[r], src_rows);
+    uint32_t *d_ids = nullptr;
+    HIP_TRY(hipMalloc((void **)&d_ids, rows * sizeof(uint32_t)));
+    hipStream_t s = pick_stream(b, stream);
+    hipError_t e = hipMemcpyAsync(d_ids, ids, rows * sizeof(uint32_t), hipMemcpyHostToDevice, s);
+    ctox_status st = CTOX_OK;
+    if (e != hipSuccess) st = fail(CTOX_ERR_INVALID_STATE, "gather ids upload failed: %s", hipGetErrorString(e));
+    GatherRowsArgs a{(const uint8_t *)d_src, (uint8_t *)d_dst, d_ids, (uint64_t)row_bytes, (uint32_t)rows, 0};
+    if (!st) st = launch(b->gather, dim3((unsigned)rows), dim3(256), s, a, "ctox_gather_rows_gfx950");
+    (void)hipStreamSynchronize(s);
+    (void)hipFree(d_ids);
+    return st;
 }
 
 // ======================================================================

@@ -58,9 +58,8 @@ struct GdnLayer {
     Mat in;                 // [qkv | z | a | b]
     float *conv_w = nullptr, *a_log = nullptr, *dt_bias = nullptr, *gnorm = nullptr;
     Mat out;
-    float *state = nullptr;  // view into the engine's state block
-    size_t conv_off = 0;     // offset of the layer's conv windows in each conv block
-    float *proj = nullptr, *ld = nullptr, *beta = nullptr;  // per-layer rows kept for the commit replay
+    size_t state_off = 0;    // offset of the layer's state in each state slot
+    size_t conv_off = 0;     // offset of the layer's conv windows in each conv slot
 };
 
 // Host bookkeeping of one paged cache (Q/src/kv_cache.rs:303-478 policy).
@@ -99,6 +98,16 @@ struct ctox_hip_engine {
     std::vector<Layer> layers;
     Mat embed, lm_head;
     float *final_norm = nullptr;
+    // Restricted MTP draft head (Q/src/decoder.rs:589-627): the LM-head rows
+    // of the release-bound draft vocabulary, gathered once into a compact
+    // matrix (s_in shared with the LM head); draft_inv maps a token to its
+    // row (0xffffffff outside). draft_n = 0: drafts use the full head.
+    Mat draft_head;
+    uint32_t draft_n = 0;
+    uint32_t *d_draft_ids = nullptr, *d_draft_inv = nullptr;
+    // Fail-closed flags: non-finite logits (device words, read back through
+    // pinned host memory with the step's one synchronization).
+    uint32_t *d_flags = nullptr, *h_flags = nullptr;
     // MTP
     bool mtp = false;
     float *mtp_norm_emb = nullptr, *mtp_norm_hid = nullptr, *mtp_norm = nullptr;
@@ -108,13 +117,14 @@ struct ctox_hip_engine {
     // geometry
     uint32_t H = 0, I = 0, Kw = 0, Vw = 0, C = 0, Rin = 0, Rq = 0, kvw = 0, V = 0, R = 0;
     uint32_t q4_token_bytes = 0, q2_token_bytes = 0, q4_page_bytes = 0, q2_page_bytes = 0;
-    // state blocks
-    float *gdn_state = nullptr, *gdn_ckpt = nullptr, *conv_state = nullptr, *conv_ckpt = nullptr;
-    // Conv windows ping-pong between conv_state and conv_state2: a target
-    // pass reads the current block and writes the other one (the fused
-    // GatedDeltaNet kernel must not update the windows in place).
-    float *conv_state2 = nullptr;
-    uint32_t conv_par = 0;
+    // Recurrent state and conv windows of every GatedDeltaNet layer, in two
+    // banks of R slots each (one slot = all layers). The current state is
+    // slot `sidx` of bank `bank`; a target pass over R rows reads it and
+    // writes the state after each row t into slot t of the other bank, so a
+    // speculative commit of n + 1 rows only selects slot n (no checkpoint
+    // copy, no replay), and the conv windows are never updated in place.
+    float *gdn_bank = nullptr, *conv_bank = nullptr;
+    uint32_t bank = 0, sidx = 0;
     size_t gdn_floats = 0, conv_floats = 0;
     // activations (sized for R rows)
     float *hid = nullptr, *hid2 = nullptr, *xn = nullptr, *proj = nullptr, *convo = nullptr, *core = nullptr, *coren = nullptr,
@@ -397,11 +407,8 @@ ctox_status attn_forward(ctox_hip_engine *e, AttnLayer &a, uint32_t R, uint32_t 
     uint32_t slots[8], pos[8];
     if (R > 8) return efail(CTOX_ERR_SHAPE, "attention rows exceed 8");
     TRY(cache_reserve(e, a.cache, R, slots, pos));
-    // Demotion reads only pages older than the recent window, never the rows
-    // appended here, so it may precede the append; the changed descriptors
-    // then travel with the append's launch.
-    if (!retain) TRY(cache_demote(e, a.cache));
     Cache &c = a.cache;
+    // The reserved pages' descriptors travel with the append's launch.
     const size_t words = (size_t)(c.pages - std::min(c.dirty, c.pages)) * 4;
     const bool carry = words > 0 && words <= 32;
     if (!carry) TRY(cache_upload(e, c));
@@ -411,33 +418,41 @@ ctox_status attn_forward(ctox_hip_engine *e, AttnLayer &a, uint32_t R, uint32_t 
                                   carry ? (const uint32_t *)(c.desc.data() + c.dirty) : nullptr, carry ? words : 0,
                                   e->s));
     if (carry) c.dirty = c.pages;
+    // Pages are demoted after the rows are appended, before attention reads
+    // them, as FullAttentionState::append pushes and then demotes
+    // (Q/src/kv_cache.rs:394-429, 463-478; decoder.rs:774): with a recent
+    // window shorter than the rows appended, a page holding new rows may go.
+    if (!retain) {
+        TRY(cache_demote(e, c));
+        TRY(cache_upload(e, c));
+    }
     const ctox_paged_gqa_params p = gqa_params(e, a.cache);
     TRY(ctox_hip_paged_gqa_device(e->b, e->q, a.cache.q2, a.cache.q4, a.cache.d_desc, &p, R, e->attn, e->s));
     ctox_input_transform x{e->attn, e->proj, nullptr, 3, qh * hd, e->Rq, 0, hd, 0.0f, nullptr, nullptr, 0, 0};
     return delta_mv(e, x, a.o, delta, R);
 }
 
-float *conv_cur(ctox_hip_engine *e) { return e->conv_par ? e->conv_state2 : e->conv_state; }
-float *conv_next(ctox_hip_engine *e) { return e->conv_par ? e->conv_state : e->conv_state2; }
+float *state_cur(ctox_hip_engine *e) { return e->gdn_bank + ((size_t)e->bank * e->R + e->sidx) * e->gdn_floats; }
+float *conv_cur(ctox_hip_engine *e) { return e->conv_bank + ((size_t)e->bank * e->R + e->sidx) * e->conv_floats; }
 
 // Causal conv, gates and recurrence of one GatedDeltaNet layer over R
-// projected rows (one launch); gates_given replays kept gate rows.
-ctox_status gdn_core(ctox_hip_engine *e, GdnLayer &g, const float *proj, uint32_t R, float *ld, float *beta,
-                     bool gates_given) {
+// projected rows (one launch): reads the current state slot and writes the
+// state after row t into slot t of the other bank.
+ctox_status gdn_core(ctox_hip_engine *e, GdnLayer &g, const float *proj, uint32_t R) {
     const uint32_t Hv = e->c.linear_num_value_heads, Hk = e->c.linear_num_key_heads;
-    return ctox_hip_gdn_fused_device(e->b, proj, e->Rin, e->C + e->Vw, e->C + e->Vw + Hv, g.conv_w,
-                                     conv_cur(e) + g.conv_off, conv_next(e) + g.conv_off,
-                                     e->c.linear_conv_kernel_dim, g.a_log, g.dt_bias, ld, beta, gates_given ? 1 : 0,
-                                     g.state, R, Hv, Hk, e->c.linear_key_head_dim, e->c.linear_value_head_dim, e->core,
-                                     e->s);
+    const size_t other = (size_t)(e->bank ^ 1u) * e->R;
+    return ctox_hip_gdn_fused_snap_device(e->b, proj, e->Rin, e->C + e->Vw, e->C + e->Vw + Hv, g.conv_w,
+                                          conv_cur(e) + g.conv_off, e->conv_bank + other * e->conv_floats + g.conv_off,
+                                          e->conv_floats, e->c.linear_conv_kernel_dim, g.a_log, g.dt_bias, e->ld,
+                                          e->beta, state_cur(e) + g.state_off,
+                                          e->gdn_bank + other * e->gdn_floats + g.state_off, e->gdn_floats, R, Hv, Hk,
+                                          e->c.linear_key_head_dim, e->c.linear_value_head_dim, e->core, e->s);
 }
 
-ctox_status gdn_forward(ctox_hip_engine *e, GdnLayer &g, uint32_t R, float *delta, bool keep_rows) {
+ctox_status gdn_forward(ctox_hip_engine *e, GdnLayer &g, uint32_t R, float *delta) {
     const uint32_t dv = e->c.linear_value_head_dim;
-    float *proj = keep_rows ? g.proj : e->proj;  // the in-projection, already computed (norm_mv)
-    float *ld = keep_rows ? g.ld : e->ld, *beta = keep_rows ? g.beta : e->beta;
-    TRY(gdn_core(e, g, proj, R, ld, beta, false));
-    ctox_input_transform x{e->core, proj + e->C, g.gnorm, 2, e->Vw, e->Rin, 0, dv, e->c.rms_norm_epsilon, nullptr, nullptr, 0, 0};
+    TRY(gdn_core(e, g, e->proj, R));  // the in-projection is already in e->proj (norm_mv)
+    ctox_input_transform x{e->core, e->proj + e->C, g.gnorm, 2, e->Vw, e->Rin, 0, dv, e->c.rms_norm_epsilon, nullptr, nullptr, 0, 0};
     return delta_mv(e, x, g.out, delta, R);
 }
 
@@ -451,7 +466,10 @@ ctox_status mlp_forward(ctox_hip_engine *e, Mlp &m, uint32_t R, const float *del
 
 // Target model over R rows (tokens in d_tok, positions position..position+R-1).
 // Leaves logits [R][V] and final hiddens [R][H] (e->fin).
-ctox_status target_forward(ctox_hip_engine *e, const uint32_t *d_tok, uint32_t R, bool keep_rows) {
+// `retain`: a speculative branch (Q4 pages are not demoted). The
+// GatedDeltaNet states after each row land in the other bank; the caller
+// selects the committed row (bank flip + slot).
+ctox_status target_forward(ctox_hip_engine *e, const uint32_t *d_tok, uint32_t R, bool retain) {
     TRY(ctox_hip_embedding_rows_device(e->b, e->embed.dtype, e->embed.w, e->embed.s_in, e->embed.s_out, d_tok, R, e->V,
                                        e->H, e->hid, e->s));
     bool pending = false;
@@ -459,15 +477,14 @@ ctox_status target_forward(ctox_hip_engine *e, const uint32_t *d_tok, uint32_t R
         const float *dl = pending ? e->delta : nullptr;
         if (L.full) {
             TRY(norm_mv(e, dl, L.f.norm, R, L.f.qkv, e->proj));
-            TRY(attn_forward(e, L.f, R, e->position, e->delta, keep_rows));
+            TRY(attn_forward(e, L.f, R, e->position, e->delta, retain));
         } else {
-            TRY(norm_mv(e, dl, L.g.norm, R, L.g.in, keep_rows ? L.g.proj : e->proj));
-            TRY(gdn_forward(e, L.g, R, e->delta, keep_rows));
+            TRY(norm_mv(e, dl, L.g.norm, R, L.g.in, e->proj));
+            TRY(gdn_forward(e, L.g, R, e->delta));
         }
         TRY(mlp_forward(e, L.mlp, R, e->delta, e->delta));
         pending = true;
     }
-    e->conv_par ^= 1u;  // every GatedDeltaNet layer wrote its windows to the other block
     return norm_mv(e, e->delta, e->final_norm, R, e->lm_head, e->logits, e->fin);
 }
 
@@ -485,7 +502,8 @@ ctox_status mtp_forward(ctox_hip_engine *e, const uint32_t *d_tok, const float *
     TRY(norm_mv(e, nullptr, e->mtp_attn.norm, R, e->mtp_attn.qkv, e->proj));
     TRY(attn_forward(e, e->mtp_attn, R, rope0, e->delta, retain));
     TRY(mlp_forward(e, e->mtp_mlp, R, e->delta, e->delta));
-    if (logits) return norm_mv(e, e->delta, e->mtp_norm, R, e->lm_head, logits, e->mtp_hidden);
+    if (logits) return norm_mv(e, e->delta, e->mtp_norm, R, e->draft_n ? e->draft_head : e->lm_head, logits,
+                               e->mtp_hidden);
     return norm(e, e->hid, e->delta, e->mtp_norm, R, e->H, e->mtp_hidden, e->H);
 }
 
@@ -500,6 +518,25 @@ ctox_status demote_all(ctox_hip_engine *e) {
         TRY(cache_upload(e, e->mtp_attn.cache));
     }
     return CTOX_OK;
+}
+
+// Queues the finite check of `n` logits into flag word `slot`.
+ctox_status check_logits(ctox_hip_engine *e, const float *x, size_t n, uint32_t slot) {
+    return ctox_hip_check_finite_device(e->b, x, n, e->d_flags + slot, e->s);
+}
+
+// After the step's synchronization: fail closed on a flagged buffer
+// (Q/src/backend/cuda_runtime.rs:10627-10632, Q/src/engine.rs:191-272).
+ctox_status flags_ok(ctox_hip_engine *e, uint32_t count) {
+    for (uint32_t i = 0; i < count; i++)
+        if (e->h_flags[i]) return efail(CTOX_ERR_INVALID_STATE, "non-finite logits in the decode step");
+    return CTOX_OK;
+}
+
+ctox_status read_flags(ctox_hip_engine *e, uint32_t count) {
+    return hipMemcpyAsync(e->h_flags, e->d_flags, count * sizeof(uint32_t), hipMemcpyDeviceToHost, e->s) == hipSuccess
+               ? CTOX_OK
+               : efail(CTOX_ERR_INVALID_STATE, "flag read failed");
 }
 
 ctox_status sync(ctox_hip_engine *e) {
@@ -526,11 +563,16 @@ extern "C" ctox_status ctox_hip_engine_create(ctox_hip_backend *b, const ctox_en
         c.num_attention_heads % c.num_key_value_heads || c.head_dim != 256 || c.linear_num_key_heads == 0 ||
         c.linear_num_value_heads % c.linear_num_key_heads || c.linear_key_head_dim > 128 ||
         c.linear_value_head_dim > 128 || c.linear_conv_kernel_dim == 0 || c.vocab_size == 0 || c.max_tokens == 0 ||
-        c.page_tokens == 0 || c.sink_tokens % c.page_tokens || c.draft_tokens > 7 ||
+        c.page_tokens == 0 || c.sink_tokens % c.page_tokens || c.draft_tokens > 7 || c.recent_tokens > c.max_tokens ||
         (c.num_attention_heads * c.head_dim) % 64 || (c.linear_num_value_heads * c.linear_value_head_dim) % 64 ||
         !(c.rms_norm_epsilon > 0.0f) || !(c.rope_theta > 0.0f) || c.rotary_dim == 0 || c.rotary_dim % 2 ||
         c.rotary_dim > c.head_dim)
         return efail(CTOX_ERR_SHAPE, "engine configuration is invalid");
+    // A zero recent window demotes the page being filled, after which the
+    // crate appends Q2 rows to it (Q/src/kv_cache.rs:199-206); the device
+    // appends Q4 rows only, so that configuration is refused.
+    if (c.recent_tokens == 0)
+        return efail(CTOX_ERR_UNSUPPORTED_OPERATION, "a zero recent KV window (Q2 appends) is not supported");
     ctox_hip_engine *e = new ctox_hip_engine();
     e->b = b;
     e->c = c;
@@ -564,14 +606,13 @@ extern "C" ctox_status ctox_hip_engine_create(ctox_hip_backend *b, const ctox_en
     const uint32_t Hv = c.linear_num_value_heads;
     e->gdn_floats = (size_t)n_gdn * Hv * c.linear_key_head_dim * c.linear_value_head_dim;
     e->conv_floats = (size_t)n_gdn * e->C * c.linear_conv_kernel_dim;
-    if ((st = dalloc_t(e, &e->gdn_state, e->gdn_floats)) || (st = dalloc_t(e, &e->conv_state, e->conv_floats)) ||
-        (st = dalloc_t(e, &e->conv_state2, e->conv_floats)))
+    if ((st = dalloc_t(e, &e->gdn_bank, 2 * (size_t)e->R * e->gdn_floats)) ||
+        (st = dalloc_t(e, &e->conv_bank, 2 * (size_t)e->R * e->conv_floats)))
         return cleanup(st);
-    if (e->mtp && ((st = dalloc_t(e, &e->gdn_ckpt, e->gdn_floats)) || (st = dalloc_t(e, &e->conv_ckpt, e->conv_floats))))
-        return cleanup(st);
-    hipMemsetAsync(e->gdn_state, 0, e->gdn_floats * 4, e->s);
-    hipMemsetAsync(e->conv_state, 0, e->conv_floats * 4, e->s);
-    hipMemsetAsync(e->conv_state2, 0, e->conv_floats * 4, e->s);
+    // Only the current slot is read before it is written.
+    if (hipMemsetAsync(e->gdn_bank, 0, e->gdn_floats * 4, e->s) != hipSuccess ||
+        hipMemsetAsync(e->conv_bank, 0, e->conv_floats * 4, e->s) != hipSuccess)
+        return cleanup(efail(CTOX_ERR_INVALID_STATE, "state clear failed"));
     e->layers.resize(c.num_hidden_layers);
     uint32_t gi = 0;
     for (uint32_t l = 0; l < c.num_hidden_layers; l++) {
@@ -588,11 +629,8 @@ extern "C" ctox_status ctox_hip_engine_create(ctox_hip_backend *b, const ctox_en
             if ((st = dalloc_t(e, &g.dt_bias, Hv)) || (st = fill(e, g.dt_bias, Hv, 4, sd++, -1.0f, 1.0f))) return cleanup(st);
             if ((st = make_vec(e, &g.gnorm, c.linear_value_head_dim, sd, 1.0f, 0.1f))) return cleanup(st);
             if ((st = make_mat(e, g.out, CTOX_DTYPE_Q4B64, e->H, e->Vw, sd))) return cleanup(st);
-            g.state = e->gdn_state + (size_t)gi * Hv * c.linear_key_head_dim * c.linear_value_head_dim;
+            g.state_off = (size_t)gi * Hv * c.linear_key_head_dim * c.linear_value_head_dim;
             g.conv_off = (size_t)gi * e->C * c.linear_conv_kernel_dim;
-            if (e->mtp && ((st = dalloc_t(e, &g.proj, (size_t)e->R * e->Rin)) || (st = dalloc_t(e, &g.ld, (size_t)e->R * Hv)) ||
-                           (st = dalloc_t(e, &g.beta, (size_t)e->R * Hv))))
-                return cleanup(st);
             gi++;
         }
         if ((st = make_mlp(e, L.mlp, sd))) return cleanup(st);
@@ -620,8 +658,12 @@ extern "C" ctox_status ctox_hip_engine_create(ctox_hip_backend *b, const ctox_en
         (st = dalloc_t(e, &e->mtp_hidden, R * e->H)) || (st = dalloc_t(e, &e->prev_hidden, R * e->H)) ||
         (st = dalloc_t(e, &e->target_hidden, (R + 1) * e->H)) || (st = dalloc_t(e, &e->d_tokens, 16)) ||
         (st = dalloc_t(e, &e->d_drafts, 16)) || (st = dalloc_t(e, &e->d_result, 16)) || (st = dalloc_t(e, &e->d_rng, 1)) ||
-        (st = dalloc_t(e, &e->rsq, 512)))
+        (st = dalloc_t(e, &e->rsq, 512)) || (st = dalloc_t(e, &e->d_flags, 64)))
         return cleanup(st);
+    if (hipHostMalloc((void **)&e->h_flags, 64 * sizeof(uint32_t), hipHostMallocDefault) != hipSuccess) {
+        e->h_flags = nullptr;
+        return cleanup(efail(CTOX_ERR_MEMORY_BUDGET, "pinned host flags allocation failed"));
+    }
     if ((st = sync(e))) return cleanup(st);
     *out = e;
     return CTOX_OK;
@@ -632,6 +674,7 @@ extern "C" void ctox_hip_engine_destroy(ctox_hip_engine *e) {
     if (e->s) hipStreamSynchronize(e->s);
     for (const void *p : e->tiled) ctox_hip_unregister_tiled_weights(e->b, p);
     for (void *p : e->allocs) hipFree(p);
+    if (e->h_flags) hipHostFree(e->h_flags);
     if (e->s) hipStreamDestroy(e->s);
     delete e;
 }
@@ -659,12 +702,17 @@ extern "C" ctox_status ctox_hip_engine_decode(ctox_hip_engine *e, uint32_t token
         e->mtp_tokens++;
     }
     TRY(target_forward(e, e->d_tokens, 1, false));
+    e->bank ^= 1u;  // the state after the row is slot 0 of the other bank
+    e->sidx = 0;
     TRY(copy_d2d(e, e->prev_hidden, e->fin, (size_t)e->H * 4));
     e->have_prev = true;
     e->position++;
     TRY(demote_all(e));
+    TRY(check_logits(e, e->logits, e->V, 0));
+    TRY(read_flags(e, 1));
     if (d_logits) *d_logits = e->logits;
-    return sync(e);
+    TRY(sync(e));
+    return flags_ok(e, 1);
 }
 
 // One speculative step: k drafts sampled at `temperature`, one batched target
@@ -683,36 +731,38 @@ extern "C" ctox_status ctox_hip_engine_mtp_step(ctox_hip_engine *e, uint32_t tok
     // target hidden, then x_i = d_i, g_i = the MTP hidden of step i.
     TRY(copy_d2d(e, e->d_drafts, e->d_tokens, 4));
     TRY(copy_d2d(e, e->target_hidden, e->prev_hidden, (size_t)e->H * 4));
+    // Draft rows: the full head, or the restricted one (draft_n scores).
+    const uint32_t dn = e->draft_n ? e->draft_n : e->V;
     for (uint32_t i = 0; i < k; i++) {
         TRY(mtp_forward(e, e->d_drafts + i, i == 0 ? e->prev_hidden : e->mtp_hidden, 1, p + i,
-                        e->draft_logits + (size_t)i * e->V, true));
-        // drafts = 0 samples the bonus row: the draft token from its own softmax.
-        TRY(ctox_hip_mtp_accept_device(e->b, e->draft_logits, e->draft_logits, e->draft_logits + (size_t)i * e->V,
-                                       e->d_drafts, 0, e->V, temperature, e->d_rng, e->d_drafts + i + 1, e->s));
+                        e->draft_logits + (size_t)i * dn, true));
+        // drafts = 0 samples the bonus row: the draft token from its own
+        // softmax (a restricted row's index mapped to its token).
+        TRY(ctox_hip_mtp_accept_restricted_device(e->b, nullptr, dn, nullptr, nullptr, e->draft_logits + (size_t)i * dn,
+                                                  e->draft_n ? e->d_draft_ids : nullptr, e->d_drafts, 0, dn,
+                                                  temperature, e->d_rng, e->d_drafts + i + 1, e->s));
     }
-    // Checkpoint the recurrent states, then verify [token, d1..dk] in one pass.
-    TRY(copy_d2d(e, e->gdn_ckpt, e->gdn_state, e->gdn_floats * 4));
-    TRY(copy_d2d(e, e->conv_ckpt, conv_cur(e), e->conv_floats * 4));
+    // Verify [token, d1..dk] in one pass; every row's GatedDeltaNet state is kept.
     TRY(target_forward(e, e->d_drafts, R, true));
-    TRY(ctox_hip_mtp_accept_device(e->b, e->draft_logits, e->logits, e->logits + (size_t)k * e->V, e->d_drafts + 1, k,
-                                   e->V, temperature, e->d_rng, e->d_result, e->s));
+    TRY(check_logits(e, e->logits, (size_t)R * e->V, 0));
+    TRY(check_logits(e, e->draft_logits, (size_t)k * dn, 1));
+    TRY(ctox_hip_mtp_accept_restricted_device(e->b, e->draft_logits, dn, e->draft_n ? e->d_draft_inv : nullptr,
+                                              e->logits, e->logits + (size_t)k * e->V, nullptr, e->d_drafts + 1, k,
+                                              e->V, temperature, e->d_rng, e->d_result, e->s));
     uint32_t host[16] = {0};
     if (hipMemcpyAsync(host, e->d_result, 8, hipMemcpyDeviceToHost, e->s) != hipSuccess ||
         hipMemcpyAsync(host + 2, e->d_drafts, 4 * R, hipMemcpyDeviceToHost, e->s) != hipSuccess)
         return efail(CTOX_ERR_INVALID_STATE, "result read failed");
+    TRY(read_flags(e, 2));
     TRY(sync(e));
+    TRY(flags_ok(e, 2));  // nothing is committed from a step with non-finite logits
     const uint32_t next = host[0], n = host[1];
     if (n > k || next >= e->V) return efail(CTOX_ERR_INVALID_STATE, "acceptance produced an invalid result");
-    // Commit n + 1 target tokens.
+    // Commit n + 1 target tokens: the state after row n, the caches truncated.
+    e->bank ^= 1u;
+    e->sidx = n;
     for (Layer &L : e->layers)
         if (L.full) cache_truncate(L.f.cache, k - n);
-    if (n < k) {
-        TRY(copy_d2d(e, e->gdn_state, e->gdn_ckpt, e->gdn_floats * 4));
-        TRY(copy_d2d(e, conv_cur(e), e->conv_ckpt, e->conv_floats * 4));
-        for (Layer &L : e->layers)
-            if (!L.full) TRY(gdn_core(e, L.g, L.g.proj, n + 1, L.g.ld, L.g.beta, true));
-        e->conv_par ^= 1u;
-    }
     // Final hiddens of the committed rows: h_p .. h_{p+n}.
     TRY(copy_d2d(e, e->target_hidden + e->H, e->fin, (size_t)(n + 1) * e->H * 4));
     // MTP cache: keep the first draft's entry (token, previous hidden), replay
@@ -781,15 +831,53 @@ extern "C" ctox_status ctox_hip_engine_buffer(ctox_hip_engine *e, uint32_t which
     case 0: *ptr = e->logits; *bytes = (size_t)e->R * e->V * 4; break;
     case 1: *ptr = e->fin; *bytes = (size_t)e->R * e->H * 4; break;
     case 2: *ptr = e->prev_hidden; *bytes = (size_t)e->H * 4; break;
-    case 3: *ptr = e->gdn_state; *bytes = e->gdn_floats * 4; break;
+    case 3: *ptr = state_cur(e); *bytes = e->gdn_floats * 4; break;
     case 4: *ptr = conv_cur(e); *bytes = e->conv_floats * 4; break;
-    case 5: *ptr = e->draft_logits; *bytes = (size_t)std::max(1u, e->c.draft_tokens) * e->V * 4; break;
+    case 5:
+        *ptr = e->draft_logits;
+        *bytes = (size_t)std::max(1u, e->c.draft_tokens) * (e->draft_n ? e->draft_n : e->V) * 4;
+        break;
     default: return efail(CTOX_ERR_SHAPE, "unknown engine buffer");
     }
     return CTOX_OK;
 }
 
 extern "C" uint32_t ctox_hip_engine_position(const ctox_hip_engine *e) { return e ? e->position : 0; }
+
+// Binds the release's MTP draft vocabulary (CpuCorrectnessExecutor::load,
+// Q/src/decoder.rs:1129-1182; ReleaseManifest::load_mtp_draft_token_ids,
+// Q/src/release.rs:414-431): strictly increasing token IDs inside the
+// vocabulary, set once. Drafts then score only those LM-head rows.
+extern "C" ctox_status ctox_hip_engine_set_draft_vocab(ctox_hip_engine *e, const uint32_t *ids, size_t n) {
+    if (!e || (!ids && n)) return efail(CTOX_ERR_SHAPE, "null argument");
+    if (!e->mtp) return efail(CTOX_ERR_UNSUPPORTED_OPERATION, "engine was created without an MTP head");
+    if (e->draft_n) return efail(CTOX_ERR_INVALID_STATE, "the draft vocabulary is already bound");
+    bool canonical = n > 0 && n <= e->V;
+    for (size_t i = 0; canonical && i < n; i++) canonical = ids[i] < e->V && (i == 0 || ids[i - 1] < ids[i]);
+    if (!canonical) return efail(CTOX_ERR_INVALID_ARTIFACT, "noncanonical MTP draft vocabulary");
+    Mat &m = e->draft_head;
+    m.dtype = e->lm_head.dtype;
+    m.rows = (uint32_t)n;
+    m.cols = e->lm_head.cols;
+    m.s_in = e->lm_head.s_in;
+    const size_t rb = (size_t)m.cols / 64 * (m.dtype == CTOX_DTYPE_Q4B64 ? 34 : 18);
+    TRY(dalloc(e, (void **)&m.w, m.bytes()));
+    TRY(dalloc_t(e, &m.s_out, n));
+    TRY(ctox_hip_gather_rows_device(e->b, e->lm_head.w, e->lm_head.rows, rb, ids, n, m.w, e->s));
+    TRY(ctox_hip_gather_rows_device(e->b, e->lm_head.s_out, e->lm_head.rows, 2, ids, n, m.s_out, e->s));
+    TRY(ctox_hip_register_tiled_weights(e->b, m.dtype, m.w, m.rows, m.cols, e->s));
+    e->tiled.push_back(m.w);
+    std::vector<uint32_t> inv(e->V, 0xffffffffu);
+    for (size_t i = 0; i < n; i++) inv[ids[i]] = (uint32_t)i;
+    TRY(dalloc_t(e, &e->d_draft_ids, n));
+    TRY(dalloc_t(e, &e->d_draft_inv, e->V));
+    if (hipMemcpyAsync(e->d_draft_ids, ids, n * 4, hipMemcpyHostToDevice, e->s) != hipSuccess ||
+        hipMemcpyAsync(e->d_draft_inv, inv.data(), (size_t)e->V * 4, hipMemcpyHostToDevice, e->s) != hipSuccess)
+        return efail(CTOX_ERR_INVALID_STATE, "draft vocabulary upload failed");
+    TRY(sync(e));
+    e->draft_n = (uint32_t)n;
+    return CTOX_OK;
+}
 
 // Weights by name, as the crate's tensor names (Q/src/tensor_contract.rs) with
 // the fused matrices named by their first member: "embed", "lm_head",
@@ -872,4 +960,25 @@ extern "C" ctox_status ctox_hip_engine_tensor(ctox_hip_engine *e, const char *na
         if (part == "out") return mat(g.out);
     }
     return efail(CTOX_ERR_SHAPE, "unknown tensor %s", name);
+}
+
+extern "C" ctox_status ctox_hip_engine_cache(ctox_hip_engine *e, uint32_t layer, ctox_engine_cache_view *v) {
+    if (!e || !v) return efail(CTOX_ERR_SHAPE, "null argument");
+    const Cache *c = nullptr;
+    if (layer == 0xffffffffu) {
+        if (!e->mtp) return efail(CTOX_ERR_SHAPE, "engine has no MTP head");
+        c = &e->mtp_attn.cache;
+    } else {
+        if (layer >= e->layers.size() || !e->layers[layer].full)
+            return efail(CTOX_ERR_SHAPE, "layer %u is not a full-attention layer", layer);
+        c = &e->layers[layer].f.cache;
+    }
+    v->descriptors = c->desc.data();
+    v->pages = c->pages;
+    v->tokens = c->tokens;
+    v->d_q4_pool = c->q4;
+    v->d_q2_pool = c->q2;
+    v->q4_page_bytes = e->q4_page_bytes;
+    v->q2_page_bytes = e->q2_page_bytes;
+    return CTOX_OK;
 }

@@ -237,6 +237,12 @@ SIGNATURES = {
     "ctox_hip_greedy_tokens_device": (_I32, [_P, _P, _SZ, _SZ, _P, _P]),
     "ctox_hip_verify_greedy_mtp_device": (_I32, [_P, _P, _P, _P, _SZ, _SZ, _P, _P]),
     "ctox_hip_mtp_accept_device": (_I32, [_P, _P, _P, _P, _P, _SZ, _SZ, ctypes.c_float, _P, _P, _P]),
+    "ctox_hip_mtp_accept_restricted_device": (_I32, [_P, _P, _SZ, _P, _P, _P, _P, _P, _SZ, _SZ, ctypes.c_float, _P,
+                                                     _P, _P]),
+    "ctox_hip_check_finite_device": (_I32, [_P, _P, _SZ, _P, _P]),
+    "ctox_hip_gather_rows_device": (_I32, [_P, _P, _SZ, _SZ, _P, _SZ, _P, _P]),
+    "ctox_hip_gdn_fused_snap_device": (_I32, [_P, _P, _SZ, _SZ, _SZ, _P, _P, _P, _SZ, _SZ, _P, _P, _P, _P, _P, _P,
+                                              _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P]),
     "ctox_hip_rms_norm_device": (_I32, [_P, _P, _SZ, _SZ, _P, ctypes.c_float, _P, _P]),
     "ctox_hip_rms_norm_gated_device": (_I32, [_P, _P, _P, _SZ, _SZ, _P, ctypes.c_float, _P, _P]),
     "ctox_hip_swiglu_device": (_I32, [_P, _P, _P, _SZ, _P, _P]),
@@ -277,6 +283,8 @@ SIGNATURES = {
     "ctox_hip_engine_fill_context": (_I32, [_P, _U32, ctypes.c_uint64]),
     "ctox_hip_engine_buffer": (_I32, [_P, _U32, ctypes.POINTER(_P), ctypes.POINTER(_SZ)]),
     "ctox_hip_engine_position": (_U32, [_P]),
+    "ctox_hip_engine_set_draft_vocab": (_I32, [_P, _P, _SZ]),
+    "ctox_hip_engine_cache": (_I32, [_P, _U32, _P]),
     "ctox_hip_engine_tensor": (_I32, [_P, ctypes.c_char_p, _P]),
 }
 

@@ -38,6 +38,11 @@ class EngineTensor(ctypes.Structure):
                 ("pad", _U32), ("s_in", _P), ("s_out", _P)]
 
 
+class EngineCacheView(ctypes.Structure):
+    _fields_ = [("descriptors", _P), ("pages", _U32), ("tokens", _U32), ("d_q4_pool", _P), ("d_q2_pool", _P),
+                ("q4_page_bytes", _U32), ("q2_page_bytes", _U32)]
+
+
 _hiprt = None
 
 
@@ -90,6 +95,12 @@ class Engine:
         n = out[1]
         return out[0], [out[2 + i] for i in range(n)]
 
+    def set_draft_vocab(self, ids) -> None:
+        """Binds the MTP draft vocabulary (strictly increasing token IDs)."""
+        a = np.ascontiguousarray(ids, dtype=np.uint32)
+        _check(_lib().ctox_hip_engine_set_draft_vocab(self.handle, a.ctypes.data, a.size))
+        self.draft_n = int(a.size)
+
     def fill_context(self, tokens: int, seed: int = 7) -> None:
         _check(_lib().ctox_hip_engine_fill_context(self.handle, tokens, seed))
 
@@ -114,6 +125,22 @@ class Engine:
 
     def logits(self, rows: int = 1) -> np.ndarray:
         return self.read(0, rows * self.config.vocab_size).reshape(rows, -1)
+
+    def cache_pages(self, layer: int):
+        """Pages of a full-attention layer's cache (layer -1: the MTP cache):
+        [(precision, tokens, first_token, bytes)] in page order; bytes hold
+        `tokens` token rows of the page's precision."""
+        v = EngineCacheView()
+        _check(_lib().ctox_hip_engine_cache(self.handle, 0xffffffff if layer < 0 else layer, ctypes.byref(v)))
+        desc = np.ctypeslib.as_array((_U32 * (4 * v.pages)).from_address(v.descriptors)).reshape(-1, 4).copy() \
+            if v.pages else np.zeros((0, 4), np.uint32)
+        kvw = 2 * self.config.num_key_value_heads * self.config.head_dim
+        out = []
+        for prec, slot, tokens, first in desc:
+            tb = kvw // 64 * (34 if prec else 18)
+            pool, pb = (v.d_q4_pool, v.q4_page_bytes) if prec else (v.d_q2_pool, v.q2_page_bytes)
+            out.append((int(prec), int(tokens), int(first), _d2h(pool + int(slot) * pb, int(tokens) * tb).tobytes()))
+        return out
 
     def tensor(self, name: str) -> dict:
         """Host copy of one weight: quantized matrices as raw blocks plus fp16

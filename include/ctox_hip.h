@@ -353,6 +353,22 @@ ctox_status ctox_hip_gdn_fused_device(ctox_hip_backend *backend, const float *d_
                                       float *d_log_decay, float *d_beta, int gates_given, float *d_state,
                                       size_t tokens, size_t heads, size_t key_heads, size_t key_dim,
                                       size_t value_dim, float *d_out, void *stream);
+/* The same core with per-row snapshots, for the speculative verify of the
+ * CUDA runtime's MTP branch (Q/src/backend/cuda_graph.rs:4565-4787 keeps a
+ * restorable branch; here every row's state is kept instead of a checkpoint
+ * and a replay): the state is read from d_state_in and the state after row
+ * t is written at d_state_out + t * snap_stride (floats, at least
+ * heads * key_dim * value_dim), the conv windows after row t at
+ * d_conv_out + t * conv_snap_stride; no snapshot may overlap d_conv_in.
+ * d_state_out may equal d_state_in. Gates are computed (never given). */
+ctox_status ctox_hip_gdn_fused_snap_device(ctox_hip_backend *backend, const float *d_proj, size_t proj_stride,
+                                           size_t a_off, size_t b_off, const float *d_conv_w,
+                                           const float *d_conv_in, float *d_conv_out, size_t conv_snap_stride,
+                                           size_t kernel, const float *d_a_log, const float *d_dt_bias,
+                                           float *d_log_decay, float *d_beta, const float *d_state_in,
+                                           float *d_state_out, size_t snap_stride, size_t tokens, size_t heads,
+                                           size_t key_heads, size_t key_dim, size_t value_dim, float *d_out,
+                                           void *stream);
 
 /* ---- decode-step glue and token selection (device buffers) ---- */
 /* GatedDeltaNet gates, Q/src/decoder.rs:881-902 (softplus :29-35):
@@ -386,6 +402,31 @@ ctox_status ctox_hip_mtp_accept_device(ctox_hip_backend *backend, const float *d
                                        const float *d_bonus, const uint32_t *d_tokens, size_t drafts,
                                        size_t vocab, float temperature, uint64_t *d_rng, uint32_t *d_out,
                                        void *stream);
+/* The same acceptance with restricted draft rows (DraftDistribution::Restricted,
+ * Q/src/engine.rs:151-200; the draft head of Q/src/decoder.rs:589-627 over the
+ * release-bound draft vocabulary): draft rows hold draft_vocab scores and
+ * d_draft_inv[t] (vocab entries) is token t's index in them, 0xffffffff for
+ * tokens outside the draft vocabulary (q = 0 there). d_bonus_ids, when set,
+ * maps a bonus-row index to its token: drafts = 0 with the bonus row a
+ * restricted draft row of `vocab` = draft-vocabulary scores samples a draft
+ * token. d_draft_inv may be NULL when draft_vocab == vocab. */
+ctox_status ctox_hip_mtp_accept_restricted_device(ctox_hip_backend *backend, const float *d_draft,
+                                                  size_t draft_vocab, const uint32_t *d_draft_inv,
+                                                  const float *d_target, const float *d_bonus,
+                                                  const uint32_t *d_bonus_ids, const uint32_t *d_tokens,
+                                                  size_t drafts, size_t vocab, float temperature, uint64_t *d_rng,
+                                                  uint32_t *d_out, void *stream);
+/* Fail-closed check of a logits buffer (Q/src/backend/cuda_runtime.rs:10627-10632):
+ * *d_flag = 1 if any of the n values is not finite, else 0. d_x 16-byte aligned. */
+ctox_status ctox_hip_check_finite_device(ctox_hip_backend *backend, const float *d_x, size_t n, uint32_t *d_flag,
+                                         void *stream);
+/* dst row r = src row ids[r] (rows of row_bytes bytes; ids host values, each
+ * below src_rows). Builds the restricted draft head's compact copy of the LM
+ * head rows once at load (the CUDA runtime gathers them per launch instead,
+ * Q/kernels/cuda/q2q4_fused_matvec_sm86.cu:607-703). Synchronizes `stream`. */
+ctox_status ctox_hip_gather_rows_device(ctox_hip_backend *backend, const void *d_src, size_t src_rows,
+                                        size_t row_bytes, const uint32_t *ids, size_t rows, void *d_dst,
+                                        void *stream);
 
 /* ---- layer glue (device buffers, fp32) ---- */
 /* rms_norm with (1 + w) weight, Q/src/reference.rs:38-62, per row of [rows][cols]. */
@@ -582,8 +623,26 @@ ctox_status ctox_hip_engine_fill_context(ctox_hip_engine *engine, uint32_t token
  * 3 GatedDeltaNet states, 4 conv states, 5 draft logits [k][V]. */
 ctox_status ctox_hip_engine_buffer(ctox_hip_engine *engine, uint32_t which, void **d_ptr, size_t *bytes);
 uint32_t ctox_hip_engine_position(const ctox_hip_engine *engine);
+/* Binds the release's MTP draft vocabulary (ModelExecutor::load's
+ * mtp_draft_token_ids, Q/src/engine.rs:331 and Q/src/decoder.rs:1129-1182;
+ * canonical: strictly increasing, inside the vocabulary, else
+ * CTOX_ERR_INVALID_ARTIFACT). Set once; drafts then use the restricted LM
+ * head (Q/src/decoder.rs:589-627) and the acceptance sees restricted draft
+ * distributions. Without it drafts score the full vocabulary. */
+ctox_status ctox_hip_engine_set_draft_vocab(ctox_hip_engine *engine, const uint32_t *ids, size_t n);
 /* Weights by name ("embed", "lm_head", "final_norm", "L<i>.<part>", "mtp.<part>"). */
 ctox_status ctox_hip_engine_tensor(ctox_hip_engine *engine, const char *name, ctox_engine_tensor *out);
+
+typedef struct {                /* one paged cache of the engine (test view) */
+    const ctox_paged_kv_descriptor *descriptors;  /* host copy, `pages` entries */
+    uint32_t pages, tokens;
+    const uint8_t *d_q4_pool, *d_q2_pool;         /* slot pools (device) */
+    uint32_t q4_page_bytes, q2_page_bytes;
+} ctox_engine_cache_view;
+/* The paged K/V cache of full-attention layer `layer` (layer index of the
+ * model; 0xffffffff: the MTP layer's cache), as PagedKvCache::page_views
+ * exposes pages (Q/src/kv_cache.rs:558-575): valid until the next step. */
+ctox_status ctox_hip_engine_cache(ctox_hip_engine *engine, uint32_t layer, ctox_engine_cache_view *out);
 
 #ifdef __cplusplus
 }

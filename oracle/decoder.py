@@ -34,6 +34,7 @@ from __future__ import annotations
 
 import copy
 import math
+import os
 
 import numpy as np
 
@@ -75,6 +76,9 @@ class OracleDecoder:
         self.mtp_cache = self._cache() if c["mtp_layers"] else None
         self.position = 0
         self.prev_hidden = None
+        # Row-parallel oracle matvecs: rows are independent, so the result
+        # equals the single-threaded one.
+        self.threads = max(1, min(16, os.cpu_count() or 1))
 
     def _cache(self):
         c = self.c
@@ -91,8 +95,23 @@ class OracleDecoder:
 
     def matvec(self, name, x):
         m = self.w(name)
-        return orc.fused_matvec(m["dtype"], m["data"], m["rows"], m["cols"], x, s_in=("f16le", m["s_in"]),
-                                s_out=("f16le", m["s_out"]))
+        return orc.MatVec(m["dtype"], m["data"], m["rows"], m["cols"], x, s_in=("f16le", m["s_in"]),
+                          s_out=("f16le", m["s_out"])).run(threads=self.threads)
+
+    def load_context(self, pages_of, position, prev_hidden):
+        """Starts from a filled context: every full-attention cache (and the
+        MTP cache, which holds position - 1 entries) takes the given pages,
+        pages_of(layer) with layer -1 for the MTP cache."""
+        for l, c in self.caches.items():
+            c.load_pages(pages_of(l))
+            if c.tokens() != position:
+                raise orc.OracleError(7)
+        if self.mtp_cache is not None:
+            self.mtp_cache.load_pages(pages_of(-1))
+            if self.mtp_cache.tokens() != position - 1:
+                raise orc.OracleError(7)
+        self.position = position
+        self.prev_hidden = np.asarray(prev_hidden, np.float32).copy()
 
     def norm(self, x, name, rows=1):
         x = np.asarray(x, np.float32).reshape(-1)

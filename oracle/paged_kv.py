@@ -109,10 +109,27 @@ class PagedKvCache:
             self.pages.append(Page(Q4, min(self.page_tokens, self.maximum_tokens - self.n_tokens),
                                    2 * self.component_values, bytearray()))
         combined = np.concatenate([np.asarray(key, np.float32), np.asarray(value, np.float32)])
-        self.pages[-1].data += quantize_values(combined, Q4)
+        # QuantizedKvPage::push (:199-206) appends in the page's precision: a
+        # partial page demoted by a zero recent window takes Q2 rows.
+        self.pages[-1].data += quantize_values(combined, self.pages[-1].precision)
         self.n_tokens += 1
         pi = len(self.pages) - 1
         return pi, self.pages[pi].tokens() - 1, (self.demote_old_pages() if demote else [])
+
+    def load_pages(self, pages) -> None:
+        """Replaces the contents with pages [(precision, tokens, first_token,
+        bytes)] in page order, as page_views reports them (a filled cache of
+        the device engine, whose page bytes are the crate's canonical ones)."""
+        self.pages, self.n_tokens = [], 0
+        for prec, tokens, first, data in pages:
+            if first != self.n_tokens or first % self.page_tokens:
+                raise orc.OracleError(7)
+            p = Page(Q4 if prec else Q2, min(self.page_tokens, self.maximum_tokens - self.n_tokens),
+                     2 * self.component_values, bytearray(data))
+            if p.tokens() != tokens:
+                raise orc.OracleError(7)
+            self.pages.append(p)
+            self.n_tokens += tokens
 
     def demote_old_pages(self) -> List[int]:
         """:463-478: a Q4 page leaves once it is past the sink and wholly older

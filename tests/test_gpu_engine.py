@@ -84,3 +84,136 @@ def test_engine_mtp_steps_match_oracle(pair):
     want = ref.decode(token)
     eng.decode(token)
     close(eng.logits(1)[0], want)
+
+
+def run_mtp_steps(eng, ref, rng, steps, token, T=0.7, drafts=4, tag=""):
+    from oracle import oracle as orc
+    state0 = 0x5EED1234ABCD
+    g = orc.Pcg32(0)
+    g.c.state = state0
+    eng.set_rng(state0)
+    accepted = []
+    for step in range(steps):
+        say(f"case engine mtp{tag} step={step} token={token} position={ref.position}")
+        nxt, acc, _ = ref.mtp_step(token, T, g, drafts)
+        got_next, got_acc = eng.mtp_step(token, T)
+        assert (got_next, got_acc) == (nxt, [int(x) for x in acc]), (step, got_next, got_acc, nxt, acc)
+        assert eng.position == ref.position
+        accepted.append(len(acc))
+        token = nxt
+    say("accepted per step", accepted)
+    return token
+
+
+def test_engine_restricted_draft_vocab_matches_oracle(hip):
+    """The restricted MTP draft head (Q/src/decoder.rs:589-627): drafts score
+    only the bound draft vocabulary; acceptance uses restricted draft laws.
+    Accepted drafts and next tokens equal the oracle's, and a following plain
+    step's logits agree."""
+    from ctox_hip.engine import Engine
+    from oracle.decoder import OracleDecoder
+    cfg = small_config()
+    eng = Engine(hip, cfg, seed=5)
+    try:
+        ids = np.sort(np.random.default_rng(9).choice(512, 96, replace=False)).astype(np.uint32)
+        eng.set_draft_vocab(ids)
+        ref = OracleDecoder(cfg.as_dict(), eng.tensor, draft_ids=ids)
+        rng = np.random.default_rng(4)
+        for step in range(20):
+            tok = int(rng.integers(0, 512))
+            ref.decode(tok)
+            eng.decode(tok)
+        token = run_mtp_steps(eng, ref, rng, 8, int(rng.integers(0, 512)), tag=" restricted")
+        # the draft rows are the restricted head's scores (draft logits view)
+        d = eng.read(5, 4 * ids.size).reshape(4, ids.size)
+        assert np.all(np.isfinite(d))
+        want = ref.decode(token)
+        eng.decode(token)
+        close(eng.logits(1)[0], want)
+    finally:
+        eng.close()
+
+
+def test_engine_draft_vocab_rejects_noncanonical(hip):
+    import ctox_hip
+    from ctox_hip.engine import Engine
+    eng = Engine(hip, small_config(), seed=5)
+    try:
+        for bad in ([4, 1], [1, 1], [1, 512], []):
+            with pytest.raises(ctox_hip.InvalidArtifact):
+                eng.set_draft_vocab(bad)
+        eng.set_draft_vocab([1, 2, 3])
+        with pytest.raises(ctox_hip.InvalidState):
+            eng.set_draft_vocab([4, 5])
+    finally:
+        eng.close()
+
+
+def test_engine_short_recent_window_matches_oracle(hip):
+    """A recent window (1 token) below the verify rows: pages are demoted only
+    after the new rows are appended, in the crate's append-then-demote order.
+    A zero window (the crate then appends Q2 rows to the page being filled)
+    is refused."""
+    import ctox_hip
+    from ctox_hip.engine import Engine
+    from oracle.decoder import OracleDecoder
+    cfg = small_config()
+    cfg.recent_tokens = 0
+    with pytest.raises(ctox_hip.UnsupportedOperation):
+        Engine(hip, cfg, seed=7)
+    cfg.recent_tokens = 1
+    cfg.sink_tokens = 0
+    eng = Engine(hip, cfg, seed=7)
+    try:
+        ref = OracleDecoder(cfg.as_dict(), eng.tensor)
+        rng = np.random.default_rng(8)
+        for step in range(36):
+            tok = int(rng.integers(0, 512))
+            say(f"case engine recent=1 decode step={step}")
+            want = ref.decode(tok)
+            eng.decode(tok)
+            close(eng.logits(1)[0], want)
+        token = run_mtp_steps(eng, ref, rng, 4, int(rng.integers(0, 512)), tag=" recent=1")
+        want = ref.decode(token)
+        eng.decode(token)
+        close(eng.logits(1)[0], want)
+        assert ref.caches[3].q2_tokens() > 0
+    finally:
+        eng.close()
+
+
+def _poison(eng, name):
+    """Writes NaN into an engine weight vector (host-side write, then the next step reads it)."""
+    import ctypes
+    from ctox_hip.engine import EngineTensor, _lib, _check
+    t = EngineTensor()
+    _check(_lib().ctox_hip_engine_tensor(eng.handle, name.encode(), ctypes.byref(t)))
+    nan = np.full(t.bytes // 4, np.nan, np.float32)
+    rt = ctypes.CDLL("libamdhip64.so")
+    rt.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    assert rt.hipMemcpy(t.data, nan.ctypes.data, t.bytes, 1) == 0
+
+
+def test_engine_fails_closed_on_nonfinite_logits(hip):
+    """Non-finite logits end the step with InvalidState
+    (Q/src/backend/cuda_runtime.rs:10627-10632, Q/src/engine.rs:191-272):
+    plain decode, and an MTP step whose draft head is poisoned."""
+    import ctox_hip
+    from ctox_hip.engine import Engine
+    eng = Engine(hip, small_config(), seed=11)
+    try:
+        eng.decode(3)
+        eng.decode(4)
+        _poison(eng, "mtp.norm")
+        with pytest.raises(ctox_hip.InvalidState):
+            eng.mtp_step(5, 0.7)
+    finally:
+        eng.close()
+    eng = Engine(hip, small_config(), seed=11)
+    try:
+        eng.decode(3)
+        _poison(eng, "final_norm")
+        with pytest.raises(ctox_hip.InvalidState):
+            eng.decode(4)
+    finally:
+        eng.close()

@@ -102,10 +102,12 @@ def test_chunked_prefill_ragged(hip, orc, case):
     close(st_gpu, st_ref, 1e-4, "state")
 
 
-def test_chunked_prefill_long(hip, orc):
-    """1024 tokens of BASELINE config 4 shapes through the chunk-64 path."""
-    say("case gdn chunked long")
-    heads, dk, dv, T = 32, 128, 128, 1024
+@pytest.mark.parametrize("T", [1024, 4096])
+def test_chunked_prefill_long(hip, orc, T):
+    """BASELINE config 4 shapes through the chunk-64 path, up to the config's
+    full 4096-token prefill."""
+    say(f"case gdn chunked long T={T}")
+    heads, dk, dv = 32, 128, 128
     q, k, v, ld, be = gdn_inputs(T, heads, 16, dk, dv, 11)
     st_ref = np.zeros(heads * dk * dv, np.float32)
     st_gpu = st_ref.copy()
@@ -238,3 +240,57 @@ def test_fused_mixer_core_matches_separate(hip, tokens, heads, key_heads, dk, dv
     ref_o, ref_s = out_a.cpu().numpy(), st_a.cpu().numpy()
     np.testing.assert_allclose(out_b.cpu().numpy(), ref_o, rtol=1e-4, atol=1e-5 * float(np.abs(ref_o).max()))
     np.testing.assert_allclose(st_b.cpu().numpy(), ref_s, rtol=1e-4, atol=1e-5 * float(np.abs(ref_s).max()))
+
+
+def test_fused_snapshots_equal_sequential_steps(hip):
+    """ctox_hip_gdn_fused_snap_device: the state and conv windows after each
+    row t equal those of running the fused core over the first t + 1 rows
+    (in place), and the outputs are the same."""
+    import torch
+    import ctox_hip
+    say("case fused snapshots")
+    lib = ctox_hip.load_library()
+    rng = np.random.default_rng(77)
+    tokens, heads, key_heads, dk, dv, K = 5, 48, 16, 128, 128, 4
+    kw, vw = key_heads * dk, heads * dv
+    C = 2 * kw + vw
+    a_off, b_off = C + vw, C + vw + heads
+    stride = b_off + heads
+    dev = lambda x: torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+    p = lambda t: t.data_ptr()
+    proj = dev(rng.standard_normal((tokens, stride)))
+    conv_w = dev(rng.standard_normal((C, K)) * 0.5)
+    conv0 = rng.standard_normal((C, K)).astype(np.float32)
+    a_log = dev(rng.standard_normal(heads) * 0.3)
+    dt_bias = dev(rng.standard_normal(heads) * 0.3)
+    state0 = (rng.standard_normal((heads, dk, dv)) * 0.1).astype(np.float32)
+    ssz, csz = heads * dk * dv, C * K
+    st_in = dev(state0)
+    snaps = torch.full((tokens, ssz), float("nan"), device="cuda")
+    csnaps = torch.full((tokens, csz), float("nan"), device="cuda")
+    conv_in = dev(conv0)
+    ld, be = torch.empty(tokens, heads, device="cuda"), torch.empty(tokens, heads, device="cuda")
+    out = torch.empty(tokens, heads, dv, device="cuda")
+    st = lib.ctox_hip_gdn_fused_snap_device(hip.handle, p(proj), stride, a_off, b_off, p(conv_w), p(conv_in),
+                                            p(csnaps), csz, K, p(a_log), p(dt_bias), p(ld), p(be), p(st_in), p(snaps),
+                                            ssz, tokens, heads, key_heads, dk, dv, p(out), None)
+    assert st == 0, lib.ctox_hip_last_error()
+    # aliasing conv windows are refused
+    assert lib.ctox_hip_gdn_fused_snap_device(hip.handle, p(proj), stride, a_off, b_off, p(conv_w), p(conv_in),
+                                              p(conv_in) - 4 * csz, csz, K, p(a_log), p(dt_bias), p(ld), p(be),
+                                              p(st_in), p(snaps), ssz, tokens, heads, key_heads, dk, dv, p(out),
+                                              None) != 0
+    torch.cuda.synchronize()
+    assert np.array_equal(st_in.cpu().numpy(), state0)  # input untouched (other output buffer)
+    for t in range(tokens):
+        st_b, cin, cout = dev(state0), dev(conv0), torch.zeros(C, K, device="cuda")
+        ld_b, be_b = torch.empty(t + 1, heads, device="cuda"), torch.empty(t + 1, heads, device="cuda")
+        out_b = torch.empty(t + 1, heads, dv, device="cuda")
+        assert lib.ctox_hip_gdn_fused_device(hip.handle, p(proj), stride, a_off, b_off, p(conv_w), p(cin), p(cout), K,
+                                             p(a_log), p(dt_bias), p(ld_b), p(be_b), 0, p(st_b), t + 1, heads,
+                                             key_heads, dk, dv, p(out_b), None) == 0
+        torch.cuda.synchronize()
+        assert np.array_equal(snaps[t].cpu().numpy(), st_b.cpu().numpy().reshape(-1)), t
+        assert np.array_equal(csnaps[t].cpu().numpy(), cout.cpu().numpy().reshape(-1)), t
+        if t == tokens - 1:
+            assert np.array_equal(out.cpu().numpy(), out_b.cpu().numpy())

@@ -83,10 +83,29 @@ def test_matvec_host_api_small_shapes(hip, orc, dtype, rows, cols):
         check(got, ref, f"dtype={dtype} {rows}x{cols} {sk}")
 
 
-# Batch 1 on columns % 512 == 0 runs the slice kernels: 28 (Q4) / 56 (Q2)
-# blocks per slice, all slices requested up front for 1..3 slices, walked
-# beyond. These widths give every slice count of both dtypes at least once.
+# Raw launches on weights without a tiled copy run the crate-layout kernels:
+# batch 1 on columns % 512 == 0 the slice kernels (28 (Q4) / 56 (Q2) blocks
+# per slice, all slices requested up front for 1..3 slices, walked beyond),
+# M = 2..8 the small-M slice kernels. These widths give every slice count of
+# both dtypes at least once.
 SLICE_COLS = [512, 1536, 3584, 5120, 7168, 10752, 17408]
+
+
+def raw_run(hip, dtype, parts, rows, cols, act):
+    """ctox_hip_launch_fused_matvec on unregistered device weights (f16 scales)."""
+    torch = _torch()
+    w, x, osi, oso, b = parts
+    dw = torch.from_numpy(np.ascontiguousarray(w)).cuda()
+    dx = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    dsi = torch.from_numpy(np.ascontiguousarray(osi[1]).view(np.int16)).cuda()
+    dso = torch.from_numpy(np.ascontiguousarray(oso[1]).view(np.int16)).cuda()
+    db = torch.from_numpy(b).cuda() if b is not None else None
+    dy = torch.empty((x.shape[0], rows), device="cuda")
+    hip.launch_fused_matvec(ctox_hip.TensorDType(dtype), dw.data_ptr(), dx.data_ptr(), dsi.data_ptr(), dso.data_ptr(),
+                            None if db is None else db.data_ptr(), dy.data_ptr(), rows, cols, act, x.shape[0],
+                            torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return dy.cpu().numpy()
 
 
 @pytest.mark.parametrize("dtype", [0, 1])
@@ -95,7 +114,7 @@ def test_batch1_slice_counts(hip, orc, dtype, cols):
     for rows in (16, 37):
         say(f"case slices dtype={dtype} rows={rows} cols={cols}")
         op, parts = make_case(dtype, rows, cols, 7 * cols + rows, "f16", True, ctox_hip.Activation.Silu)
-        got = hip.fused_matvec(op)
+        got = raw_run(hip, dtype, parts, rows, cols, ctox_hip.Activation.Silu)[0]
         ref = oracle_rows(orc, dtype, rows, cols, parts, ctox_hip.Activation.Silu)[0]
         check(got, ref, f"slices dtype={dtype} {rows}x{cols}")
 
@@ -200,7 +219,7 @@ def test_small_m_slice_counts(hip, orc, batch, dtype):
         say(f"case small-m slices batch={batch} dtype={dtype} {rows}x{cols}")
         op, parts = make_case(dtype, rows, cols, 3 * cols + batch, "f16", bias=True, act=ctox_hip.Activation.Silu,
                               batch=batch)
-        got = resident_run(hip, op, parts[1])
+        got = raw_run(hip, dtype, parts, rows, cols, ctox_hip.Activation.Silu)
         ref = oracle_rows(orc, dtype, rows, cols, parts, ctox_hip.Activation.Silu)
         check(got, ref, f"small-m slices batch={batch} dtype={dtype} {rows}x{cols}")
 
@@ -407,3 +426,30 @@ def test_artifact_mixed_recovered_upload(hip, orc, tmp_path):
                                s_out=("f16le", s_out.view(np.uint8)),
                                segments=[(0, 0, r2, 0, 0, q2.size), (1, r2, r2 + r4, 1, q2.size, q4.size)])
         check(got[b], ref, f"artifact mixed batch row {b}")
+
+
+def test_calls_on_two_streams_are_ordered(hip, orc):
+    """The backend's scratch (activation staging, combine slots) is shared:
+    device calls issued back to back on two streams, with no host wait in
+    between, still each see their own inputs (the second stream waits for
+    the first)."""
+    torch = _torch()
+    say("case two streams")
+    rows, cols = 5120, 17408
+    op, parts = make_case(0, rows, cols, 31, "f16", bias=False, batch=1)
+    m = hip.prepare(op)
+    x2 = synth.activation("normal", cols, 32, 1)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    d1 = torch.from_numpy(parts[1]).cuda()
+    d2 = torch.from_numpy(x2).cuda()
+    y1 = torch.empty((1, rows), device="cuda")
+    y2 = torch.empty((1, rows), device="cuda")
+    torch.cuda.synchronize()
+    for _ in range(3):
+        m.dispatch(d1.data_ptr(), 1, y1.data_ptr(), s1.cuda_stream)
+        m.dispatch(d2.data_ptr(), 1, y2.data_ptr(), s2.cuda_stream)
+    torch.cuda.synchronize()
+    w, x, osi, oso, b = parts
+    check(y1.cpu().numpy()[0], orc.fused_matvec(0, w, rows, cols, x[0], osi, oso), "stream 1")
+    check(y2.cpu().numpy()[0], orc.fused_matvec(0, w, rows, cols, x2[0], osi, oso), "stream 2")
+    m.close()

@@ -145,3 +145,19 @@ def test_paged_cache_contract_errors(orc):
     cache.push(np.zeros(64), np.zeros(64))
     with pytest.raises(orc_mod.OracleError):
         cache.push(np.zeros(64), np.zeros(64))
+
+
+def test_zero_recent_window_appends_in_page_precision(orc):
+    """Q/src/kv_cache.rs:199-206, 463-478: with recent 0 the page being filled
+    is demoted after each push and later tokens are appended to it as Q2."""
+    from oracle import paged_kv as pk
+    c = pk.PagedKvCache(64, 64, 16, 0, 0)
+    rng = np.random.default_rng(0)
+    rows = rng.standard_normal((3, 2, 64)).astype(np.float32)
+    for k, v in rows:
+        c.push(k, v)
+    assert c.q2_tokens() == 3 and c.q4_tokens() == 0
+    want = np.concatenate([pk.dequantize_bytes(pk.quantize_values(np.concatenate([k, v]), pk.Q2), pk.Q2)
+                           for k, v in rows[1:]])
+    got = np.concatenate([c.pages[0].token(t) for t in (1, 2)])
+    np.testing.assert_array_equal(got, want)
