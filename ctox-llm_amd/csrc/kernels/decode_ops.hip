@@ -112,7 +112,14 @@ extern "C" __global__ __launch_bounds__(256) void ctox_row_partials_gfx950(Parti
     }
     const float invt = 1.0f / a.temperature;
     float m = -INFINITY;
-    for (uint32_t i = b + threadIdx.x; i < e; i += 256) m = fmaxf(m, row[i] * invt);
+    int bad = 0;
+    for (uint32_t i = b + threadIdx.x; i < e; i += 256) {
+        bad |= !__builtin_isfinite(row[i]);
+        m = fmaxf(m, row[i] * invt);
+    }
+    // A non-finite logit anywhere in the row makes its part's sum NaN, which
+    // the decision pass reports (the step fails closed).
+    bad = __syncthreads_or(bad);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
     if (lane == 0) s0[w] = m;
@@ -127,7 +134,7 @@ extern "C" __global__ __launch_bounds__(256) void ctox_row_partials_gfx950(Parti
     __syncthreads();
     if (threadIdx.x == 0) {
         o[0] = mm;
-        o[1] = (s1[0] + s1[1]) + (s1[2] + s1[3]);
+        o[1] = bad ? __builtin_nanf("") : (s1[0] + s1[1]) + (s1[2] + s1[3]);
     }
 }
 
@@ -216,6 +223,19 @@ extern "C" __global__ __launch_bounds__(64) void ctox_mtp_decide_gfx950(AcceptAr
     uint64_t s = *a.rng;  // every lane replays the same draws
     PickState st{};
     uint32_t acc = 0;
+    // Fail closed: a non-finite logit in any row (NaN part sum) ends the
+    // step with no token (mode 3) and consumes no draw.
+    bool finite = true;
+    for (uint32_t r = 0; r < 2 * a.drafts + 1; r++) {
+        float m, z;
+        merge_stats(a.partials + (size_t)r * a.parts * 2, a.parts, m, z);
+        finite = finite && __builtin_isfinite(z) && z > 0.0f;
+    }
+    if (!finite) {
+        st.mode = 3;
+        if (lead) *a.state = st;
+        return;
+    }
     for (uint32_t i = 0; i < a.drafts; i++) {
         float tm, tz, dm, dz;
         merge_stats(a.partials + (size_t)(a.drafts + i) * a.parts * 2, a.parts, tm, tz);
@@ -277,7 +297,7 @@ __device__ __forceinline__ float pick_weight(const AcceptArgs &a, const PickStat
 extern "C" __global__ __launch_bounds__(256) void ctox_pick_sums_gfx950(AcceptArgs a) {
     __shared__ float red[4];
     const PickState st = *a.state;
-    if (st.mode == 2) return;
+    if (st.mode >= 2) return;
     const float invt = 1.0f / a.temperature;
     const uint32_t per = (a.vocab + a.parts2 - 1) / a.parts2;
     const uint32_t b = blockIdx.x * per, e = min(a.vocab, b + per);
@@ -300,9 +320,9 @@ extern "C" __global__ __launch_bounds__(1024) void ctox_pick_final_gfx950(Accept
     __shared__ uint32_t res[3];
     const PickState st = *a.state;
     const uint32_t tid = threadIdx.x;
-    if (st.mode == 2) {
+    if (st.mode >= 2) {  // 2: a proposed token outside the vocabulary, 3: non-finite logits
         if (tid == 0) {
-            a.out[0] = 0xffffffffu;
+            a.out[0] = st.mode == 3 ? 0xfffffffeu : 0xffffffffu;
             a.out[1] = st.accepted;
         }
         return;

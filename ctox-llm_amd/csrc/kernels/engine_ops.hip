@@ -18,7 +18,7 @@
 //  * ctox_swiglu_rows_gfx950: out[t][c] = silu(in[t][c]) * in[t][off + c]
 //    over token rows of a fused gate|up projection (Q/src/reference.rs:96-112).
 //  * ctox_copy_rows_gfx950: strided row copy.
-//  * ctox_finite_check_gfx950: one workgroup flags a non-finite value in a
+//  * ctox_finite_check_gfx950: per-part flags of non-finite values in a
 //    buffer (the engine's fail-closed check of logits).
 //  * ctox_gather_rows_gfx950: byte rows gathered by index (the restricted
 //    draft head's compact LM-head copy).
@@ -190,18 +190,21 @@ extern "C" __global__ __launch_bounds__(64) void ctox_write_words_gfx950(WordsAr
     if (threadIdx.x < a.count) a.dst[threadIdx.x] = a.words[threadIdx.x];
 }
 
-// One workgroup of 1024 threads; the flag is always written (no clear needed).
-extern "C" __global__ __launch_bounds__(1024) void ctox_finite_check_gfx950(FiniteArgs a) {
+// grid (parts), 256 threads: part p checks its contiguous range of float4
+// (the tail floats by the last part) and always writes flags[p].
+extern "C" __global__ __launch_bounds__(256) void ctox_finite_check_gfx950(FiniteArgs a) {
     int bad = 0;
-    const uint64_t n4 = a.n / 4;
+    const uint64_t n4 = a.n / 4, per = (n4 + gridDim.x - 1) / gridDim.x;
+    const uint64_t b = (uint64_t)blockIdx.x * per, e = min(n4, b + per);
     const float4 *x4 = (const float4 *)a.x;
-    for (uint64_t i = threadIdx.x; i < n4; i += 1024) {
+    for (uint64_t i = b + threadIdx.x; i < e; i += 256) {
         const float4 v = x4[i];
         bad |= !__builtin_isfinite(v.x) | !__builtin_isfinite(v.y) | !__builtin_isfinite(v.z) | !__builtin_isfinite(v.w);
     }
-    for (uint64_t i = 4 * n4 + threadIdx.x; i < a.n; i += 1024) bad |= !__builtin_isfinite(a.x[i]);
+    if (blockIdx.x + 1 == gridDim.x)
+        for (uint64_t i = 4 * n4 + threadIdx.x; i < a.n; i += 256) bad |= !__builtin_isfinite(a.x[i]);
     bad = __syncthreads_or(bad);
-    if (threadIdx.x == 0) *a.flag = bad ? 1u : 0u;
+    if (threadIdx.x == 0) a.flags[blockIdx.x] = bad ? 1u : 0u;
 }
 
 // grid (rows), 256 threads: dst row r = src row ids[r], 16 bytes per thread step.

@@ -125,6 +125,7 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_scan_gfx950(GdnArgs a
 // conv arithmetic is that of ctox_conv_update_gfx950, the gates that of
 // ctox_gdn_gates_gfx950 (same operation order).
 #define GDN_MAX_KERNEL 8
+#define GDN_PREFETCH 8  // token rows whose inputs are loaded up front
 extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_gfx950(GdnFusedArgs a) {
     __shared__ float red_mem[GDN_GROUPS][GDN_COLS];
     __shared__ float red_out[GDN_GROUPS][GDN_COLS];
@@ -158,16 +159,56 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_gfx950(GdnFused
         sv_[i] = v_thr && ok ? a.conv_in[(size_t)v_ch * K + i] : 0.0f;
     }
 
-    float *S = a.state + (size_t)h * dk * a.value_dim;
     float s[GDN_MAX_ROWS];
+    // Blocked layout: this thread's 8 rows at one 32-byte run.
+    const size_t blk = (((size_t)h * slices + slice) * 256 + tid) * 8;
+    const size_t head_floats = a.state_blocked ? (size_t)slices * 2048 : (size_t)dk * a.value_dim;
+    if (a.state_blocked) {
+        const float4 *S4 = (const float4 *)(a.state + blk);
+        const float4 lo = S4[0], hi = S4[1];
+        s[0] = lo.x; s[1] = lo.y; s[2] = lo.z; s[3] = lo.w;
+        s[4] = hi.x; s[5] = hi.y; s[6] = hi.z; s[7] = hi.w;
 #pragma unroll
-    for (int r = 0; r < GDN_MAX_ROWS; r++) {
-        const uint32_t i = ig + GDN_GROUPS * r;
-        s[r] = ((uint32_t)r < nrows && i < dk && colok) ? S[(size_t)i * a.value_dim + j] : 0.0f;
+        for (int r = 8; r < GDN_MAX_ROWS; r++) s[r] = 0.0f;
+    } else {
+        const float *S = a.state + (size_t)h * head_floats;
+#pragma unroll
+        for (int r = 0; r < GDN_MAX_ROWS; r++) {
+            const uint32_t i = ig + GDN_GROUPS * r;
+            s[r] = ((uint32_t)r < nrows && i < dk && colok) ? S[(size_t)i * a.value_dim + j] : 0.0f;
+        }
     }
+    auto store_state = [&](float *base) {
+        if (a.state_blocked) {
+            float4 *S4 = (float4 *)(base + blk);
+            S4[0] = make_float4(s[0], s[1], s[2], s[3]);
+            S4[1] = make_float4(s[4], s[5], s[6], s[7]);
+            return;
+        }
+        float *So = base + (size_t)h * head_floats;
+#pragma unroll
+        for (int r = 0; r < GDN_MAX_ROWS; r++) {
+            const uint32_t i = ig + GDN_GROUPS * r;
+            if ((uint32_t)r < nrows && i < dk && colok) So[(size_t)i * a.value_dim + j] = s[r];
+        }
+    };
 
-    for (uint32_t t = 0; t < a.tokens; t++) {
+    // This thread's inputs of a token (its conv channels, and the gate
+    // inputs for thread 255) are loaded ahead of the stores of earlier
+    // tokens: a load issued after a store waits for it (loads and stores
+    // retire in one in-order counter).
+    auto load_in = [&](uint32_t t, float &xq, float &xv, float &ga, float &gb) {
         const float *row = a.proj + (size_t)t * a.proj_stride;
+        xq = qk_thr ? row[qk_ch] : 0.0f;
+        xv = v_thr ? row[v_ch] : 0.0f;
+        const size_t th = (size_t)t * a.heads + h;
+        ga = tid != 255 ? 0.0f : (a.gates_given ? a.log_decay[th] : row[a.a_off + h]);
+        gb = tid != 255 ? 0.0f : (a.gates_given ? a.beta[th] : row[a.b_off + h]);
+    };
+    const float dtb = tid == 255 && !a.gates_given ? a.dt_bias[h] : 0.0f;
+    const float alog = tid == 255 && !a.gates_given ? a.a_log[h] : 0.0f;
+    // One token's step on inputs already in registers.
+    auto step = [&](uint32_t t, float cxq, float cxv, float cga, float cgb) {
         // Conv step: shift the window left by one, append the input.
         if (qk_thr) {
             float sum = 0.0f;
@@ -178,7 +219,7 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_gfx950(GdnFused
                     sq_[i] = v;
                     sum += v * wq[i];
                 }
-            const float x = row[qk_ch];
+            const float x = cxq;
 #pragma unroll
             for (int i = 0; i < GDN_MAX_KERNEL; i++)
                 if ((uint32_t)i == K - 1) sq_[i] = x;
@@ -200,7 +241,7 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_gfx950(GdnFused
                     sv_[i] = v;
                     sum += v * wv[i];
                 }
-            const float x = row[v_ch];
+            const float x = cxv;
             float wl = 0.0f;
 #pragma unroll
             for (int i = 0; i < GDN_MAX_KERNEL; i++)
@@ -215,13 +256,13 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_gfx950(GdnFused
             const size_t th = (size_t)t * a.heads + h;
             float be, ld;
             if (a.gates_given) {
-                be = a.beta[th];
-                ld = a.log_decay[th];
+                be = cgb;
+                ld = cga;
             } else {
-                be = 1.0f / (1.0f + expf(-row[a.b_off + h]));
-                const float x = row[a.a_off + h] + a.dt_bias[h];
+                be = 1.0f / (1.0f + expf(-cgb));
+                const float x = cga + dtb;
                 const float sp = x > 20.0f ? x : log1pf(expf(x));
-                ld = -expf(a.a_log[h]) * sp;
+                ld = -expf(alog) * sp;
                 if (slice == 0) {
                     a.beta[th] = be;
                     a.log_decay[th] = ld;
@@ -277,12 +318,7 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_gfx950(GdnFused
         }
         if (a.snap_stride) {
             // Row snapshot: the state and conv windows after token t.
-            float *So = a.state_out + (size_t)t * a.snap_stride + (size_t)h * dk * a.value_dim;
-#pragma unroll
-            for (int r = 0; r < GDN_MAX_ROWS; r++) {
-                const uint32_t i = ig + GDN_GROUPS * r;
-                if ((uint32_t)r < nrows && i < dk && colok) So[(size_t)i * a.value_dim + j] = s[r];
-            }
+            store_state(a.state_out + (size_t)t * a.snap_stride);
             float *co = a.conv_out + (size_t)t * a.conv_snap_stride;
             if (qk_thr && h % rep == 0 && slice == 0)
 #pragma unroll
@@ -296,15 +332,36 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_gfx950(GdnFused
         // qs/ks/vs/gsc and red_* are rewritten next token only after every
         // thread has passed this barrier.
         __syncthreads();
+    };
+    if (a.tokens <= GDN_PREFETCH) {
+        // Every token's inputs are loaded before the first token's stores,
+        // so no wait inside the loop ever covers an earlier store (the
+        // verify rows' snapshots stream out while later tokens compute).
+        float pq[GDN_PREFETCH], pv[GDN_PREFETCH], pa[GDN_PREFETCH], pb[GDN_PREFETCH];
+#pragma unroll
+        for (int u = 0; u < GDN_PREFETCH; u++) load_in(min((uint32_t)u, a.tokens - 1), pq[u], pv[u], pa[u], pb[u]);
+        for (uint32_t t = 0; t < a.tokens; t++) {
+            step(t, pq[0], pv[0], pa[0], pb[0]);
+#pragma unroll
+            for (int u = 0; u + 1 < GDN_PREFETCH; u++) {
+                pq[u] = pq[u + 1];
+                pv[u] = pv[u + 1];
+                pa[u] = pa[u + 1];
+                pb[u] = pb[u + 1];
+            }
+        }
+    } else {
+        float nxq, nxv, nga, ngb;
+        load_in(0, nxq, nxv, nga, ngb);
+        for (uint32_t t = 0; t < a.tokens; t++) {
+            const float cxq = nxq, cxv = nxv, cga = nga, cgb = ngb;
+            if (t + 1 < a.tokens) load_in(t + 1, nxq, nxv, nga, ngb);
+            step(t, cxq, cxv, cga, cgb);
+        }
     }
     if (a.snap_stride) return;
 
-    float *So = a.state_out + (size_t)h * dk * a.value_dim;
-#pragma unroll
-    for (int r = 0; r < GDN_MAX_ROWS; r++) {
-        const uint32_t i = ig + GDN_GROUPS * r;
-        if ((uint32_t)r < nrows && i < dk && colok) So[(size_t)i * a.value_dim + j] = s[r];
-    }
+    store_state(a.state_out);
     // Final conv windows, each written once.
     if (qk_thr && h % rep == 0 && slice == 0)
 #pragma unroll

@@ -260,6 +260,12 @@ struct GdnFusedArgs {
     uint32_t a_off;
     uint32_t b_off;
     uint32_t gates_given;
+    // 0: state [head][key i][value j] (the crate's layout); 1: the engine's
+    // blocked layout, per head and 16-column slice the 256 threads' 8 rows
+    // contiguous ([head][slice][ig * 16 + jj][r] for i = ig + 16 r,
+    // j = 16 slice + jj; key_dim <= 128), so a wave moves 2 KiB per access.
+    uint32_t state_blocked;
+    uint32_t pad;
 };
 
 // Decode-step glue and token selection (decode_ops.hip).
@@ -309,7 +315,7 @@ struct PickState {
     float m_d, z_d;          // draft row stats (residual mode)
     uint32_t row;            // draft index of the rejection (residual) or drafts (bonus)
     uint32_t accepted;
-    uint32_t mode;           // 0 residual max(0, p - q), 1 bonus softmax, 2 invalid token
+    uint32_t mode;           // 0 residual max(0, p - q), 1 bonus softmax, 2 invalid token, 3 non-finite logits
 };
 
 struct VerifyArgs {
@@ -527,7 +533,7 @@ struct RowsArgs {
 
 struct FiniteArgs {          // ctox_finite_check_gfx950
     const float *x;
-    uint32_t *flag;          // written: 1 if any of the n values is not finite, else 0
+    uint32_t *flags;         // [gridDim.x]: 1 if a value of the workgroup's range is not finite, else 0
     uint64_t n;
 };
 

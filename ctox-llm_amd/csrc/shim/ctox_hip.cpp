@@ -1416,8 +1416,8 @@ ctox_status gdn_fused_impl(ctox_hip_backend *b, const float *d_proj, size_t proj
                            const float *d_conv_w, const float *d_conv_in, float *d_conv_out, size_t kernel,
                            const float *d_a_log, const float *d_dt_bias, float *d_log_decay, float *d_beta,
                            int gates_given, const float *d_state_in, float *d_state_out, size_t snap_stride,
-                           size_t conv_snap_stride, size_t tokens, size_t heads, size_t key_heads, size_t key_dim,
-                           size_t value_dim, float *d_out, void *stream) {
+                           size_t conv_snap_stride, int blocked, size_t tokens, size_t heads, size_t key_heads,
+                           size_t key_dim, size_t value_dim, float *d_out, void *stream) {
     if (!b || !d_proj || !d_conv_w || !d_conv_in || !d_conv_out || !d_log_decay || !d_beta || !d_state_in ||
         !d_state_out || !d_out || (!gates_given && (!d_a_log || !d_dt_bias)))
         return fail(CTOX_ERR_SHAPE, "null argument");
@@ -1430,7 +1430,10 @@ ctox_status gdn_fused_impl(ctox_hip_backend *b, const float *d_proj, size_t proj
         return fail(CTOX_ERR_SHAPE, "fused gated delta shapes");
     // The conv windows written (every snapshot, or the final one) never
     // overlap the ones read: other workgroups still read them.
-    const size_t cw = channels * kernel, sw = heads * key_dim * value_dim;
+    const size_t cw = channels * kernel;
+    const size_t sw = blocked ? heads * ((value_dim + 15) / 16) * 2048 : heads * key_dim * value_dim;
+    if (blocked && (((uintptr_t)d_state_in | (uintptr_t)d_state_out) % 16 || (snap_stride % 4)))
+        return fail(CTOX_ERR_SHAPE, "blocked gated delta state needs 16-byte alignment");
     const size_t nsnap = snap_stride ? tokens : 1;
     if ((snap_stride && (snap_stride < sw || conv_snap_stride < cw)) || (!snap_stride && conv_snap_stride))
         return fail(CTOX_ERR_SHAPE, "fused gated delta snapshot strides");
@@ -1463,6 +1466,7 @@ ctox_status gdn_fused_impl(ctox_hip_backend *b, const float *d_proj, size_t proj
     a.a_off = (uint32_t)a_off;
     a.b_off = (uint32_t)b_off;
     a.gates_given = gates_given ? 1u : 0u;
+    a.state_blocked = blocked ? 1u : 0u;
     const size_t slices = (value_dim + 15) / 16;
     return launch(b->gdn_fused, dim3((unsigned)(heads * slices)), dim3(256), pick_stream(b, stream), a,
                   "ctox_gdn_fused_gfx950");
@@ -1477,7 +1481,7 @@ extern "C" ctox_status ctox_hip_gdn_fused_device(ctox_hip_backend *b, const floa
                                                  size_t heads, size_t key_heads, size_t key_dim, size_t value_dim,
                                                  float *d_out, void *stream) {
     return gdn_fused_impl(b, d_proj, proj_stride, a_off, b_off, d_conv_w, d_conv_in, d_conv_out, kernel, d_a_log,
-                          d_dt_bias, d_log_decay, d_beta, gates_given, d_state, d_state, 0, 0, tokens, heads,
+                          d_dt_bias, d_log_decay, d_beta, gates_given, d_state, d_state, 0, 0, 0, tokens, heads,
                           key_heads, key_dim, value_dim, d_out, stream);
 }
 
@@ -1487,13 +1491,13 @@ extern "C" ctox_status ctox_hip_gdn_fused_snap_device(ctox_hip_backend *b, const
                                                       size_t conv_snap_stride, size_t kernel, const float *d_a_log,
                                                       const float *d_dt_bias, float *d_log_decay, float *d_beta,
                                                       const float *d_state_in, float *d_state_out,
-                                                      size_t snap_stride, size_t tokens, size_t heads,
+                                                      size_t snap_stride, int blocked, size_t tokens, size_t heads,
                                                       size_t key_heads, size_t key_dim, size_t value_dim,
                                                       float *d_out, void *stream) {
     if (snap_stride == 0) return fail(CTOX_ERR_SHAPE, "snapshot stride must be non-zero");
     return gdn_fused_impl(b, d_proj, proj_stride, a_off, b_off, d_conv_w, d_conv_in, d_conv_out, kernel, d_a_log,
                           d_dt_bias, d_log_decay, d_beta, 0, d_state_in, d_state_out, snap_stride, conv_snap_stride,
-                          tokens, heads, key_heads, key_dim, value_dim, d_out, stream);
+                          blocked, tokens, heads, key_heads, key_dim, value_dim, d_out, stream);
 }
 
 // ======================================================================
@@ -1638,11 +1642,12 @@ extern "C" ctox_status ctox_hip_mtp_accept_device(ctox_hip_backend *b, const flo
 }
 
 extern "C" ctox_status ctox_hip_check_finite_device(ctox_hip_backend *b, const float *d_x, size_t n,
-                                                    uint32_t *d_flag, void *stream) {
-    if (!b || !d_x || !d_flag) return fail(CTOX_ERR_SHAPE, "null argument");
+                                                    uint32_t *d_flags, size_t parts, void *stream) {
+    if (!b || !d_x || !d_flags) return fail(CTOX_ERR_SHAPE, "null argument");
     if ((uintptr_t)d_x % 16) return fail(CTOX_ERR_SHAPE, "finite check needs a 16-byte aligned buffer");
-    FiniteArgs a{d_x, d_flag, (uint64_t)n};
-    return launch(b->finite, dim3(1), dim3(1024), pick_stream(b, stream), a, "ctox_finite_check_gfx950");
+    if (parts == 0 || parts > 1024) return fail(CTOX_ERR_SHAPE, "finite check parts outside 1..1024");
+    FiniteArgs a{d_x, d_flags, (uint64_t)n};
+    return launch(b->finite, dim3((unsigned)parts), dim3(256), pick_stream(b, stream), a, "ctox_finite_check_gfx950");
 }
 
 extern "C" ctox_status ctox_hip_gather_rows_device(ctox_hip_backend *b, const void *d_src, size_t src_rows,

@@ -445,7 +445,7 @@ ctox_status gdn_core(ctox_hip_engine *e, GdnLayer &g, const float *proj, uint32_
                                           conv_cur(e) + g.conv_off, e->conv_bank + other * e->conv_floats + g.conv_off,
                                           e->conv_floats, e->c.linear_conv_kernel_dim, g.a_log, g.dt_bias, e->ld,
                                           e->beta, state_cur(e) + g.state_off,
-                                          e->gdn_bank + other * e->gdn_floats + g.state_off, e->gdn_floats, R, Hv, Hk,
+                                          e->gdn_bank + other * e->gdn_floats + g.state_off, e->gdn_floats, 1, R, Hv, Hk,
                                           e->c.linear_key_head_dim, e->c.linear_value_head_dim, e->core, e->s);
 }
 
@@ -520,9 +520,10 @@ ctox_status demote_all(ctox_hip_engine *e) {
     return CTOX_OK;
 }
 
-// Queues the finite check of `n` logits into flag word `slot`.
-ctox_status check_logits(ctox_hip_engine *e, const float *x, size_t n, uint32_t slot) {
-    return ctox_hip_check_finite_device(e->b, x, n, e->d_flags + slot, e->s);
+// Queues the finite check of `n` logits into flag words [0, kFlagParts).
+constexpr uint32_t kFlagParts = 64;
+ctox_status check_logits(ctox_hip_engine *e, const float *x, size_t n) {
+    return ctox_hip_check_finite_device(e->b, x, n, e->d_flags, kFlagParts, e->s);
 }
 
 // After the step's synchronization: fail closed on a flagged buffer
@@ -604,7 +605,9 @@ extern "C" ctox_status ctox_hip_engine_create(ctox_hip_backend *b, const ctox_en
     uint32_t n_gdn = 0;
     for (uint32_t l = 0; l < c.num_hidden_layers; l++) n_gdn += ((l + 1) % c.full_attention_interval) != 0;
     const uint32_t Hv = c.linear_num_value_heads;
-    e->gdn_floats = (size_t)n_gdn * Hv * c.linear_key_head_dim * c.linear_value_head_dim;
+    // States in the fused kernel's blocked layout: 128 x ceil16(value_dim) floats per head.
+    const size_t head_floats = (size_t)(c.linear_value_head_dim + 15) / 16 * 2048;
+    e->gdn_floats = (size_t)n_gdn * Hv * head_floats;
     e->conv_floats = (size_t)n_gdn * e->C * c.linear_conv_kernel_dim;
     if ((st = dalloc_t(e, &e->gdn_bank, 2 * (size_t)e->R * e->gdn_floats)) ||
         (st = dalloc_t(e, &e->conv_bank, 2 * (size_t)e->R * e->conv_floats)))
@@ -629,7 +632,7 @@ extern "C" ctox_status ctox_hip_engine_create(ctox_hip_backend *b, const ctox_en
             if ((st = dalloc_t(e, &g.dt_bias, Hv)) || (st = fill(e, g.dt_bias, Hv, 4, sd++, -1.0f, 1.0f))) return cleanup(st);
             if ((st = make_vec(e, &g.gnorm, c.linear_value_head_dim, sd, 1.0f, 0.1f))) return cleanup(st);
             if ((st = make_mat(e, g.out, CTOX_DTYPE_Q4B64, e->H, e->Vw, sd))) return cleanup(st);
-            g.state_off = (size_t)gi * Hv * c.linear_key_head_dim * c.linear_value_head_dim;
+            g.state_off = (size_t)gi * Hv * head_floats;
             g.conv_off = (size_t)gi * e->C * c.linear_conv_kernel_dim;
             gi++;
         }
@@ -708,11 +711,11 @@ extern "C" ctox_status ctox_hip_engine_decode(ctox_hip_engine *e, uint32_t token
     e->have_prev = true;
     e->position++;
     TRY(demote_all(e));
-    TRY(check_logits(e, e->logits, e->V, 0));
-    TRY(read_flags(e, 1));
+    TRY(check_logits(e, e->logits, e->V));
+    TRY(read_flags(e, kFlagParts));
     if (d_logits) *d_logits = e->logits;
     TRY(sync(e));
-    return flags_ok(e, 1);
+    return flags_ok(e, kFlagParts);
 }
 
 // One speculative step: k drafts sampled at `temperature`, one batched target
@@ -744,8 +747,6 @@ extern "C" ctox_status ctox_hip_engine_mtp_step(ctox_hip_engine *e, uint32_t tok
     }
     // Verify [token, d1..dk] in one pass; every row's GatedDeltaNet state is kept.
     TRY(target_forward(e, e->d_drafts, R, true));
-    TRY(check_logits(e, e->logits, (size_t)R * e->V, 0));
-    TRY(check_logits(e, e->draft_logits, (size_t)k * dn, 1));
     TRY(ctox_hip_mtp_accept_restricted_device(e->b, e->draft_logits, dn, e->draft_n ? e->d_draft_inv : nullptr,
                                               e->logits, e->logits + (size_t)k * e->V, nullptr, e->d_drafts + 1, k,
                                               e->V, temperature, e->d_rng, e->d_result, e->s));
@@ -753,9 +754,10 @@ extern "C" ctox_status ctox_hip_engine_mtp_step(ctox_hip_engine *e, uint32_t tok
     if (hipMemcpyAsync(host, e->d_result, 8, hipMemcpyDeviceToHost, e->s) != hipSuccess ||
         hipMemcpyAsync(host + 2, e->d_drafts, 4 * R, hipMemcpyDeviceToHost, e->s) != hipSuccess)
         return efail(CTOX_ERR_INVALID_STATE, "result read failed");
-    TRY(read_flags(e, 2));
     TRY(sync(e));
-    TRY(flags_ok(e, 2));  // nothing is committed from a step with non-finite logits
+    // The acceptance reports non-finite draft or target logits as 0xfffffffe;
+    // nothing is committed from such a step.
+    if (host[0] == 0xfffffffeu) return efail(CTOX_ERR_INVALID_STATE, "non-finite logits in the speculative step");
     const uint32_t next = host[0], n = host[1];
     if (n > k || next >= e->V) return efail(CTOX_ERR_INVALID_STATE, "acceptance produced an invalid result");
     // Commit n + 1 target tokens: the state after row n, the caches truncated.
@@ -823,7 +825,7 @@ extern "C" ctox_status ctox_hip_engine_fill_context(ctox_hip_engine *e, uint32_t
 }
 
 // Device views for tests and tools. which: 0 logits [R][V], 1 final hidden
-// [R][H], 2 previous target hidden [H], 3 GatedDeltaNet states, 4 conv states,
+// [R][H], 2 previous target hidden [H], 3 GatedDeltaNet states (blocked layout of ctox_hip_gdn_fused_snap_device), 4 conv states,
 // 5 draft logits [k][V].
 extern "C" ctox_status ctox_hip_engine_buffer(ctox_hip_engine *e, uint32_t which, void **ptr, size_t *bytes) {
     if (!e || !ptr || !bytes) return efail(CTOX_ERR_SHAPE, "null argument");

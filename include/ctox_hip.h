@@ -360,15 +360,21 @@ ctox_status ctox_hip_gdn_fused_device(ctox_hip_backend *backend, const float *d_
  * t is written at d_state_out + t * snap_stride (floats, at least
  * heads * key_dim * value_dim), the conv windows after row t at
  * d_conv_out + t * conv_snap_stride; no snapshot may overlap d_conv_in.
- * d_state_out may equal d_state_in. Gates are computed (never given). */
+ * d_state_out may equal d_state_in. Gates are computed (never given).
+ * blocked = 0: states [heads][key_dim][value_dim]; blocked = 1: the
+ * engine's layout, per head and 16-column slice of the value dimension
+ * 256 runs of 8 floats: element (h, i, j) at
+ * ((h * S + j / 16) * 256 + (i % 16) * 16 + j % 16) * 8 + i / 16,
+ * S = ceil(value_dim / 16), heads * S * 2048 floats per state, 16-byte
+ * aligned (a wave moves 2 KiB per access instead of 64-byte pieces). */
 ctox_status ctox_hip_gdn_fused_snap_device(ctox_hip_backend *backend, const float *d_proj, size_t proj_stride,
                                            size_t a_off, size_t b_off, const float *d_conv_w,
                                            const float *d_conv_in, float *d_conv_out, size_t conv_snap_stride,
                                            size_t kernel, const float *d_a_log, const float *d_dt_bias,
                                            float *d_log_decay, float *d_beta, const float *d_state_in,
-                                           float *d_state_out, size_t snap_stride, size_t tokens, size_t heads,
-                                           size_t key_heads, size_t key_dim, size_t value_dim, float *d_out,
-                                           void *stream);
+                                           float *d_state_out, size_t snap_stride, int blocked, size_t tokens,
+                                           size_t heads, size_t key_heads, size_t key_dim, size_t value_dim,
+                                           float *d_out, void *stream);
 
 /* ---- decode-step glue and token selection (device buffers) ---- */
 /* GatedDeltaNet gates, Q/src/decoder.rs:881-902 (softplus :29-35):
@@ -409,7 +415,8 @@ ctox_status ctox_hip_mtp_accept_device(ctox_hip_backend *backend, const float *d
  * tokens outside the draft vocabulary (q = 0 there). d_bonus_ids, when set,
  * maps a bonus-row index to its token: drafts = 0 with the bonus row a
  * restricted draft row of `vocab` = draft-vocabulary scores samples a draft
- * token. d_draft_inv may be NULL when draft_vocab == vocab. */
+ * token. d_draft_inv may be NULL when draft_vocab == vocab. A non-finite
+ * logit in any row fails closed: d_out[0] = 0xfffffffe, no draw is consumed. */
 ctox_status ctox_hip_mtp_accept_restricted_device(ctox_hip_backend *backend, const float *d_draft,
                                                   size_t draft_vocab, const uint32_t *d_draft_inv,
                                                   const float *d_target, const float *d_bonus,
@@ -417,9 +424,11 @@ ctox_status ctox_hip_mtp_accept_restricted_device(ctox_hip_backend *backend, con
                                                   size_t drafts, size_t vocab, float temperature, uint64_t *d_rng,
                                                   uint32_t *d_out, void *stream);
 /* Fail-closed check of a logits buffer (Q/src/backend/cuda_runtime.rs:10627-10632):
- * *d_flag = 1 if any of the n values is not finite, else 0. d_x 16-byte aligned. */
-ctox_status ctox_hip_check_finite_device(ctox_hip_backend *backend, const float *d_x, size_t n, uint32_t *d_flag,
-                                         void *stream);
+ * the n values are split into `parts` (1..1024) contiguous ranges and
+ * d_flags[p] = 1 if range p holds a non-finite value, else 0 (every flag is
+ * written). d_x 16-byte aligned. */
+ctox_status ctox_hip_check_finite_device(ctox_hip_backend *backend, const float *d_x, size_t n, uint32_t *d_flags,
+                                         size_t parts, void *stream);
 /* dst row r = src row ids[r] (rows of row_bytes bytes; ids host values, each
  * below src_rows). Builds the restricted draft head's compact copy of the LM
  * head rows once at load (the CUDA runtime gathers them per launch instead,
@@ -620,7 +629,8 @@ ctox_status ctox_hip_engine_mtp_step(ctox_hip_engine *engine, uint32_t token, fl
 /* Fill every paged cache with `tokens` random K/V rows (an empty engine only). */
 ctox_status ctox_hip_engine_fill_context(ctox_hip_engine *engine, uint32_t tokens, uint64_t seed);
 /* which: 0 logits [R][V], 1 final hiddens [R][H], 2 previous target hidden,
- * 3 GatedDeltaNet states, 4 conv states, 5 draft logits [k][V]. */
+ * 3 GatedDeltaNet states (the blocked layout of
+ * ctox_hip_gdn_fused_snap_device), 4 conv states, 5 draft logits [k][V]. */
 ctox_status ctox_hip_engine_buffer(ctox_hip_engine *engine, uint32_t which, void **d_ptr, size_t *bytes);
 uint32_t ctox_hip_engine_position(const ctox_hip_engine *engine);
 /* Binds the release's MTP draft vocabulary (ModelExecutor::load's

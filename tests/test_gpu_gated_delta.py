@@ -273,12 +273,12 @@ def test_fused_snapshots_equal_sequential_steps(hip):
     out = torch.empty(tokens, heads, dv, device="cuda")
     st = lib.ctox_hip_gdn_fused_snap_device(hip.handle, p(proj), stride, a_off, b_off, p(conv_w), p(conv_in),
                                             p(csnaps), csz, K, p(a_log), p(dt_bias), p(ld), p(be), p(st_in), p(snaps),
-                                            ssz, tokens, heads, key_heads, dk, dv, p(out), None)
+                                            ssz, 0, tokens, heads, key_heads, dk, dv, p(out), None)
     assert st == 0, lib.ctox_hip_last_error()
     # aliasing conv windows are refused
     assert lib.ctox_hip_gdn_fused_snap_device(hip.handle, p(proj), stride, a_off, b_off, p(conv_w), p(conv_in),
                                               p(conv_in) - 4 * csz, csz, K, p(a_log), p(dt_bias), p(ld), p(be),
-                                              p(st_in), p(snaps), ssz, tokens, heads, key_heads, dk, dv, p(out),
+                                              p(st_in), p(snaps), ssz, 0, tokens, heads, key_heads, dk, dv, p(out),
                                               None) != 0
     torch.cuda.synchronize()
     assert np.array_equal(st_in.cpu().numpy(), state0)  # input untouched (other output buffer)
@@ -294,3 +294,26 @@ def test_fused_snapshots_equal_sequential_steps(hip):
         assert np.array_equal(csnaps[t].cpu().numpy(), cout.cpu().numpy().reshape(-1)), t
         if t == tokens - 1:
             assert np.array_equal(out.cpu().numpy(), out_b.cpu().numpy())
+    # The blocked layout (the engine's): the same states, permuted.
+    sl = (dv + 15) // 16
+
+    def to_blocked(x):  # [heads][dk][dv] -> [heads][slice][ig*16 + jj][r], i = ig + 16 r, j = 16 slice + jj
+        b = np.zeros((heads, sl, 16, 16, 8), np.float32)
+        xx = x.reshape(heads, 8, 16, sl, 16)  # [h][r][ig][slice][jj]
+        b[:] = xx.transpose(0, 3, 2, 4, 1)
+        return b.reshape(-1)
+
+    bsz = heads * sl * 2048
+    st_blk = dev(to_blocked(state0))
+    bsnaps = torch.full((tokens, bsz), float("nan"), device="cuda")
+    csn2 = torch.full((tokens, csz), float("nan"), device="cuda")
+    out2 = torch.empty(tokens, heads, dv, device="cuda")
+    st = lib.ctox_hip_gdn_fused_snap_device(hip.handle, p(proj), stride, a_off, b_off, p(conv_w), p(conv_in),
+                                            p(csn2), csz, K, p(a_log), p(dt_bias), p(ld), p(be), p(st_blk),
+                                            p(bsnaps), bsz, 1, tokens, heads, key_heads, dk, dv, p(out2), None)
+    assert st == 0, lib.ctox_hip_last_error()
+    torch.cuda.synchronize()
+    for t in range(tokens):
+        assert np.array_equal(bsnaps[t].cpu().numpy(), to_blocked(snaps[t].cpu().numpy())), t
+    assert np.array_equal(out2.cpu().numpy(), out.cpu().numpy())
+    assert np.array_equal(csn2.cpu().numpy(), csnaps.cpu().numpy())
