@@ -178,9 +178,15 @@ struct TileMatvecArgs {
     uint32_t head_dim;
     float eps;
     // Small-M kernels (ctox_q*_mv_tilem*): activation rows (2..8, staged in
-    // xa/xc by a prep kernel) and the output row stride.
+    // xa/xc by a prep kernel, or built in the kernel by ctox_q*_mv_tilemx*)
+    // and the output row stride.
     uint32_t batch;
     uint32_t out_stride;
+    // tilemx: floats between rows of `input` and of xb / delta. Rows of
+    // x_out / norm_out are `blocks * 64` apart, sq_in rows sq_n apart, and a
+    // producer's res_h / res_sq rows `rows` / `tiles` apart.
+    uint32_t a_stride;
+    uint32_t b_stride;
 };
 
 struct RecoveredRowArgs {

@@ -138,10 +138,18 @@ __device__ __forceinline__ float tl_silu(float v) { return v / (1.0f + expf(-v))
 // the prep kernel's xa order); lane (g, j) receives the constants of
 // block g. With `keep` the residual and normalized values of the lane's
 // columns are stored (residual norm, segment-0 workgroup).
+// `bstride`: bytes between the group's blocks in `frag` (192: the blocks of
+// one row; M * 192: the [block][row] order of the small-M kernels); x_out /
+// norm_out: this row's outputs of the residual norm. Columns past the
+// matrix are built as zeros (their weights are zero padding, and a zero X
+// keeps the block's offset term zero).
 template <int DT>
 __device__ __forceinline__ float4 frag_group_build(const TileMatvecArgs &a, uint32_t grp, uint32_t lane,
-                                                   const GroupIn &in, float inv, bool keep, int8_t *frag) {
+                                                   const GroupIn &in, float inv, bool keep, int8_t *frag,
+                                                   uint32_t bstride = 192, float *x_out = nullptr,
+                                                   float *norm_out = nullptr) {
     const uint32_t g = lane >> 4, m = lane & 15, xm = a.xmode;
+    const bool in_matrix = (4 * grp + g) * CTOX_BLOCK_LEN + 4 * m < a.blocks * CTOX_BLOCK_LEN;
     float xa[4], yb[4], wv[4], v[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -157,10 +165,10 @@ __device__ __forceinline__ float4 frag_group_build(const TileMatvecArgs &a, uint
         float h[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) h[i] = xa[i] + yb[i];
-        if (keep && inside && a.x_out) *(float4 *)(a.x_out + col) = make_float4(h[0], h[1], h[2], h[3]);
+        if (keep && inside && x_out) *(float4 *)(x_out + col) = make_float4(h[0], h[1], h[2], h[3]);
 #pragma unroll
         for (int i = 0; i < 4; i++) v[i] = h[i] * inv * (1.0f + wv[i]);
-        if (keep && inside && a.norm_out) *(float4 *)(a.norm_out + col) = make_float4(v[0], v[1], v[2], v[3]);
+        if (keep && inside && norm_out) *(float4 *)(norm_out + col) = make_float4(v[0], v[1], v[2], v[3]);
     } else if (xm == 2) {
 #pragma unroll
         for (int i = 0; i < 4; i++) v[i] = tl_silu(xa[i]) * yb[i];
@@ -190,6 +198,7 @@ __device__ __forceinline__ float4 frag_group_build(const TileMatvecArgs &a, uint
 #pragma unroll
         for (int i = 0; i < 4; i++) v[i] *= __int_as_float(in.s[i]);
     }
+    if (!in_matrix) v[0] = v[1] = v[2] = v[3] = 0.0f;
     // A non-finite value anywhere in the block makes its quantum NaN (the
     // lane sum of a finite row can only overflow for |x'| near 2^128).
     const bool bad = !__builtin_isfinite((v[0] + v[1]) + (v[2] + v[3]));
@@ -218,7 +227,7 @@ __device__ __forceinline__ float4 frag_group_build(const TileMatvecArgs &a, uint
     // Balanced limbs X = X0 + 256 X1 + 65536 X2 (X0, X1 in [-128, 127]):
     // X0 is byte 0 of X, X1 byte 1 of X + 0x80, X2 byte 2 of X + 0x8080.
     // Element 4m + i of block g goes to quarter m / 4, element 4 (m % 4) + i.
-    int8_t *blkp = frag + g * 192 + (m >> 2) * 16;
+    int8_t *blkp = frag + g * bstride + (m >> 2) * 16;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int pos = frag_pos(DT, (int)(4 * (m & 3) + i));
@@ -391,7 +400,8 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
             inv = 1.0f / sqrtf(((wss[0] + wss[1]) + (wss[2] + wss[3])) / (float)(a.blocks * CTOX_BLOCK_LEN) + a.eps);
         }
         const bool keep = ((blockIdx.x * (blockDim.x >> 6)) % a.segs) == 0;  // segment 0 of the chunk
-        const float4 k = frag_group_build<DT>(a, c * 4 + wg_wave, lane, gin, inv, keep, xs + wg_wave * 768);
+        const float4 k = frag_group_build<DT>(a, c * 4 + wg_wave, lane, gin, inv, keep, xs + wg_wave * 768, 192,
+                                              a.x_out, a.norm_out);
         if (j == 0) kqs[4 * wg_wave + g] = k;
         lds_barrier();  // orders LDS only: the weight loads stay in flight
         if (t0 >= a.tiles) return;
@@ -526,6 +536,16 @@ __device__ __forceinline__ void transpose4(uint32_t &r0, uint32_t &r1, uint32_t 
     r3 = s23[1];
 }
 
+// Per 16-row tile and row tok: sum over the tile's rows of (res_h + y)^2.
+__device__ __forceinline__ void residual_tile_sum_m(const TileMatvecArgs &a, uint32_t tok, uint32_t tile,
+                                                    uint32_t row, bool mine, float y, uint32_t j) {
+    const float h = mine && row < a.rows ? a.res_h[(size_t)tok * a.rows + row] + y : 0.0f;
+    const float s = row16_reduce(h * h, [](float x, float z) { return x + z; });
+    if (mine && j == 0) a.res_sq[(size_t)tok * a.tiles + tile] = s;
+}
+
+// MR = M, the row count, is a compile-time constant: every LDS address of
+// the MFMA loop is a per-lane base plus an immediate offset.
 template <int DT, int U, int TG>
 __device__ __forceinline__ void tile_matvec_m(const TileMatvecArgs &a) {
     using C = TlCfg<DT>;
@@ -637,9 +657,11 @@ __device__ __forceinline__ void tile_matvec_m(const TileMatvecArgs &a) {
         for (int k = 0; k < U; k++)
 #pragma unroll
             for (int tg = 0; tg < TG; tg++) {
-                const uint32_t tok = 4 * tg + g, row = (t0 + k) * CTOX_TILE_ROWS + j;
-                if ((uint32_t)k < n && tok < M && row < a.rows)
-                    a.output[(size_t)tok * a.out_stride + row] = tile_epilogue(acc[k][tg] / C::DEN, row, a);
+                const uint32_t tok = 4 * tg + g, tile = t0 + k, row = tile * CTOX_TILE_ROWS + j;
+                const bool want = (uint32_t)k < n && tok < M;
+                const float y = want && row < a.rows ? tile_epilogue(acc[k][tg] / C::DEN, row, a) : 0.0f;
+                if (want && row < a.rows) a.output[(size_t)tok * a.out_stride + row] = y;
+                if (a.res_sq) residual_tile_sum_m(a, min(tok, M - 1), tile, row, want, y, j);
             }
         return;
     }
@@ -659,10 +681,12 @@ __device__ __forceinline__ void tile_matvec_m(const TileMatvecArgs &a) {
     for (int k = 0; k < U; k++)
 #pragma unroll
         for (int tg = 0; tg < TG; tg++) {
-            const uint32_t tok = 4 * tg + g, row = (t0 + k) * CTOX_TILE_ROWS + j;
+            const uint32_t tok = 4 * tg + g, tile = t0 + k, row = tile * CTOX_TILE_ROWS + j;
             const bool want = (uint32_t)k < n && tok < M;
             const float sum = combine_poll(&a.partial[tok * tstride + row], cstride, a.chunks - 1, a.seq, acc[k][tg], want);
-            if (want && row < a.rows) a.output[(size_t)tok * a.out_stride + row] = tile_epilogue(sum / C::DEN, row, a);
+            const float y = want && row < a.rows ? tile_epilogue(sum / C::DEN, row, a) : 0.0f;
+            if (want && row < a.rows) a.output[(size_t)tok * a.out_stride + row] = y;
+            if (a.res_sq) residual_tile_sum_m(a, min(tok, M - 1), tile, row, want, y, j);
         }
 }
 
@@ -672,6 +696,227 @@ CTOX_TILE_M_KERNEL(ctox_q2_mv_tilem1_gfx950, 0, 2, 1)
 CTOX_TILE_M_KERNEL(ctox_q2_mv_tilem2_gfx950, 0, 2, 2)
 CTOX_TILE_M_KERNEL(ctox_q4_mv_tilem1_gfx950, 1, 2, 1)
 CTOX_TILE_M_KERNEL(ctox_q4_mv_tilem2_gfx950, 1, 2, 2)
+
+// ---------------------------------------------------------------------------
+// Small-M tiled matvec with the activation rows built in the kernel
+// (ctox_q{2,4}_mv_tilemx{2,3,4,5}_gfx950, 2..5 rows): the MTP verify
+// projections without a staging launch. The MFMA scheme, chunks and combine
+// are those of tile_matvec_m; what differs is where the fragments come from:
+//  * each wave copies its group's inputs of every row (the producer rows
+//    the transform reads, 1 KiB per row and operand) straight into LDS with
+//    buffer loads that write LDS (no registers held while the weight loads
+//    are in flight), then issues its weight loads;
+//  * after an explicit wait that leaves the weight loads outstanding, it
+//    builds its group's fragments of every row (frag_group_build, the
+//    batch-1 arithmetic) into the workgroup's [block][row] fragment area;
+//  * the residual norm reads the producer's per-tile sums of squares of
+//    every row (wave 0 copies them into LDS; one LDS barrier shares them).
+// A producer with a residual in view writes those sums for every row.
+// Waits until at most n vector-memory operations of this wave are
+// outstanding (gfx9 s_waitcnt: vmcnt in bits 3:0 and 15:14, expcnt and
+// lgkmcnt left at their maxima).
+#define CTOX_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, void *lds, uint32_t voff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, 0, 0, 0);
+}
+
+template <int DT, int MR>
+__device__ __forceinline__ void tile_matvec_mx(const TileMatvecArgs &a) {
+    using C = TlCfg<DT>;
+    constexpr uint32_t U = 2, TG = (MR + 3) / 4, INB = 2048;
+    constexpr uint32_t WLOADS = U * (C::LPU + 4);  // weight loads issued after the input copies
+    __shared__ __align__(16) uint8_t ins[4 * MR * INB];
+    __shared__ __align__(16) int8_t xas[CTOX_TILE_BLOCKS * MR * 192];
+    __shared__ float4 kqs[CTOX_TILE_BLOCKS * MR];
+    __shared__ __align__(16) float sqs[MR * 512];
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t v = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + w);
+    const uint32_t c = v / a.segs, s = v - c * a.segs;
+    constexpr uint32_t M = MR;
+    const uint32_t t0 = s * U;
+    if (c >= a.chunks) return;  // uniform over the workgroup (segs is a multiple of 4)
+    const uint32_t n = t0 < a.tiles ? min(U, a.tiles - t0) : 0u;
+    const uint8_t *base = a.weights + ((size_t)c * a.tiles + min(t0, a.tiles - 1)) * C::UB;
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)(n * C::UB), 0x00020000);
+    const uint32_t g = lane >> 4, j = lane & 15, limb = j & 3;
+    const uint32_t cols = a.blocks * CTOX_BLOCK_LEN, xm = a.xmode, dh = a.head_dim ? a.head_dim : 1u;
+    const uint32_t grp = c * 4 + w, col = grp * 256 + 4 * lane;
+
+    // Input copies (rows t < M): operand a at [0, 1 KiB), b at [1 KiB, 2 KiB)
+    // of the wave's row area; an absent operand reads zeros.
+    {
+        const uint32_t aext = xm == 2 ? a.off + cols : cols;
+        const __amdgpu_buffer_rsrc_t ar = f32_rsrc(a.input, (M - 1) * a.a_stride + aext);
+        const void *bp = xm == 1 ? (const void *)a.delta : (xm == 2 ? (const void *)a.input : (const void *)a.xb);
+        const uint32_t bext = xm == 1 || xm == 3 ? cols : (xm == 2 ? a.off + cols : (xm == 4 ? 2 * cols : 0u));
+        const uint32_t bstr = xm == 2 ? a.a_stride : a.b_stride;
+        const __amdgpu_buffer_rsrc_t br = f32_rsrc(xm == 0 ? nullptr : bp, bext ? (M - 1) * bstr + bext : 0u);
+        const uint32_t bo = xm == 2 ? a.off + col : (xm == 4 ? (col / dh) * 2 * dh + dh + col % dh : col);
+        for (uint32_t t = 0; t < M; t++) {
+            uint8_t *dst = ins + (w * MR + t) * INB;
+            lds_dma16(ar, dst, (t * a.a_stride + col) * 4);
+            lds_dma16(br, dst + 1024, (t * bstr + bo) * 4);
+        }
+        if (xm == 1 && w == 0) {
+            const __amdgpu_buffer_rsrc_t sr = f32_rsrc(a.sq_in, M * a.sq_n);
+            for (uint32_t t = 0; t < M; t++) {
+                lds_dma16(sr, sqs + t * 512, (t * a.sq_n + 4 * lane) * 4);
+                lds_dma16(sr, sqs + t * 512 + 256, (t * a.sq_n + 256 + 4 * lane) * 4);
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // Row-independent operands: the norm weight and s_in of the lane's columns.
+    GroupIn gin;
+    {
+        const uint32_t sbytes = a.s_in_kind == CTOX_KSCALE_F32 ? 4u : 2u;
+        const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)a.s_in, (short)0, a.s_in_kind == CTOX_KSCALE_NONE ? 0 : (int)(cols * sbytes), 0x00020000);
+        const __amdgpu_buffer_rsrc_t wr2 = f32_rsrc(xm == 1 || xm == 3 ? a.xw : nullptr, xm == 1 ? cols : dh);
+        gin.w = __builtin_amdgcn_raw_buffer_load_b128(wr2, (xm == 3 ? col % dh : col) * 4, 0, 0);
+        gin.s = __builtin_amdgcn_raw_buffer_load_b128(sr, col * sbytes, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    TileUnit<DT> u[U];
+    v2u sc[U][4];
+#pragma unroll
+    for (int k = 0; k < (int)U; k++) {
+#pragma unroll
+        for (int i = 0; i < (int)C::LPU; i++)
+            u[k].w[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, lane * 16, k * C::UB + i * 1024, CTOX_LOAD_NT);
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            sc[k][q] = __builtin_amdgcn_raw_buffer_load_b64(wr, C::CB + (q * 16 + j) * 8, k * C::UB, CTOX_LOAD_NT);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    CTOX_WAIT_VMCNT(WLOADS);  // the input copies and the two operand loads have landed
+    __builtin_amdgcn_sched_barrier(0);
+    if (xm == 1) lds_barrier();  // wave 0's copy of the sums is visible
+    const bool keep = ((blockIdx.x * (blockDim.x >> 6)) % a.segs) == 0;  // segment 0 of the chunk
+    // One row at a time (not unrolled: the build's temporaries are live
+    // beside the weight loads in flight).
+#pragma unroll 1
+    for (uint32_t t = 0; t < M; t++) {
+        float inv = 0.0f;
+        if (xm == 1) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const uint32_t idx = lane + 64 * k;
+                ss += idx < a.sq_n ? sqs[t * 512 + idx] : 0.0f;
+            }
+            ss = row16_reduce(ss, [](float x, float y) { return x + y; });
+            ss += __shfl_xor(ss, 16);
+            ss += __shfl_xor(ss, 32);
+            inv = 1.0f / sqrtf(ss / (float)cols + a.eps);
+        }
+        const uint8_t *src = ins + (w * MR + t) * INB;
+        gin.a = *(const v4i *)(src + lane * 16);
+        gin.b = *(const v4i *)(src + 1024 + lane * 16);
+        const float4 k = frag_group_build<DT>(a, grp, lane, gin, inv, keep, xas + ((4 * w) * M + t) * 192, M * 192,
+                                              a.x_out ? a.x_out + (size_t)t * cols : nullptr,
+                                              a.norm_out ? a.norm_out + (size_t)t * cols : nullptr);
+        if (j == 0) kqs[(4 * w + g) * M + t] = k;
+    }
+    lds_barrier();  // fragments and constants of every group and row
+    if (t0 >= a.tiles) return;
+
+    // Per lane and token group: the A fragment base (row 4 tg + j / 4, limb
+    // j % 4, quarter g; lanes outside the rows or on limb 3 read a valid row
+    // whose C row nothing uses) and the epilogue constants' row.
+    const int8_t *abase[TG];
+    const float4 *kbase[TG];
+#pragma unroll
+    for (int tg = 0; tg < (int)TG; tg++) {
+        const uint32_t tok = min(4 * tg + (j >> 2), M - 1);
+        abase[tg] = xas + tok * 192 + min(limb, 2u) * 64 + g * 16;
+        kbase[tg] = kqs + min(4 * tg + g, M - 1);
+    }
+    float acc[U][TG];
+#pragma unroll
+    for (int k = 0; k < (int)U; k++) {
+#pragma unroll
+        for (int tg = 0; tg < (int)TG; tg++) acc[k][tg] = 0.0f;
+#pragma unroll
+        for (int G = 0; G < 4; G++) {
+            uint32_t e[4], o[4];
+            if (DT) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const v4i W = u[k].w[2 * G + (q >> 1)];
+                    e[q] = (uint32_t)W[2 * (q & 1)];
+                    o[q] = (uint32_t)W[2 * (q & 1) + 1];
+                }
+                transpose4(e[0], e[1], e[2], e[3]);
+                transpose4(o[0], o[1], o[2], o[3]);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; q++) e[q] = (uint32_t)u[k].w[G][q];
+                transpose4(e[0], e[1], e[2], e[3]);
+            }
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const v4i bf = DT ? unpack_quarter<DT>(e[b], o[b]) : unpack_quarter<DT>(e[b], 0);
+                const uint32_t sw = sc[k][b][G >> 1];
+                const float scale = half_bits_to_float((G & 1) ? (sw >> 16) : (sw & 0xffffu));
+#pragma unroll
+                for (int tg = 0; tg < (int)TG; tg++) {
+                    const v4i af = *(const v4i *)(abase[tg] + (4 * G + b) * M * 192);
+                    const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf, (v4i){0, 0, 0, 0}, 0, 0, 0);
+                    const float4 kq = kbase[tg][(4 * G + b) * M];
+                    float f;
+                    if (DT) {
+                        f = fmaf((float)cc[0], kq.x, kq.w);
+                        f = fmaf((float)cc[1], kq.y, f);
+                        f = fmaf((float)cc[2], kq.z, f);
+                    } else {
+                        f = fmaf((float)(cc[0] + (cc[1] << 8) + (cc[2] << 16)), kq.x, kq.w);
+                    }
+                    acc[k][tg] = fmaf(f, scale, acc[k][tg]);
+                }
+            }
+        }
+    }
+    // Lane (g, j) of unit k and token group tg holds (row 4 tg + g, output row j).
+    const size_t tstride = (size_t)a.tiles * CTOX_TILE_ROWS, cstride = tstride * M;
+    if (a.chunks > 1 && c + 1 < a.chunks) {
+#pragma unroll
+        for (int k = 0; k < (int)U; k++)
+#pragma unroll
+            for (int tg = 0; tg < (int)TG; tg++) {
+                const uint32_t tok = 4 * tg + g, row = (t0 + k) * CTOX_TILE_ROWS + j;
+                if ((uint32_t)k < n && tok < M) combine_store(&a.partial[c * cstride + tok * tstride + row], acc[k][tg], a.seq);
+            }
+        return;
+    }
+#pragma unroll
+    for (int k = 0; k < (int)U; k++)
+#pragma unroll
+        for (int tg = 0; tg < (int)TG; tg++) {
+            const uint32_t tok = 4 * tg + g, tile = t0 + k, row = tile * CTOX_TILE_ROWS + j;
+            const bool want = (uint32_t)k < n && tok < M;
+            const float sum = a.chunks == 1 ? acc[k][tg]
+                                            : combine_poll(&a.partial[tok * tstride + row], cstride, a.chunks - 1,
+                                                           a.seq, acc[k][tg], want);
+            const float y = want && row < a.rows ? tile_epilogue(sum / C::DEN, row, a) : 0.0f;
+            if (want && row < a.rows) a.output[(size_t)tok * a.out_stride + row] = y;
+            if (a.res_sq) residual_tile_sum_m(a, min(tok, M - 1), tile, row, want, y, j);
+        }
+}
+
+#define CTOX_TILE_MX_KERNEL(name, dt, mr) \
+    extern "C" __global__ __launch_bounds__(256, 2) void name(TileMatvecArgs a) { tile_matvec_mx<dt, mr>(a); }
+CTOX_TILE_MX_KERNEL(ctox_q2_mv_tilemx2_gfx950, 0, 2)
+CTOX_TILE_MX_KERNEL(ctox_q2_mv_tilemx3_gfx950, 0, 3)
+CTOX_TILE_MX_KERNEL(ctox_q2_mv_tilemx4_gfx950, 0, 4)
+CTOX_TILE_MX_KERNEL(ctox_q2_mv_tilemx5_gfx950, 0, 5)
+CTOX_TILE_MX_KERNEL(ctox_q4_mv_tilemx2_gfx950, 1, 2)
+CTOX_TILE_MX_KERNEL(ctox_q4_mv_tilemx3_gfx950, 1, 3)
+CTOX_TILE_MX_KERNEL(ctox_q4_mv_tilemx4_gfx950, 1, 4)
+CTOX_TILE_MX_KERNEL(ctox_q4_mv_tilemx5_gfx950, 1, 5)
 
 // Rewrites crate rows (Q/src/quant.rs:20-29 block layout, rows dense) into
 // the tiled layout; one workgroup per unit, lane (g, j) moves its fragment

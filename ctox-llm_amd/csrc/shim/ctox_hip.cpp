@@ -159,6 +159,9 @@ struct ctox_hip_backend {
     hipFunction_t tilex[2][CTOX_TILE_MAXU] = {};
     // Small-M tiled kernels per dtype: [0] 2..4 rows, [1] 5..8 rows (2 row tiles per wave).
     hipFunction_t tilem[2][2] = {};
+    // The same building the rows' fragments in the kernel, per row count 2..5.
+    hipFunction_t tilemx[2][4] = {};
+    bool no_mx = false;
     hipFunction_t repack = nullptr;
     hipFunction_t gdn_fused = nullptr;
     int cus = 0;
@@ -373,7 +376,21 @@ struct TileXform {
     uint32_t sq_n = 0;
     bool parts_out = false;        // batch 1: chunk partials to output [chunks][rows]
     uint32_t a_parts = 0, a_pstride = 0;  // xmode 2: input as producer chunk partials
+    uint32_t a_stride = 0, b_stride = 0;  // small M: floats between rows of the input and of b / delta
 };
+
+// Small-M rows the in-kernel fragment build takes (ctox_q*_mv_tilemx*).
+constexpr size_t kMaxBuildRows = 5;
+size_t max_build_rows(const ctox_hip_backend *b) { return b->no_mx ? 1 : kMaxBuildRows; }
+// Every workgroup of a chunk rebuilds the chunk's rows, so the in-kernel
+// build pays off only for small matrices: up to 40 Mi weights (o_proj and
+// out_proj, 5120 x 6144: 5 rows in 17.5 us against 15.9 us + a 4.8 us
+// staging launch); the decode engine's larger projections measured faster
+// staged (in the engine, 5 rows of the 5120 x 17408 Q2 down: 26.8 us
+// in-kernel against 19.9 + 4.8 us).
+bool build_in_kernel(const ctox_hip_backend *b, size_t batch, size_t rows, size_t columns) {
+    return batch >= 2 && batch <= max_build_rows(b) && (uint64_t)rows * columns <= (uint64_t)40 << 20;
+}
 
 ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows, size_t columns,
                             const void *d_s_out, uint32_t s_out_kind, const float *d_bias, float *d_output, uint32_t act,
@@ -382,7 +399,13 @@ ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy 
 
 ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows, size_t columns,
                               size_t batch, const void *d_s_out, uint32_t s_out_kind, const float *d_bias,
-                              float *d_output, size_t out_stride, uint32_t act, hipStream_t s);
+                              float *d_output, size_t out_stride, uint32_t act, hipStream_t s,
+                              const float *res_h = nullptr, float *res_sq = nullptr);
+
+ctox_status run_tile_matvec_mx(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows, size_t columns,
+                               size_t batch, const void *d_s_out, uint32_t s_out_kind, const float *d_bias,
+                               float *d_output, size_t out_stride, uint32_t act, hipStream_t s, const float *d_input,
+                               const void *d_s_in, uint32_t s_in_kind, const TileXform &xf);
 
 // One launch over `rows` packed rows of one dtype (a pure matrix or one
 // mixed segment), output rows written at d_output[m*out_stride + r], with
@@ -392,7 +415,8 @@ ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCop
 ctox_status run_matvec(ctox_hip_backend *b, int layout, int32_t dtype, const void *d_weights, size_t rows,
                        size_t columns, size_t batch, const void *d_s_out, uint32_t s_out_kind,
                        const float *d_bias, float *d_output, size_t out_stride, uint32_t act,
-                       hipStream_t s, bool split = false, uint32_t *parts = nullptr) {
+                       hipStream_t s, bool split = false, uint32_t *parts = nullptr, const float *res_h = nullptr,
+                       float *res_sq = nullptr) {
     if (parts) *parts = 1;
     const size_t groups = (rows + CTOX_MV_ROWS - 1) / CTOX_MV_ROWS;
     const size_t tgroups = (batch + 3) / 4;
@@ -419,7 +443,7 @@ ctox_status run_matvec(ctox_hip_backend *b, int layout, int32_t dtype, const voi
             return batch == 1 ? run_tile_matvec(b, dtype, it->second, rows, columns, d_s_out, s_out_kind, d_bias,
                                                 d_output, act, s)
                               : run_tile_matvec_m(b, dtype, it->second, rows, columns, batch, d_s_out, s_out_kind,
-                                                  d_bias, d_output, out_stride, act, s);
+                                                  d_bias, d_output, out_stride, act, s, res_h, res_sq);
     }
     // Batch 1 on rows of whole 16-byte units: the slice kernels (all slices
     // requested up front when there are at most three, else walked).
@@ -529,7 +553,8 @@ ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy 
 // One launch of the small-M tiled matvec (2..8 rows staged in xa/xc).
 ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows, size_t columns,
                               size_t batch, const void *d_s_out, uint32_t s_out_kind, const float *d_bias,
-                              float *d_output, size_t out_stride, uint32_t act, hipStream_t s) {
+                              float *d_output, size_t out_stride, uint32_t act, hipStream_t s, const float *res_h,
+                              float *res_sq) {
     const int q4 = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
     const uint32_t tg = batch > 4 ? 2 : 1;
     const uint32_t u = 2;
@@ -560,7 +585,65 @@ ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCop
     a.activation = act;
     a.batch = (uint32_t)batch;
     a.out_stride = (uint32_t)out_stride;
+    a.res_h = res_h;
+    a.res_sq = res_sq;
     return launch(b->tilem[q4][tg - 1], dim3((unsigned)(waves / 4)), dim3(256), s, a, "ctox_q*_mv_tilem*_gfx950");
+}
+
+// One launch of the small-M tiled matvec that builds its 2..5 rows'
+// fragments from d_input (and the transform's operands in xf) itself.
+ctox_status run_tile_matvec_mx(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows, size_t columns,
+                               size_t batch, const void *d_s_out, uint32_t s_out_kind, const float *d_bias,
+                               float *d_output, size_t out_stride, uint32_t act, hipStream_t s, const float *d_input,
+                               const void *d_s_in, uint32_t s_in_kind, const TileXform &xf) {
+    const int q4 = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
+    const uint32_t u = 2;
+    const uint32_t segs = (((t.tiles + u - 1) / u) + 3) & ~3u;
+    const size_t waves = (size_t)segs * t.chunks;
+    if (batch < 2 || batch > kMaxBuildRows) return fail(CTOX_ERR_SHAPE, "in-kernel row build takes 2..5 rows");
+    if (waves / 4 > 0x7fffffffu || out_stride > 0xffffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
+    if (t.chunks > 1) {
+        ctox_status st =
+            ensure(b, b->tpart, (size_t)(t.chunks - 1) * batch * t.tiles * CTOX_TILE_ROWS * sizeof(uint64_t), true);
+        if (st) return st;
+    }
+    TileMatvecArgs a{};
+    a.weights = (const uint8_t *)t.d;
+    a.s_out = d_s_out;
+    a.bias = d_bias;
+    a.output = d_output;
+    a.partial = (uint64_t *)b->tpart.ptr;
+    a.seq = next_tile_seq(b);
+    a.rows = (uint32_t)rows;
+    a.blocks = (uint32_t)(columns / kBlockLen);
+    a.tiles = t.tiles;
+    a.chunks = t.chunks;
+    a.segs = segs;
+    a.tpw = u;
+    a.s_out_kind = s_out_kind;
+    a.activation = act;
+    a.input = d_input;
+    a.s_in = d_s_in;
+    a.s_in_kind = s_in_kind;
+    a.xmode = xf.xmode;
+    a.xb = xf.b;
+    a.xw = xf.w;
+    a.delta = xf.delta;
+    a.x_out = xf.x_out;
+    a.norm_out = xf.norm_out;
+    a.off = xf.off;
+    a.head_dim = xf.head_dim;
+    a.eps = xf.eps;
+    a.res_h = xf.res_h;
+    a.res_sq = xf.res_sq;
+    a.sq_in = xf.sq_in;
+    a.sq_n = xf.sq_in ? xf.sq_n : 0u;
+    a.batch = (uint32_t)batch;
+    a.out_stride = (uint32_t)out_stride;
+    a.a_stride = xf.a_stride;
+    a.b_stride = xf.b_stride;
+    return launch(b->tilemx[q4][batch - 2], dim3((unsigned)(waves / 4)), dim3(256), s, a,
+                  "ctox_q*_mv_tilemx*_gfx950");
 }
 
 // The registered tiled copy of raw weights, or NULL.
@@ -589,6 +672,21 @@ ctox_status dispatch_matrix(ctox_hip_backend *b, const ctox_hip_matrix *m, const
             ctox_status st = run_tile_matvec(b, seg.dtype, m->tiled[si], nrows, m->columns, so, m->s_out_kind,
                                              m->d_bias ? m->d_bias + r0 : nullptr, d_output + r0, act, s, d_input,
                                              m->d_s_in, m->s_in_kind);
+            if (st) return st;
+            si++;
+            continue;
+        }
+        if (build_in_kernel(b, batch, seg.row_end - seg.row_start, m->columns) && si < m->tiled.size()) {
+            // 2..5 rows: fragments built in the kernel (no staging launch).
+            const size_t r0 = seg.row_start, nrows = seg.row_end - seg.row_start;
+            const void *so = nullptr;
+            if (m->s_out_kind == CTOX_KSCALE_F32) so = (const float *)m->d_s_out + r0;
+            if (m->s_out_kind == CTOX_KSCALE_F16) so = (const uint16_t *)m->d_s_out + r0;
+            TileXform xf;
+            xf.a_stride = (uint32_t)m->columns;
+            ctox_status st = run_tile_matvec_mx(b, seg.dtype, m->tiled[si], nrows, m->columns, batch, so, m->s_out_kind,
+                                                m->d_bias ? m->d_bias + r0 : nullptr, d_output + r0, m->rows, act, s,
+                                                d_input, m->d_s_in, m->s_in_kind, xf);
             if (st) return st;
             si++;
             continue;
@@ -695,6 +793,10 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->tilex[1][2], "ctox_q4_mv_tile3x_gfx950"}, {&b->tilex[1][3], "ctox_q4_mv_tile4x_gfx950"},
                {&b->tilem[0][0], "ctox_q2_mv_tilem1_gfx950"}, {&b->tilem[0][1], "ctox_q2_mv_tilem2_gfx950"},
                {&b->tilem[1][0], "ctox_q4_mv_tilem1_gfx950"}, {&b->tilem[1][1], "ctox_q4_mv_tilem2_gfx950"},
+               {&b->tilemx[0][0], "ctox_q2_mv_tilemx2_gfx950"}, {&b->tilemx[0][1], "ctox_q2_mv_tilemx3_gfx950"},
+               {&b->tilemx[0][2], "ctox_q2_mv_tilemx4_gfx950"}, {&b->tilemx[0][3], "ctox_q2_mv_tilemx5_gfx950"},
+               {&b->tilemx[1][0], "ctox_q4_mv_tilemx2_gfx950"}, {&b->tilemx[1][1], "ctox_q4_mv_tilemx3_gfx950"},
+               {&b->tilemx[1][2], "ctox_q4_mv_tilemx4_gfx950"}, {&b->tilemx[1][3], "ctox_q4_mv_tilemx5_gfx950"},
                {&b->repack, "ctox_tile_repack_gfx950"}, {&b->gdn_fused, "ctox_gdn_fused_gfx950"},
                {&b->finite, "ctox_finite_check_gfx950"}, {&b->gather, "ctox_gather_rows_gfx950"}};
     for (auto &f : fns) {
@@ -711,6 +813,9 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
         return fail(CTOX_ERR_UNSUPPORTED_OPERATION, "HIP module setup failed: %s", hipGetErrorString(le));
     }
     b->cus = prop.multiProcessorCount;
+    // CTOX_SMALL_M_BUILD=0: 2..5-row projections stage their fragments in a
+    // separate launch (the tilem kernels) instead of building them in-kernel.
+    if (const char *m = std::getenv("CTOX_SMALL_M_BUILD")) b->no_mx = std::atoi(m) == 0;
     if (const char *u = std::getenv("CTOX_TILE_U")) {
         const int v = std::atoi(u);
         if (v >= 1 && v <= CTOX_TILE_MAXU) b->tile_u = (uint32_t)v;
@@ -905,11 +1010,19 @@ extern "C" ctox_status ctox_hip_launch_fused_matvec(ctox_hip_backend *b, int32_t
     if (activation > 1) return fail(CTOX_ERR_SHAPE, "activation %u is not identity (0) or SiLU (1)", activation);
     hipStream_t s = pick_stream(b, stream);
     const int layout = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
-    if (batch == 1)
-        if (const TiledCopy *t = registered(b, d_weights, rows, columns))
+    if (const TiledCopy *t = registered(b, d_weights, rows, columns)) {
+        if (batch == 1)
             return run_tile_matvec(b, dtype, *t, rows, columns, d_s_out, d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE,
                                    d_bias, d_output, activation, s, d_input, d_s_in,
                                    d_s_in ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE);
+        if (build_in_kernel(b, batch, rows, columns)) {
+            TileXform xf;
+            xf.a_stride = columns;
+            return run_tile_matvec_mx(b, dtype, *t, rows, columns, batch, d_s_out,
+                                      d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, d_bias, d_output, rows, activation,
+                                      s, d_input, d_s_in, d_s_in ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, xf);
+        }
+    }
     ctox_status st = run_prep(b, layout, d_input, columns, batch, d_s_in,
                               d_s_in ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, s);
     if (st) return st;
@@ -1023,6 +1136,26 @@ extern "C" ctox_status ctox_hip_norm_matvec_parts_device(ctox_hip_backend *b, co
                                    nullptr, d_output, 0, s, d_x, d_s_in, d_s_in ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, &xf);
         }
     }
+    // Registered weights, 2..5 rows with the producer's sums of squares: one
+    // launch that builds every row's fragments.
+    if (build_in_kernel(b, batch, rows, columns) && d_sums && (!d_delta || delta_parts == 1)) {
+        if (const TiledCopy *t = registered(b, d_weights, rows, columns)) {
+            TileXform xf;
+            xf.xmode = 1;
+            xf.w = d_norm_w;
+            xf.delta = d_delta;
+            xf.x_out = d_delta ? d_x_out : nullptr;
+            xf.norm_out = d_norm_out;
+            xf.eps = eps;
+            xf.sq_in = d_sums;
+            xf.sq_n = sum_count;
+            xf.a_stride = columns;
+            xf.b_stride = columns;
+            return run_tile_matvec_mx(b, dtype, *t, rows, columns, batch, d_s_out,
+                                      d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, nullptr, d_output, rows, 0, s, d_x,
+                                      d_s_in, d_s_in ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, xf);
+        }
+    }
     ctox_status st = ensure(b, b->xa[layout], blocks * batch * 192, false);
     if (!st) st = ensure(b, b->xc[layout], blocks * batch * 4 * sizeof(float), false);
     if (st) return st;
@@ -1092,8 +1225,30 @@ extern "C" ctox_status ctox_hip_transform_matvec_device(ctox_hip_backend *b, con
                                    nullptr, d_output, 0, s, x->a, d_s_in, d_s_in ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, &xf);
         }
     }
-    if (x->res_sums || x->a_parts > 1)
-        return fail(CTOX_ERR_UNSUPPORTED_OPERATION, "residual sums and input partials need batch 1 on registered weights");
+    // Registered weights, 2..5 rows: one launch that builds every row's fragments.
+    if (build_in_kernel(b, batch, rows, columns) && x->a_parts <= 1 &&
+        (x->mode != 2 || x->head_dim == 64 || x->head_dim == 128 || x->head_dim == 256)) {
+        if (const TiledCopy *t = registered(b, d_weights, rows, columns)) {
+            TileXform xf;
+            xf.xmode = x->mode + 1;
+            xf.b = x->b;
+            xf.w = x->w;
+            xf.off = x->off;
+            xf.head_dim = x->head_dim;
+            xf.eps = x->eps;
+            xf.res_h = x->res_h;
+            xf.res_sq = x->res_sums;
+            xf.a_stride = x->a_stride;
+            xf.b_stride = x->b_stride;
+            return run_tile_matvec_mx(b, dtype, *t, rows, columns, batch, d_s_out,
+                                      d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, nullptr, d_output, rows, 0, s, x->a,
+                                      d_s_in, d_s_in ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, xf);
+        }
+    }
+    const bool reg = registered(b, d_weights, rows, columns) != nullptr;
+    if ((x->res_sums && (!reg || batch > CTOX_MAX_BATCH)) || x->a_parts > 1)
+        return fail(CTOX_ERR_UNSUPPORTED_OPERATION,
+                    "residual sums need registered weights; input partials need 1 row on registered weights");
     ctox_status st = ensure(b, b->xa[layout], blocks * batch * 192, false);
     if (!st) st = ensure(b, b->xc[layout], blocks * batch * 4 * sizeof(float), false);
     if (st) return st;
@@ -1117,7 +1272,8 @@ extern "C" ctox_status ctox_hip_transform_matvec_device(ctox_hip_backend *b, con
     a.eps = x->eps;
     if ((st = launch(b->prep_x, dim3((unsigned)blocks, batch), dim3(64), s, a, "ctox_prep_transform_gfx950"))) return st;
     return run_matvec(b, layout, dtype, d_weights, rows, columns, batch, d_s_out,
-                      d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, nullptr, d_output, rows, 0, s, split_k != 0, parts);
+                      d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, nullptr, d_output, rows, 0, s, split_k != 0, parts,
+                      x->res_h, x->res_sums);
 }
 
 extern "C" ctox_status ctox_hip_fused_matvec(ctox_hip_backend *b, const ctox_fused_matvec *op, float *output,

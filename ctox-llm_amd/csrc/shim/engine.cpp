@@ -213,13 +213,17 @@ ctox_status matvec(ctox_hip_engine *e, const Mat &m, const float *in, float *out
                                         e->s);
 }
 
+// Rows whose residual producers hand the next norm its per-tile sums of
+// squares (the projections build up to 5 rows in the kernel).
+constexpr uint32_t kSumRows = 5;
+
 // x += delta (when set), (1 + w) RMS norm, then the projection m of the
 // normalized rows into out; the normalized rows also go to norm_out if set.
 // The residual stream ping-pongs between e->hid and e->hid2: with a delta the
 // sum goes to the other buffer, which becomes the stream.
 ctox_status norm_mv(ctox_hip_engine *e, const float *delta, const float *w, uint32_t rows, const Mat &m, float *out,
                     float *norm_out = nullptr, uint32_t max_parts = 1, uint32_t *parts = nullptr) {
-    const bool sums = delta && rows == 1 && e->rsq_delta == delta && e->rsq_hid == e->hid && e->delta_parts == 1;
+    const bool sums = delta && rows <= kSumRows && e->rsq_delta == delta && e->rsq_hid == e->hid && e->delta_parts == 1;
     e->rsq_delta = e->rsq_hid = nullptr;
     TRY(ctox_hip_norm_matvec_parts_device(e->b, e->hid, delta, e->delta_parts, (size_t)rows * e->H, delta ? e->hid2 : nullptr,
                                     w, e->c.rms_norm_epsilon, norm_out, m.dtype, m.w, m.s_in, m.s_out, out, m.rows,
@@ -231,14 +235,14 @@ ctox_status norm_mv(ctox_hip_engine *e, const float *delta, const float *w, uint
 // A single-row producer of residual delta `out` also leaves the next norm's
 // per-tile sums of squares (ctox_input_transform::res_sums).
 ctox_status delta_mv(ctox_hip_engine *e, ctox_input_transform &x, const Mat &m, float *out, uint32_t R) {
-    if (R == 1) {
+    if (R <= kSumRows) {
         x.res_h = e->hid;
         x.res_sums = e->rsq;
     }
     e->rsq_delta = e->rsq_hid = nullptr;
     TRY(ctox_hip_transform_matvec_device(e->b, &x, m.dtype, m.w, m.s_in, m.s_out, out, m.rows, m.cols, R, 1,
                                          &e->delta_parts, e->s));
-    if (R == 1) {
+    if (R <= kSumRows) {
         e->rsq_delta = out;
         e->rsq_hid = e->hid;
     }
@@ -661,7 +665,7 @@ extern "C" ctox_status ctox_hip_engine_create(ctox_hip_backend *b, const ctox_en
         (st = dalloc_t(e, &e->mtp_hidden, R * e->H)) || (st = dalloc_t(e, &e->prev_hidden, R * e->H)) ||
         (st = dalloc_t(e, &e->target_hidden, (R + 1) * e->H)) || (st = dalloc_t(e, &e->d_tokens, 16)) ||
         (st = dalloc_t(e, &e->d_drafts, 16)) || (st = dalloc_t(e, &e->d_result, 16)) || (st = dalloc_t(e, &e->d_rng, 1)) ||
-        (st = dalloc_t(e, &e->rsq, 512)) || (st = dalloc_t(e, &e->d_flags, 64)))
+        (st = dalloc_t(e, &e->rsq, 8 * 512)) || (st = dalloc_t(e, &e->d_flags, 64)))
         return cleanup(st);
     if (hipHostMalloc((void **)&e->h_flags, 64 * sizeof(uint32_t), hipHostMallocDefault) != hipSuccess) {
         e->h_flags = nullptr;

@@ -227,10 +227,12 @@ ctox_status ctox_hip_norm_matvec_device(ctox_hip_backend *backend, const float *
                                         void *stream);
 
 /* ctox_hip_norm_matvec_device with the residual's sum of squares given as
- * d_sums[sum_count] per-16-row-tile partials (a producing
- * ctox_hip_transform_matvec_device's res_sums over d_x + d_delta); they are
- * added in tile order. Used on the batch-1 registered-weights path only
- * (otherwise the sum is computed from the rows as before). */
+ * per-16-row-tile partials, d_sums[batch][sum_count] (a producing
+ * ctox_hip_transform_matvec_device's res_sums over d_x + d_delta). Used on
+ * registered weights for 1 row and for 2..5 rows of matrices up to 120 Mi
+ * weights (there the fragments of every row are built in the projection's
+ * launch, no staging kernel); otherwise the sums are computed from the rows
+ * as before. */
 ctox_status ctox_hip_norm_matvec_sums_device(ctox_hip_backend *backend, const float *d_x, const float *d_delta,
                                              uint32_t delta_parts, size_t delta_part_stride, float *d_x_out,
                                              const float *d_norm_w, float eps, float *d_norm_out, int32_t dtype,
@@ -270,7 +272,9 @@ typedef struct {
      * the sum over its rows r of (res_h[r] + out[r])^2: the sum of squares a
      * following ctox_hip_norm_matvec_sums_device needs (Q/src/reference.rs:38-62),
      * so that it need not re-read the whole residual row in every workgroup.
-     * Batch 1 on registered weights only; otherwise the call fails with
+     * 1 row, or 2..5 rows of a matrix of at most 120 Mi weights, on
+     * registered weights (row t: res_h + t * rows and
+     * res_sums + t * ceil(rows / 16)); otherwise the call fails with
      * CTOX_ERR_UNSUPPORTED_OPERATION. No crate counterpart (the CPU decoder
      * adds and normalizes in one pass, Q/src/decoder.rs:636-680). */
     const float *res_h;

@@ -397,3 +397,160 @@ def test_gate_up_partials_chain(hip, orc, cols):
     np.testing.assert_allclose(out[0].cpu().numpy(), ref, rtol=1e-3, atol=1e-4 * float(np.abs(ref).max()))
     hip.unregister_tiled_weights(dgu.data_ptr())
     hip.unregister_tiled_weights(ddn.data_ptr())
+
+
+def _qmat(rng, r, c, dtype):
+    bb = 34 if dtype == 1 else 18
+    blocks = rng.integers(0, 256, size=(r, c // 64, bb), dtype=np.uint8)
+    blocks[:, :, :2] = (np.abs(rng.standard_normal((r, c // 64))) * 0.02).astype(np.float16).view(
+        np.uint8).reshape(r, c // 64, 2)
+    return blocks.tobytes()
+
+
+def _close_rows(got, ref):
+    rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
+    assert np.all(np.abs(got - ref) <= 1e-3 * (np.abs(ref) + rms)), float(np.abs(got - ref).max())
+
+
+@pytest.mark.parametrize("batch", [2, 3, 5])
+@pytest.mark.parametrize("mode,dtype,hd,heads,rows", [(1, 0, 0, 0, 200), (2, 1, 128, 12, 200), (3, 1, 256, 6, 200),
+                                                      (2, 0, 64, 8, 200), (1, 0, 0, 0, 8256)])
+def test_transform_matvec_rows_built_in_kernel(hip, orc, batch, mode, dtype, hd, heads, rows):
+    """2..5 rows of a producer fused into a projection on registered weights
+    (up to 40 Mi weights ctox_q*_mv_tilemx*, every row's fragments built in
+    the launch; the 8256 x 5120 case runs the staging launch and the staged
+    kernel), with the residual sums of every row, against the oracle producer
+    + matvec per row and float64 sums. Widths with a partial last
+    1024-column chunk and ragged row tiles."""
+    import ctox_hip
+    say(f"case transform rows batch={batch} mode={mode} dtype={dtype} rows={rows}")
+    rng = np.random.default_rng(100 * batch + 10 * mode + dtype)
+    cols = {1: 1536 if rows < 1000 else 5120, 2: heads * hd, 3: heads * hd}[mode]
+    w = _qmat(rng, rows, cols, dtype)
+    s_in = rng.uniform(0.75, 1.25, cols).astype(np.float16)
+    s_out = rng.uniform(0.75, 1.25, rows).astype(np.float16)
+    nw = (rng.standard_normal(max(hd, 1)) * 0.1 + 1.0).astype(np.float32)
+    astr = {1: 2 * cols + 64, 2: cols + 64, 3: cols + 32}[mode]
+    bstr = {1: 0, 2: cols + 128, 3: 2 * cols + 64}[mode]
+    a = rng.standard_normal((batch, astr)).astype(np.float32)
+    b = rng.standard_normal((batch, max(bstr, 1))).astype(np.float32)
+    xs = []
+    for t in range(batch):
+        if mode == 1:
+            xs.append(orc.swiglu(a[t, :cols], a[t, cols:2 * cols]))
+        elif mode == 2:
+            xs.append(orc.rms_norm_gated(a[t, :cols], b[t, :cols], heads, hd, nw, 1e-6))
+        else:
+            x = a[t, :cols].copy()
+            orc.sigmoid_gate(x, b[t, :2 * cols].reshape(heads, 2 * hd)[:, hd:].reshape(-1))
+            xs.append(x)
+    hres = rng.standard_normal((batch, rows)).astype(np.float32)
+    da, db, dwn, dh = dev(a), dev(b), dev(nw), dev(hres)
+    tiles = (rows + 15) // 16
+    sums = torch.full((batch, tiles), float("nan"), device="cuda")
+    tr = _Transform(da.data_ptr(), db.data_ptr() if mode != 1 else None, dwn.data_ptr() if mode == 2 else None, mode,
+                    astr, bstr, cols if mode == 1 else 0, hd, 1e-6, dh.data_ptr(), sums.data_ptr())
+    dwt = torch.from_numpy(np.frombuffer(w, np.uint8).copy()).cuda()
+    dsi = torch.from_numpy(s_in.view(np.int16).copy()).cuda()
+    dso = torch.from_numpy(s_out.view(np.int16).copy()).cuda()
+    out = torch.full((batch, rows), float("nan"), device="cuda")
+    lib = ctox_hip.load_library()
+    hip.register_tiled_weights(ctox_hip.TensorDType(dtype), dwt.data_ptr(), rows, cols)
+    try:
+        parts = ctypes.c_uint32(0)
+        st = lib.ctox_hip_transform_matvec_device(hip.handle, ctypes.byref(tr), dtype, dwt.data_ptr(), dsi.data_ptr(),
+                                                  dso.data_ptr(), out.data_ptr(), rows, cols, batch, 1,
+                                                  ctypes.byref(parts), None)
+        assert st == 0, lib.ctox_hip_last_error()
+        torch.cuda.synchronize()
+    finally:
+        hip.unregister_tiled_weights(dwt.data_ptr())
+    got = out.cpu().numpy()
+    for t in range(batch):
+        ref = orc.fused_matvec(dtype, w, rows, cols, xs[t], s_in=("f16le", s_in.view(np.uint8)),
+                               s_out=("f16le", s_out.view(np.uint8)))
+        _close_rows(got[t], ref)
+        h = (hres[t] + got[t]).astype(np.float64)
+        want = np.array([np.sum(h[i * 16:(i + 1) * 16] ** 2) for i in range(tiles)])
+        np.testing.assert_allclose(sums[t].cpu().numpy(), want, rtol=1e-5)
+
+
+@pytest.mark.parametrize("batch", [2, 4, 5])
+@pytest.mark.parametrize("with_delta", [True, False])
+@pytest.mark.parametrize("dtype,rows,cols", [(1, 300, 5120), (0, 64, 1536)])
+def test_norm_matvec_rows_with_sums(hip, orc, batch, with_delta, dtype, rows, cols):
+    """Residual add + (1 + w) RMS norm + projection of 2..5 rows from the
+    producer's per-tile sums (ctox_q*_mv_tilemx*), against the oracle norm and
+    matvec per row; the residual and normalized rows are written once."""
+    import ctox_hip
+    say(f"case norm rows batch={batch} delta={with_delta} dtype={dtype} {rows}x{cols}")
+    rng = np.random.default_rng(batch * 7 + dtype + with_delta)
+    w = _qmat(rng, rows, cols, dtype)
+    s_in = rng.uniform(0.75, 1.25, cols).astype(np.float16)
+    s_out = rng.uniform(0.75, 1.25, rows).astype(np.float16)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    d = rng.standard_normal((batch, cols)).astype(np.float32)
+    nw = (rng.standard_normal(cols) * 0.1).astype(np.float32)
+    h = (x + d) if with_delta else x
+    tiles = (cols + 15) // 16
+    sums = np.array([[np.sum(h[t, i * 16:(i + 1) * 16].astype(np.float64) ** 2) for i in range(tiles)]
+                     for t in range(batch)], np.float32)
+    dx, dd, dw, ds = dev(x), dev(d), dev(nw), dev(sums)
+    dwt = torch.from_numpy(np.frombuffer(w, np.uint8).copy()).cuda()
+    dsi = torch.from_numpy(s_in.view(np.int16).copy()).cuda()
+    dso = torch.from_numpy(s_out.view(np.int16).copy()).cuda()
+    xo = torch.full((batch, cols), float("nan"), device="cuda")
+    no = torch.full((batch, cols), float("nan"), device="cuda")
+    out = torch.full((batch, rows), float("nan"), device="cuda")
+    lib = ctox_hip.load_library()
+    hip.register_tiled_weights(ctox_hip.TensorDType(dtype), dwt.data_ptr(), rows, cols)
+    try:
+        st = lib.ctox_hip_norm_matvec_sums_device(hip.handle, dx.data_ptr(), dd.data_ptr() if with_delta else None, 1,
+                                                  0, xo.data_ptr() if with_delta else None, dw.data_ptr(), 1e-6,
+                                                  no.data_ptr(), dtype, dwt.data_ptr(), dsi.data_ptr(), dso.data_ptr(),
+                                                  out.data_ptr(), rows, cols, batch, ds.data_ptr(), tiles, None)
+        assert st == 0, lib.ctox_hip_last_error()
+        torch.cuda.synchronize()
+    finally:
+        hip.unregister_tiled_weights(dwt.data_ptr())
+    for t in range(batch):
+        if with_delta:
+            assert np.array_equal(xo[t].cpu().numpy(), h[t])
+        y = orc.rms_norm_1p_weight(h[t], 1, cols, nw, 1e-6)
+        np.testing.assert_allclose(no[t].cpu().numpy(), y, rtol=1e-5, atol=1e-6)
+        ref = orc.fused_matvec(dtype, w, rows, cols, y, s_in=("f16le", s_in.view(np.uint8)),
+                               s_out=("f16le", s_out.view(np.uint8)))
+        _close_rows(out[t].cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("batch", [2, 3, 5])
+@pytest.mark.parametrize("dtype", [0, 1])
+def test_raw_launch_rows_built_in_kernel(hip, orc, batch, dtype):
+    """The raw 9-parameter launch on registered weights with 2..5 rows (no
+    staging launch) against the oracle per row, with bias and SiLU."""
+    import ctox_hip
+    say(f"case raw rows batch={batch} dtype={dtype}")
+    rng = np.random.default_rng(batch + 5 * dtype)
+    rows, cols = 333, 3072
+    w = _qmat(rng, rows, cols, dtype)
+    s_in = rng.uniform(0.75, 1.25, cols).astype(np.float16)
+    s_out = rng.uniform(0.75, 1.25, rows).astype(np.float16)
+    bias = (rng.standard_normal(rows) * 0.05).astype(np.float32)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    dwt = torch.from_numpy(np.frombuffer(w, np.uint8).copy()).cuda()
+    dsi = torch.from_numpy(s_in.view(np.int16).copy()).cuda()
+    dso = torch.from_numpy(s_out.view(np.int16).copy()).cuda()
+    dx, db = dev(x), dev(bias)
+    out = torch.full((batch, rows), float("nan"), device="cuda")
+    hip.register_tiled_weights(ctox_hip.TensorDType(dtype), dwt.data_ptr(), rows, cols)
+    try:
+        hip.launch_fused_matvec(ctox_hip.TensorDType(dtype), dwt.data_ptr(), dx.data_ptr(), dsi.data_ptr(),
+                                dso.data_ptr(), db.data_ptr(), out.data_ptr(), rows, cols, ctox_hip.Activation.Silu,
+                                batch, None)
+        torch.cuda.synchronize()
+    finally:
+        hip.unregister_tiled_weights(dwt.data_ptr())
+    for t in range(batch):
+        ref = orc.fused_matvec(dtype, w, rows, cols, x[t], s_in=("f16le", s_in.view(np.uint8)),
+                               s_out=("f16le", s_out.view(np.uint8)), bias=bias, activation=1)
+        _close_rows(out[t].cpu().numpy(), ref)
