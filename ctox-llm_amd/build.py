@@ -42,15 +42,26 @@ def build_kernels() -> str:
     return out
 
 
+def build_noalloc() -> str:
+    """The static device scratch of the allocation-free entry point: a HIP
+    source compiled with hipcc (its __device__ array is registered with the
+    runtime when the library loads)."""
+    out = os.path.join(LIB, "noalloc.o")
+    src = os.path.join(PKG, "csrc", "shim", "noalloc.hip")
+    _run([HIPCC, *HIP_FLAGS, "-fPIC", "-c", f"-I{os.path.join(ROOT, 'include')}", src, "-o", out])
+    return out
+
+
 def build_shim(hsaco: str) -> str:
     out = os.path.join(LIB, "libctox_hip.so")
     src = os.path.join(PKG, "csrc", "shim", "ctox_hip.cpp")
     engine = os.path.join(PKG, "csrc", "shim", "engine.cpp")
+    noalloc = build_noalloc()
     _run([
         "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra",
         "-D__HIP_PLATFORM_AMD__", f"-DCTOX_HSACO_PATH=\"{hsaco}\"",
         f"-I{os.path.join(ROOT, 'include')}", f"-I{os.path.join(ROCM, 'include')}",
-        src, engine, "-o", out,
+        src, engine, noalloc, "-o", out,
         f"-L{os.path.join(ROCM, 'lib')}", "-lamdhip64", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}",
     ])
     return out

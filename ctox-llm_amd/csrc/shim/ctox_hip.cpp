@@ -28,6 +28,10 @@
 
 #include "../kernels/kernel_args.h"
 
+// Static scratch of the allocation-free entry point (noalloc.hip).
+extern "C" ctox_status ctox_noalloc_setup(int device);
+extern "C" ctox_status ctox_noalloc_slots(int device, void *stream, uint64_t **ptr, size_t *bytes, uint32_t *seq);
+
 // ---- embedded gfx950 code object ----
 extern "C" const unsigned char ctox_hsaco_begin[];
 extern "C" const unsigned char ctox_hsaco_end[];
@@ -162,6 +166,7 @@ struct ctox_hip_backend {
     // The same building the rows' fragments in the kernel, per row count 2..5.
     hipFunction_t tilemx[2][4] = {};
     bool no_mx = false;
+    bool noalloc_ok = false;  // the static scratch of ctox_hip_launch_fused_matvec_noalloc is set up
     hipFunction_t repack = nullptr;
     hipFunction_t gdn_fused = nullptr;
     int cus = 0;
@@ -379,6 +384,14 @@ struct TileXform {
     uint32_t a_stride = 0, b_stride = 0;  // small M: floats between rows of the input and of b / delta
 };
 
+// Caller-provided combine slots (the allocation-free entry point's static
+// device scratch) in place of the backend's grown buffer, with their tag.
+struct PartialSlots {
+    uint64_t *p = nullptr;
+    size_t bytes = 0;
+    uint32_t seq = 0;
+};
+
 // Small-M rows the in-kernel fragment build takes (ctox_q*_mv_tilemx*).
 constexpr size_t kMaxBuildRows = 5;
 size_t max_build_rows(const ctox_hip_backend *b) { return b->no_mx ? 1 : kMaxBuildRows; }
@@ -395,7 +408,8 @@ bool build_in_kernel(const ctox_hip_backend *b, size_t batch, size_t rows, size_
 ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows, size_t columns,
                             const void *d_s_out, uint32_t s_out_kind, const float *d_bias, float *d_output, uint32_t act,
                             hipStream_t s, const float *d_input = nullptr, const void *d_s_in = nullptr,
-                            uint32_t s_in_kind = CTOX_KSCALE_NONE, const TileXform *xf = nullptr);
+                            uint32_t s_in_kind = CTOX_KSCALE_NONE, const TileXform *xf = nullptr,
+                            const PartialSlots *ps = nullptr);
 
 ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows, size_t columns,
                               size_t batch, const void *d_s_out, uint32_t s_out_kind, const float *d_bias,
@@ -405,7 +419,8 @@ ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCop
 ctox_status run_tile_matvec_mx(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows, size_t columns,
                                size_t batch, const void *d_s_out, uint32_t s_out_kind, const float *d_bias,
                                float *d_output, size_t out_stride, uint32_t act, hipStream_t s, const float *d_input,
-                               const void *d_s_in, uint32_t s_in_kind, const TileXform &xf);
+                               const void *d_s_in, uint32_t s_in_kind, const TileXform &xf,
+                               const PartialSlots *ps = nullptr);
 
 // One launch over `rows` packed rows of one dtype (a pure matrix or one
 // mixed segment), output rows written at d_output[m*out_stride + r], with
@@ -493,7 +508,7 @@ uint32_t next_tile_seq(ctox_hip_backend *b) {
 ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows,
                             size_t columns, const void *d_s_out, uint32_t s_out_kind, const float *d_bias,
                             float *d_output, uint32_t act, hipStream_t s, const float *d_input,
-                            const void *d_s_in, uint32_t s_in_kind, const TileXform *xf) {
+                            const void *d_s_in, uint32_t s_in_kind, const TileXform *xf, const PartialSlots *ps) {
     const int q4 = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
     const size_t units = (size_t)t.tiles * t.chunks;
     const size_t slots = (size_t)(b->cus > 0 ? b->cus : 256) * 12;
@@ -503,8 +518,12 @@ ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy 
     if (d_input) segs = (segs + 3) & ~3u;
     const size_t waves = (size_t)segs * t.chunks;
     if ((waves + 3) / 4 > 0x7fffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
-    if (t.chunks > 1) {
-        ctox_status st = ensure(b, b->tpart, (size_t)(t.chunks - 1) * t.tiles * CTOX_TILE_ROWS * sizeof(uint64_t), true);
+    const size_t slot_bytes = (size_t)(t.chunks - 1) * t.tiles * CTOX_TILE_ROWS * sizeof(uint64_t);
+    if (ps && slot_bytes > ps->bytes)
+        return fail(CTOX_ERR_MEMORY_BUDGET, "combine slots need %zu bytes, the static scratch holds %zu", slot_bytes,
+                    ps->bytes);
+    if (t.chunks > 1 && !ps) {
+        ctox_status st = ensure(b, b->tpart, slot_bytes, true);
         if (st) return st;
     }
     TileMatvecArgs a{};
@@ -514,8 +533,8 @@ ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy 
     a.s_out = d_s_out;
     a.bias = d_bias;
     a.output = d_output;
-    a.partial = (uint64_t *)b->tpart.ptr;
-    a.seq = next_tile_seq(b);
+    a.partial = ps ? ps->p : (uint64_t *)b->tpart.ptr;
+    a.seq = ps ? ps->seq : next_tile_seq(b);
     a.rows = (uint32_t)rows;
     a.blocks = (uint32_t)(columns / kBlockLen);
     a.tiles = t.tiles;
@@ -595,16 +614,19 @@ ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCop
 ctox_status run_tile_matvec_mx(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows, size_t columns,
                                size_t batch, const void *d_s_out, uint32_t s_out_kind, const float *d_bias,
                                float *d_output, size_t out_stride, uint32_t act, hipStream_t s, const float *d_input,
-                               const void *d_s_in, uint32_t s_in_kind, const TileXform &xf) {
+                               const void *d_s_in, uint32_t s_in_kind, const TileXform &xf, const PartialSlots *ps) {
     const int q4 = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
     const uint32_t u = 2;
     const uint32_t segs = (((t.tiles + u - 1) / u) + 3) & ~3u;
     const size_t waves = (size_t)segs * t.chunks;
     if (batch < 2 || batch > kMaxBuildRows) return fail(CTOX_ERR_SHAPE, "in-kernel row build takes 2..5 rows");
     if (waves / 4 > 0x7fffffffu || out_stride > 0xffffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
-    if (t.chunks > 1) {
-        ctox_status st =
-            ensure(b, b->tpart, (size_t)(t.chunks - 1) * batch * t.tiles * CTOX_TILE_ROWS * sizeof(uint64_t), true);
+    const size_t slot_bytes = (size_t)(t.chunks - 1) * batch * t.tiles * CTOX_TILE_ROWS * sizeof(uint64_t);
+    if (ps && slot_bytes > ps->bytes)
+        return fail(CTOX_ERR_MEMORY_BUDGET, "combine slots need %zu bytes, the static scratch holds %zu", slot_bytes,
+                    ps->bytes);
+    if (t.chunks > 1 && !ps) {
+        ctox_status st = ensure(b, b->tpart, slot_bytes, true);
         if (st) return st;
     }
     TileMatvecArgs a{};
@@ -612,8 +634,8 @@ ctox_status run_tile_matvec_mx(ctox_hip_backend *b, int32_t dtype, const TiledCo
     a.s_out = d_s_out;
     a.bias = d_bias;
     a.output = d_output;
-    a.partial = (uint64_t *)b->tpart.ptr;
-    a.seq = next_tile_seq(b);
+    a.partial = ps ? ps->p : (uint64_t *)b->tpart.ptr;
+    a.seq = ps ? ps->seq : next_tile_seq(b);
     a.rows = (uint32_t)rows;
     a.blocks = (uint32_t)(columns / kBlockLen);
     a.tiles = t.tiles;
@@ -749,6 +771,9 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
     std::snprintf(b->arch, sizeof b->arch, "%s", prop.gcnArchName);
     hipError_t le = hipSetDevice(device);
     if (le == hipSuccess) le = hipModuleLoadData(&b->module, ctox_hsaco_begin);
+    // The allocation-free entry point's static scratch on this device
+    // (address taken once per device, with the device current).
+    if (le == hipSuccess) b->noalloc_ok = ctox_noalloc_setup(device) == CTOX_OK;
     if (le == hipSuccess) le = hipStreamCreateWithFlags(&b->stream, hipStreamNonBlocking);
     struct {
         hipFunction_t *f;
@@ -1028,6 +1053,36 @@ extern "C" ctox_status ctox_hip_launch_fused_matvec(ctox_hip_backend *b, int32_t
     if (st) return st;
     return run_matvec(b, layout, dtype, d_weights, rows, columns, batch, d_s_out,
                       d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, d_bias, d_output, rows, activation, s);
+}
+
+extern "C" ctox_status ctox_hip_launch_fused_matvec_noalloc(ctox_hip_backend *b, int32_t dtype,
+                                                            const void *d_weights, const float *d_input,
+                                                            const uint16_t *d_s_in, const uint16_t *d_s_out,
+                                                            const float *d_bias, float *d_output, uint32_t rows,
+                                                            uint32_t columns, uint32_t activation, uint32_t batch,
+                                                            void *stream) {
+    if (!b || !d_weights || !d_input || !d_output) return fail(CTOX_ERR_SHAPE, "null argument");
+    if (dtype != CTOX_DTYPE_Q2B64 && dtype != CTOX_DTYPE_Q4B64)
+        return fail(CTOX_ERR_UNSUPPORTED_DTYPE, "raw launch takes pure Q2_B64 or Q4_B64 weights");
+    if (rows == 0 || columns == 0 || columns % kBlockLen)
+        return fail(CTOX_ERR_SHAPE, "Q2/Q4 fused matvec dimensions must be non-zero and columns divisible by 64");
+    if (batch == 0 || batch > kMaxBuildRows) return fail(CTOX_ERR_SHAPE, "allocation-free launch takes 1..5 rows");
+    if (activation > 1) return fail(CTOX_ERR_SHAPE, "activation %u is not identity (0) or SiLU (1)", activation);
+    if (!b->noalloc_ok) return fail(CTOX_ERR_INVALID_STATE, "the static scratch of this device is not set up");
+    const TiledCopy *t = registered(b, d_weights, rows, columns);
+    if (!t) return fail(CTOX_ERR_UNSUPPORTED_OPERATION, "allocation-free launch needs registered tiled weights");
+    hipStream_t s = pick_stream(b, stream);
+    PartialSlots ps;
+    if (ctox_noalloc_slots(b->device, s, &ps.p, &ps.bytes, &ps.seq) != CTOX_OK)
+        return fail(CTOX_ERR_INVALID_STATE, "static scratch unavailable");
+    const uint32_t sk = d_s_in ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, ok = d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE;
+    if (batch == 1)
+        return run_tile_matvec(b, dtype, *t, rows, columns, d_s_out, ok, d_bias, d_output, activation, s, d_input,
+                               d_s_in, sk, nullptr, &ps);
+    TileXform xf;
+    xf.a_stride = columns;
+    return run_tile_matvec_mx(b, dtype, *t, rows, columns, batch, d_s_out, ok, d_bias, d_output, rows, activation, s,
+                              d_input, d_s_in, sk, xf, &ps);
 }
 
 extern "C" ctox_status ctox_hip_register_tiled_weights(ctox_hip_backend *b, int32_t dtype, const void *d_weights,

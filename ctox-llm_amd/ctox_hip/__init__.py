@@ -225,6 +225,7 @@ SIGNATURES = {
     "ctox_hip_matrix_dispatch_fanout": (_I32, [_P, ctypes.POINTER(_P), _SZ, _P, _SZ, ctypes.POINTER(_P), _P]),
     "ctox_hip_launch_fused_matvec": (_I32, [_P, _I32, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "ctox_hip_register_tiled_weights": (_I32, [_P, _I32, _P, _U32, _U32, _P]),
+    "ctox_hip_launch_fused_matvec_noalloc": (_I32, [_P, _I32, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "ctox_hip_gdn_fused_device": (_I32, [_P, _P, _SZ, _SZ, _SZ, _P, _P, _P, _SZ, _P, _P, _P, _P, ctypes.c_int, _P,
                                          _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P]),
     "ctox_hip_unregister_tiled_weights": (None, [_P, _P]),

@@ -195,6 +195,25 @@ ctox_status ctox_hip_launch_fused_matvec(ctox_hip_backend *backend, int32_t dtyp
                                          uint32_t columns, uint32_t activation, uint32_t batch,
                                          void *stream);
 
+/* Allocation-free variant of ctox_hip_launch_fused_matvec. NO COUNTERPART
+ * IN THE REFERENCE: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments and results; the weights must have a tiled
+ * copy (ctox_hip_register_tiled_weights, else CTOX_ERR_UNSUPPORTED_OPERATION)
+ * and batch is 1..5. The cross-chunk combine slots come from a static device
+ * array of CTOX_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends),
+ * not from the backend's grown buffer; a matrix whose slots do not fit,
+ * (chunks - 1) * batch * 16 * ceil(rows / 16) * 8 bytes with
+ * chunks = ceil(columns / 1024), fails with CTOX_ERR_MEMORY_BUDGET. The call
+ * allocates nothing. Every call on one GPU shares that GPU's array: calls
+ * that overlap on one GPU (other streams, other threads, other backends)
+ * race and must be ordered by the caller. */
+#define CTOX_NOALLOC_SCRATCH_BYTES (8u << 20)
+ctox_status ctox_hip_launch_fused_matvec_noalloc(ctox_hip_backend *backend, int32_t dtype, const void *d_weights,
+                                                 const float *d_input, const uint16_t *d_s_in,
+                                                 const uint16_t *d_s_out, const float *d_bias, float *d_output,
+                                                 uint32_t rows, uint32_t columns, uint32_t activation,
+                                                 uint32_t batch, void *stream);
 /* Registers a tiled copy of raw packed weights already on the device
  * (pure Q2_B64 / Q4_B64, `rows` x `columns`, the crate's row layout at
  * d_weights). Batch-1 launches of the raw device entry points
