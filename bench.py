@@ -206,6 +206,11 @@ def bench_gdn(torch, hip, steps):
     return out
 
 
+def ctox_lib():
+    import ctox_hip
+    return ctox_hip.load_library()
+
+
 def bench_token_selection(torch, hip, steps):
     """Config 5's per-step token selection: k = 4 drafts, vocab 151936, greedy
     verification and the T = 0.7 rejection-sampling accept."""
@@ -223,7 +228,9 @@ def bench_token_selection(torch, hip, steps):
                           draft.data_ptr(), target.data_ptr(), bonus.data_ptr(), K, V, out.data_ptr(), s)),
                      ("mtp_accept_t0.7_k4", lambda: hip.mtp_accept_device(
                           draft.data_ptr(), target.data_ptr(), bonus.data_ptr(), toks.data_ptr(), K, V, 0.7,
-                          rng.data_ptr(), out.data_ptr(), s))):
+                          rng.data_ptr(), out.data_ptr(), s)),
+                     ("sample_topk40_topp0.95_t0.8", lambda: ctox_lib().ctox_hip_sample_topk_topp_device(
+                          hip.handle, bonus.data_ptr(), V, 0.8, 40, 0.95, 0.37, out.data_ptr(), s))):
         fn()
         with Timer(torch) as t:
             for _ in range(steps):

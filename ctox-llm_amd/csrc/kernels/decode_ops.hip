@@ -382,3 +382,128 @@ extern "C" __global__ __launch_bounds__(1024) void ctox_pick_final_gfx950(Accept
         a.out[1] = st.accepted;
     }
 }
+
+// ---------------------------------------------------------------------------
+// Top-k / top-p sampling with a caller-supplied draw: Sampler::sample_with_draw
+// (Q/src/sampler.rs:65-144) for 1 <= top_k <= 256, the bound of the CUDA
+// runtime's sampler (Q/kernels/cuda/q2q4_fused_matvec_sm86.cu:2647-2776).
+// Candidates are ordered by scaled logit, then by token, both descending
+// (the crate's sort: ties go to the later token); a candidate is the 64-bit
+// key (order-preserving bits of the scaled logit << 32) | token, so one
+// integer comparison orders them. Stage 1 (one workgroup per 4096 logits)
+// sorts its part's keys in LDS (bitonic, descending) and keeps the first
+// top_k; stage 2 sorts the parts' candidates and one thread runs the crate's
+// sequential arithmetic over the top_k: exp weights, the nucleus cut at
+// top_p of their sum, and the cumulative search of draw x the nucleus total.
+// out = {token, status, nucleus length, nucleus total bits}; status 0 is
+// success, 2 a non-finite logit or scaled logit, 4 an invalid normalization.
+__device__ __forceinline__ uint32_t topk_key(float v) {
+    const uint32_t b = __float_as_uint(v);
+    return b ^ ((b & 0x80000000u) ? 0xffffffffu : 0x80000000u);
+}
+__device__ __forceinline__ float topk_value(uint32_t k) {
+    return __uint_as_float(k ^ ((k & 0x80000000u) ? 0x80000000u : 0xffffffffu));
+}
+
+// Descending bitonic sort of n (a power of two) keys in LDS.
+__device__ __forceinline__ void bitonic_desc(uint64_t *sk, uint32_t n) {
+    for (uint32_t k2 = 2; k2 <= n; k2 <<= 1)
+        for (uint32_t j = k2 >> 1; j > 0; j >>= 1) {
+            for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+                const uint32_t ixj = i ^ j;
+                if (ixj > i) {
+                    const uint64_t x = sk[i], y = sk[ixj];
+                    const bool desc = (i & k2) == 0;
+                    if (desc ? x < y : x > y) {
+                        sk[i] = y;
+                        sk[ixj] = x;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+}
+
+extern "C" __global__ __launch_bounds__(1024) void ctox_topk_part_gfx950(TopkArgs a) {
+    __shared__ uint64_t sk[CTOX_TOPK_PART];
+    const uint32_t b0 = blockIdx.x * CTOX_TOPK_PART;
+    const uint32_t n = min((uint32_t)CTOX_TOPK_PART, a.vocab - b0);
+    int bad = 0;
+    for (uint32_t i = threadIdx.x; i < CTOX_TOPK_PART; i += blockDim.x) {
+        uint64_t key = 0;  // below every candidate
+        if (i < n) {
+            const float x = a.logits[b0 + i], v = x * a.inv_temperature;
+            bad |= !__builtin_isfinite(x) | !__builtin_isfinite(v);
+            key = ((uint64_t)topk_key(v) << 32) | (b0 + i);
+        }
+        sk[i] = key;
+    }
+    bad = __syncthreads_or(bad);
+    bitonic_desc(sk, CTOX_TOPK_PART);
+    for (uint32_t r = threadIdx.x; r < a.top_k; r += blockDim.x) a.cand[(size_t)blockIdx.x * a.top_k + r] = sk[r];
+    if (threadIdx.x == 0) a.flags[blockIdx.x] = bad ? 1u : 0u;
+}
+
+extern "C" __global__ __launch_bounds__(1024) void ctox_topk_final_gfx950(TopkArgs a) {
+    __shared__ uint64_t sk[CTOX_TOPK_CANDS];  // parts * top_k <= CTOX_TOPK_CANDS (host-checked)
+    __shared__ float w[CTOX_TOPK_MAX];
+    const uint32_t n = a.parts * a.top_k;
+    uint32_t n2 = 1;
+    while (n2 < n) n2 <<= 1;
+    int bad = 0;
+    for (uint32_t i = threadIdx.x; i < n2; i += blockDim.x) sk[i] = i < n ? a.cand[i] : 0;
+    for (uint32_t p = threadIdx.x; p < a.parts; p += blockDim.x) bad |= a.flags[p] != 0;
+    bad = __syncthreads_or(bad);
+    if (bad) {
+        if (threadIdx.x == 0) {
+            a.out[0] = 0xffffffffu;
+            a.out[1] = 2;
+            a.out[2] = 0;
+            a.out[3] = 0;
+        }
+        return;
+    }
+    bitonic_desc(sk, n2);
+    if (threadIdx.x != 0) return;
+    // Sampler::sample_with_draw from the sort on, in its order of operations.
+    const uint32_t len = min(a.top_k, a.vocab);
+    const float m = topk_value((uint32_t)(sk[0] >> 32));
+    float norm = 0.0f;
+    for (uint32_t r = 0; r < len; r++) {
+        w[r] = expf(topk_value((uint32_t)(sk[r] >> 32)) - m);
+        norm += w[r];
+    }
+    if (!__builtin_isfinite(norm) || norm <= 0.0f) {
+        a.out[0] = 0xffffffffu;
+        a.out[1] = 4;
+        a.out[2] = 0;
+        a.out[3] = 0;
+        return;
+    }
+    const float cut = a.top_p * norm;
+    float cum = 0.0f;
+    uint32_t nuc = len;
+    for (uint32_t r = 0; r < len; r++) {
+        cum += w[r];
+        if (cum >= cut) {
+            nuc = r + 1;
+            break;
+        }
+    }
+    float total = 0.0f;
+    for (uint32_t r = 0; r < nuc; r++) total += w[r];
+    const float thr = a.draw * total;
+    cum = 0.0f;
+    uint32_t tok = (uint32_t)sk[nuc - 1];
+    for (uint32_t r = 0; r < nuc; r++) {
+        cum += w[r];
+        if (thr <= cum) {
+            tok = (uint32_t)sk[r];
+            break;
+        }
+    }
+    a.out[0] = tok;
+    a.out[1] = 0;
+    a.out[2] = nuc;
+    a.out[3] = __float_as_uint(total);
+}

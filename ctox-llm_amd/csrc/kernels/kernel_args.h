@@ -324,6 +324,23 @@ struct PickState {
     uint32_t mode;           // 0 residual max(0, p - q), 1 bonus softmax, 2 invalid token, 3 non-finite logits
 };
 
+// Top-k / top-p sampling with a host draw (decode_ops.hip).
+#define CTOX_TOPK_PART 4096  // logits per part of the first stage
+#define CTOX_TOPK_MAX 256    // largest top_k
+#define CTOX_TOPK_CANDS 16384  // candidates the second stage sorts (parts * top_k)
+struct TopkArgs {
+    const float *logits;     // [vocab]
+    uint64_t *cand;          // [parts][top_k] (stage 1 out, stage 2 in): (order key << 32) | token
+    uint32_t *flags;         // [parts]: a non-finite logit or scaled logit in the part
+    uint32_t *out;           // [4]: token, status, nucleus length, nucleus total (f32 bits)
+    uint32_t vocab;
+    uint32_t top_k;
+    uint32_t parts;
+    float inv_temperature;
+    float top_p;
+    float draw;
+};
+
 struct VerifyArgs {
     const float *partials;   // PartialArgs mode 0 output
     uint32_t *out;           // [3 + drafts]: next, verified, accepted count, accepted tokens

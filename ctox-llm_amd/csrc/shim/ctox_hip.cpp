@@ -149,7 +149,7 @@ struct ctox_hip_backend {
                   conv = nullptr, rope = nullptr, kv_pack = nullptr, attn_prep = nullptr, kv_demote = nullptr, gqa_part[2] = {}, gqa_part16[2] = {},
                   gqa_combine = nullptr, fill = nullptr, embed = nullptr, norm_rows = nullptr, attn_gate = nullptr,
                   swiglu_rows = nullptr, copy_rows = nullptr, write_words = nullptr, norm_prep = nullptr,
-                  prep_x = nullptr, finite = nullptr, gather = nullptr;
+                  prep_x = nullptr, finite = nullptr, gather = nullptr, topk_part = nullptr, topk_final = nullptr;
     // Batch-1 slice kernels per dtype [Q2, Q4]: [0] walks the slices, [n]
     // requests all n slices up front (n <= 3: more slices up front measured
     // slower than walking them).
@@ -823,7 +823,8 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->tilemx[1][0], "ctox_q4_mv_tilemx2_gfx950"}, {&b->tilemx[1][1], "ctox_q4_mv_tilemx3_gfx950"},
                {&b->tilemx[1][2], "ctox_q4_mv_tilemx4_gfx950"}, {&b->tilemx[1][3], "ctox_q4_mv_tilemx5_gfx950"},
                {&b->repack, "ctox_tile_repack_gfx950"}, {&b->gdn_fused, "ctox_gdn_fused_gfx950"},
-               {&b->finite, "ctox_finite_check_gfx950"}, {&b->gather, "ctox_gather_rows_gfx950"}};
+               {&b->finite, "ctox_finite_check_gfx950"}, {&b->gather, "ctox_gather_rows_gfx950"},
+               {&b->topk_part, "ctox_topk_part_gfx950"}, {&b->topk_final, "ctox_topk_final_gfx950"}};
     for (auto &f : fns) {
         if (le != hipSuccess) break;
         le = hipModuleGetFunction(f.f, b->module, f.name);
@@ -1850,6 +1851,48 @@ extern "C" ctox_status ctox_hip_mtp_accept_device(ctox_hip_backend *b, const flo
         return fail(CTOX_ERR_SHAPE, "null argument");
     return ctox_hip_mtp_accept_restricted_device(b, d_draft, vocab, nullptr, d_target, d_bonus, nullptr, d_tokens,
                                                  drafts, vocab, temperature, d_rng, d_out, stream);
+}
+
+extern "C" ctox_status ctox_hip_sample_topk_topp_device(ctox_hip_backend *b, const float *d_logits, size_t vocab,
+                                                        float temperature, uint32_t top_k, float top_p, float draw,
+                                                        uint32_t *d_out, void *stream) {
+    if (!b || !d_logits || !d_out) return fail(CTOX_ERR_SHAPE, "null argument");
+    // Q/src/sampler.rs:65-78, 84-89 argument checks.
+    if (vocab == 0) return fail(CTOX_ERR_INVALID_ARTIFACT, "sampler logits are empty or non-finite");
+    if (!std::isfinite(draw) || !(draw >= 0.0f && draw < 1.0f))
+        return fail(CTOX_ERR_INVALID_ARTIFACT, "sampler draw must be finite and in [0, 1)");
+    if (!std::isfinite(temperature) || temperature < 0.0f || !std::isfinite(top_p) || !(top_p > 0.0f) || top_p > 1.0f)
+        return fail(CTOX_ERR_INVALID_ARTIFACT, "sampler temperature or top_p is invalid");
+    hipStream_t s = pick_stream(b, stream);
+    if (temperature == 0.0f) {  // greedy: the later token wins ties (sampler.rs:76-82)
+        ctox_status st = ctox_hip_greedy_tokens_device(b, d_logits, 1, vocab, d_out, s);
+        if (st) return st;
+        const uint32_t zeros[3] = {0, 1, 0};
+        return ctox_hip_write_words_device(b, d_out + 1, zeros, 3, s);
+    }
+    const float invt = 1.0f / temperature;
+    if (!std::isfinite(invt)) return fail(CTOX_ERR_INVALID_ARTIFACT, "sampler inverse temperature must be finite");
+    const size_t parts = (vocab + CTOX_TOPK_PART - 1) / CTOX_TOPK_PART;
+    if (top_k == 0 || top_k > CTOX_TOPK_MAX || parts * top_k > CTOX_TOPK_CANDS || vocab > 0xffffffffu)
+        return fail(CTOX_ERR_UNSUPPORTED_OPERATION,
+                    "device sampling takes 1 <= top_k <= %d and parts * top_k <= %d (full-vocabulary top_p is not built)",
+                    CTOX_TOPK_MAX, CTOX_TOPK_CANDS);
+    const size_t flags_off = (parts * top_k * sizeof(uint64_t) + 255) & ~(size_t)255;
+    ctox_status st = ensure(b, b->stats, flags_off + parts * sizeof(uint32_t), false);
+    if (st) return st;
+    TopkArgs a{};
+    a.logits = d_logits;
+    a.cand = (uint64_t *)b->stats.ptr;
+    a.flags = (uint32_t *)((char *)b->stats.ptr + flags_off);
+    a.out = d_out;
+    a.vocab = (uint32_t)vocab;
+    a.top_k = top_k;
+    a.parts = (uint32_t)parts;
+    a.inv_temperature = invt;
+    a.top_p = top_p;
+    a.draw = draw;
+    if ((st = launch(b->topk_part, dim3((unsigned)parts), dim3(1024), s, a, "ctox_topk_part_gfx950"))) return st;
+    return launch(b->topk_final, dim3(1), dim3(1024), s, a, "ctox_topk_final_gfx950");
 }
 
 extern "C" ctox_status ctox_hip_check_finite_device(ctox_hip_backend *b, const float *d_x, size_t n,

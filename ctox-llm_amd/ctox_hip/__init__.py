@@ -241,6 +241,8 @@ SIGNATURES = {
     "ctox_hip_mtp_accept_restricted_device": (_I32, [_P, _P, _SZ, _P, _P, _P, _P, _P, _SZ, _SZ, ctypes.c_float, _P,
                                                      _P, _P]),
     "ctox_hip_check_finite_device": (_I32, [_P, _P, _SZ, _P, _SZ, _P]),
+    "ctox_hip_sample_topk_topp_device": (_I32, [_P, _P, _SZ, ctypes.c_float, _U32, ctypes.c_float, ctypes.c_float, _P,
+                                                _P]),
     "ctox_hip_gather_rows_device": (_I32, [_P, _P, _SZ, _SZ, _P, _SZ, _P, _P]),
     "ctox_hip_gdn_fused_snap_device": (_I32, [_P, _P, _SZ, _SZ, _SZ, _P, _P, _P, _SZ, _SZ, _P, _P, _P, _P, _P, _P,
                                               _SZ, ctypes.c_int, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P]),

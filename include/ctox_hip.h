@@ -446,6 +446,22 @@ ctox_status ctox_hip_mtp_accept_restricted_device(ctox_hip_backend *backend, con
                                                   const uint32_t *d_bonus_ids, const uint32_t *d_tokens,
                                                   size_t drafts, size_t vocab, float temperature, uint64_t *d_rng,
                                                   uint32_t *d_out, void *stream);
+/* Sampler::sample_with_draw, Q/src/sampler.rs:65-144, on device logits
+ * [vocab] with the caller's draw in [0, 1): temperature 0 is greedy (the
+ * later token wins ties); otherwise the top_k scaled logits (ties to the
+ * later token), exp weights from their maximum, the nucleus where the
+ * running weight first reaches top_p of the weights' sum, and the first
+ * nucleus token whose running weight reaches draw x the nucleus total, in
+ * the crate's sequential float arithmetic. As the CUDA runtime's sampler
+ * (Q/kernels/cuda/q2q4_fused_matvec_sm86.cu:2647-2776), 1 <= top_k <= 256
+ * (top_k = 0, the full-vocabulary nucleus, is not built:
+ * CTOX_ERR_UNSUPPORTED_OPERATION), and ceil(vocab / 4096) * top_k <= 16384.
+ * d_out[4] = {token, status, nucleus length, nucleus total (f32 bits)};
+ * status 0 ok, 2 a non-finite logit or scaled logit, 4 an invalid
+ * normalization (the crate's InvalidArtifact cases, reported on the device). */
+ctox_status ctox_hip_sample_topk_topp_device(ctox_hip_backend *backend, const float *d_logits, size_t vocab,
+                                             float temperature, uint32_t top_k, float top_p, float draw,
+                                             uint32_t *d_out, void *stream);
 /* Fail-closed check of a logits buffer (Q/src/backend/cuda_runtime.rs:10627-10632):
  * the n values are split into `parts` (1..1024) contiguous ranges and
  * d_flags[p] = 1 if range p holds a non-finite value, else 0 (every flag is

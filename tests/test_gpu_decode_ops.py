@@ -214,3 +214,85 @@ def test_decode_ops_errors(hip):
                           o.data_ptr())
     torch.cuda.synchronize()
     assert int(o[0]) == -1
+
+
+def _nucleus_boundary_tie(orc, logits, T, k, p, draw, a, b):
+    """True when tokens a and b are neighbours in the crate's candidate order
+    and draw x the nucleus total lies within 2e-6 (relative) of the running
+    weight between them: the f32 sums of two exp implementations may fall
+    on either side (checked in float64)."""
+    v = logits.astype(np.float32) * np.float32(1.0 / T)
+    order = sorted(range(v.size), key=lambda i: (-float(v[i]), -i))[:k]
+    w = np.exp(np.array([v[i] for i in order], np.float64) - float(v[order[0]]))
+    cum = np.cumsum(w)
+    nuc = int(np.searchsorted(cum, p * cum[-1])) + 1
+    thr = draw * cum[min(nuc, len(cum)) - 1]
+    if a not in order or b not in order:
+        return False
+    ia, ib = order.index(a), order.index(b)
+    if abs(ia - ib) != 1:
+        return False
+    return abs(thr - cum[min(ia, ib)]) <= 2e-6 * cum[-1]
+
+
+@pytest.mark.parametrize("case", ["crate_defaults", "ties", "k1", "k256", "p1", "small_vocab", "greedy"])
+def test_sample_topk_topp_matches_oracle(hip, orc, case):
+    """ctox_hip_sample_topk_topp_device against orc.sample_with_draw
+    (Q/src/sampler.rs:65-144) with the same draws: the crate defaults
+    (T = 0.8, k = 40, p = 0.95) at vocab 151936, logits with many exact ties
+    (the later token wins), k = 1 and 256, p = 1, a vocabulary smaller than
+    k, and T = 0 (greedy). Tokens equal the oracle's, except where float64
+    shows the draw on a cumulative boundary."""
+    import ctox_hip
+    lib = ctox_hip.load_library()
+    T, k, p, V = 0.8, 40, 0.95, 151936
+    if case == "k1":
+        k = 1
+    elif case == "k256":
+        k = 256
+    elif case == "p1":
+        p = 1.0
+    elif case == "small_vocab":
+        V, k = 100, 256
+    elif case == "greedy":
+        T = 0.0
+    rng = np.random.default_rng(abs(hash(case)) % 1000)
+    say(f"case topk/topp {case}")
+    out = torch.zeros(4, dtype=torch.int32, device="cuda")
+    boundary = 0
+    for trial in range(24):
+        logits = (rng.standard_normal(V) * 2.5).astype(np.float32)
+        if case == "ties":
+            logits = np.round(logits * 2) / 2  # few distinct values: many exact ties
+        d = torch.from_numpy(logits).cuda()
+        for draw in rng.uniform(0, 1, 3).astype(np.float32):
+            st = lib.ctox_hip_sample_topk_topp_device(hip.handle, d.data_ptr(), V, T, k, p, float(draw),
+                                                      out.data_ptr(), None)
+            assert st == 0, lib.ctox_hip_last_error()
+            torch.cuda.synchronize()
+            got = out.cpu().numpy().view(np.uint32)
+            want = orc.sample_with_draw(logits, T, k, p, float(draw))
+            assert got[1] == 0
+            if int(got[0]) != want:
+                assert T > 0 and _nucleus_boundary_tie(orc, logits, T, k, p, float(draw), int(got[0]), want), \
+                    (case, trial, float(draw), int(got[0]), want)
+                boundary += 1
+    assert boundary <= 1
+
+
+def test_sample_topk_topp_fails_closed(hip):
+    import ctox_hip
+    lib = ctox_hip.load_library()
+    say("case topk/topp errors")
+    logits = np.random.default_rng(0).standard_normal(5000).astype(np.float32)
+    logits[1234] = np.nan
+    d = torch.from_numpy(logits).cuda()
+    out = torch.zeros(4, dtype=torch.int32, device="cuda")
+    assert lib.ctox_hip_sample_topk_topp_device(hip.handle, d.data_ptr(), 5000, 0.8, 40, 0.95, 0.5,
+                                                out.data_ptr(), None) == 0
+    torch.cuda.synchronize()
+    assert out.cpu().numpy().view(np.uint32)[1] == 2
+    for args in ((0.8, 0, 0.95, 0.5), (0.8, 257, 0.95, 0.5)):
+        assert lib.ctox_hip_sample_topk_topp_device(hip.handle, d.data_ptr(), 5000, *args, out.data_ptr(), None) == 5
+    for args in ((0.8, 40, 0.95, 1.0), (0.8, 40, 0.0, 0.5), (-1.0, 40, 0.95, 0.5)):
+        assert lib.ctox_hip_sample_topk_topp_device(hip.handle, d.data_ptr(), 5000, *args, out.data_ptr(), None) == 3
