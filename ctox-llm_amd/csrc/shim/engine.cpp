@@ -32,6 +32,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "ctox_hip.h"
@@ -94,7 +95,13 @@ struct ctox_hip_engine {
     ctox_engine_config c{};
     hipStream_t s = nullptr;
     std::vector<void *> allocs;
-    std::vector<const void *> tiled;  // weights with a registered tiled copy
+    struct Tiled {
+        const void *w;
+        int32_t dtype;
+        uint32_t rows, cols;
+    };
+    std::vector<Tiled> tiled;  // weights with a registered tiled copy
+    bool loading = false;      // tensors written since the last finish_load
     std::vector<Layer> layers;
     Mat embed, lm_head;
     float *final_norm = nullptr;
@@ -139,6 +146,9 @@ struct ctox_hip_engine {
     // sum of squares); valid until that norm consumes them.
     float *rsq = nullptr;
     const float *rsq_delta = nullptr, *rsq_hid = nullptr;
+    // Matrix dtypes by engine name (ctox_hip_engine_create_with_dtypes); the
+    // default plan is Q4 projections and Q2 down projections.
+    std::unordered_map<std::string, int32_t> dtype_plan;
     uint32_t position = 0;   // tokens processed by the target model
     uint32_t mtp_tokens = 0; // entries in the MTP cache
     bool have_prev = false;  // prev_hidden holds the last target final hidden
@@ -179,8 +189,10 @@ ctox_status fill(ctox_hip_engine *e, void *p, uint64_t n, uint32_t kind, uint64_
 }
 
 // A quantized matrix with fp16 s_in / s_out in U(0.75, 1.25) and block scales |N(0, 0.02)|.
-ctox_status make_mat(ctox_hip_engine *e, Mat &m, int32_t dtype, uint32_t rows, uint32_t cols, uint64_t &seed,
-                     uint16_t *shared_s_in = nullptr, bool projection = true) {
+ctox_status make_mat(ctox_hip_engine *e, const std::string &name, Mat &m, int32_t dtype, uint32_t rows, uint32_t cols,
+                     uint64_t &seed, uint16_t *shared_s_in = nullptr, bool projection = true) {
+    auto planned = e->dtype_plan.find(name);
+    if (planned != e->dtype_plan.end()) dtype = planned->second;
     m.dtype = dtype;
     m.rows = rows;
     m.cols = cols;
@@ -198,7 +210,7 @@ ctox_status make_mat(ctox_hip_engine *e, Mat &m, int32_t dtype, uint32_t rows, u
         // Batch-1 projections stream the tiled copy; the crate-layout rows stay
         // for the small-M verify kernels.
         TRY(ctox_hip_register_tiled_weights(e->b, dtype, m.w, rows, cols, e->s));
-        e->tiled.push_back(m.w);
+        e->tiled.push_back({m.w, dtype, rows, cols});
     }
     return CTOX_OK;
 }
@@ -383,20 +395,20 @@ ctox_paged_gqa_params gqa_params(ctox_hip_engine *e, const Cache &c) {
 }
 
 // ---- layers ----
-ctox_status make_attn(ctox_hip_engine *e, AttnLayer &a, uint64_t &seed) {
+ctox_status make_attn(ctox_hip_engine *e, const std::string &prefix, AttnLayer &a, uint64_t &seed) {
     const uint32_t H = e->H, qh = e->c.num_attention_heads, hd = e->c.head_dim;
     TRY(make_vec(e, &a.norm, H, seed, 0.0f, 0.1f));
-    TRY(make_mat(e, a.qkv, CTOX_DTYPE_Q4B64, e->Rq, H, seed));
+    TRY(make_mat(e, prefix + ".qkv", a.qkv, CTOX_DTYPE_Q4B64, e->Rq, H, seed));
     TRY(make_vec(e, &a.q_norm, hd, seed, 0.0f, 0.1f));
     TRY(make_vec(e, &a.k_norm, hd, seed, 0.0f, 0.1f));
-    TRY(make_mat(e, a.o, CTOX_DTYPE_Q4B64, H, qh * hd, seed));
+    TRY(make_mat(e, prefix + ".o", a.o, CTOX_DTYPE_Q4B64, H, qh * hd, seed));
     return cache_init(e, a.cache);
 }
 
-ctox_status make_mlp(ctox_hip_engine *e, Mlp &m, uint64_t &seed) {
+ctox_status make_mlp(ctox_hip_engine *e, const std::string &prefix, Mlp &m, uint64_t &seed) {
     TRY(make_vec(e, &m.norm, e->H, seed, 0.0f, 0.1f));
-    TRY(make_mat(e, m.gate_up, CTOX_DTYPE_Q4B64, 2 * e->I, e->H, seed));
-    return make_mat(e, m.down, CTOX_DTYPE_Q2B64, e->H, e->I, seed);
+    TRY(make_mat(e, prefix + ".gate_up", m.gate_up, CTOX_DTYPE_Q4B64, 2 * e->I, e->H, seed));
+    return make_mat(e, prefix + ".down", m.down, CTOX_DTYPE_Q2B64, e->H, e->I, seed);
 }
 
 // Full-attention token mixer over R rows at rope positions rope0.. (the
@@ -559,7 +571,16 @@ ctox_status copy_d2d(ctox_hip_engine *e, void *dst, const void *src, size_t byte
 
 extern "C" ctox_status ctox_hip_engine_create(ctox_hip_backend *b, const ctox_engine_config *cfg, uint64_t seed,
                                               ctox_hip_engine **out) {
-    if (!b || !cfg || !out) return efail(CTOX_ERR_SHAPE, "null argument");
+    return ctox_hip_engine_create_with_dtypes(b, cfg, seed, nullptr, 0, out);
+}
+
+extern "C" ctox_status ctox_hip_engine_create_with_dtypes(ctox_hip_backend *b, const ctox_engine_config *cfg,
+                                                          uint64_t seed, const ctox_engine_matrix_dtype *plan,
+                                                          size_t plan_len, ctox_hip_engine **out) {
+    if (!b || !cfg || !out || (!plan && plan_len)) return efail(CTOX_ERR_SHAPE, "null argument");
+    for (size_t i = 0; i < plan_len; i++)
+        if (!plan[i].name || (plan[i].dtype != CTOX_DTYPE_Q2B64 && plan[i].dtype != CTOX_DTYPE_Q4B64))
+            return efail(CTOX_ERR_UNSUPPORTED_DTYPE, "an engine matrix is pure Q2_B64 or Q4_B64");
     *out = nullptr;
     const ctox_engine_config &c = *cfg;
     // Q/src/config.rs:35-73 geometry; the attention kernel needs head_dim 256.
@@ -581,6 +602,7 @@ extern "C" ctox_status ctox_hip_engine_create(ctox_hip_backend *b, const ctox_en
     ctox_hip_engine *e = new ctox_hip_engine();
     e->b = b;
     e->c = c;
+    for (size_t i = 0; i < plan_len; i++) e->dtype_plan[plan[i].name] = plan[i].dtype;
     e->mtp = c.mtp_layers > 0 && c.draft_tokens > 0;
     e->R = e->mtp ? c.draft_tokens + 1 : 1;
     e->H = c.hidden_size;
@@ -603,8 +625,8 @@ extern "C" ctox_status ctox_hip_engine_create(ctox_hip_backend *b, const ctox_en
     if (hipStreamCreate(&e->s) != hipSuccess) return cleanup(efail(CTOX_ERR_INVALID_STATE, "stream creation failed"));
     ctox_status st;
     uint64_t sd = seed * 1000003ull + 17;
-    if ((st = make_mat(e, e->embed, CTOX_DTYPE_Q4B64, e->V, e->H, sd, nullptr, false))) return cleanup(st);
-    if ((st = make_mat(e, e->lm_head, CTOX_DTYPE_Q4B64, e->V, e->H, sd))) return cleanup(st);
+    if ((st = make_mat(e, "embed", e->embed, CTOX_DTYPE_Q4B64, e->V, e->H, sd, nullptr, false))) return cleanup(st);
+    if ((st = make_mat(e, "lm_head", e->lm_head, CTOX_DTYPE_Q4B64, e->V, e->H, sd))) return cleanup(st);
     if ((st = make_vec(e, &e->final_norm, e->H, sd, 0.0f, 0.1f))) return cleanup(st);
     uint32_t n_gdn = 0;
     for (uint32_t l = 0; l < c.num_hidden_layers; l++) n_gdn += ((l + 1) % c.full_attention_interval) != 0;
@@ -626,28 +648,30 @@ extern "C" ctox_status ctox_hip_engine_create(ctox_hip_backend *b, const ctox_en
         Layer &L = e->layers[l];
         L.full = ((l + 1) % c.full_attention_interval) == 0;  // config.rs:61-72
         if (L.full) {
-            if ((st = make_attn(e, L.f, sd))) return cleanup(st);
+            if ((st = make_attn(e, "L" + std::to_string(l), L.f, sd))) return cleanup(st);
         } else {
             GdnLayer &g = L.g;
             if ((st = make_vec(e, &g.norm, e->H, sd, 0.0f, 0.1f))) return cleanup(st);
-            if ((st = make_mat(e, g.in, CTOX_DTYPE_Q4B64, e->Rin, e->H, sd))) return cleanup(st);
+            if ((st = make_mat(e, "L" + std::to_string(l) + ".in", g.in, CTOX_DTYPE_Q4B64, e->Rin, e->H, sd)))
+                return cleanup(st);
             if ((st = make_vec(e, &g.conv_w, (size_t)e->C * c.linear_conv_kernel_dim, sd, 0.0f, 0.5f))) return cleanup(st);
             if ((st = dalloc_t(e, &g.a_log, Hv)) || (st = fill(e, g.a_log, Hv, 4, sd++, -2.0f, 1.0f))) return cleanup(st);
             if ((st = dalloc_t(e, &g.dt_bias, Hv)) || (st = fill(e, g.dt_bias, Hv, 4, sd++, -1.0f, 1.0f))) return cleanup(st);
             if ((st = make_vec(e, &g.gnorm, c.linear_value_head_dim, sd, 1.0f, 0.1f))) return cleanup(st);
-            if ((st = make_mat(e, g.out, CTOX_DTYPE_Q4B64, e->H, e->Vw, sd))) return cleanup(st);
+            if ((st = make_mat(e, "L" + std::to_string(l) + ".out", g.out, CTOX_DTYPE_Q4B64, e->H, e->Vw, sd)))
+                return cleanup(st);
             g.state_off = (size_t)gi * Hv * head_floats;
             g.conv_off = (size_t)gi * e->C * c.linear_conv_kernel_dim;
             gi++;
         }
-        if ((st = make_mlp(e, L.mlp, sd))) return cleanup(st);
+        if ((st = make_mlp(e, "L" + std::to_string(l), L.mlp, sd))) return cleanup(st);
     }
     if (e->mtp) {
         if ((st = make_vec(e, &e->mtp_norm_emb, e->H, sd, 0.0f, 0.1f)) ||
             (st = make_vec(e, &e->mtp_norm_hid, e->H, sd, 0.0f, 0.1f)) ||
             (st = make_vec(e, &e->mtp_norm, e->H, sd, 0.0f, 0.1f)) ||
-            (st = make_mat(e, e->mtp_fc, CTOX_DTYPE_Q4B64, e->H, 2 * e->H, sd)) ||
-            (st = make_attn(e, e->mtp_attn, sd)) || (st = make_mlp(e, e->mtp_mlp, sd)))
+            (st = make_mat(e, "mtp.fc", e->mtp_fc, CTOX_DTYPE_Q4B64, e->H, 2 * e->H, sd)) ||
+            (st = make_attn(e, "mtp", e->mtp_attn, sd)) || (st = make_mlp(e, "mtp", e->mtp_mlp, sd)))
             return cleanup(st);
     }
     const size_t R = e->R, qh = c.num_attention_heads, hd = c.head_dim;
@@ -679,7 +703,7 @@ extern "C" ctox_status ctox_hip_engine_create(ctox_hip_backend *b, const ctox_en
 extern "C" void ctox_hip_engine_destroy(ctox_hip_engine *e) {
     if (!e) return;
     if (e->s) hipStreamSynchronize(e->s);
-    for (const void *p : e->tiled) ctox_hip_unregister_tiled_weights(e->b, p);
+    for (const auto &t : e->tiled) ctox_hip_unregister_tiled_weights(e->b, t.w);
     for (void *p : e->allocs) hipFree(p);
     if (e->h_flags) hipHostFree(e->h_flags);
     if (e->s) hipStreamDestroy(e->s);
@@ -699,6 +723,7 @@ extern "C" ctox_status ctox_hip_engine_set_rng(ctox_hip_engine *e, uint64_t stat
 // logits of the next position in the engine's logits buffer; *d_logits points there.
 extern "C" ctox_status ctox_hip_engine_decode(ctox_hip_engine *e, uint32_t token, const float **d_logits) {
     if (!e) return efail(CTOX_ERR_SHAPE, "null argument");
+    if (e->loading) return efail(CTOX_ERR_INVALID_STATE, "weights written without ctox_hip_engine_finish_load");
     if (token >= e->V) return efail(CTOX_ERR_SHAPE, "token outside the vocabulary");
     if (e->position >= e->c.max_tokens) return efail(CTOX_ERR_MEMORY_BUDGET, "context is full");
     TRY(ctox_hip_write_words_device(e->b, e->d_tokens, &token, 1, e->s));
@@ -729,6 +754,7 @@ extern "C" ctox_status ctox_hip_engine_mtp_step(ctox_hip_engine *e, uint32_t tok
                                                 uint32_t *out) {
     if (!e || !out) return efail(CTOX_ERR_SHAPE, "null argument");
     if (!e->mtp) return efail(CTOX_ERR_UNSUPPORTED_OPERATION, "engine was created without an MTP head");
+    if (e->loading) return efail(CTOX_ERR_INVALID_STATE, "weights written without ctox_hip_engine_finish_load");
     if (!e->have_prev) return efail(CTOX_ERR_INVALID_STATE, "MTP step needs a previous target step");
     if (token >= e->V) return efail(CTOX_ERR_SHAPE, "token outside the vocabulary");
     const uint32_t k = e->c.draft_tokens, R = k + 1, p = e->position;
@@ -790,6 +816,7 @@ extern "C" ctox_status ctox_hip_engine_mtp_step(ctox_hip_engine *e, uint32_t tok
 // filled with random K/V".
 extern "C" ctox_status ctox_hip_engine_fill_context(ctox_hip_engine *e, uint32_t tokens, uint64_t seed) {
     if (!e) return efail(CTOX_ERR_SHAPE, "null argument");
+    if (e->loading) return efail(CTOX_ERR_INVALID_STATE, "weights written without ctox_hip_engine_finish_load");
     if (e->position != 0 || tokens == 0 || tokens + e->R > e->c.max_tokens)
         return efail(CTOX_ERR_SHAPE, "context fill needs an empty engine and room for a step");
     const uint32_t chunk = 1024;
@@ -872,7 +899,7 @@ extern "C" ctox_status ctox_hip_engine_set_draft_vocab(ctox_hip_engine *e, const
     TRY(ctox_hip_gather_rows_device(e->b, e->lm_head.w, e->lm_head.rows, rb, ids, n, m.w, e->s));
     TRY(ctox_hip_gather_rows_device(e->b, e->lm_head.s_out, e->lm_head.rows, 2, ids, n, m.s_out, e->s));
     TRY(ctox_hip_register_tiled_weights(e->b, m.dtype, m.w, m.rows, m.cols, e->s));
-    e->tiled.push_back(m.w);
+    e->tiled.push_back({m.w, m.dtype, m.rows, m.cols});
     std::vector<uint32_t> inv(e->V, 0xffffffffu);
     for (size_t i = 0; i < n; i++) inv[ids[i]] = (uint32_t)i;
     TRY(dalloc_t(e, &e->d_draft_ids, n));
@@ -986,5 +1013,44 @@ extern "C" ctox_status ctox_hip_engine_cache(ctox_hip_engine *e, uint32_t layer,
     v->d_q2_pool = c->q2;
     v->q4_page_bytes = e->q4_page_bytes;
     v->q2_page_bytes = e->q2_page_bytes;
+    return CTOX_OK;
+}
+
+extern "C" ctox_status ctox_hip_engine_write(ctox_hip_engine *e, const char *name, uint32_t part, size_t offset,
+                                             const void *host, size_t bytes) {
+    if (!e || !name || (!host && bytes)) return efail(CTOX_ERR_SHAPE, "null argument");
+    if (e->position || e->draft_n || e->have_prev)
+        return efail(CTOX_ERR_INVALID_STATE, "weights are written into a fresh engine, before the draft vocabulary");
+    ctox_engine_tensor t;
+    TRY(ctox_hip_engine_tensor(e, name, &t));
+    void *dst = nullptr;
+    size_t cap = 0;
+    if (part == CTOX_ENGINE_PART_DATA) {
+        dst = t.data;
+        cap = t.bytes;
+    } else if (t.dtype < 0) {
+        return efail(CTOX_ERR_SHAPE, "tensor %s is a vector without scales", name);
+    } else if (part == CTOX_ENGINE_PART_S_IN) {
+        dst = (void *)t.s_in;
+        cap = (size_t)t.cols * 2;
+    } else if (part == CTOX_ENGINE_PART_S_OUT) {
+        dst = (void *)t.s_out;
+        cap = (size_t)t.rows * 2;
+    } else {
+        return efail(CTOX_ERR_SHAPE, "unknown tensor part %u", part);
+    }
+    if (offset > cap || bytes > cap - offset)
+        return efail(CTOX_ERR_SHAPE, "write of %zu bytes at %zu exceeds %s (%zu bytes)", bytes, offset, name, cap);
+    e->loading = true;
+    if (bytes && hipMemcpyAsync((uint8_t *)dst + offset, host, bytes, hipMemcpyHostToDevice, e->s) != hipSuccess)
+        return efail(CTOX_ERR_INVALID_STATE, "weight upload failed");
+    return sync(e);
+}
+
+extern "C" ctox_status ctox_hip_engine_finish_load(ctox_hip_engine *e) {
+    if (!e) return efail(CTOX_ERR_SHAPE, "null argument");
+    for (const auto &t : e->tiled) TRY(ctox_hip_register_tiled_weights(e->b, t.dtype, t.w, t.rows, t.cols, e->s));
+    TRY(sync(e));
+    e->loading = false;
     return CTOX_OK;
 }

@@ -142,6 +142,21 @@ class Engine:
             out.append((int(prec), int(tokens), int(first), _d2h(pool + int(slot) * pb, int(tokens) * tb).tobytes()))
         return out
 
+    def write(self, name: str, part: int, offset: int, data) -> None:
+        """Copies host bytes into part `part` (0 data, 1 s_in, 2 s_out) of a
+        named tensor at byte `offset`; steps wait for finish_load."""
+        buf = np.ascontiguousarray(data if isinstance(data, np.ndarray) else np.frombuffer(data, np.uint8))
+        _check(_lib().ctox_hip_engine_write(self.handle, name.encode(), part, offset, buf.ctypes.data, buf.nbytes))
+
+    def finish_load(self) -> None:
+        _check(_lib().ctox_hip_engine_finish_load(self.handle))
+
+    def tensor_info(self, name: str) -> dict:
+        """Geometry of one weight without copying it: rows, cols, dtype (-1: f32 vector)."""
+        t = EngineTensor()
+        _check(_lib().ctox_hip_engine_tensor(self.handle, name.encode(), ctypes.byref(t)))
+        return {"rows": t.rows, "cols": t.cols, "dtype": t.dtype, "bytes": t.bytes}
+
     def tensor(self, name: str) -> dict:
         """Host copy of one weight: quantized matrices as raw blocks plus fp16
         s_in / s_out bytes, vectors as float32."""

@@ -655,6 +655,36 @@ typedef struct ctox_hip_engine ctox_hip_engine;
 
 ctox_status ctox_hip_engine_create(ctox_hip_backend *backend, const ctox_engine_config *config, uint64_t seed,
                                    ctox_hip_engine **out);
+
+/* Loading a `.ctoxq` model artifact into the engine (CpuCorrectnessExecutor::load,
+ * Q/src/decoder.rs:1149-1182, over the tensor contract of
+ * Q/src/tensor_contract.rs:137-244). The engine's matrices are the crate's
+ * fan-out groups concatenated by rows ("L<i>.in" = in_proj_qkv|z|a|b,
+ * "L<i>.qkv" = q|k|v, "L<i>.gate_up" = gate|up), one packed dtype each:
+ * create with the dtype plan of the artifact (names as ctox_hip_engine_tensor;
+ * unnamed matrices keep the default plan: Q4_B64, down projections Q2_B64),
+ * write every tensor, then finish. A mixed or mixed-member matrix is created
+ * Q4_B64 and its Q2 rows are written widened (Q2 code c -> Q4 code 5c, the
+ * same block scale: value-exact, Q/src/quant.rs codebooks). */
+typedef struct {
+    const char *name;
+    int32_t dtype;            /* CTOX_DTYPE_Q2B64 or CTOX_DTYPE_Q4B64 */
+} ctox_engine_matrix_dtype;
+ctox_status ctox_hip_engine_create_with_dtypes(ctox_hip_backend *backend, const ctox_engine_config *config,
+                                               uint64_t seed, const ctox_engine_matrix_dtype *plan, size_t plan_len,
+                                               ctox_hip_engine **out);
+/* Parts of a named tensor. */
+#define CTOX_ENGINE_PART_DATA 0   /* packed rows of a matrix, or the f32 values of a vector */
+#define CTOX_ENGINE_PART_S_IN 1   /* fp16 s_in of a matrix */
+#define CTOX_ENGINE_PART_S_OUT 2  /* fp16 s_out of a matrix */
+/* Copies `bytes` host bytes into part `part` of tensor `name` at byte offset
+ * `offset` (an engine at position 0 with no draft vocabulary bound, else
+ * CTOX_ERR_INVALID_STATE; out of range: CTOX_ERR_SHAPE). Steps are refused
+ * until ctox_hip_engine_finish_load. */
+ctox_status ctox_hip_engine_write(ctox_hip_engine *engine, const char *name, uint32_t part, size_t offset,
+                                  const void *host, size_t bytes);
+/* Rebuilds the tiled copies of every written matrix; steps are allowed again. */
+ctox_status ctox_hip_engine_finish_load(ctox_hip_engine *engine);
 void ctox_hip_engine_destroy(ctox_hip_engine *engine);
 void *ctox_hip_engine_stream(ctox_hip_engine *engine);
 /* Pcg32 state of the sampler (Q/src/sampler.rs:149-174). */

@@ -96,7 +96,19 @@ class OracleDecoder:
     def matvec(self, name, x):
         m = self.w(name)
         return orc.MatVec(m["dtype"], m["data"], m["rows"], m["cols"], x, s_in=("f16le", m["s_in"]),
-                          s_out=("f16le", m["s_out"])).run(threads=self.threads)
+                          s_out=("f16le", m["s_out"]), segments=m.get("segments", ())).run(threads=self.threads)
+
+    @staticmethod
+    def _row(m, r):
+        """(dtype, packed bytes) of row r; a mixed matrix resolves the row's
+        segment (loader.rs:54-127)."""
+        dtype, base, local = m["dtype"], 0, r
+        for g, start, end, d, off, _ in m.get("segments", ()):
+            if start <= r < end:
+                dtype, base, local = d, off, r - start
+                break
+        rb = m["cols"] // 64 * (34 if dtype == orc.Q4B64 else 18)
+        return dtype, bytes(m["data"][base + local * rb:base + (local + 1) * rb])
 
     def load_context(self, pages_of, position, prev_hidden):
         """Starts from a filled context: every full-attention cache (and the
@@ -121,10 +133,9 @@ class OracleDecoder:
         m = self.w("embed")
         if not 0 <= token < m["rows"]:
             raise orc.OracleError(1)
-        rb = m["cols"] // 64 * (34 if m["dtype"] == orc.Q4B64 else 18)
         s_out = float(np.frombuffer(m["s_out"].tobytes(), np.float16)[token])
-        return orc.recovered_row(m["dtype"], m["data"][token * rb:(token + 1) * rb], m["cols"],
-                                 ("f16le", m["s_in"]), s_out)
+        dtype, row = self._row(m, token)
+        return orc.recovered_row(dtype, row, m["cols"], ("f16le", m["s_in"]), s_out)
 
     # -- mixers ---------------------------------------------------------------
     def attention(self, prefix, x, rope_pos, cache, retain):
@@ -185,9 +196,8 @@ class OracleDecoder:
         s_in = np.frombuffer(m["s_in"].tobytes(), np.float16).astype(np.float32)
         s_out = np.frombuffer(m["s_out"].tobytes(), np.float16).astype(np.float32)
         x = (np.asarray(fin, np.float32) * s_in).astype(np.float32)
-        rb = m["cols"] // 64 * (34 if m["dtype"] == orc.Q4B64 else 18)
-        return np.array([orc.recovered_row_matvec(m["dtype"], m["data"][int(t) * rb:(int(t) + 1) * rb], x,
-                                                  float(s_out[t])) for t in ids], np.float32)
+        return np.array([orc.recovered_row_matvec(*self._row(m, int(t)), x, float(s_out[t])) for t in ids],
+                        np.float32)
 
     def attention_residual(self, prefix, h, position, cache):
         """full_attention_residual (Q/src/decoder.rs:676-800): the position
@@ -259,3 +269,102 @@ class OracleDecoder:
         self.prev_hidden = hiddens[n]
         self._demote_all()
         return nxt, xs[1:n + 1], {"draft_logits": draft_logits, "target_logits": target, "drafts": xs[1:]}
+
+
+# ---------------------------------------------------------------- artifacts
+class ArtifactTensors:
+    """Tensor provider of OracleDecoder over a `.ctoxq` file written with the
+    crate's tensor names (Q/src/tensor_contract.rs:137-244).
+
+    Reads the file independently of the product's loader: the 64-byte header
+    (Q/src/format.rs:394-450), the JSON manifest, tensor payloads at
+    data_offset + offset. An engine name resolves to the crate tensors the
+    crate's decoder reads for it (decoder.rs:687-725 q/k/v fan-out, 806-860
+    in_proj_qkv/z/a/b, 636-655 gate/up, 1009-1046 the MTP head), rows
+    concatenated in that order; members of any dtype keep their own rows, so
+    a fused matrix of several dtypes is a mixed matrix with one segment per
+    member run (the crate's fan-out computes the same rows member by member)."""
+
+    DT = {"q2_b64": orc.Q2B64, "q4_b64": orc.Q4B64, "mixed_q2_q4_b64": orc.MIXED, "f16": 3, "f32": 4}
+
+    def __init__(self, path, cfg):
+        import json
+        import struct
+        with open(path, "rb") as f:
+            self.raw = f.read()
+        if self.raw[:8] != b"CTOXQ2Q4":
+            raise orc.OracleError(3)
+        _, _, mlen, self.data_offset, _, _ = struct.unpack_from("<IIQQII", self.raw, 8)
+        man = json.loads(self.raw[64:64 + mlen])
+        self.entries = {t["name"]: t for t in man["tensors"]}
+        self.c = cfg
+
+    def _payload(self, e):
+        start = self.data_offset + e["offset"]
+        return self.raw[start:start + e["length"]]
+
+    def _runs(self, name):
+        e = self.entries[name]
+        d = self.DT[e["dtype"]]
+        if d != orc.MIXED:
+            return [(d, e["shape"][0], self._payload(e))]
+        p = self._payload(e)
+        return [(self.DT[s["dtype"]], s["row_end"] - s["row_start"], p[s["offset"]:s["offset"] + s["length"]])
+                for s in e["segments"]]
+
+    def _f32(self, name):
+        e = self.entries[name]
+        dt = np.float16 if e["dtype"] == "f16" else np.float32
+        return np.frombuffer(self._payload(e), dt).astype(np.float32)
+
+    def members(self, name):
+        c = self.c
+        if name == "embed":
+            return ["model.language_model.embed_tokens.weight"]
+        if name == "lm_head":
+            return ["lm_head.weight"]
+        if name == "final_norm":
+            return ["model.language_model.norm.weight"]
+        if name.startswith("mtp."):
+            part, layer, top = name[4:], "mtp.layers.0", {"fc": "mtp.fc.weight", "norm": "mtp.norm.weight",
+                                                         "norm_emb": "mtp.pre_fc_norm_embedding.weight",
+                                                         "norm_hid": "mtp.pre_fc_norm_hidden.weight"}
+            if part in top:
+                return [top[part]]
+            if part == "attn_norm":
+                part = "norm"
+        else:
+            l, part = name[1:].split(".", 1)
+            layer = f"model.language_model.layers.{int(l)}"
+        a, g, m = f"{layer}.self_attn", f"{layer}.linear_attn", f"{layer}.mlp"
+        return {"norm": [f"{layer}.input_layernorm.weight"], "mlp_norm": [f"{layer}.post_attention_layernorm.weight"],
+                "gate_up": [f"{m}.gate_proj.weight", f"{m}.up_proj.weight"], "down": [f"{m}.down_proj.weight"],
+                "qkv": [f"{a}.q_proj.weight", f"{a}.k_proj.weight", f"{a}.v_proj.weight"],
+                "o": [f"{a}.o_proj.weight"], "q_norm": [f"{a}.q_norm.weight"], "k_norm": [f"{a}.k_norm.weight"],
+                "in": [f"{g}.in_proj_qkv.weight", f"{g}.in_proj_z.weight", f"{g}.in_proj_a.weight",
+                       f"{g}.in_proj_b.weight"],
+                "out": [f"{g}.out_proj.weight"], "conv_w": [f"{g}.conv1d.weight"], "a_log": [f"{g}.A_log"],
+                "dt_bias": [f"{g}.dt_bias"], "gnorm": [f"{g}.norm.weight"]}[part]
+
+    def __call__(self, name):
+        members = self.members(name)
+        first = self.entries[members[0]]
+        if first["dtype"] in ("f16", "f32"):
+            return {"kind": "f32", "data": self._f32(members[0])}
+        runs = [r for m in members for r in self._runs(m)]
+        cols = first["shape"][1]
+        data, segs, row, off = [], [], 0, 0
+        for i, (d, rows, p) in enumerate(runs):
+            segs.append((i, row, row + rows, d, off, len(p)))
+            data.append(p)
+            row, off = row + rows, off + len(p)
+        s_in = np.frombuffer(self._payload(self.entries[members[0] + ".s_in"]), np.uint8)
+        if any(self._payload(self.entries[m + ".s_in"]) != s_in.tobytes() for m in members[1:]):
+            raise orc.OracleError(3)  # fan-out members share one s_in (fanout.rs:77-120)
+        s_out = np.frombuffer(b"".join(self._payload(self.entries[m + ".s_out"]) for m in members), np.uint8)
+        t = {"kind": "quant", "rows": row, "cols": cols, "data": b"".join(data), "s_in": s_in, "s_out": s_out}
+        if len({d for d, _, _ in runs}) == 1:
+            t["dtype"] = runs[0][0]
+        else:
+            t["dtype"], t["segments"] = orc.MIXED, segs
+        return t
