@@ -14,10 +14,13 @@
 // keeps rows i = ig + 16r of column jj in registers, so one token reads and
 // writes each state element exactly once; the token-serial scan keeps the
 // slice register-resident across all tokens. Column reductions over i go
-// through LDS.
+// through LDS. The workgroup barriers order LDS only (lds_barrier): a
+// __syncthreads would also wait for every global store issued before it
+// (the gate and output stores), which costs a memory round trip per barrier.
 #include <hip/hip_runtime.h>
 
 #include "kernel_args.h"
+#include "lds_barrier.h"
 
 #define GDN_COLS 16
 #define GDN_GROUPS 16
@@ -75,7 +78,7 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_scan_gfx950(GdnArgs a
             red_nrm[0][ig] = sk;
             red_nrm[1][ig] = sq;
         }
-        __syncthreads();
+        lds_barrier();
         float memj = 0.0f, ssk = 0.0f, ssq = 0.0f;
 #pragma unroll
         for (int gi = 0; gi < GDN_GROUPS; gi++) {
@@ -92,7 +95,7 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_scan_gfx950(GdnArgs a
             o += s[r] * qq[r];
         }
         red_out[ig][jj] = o;
-        __syncthreads();
+        lds_barrier();
         if (ig == 0 && colok) {
             float oj = 0.0f;
 #pragma unroll
@@ -102,7 +105,7 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_scan_gfx950(GdnArgs a
         // red_* are rewritten next token only after every thread has passed
         // the second barrier of this token and read red_mem / red_nrm; the
         // reads of red_out happen before the next token's first barrier.
-        __syncthreads();
+        lds_barrier();
     }
 
 #pragma unroll
@@ -126,7 +129,34 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_scan_gfx950(GdnArgs a
 // ctox_gdn_gates_gfx950 (same operation order).
 #define GDN_MAX_KERNEL 8
 #define GDN_PREFETCH 8  // token rows whose inputs are loaded up front
-extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_gfx950(GdnFusedArgs a) {
+// A buffer for branch-free loads: a lane without an element reads at `end`
+// (the buffer's byte size), which the range check turns into a zero without
+// a memory access. The address stays inside the allocation's pages (an
+// offset far past the buffer made every such read pay a translation miss).
+struct GdnBuf {
+    __amdgpu_buffer_rsrc_t r;
+    uint32_t end;
+};
+__device__ __forceinline__ GdnBuf gdn_buf(const float *p, size_t floats) {
+    const uint32_t bytes = p ? (uint32_t)min(floats * 4, (size_t)0x7ffffff0) : 0u;
+    return GdnBuf{__builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, (int)bytes, 0x00020000), bytes};
+}
+__device__ __forceinline__ float gdn_ld(const GdnBuf &b, bool ok, uint32_t off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(b.r, ok ? off : b.end, 0, 0));
+}
+// The k (<= 8) floats at byte offset off (ok) as two 16-byte reads. Entries
+// past k hold the next channel's values: the conv step never reads them.
+__device__ __forceinline__ void gdn_load8(const GdnBuf &b, bool ok, uint32_t off, uint32_t k, float v[GDN_MAX_KERNEL]) {
+    const v4i lo = __builtin_amdgcn_raw_buffer_load_b128(b.r, ok ? off : b.end, 0, 0);
+    const v4i hi = __builtin_amdgcn_raw_buffer_load_b128(b.r, ok && k > 4 ? off + 16 : b.end, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        v[i] = __int_as_float(lo[i]);
+        v[4 + i] = __int_as_float(hi[i]);
+    }
+}
+template <bool BLOCKED>
+__device__ __forceinline__ void gdn_fused(const GdnFusedArgs &a) {
     __shared__ float red_mem[GDN_GROUPS][GDN_COLS];
     __shared__ float red_out[GDN_GROUPS][GDN_COLS];
     __shared__ float red_nrm[2][GDN_GROUPS];
@@ -149,37 +179,47 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_gfx950(GdnFused
     const uint32_t vj = slice * GDN_COLS + tid;
     const bool v_thr = tid < GDN_COLS && vj < a.value_dim;
     const uint32_t v_ch = 2 * kw + h * a.value_dim + vj;
+    // Every input read of the workgroup is a buffer load issued before the
+    // first wait, with no branch around it: a thread without a channel reads
+    // past the buffer's range (zeros, no memory traffic). Loads issued inside
+    // divergent branches made the compiler wait for earlier loads before
+    // reusing their registers, which serialized the round trips.
+    const uint32_t C = 2 * kw + a.heads * a.value_dim;  // conv channels
+    const GdnBuf wr = gdn_buf(a.conv_w, (size_t)C * K), cr = gdn_buf(a.conv_in, (size_t)C * K);
+    const uint32_t qko = qk_ch * K * 4, vo = v_ch * K * 4;
     float wq[GDN_MAX_KERNEL], sq_[GDN_MAX_KERNEL], wv[GDN_MAX_KERNEL], sv_[GDN_MAX_KERNEL];
-#pragma unroll
-    for (int i = 0; i < GDN_MAX_KERNEL; i++) {
-        const bool ok = (uint32_t)i < K;
-        wq[i] = qk_thr && ok ? a.conv_w[(size_t)qk_ch * K + i] : 0.0f;
-        sq_[i] = qk_thr && ok ? a.conv_in[(size_t)qk_ch * K + i] : 0.0f;
-        wv[i] = v_thr && ok ? a.conv_w[(size_t)v_ch * K + i] : 0.0f;
-        sv_[i] = v_thr && ok ? a.conv_in[(size_t)v_ch * K + i] : 0.0f;
-    }
+    gdn_load8(wr, qk_thr, qko, K, wq);
+    gdn_load8(cr, qk_thr, qko, K, sq_);
+    gdn_load8(wr, v_thr, vo, K, wv);
+    gdn_load8(cr, v_thr, vo, K, sv_);
 
     float s[GDN_MAX_ROWS];
     // Blocked layout: this thread's 8 rows at one 32-byte run.
     const size_t blk = (((size_t)h * slices + slice) * 256 + tid) * 8;
-    const size_t head_floats = a.state_blocked ? (size_t)slices * 2048 : (size_t)dk * a.value_dim;
-    if (a.state_blocked) {
-        const float4 *S4 = (const float4 *)(a.state + blk);
-        const float4 lo = S4[0], hi = S4[1];
-        s[0] = lo.x; s[1] = lo.y; s[2] = lo.z; s[3] = lo.w;
-        s[4] = hi.x; s[5] = hi.y; s[6] = hi.z; s[7] = hi.w;
+    const size_t head_floats = BLOCKED ? (size_t)slices * 2048 : (size_t)dk * a.value_dim;
+    {
+        const GdnBuf sr = gdn_buf(a.state + (size_t)h * head_floats, head_floats);
+        if (BLOCKED) {
+            const uint32_t bo = (uint32_t)(blk - (size_t)h * head_floats) * 4;
+            const v4i lo = __builtin_amdgcn_raw_buffer_load_b128(sr.r, bo, 0, 0);
+            const v4i hi = __builtin_amdgcn_raw_buffer_load_b128(sr.r, bo + 16, 0, 0);
 #pragma unroll
-        for (int r = 8; r < GDN_MAX_ROWS; r++) s[r] = 0.0f;
-    } else {
-        const float *S = a.state + (size_t)h * head_floats;
+            for (int r = 0; r < 4; r++) {
+                s[r] = __int_as_float(lo[r]);
+                s[4 + r] = __int_as_float(hi[r]);
+            }
 #pragma unroll
-        for (int r = 0; r < GDN_MAX_ROWS; r++) {
-            const uint32_t i = ig + GDN_GROUPS * r;
-            s[r] = ((uint32_t)r < nrows && i < dk && colok) ? S[(size_t)i * a.value_dim + j] : 0.0f;
+            for (int r = 8; r < GDN_MAX_ROWS; r++) s[r] = 0.0f;
+        } else {
+#pragma unroll
+            for (int r = 0; r < GDN_MAX_ROWS; r++) {
+                const uint32_t i = ig + GDN_GROUPS * r;
+                s[r] = gdn_ld(sr, (uint32_t)r < nrows && i < dk && colok, (i * a.value_dim + j) * 4);
+            }
         }
     }
     auto store_state = [&](float *base) {
-        if (a.state_blocked) {
+        if (BLOCKED) {
             float4 *S4 = (float4 *)(base + blk);
             S4[0] = make_float4(s[0], s[1], s[2], s[3]);
             S4[1] = make_float4(s[4], s[5], s[6], s[7]);
@@ -197,13 +237,21 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_gfx950(GdnFused
     // inputs for thread 255) are loaded ahead of the stores of earlier
     // tokens: a load issued after a store waits for it (loads and stores
     // retire in one in-order counter).
+    const GdnBuf pr = gdn_buf(a.proj, (size_t)a.tokens * a.proj_stride);
+    const GdnBuf dr = gdn_buf(a.gates_given ? a.log_decay : nullptr, (size_t)a.tokens * a.heads);
+    const GdnBuf br = gdn_buf(a.gates_given ? a.beta : nullptr, (size_t)a.tokens * a.heads);
     auto load_in = [&](uint32_t t, float &xq, float &xv, float &ga, float &gb) {
-        const float *row = a.proj + (size_t)t * a.proj_stride;
-        xq = qk_thr ? row[qk_ch] : 0.0f;
-        xv = v_thr ? row[v_ch] : 0.0f;
-        const size_t th = (size_t)t * a.heads + h;
-        ga = tid != 255 ? 0.0f : (a.gates_given ? a.log_decay[th] : row[a.a_off + h]);
-        gb = tid != 255 ? 0.0f : (a.gates_given ? a.beta[th] : row[a.b_off + h]);
+        const uint32_t row = t * a.proj_stride, th = t * a.heads + h;
+        xq = gdn_ld(pr, qk_thr, (row + qk_ch) * 4);
+        xv = gdn_ld(pr, v_thr, (row + v_ch) * 4);
+        const bool g = tid == 255;
+        if (a.gates_given) {
+            ga = gdn_ld(dr, g, th * 4);
+            gb = gdn_ld(br, g, th * 4);
+        } else {
+            ga = gdn_ld(pr, g, (row + a.a_off + h) * 4);
+            gb = gdn_ld(pr, g, (row + a.b_off + h) * 4);
+        }
     };
     const float dtb = tid == 255 && !a.gates_given ? a.dt_bias[h] : 0.0f;
     const float alog = tid == 255 && !a.gates_given ? a.a_log[h] : 0.0f;
@@ -271,7 +319,7 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_gfx950(GdnFused
             gsc[0] = expf(ld);
             gsc[1] = be;
         }
-        __syncthreads();
+        lds_barrier();
         const float decay = gsc[0], beta = gsc[1];
         const float vjv = colok ? vs[jj] : 0.0f;
         float kk[GDN_MAX_ROWS], qq[GDN_MAX_ROWS];
@@ -292,7 +340,7 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_gfx950(GdnFused
             red_nrm[0][ig] = sk;
             red_nrm[1][ig] = sqq;
         }
-        __syncthreads();
+        lds_barrier();
         float memj = 0.0f, ssk = 0.0f, ssq = 0.0f;
 #pragma unroll
         for (int gi = 0; gi < GDN_GROUPS; gi++) {
@@ -309,7 +357,7 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_gfx950(GdnFused
             o += s[r] * qq[r];
         }
         red_out[ig][jj] = o;
-        __syncthreads();
+        lds_barrier();
         if (ig == 0 && colok) {
             float oj = 0.0f;
 #pragma unroll
@@ -331,7 +379,7 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_gfx950(GdnFused
         }
         // qs/ks/vs/gsc and red_* are rewritten next token only after every
         // thread has passed this barrier.
-        __syncthreads();
+        lds_barrier();
     };
     if (a.tokens <= GDN_PREFETCH) {
         // Every token's inputs are loaded before the first token's stores,
@@ -372,3 +420,7 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_gfx950(GdnFused
         for (int i = 0; i < GDN_MAX_KERNEL; i++)
             if ((uint32_t)i < K) a.conv_out[(size_t)v_ch * K + i] = sv_[i];
 }
+
+// The crate's state layout, and the engine's blocked one (state_blocked).
+extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_gfx950(GdnFusedArgs a) { gdn_fused<false>(a); }
+extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_blk_gfx950(GdnFusedArgs a) { gdn_fused<true>(a); }

@@ -36,6 +36,7 @@
 #include <hip/hip_runtime.h>
 
 #include "kernel_args.h"
+#include "lds_barrier.h"
 
 typedef float pa_v4f __attribute__((ext_vector_type(4)));
 

@@ -23,6 +23,7 @@
 //  * Every wave keeps its per-row partial in a register across slices; the
 //    eight partials are added in LDS in a fixed order (deterministic), then
 //    /15 (Q4) or /3 (Q2), bias, s_out and SiLU.
+#include "lds_barrier.h"
 
 template <int DT>
 struct SlCfg {
@@ -37,13 +38,6 @@ struct SlCfg {
     static constexpr uint32_t STR = 1040;             // LDS bytes per staged row
     static constexpr float DEN = DT ? 15.0f : 3.0f;
 };
-
-// Workgroup barrier that orders LDS accesses only (no wait on global loads).
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 template <int DT>
 struct SlLoad {

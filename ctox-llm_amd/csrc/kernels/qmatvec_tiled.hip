@@ -21,6 +21,7 @@
 //    chunk sums of a row tile are combined by the wave that arrives last at
 //    the tile's counter, in chunk order, so the result is deterministic.
 #include "kernel_args.h"
+#include "lds_barrier.h"
 
 // Cache policy of streamed weight loads: non-temporal.
 #define CTOX_LOAD_NT 2
@@ -306,7 +307,7 @@ template <int DT, int U, int AB>
 __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
     using C = TlCfg<DT>;
     const uint32_t lane = threadIdx.x & 63;
-    const uint32_t v = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
+    const uint32_t v = __builtin_amdgcn_readfirstlane(blockIdx.x * 4u + (threadIdx.x >> 6));
     const uint32_t c = v / a.segs, s = v - c * a.segs;
     const uint32_t t0 = s * U;
     // With AB the host makes segs a multiple of the workgroup's wave count,
@@ -399,7 +400,7 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
             lds_barrier();
             inv = 1.0f / sqrtf(((wss[0] + wss[1]) + (wss[2] + wss[3])) / (float)(a.blocks * CTOX_BLOCK_LEN) + a.eps);
         }
-        const bool keep = ((blockIdx.x * (blockDim.x >> 6)) % a.segs) == 0;  // segment 0 of the chunk
+        const bool keep = ((blockIdx.x * 4u) % a.segs) == 0;  // segment 0 of the chunk
         const float4 k = frag_group_build<DT>(a, c * 4 + wg_wave, lane, gin, inv, keep, xs + wg_wave * 768, 192,
                                               a.x_out, a.norm_out);
         if (j == 0) kqs[4 * wg_wave + g] = k;
@@ -556,7 +557,7 @@ __device__ __forceinline__ void tile_matvec_m(const TileMatvecArgs &a) {
     __shared__ __align__(16) int8_t xas[CTOX_TILE_BLOCKS * MAXM * 192 + 16];
     __shared__ float4 kqs[CTOX_TILE_BLOCKS * MAXM];
     const uint32_t lane = threadIdx.x & 63;
-    const uint32_t v = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
+    const uint32_t v = __builtin_amdgcn_readfirstlane(blockIdx.x * 4u + (threadIdx.x >> 6));
     const uint32_t c = v / a.segs, s = v - c * a.segs;
     const uint32_t t0 = s * U, M = a.batch;
     if (c >= a.chunks) return;  // uniform over the workgroup (segs is a multiple of 4)
@@ -733,7 +734,7 @@ __device__ __forceinline__ void tile_matvec_mx(const TileMatvecArgs &a) {
     __shared__ float4 kqs[CTOX_TILE_BLOCKS * MR];
     __shared__ __align__(16) float sqs[MR * 512];
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const uint32_t v = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + w);
+    const uint32_t v = __builtin_amdgcn_readfirstlane(blockIdx.x * 4u + w);
     const uint32_t c = v / a.segs, s = v - c * a.segs;
     constexpr uint32_t M = MR;
     const uint32_t t0 = s * U;
@@ -795,7 +796,7 @@ __device__ __forceinline__ void tile_matvec_mx(const TileMatvecArgs &a) {
     CTOX_WAIT_VMCNT(WLOADS);  // the input copies and the two operand loads have landed
     __builtin_amdgcn_sched_barrier(0);
     if (xm == 1) lds_barrier();  // wave 0's copy of the sums is visible
-    const bool keep = ((blockIdx.x * (blockDim.x >> 6)) % a.segs) == 0;  // segment 0 of the chunk
+    const bool keep = ((blockIdx.x * 4u) % a.segs) == 0;  // segment 0 of the chunk
     // One row at a time (not unrolled: the build's temporaries are live
     // beside the weight loads in flight).
 #pragma unroll 1

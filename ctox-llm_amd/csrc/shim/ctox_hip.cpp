@@ -168,7 +168,7 @@ struct ctox_hip_backend {
     bool no_mx = false;
     bool noalloc_ok = false;  // the static scratch of ctox_hip_launch_fused_matvec_noalloc is set up
     hipFunction_t repack = nullptr;
-    hipFunction_t gdn_fused = nullptr;
+    hipFunction_t gdn_fused = nullptr, gdn_fused_blk = nullptr;
     int cus = 0;
     uint32_t tile_u = 0;  // CTOX_TILE_U: fixed row tiles per wave (0 = planned)
     // Tiled matvec chunk partials (64-bit slots tagged with a launch sequence
@@ -822,7 +822,7 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->tilemx[0][2], "ctox_q2_mv_tilemx4_gfx950"}, {&b->tilemx[0][3], "ctox_q2_mv_tilemx5_gfx950"},
                {&b->tilemx[1][0], "ctox_q4_mv_tilemx2_gfx950"}, {&b->tilemx[1][1], "ctox_q4_mv_tilemx3_gfx950"},
                {&b->tilemx[1][2], "ctox_q4_mv_tilemx4_gfx950"}, {&b->tilemx[1][3], "ctox_q4_mv_tilemx5_gfx950"},
-               {&b->repack, "ctox_tile_repack_gfx950"}, {&b->gdn_fused, "ctox_gdn_fused_gfx950"},
+               {&b->repack, "ctox_tile_repack_gfx950"}, {&b->gdn_fused, "ctox_gdn_fused_gfx950"}, {&b->gdn_fused_blk, "ctox_gdn_fused_blk_gfx950"},
                {&b->finite, "ctox_finite_check_gfx950"}, {&b->gather, "ctox_gather_rows_gfx950"},
                {&b->topk_part, "ctox_topk_part_gfx950"}, {&b->topk_final, "ctox_topk_final_gfx950"}};
     for (auto &f : fns) {
@@ -1680,8 +1680,8 @@ ctox_status gdn_fused_impl(ctox_hip_backend *b, const float *d_proj, size_t proj
     a.gates_given = gates_given ? 1u : 0u;
     a.state_blocked = blocked ? 1u : 0u;
     const size_t slices = (value_dim + 15) / 16;
-    return launch(b->gdn_fused, dim3((unsigned)(heads * slices)), dim3(256), pick_stream(b, stream), a,
-                  "ctox_gdn_fused_gfx950");
+    return launch(a.state_blocked ? b->gdn_fused_blk : b->gdn_fused, dim3((unsigned)(heads * slices)), dim3(256),
+                  pick_stream(b, stream), a, "ctox_gdn_fused_gfx950");
 }
 }  // namespace
 
