@@ -146,6 +146,36 @@ def copy_reference(torch, mib=256, reps=5):
             "GBps_read_plus_write": 2 * (mib << 20) / (us * 1e-6) / 1e9}
 
 
+def read_floor(torch, hip, nbytes, steps=200):
+    """The HBM floor of one launch: ctox_stream_read_gfx950 reading `nbytes`
+    (the matvec's algorithmic bytes) with the tiled kernel's access pattern,
+    rotating over copies above the Infinity Cache, median of REPLICATES
+    windows of `steps` back-to-back launches."""
+    import ctypes
+    nbytes = (nbytes + 15) // 16 * 16
+    copies = max(2, -(-2 * INFINITY_CACHE // nbytes))
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(copies)]
+    out = torch.empty((nbytes + 8191) // 8192, dtype=torch.int32, device="cuda")
+    lib = ctox_lib()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def run(i):
+        st = lib.ctox_hip_stream_read_device(hip.handle, ctypes.c_void_p(bufs[i % copies].data_ptr()), nbytes,
+                                             ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(stream))
+        if st != 0:
+            raise RuntimeError("stream read failed")
+    for i in range(20):
+        run(i)
+    wins = []
+    for _ in range(REPLICATES):
+        with Timer(torch) as t:
+            for i in range(steps):
+                run(i)
+        wins.append(t.ms / steps)
+    us = float(np.median(wins)) * 1e3
+    return {"bytes": nbytes, "us": us, "GBps": nbytes / (us * 1e-6) / 1e9, "frac_of_8TBps": nbytes / (us * 1e-6) / 8e12}
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -340,7 +370,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only")
-    ap.add_argument("--only", choices=["decode", "attention", "gdn", "selection", "verify", "config1", "config2"],
+    ap.add_argument("--only", choices=["decode", "attention", "gdn", "selection", "verify", "config1", "config2",
+                                       "floor"],
                     help="run one extra workload alone and print its result (for profiling)")
     ap.add_argument("--context", type=int, default=32768, help="context of --only decode / attention")
     args = ap.parse_args()
@@ -364,7 +395,10 @@ def main():
                "config1": lambda: bench_matvec(torch, hip, ctox_hip, synth, 1, 17408, 5120, "normal", args.steps,
                                                args.warmup)[0],
                "config2": lambda: bench_matvec(torch, hip, ctox_hip, synth, 0, 5120, 17408, "swiglu", args.steps,
-                                               args.warmup)[0]}[args.only]()
+                                               args.warmup)[0],
+               "floor": lambda: {"config2_bytes": read_floor(torch, hip, matvec_bytes(5120, 17408, 0), args.steps),
+                                 "config1_bytes": read_floor(torch, hip, matvec_bytes(17408, 5120, 1), args.steps)}
+               }[args.only]()
         print(json.dumps({"only": args.only, "result": res}), flush=True)
         return
 
@@ -388,6 +422,9 @@ def main():
         log("config5 decode", extra["config5_decode_27b"])
 
     extra["copy_reference"] = copy_reference(torch)
+    extra["read_floor"] = {"config2_bytes": read_floor(torch, hip, matvec_bytes(5120, 17408, 0), args.steps),
+                           "config1_bytes": read_floor(torch, hip, matvec_bytes(17408, 5120, 1), args.steps)}
+    log("read floor", extra["read_floor"])
     log("copy", extra["copy_reference"])
     cpu = None if args.no_cpu else cpu_baseline(0, 5120, 17408, host2)
     line = {

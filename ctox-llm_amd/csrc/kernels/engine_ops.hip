@@ -22,6 +22,10 @@
 //    buffer (the engine's fail-closed check of logits).
 //  * ctox_gather_rows_gfx950: byte rows gathered by index (the restricted
 //    draft head's compact LM-head copy).
+//  * ctox_stream_read_gfx950: a plain streaming read (the HBM floor the
+//    matvec kernels are measured against): each wave reads 8 KiB with the
+//    access pattern of the tiled matvec (every 16-byte load issued before
+//    the first wait, non-temporal) and stores their xor.
 //  * ctox_write_words_gfx950: up to 32 words carried in the kernel arguments
 //    (token ids, page descriptors): ordered on the stream, no host buffer to keep alive.
 #include <hip/hip_runtime.h>
@@ -213,4 +217,23 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gather_rows_gfx950(Gather
     const uint8_t *src = a.src + (uint64_t)a.ids[r] * a.row_bytes;
     uint8_t *dst = a.dst + (uint64_t)r * a.row_bytes;
     for (uint64_t i = threadIdx.x; i < a.row_bytes; i += 256) dst[i] = src[i];
+}
+
+extern "C" __global__ __launch_bounds__(256) void ctox_stream_read_gfx950(StreamReadArgs a) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint64_t w = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const uint64_t base = w * 8192;
+    if (base >= a.bytes) return;
+    const uint64_t n = a.bytes - base < 8192 ? a.bytes - base : 8192;
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(a.src + base), (short)0, (int)n, 0x00020000);
+    v4i v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, lane * 16 + i * 1024, 0, 2);
+    uint32_t x = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) x ^= (uint32_t)(v[i][0] ^ v[i][1] ^ v[i][2] ^ v[i][3]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o);
+    if (lane == 0) a.out[w] = x;
 }

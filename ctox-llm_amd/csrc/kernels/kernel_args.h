@@ -560,6 +560,12 @@ struct FiniteArgs {          // ctox_finite_check_gfx950
     uint64_t n;
 };
 
+struct StreamReadArgs {      // ctox_stream_read_gfx950
+    const uint8_t *src;
+    uint32_t *out;           // [ceil(bytes / 8 KiB)]: xor of each wave's 8 KiB
+    uint64_t bytes;          // multiple of 16
+};
+
 struct GatherRowsArgs {      // ctox_gather_rows_gfx950: dst row r = src row ids[r] (bytes)
     const uint8_t *src;
     uint8_t *dst;

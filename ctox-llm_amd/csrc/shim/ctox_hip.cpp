@@ -149,7 +149,7 @@ struct ctox_hip_backend {
                   conv = nullptr, rope = nullptr, kv_pack = nullptr, attn_prep = nullptr, kv_demote = nullptr, gqa_part[2] = {}, gqa_part16[2] = {},
                   gqa_combine = nullptr, fill = nullptr, embed = nullptr, norm_rows = nullptr, attn_gate = nullptr,
                   swiglu_rows = nullptr, copy_rows = nullptr, write_words = nullptr, norm_prep = nullptr,
-                  prep_x = nullptr, finite = nullptr, gather = nullptr, topk_part = nullptr, topk_final = nullptr;
+                  prep_x = nullptr, finite = nullptr, gather = nullptr, topk_part = nullptr, topk_final = nullptr, stream_read = nullptr;
     // Batch-1 slice kernels per dtype [Q2, Q4]: [0] walks the slices, [n]
     // requests all n slices up front (n <= 3: more slices up front measured
     // slower than walking them).
@@ -823,7 +823,7 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->tilemx[1][0], "ctox_q4_mv_tilemx2_gfx950"}, {&b->tilemx[1][1], "ctox_q4_mv_tilemx3_gfx950"},
                {&b->tilemx[1][2], "ctox_q4_mv_tilemx4_gfx950"}, {&b->tilemx[1][3], "ctox_q4_mv_tilemx5_gfx950"},
                {&b->repack, "ctox_tile_repack_gfx950"}, {&b->gdn_fused, "ctox_gdn_fused_gfx950"}, {&b->gdn_fused_blk, "ctox_gdn_fused_blk_gfx950"},
-               {&b->finite, "ctox_finite_check_gfx950"}, {&b->gather, "ctox_gather_rows_gfx950"},
+               {&b->finite, "ctox_finite_check_gfx950"}, {&b->gather, "ctox_gather_rows_gfx950"}, {&b->stream_read, "ctox_stream_read_gfx950"},
                {&b->topk_part, "ctox_topk_part_gfx950"}, {&b->topk_final, "ctox_topk_final_gfx950"}};
     for (auto &f : fns) {
         if (le != hipSuccess) break;
@@ -1923,6 +1923,18 @@ extern "C" ctox_status ctox_hip_gather_rows_device(ctox_hip_backend *b, const vo
     (void)hipStreamSynchronize(s);
     (void)hipFree(d_ids);
     return st;
+}
+
+// A plain streaming read of `bytes` (a multiple of 16) with the tiled
+// matvec's access pattern; d_out receives one word per 8 KiB.
+extern "C" ctox_status ctox_hip_stream_read_device(ctox_hip_backend *b, const void *d_src, size_t bytes,
+                                                   uint32_t *d_out, void *stream) {
+    if (!b || !d_src || !d_out) return fail(CTOX_ERR_SHAPE, "null argument");
+    if (bytes == 0 || bytes % 16 || bytes > ((size_t)1 << 40)) return fail(CTOX_ERR_SHAPE, "read size");
+    const size_t waves = (bytes + 8191) / 8192;
+    StreamReadArgs a{(const uint8_t *)d_src, d_out, (uint64_t)bytes};
+    return launch(b->stream_read, dim3((unsigned)((waves + 3) / 4)), dim3(256), pick_stream(b, stream), a,
+                  "ctox_stream_read_gfx950");
 }
 
 // ======================================================================

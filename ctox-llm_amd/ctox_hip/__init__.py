@@ -292,6 +292,7 @@ SIGNATURES = {
     "ctox_hip_engine_create_with_dtypes": (_I32, [_P, _P, ctypes.c_uint64, _P, _SZ, ctypes.POINTER(_P)]),
     "ctox_hip_engine_write": (_I32, [_P, ctypes.c_char_p, _U32, _SZ, _P, _SZ]),
     "ctox_hip_engine_finish_load": (_I32, [_P]),
+    "ctox_hip_stream_read_device": (_I32, [_P, _P, _SZ, _P, _P]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

@@ -625,6 +625,14 @@ ctox_status ctox_hip_copy_rows_device(ctox_hip_backend *backend, const float *d_
 ctox_status ctox_hip_write_words_device(ctox_hip_backend *backend, uint32_t *d_dst, const uint32_t *words,
                                         size_t count, void *stream);
 
+/* A plain streaming read of `bytes` (a multiple of 16) with the tiled
+ * matvec's access pattern (each wave 8 KiB, every 16-byte load issued before
+ * the first wait, non-temporal); d_out receives ceil(bytes / 8192) words.
+ * No counterpart in the reference: the HBM read floor the matvec kernels
+ * are measured against (bench.py). */
+ctox_status ctox_hip_stream_read_device(ctox_hip_backend *backend, const void *d_src, size_t bytes, uint32_t *d_out,
+                                        void *stream);
+
 /* ---- device-resident decode engine (engine.cpp) ----
  * The crate's model graph (Q/src/decoder.rs:427-1114) and MTP executor
  * (:1217-1458, CUDA MTP4 flow cuda_executor.rs:797-889) over the entry points
