@@ -157,10 +157,15 @@ __device__ __forceinline__ void gdn_load8(const GdnBuf &b, bool ok, uint32_t off
 }
 template <bool BLOCKED>
 __device__ __forceinline__ void gdn_fused(const GdnFusedArgs &a) {
-    __shared__ float red_mem[GDN_GROUPS][GDN_COLS];
-    __shared__ float red_out[GDN_GROUPS][GDN_COLS];
-    __shared__ float red_nrm[2][GDN_GROUPS];
-    __shared__ float qs[256], ks[256], vs[GDN_COLS], gsc[2];
+    // Rows are processed in blocks of up to GDN_PREFETCH. Phase 1 of a block
+    // runs every row's conv + SiLU and gates (they do not depend on the
+    // state) into LDS; phase 2 runs the recurrence row by row with two
+    // barriers per row, its reduction buffers alternating between rows so no
+    // third barrier is needed before the next row writes them.
+    __shared__ float red_mem[2][GDN_GROUPS][GDN_COLS];
+    __shared__ float red_out[2][GDN_GROUPS][GDN_COLS];
+    __shared__ float red_nrm[2][2][GDN_GROUPS];
+    __shared__ float qs[GDN_PREFETCH][256], ks[GDN_PREFETCH][256], vs[GDN_PREFETCH][GDN_COLS], gsc[GDN_PREFETCH][2];
 
     const uint32_t slices = (a.value_dim + GDN_COLS - 1) / GDN_COLS;
     const uint32_t h = blockIdx.x / slices, slice = blockIdx.x % slices;
@@ -233,178 +238,157 @@ __device__ __forceinline__ void gdn_fused(const GdnFusedArgs &a) {
         }
     };
 
-    // This thread's inputs of a token (its conv channels, and the gate
-    // inputs for thread 255) are loaded ahead of the stores of earlier
-    // tokens: a load issued after a store waits for it (loads and stores
-    // retire in one in-order counter).
+    // The gate inputs of block row u are read by thread 256 - GDN_PREFETCH + u.
     const GdnBuf pr = gdn_buf(a.proj, (size_t)a.tokens * a.proj_stride);
     const GdnBuf dr = gdn_buf(a.gates_given ? a.log_decay : nullptr, (size_t)a.tokens * a.heads);
     const GdnBuf br = gdn_buf(a.gates_given ? a.beta : nullptr, (size_t)a.tokens * a.heads);
-    auto load_in = [&](uint32_t t, float &xq, float &xv, float &ga, float &gb) {
-        const uint32_t row = t * a.proj_stride, th = t * a.heads + h;
-        xq = gdn_ld(pr, qk_thr, (row + qk_ch) * 4);
-        xv = gdn_ld(pr, v_thr, (row + v_ch) * 4);
-        const bool g = tid == 255;
+    const uint32_t gu = tid - (256 - GDN_PREFETCH);  // block row of this thread's gates (< GDN_PREFETCH)
+    const bool g_thr = tid >= 256 - GDN_PREFETCH;
+    // One conv step (shift the window left, append x) and its SiLU output.
+    auto conv_step = [&](float (&win)[GDN_MAX_KERNEL], const float (&w)[GDN_MAX_KERNEL], float x) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i + 1 < GDN_MAX_KERNEL; i++)
+            if ((uint32_t)i + 1 < K) {
+                const float v = win[i + 1];
+                win[i] = v;
+                sum += v * w[i];
+            }
+        float wl = 0.0f;
+#pragma unroll
+        for (int i = 0; i < GDN_MAX_KERNEL; i++)
+            if ((uint32_t)i == K - 1) {
+                win[i] = x;
+                wl = w[i];
+            }
+        sum += x * wl;
+        return sum / (1.0f + expf(-sum));
+    };
+    // Inputs of one block of rows: the conv channels' values and, for thread
+    // 256 - GDN_PREFETCH + u, row u's gate inputs. The first block's are read
+    // here, ahead of any use of the conv windows and state loaded above, so
+    // every input read of the launch is in flight before the first wait;
+    // later blocks' during the previous block's recurrence.
+    float xq[GDN_PREFETCH], xv[GDN_PREFETCH], ga = 0.0f, gb = 0.0f;
+    auto load_block = [&](uint32_t t0) {
+        const uint32_t nb = min((uint32_t)GDN_PREFETCH, a.tokens - t0);
+#pragma unroll
+        for (int u = 0; u < GDN_PREFETCH; u++) {
+            const uint32_t row = (t0 + min((uint32_t)u, nb - 1)) * a.proj_stride;
+            xq[u] = gdn_ld(pr, qk_thr, (row + qk_ch) * 4);
+            xv[u] = gdn_ld(pr, v_thr, (row + v_ch) * 4);
+        }
+        const bool g_row = g_thr && gu < nb;
+        const uint32_t gt = t0 + (g_row ? gu : 0), gth = gt * a.heads + h, grow = gt * a.proj_stride;
         if (a.gates_given) {
-            ga = gdn_ld(dr, g, th * 4);
-            gb = gdn_ld(br, g, th * 4);
+            ga = gdn_ld(dr, g_row, gth * 4);
+            gb = gdn_ld(br, g_row, gth * 4);
         } else {
-            ga = gdn_ld(pr, g, (row + a.a_off + h) * 4);
-            gb = gdn_ld(pr, g, (row + a.b_off + h) * 4);
+            ga = gdn_ld(pr, g_row, (grow + a.a_off + h) * 4);
+            gb = gdn_ld(pr, g_row, (grow + a.b_off + h) * 4);
         }
     };
-    const float dtb = tid == 255 && !a.gates_given ? a.dt_bias[h] : 0.0f;
-    const float alog = tid == 255 && !a.gates_given ? a.a_log[h] : 0.0f;
-    // One token's step on inputs already in registers.
-    auto step = [&](uint32_t t, float cxq, float cxv, float cga, float cgb) {
-        // Conv step: shift the window left by one, append the input.
-        if (qk_thr) {
-            float sum = 0.0f;
+    load_block(0);
+    const GdnBuf gbuf_dt = gdn_buf(a.dt_bias, a.heads), gbuf_al = gdn_buf(a.a_log, a.heads);
+    const float dtb = gdn_ld(gbuf_dt, g_thr && !a.gates_given, h * 4);
+    const float alog = gdn_ld(gbuf_al, g_thr && !a.gates_given, h * 4);
+    __builtin_amdgcn_sched_barrier(0);
+    for (uint32_t t0 = 0; t0 < a.tokens; t0 += GDN_PREFETCH) {
+        const uint32_t nb = min((uint32_t)GDN_PREFETCH, a.tokens - t0);
+        const bool g_row = g_thr && gu < nb;
+        const uint32_t gth = (t0 + (g_row ? gu : 0)) * a.heads + h;
+        // Phase 1: conv + SiLU of every block row in order (the windows after
+        // row t go to the row's conv snapshot), and the gates of row gu.
 #pragma unroll
-            for (int i = 0; i + 1 < GDN_MAX_KERNEL; i++)
-                if ((uint32_t)i + 1 < K) {
-                    const float v = sq_[i + 1];
-                    sq_[i] = v;
-                    sum += v * wq[i];
-                }
-            const float x = cxq;
+        for (int u = 0; u < GDN_PREFETCH; u++) {
+            if ((uint32_t)u >= nb) break;
+            if (qk_thr) {
+                const float y = conv_step(sq_, wq, xq[u]);
+                if (tid < dk) qs[u][tid] = y;
+                else ks[u][tid - dk] = y;
+            }
+            if (v_thr) vs[u][tid] = conv_step(sv_, wv, xv[u]);
+            if (a.snap_stride) {
+                float *co = a.conv_out + (size_t)(t0 + u) * a.conv_snap_stride;
+                if (qk_thr && h % rep == 0 && slice == 0)
 #pragma unroll
-            for (int i = 0; i < GDN_MAX_KERNEL; i++)
-                if ((uint32_t)i == K - 1) sq_[i] = x;
-            float wl = 0.0f;
+                    for (int i = 0; i < GDN_MAX_KERNEL; i++)
+                        if ((uint32_t)i < K) co[(size_t)qk_ch * K + i] = sq_[i];
+                if (v_thr)
 #pragma unroll
-            for (int i = 0; i < GDN_MAX_KERNEL; i++)
-                if ((uint32_t)i == K - 1) wl = wq[i];
-            sum += x * wl;
-            const float y = sum / (1.0f + expf(-sum));
-            if (tid < dk) qs[tid] = y;
-            else ks[tid - dk] = y;
+                    for (int i = 0; i < GDN_MAX_KERNEL; i++)
+                        if ((uint32_t)i < K) co[(size_t)v_ch * K + i] = sv_[i];
+            }
         }
-        if (v_thr) {
-            float sum = 0.0f;
-#pragma unroll
-            for (int i = 0; i + 1 < GDN_MAX_KERNEL; i++)
-                if ((uint32_t)i + 1 < K) {
-                    const float v = sv_[i + 1];
-                    sv_[i] = v;
-                    sum += v * wv[i];
-                }
-            const float x = cxv;
-            float wl = 0.0f;
-#pragma unroll
-            for (int i = 0; i < GDN_MAX_KERNEL; i++)
-                if ((uint32_t)i == K - 1) {
-                    sv_[i] = x;
-                    wl = wv[i];
-                }
-            sum += x * wl;
-            vs[tid] = sum / (1.0f + expf(-sum));
-        }
-        if (tid == 255) {
-            const size_t th = (size_t)t * a.heads + h;
+        if (g_row) {
             float be, ld;
             if (a.gates_given) {
-                be = cgb;
-                ld = cga;
+                be = gb;
+                ld = ga;
             } else {
-                be = 1.0f / (1.0f + expf(-cgb));
-                const float x = cga + dtb;
+                be = 1.0f / (1.0f + expf(-gb));
+                const float x = ga + dtb;
                 const float sp = x > 20.0f ? x : log1pf(expf(x));
                 ld = -expf(alog) * sp;
                 if (slice == 0) {
-                    a.beta[th] = be;
-                    a.log_decay[th] = ld;
+                    a.beta[gth] = be;
+                    a.log_decay[gth] = ld;
                 }
             }
-            gsc[0] = expf(ld);
-            gsc[1] = be;
+            gsc[gu][0] = expf(ld);
+            gsc[gu][1] = be;
         }
+        if (t0 + GDN_PREFETCH < a.tokens) load_block(t0 + GDN_PREFETCH);
         lds_barrier();
-        const float decay = gsc[0], beta = gsc[1];
-        const float vjv = colok ? vs[jj] : 0.0f;
-        float kk[GDN_MAX_ROWS], qq[GDN_MAX_ROWS];
-        float mem = 0.0f, sk = 0.0f, sqq = 0.0f;
+        // Phase 2: the recurrence, row by row.
+        for (uint32_t u = 0; u < nb; u++) {
+            const uint32_t t = t0 + u, bsel = u & 1;
+            const float decay = gsc[u][0], beta = gsc[u][1];
+            const float vjv = colok ? vs[u][jj] : 0.0f;
+            float kk[GDN_MAX_ROWS], qq[GDN_MAX_ROWS];
+            float mem = 0.0f, sk = 0.0f, sqq = 0.0f;
 #pragma unroll
-        for (int r = 0; r < GDN_MAX_ROWS; r++) {
-            const uint32_t i = ig + GDN_GROUPS * r;
-            const bool ok = (uint32_t)r < nrows && i < dk;
-            kk[r] = ok ? ks[i] : 0.0f;
-            qq[r] = ok ? qs[i] : 0.0f;
-            sk += kk[r] * kk[r];
-            sqq += qq[r] * qq[r];
-            s[r] = s[r] * decay;
-            mem += s[r] * kk[r];
-        }
-        red_mem[ig][jj] = mem;
-        if (jj == 0) {
-            red_nrm[0][ig] = sk;
-            red_nrm[1][ig] = sqq;
-        }
-        lds_barrier();
-        float memj = 0.0f, ssk = 0.0f, ssq = 0.0f;
-#pragma unroll
-        for (int gi = 0; gi < GDN_GROUPS; gi++) {
-            memj += red_mem[gi][jj];
-            ssk += red_nrm[0][gi];
-            ssq += red_nrm[1][gi];
-        }
-        const float kinv = 1.0f / sqrtf(ssk + 1e-6f), qinv = 1.0f / sqrtf(ssq + 1e-6f);
-        const float delta = (vjv - memj * kinv) * beta;
-        float o = 0.0f;
-#pragma unroll
-        for (int r = 0; r < GDN_MAX_ROWS; r++) {
-            s[r] += kk[r] * kinv * delta;
-            o += s[r] * qq[r];
-        }
-        red_out[ig][jj] = o;
-        lds_barrier();
-        if (ig == 0 && colok) {
-            float oj = 0.0f;
-#pragma unroll
-            for (int gi = 0; gi < GDN_GROUPS; gi++) oj += red_out[gi][jj];
-            a.out[((size_t)t * a.heads + h) * a.value_dim + j] = oj * qinv * qscale;
-        }
-        if (a.snap_stride) {
-            // Row snapshot: the state and conv windows after token t.
-            store_state(a.state_out + (size_t)t * a.snap_stride);
-            float *co = a.conv_out + (size_t)t * a.conv_snap_stride;
-            if (qk_thr && h % rep == 0 && slice == 0)
-#pragma unroll
-                for (int i = 0; i < GDN_MAX_KERNEL; i++)
-                    if ((uint32_t)i < K) co[(size_t)qk_ch * K + i] = sq_[i];
-            if (v_thr)
-#pragma unroll
-                for (int i = 0; i < GDN_MAX_KERNEL; i++)
-                    if ((uint32_t)i < K) co[(size_t)v_ch * K + i] = sv_[i];
-        }
-        // qs/ks/vs/gsc and red_* are rewritten next token only after every
-        // thread has passed this barrier.
-        lds_barrier();
-    };
-    if (a.tokens <= GDN_PREFETCH) {
-        // Every token's inputs are loaded before the first token's stores,
-        // so no wait inside the loop ever covers an earlier store (the
-        // verify rows' snapshots stream out while later tokens compute).
-        float pq[GDN_PREFETCH], pv[GDN_PREFETCH], pa[GDN_PREFETCH], pb[GDN_PREFETCH];
-#pragma unroll
-        for (int u = 0; u < GDN_PREFETCH; u++) load_in(min((uint32_t)u, a.tokens - 1), pq[u], pv[u], pa[u], pb[u]);
-        for (uint32_t t = 0; t < a.tokens; t++) {
-            step(t, pq[0], pv[0], pa[0], pb[0]);
-#pragma unroll
-            for (int u = 0; u + 1 < GDN_PREFETCH; u++) {
-                pq[u] = pq[u + 1];
-                pv[u] = pv[u + 1];
-                pa[u] = pa[u + 1];
-                pb[u] = pb[u + 1];
+            for (int r = 0; r < GDN_MAX_ROWS; r++) {
+                const uint32_t i = ig + GDN_GROUPS * r;
+                const bool ok = (uint32_t)r < nrows && i < dk;
+                kk[r] = ok ? ks[u][i] : 0.0f;
+                qq[r] = ok ? qs[u][i] : 0.0f;
+                sk += kk[r] * kk[r];
+                sqq += qq[r] * qq[r];
+                s[r] = s[r] * decay;
+                mem += s[r] * kk[r];
             }
-        }
-    } else {
-        float nxq, nxv, nga, ngb;
-        load_in(0, nxq, nxv, nga, ngb);
-        for (uint32_t t = 0; t < a.tokens; t++) {
-            const float cxq = nxq, cxv = nxv, cga = nga, cgb = ngb;
-            if (t + 1 < a.tokens) load_in(t + 1, nxq, nxv, nga, ngb);
-            step(t, cxq, cxv, cga, cgb);
+            red_mem[bsel][ig][jj] = mem;
+            if (jj == 0) {
+                red_nrm[bsel][0][ig] = sk;
+                red_nrm[bsel][1][ig] = sqq;
+            }
+            lds_barrier();
+            float memj = 0.0f, ssk = 0.0f, ssq = 0.0f;
+#pragma unroll
+            for (int gi = 0; gi < GDN_GROUPS; gi++) {
+                memj += red_mem[bsel][gi][jj];
+                ssk += red_nrm[bsel][0][gi];
+                ssq += red_nrm[bsel][1][gi];
+            }
+            const float kinv = 1.0f / sqrtf(ssk + 1e-6f), qinv = 1.0f / sqrtf(ssq + 1e-6f);
+            const float delta = (vjv - memj * kinv) * beta;
+            float o = 0.0f;
+#pragma unroll
+            for (int r = 0; r < GDN_MAX_ROWS; r++) {
+                s[r] += kk[r] * kinv * delta;
+                o += s[r] * qq[r];
+            }
+            red_out[bsel][ig][jj] = o;
+            lds_barrier();
+            if (ig == 0 && colok) {
+                float oj = 0.0f;
+#pragma unroll
+                for (int gi = 0; gi < GDN_GROUPS; gi++) oj += red_out[bsel][gi][jj];
+                a.out[((size_t)t * a.heads + h) * a.value_dim + j] = oj * qinv * qscale;
+            }
+            // Row snapshot: the state after row t.
+            if (a.snap_stride) store_state(a.state_out + (size_t)t * a.snap_stride);
         }
     }
     if (a.snap_stride) return;
