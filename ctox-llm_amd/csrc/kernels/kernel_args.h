@@ -137,6 +137,9 @@ struct TileMatvecArgs {
     const float *bias;      // NULL or f32[rows]
     float *output;          // [rows]
     uint64_t *partial;      // [chunks - 1][tiles * 16] when chunks > 1: f32 bits | seq << 32
+                            // ([chunks][tiles * 16] with arrive)
+    uint32_t *arrive;       // batch 1: per row tile, chunks arrived (zero between launches); NULL: the
+                            // last chunk combines
     uint32_t seq;           // this launch's tag in the partial slots (never 0)
     uint32_t sq_n;          // xmode 1: entries of sq_in (0: reduce the row itself)
     uint32_t parts_out;     // batch 1: write each chunk's s_out-scaled sum to output[chunk * out_stride + row]

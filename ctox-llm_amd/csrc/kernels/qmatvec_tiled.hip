@@ -18,8 +18,9 @@
 //    code, loads past the wave's tiles fall outside the buffer range and
 //    return zeros without memory traffic).
 //  * Splitting K into chunks spreads any matrix evenly over the CUs. The
-//    chunk sums of a row tile are combined by the wave that arrives last at
-//    the tile's counter, in chunk order, so the result is deterministic.
+//    chunk sums of a row tile are added in chunk order (deterministic) by
+//    the last chunk's waves when the whole launch is resident at once, else
+//    by the chunk that arrives last at the tile's count.
 #include "kernel_args.h"
 #include "lds_barrier.h"
 
@@ -240,15 +241,16 @@ __device__ __forceinline__ float4 frag_group_build(const TileMatvecArgs &a, uint
 }
 
 
-// Cross-chunk combine. The waves of the last chunk are dispatched after every
-// other chunk's waves (wave index = chunk * segs + segment), so they combine:
-// the other chunks store their row partials, tagged with the launch's
-// sequence number, as single 64-bit agent-scope atomic stores (coherent
-// across the XCDs' L2s without cache maintenance) and leave; the combining
-// lane polls its row's slots until every tag is this launch's and adds the
-// partials in chunk order (deterministic). Producers never wait, so the
-// polls always end; a poll count past CTOX_COMBINE_POLLS (only a broken
-// invariant) yields NaN, which the host reports, instead of a hang.
+// Cross-chunk combine. Partials are 64-bit slots (f32 bits | the launch's
+// sequence number << 32) written with single agent-scope atomic stores
+// (coherent across the XCDs' L2s without cache maintenance). In a launch
+// the device holds at once (the host checks the occupancy), the last
+// chunk's waves combine: the other chunks store and leave, and the
+// combining lane polls its row's slots until every tag is this launch's,
+// then adds them in chunk order. A larger launch combines by arrival
+// (tile_matvec). Either way a combining wave waits only for producers that
+// are resident, so the polls end; a poll count past CTOX_COMBINE_POLLS (only
+// a broken invariant) yields NaN, which the engine reports, not a hang.
 #define CTOX_COMBINE_POLLS (1u << 16)
 __device__ __forceinline__ void combine_store(uint64_t *slot, float v, uint32_t seq) {
     __hip_atomic_store(slot, (uint64_t)__float_as_uint(v) | ((uint64_t)seq << 32), __ATOMIC_RELAXED,
@@ -293,6 +295,45 @@ __device__ __forceinline__ float combine_poll(const uint64_t *slots, size_t stri
 }
 
 
+// Arrival combine: the sum over k < n of slots[k * stride] in chunk order,
+// the lane's own chunk `own_k` taken from `own`; polls until every other
+// slot carries this launch's tag. `want` false returns at once with 0.
+__device__ __forceinline__ float combine_poll_all(const uint64_t *slots, size_t stride, uint32_t n, uint32_t own_k,
+                                                  uint32_t seq, float own, bool want) {
+    float sum = 0.0f;
+    bool done = !want;
+    for (uint32_t poll = 0; __builtin_amdgcn_ballot_w64(!done) != 0; poll++) {
+        if (poll >= CTOX_COMBINE_POLLS) {
+            if (!done) sum = __builtin_nanf("");
+            break;
+        }
+        if (poll) __builtin_amdgcn_s_sleep(1);
+        if (!done) {
+            float s = 0.0f;
+            bool all = true;
+            for (uint32_t c0 = 0; c0 < n; c0 += 16) {
+                uint64_t pv[16];
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    pv[i] = __hip_atomic_load(&slots[(size_t)min(c0 + i, n - 1) * stride], __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    if (c0 + i < n) {
+                        const bool mine_k = c0 + i == own_k;
+                        all = all && (mine_k || (uint32_t)(pv[i] >> 32) == seq);
+                        s += mine_k ? own : __uint_as_float((uint32_t)pv[i]);
+                    }
+            }
+            if (all) {
+                sum = s;
+                done = true;
+            }
+        }
+    }
+    return sum;
+}
+
 // Producer side of the residual sums: per 16-row tile, sum of (res_h + y)^2
 // over its rows (the 16 lanes of one row group, DPP within the row).
 __device__ __forceinline__ void residual_tile_sum(const TileMatvecArgs &a, uint32_t tile, uint32_t row, bool mine,
@@ -303,7 +344,7 @@ __device__ __forceinline__ void residual_tile_sum(const TileMatvecArgs &a, uint3
     if (mine && j == 0) a.res_sq[tile] = s;
 }
 
-template <int DT, int U, int AB>
+template <int DT, int U, int AB, int ARR>
 __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
     using C = TlCfg<DT>;
     const uint32_t lane = threadIdx.x & 63;
@@ -482,20 +523,41 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
         return;
     }
     const size_t cstride = (size_t)a.tiles * CTOX_TILE_ROWS;
-    if (c + 1 < a.chunks) {
+    float sum;
+    if (ARR) {
+        // Arrival combine: every chunk stores its tagged partial, then counts
+        // itself in for the tile; the chunk that arrives last adds the
+        // tile's partials in chunk order and resets the count. It waits
+        // only for stores of waves that have already arrived (issued before
+        // their count), so no wave waits on one not yet dispatched.
         if (mine) combine_store(&a.partial[(size_t)c * cstride + row], val, a.seq);
-        return;
+        uint32_t old = 0;
+        if (mine && j == 0)
+            old = __hip_atomic_fetch_add(&a.arrive[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        old = __shfl(old, 16 * g);
+        const bool last = mine && old + 1 == a.chunks;
+        if (__builtin_amdgcn_ballot_w64(last) == 0) return;
+        sum = combine_poll_all(&a.partial[row], cstride, a.chunks, c, a.seq, val, last);
+        if (last && j == 0) __hip_atomic_store(&a.arrive[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (!last) return;
+    } else {
+        if (c + 1 < a.chunks) {
+            if (mine) combine_store(&a.partial[(size_t)c * cstride + row], val, a.seq);
+            return;
+        }
+        sum = combine_poll(&a.partial[row], cstride, a.chunks - 1, a.seq, val, mine);
     }
-    const float sum = combine_poll(&a.partial[row], cstride, a.chunks - 1, a.seq, val, mine);
     const float y = mine && row < a.rows ? tile_epilogue(sum / C::DEN, row, a) : 0.0f;
     if (mine && row < a.rows) a.output[row] = y;
     residual_tile_sum(a, tile, row, mine, y, j);
 }
 
 // ctox_q{2,4}_mv_tile{U}_gfx950 take prep-staged fragments; the _x
-// variants build them from x and s_in.
+// variants build them from x and s_in. The _arrive variants combine by
+// arrival (launches larger than the device holds at once).
 #define CTOX_TILE_KERNEL(name, dt, u, ab) \
-    extern "C" __global__ __launch_bounds__(256) void name(TileMatvecArgs a) { tile_matvec<dt, u, ab>(a); }
+    extern "C" __global__ __launch_bounds__(256) void name(TileMatvecArgs a) { tile_matvec<dt, u, ab, 0>(a); } \
+    extern "C" __global__ __launch_bounds__(256) void name##_arrive(TileMatvecArgs a) { tile_matvec<dt, u, ab, 1>(a); }
 CTOX_TILE_KERNEL(ctox_q2_mv_tile1_gfx950, 0, 1, 0)
 CTOX_TILE_KERNEL(ctox_q2_mv_tile2_gfx950, 0, 2, 0)
 CTOX_TILE_KERNEL(ctox_q2_mv_tile3_gfx950, 0, 3, 0)

@@ -30,7 +30,8 @@
 
 // Static scratch of the allocation-free entry point (noalloc.hip).
 extern "C" ctox_status ctox_noalloc_setup(int device);
-extern "C" ctox_status ctox_noalloc_slots(int device, void *stream, uint64_t **ptr, size_t *bytes, uint32_t *seq);
+extern "C" ctox_status ctox_noalloc_slots(int device, void *stream, uint64_t **ptr, size_t *bytes, uint32_t *seq,
+                                          uint32_t **arrive, size_t *arrive_n);
 
 // ---- embedded gfx950 code object ----
 extern "C" const unsigned char ctox_hsaco_begin[];
@@ -161,6 +162,7 @@ struct ctox_hip_backend {
     hipFunction_t tile[2][CTOX_TILE_MAXU] = {};
     // The same with the activation fragments built inside the kernel.
     hipFunction_t tilex[2][CTOX_TILE_MAXU] = {};
+    hipFunction_t tile_arr[2][2][CTOX_TILE_MAXU] = {};  // [staged|built][q4][u - 1], combine by arrival
     // Small-M tiled kernels per dtype: [0] 2..4 rows, [1] 5..8 rows (2 row tiles per wave).
     hipFunction_t tilem[2][2] = {};
     // The same building the rows' fragments in the kernel, per row count 2..5.
@@ -171,9 +173,12 @@ struct ctox_hip_backend {
     hipFunction_t gdn_fused = nullptr, gdn_fused_blk = nullptr;
     int cus = 0;
     uint32_t tile_u = 0;  // CTOX_TILE_U: fixed row tiles per wave (0 = planned)
+    int arrive = -1;      // CTOX_ARRIVE: 1 / 0 forces the batch-1 combine by arrival / by the last chunk
+    uint32_t tile_cap[2][2][CTOX_TILE_MAXU] = {};  // [staged|built][q4][u - 1]: workgroups resident at once
     // Tiled matvec chunk partials (64-bit slots tagged with a launch sequence
     // number; zeroed when allocated) and the last sequence number used.
     DevBuf tpart;
+    DevBuf tarrive;  // batch-1 per-tile arrival counts (zero between launches)
     uint32_t tile_seq = 0;
     // Tiled copies of raw device weights (ctox_hip_register_tiled_weights).
     std::unordered_map<const void *, TiledCopy> raw_tiled;
@@ -390,6 +395,8 @@ struct PartialSlots {
     uint64_t *p = nullptr;
     size_t bytes = 0;
     uint32_t seq = 0;
+    uint32_t *arrive = nullptr;  // batch-1 arrival counts
+    size_t arrive_n = 0;
 };
 
 // Small-M rows the in-kernel fragment build takes (ctox_q*_mv_tilemx*).
@@ -518,15 +525,26 @@ ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy 
     if (d_input) segs = (segs + 3) & ~3u;
     const size_t waves = (size_t)segs * t.chunks;
     if ((waves + 3) / 4 > 0x7fffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
-    const size_t slot_bytes = (size_t)(t.chunks - 1) * t.tiles * CTOX_TILE_ROWS * sizeof(uint64_t);
-    if (ps && slot_bytes > ps->bytes)
+    // Chunks meet in one of two ways. When every workgroup of the launch is
+    // resident at once, the last chunk's waves combine (they wait only for
+    // resident producers, whatever the dispatch order). Otherwise by
+    // arrival: every chunk stores its partial and counts itself in, and the
+    // last to arrive for a tile combines, waiting only for chunks that have
+    // already arrived.
+    const bool combine = t.chunks > 1 && !(xf && xf->parts_out);
+    const size_t wgs = ((size_t)segs * t.chunks + 3) / 4;
+    const bool arrive = combine && (b->arrive >= 0 ? b->arrive != 0 : wgs > b->tile_cap[d_input ? 1 : 0][q4][u - 1]);
+    const size_t slot_bytes = (size_t)(arrive ? t.chunks : t.chunks - 1) * t.tiles * CTOX_TILE_ROWS * sizeof(uint64_t);
+    if (ps && combine && (slot_bytes > ps->bytes || (arrive && t.tiles > ps->arrive_n)))
         return fail(CTOX_ERR_MEMORY_BUDGET, "combine slots need %zu bytes, the static scratch holds %zu", slot_bytes,
                     ps->bytes);
-    if (t.chunks > 1 && !ps) {
+    if (combine && !ps) {
         ctox_status st = ensure(b, b->tpart, slot_bytes, true);
+        if (!st && arrive) st = ensure(b, b->tarrive, (size_t)t.tiles * sizeof(uint32_t), true);
         if (st) return st;
     }
     TileMatvecArgs a{};
+    a.arrive = arrive ? (ps ? ps->arrive : (uint32_t *)b->tarrive.ptr) : nullptr;
     a.weights = (const uint8_t *)t.d;
     a.xa = (const int8_t *)b->xa[q4].ptr;
     a.xc = (const float *)b->xc[q4].ptr;
@@ -565,7 +583,8 @@ ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy 
         a.a_parts = xf->a_parts;
         a.a_pstride = xf->a_pstride;
     }
-    hipFunction_t f = d_input ? b->tilex[q4][u - 1] : b->tile[q4][u - 1];
+    hipFunction_t f = arrive ? b->tile_arr[d_input ? 1 : 0][q4][u - 1]
+                             : (d_input ? b->tilex[q4][u - 1] : b->tile[q4][u - 1]);
     return launch(f, dim3((unsigned)((waves + 3) / 4)), dim3(256), s, a, "ctox_q*_mv_tile*_gfx950");
 }
 
@@ -816,6 +835,14 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->tilex[0][2], "ctox_q2_mv_tile3x_gfx950"}, {&b->tilex[0][3], "ctox_q2_mv_tile4x_gfx950"},
                {&b->tilex[1][0], "ctox_q4_mv_tile1x_gfx950"}, {&b->tilex[1][1], "ctox_q4_mv_tile2x_gfx950"},
                {&b->tilex[1][2], "ctox_q4_mv_tile3x_gfx950"}, {&b->tilex[1][3], "ctox_q4_mv_tile4x_gfx950"},
+               {&b->tile_arr[0][0][0], "ctox_q2_mv_tile1_gfx950_arrive"}, {&b->tile_arr[0][0][1], "ctox_q2_mv_tile2_gfx950_arrive"},
+               {&b->tile_arr[0][0][2], "ctox_q2_mv_tile3_gfx950_arrive"}, {&b->tile_arr[0][0][3], "ctox_q2_mv_tile4_gfx950_arrive"},
+               {&b->tile_arr[0][1][0], "ctox_q4_mv_tile1_gfx950_arrive"}, {&b->tile_arr[0][1][1], "ctox_q4_mv_tile2_gfx950_arrive"},
+               {&b->tile_arr[0][1][2], "ctox_q4_mv_tile3_gfx950_arrive"}, {&b->tile_arr[0][1][3], "ctox_q4_mv_tile4_gfx950_arrive"},
+               {&b->tile_arr[1][0][0], "ctox_q2_mv_tile1x_gfx950_arrive"}, {&b->tile_arr[1][0][1], "ctox_q2_mv_tile2x_gfx950_arrive"},
+               {&b->tile_arr[1][0][2], "ctox_q2_mv_tile3x_gfx950_arrive"}, {&b->tile_arr[1][0][3], "ctox_q2_mv_tile4x_gfx950_arrive"},
+               {&b->tile_arr[1][1][0], "ctox_q4_mv_tile1x_gfx950_arrive"}, {&b->tile_arr[1][1][1], "ctox_q4_mv_tile2x_gfx950_arrive"},
+               {&b->tile_arr[1][1][2], "ctox_q4_mv_tile3x_gfx950_arrive"}, {&b->tile_arr[1][1][3], "ctox_q4_mv_tile4x_gfx950_arrive"},
                {&b->tilem[0][0], "ctox_q2_mv_tilem1_gfx950"}, {&b->tilem[0][1], "ctox_q2_mv_tilem2_gfx950"},
                {&b->tilem[1][0], "ctox_q4_mv_tilem1_gfx950"}, {&b->tilem[1][1], "ctox_q4_mv_tilem2_gfx950"},
                {&b->tilemx[0][0], "ctox_q2_mv_tilemx2_gfx950"}, {&b->tilemx[0][1], "ctox_q2_mv_tilemx3_gfx950"},
@@ -842,6 +869,19 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
     // CTOX_SMALL_M_BUILD=0: 2..5-row projections stage their fragments in a
     // separate launch (the tilem kernels) instead of building them in-kernel.
     if (const char *m = std::getenv("CTOX_SMALL_M_BUILD")) b->no_mx = std::atoi(m) == 0;
+    if (const char *m = std::getenv("CTOX_ARRIVE")) b->arrive = std::atoi(m) != 0;
+    // How many workgroups of each batch-1 tiled kernel the device holds at
+    // once: launches within it may combine by the last chunk's waves (every
+    // producer is resident whatever the dispatch order); larger ones combine
+    // by arrival.
+    for (int x = 0; x < 2; x++)
+        for (int q = 0; q < 2; q++)
+            for (int u = 0; u < CTOX_TILE_MAXU; u++) {
+                int n = 0;
+                hipFunction_t f = x ? b->tilex[q][u] : b->tile[q][u];
+                if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, 256, 0) != hipSuccess) n = 0;
+                b->tile_cap[x][q][u] = (uint32_t)std::max(0, n) * (uint32_t)b->cus;
+            }
     if (const char *u = std::getenv("CTOX_TILE_U")) {
         const int v = std::atoi(u);
         if (v >= 1 && v <= CTOX_TILE_MAXU) b->tile_u = (uint32_t)v;
@@ -855,7 +895,7 @@ extern "C" void ctox_hip_backend_destroy(ctox_hip_backend *b) {
     (void)hipSetDevice(b->device);
     (void)hipDeviceSynchronize();
     DevBuf *bufs[] = {&b->xa[0], &b->xa[1], &b->xc[0], &b->xc[1], &b->norms, &b->tok, &b->stats, &b->attn,
-                      &b->tpart};
+                      &b->tpart, &b->tarrive};
     for (auto &kv : b->raw_tiled)
         if (kv.second.d) (void)hipFree(kv.second.d);
     for (DevBuf *d : bufs)
@@ -1074,7 +1114,7 @@ extern "C" ctox_status ctox_hip_launch_fused_matvec_noalloc(ctox_hip_backend *b,
     if (!t) return fail(CTOX_ERR_UNSUPPORTED_OPERATION, "allocation-free launch needs registered tiled weights");
     hipStream_t s = pick_stream(b, stream);
     PartialSlots ps;
-    if (ctox_noalloc_slots(b->device, s, &ps.p, &ps.bytes, &ps.seq) != CTOX_OK)
+    if (ctox_noalloc_slots(b->device, s, &ps.p, &ps.bytes, &ps.seq, &ps.arrive, &ps.arrive_n) != CTOX_OK)
         return fail(CTOX_ERR_INVALID_STATE, "static scratch unavailable");
     const uint32_t sk = d_s_in ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, ok = d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE;
     if (batch == 1)

@@ -62,7 +62,12 @@ extern "C" ctox_status ctox_noalloc_setup(int device) {
 
 // The device's slots and the tag of the next launch, queued on `stream`
 // (a wrap of the tag clears the array first, with a kernel).
-extern "C" ctox_status ctox_noalloc_slots(int device, void *stream, uint64_t **ptr, size_t *bytes, uint32_t *seq) {
+// The last CTOX_NOALLOC_ARRIVE_BYTES of the array are the batch-1 kernel's
+// per-tile arrival counts (zero between launches: each launch's last arrival
+// resets its count, and a wrap clears the whole array); the rest are slots.
+#define CTOX_NOALLOC_ARRIVE_BYTES (256u << 10)
+extern "C" ctox_status ctox_noalloc_slots(int device, void *stream, uint64_t **ptr, size_t *bytes, uint32_t *seq,
+                                          uint32_t **arrive, size_t *arrive_n) {
     if (device < 0 || device >= kMaxDevices) return CTOX_ERR_UNSUPPORTED_OPERATION;
     DeviceScratch &d = g_dev[device];
     std::lock_guard<std::mutex> lock(d.m);
@@ -73,7 +78,9 @@ extern "C" ctox_status ctox_noalloc_slots(int device, void *stream, uint64_t **p
         d.seq = 1;
     }
     *ptr = d.ptr;
-    *bytes = CTOX_NOALLOC_SCRATCH_BYTES;
+    *bytes = CTOX_NOALLOC_SCRATCH_BYTES - CTOX_NOALLOC_ARRIVE_BYTES;
     *seq = d.seq;
+    *arrive = (uint32_t *)((char *)d.ptr + *bytes);
+    *arrive_n = CTOX_NOALLOC_ARRIVE_BYTES / 4;
     return CTOX_OK;
 }

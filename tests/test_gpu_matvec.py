@@ -181,6 +181,40 @@ def test_baseline_full_shapes(hip, orc, cfg):
         say(f"  normwise rel err {n:.3e}")
 
 
+
+@pytest.mark.parametrize("mode", ["1", "0"])
+def test_batch1_combine_modes(orc, mode, monkeypatch):
+    """Both ways the batch-1 tiled kernel's chunks meet give the oracle's
+    rows: by arrival (the last chunk to arrive for a tile adds them, used for
+    launches larger than the device holds at once) and by the last chunk's
+    waves (used when every workgroup is resident). CTOX_ARRIVE forces one
+    of them for a backend of this test's own; the 151936-row LM-head shape
+    takes the arrival path by itself."""
+    import ctox_hip
+    monkeypatch.setenv("CTOX_ARRIVE", mode)
+    hip2 = ctox_hip.HipBackend(0)
+    try:
+        for dtype, rows, cols, xkind in ((1, 17408, 5120, "normal"), (0, 5120, 17408, "swiglu"),
+                                         (1, 4096 + 48, 1024, "normal")):
+            say(f"case combine mode={mode} dtype={dtype} {rows}x{cols}")
+            op, parts = make_case(dtype, rows, cols, 41, "f16", bias=False, xkind=xkind)
+            for rep in range(2):  # the counts are back at zero for the next launch
+                got = resident_run(hip2, op, parts[1])
+                ref = oracle_rows(orc, dtype, rows, cols, parts, ctox_hip.Activation.Identity)
+                check(got, ref, f"combine mode={mode} rep={rep}")
+    finally:
+        hip2.close()
+    monkeypatch.delenv("CTOX_ARRIVE")
+    hip3 = ctox_hip.HipBackend(0)
+    try:
+        say("case combine default: LM-head shape 151936x5120")
+        op, parts = make_case(1, 151936, 5120, 43, "f16", bias=False)
+        got = resident_run(hip3, op, parts[1])
+        ref = oracle_rows(orc, 1, 151936, 5120, parts, ctox_hip.Activation.Identity)
+        check(got, ref, "LM head")
+    finally:
+        hip3.close()
+
 # One decoder layer (Q/src/tensor_contract.rs:70-240): q_proj 12288 (crate) / 6144 (BASELINE),
 # k/v 1024, o 5120x6144, gate/up 17408x5120, down 5120x17408.
 LAYER = [("q_proj_crate", 1, 12288, 5120), ("q_proj_baseline", 1, 6144, 5120), ("k_proj", 1, 1024, 5120),
