@@ -609,7 +609,74 @@ __device__ __forceinline__ void residual_tile_sum_m(const TileMatvecArgs &a, uin
 
 // MR = M, the row count, is a compile-time constant: every LDS address of
 // the MFMA loop is a per-lane base plus an immediate offset.
-template <int DT, int U, int TG>
+// Tail of the small-M kernels: lane (g, j) of unit k and token group tg
+// holds (token 4 tg + g, row j) of the wave's tiles t0 .. t0 + n - 1 for
+// chunk c. Partials [chunk][token][tiles * 16] meet as in the batch-1
+// kernel: by the last chunk's waves when the launch is resident at once
+// (ARR = 0), else by the chunk that arrives last at the tile's count.
+template <int DT, int U, int TG, int ARR>
+__device__ __forceinline__ void small_m_finish(const TileMatvecArgs &a, uint32_t c, uint32_t t0, uint32_t n,
+                                               uint32_t g, uint32_t j, uint32_t M, const float (&acc)[U][TG]) {
+    using C = TlCfg<DT>;
+    const size_t tstride = (size_t)a.tiles * CTOX_TILE_ROWS, cstride = tstride * M;
+    bool last[U];
+    if (a.chunks == 1) {
+#pragma unroll
+        for (int k = 0; k < U; k++) last[k] = true;
+    } else if (ARR) {
+#pragma unroll
+        for (int k = 0; k < U; k++)
+#pragma unroll
+            for (int tg = 0; tg < TG; tg++) {
+                const uint32_t tok = 4 * tg + g, row = (t0 + k) * CTOX_TILE_ROWS + j;
+                if ((uint32_t)k < n && tok < M) combine_store(&a.partial[c * cstride + tok * tstride + row], acc[k][tg], a.seq);
+            }
+        bool any = false;
+#pragma unroll
+        for (int k = 0; k < U; k++) {
+            uint32_t old = 0;
+            if ((threadIdx.x & 63) == 0 && (uint32_t)k < n)
+                old = __hip_atomic_fetch_add(&a.arrive[t0 + k], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            old = __builtin_amdgcn_readfirstlane(old);
+            last[k] = (uint32_t)k < n && old + 1 == a.chunks;
+            any = any || last[k];
+        }
+        if (!any) return;
+    } else {
+        if (c + 1 < a.chunks) {
+#pragma unroll
+            for (int k = 0; k < U; k++)
+#pragma unroll
+                for (int tg = 0; tg < TG; tg++) {
+                    const uint32_t tok = 4 * tg + g, row = (t0 + k) * CTOX_TILE_ROWS + j;
+                    if ((uint32_t)k < n && tok < M) combine_store(&a.partial[c * cstride + tok * tstride + row], acc[k][tg], a.seq);
+                }
+            return;
+        }
+#pragma unroll
+        for (int k = 0; k < U; k++) last[k] = true;
+    }
+#pragma unroll
+    for (int k = 0; k < U; k++) {
+        if (!last[k]) continue;  // wave-uniform
+#pragma unroll
+        for (int tg = 0; tg < TG; tg++) {
+            const uint32_t tok = 4 * tg + g, tile = t0 + k, row = tile * CTOX_TILE_ROWS + j;
+            const bool want = (uint32_t)k < n && tok < M;
+            float sum = acc[k][tg];
+            if (a.chunks > 1)
+                sum = ARR ? combine_poll_all(&a.partial[tok * tstride + row], cstride, a.chunks, c, a.seq, acc[k][tg], want)
+                          : combine_poll(&a.partial[tok * tstride + row], cstride, a.chunks - 1, a.seq, acc[k][tg], want);
+            const float y = want && row < a.rows ? tile_epilogue(sum / C::DEN, row, a) : 0.0f;
+            if (want && row < a.rows) a.output[(size_t)tok * a.out_stride + row] = y;
+            if (a.res_sq) residual_tile_sum_m(a, min(tok, M - 1), tile, row, want, y, j);
+        }
+        if (ARR && a.chunks > 1 && (threadIdx.x & 63) == 0)
+            __hip_atomic_store(&a.arrive[t0 + k], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+template <int DT, int U, int TG, int ARR>
 __device__ __forceinline__ void tile_matvec_m(const TileMatvecArgs &a) {
     using C = TlCfg<DT>;
     constexpr uint32_t MAXM = 4 * TG;
@@ -714,47 +781,12 @@ __device__ __forceinline__ void tile_matvec_m(const TileMatvecArgs &a) {
             }
         }
     }
-    // Lane (g, j) of unit k and token group tg holds (token 4 tg + g, row j).
-    if (a.chunks == 1) {
-#pragma unroll
-        for (int k = 0; k < U; k++)
-#pragma unroll
-            for (int tg = 0; tg < TG; tg++) {
-                const uint32_t tok = 4 * tg + g, tile = t0 + k, row = tile * CTOX_TILE_ROWS + j;
-                const bool want = (uint32_t)k < n && tok < M;
-                const float y = want && row < a.rows ? tile_epilogue(acc[k][tg] / C::DEN, row, a) : 0.0f;
-                if (want && row < a.rows) a.output[(size_t)tok * a.out_stride + row] = y;
-                if (a.res_sq) residual_tile_sum_m(a, min(tok, M - 1), tile, row, want, y, j);
-            }
-        return;
-    }
-    // Partials [chunk][token][tiles * 16], combined as in the batch-1 kernel.
-    const size_t tstride = (size_t)a.tiles * CTOX_TILE_ROWS, cstride = tstride * M;
-    if (c + 1 < a.chunks) {
-#pragma unroll
-        for (int k = 0; k < U; k++)
-#pragma unroll
-            for (int tg = 0; tg < TG; tg++) {
-                const uint32_t tok = 4 * tg + g, row = (t0 + k) * CTOX_TILE_ROWS + j;
-                if ((uint32_t)k < n && tok < M) combine_store(&a.partial[c * cstride + tok * tstride + row], acc[k][tg], a.seq);
-            }
-        return;
-    }
-#pragma unroll
-    for (int k = 0; k < U; k++)
-#pragma unroll
-        for (int tg = 0; tg < TG; tg++) {
-            const uint32_t tok = 4 * tg + g, tile = t0 + k, row = tile * CTOX_TILE_ROWS + j;
-            const bool want = (uint32_t)k < n && tok < M;
-            const float sum = combine_poll(&a.partial[tok * tstride + row], cstride, a.chunks - 1, a.seq, acc[k][tg], want);
-            const float y = want && row < a.rows ? tile_epilogue(sum / C::DEN, row, a) : 0.0f;
-            if (want && row < a.rows) a.output[(size_t)tok * a.out_stride + row] = y;
-            if (a.res_sq) residual_tile_sum_m(a, min(tok, M - 1), tile, row, want, y, j);
-        }
+    small_m_finish<DT, U, TG, ARR>(a, c, t0, n, g, j, M, acc);
 }
 
 #define CTOX_TILE_M_KERNEL(name, dt, u, tg) \
-    extern "C" __global__ __launch_bounds__(256) void name(TileMatvecArgs a) { tile_matvec_m<dt, u, tg>(a); }
+    extern "C" __global__ __launch_bounds__(256) void name(TileMatvecArgs a) { tile_matvec_m<dt, u, tg, 0>(a); } \
+    extern "C" __global__ __launch_bounds__(256) void name##_arrive(TileMatvecArgs a) { tile_matvec_m<dt, u, tg, 1>(a); }
 CTOX_TILE_M_KERNEL(ctox_q2_mv_tilem1_gfx950, 0, 2, 1)
 CTOX_TILE_M_KERNEL(ctox_q2_mv_tilem2_gfx950, 0, 2, 2)
 CTOX_TILE_M_KERNEL(ctox_q4_mv_tilem1_gfx950, 1, 2, 1)
@@ -786,7 +818,7 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, void *lds, u
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, 0, 0, 0);
 }
 
-template <int DT, int MR>
+template <int DT, int MR, int ARR>
 __device__ __forceinline__ void tile_matvec_mx(const TileMatvecArgs &a) {
     using C = TlCfg<DT>;
     constexpr uint32_t U = 2, TG = (MR + 3) / 4, INB = 2048;
@@ -943,35 +975,12 @@ __device__ __forceinline__ void tile_matvec_mx(const TileMatvecArgs &a) {
             }
         }
     }
-    // Lane (g, j) of unit k and token group tg holds (row 4 tg + g, output row j).
-    const size_t tstride = (size_t)a.tiles * CTOX_TILE_ROWS, cstride = tstride * M;
-    if (a.chunks > 1 && c + 1 < a.chunks) {
-#pragma unroll
-        for (int k = 0; k < (int)U; k++)
-#pragma unroll
-            for (int tg = 0; tg < (int)TG; tg++) {
-                const uint32_t tok = 4 * tg + g, row = (t0 + k) * CTOX_TILE_ROWS + j;
-                if ((uint32_t)k < n && tok < M) combine_store(&a.partial[c * cstride + tok * tstride + row], acc[k][tg], a.seq);
-            }
-        return;
-    }
-#pragma unroll
-    for (int k = 0; k < (int)U; k++)
-#pragma unroll
-        for (int tg = 0; tg < (int)TG; tg++) {
-            const uint32_t tok = 4 * tg + g, tile = t0 + k, row = tile * CTOX_TILE_ROWS + j;
-            const bool want = (uint32_t)k < n && tok < M;
-            const float sum = a.chunks == 1 ? acc[k][tg]
-                                            : combine_poll(&a.partial[tok * tstride + row], cstride, a.chunks - 1,
-                                                           a.seq, acc[k][tg], want);
-            const float y = want && row < a.rows ? tile_epilogue(sum / C::DEN, row, a) : 0.0f;
-            if (want && row < a.rows) a.output[(size_t)tok * a.out_stride + row] = y;
-            if (a.res_sq) residual_tile_sum_m(a, min(tok, M - 1), tile, row, want, y, j);
-        }
+    small_m_finish<DT, U, TG, ARR>(a, c, t0, n, g, j, M, acc);
 }
 
 #define CTOX_TILE_MX_KERNEL(name, dt, mr) \
-    extern "C" __global__ __launch_bounds__(256, 2) void name(TileMatvecArgs a) { tile_matvec_mx<dt, mr>(a); }
+    extern "C" __global__ __launch_bounds__(256, 2) void name(TileMatvecArgs a) { tile_matvec_mx<dt, mr, 0>(a); } \
+    extern "C" __global__ __launch_bounds__(256, 2) void name##_arrive(TileMatvecArgs a) { tile_matvec_mx<dt, mr, 1>(a); }
 CTOX_TILE_MX_KERNEL(ctox_q2_mv_tilemx2_gfx950, 0, 2)
 CTOX_TILE_MX_KERNEL(ctox_q2_mv_tilemx3_gfx950, 0, 3)
 CTOX_TILE_MX_KERNEL(ctox_q2_mv_tilemx4_gfx950, 0, 4)

@@ -165,16 +165,20 @@ struct ctox_hip_backend {
     hipFunction_t tile_arr[2][2][CTOX_TILE_MAXU] = {};  // [staged|built][q4][u - 1], combine by arrival
     // Small-M tiled kernels per dtype: [0] 2..4 rows, [1] 5..8 rows (2 row tiles per wave).
     hipFunction_t tilem[2][2] = {};
+    hipFunction_t tilem_arr[2][2] = {};  // combine by arrival
     // The same building the rows' fragments in the kernel, per row count 2..5.
     hipFunction_t tilemx[2][4] = {};
+    hipFunction_t tilemx_arr[2][4] = {};  // combine by arrival
     bool no_mx = false;
     bool noalloc_ok = false;  // the static scratch of ctox_hip_launch_fused_matvec_noalloc is set up
     hipFunction_t repack = nullptr;
     hipFunction_t gdn_fused = nullptr, gdn_fused_blk = nullptr;
     int cus = 0;
     uint32_t tile_u = 0;  // CTOX_TILE_U: fixed row tiles per wave (0 = planned)
-    int arrive = -1;      // CTOX_ARRIVE: 1 / 0 forces the batch-1 combine by arrival / by the last chunk
+    int arrive = -1;      // CTOX_ARRIVE: 1 / 0 forces the tiled combine by arrival / by the last chunk
     uint32_t tile_cap[2][2][CTOX_TILE_MAXU] = {};  // [staged|built][q4][u - 1]: workgroups resident at once
+    uint32_t tilem_cap[2][2] = {};                  // [q4][tg - 1], same for the small-M kernels
+    uint32_t tilemx_cap[2][4] = {};                 // [q4][rows - 2]
     // Tiled matvec chunk partials (64-bit slots tagged with a launch sequence
     // number; zeroed when allocated) and the last sequence number used.
     DevBuf tpart;
@@ -599,12 +603,18 @@ ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCop
     const uint32_t segs = (((t.tiles + u - 1) / u) + 3) & ~3u;
     const size_t waves = (size_t)segs * t.chunks;
     if (waves / 4 > 0x7fffffffu || out_stride > 0xffffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
+    // Chunks meet as in the batch-1 launch: by the last chunk when the
+    // device holds every workgroup at once, else by arrival.
+    const bool arrive = t.chunks > 1 && (b->arrive >= 0 ? b->arrive != 0 : waves / 4 > b->tilem_cap[q4][tg - 1]);
     if (t.chunks > 1) {
-        ctox_status st =
-            ensure(b, b->tpart, (size_t)(t.chunks - 1) * batch * t.tiles * CTOX_TILE_ROWS * sizeof(uint64_t), true);
+        ctox_status st = ensure(b, b->tpart,
+                                (size_t)(arrive ? t.chunks : t.chunks - 1) * batch * t.tiles * CTOX_TILE_ROWS * sizeof(uint64_t),
+                                true);
+        if (!st && arrive) st = ensure(b, b->tarrive, (size_t)t.tiles * sizeof(uint32_t), true);
         if (st) return st;
     }
     TileMatvecArgs a{};
+    a.arrive = arrive ? (uint32_t *)b->tarrive.ptr : nullptr;
     a.weights = (const uint8_t *)t.d;
     a.xa = (const int8_t *)b->xa[q4].ptr;
     a.xc = (const float *)b->xc[q4].ptr;
@@ -625,7 +635,7 @@ ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCop
     a.out_stride = (uint32_t)out_stride;
     a.res_h = res_h;
     a.res_sq = res_sq;
-    return launch(b->tilem[q4][tg - 1], dim3((unsigned)(waves / 4)), dim3(256), s, a, "ctox_q*_mv_tilem*_gfx950");
+    return launch(arrive ? b->tilem_arr[q4][tg - 1] : b->tilem[q4][tg - 1], dim3((unsigned)(waves / 4)), dim3(256), s, a, "ctox_q*_mv_tilem*_gfx950");
 }
 
 // One launch of the small-M tiled matvec that builds its 2..5 rows'
@@ -640,15 +650,20 @@ ctox_status run_tile_matvec_mx(ctox_hip_backend *b, int32_t dtype, const TiledCo
     const size_t waves = (size_t)segs * t.chunks;
     if (batch < 2 || batch > kMaxBuildRows) return fail(CTOX_ERR_SHAPE, "in-kernel row build takes 2..5 rows");
     if (waves / 4 > 0x7fffffffu || out_stride > 0xffffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
-    const size_t slot_bytes = (size_t)(t.chunks - 1) * batch * t.tiles * CTOX_TILE_ROWS * sizeof(uint64_t);
-    if (ps && slot_bytes > ps->bytes)
+    const bool arrive =
+        t.chunks > 1 && (b->arrive >= 0 ? b->arrive != 0 : waves / 4 > b->tilemx_cap[q4][batch - 2]);
+    const size_t slot_bytes =
+        (size_t)(arrive ? t.chunks : t.chunks - 1) * batch * t.tiles * CTOX_TILE_ROWS * sizeof(uint64_t);
+    if (ps && t.chunks > 1 && (slot_bytes > ps->bytes || (arrive && t.tiles > ps->arrive_n)))
         return fail(CTOX_ERR_MEMORY_BUDGET, "combine slots need %zu bytes, the static scratch holds %zu", slot_bytes,
                     ps->bytes);
     if (t.chunks > 1 && !ps) {
         ctox_status st = ensure(b, b->tpart, slot_bytes, true);
+        if (!st && arrive) st = ensure(b, b->tarrive, (size_t)t.tiles * sizeof(uint32_t), true);
         if (st) return st;
     }
     TileMatvecArgs a{};
+    a.arrive = arrive ? (ps ? ps->arrive : (uint32_t *)b->tarrive.ptr) : nullptr;
     a.weights = (const uint8_t *)t.d;
     a.s_out = d_s_out;
     a.bias = d_bias;
@@ -683,7 +698,7 @@ ctox_status run_tile_matvec_mx(ctox_hip_backend *b, int32_t dtype, const TiledCo
     a.out_stride = (uint32_t)out_stride;
     a.a_stride = xf.a_stride;
     a.b_stride = xf.b_stride;
-    return launch(b->tilemx[q4][batch - 2], dim3((unsigned)(waves / 4)), dim3(256), s, a,
+    return launch(arrive ? b->tilemx_arr[q4][batch - 2] : b->tilemx[q4][batch - 2], dim3((unsigned)(waves / 4)), dim3(256), s, a,
                   "ctox_q*_mv_tilemx*_gfx950");
 }
 
@@ -849,6 +864,12 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->tilemx[0][2], "ctox_q2_mv_tilemx4_gfx950"}, {&b->tilemx[0][3], "ctox_q2_mv_tilemx5_gfx950"},
                {&b->tilemx[1][0], "ctox_q4_mv_tilemx2_gfx950"}, {&b->tilemx[1][1], "ctox_q4_mv_tilemx3_gfx950"},
                {&b->tilemx[1][2], "ctox_q4_mv_tilemx4_gfx950"}, {&b->tilemx[1][3], "ctox_q4_mv_tilemx5_gfx950"},
+               {&b->tilem_arr[0][0], "ctox_q2_mv_tilem1_gfx950_arrive"}, {&b->tilem_arr[0][1], "ctox_q2_mv_tilem2_gfx950_arrive"},
+               {&b->tilem_arr[1][0], "ctox_q4_mv_tilem1_gfx950_arrive"}, {&b->tilem_arr[1][1], "ctox_q4_mv_tilem2_gfx950_arrive"},
+               {&b->tilemx_arr[0][0], "ctox_q2_mv_tilemx2_gfx950_arrive"}, {&b->tilemx_arr[0][1], "ctox_q2_mv_tilemx3_gfx950_arrive"},
+               {&b->tilemx_arr[0][2], "ctox_q2_mv_tilemx4_gfx950_arrive"}, {&b->tilemx_arr[0][3], "ctox_q2_mv_tilemx5_gfx950_arrive"},
+               {&b->tilemx_arr[1][0], "ctox_q4_mv_tilemx2_gfx950_arrive"}, {&b->tilemx_arr[1][1], "ctox_q4_mv_tilemx3_gfx950_arrive"},
+               {&b->tilemx_arr[1][2], "ctox_q4_mv_tilemx4_gfx950_arrive"}, {&b->tilemx_arr[1][3], "ctox_q4_mv_tilemx5_gfx950_arrive"},
                {&b->repack, "ctox_tile_repack_gfx950"}, {&b->gdn_fused, "ctox_gdn_fused_gfx950"}, {&b->gdn_fused_blk, "ctox_gdn_fused_blk_gfx950"},
                {&b->finite, "ctox_finite_check_gfx950"}, {&b->gather, "ctox_gather_rows_gfx950"}, {&b->stream_read, "ctox_stream_read_gfx950"},
                {&b->topk_part, "ctox_topk_part_gfx950"}, {&b->topk_final, "ctox_topk_final_gfx950"}};
@@ -870,18 +891,23 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
     // separate launch (the tilem kernels) instead of building them in-kernel.
     if (const char *m = std::getenv("CTOX_SMALL_M_BUILD")) b->no_mx = std::atoi(m) == 0;
     if (const char *m = std::getenv("CTOX_ARRIVE")) b->arrive = std::atoi(m) != 0;
-    // How many workgroups of each batch-1 tiled kernel the device holds at
-    // once: launches within it may combine by the last chunk's waves (every
+    // How many workgroups of each tiled kernel the device holds at once:
+    // launches within it may combine by the last chunk's waves (every
     // producer is resident whatever the dispatch order); larger ones combine
     // by arrival.
-    for (int x = 0; x < 2; x++)
-        for (int q = 0; q < 2; q++)
-            for (int u = 0; u < CTOX_TILE_MAXU; u++) {
-                int n = 0;
-                hipFunction_t f = x ? b->tilex[q][u] : b->tile[q][u];
-                if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, 256, 0) != hipSuccess) n = 0;
-                b->tile_cap[x][q][u] = (uint32_t)std::max(0, n) * (uint32_t)b->cus;
-            }
+    auto cap = [&](hipFunction_t f) {
+        int n = 0;
+        if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, 256, 0) != hipSuccess) n = 0;
+        return (uint32_t)std::max(0, n) * (uint32_t)b->cus;
+    };
+    for (int q = 0; q < 2; q++) {
+        for (int u = 0; u < CTOX_TILE_MAXU; u++) {
+            b->tile_cap[0][q][u] = cap(b->tile[q][u]);
+            b->tile_cap[1][q][u] = cap(b->tilex[q][u]);
+        }
+        for (int g = 0; g < 2; g++) b->tilem_cap[q][g] = cap(b->tilem[q][g]);
+        for (int r = 0; r < 4; r++) b->tilemx_cap[q][r] = cap(b->tilemx[q][r]);
+    }
     if (const char *u = std::getenv("CTOX_TILE_U")) {
         const int v = std::atoi(u);
         if (v >= 1 && v <= CTOX_TILE_MAXU) b->tile_u = (uint32_t)v;

@@ -183,8 +183,8 @@ def test_baseline_full_shapes(hip, orc, cfg):
 
 
 @pytest.mark.parametrize("mode", ["1", "0"])
-def test_batch1_combine_modes(orc, mode, monkeypatch):
-    """Both ways the batch-1 tiled kernel's chunks meet give the oracle's
+def test_tiled_combine_modes(orc, mode, monkeypatch):
+    """Both ways the tiled kernels' chunks meet give the oracle's
     rows: by arrival (the last chunk to arrive for a tile adds them, used for
     launches larger than the device holds at once) and by the last chunk's
     waves (used when every workgroup is resident). CTOX_ARRIVE forces one
@@ -202,6 +202,13 @@ def test_batch1_combine_modes(orc, mode, monkeypatch):
                 got = resident_run(hip2, op, parts[1])
                 ref = oracle_rows(orc, dtype, rows, cols, parts, ctox_hip.Activation.Identity)
                 check(got, ref, f"combine mode={mode} rep={rep}")
+        for batch in (3, 8):  # the small-M kernels (one and two token groups)
+            say(f"case combine mode={mode} small-m batch={batch}")
+            op, parts = make_case(1, 17408, 5120, 45, "f16", bias=False, batch=batch)
+            for rep in range(2):
+                got = resident_run(hip2, op, parts[1])
+                ref = oracle_rows(orc, 1, 17408, 5120, parts, ctox_hip.Activation.Identity)
+                check(got, ref, f"combine mode={mode} batch={batch} rep={rep}")
     finally:
         hip2.close()
     monkeypatch.delenv("CTOX_ARRIVE")
