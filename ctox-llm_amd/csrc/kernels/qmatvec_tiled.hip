@@ -787,10 +787,10 @@ __device__ __forceinline__ void tile_matvec_m(const TileMatvecArgs &a) {
 #define CTOX_TILE_M_KERNEL(name, dt, u, tg) \
     extern "C" __global__ __launch_bounds__(256) void name(TileMatvecArgs a) { tile_matvec_m<dt, u, tg, 0>(a); } \
     extern "C" __global__ __launch_bounds__(256) void name##_arrive(TileMatvecArgs a) { tile_matvec_m<dt, u, tg, 1>(a); }
-CTOX_TILE_M_KERNEL(ctox_q2_mv_tilem1_gfx950, 0, 2, 1)
-CTOX_TILE_M_KERNEL(ctox_q2_mv_tilem2_gfx950, 0, 2, 2)
-CTOX_TILE_M_KERNEL(ctox_q4_mv_tilem1_gfx950, 1, 2, 1)
-CTOX_TILE_M_KERNEL(ctox_q4_mv_tilem2_gfx950, 1, 2, 2)
+CTOX_TILE_M_KERNEL(ctox_q2_mv_tilem1_gfx950, 0, 1, 1)
+CTOX_TILE_M_KERNEL(ctox_q2_mv_tilem2_gfx950, 0, 1, 2)
+CTOX_TILE_M_KERNEL(ctox_q4_mv_tilem1_gfx950, 1, 1, 1)
+CTOX_TILE_M_KERNEL(ctox_q4_mv_tilem2_gfx950, 1, 1, 2)
 
 // ---------------------------------------------------------------------------
 // Small-M tiled matvec with the activation rows built in the kernel
@@ -821,7 +821,7 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, void *lds, u
 template <int DT, int MR, int ARR>
 __device__ __forceinline__ void tile_matvec_mx(const TileMatvecArgs &a) {
     using C = TlCfg<DT>;
-    constexpr uint32_t U = 2, TG = (MR + 3) / 4, INB = 2048;
+    constexpr uint32_t U = 1, TG = (MR + 3) / 4, INB = 2048;
     constexpr uint32_t WLOADS = U * (C::LPU + 4);  // weight loads issued after the input copies
     __shared__ __align__(16) uint8_t ins[4 * MR * INB];
     __shared__ __align__(16) int8_t xas[CTOX_TILE_BLOCKS * MR * 192];

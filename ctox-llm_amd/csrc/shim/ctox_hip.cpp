@@ -163,7 +163,7 @@ struct ctox_hip_backend {
     // The same with the activation fragments built inside the kernel.
     hipFunction_t tilex[2][CTOX_TILE_MAXU] = {};
     hipFunction_t tile_arr[2][2][CTOX_TILE_MAXU] = {};  // [staged|built][q4][u - 1], combine by arrival
-    // Small-M tiled kernels per dtype: [0] 2..4 rows, [1] 5..8 rows (2 row tiles per wave).
+    // Small-M tiled kernels per dtype: [0] 2..4 rows, [1] 5..8 rows (one row tile per wave).
     hipFunction_t tilem[2][2] = {};
     hipFunction_t tilem_arr[2][2] = {};  // combine by arrival
     // The same building the rows' fragments in the kernel, per row count 2..5.
@@ -599,7 +599,7 @@ ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCop
                               float *res_sq) {
     const int q4 = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
     const uint32_t tg = batch > 4 ? 2 : 1;
-    const uint32_t u = 2;
+    const uint32_t u = 1;
     const uint32_t segs = (((t.tiles + u - 1) / u) + 3) & ~3u;
     const size_t waves = (size_t)segs * t.chunks;
     if (waves / 4 > 0x7fffffffu || out_stride > 0xffffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
@@ -645,7 +645,7 @@ ctox_status run_tile_matvec_mx(ctox_hip_backend *b, int32_t dtype, const TiledCo
                                float *d_output, size_t out_stride, uint32_t act, hipStream_t s, const float *d_input,
                                const void *d_s_in, uint32_t s_in_kind, const TileXform &xf, const PartialSlots *ps) {
     const int q4 = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
-    const uint32_t u = 2;
+    const uint32_t u = 1;
     const uint32_t segs = (((t.tiles + u - 1) / u) + 3) & ~3u;
     const size_t waves = (size_t)segs * t.chunks;
     if (batch < 2 || batch > kMaxBuildRows) return fail(CTOX_ERR_SHAPE, "in-kernel row build takes 2..5 rows");
