@@ -39,13 +39,6 @@ struct TlCfg {
     static constexpr float DEN = DT ? 15.0f : 3.0f;
 };
 
-__device__ __forceinline__ float tile_epilogue(float v, uint32_t row, const TileMatvecArgs &a) {
-    if (a.bias) v += a.bias[row];
-    if (a.s_out_kind != CTOX_KSCALE_NONE) v *= load_scale(a.s_out, a.s_out_kind, row);
-    if (a.activation == 1) v = v / (1.0f + expf(-v));
-    return v;
-}
-
 template <int DT>
 struct TileUnit {
     v4i w[TlCfg<DT>::LPU];
@@ -79,6 +72,34 @@ struct GroupIn {
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t f32_rsrc(const void *p, uint32_t floats) {
     return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, p ? (int)(floats * 4) : 0, 0x00020000);
+}
+
+// Epilogue operands of one output row (bias, s_out and, with residual sums,
+// the residual input of token row `tok`; res_h rows are `rows` apart), read
+// ahead of the combine so their latency overlaps the poll. Branch-free: an
+// absent operand has an empty range and reads 0. Raw bits until applied.
+struct EpiIn {
+    uint32_t bias, s16, s32, h;
+};
+__device__ __forceinline__ EpiIn epi_load(const TileMatvecArgs &a, uint32_t row, uint32_t tok) {
+    const bool f16 = a.s_out_kind == CTOX_KSCALE_F16, f32 = a.s_out_kind == CTOX_KSCALE_F32;
+    const __amdgpu_buffer_rsrc_t s16 =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.s_out, (short)0, f16 ? (int)(a.rows * 2) : 0, 0x00020000);
+    EpiIn e;
+    e.bias = __builtin_amdgcn_raw_buffer_load_b32(f32_rsrc(a.bias, a.rows), row * 4, 0, 0);
+    e.s16 = __builtin_amdgcn_raw_buffer_load_b16(s16, row * 2, 0, 0);
+    e.s32 = __builtin_amdgcn_raw_buffer_load_b32(f32_rsrc(f32 ? a.s_out : nullptr, a.rows), row * 4, 0, 0);
+    e.h = __builtin_amdgcn_raw_buffer_load_b32(f32_rsrc(a.res_sq ? a.res_h : nullptr, (tok + 1) * a.rows),
+                                               (tok * a.rows + row) * 4, 0, 0);
+    return e;
+}
+// Output epilogue: + bias, x s_out, then SiLU when asked.
+__device__ __forceinline__ float epi_apply(float v, const EpiIn &e, const TileMatvecArgs &a) {
+    if (a.bias) v += __uint_as_float(e.bias);
+    if (a.s_out_kind == CTOX_KSCALE_F16) v *= half_bits_to_float(e.s16 & 0xffffu);
+    if (a.s_out_kind == CTOX_KSCALE_F32) v *= __uint_as_float(e.s32);
+    if (a.activation == 1) v = v / (1.0f + expf(-v));
+    return v;
 }
 
 // Loads of one 4-block group's activation inputs (TileMatvecArgs::xmode);
@@ -257,89 +278,79 @@ __device__ __forceinline__ void combine_store(uint64_t *slot, float v, uint32_t 
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Sum of slots[k * stride], k < n (n = chunks - 1), in order, then + own.
-// `want` false (no row for this lane) returns at once with 0.
-__device__ __forceinline__ float combine_poll(const uint64_t *slots, size_t stride, uint32_t n, uint32_t seq, float own,
-                                              bool want) {
-    float sum = 0.0f;
-    bool done = !want;
-    for (uint32_t poll = 0; __builtin_amdgcn_ballot_w64(!done) != 0; poll++) {
-        if (poll >= CTOX_COMBINE_POLLS) {
-            if (!done) sum = __builtin_nanf("");
-            break;
-        }
-        if (poll) __builtin_amdgcn_s_sleep(2);
-        if (!done) {
-            float s = 0.0f;
-            bool all = true;
-            for (uint32_t c0 = 0; c0 < n; c0 += 16) {
-                uint64_t pv[16];
+// Row sums of T slot sets at once (the small-M kernels' token groups):
+// set i adds, in chunk order over chunks k < n, slots[i][k * stride] and,
+// for chunk own_k, own[i] in place of a slot (that slot is never read: with
+// the last chunk combining it does not exist). A set with want[i] false is
+// done at once with 0. All sets' loads of a round go out together, so T
+// sets cost one round trip, not T.
+template <int T>
+__device__ __forceinline__ void combine_poll_n(const uint64_t *const (&slots)[T], size_t stride, uint32_t n,
+                                               uint32_t own_k, uint32_t seq, const float (&own)[T],
+                                               const bool (&want)[T], float (&sum)[T]) {
+    const uint32_t ns = n - 1;  // slots to read: chunks other than own_k
+    bool done[T];
+    bool pending = false;
 #pragma unroll
-                for (int i = 0; i < 16; i++)
-                    pv[i] = __hip_atomic_load(&slots[(size_t)min(c0 + i, n - 1) * stride], __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-                for (int i = 0; i < 16; i++)
-                    if (c0 + i < n) {
-                        all = all && (uint32_t)(pv[i] >> 32) == seq;
-                        s += __uint_as_float((uint32_t)pv[i]);
-                    }
-            }
-            if (all) {
-                sum = s;
-                done = true;
-            }
-        }
+    for (int t = 0; t < T; t++) {
+        sum[t] = 0.0f;
+        done[t] = !want[t];
+        pending = pending || want[t];
     }
-    return sum + own;
-}
-
-
-// Arrival combine: the sum over k < n of slots[k * stride] in chunk order,
-// the lane's own chunk `own_k` taken from `own`; polls until every other
-// slot carries this launch's tag. `want` false returns at once with 0.
-__device__ __forceinline__ float combine_poll_all(const uint64_t *slots, size_t stride, uint32_t n, uint32_t own_k,
-                                                  uint32_t seq, float own, bool want) {
-    float sum = 0.0f;
-    bool done = !want;
-    for (uint32_t poll = 0; __builtin_amdgcn_ballot_w64(!done) != 0; poll++) {
+    for (uint32_t poll = 0; __builtin_amdgcn_ballot_w64(pending) != 0; poll++) {
         if (poll >= CTOX_COMBINE_POLLS) {
-            if (!done) sum = __builtin_nanf("");
+#pragma unroll
+            for (int t = 0; t < T; t++)
+                if (!done[t]) sum[t] = __builtin_nanf("");
             break;
         }
         if (poll) __builtin_amdgcn_s_sleep(1);
-        if (!done) {
-            float s = 0.0f;
-            bool all = true;
-            for (uint32_t c0 = 0; c0 < n; c0 += 16) {
-                uint64_t pv[16];
+        float acc[T];
+        bool all[T];
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            acc[t] = 0.0f;
+            all[t] = true;
+        }
+        for (uint32_t i0 = 0; i0 < ns; i0 += 16) {
+            uint64_t pv[T][16];
+#pragma unroll
+            for (int t = 0; t < T; t++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const uint32_t k = min(i0 + i, ns - 1);
+                    pv[t][i] = __hip_atomic_load(&slots[t][(size_t)(k < own_k ? k : k + 1) * stride], __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+                }
+#pragma unroll
+            for (int t = 0; t < T; t++)
 #pragma unroll
                 for (int i = 0; i < 16; i++)
-                    pv[i] = __hip_atomic_load(&slots[(size_t)min(c0 + i, n - 1) * stride], __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-                for (int i = 0; i < 16; i++)
-                    if (c0 + i < n) {
-                        const bool mine_k = c0 + i == own_k;
-                        all = all && (mine_k || (uint32_t)(pv[i] >> 32) == seq);
-                        s += mine_k ? own : __uint_as_float((uint32_t)pv[i]);
+                    if (i0 + i < ns) {
+                        if (i0 + i == own_k) acc[t] += own[t];  // own chunk comes before chunk own_k + 1
+                        all[t] = all[t] && (uint32_t)(pv[t][i] >> 32) == seq;
+                        acc[t] += __uint_as_float((uint32_t)pv[t][i]);
                     }
+        }
+        pending = false;
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            if (own_k == ns) acc[t] += own[t];  // own chunk is the last
+            if (!done[t] && all[t]) {
+                sum[t] = acc[t];
+                done[t] = true;
             }
-            if (all) {
-                sum = s;
-                done = true;
-            }
+            pending = pending || !done[t];
         }
     }
-    return sum;
 }
 
 // Producer side of the residual sums: per 16-row tile, sum of (res_h + y)^2
 // over its rows (the 16 lanes of one row group, DPP within the row).
 __device__ __forceinline__ void residual_tile_sum(const TileMatvecArgs &a, uint32_t tile, uint32_t row, bool mine,
-                                                  float y, uint32_t j) {
+                                                  float y, uint32_t j, const EpiIn &e) {
     if (!a.res_sq) return;
-    const float h = mine && row < a.rows ? a.res_h[row] + y : 0.0f;
+    const float h = mine && row < a.rows ? __uint_as_float(e.h) + y : 0.0f;
     const float s = row16_reduce(h * h, [](float x, float z) { return x + z; });
     if (mine && j == 0) a.res_sq[tile] = s;
 }
@@ -511,45 +522,49 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
         if (g == (uint32_t)k) val = part[k];
     const uint32_t tile = t0 + g, row = tile * CTOX_TILE_ROWS + j;
     const bool mine = g < n;
-    if (a.chunks == 1) {
-        const float y = mine && row < a.rows ? tile_epilogue(val / C::DEN, row, a) : 0.0f;
-        if (mine && row < a.rows) a.output[row] = y;
-        residual_tile_sum(a, tile, row, mine, y, j);
-        return;
-    }
-    if (a.parts_out) {
-        // Chunk partials for a consumer that adds them (no combine here).
-        if (mine && row < a.rows) a.output[(size_t)c * a.out_stride + row] = tile_epilogue(val / C::DEN, row, a);
-        return;
-    }
     const size_t cstride = (size_t)a.tiles * CTOX_TILE_ROWS;
-    float sum;
-    if (ARR) {
-        // Arrival combine: every chunk stores its tagged partial, then counts
-        // itself in for the tile; the chunk that arrives last adds the
-        // tile's partials in chunk order and resets the count. It waits
-        // only for stores of waves that have already arrived (issued before
-        // their count), so no wave waits on one not yet dispatched.
+    const bool combine = a.chunks > 1 && !a.parts_out;
+    if (combine && !ARR && c + 1 < a.chunks) {
         if (mine) combine_store(&a.partial[(size_t)c * cstride + row], val, a.seq);
-        uint32_t old = 0;
-        if (mine && j == 0)
-            old = __hip_atomic_fetch_add(&a.arrive[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        old = __shfl(old, 16 * g);
-        const bool last = mine && old + 1 == a.chunks;
-        if (__builtin_amdgcn_ballot_w64(last) == 0) return;
-        sum = combine_poll_all(&a.partial[row], cstride, a.chunks, c, a.seq, val, last);
-        if (last && j == 0) __hip_atomic_store(&a.arrive[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (!last) return;
-    } else {
-        if (c + 1 < a.chunks) {
-            if (mine) combine_store(&a.partial[(size_t)c * cstride + row], val, a.seq);
-            return;
-        }
-        sum = combine_poll(&a.partial[row], cstride, a.chunks - 1, a.seq, val, mine);
+        return;
     }
-    const float y = mine && row < a.rows ? tile_epilogue(sum / C::DEN, row, a) : 0.0f;
+    // This wave may write rows: its epilogue operands go out now.
+    const EpiIn e = epi_load(a, row, 0);
+    if (a.parts_out && a.chunks > 1) {
+        // Chunk partials for a consumer that adds them (no combine here).
+        if (mine && row < a.rows) a.output[(size_t)c * a.out_stride + row] = epi_apply(val / C::DEN, e, a);
+        return;
+    }
+    float sum = val;
+    if (combine) {
+        bool want = mine;
+        if (ARR) {
+            // Arrival combine: every chunk stores its tagged partial, then
+            // counts itself in for the tile; the chunk that arrives last adds
+            // the tile's partials in chunk order and resets the count. It
+            // waits only for stores of waves that have already arrived
+            // (issued before their count), so no wave waits on one not yet
+            // dispatched.
+            if (mine) combine_store(&a.partial[(size_t)c * cstride + row], val, a.seq);
+            uint32_t old = 0;
+            if (mine && j == 0)
+                old = __hip_atomic_fetch_add(&a.arrive[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            old = __shfl(old, 16 * g);
+            want = mine && old + 1 == a.chunks;
+            if (__builtin_amdgcn_ballot_w64(want) == 0) return;
+        }
+        const uint64_t *const slots[1] = {&a.partial[want ? row : j]};  // in range for every lane
+        const float own[1] = {val};
+        const bool w1[1] = {want};
+        float got[1];
+        combine_poll_n<1>(slots, cstride, a.chunks, c, a.seq, own, w1, got);
+        sum = got[0];
+        if (ARR && want && j == 0) __hip_atomic_store(&a.arrive[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (ARR && !want) return;
+    }
+    const float y = mine && row < a.rows ? epi_apply(sum / C::DEN, e, a) : 0.0f;
     if (mine && row < a.rows) a.output[row] = y;
-    residual_tile_sum(a, tile, row, mine, y, j);
+    residual_tile_sum(a, tile, row, mine, y, j, e);
 }
 
 // ctox_q{2,4}_mv_tile{U}_gfx950 take prep-staged fragments; the _x
@@ -601,8 +616,8 @@ __device__ __forceinline__ void transpose4(uint32_t &r0, uint32_t &r1, uint32_t 
 
 // Per 16-row tile and row tok: sum over the tile's rows of (res_h + y)^2.
 __device__ __forceinline__ void residual_tile_sum_m(const TileMatvecArgs &a, uint32_t tok, uint32_t tile,
-                                                    uint32_t row, bool mine, float y, uint32_t j) {
-    const float h = mine && row < a.rows ? a.res_h[(size_t)tok * a.rows + row] + y : 0.0f;
+                                                    uint32_t row, bool mine, float y, uint32_t j, const EpiIn &e) {
+    const float h = mine && row < a.rows ? __uint_as_float(e.h) + y : 0.0f;
     const float s = row16_reduce(h * h, [](float x, float z) { return x + z; });
     if (mine && j == 0) a.res_sq[(size_t)tok * a.tiles + tile] = s;
 }
@@ -619,11 +634,26 @@ __device__ __forceinline__ void small_m_finish(const TileMatvecArgs &a, uint32_t
                                                uint32_t g, uint32_t j, uint32_t M, const float (&acc)[U][TG]) {
     using C = TlCfg<DT>;
     const size_t tstride = (size_t)a.tiles * CTOX_TILE_ROWS, cstride = tstride * M;
-    bool last[U];
-    if (a.chunks == 1) {
+    if (a.chunks > 1 && !ARR && c + 1 < a.chunks) {
 #pragma unroll
-        for (int k = 0; k < U; k++) last[k] = true;
-    } else if (ARR) {
+        for (int k = 0; k < U; k++)
+#pragma unroll
+            for (int tg = 0; tg < TG; tg++) {
+                const uint32_t tok = 4 * tg + g, row = (t0 + k) * CTOX_TILE_ROWS + j;
+                if ((uint32_t)k < n && tok < M) combine_store(&a.partial[c * cstride + tok * tstride + row], acc[k][tg], a.seq);
+            }
+        return;
+    }
+    // This wave may write rows: its epilogue operands go out now.
+    EpiIn e[U][TG];
+#pragma unroll
+    for (int k = 0; k < U; k++)
+#pragma unroll
+        for (int tg = 0; tg < TG; tg++) e[k][tg] = epi_load(a, (t0 + k) * CTOX_TILE_ROWS + j, min(4 * tg + g, M - 1));
+    bool last[U];
+#pragma unroll
+    for (int k = 0; k < U; k++) last[k] = true;
+    if (a.chunks > 1 && ARR) {
 #pragma unroll
         for (int k = 0; k < U; k++)
 #pragma unroll
@@ -642,34 +672,31 @@ __device__ __forceinline__ void small_m_finish(const TileMatvecArgs &a, uint32_t
             any = any || last[k];
         }
         if (!any) return;
-    } else {
-        if (c + 1 < a.chunks) {
-#pragma unroll
-            for (int k = 0; k < U; k++)
-#pragma unroll
-                for (int tg = 0; tg < TG; tg++) {
-                    const uint32_t tok = 4 * tg + g, row = (t0 + k) * CTOX_TILE_ROWS + j;
-                    if ((uint32_t)k < n && tok < M) combine_store(&a.partial[c * cstride + tok * tstride + row], acc[k][tg], a.seq);
-                }
-            return;
-        }
-#pragma unroll
-        for (int k = 0; k < U; k++) last[k] = true;
     }
 #pragma unroll
     for (int k = 0; k < U; k++) {
         if (!last[k]) continue;  // wave-uniform
+        const uint32_t tile = t0 + k, row = tile * CTOX_TILE_ROWS + j;
+        float sum[TG];
+        bool want[TG];
 #pragma unroll
         for (int tg = 0; tg < TG; tg++) {
-            const uint32_t tok = 4 * tg + g, tile = t0 + k, row = tile * CTOX_TILE_ROWS + j;
-            const bool want = (uint32_t)k < n && tok < M;
-            float sum = acc[k][tg];
-            if (a.chunks > 1)
-                sum = ARR ? combine_poll_all(&a.partial[tok * tstride + row], cstride, a.chunks, c, a.seq, acc[k][tg], want)
-                          : combine_poll(&a.partial[tok * tstride + row], cstride, a.chunks - 1, a.seq, acc[k][tg], want);
-            const float y = want && row < a.rows ? tile_epilogue(sum / C::DEN, row, a) : 0.0f;
-            if (want && row < a.rows) a.output[(size_t)tok * a.out_stride + row] = y;
-            if (a.res_sq) residual_tile_sum_m(a, min(tok, M - 1), tile, row, want, y, j);
+            want[tg] = (uint32_t)k < n && 4 * tg + g < M;
+            sum[tg] = acc[k][tg];
+        }
+        if (a.chunks > 1) {
+            // Every token group's slots in one poll.
+            const uint64_t *slots[TG];
+#pragma unroll
+            for (int tg = 0; tg < TG; tg++) slots[tg] = &a.partial[want[tg] ? (size_t)(4 * tg + g) * tstride + row : j];
+            combine_poll_n<TG>(slots, cstride, a.chunks, c, a.seq, acc[k], want, sum);
+        }
+#pragma unroll
+        for (int tg = 0; tg < TG; tg++) {
+            const uint32_t tok = 4 * tg + g;
+            const float y = want[tg] && row < a.rows ? epi_apply(sum[tg] / C::DEN, e[k][tg], a) : 0.0f;
+            if (want[tg] && row < a.rows) a.output[(size_t)tok * a.out_stride + row] = y;
+            if (a.res_sq) residual_tile_sum_m(a, min(tok, M - 1), tile, row, want[tg], y, j, e[k][tg]);
         }
         if (ARR && a.chunks > 1 && (threadIdx.x & 63) == 0)
             __hip_atomic_store(&a.arrive[t0 + k], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
