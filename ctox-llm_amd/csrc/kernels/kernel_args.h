@@ -65,6 +65,8 @@ struct PrepXArgs {
     uint32_t off;
     uint32_t head_dim;
     float eps;
+    uint32_t a_parts;       // mode 1: a is the sum of this many partials (0/1: one)
+    uint32_t a_pstride;     // floats between partials
 };
 
 // One workgroup per 16 output rows (grid = ceil(rows / 16)); its four waves
@@ -142,7 +144,8 @@ struct TileMatvecArgs {
                             // last chunk combines
     uint32_t seq;           // this launch's tag in the partial slots (never 0)
     uint32_t sq_n;          // xmode 1: entries of sq_in (0: reduce the row itself)
-    uint32_t parts_out;     // batch 1: write each chunk's s_out-scaled sum to output[chunk * out_stride + row]
+    uint32_t parts_out;     // write each chunk's s_out-scaled sum to output[chunk * out_stride + row]
+                            // (batch 1) or output[(chunk * batch + token) * out_stride + row] (small M)
     uint32_t a_parts;       // xmode 2: input holds a_parts partial rows a_pstride floats apart (summed in order)
     uint32_t a_pstride;
     uint32_t pad3;

@@ -207,7 +207,8 @@ extern "C" __global__ __launch_bounds__(256) void ctox_norm_prep_gfx950(NormPrep
 //                                                            Q/src/reference.rs:66-93
 //   mode 3  attention gate: x = a[t][c] * sigmoid(b[t][h * 2 hd + hd + d]),
 //           h = c / head_dim, d = c % head_dim              Q/src/decoder.rs:727-737, :788
-// a rows are a_stride floats apart, b rows b_stride.
+// a rows are a_stride floats apart, b rows b_stride; in mode 1 a may be
+// a_parts partials a_pstride floats apart, added in part order.
 __device__ __forceinline__ float px_silu(float v) { return v / (1.0f + expf(-v)); }
 
 extern "C" __global__ __launch_bounds__(64) void ctox_prep_transform_gfx950(PrepXArgs a) {
@@ -216,7 +217,13 @@ extern "C" __global__ __launch_bounds__(64) void ctox_prep_transform_gfx950(Prep
     const float *ar = a.a + (size_t)t * a.a_stride;
     float x;
     if (a.mode == 1) {
-        x = px_silu(ar[col]) * ar[a.off + col];
+        // A producer's chunk partials are added in part order.
+        float ga = ar[col], ua = ar[a.off + col];
+        for (uint32_t k = 1; k < a.a_parts; k++) {
+            ga += ar[(size_t)k * a.a_pstride + col];
+            ua += ar[(size_t)k * a.a_pstride + a.off + col];
+        }
+        x = px_silu(ga) * ua;
     } else if (a.mode == 2) {
         const uint32_t head0 = col / a.head_dim * a.head_dim;
         float ss = 0.0f;

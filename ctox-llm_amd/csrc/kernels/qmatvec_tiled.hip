@@ -634,6 +634,20 @@ __device__ __forceinline__ void small_m_finish(const TileMatvecArgs &a, uint32_t
                                                uint32_t g, uint32_t j, uint32_t M, const float (&acc)[U][TG]) {
     using C = TlCfg<DT>;
     const size_t tstride = (size_t)a.tiles * CTOX_TILE_ROWS, cstride = tstride * M;
+    if (a.parts_out) {
+        // Chunk partials [chunk][token][out_stride] for a consumer that adds
+        // them (no combine here).
+#pragma unroll
+        for (int k = 0; k < U; k++)
+#pragma unroll
+            for (int tg = 0; tg < TG; tg++) {
+                const uint32_t tok = 4 * tg + g, row = (t0 + k) * CTOX_TILE_ROWS + j;
+                const EpiIn e = epi_load(a, row, 0);
+                if ((uint32_t)k < n && tok < M && row < a.rows)
+                    a.output[((size_t)c * M + tok) * a.out_stride + row] = epi_apply(acc[k][tg] / C::DEN, e, a);
+            }
+        return;
+    }
     if (a.chunks > 1 && !ARR && c + 1 < a.chunks) {
 #pragma unroll
         for (int k = 0; k < U; k++)

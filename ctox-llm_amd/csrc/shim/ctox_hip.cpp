@@ -425,7 +425,7 @@ ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy 
 ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows, size_t columns,
                               size_t batch, const void *d_s_out, uint32_t s_out_kind, const float *d_bias,
                               float *d_output, size_t out_stride, uint32_t act, hipStream_t s,
-                              const float *res_h = nullptr, float *res_sq = nullptr);
+                              const float *res_h = nullptr, float *res_sq = nullptr, bool parts_out = false);
 
 ctox_status run_tile_matvec_mx(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows, size_t columns,
                                size_t batch, const void *d_s_out, uint32_t s_out_kind, const float *d_bias,
@@ -593,10 +593,11 @@ ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy 
 }
 
 // One launch of the small-M tiled matvec (2..8 rows staged in xa/xc).
+// parts_out: chunk partials [chunk][batch][out_stride] instead of the combine.
 ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows, size_t columns,
                               size_t batch, const void *d_s_out, uint32_t s_out_kind, const float *d_bias,
                               float *d_output, size_t out_stride, uint32_t act, hipStream_t s, const float *res_h,
-                              float *res_sq) {
+                              float *res_sq, bool parts_out) {
     const int q4 = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
     const uint32_t tg = batch > 4 ? 2 : 1;
     const uint32_t u = 1;
@@ -605,8 +606,10 @@ ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCop
     if (waves / 4 > 0x7fffffffu || out_stride > 0xffffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
     // Chunks meet as in the batch-1 launch: by the last chunk when the
     // device holds every workgroup at once, else by arrival.
-    const bool arrive = t.chunks > 1 && (b->arrive >= 0 ? b->arrive != 0 : waves / 4 > b->tilem_cap[q4][tg - 1]);
-    if (t.chunks > 1) {
+    parts_out = parts_out && t.chunks > 1;
+    const bool arrive =
+        t.chunks > 1 && !parts_out && (b->arrive >= 0 ? b->arrive != 0 : waves / 4 > b->tilem_cap[q4][tg - 1]);
+    if (t.chunks > 1 && !parts_out) {
         ctox_status st = ensure(b, b->tpart,
                                 (size_t)(arrive ? t.chunks : t.chunks - 1) * batch * t.tiles * CTOX_TILE_ROWS * sizeof(uint64_t),
                                 true);
@@ -635,6 +638,7 @@ ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCop
     a.out_stride = (uint32_t)out_stride;
     a.res_h = res_h;
     a.res_sq = res_sq;
+    a.parts_out = parts_out ? 1u : 0u;
     return launch(arrive ? b->tilem_arr[q4][tg - 1] : b->tilem[q4][tg - 1], dim3((unsigned)(waves / 4)), dim3(256), s, a, "ctox_q*_mv_tilem*_gfx950");
 }
 
@@ -1300,6 +1304,16 @@ extern "C" ctox_status ctox_hip_norm_matvec_parts_device(ctox_hip_backend *b, co
     a.eps = eps;
     if ((st = launch(b->norm_prep, dim3((unsigned)((blocks + 3) / 4), batch), dim3(256), s, a, "ctox_norm_prep_gfx950")))
         return st;
+    // Registered weights, 2..8 staged rows: chunk partials for a consumer
+    // that adds them, when it takes that many.
+    if (batch > 1 && parts && max_parts > 1)
+        if (const TiledCopy *t = registered(b, d_weights, rows, columns))
+            if (t->chunks > 1 && t->chunks <= max_parts) {
+                *parts = t->chunks;
+                return run_tile_matvec_m(b, dtype, *t, rows, columns, batch, d_s_out,
+                                         d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, nullptr, d_output, rows, 0, s,
+                                         nullptr, nullptr, true);
+            }
     return run_matvec(b, layout, dtype, d_weights, rows, columns, batch, d_s_out,
                       d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, nullptr, d_output, rows, 0, s);
 }
@@ -1314,8 +1328,9 @@ extern "C" ctox_status ctox_hip_transform_matvec_device(ctox_hip_backend *b, con
         (x->mode == 2 && !x->w) || (x->res_sums && !x->res_h))
         return fail(CTOX_ERR_SHAPE, "null argument");
     if (x->mode < 1 || x->mode > 3) return fail(CTOX_ERR_SHAPE, "unknown input transform %u", x->mode);
-    if (x->a_parts > 1 && (x->mode != 1 || x->a_parts > 6 || x->a_part_stride < x->off + columns))
-        return fail(CTOX_ERR_SHAPE, "input partials: swiglu only, at most 6, a_part_stride covering a row");
+    if (x->a_parts > 1 && (x->mode != 1 || x->a_parts > 6 ||
+                           x->a_part_stride < (uint64_t)(batch - 1) * x->a_stride + x->off + columns))
+        return fail(CTOX_ERR_SHAPE, "input partials: swiglu only, at most 6, a_part_stride covering the rows");
     if (dtype != CTOX_DTYPE_Q2B64 && dtype != CTOX_DTYPE_Q4B64)
         return fail(CTOX_ERR_UNSUPPORTED_DTYPE, "transform-matvec takes pure Q2_B64 or Q4_B64 weights");
     if (rows == 0 || columns == 0 || columns % kBlockLen) return fail(CTOX_ERR_SHAPE, "transform-matvec dimensions");
@@ -1368,9 +1383,8 @@ extern "C" ctox_status ctox_hip_transform_matvec_device(ctox_hip_backend *b, con
         }
     }
     const bool reg = registered(b, d_weights, rows, columns) != nullptr;
-    if ((x->res_sums && (!reg || batch > CTOX_MAX_BATCH)) || x->a_parts > 1)
-        return fail(CTOX_ERR_UNSUPPORTED_OPERATION,
-                    "residual sums need registered weights; input partials need 1 row on registered weights");
+    if ((x->res_sums || x->a_parts > 1) && !reg)
+        return fail(CTOX_ERR_UNSUPPORTED_OPERATION, "residual sums and input partials need registered weights");
     ctox_status st = ensure(b, b->xa[layout], blocks * batch * 192, false);
     if (!st) st = ensure(b, b->xc[layout], blocks * batch * 4 * sizeof(float), false);
     if (st) return st;
@@ -1392,6 +1406,8 @@ extern "C" ctox_status ctox_hip_transform_matvec_device(ctox_hip_backend *b, con
     a.off = x->off;
     a.head_dim = x->head_dim;
     a.eps = x->eps;
+    a.a_parts = x->a_parts > 1 ? x->a_parts : 1u;
+    a.a_pstride = x->a_part_stride;
     if ((st = launch(b->prep_x, dim3((unsigned)blocks, batch), dim3(64), s, a, "ctox_prep_transform_gfx950"))) return st;
     return run_matvec(b, layout, dtype, d_weights, rows, columns, batch, d_s_out,
                       d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, nullptr, d_output, rows, 0, s, split_k != 0, parts,

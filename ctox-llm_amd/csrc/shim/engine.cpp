@@ -473,10 +473,10 @@ ctox_status gdn_forward(ctox_hip_engine *e, GdnLayer &g, uint32_t R, float *delt
 }
 
 ctox_status mlp_forward(ctox_hip_engine *e, Mlp &m, uint32_t R, const float *delta_in, float *delta_out) {
-    // Single row: gate|up leaves its chunk partials and down's SwiGLU build adds them.
+    // gate|up leaves its chunk partials and down's SwiGLU build or staging adds them.
     uint32_t parts = 1;
-    TRY(norm_mv(e, delta_in, m.norm, R, m.gate_up, e->gu, nullptr, R == 1 ? 6 : 1, &parts));
-    ctox_input_transform x{e->gu, nullptr, nullptr, 1, 2 * e->I, 0, e->I, 0, 0.0f, nullptr, nullptr, parts, 2 * e->I};
+    TRY(norm_mv(e, delta_in, m.norm, R, m.gate_up, e->gu, nullptr, 6, &parts));
+    ctox_input_transform x{e->gu, nullptr, nullptr, 1, 2 * e->I, 0, e->I, 0, 0.0f, nullptr, nullptr, parts, R * 2 * e->I};
     return delta_mv(e, x, m.down, delta_out, R);
 }
 
@@ -681,7 +681,7 @@ extern "C" ctox_status ctox_hip_engine_create_with_dtypes(ctox_hip_backend *b, c
         (st = dalloc_t(e, &e->core, R * e->Vw)) || (st = dalloc_t(e, &e->coren, R * e->Vw)) ||
         (st = dalloc_t(e, &e->delta, 16 * R * e->H)) || (st = dalloc_t(e, &e->q, R * qh * hd)) ||
         (st = dalloc_t(e, &e->k, R * e->kvw)) || (st = dalloc_t(e, &e->v, R * e->kvw)) ||
-        (st = dalloc_t(e, &e->attn, R * qh * hd)) || (st = dalloc_t(e, &e->gu, std::max<size_t>(R, 6) * 2 * e->I)) ||
+        (st = dalloc_t(e, &e->attn, R * qh * hd)) || (st = dalloc_t(e, &e->gu, (size_t)R * 6 * 2 * e->I)) ||
         (st = dalloc_t(e, &e->act, R * e->I)) || (st = dalloc_t(e, &e->fin, R * e->H)) ||
         (st = dalloc_t(e, &e->logits, R * e->V)) || (st = dalloc_t(e, &e->ld, R * Hv)) ||
         (st = dalloc_t(e, &e->beta, R * Hv)) || (st = dalloc_t(e, &e->fcin, R * 2 * e->H)) ||

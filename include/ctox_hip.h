@@ -260,11 +260,11 @@ ctox_status ctox_hip_norm_matvec_sums_device(ctox_hip_backend *backend, const fl
                                              const float *d_sums, uint32_t sum_count, void *stream);
 
 /* ctox_hip_norm_matvec_sums_device whose output may be left as partial
- * rows: on the batch-1 registered-weights path, when the K range is split
- * into n <= max_parts chunks, d_output receives n rows [n][rows] (each
+ * rows: on registered weights, when the K range is split into
+ * n <= max_parts chunks, d_output receives n parts [n][batch][rows] (each
  * chunk's sum times s_out) whose sum in order is the projection, *parts = n,
  * and the cross-chunk combine is skipped; otherwise the result itself and
- * *parts = 1. For a consumer that adds them (ctox_input_transform::a_parts).
+ * *parts = 1 (also for 2..5 rows built in the kernel from d_sums). For a consumer that adds them (ctox_input_transform::a_parts).
  * No crate counterpart (the crate's projection returns finished rows,
  * Q/src/backend/mod.rs:153-169). */
 ctox_status ctox_hip_norm_matvec_parts_device(ctox_hip_backend *backend, const float *d_x, const float *d_delta,
@@ -298,10 +298,10 @@ typedef struct {
      * adds and normalizes in one pass, Q/src/decoder.rs:636-680). */
     const float *res_h;
     float *res_sums;
-    /* Mode 1 only, batch 1 on registered weights: a holds a_parts (2..6)
-     * partial rows a_part_stride floats apart whose sum (in order) is the
-     * gate|up row, as ctox_hip_norm_matvec_parts_device leaves them (0 or 1:
-     * a is the row itself). */
+    /* Mode 1 only, on registered weights: a holds a_parts (2..6) partials
+     * a_part_stride floats apart (each batch rows of a_stride floats) whose
+     * sum (in order) is the gate|up rows, as ctox_hip_norm_matvec_parts_device
+     * leaves them (0 or 1: a is the rows themselves). */
     uint32_t a_parts, a_part_stride;
 } ctox_input_transform;
 /* split_k != 0 lets a batch-1 projection split its K range into one partial

@@ -344,16 +344,19 @@ def test_residual_sums_chain(hip, orc, rows, cols):
     hip.unregister_tiled_weights(d2.data_ptr())
 
 
+@pytest.mark.parametrize("batch", [1, 5])
 @pytest.mark.parametrize("cols", [5120, 1024])
-def test_gate_up_partials_chain(hip, orc, cols):
+def test_gate_up_partials_chain(hip, orc, cols, batch):
     """gate|up as a norm-matvec that leaves its chunk partials
-    (ctox_hip_norm_matvec_parts_device; registered weights, batch 1), then
-    swiglu -> down adding them in its in-kernel build (a_parts), against the
-    oracle norm, gate|up, swiglu and down; the partials' sum equals the
-    finished gate|up rows within rounding."""
+    (ctox_hip_norm_matvec_parts_device on registered weights: built in the
+    kernel at batch 1, on staged rows at batch 5), then swiglu -> down
+    adding them (in its in-kernel build at batch 1, in its staging at
+    batch 5; a_parts), against the oracle norm, gate|up, swiglu and down per
+    row; the partials' sum equals the finished gate|up rows within
+    rounding."""
     import ctox_hip
-    say(f"case gate|up partials cols={cols}")
-    rng = np.random.default_rng(cols)
+    say(f"case gate|up partials cols={cols} batch={batch}")
+    rng = np.random.default_rng(cols + batch)
     lib = ctox_hip.load_library()
     inter, out_rows = 1024, 256
 
@@ -366,7 +369,7 @@ def test_gate_up_partials_chain(hip, orc, cols):
 
     wgu, wdn = qmat(2 * inter, cols, 1), qmat(out_rows, inter, 0)
     so = rng.uniform(0.75, 1.25, 2 * inter).astype(np.float16)
-    x = rng.standard_normal(cols).astype(np.float32)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
     nw = (rng.standard_normal(cols) * 0.1).astype(np.float32)
     dgu = torch.from_numpy(np.frombuffer(wgu, np.uint8).copy()).cuda()
     ddn = torch.from_numpy(np.frombuffer(wdn, np.uint8).copy()).cuda()
@@ -374,27 +377,29 @@ def test_gate_up_partials_chain(hip, orc, cols):
     hip.register_tiled_weights(ctox_hip.TensorDType(1), dgu.data_ptr(), 2 * inter, cols)
     hip.register_tiled_weights(ctox_hip.TensorDType(0), ddn.data_ptr(), out_rows, inter)
     dx, dw = dev(x), dev(nw)
-    gu = torch.full((6, 2 * inter), float("nan"), device="cuda")
+    gu = torch.full((6, batch, 2 * inter), float("nan"), device="cuda")
     parts = ctypes.c_uint32(0)
     st = lib.ctox_hip_norm_matvec_parts_device(hip.handle, dx.data_ptr(), None, 1, 0, None, dw.data_ptr(), 1e-6, None,
                                                1, dgu.data_ptr(), None, dso.data_ptr(), gu.data_ptr(), 2 * inter,
-                                               cols, 1, None, 0, 6, ctypes.byref(parts), None)
+                                               cols, batch, None, 0, 6, ctypes.byref(parts), None)
     assert st == 0, lib.ctox_hip_last_error()
     n = parts.value
     assert n == (cols // 64 + 15) // 16 or n == 1
-    out = torch.empty(1, out_rows, device="cuda")
-    tr = _Transform(gu.data_ptr(), None, None, 1, 2 * inter, 0, inter, 0, 0.0, None, None, n, 2 * inter)
+    assert n > 1 or cols == 1024
+    out = torch.empty(batch, out_rows, device="cuda")
+    tr = _Transform(gu.data_ptr(), None, None, 1, 2 * inter, 0, inter, 0, 0.0, None, None, n, batch * 2 * inter)
     pp = ctypes.c_uint32(0)
     st = lib.ctox_hip_transform_matvec_device(hip.handle, ctypes.byref(tr), 0, ddn.data_ptr(), None, None,
-                                              out.data_ptr(), out_rows, inter, 1, 1, ctypes.byref(pp), None)
+                                              out.data_ptr(), out_rows, inter, batch, 1, ctypes.byref(pp), None)
     assert st == 0, lib.ctox_hip_last_error()
     torch.cuda.synchronize()
-    y = orc.rms_norm_1p_weight(x, 1, cols, nw, 1e-6)
-    ref_gu = orc.fused_matvec(1, wgu, 2 * inter, cols, y, s_out=("f16le", so.view(np.uint8)))
-    got_gu = gu[:n].cpu().numpy().sum(axis=0)
-    np.testing.assert_allclose(got_gu, ref_gu, rtol=1e-3, atol=1e-4 * float(np.abs(ref_gu).max()))
-    ref = orc.fused_matvec(0, wdn, out_rows, inter, orc.swiglu(ref_gu[:inter], ref_gu[inter:]))
-    np.testing.assert_allclose(out[0].cpu().numpy(), ref, rtol=1e-3, atol=1e-4 * float(np.abs(ref).max()))
+    for t in range(batch):
+        y = orc.rms_norm_1p_weight(x[t], 1, cols, nw, 1e-6)
+        ref_gu = orc.fused_matvec(1, wgu, 2 * inter, cols, y, s_out=("f16le", so.view(np.uint8)))
+        got_gu = gu[:n, t].cpu().numpy().sum(axis=0)
+        np.testing.assert_allclose(got_gu, ref_gu, rtol=1e-3, atol=1e-4 * float(np.abs(ref_gu).max()))
+        ref = orc.fused_matvec(0, wdn, out_rows, inter, orc.swiglu(ref_gu[:inter], ref_gu[inter:]))
+        np.testing.assert_allclose(out[t].cpu().numpy(), ref, rtol=1e-3, atol=1e-4 * float(np.abs(ref).max()))
     hip.unregister_tiled_weights(dgu.data_ptr())
     hip.unregister_tiled_weights(ddn.data_ptr())
 
