@@ -288,6 +288,7 @@ template <int T>
 __device__ __forceinline__ void combine_poll_n(const uint64_t *const (&slots)[T], size_t stride, uint32_t n,
                                                uint32_t own_k, uint32_t seq, const float (&own)[T],
                                                const bool (&want)[T], float (&sum)[T]) {
+    constexpr int CB = 16 / T;  // slots per set and round: 16 loads in flight
     const uint32_t ns = n - 1;  // slots to read: chunks other than own_k
     bool done[T];
     bool pending = false;
@@ -312,12 +313,12 @@ __device__ __forceinline__ void combine_poll_n(const uint64_t *const (&slots)[T]
             acc[t] = 0.0f;
             all[t] = true;
         }
-        for (uint32_t i0 = 0; i0 < ns; i0 += 16) {
-            uint64_t pv[T][16];
+        for (uint32_t i0 = 0; i0 < ns; i0 += CB) {
+            uint64_t pv[T][CB];
 #pragma unroll
             for (int t = 0; t < T; t++)
 #pragma unroll
-                for (int i = 0; i < 16; i++) {
+                for (int i = 0; i < CB; i++) {
                     const uint32_t k = min(i0 + i, ns - 1);
                     pv[t][i] = __hip_atomic_load(&slots[t][(size_t)(k < own_k ? k : k + 1) * stride], __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
@@ -325,7 +326,7 @@ __device__ __forceinline__ void combine_poll_n(const uint64_t *const (&slots)[T]
 #pragma unroll
             for (int t = 0; t < T; t++)
 #pragma unroll
-                for (int i = 0; i < 16; i++)
+                for (int i = 0; i < CB; i++)
                     if (i0 + i < ns) {
                         if (i0 + i == own_k) acc[t] += own[t];  // own chunk comes before chunk own_k + 1
                         all[t] = all[t] && (uint32_t)(pv[t][i] >> 32) == seq;
@@ -717,10 +718,12 @@ __device__ __forceinline__ void small_m_finish(const TileMatvecArgs &a, uint32_t
     }
 }
 
-template <int DT, int U, int TG, int ARR>
+// MM = a.batch, the row count: the LDS areas hold exactly MM rows (more
+// workgroups per CU).
+template <int DT, int U, int MM, int ARR>
 __device__ __forceinline__ void tile_matvec_m(const TileMatvecArgs &a) {
     using C = TlCfg<DT>;
-    constexpr uint32_t MAXM = 4 * TG;
+    constexpr uint32_t MAXM = MM, TG = (MM + 3) / 4;
     // The chunk's staged activation rows (xa order: [block][token][192]) and
     // epilogue constants, shared by the workgroup's four waves (same chunk),
     // plus a zero line for the A lanes outside the token/limb range.
@@ -825,13 +828,24 @@ __device__ __forceinline__ void tile_matvec_m(const TileMatvecArgs &a) {
     small_m_finish<DT, U, TG, ARR>(a, c, t0, n, g, j, M, acc);
 }
 
-#define CTOX_TILE_M_KERNEL(name, dt, u, tg) \
-    extern "C" __global__ __launch_bounds__(256) void name(TileMatvecArgs a) { tile_matvec_m<dt, u, tg, 0>(a); } \
-    extern "C" __global__ __launch_bounds__(256) void name##_arrive(TileMatvecArgs a) { tile_matvec_m<dt, u, tg, 1>(a); }
-CTOX_TILE_M_KERNEL(ctox_q2_mv_tilem1_gfx950, 0, 1, 1)
+// ctox_q{2,4}_mv_tilem{M}_gfx950: M = 2..8 staged rows, one tile per wave.
+#define CTOX_TILE_M_KERNEL(name, dt, u, m) \
+    extern "C" __global__ __launch_bounds__(256) void name(TileMatvecArgs a) { tile_matvec_m<dt, u, m, 0>(a); } \
+    extern "C" __global__ __launch_bounds__(256) void name##_arrive(TileMatvecArgs a) { tile_matvec_m<dt, u, m, 1>(a); }
 CTOX_TILE_M_KERNEL(ctox_q2_mv_tilem2_gfx950, 0, 1, 2)
-CTOX_TILE_M_KERNEL(ctox_q4_mv_tilem1_gfx950, 1, 1, 1)
+CTOX_TILE_M_KERNEL(ctox_q2_mv_tilem3_gfx950, 0, 1, 3)
+CTOX_TILE_M_KERNEL(ctox_q2_mv_tilem4_gfx950, 0, 1, 4)
+CTOX_TILE_M_KERNEL(ctox_q2_mv_tilem5_gfx950, 0, 1, 5)
+CTOX_TILE_M_KERNEL(ctox_q2_mv_tilem6_gfx950, 0, 1, 6)
+CTOX_TILE_M_KERNEL(ctox_q2_mv_tilem7_gfx950, 0, 1, 7)
+CTOX_TILE_M_KERNEL(ctox_q2_mv_tilem8_gfx950, 0, 1, 8)
 CTOX_TILE_M_KERNEL(ctox_q4_mv_tilem2_gfx950, 1, 1, 2)
+CTOX_TILE_M_KERNEL(ctox_q4_mv_tilem3_gfx950, 1, 1, 3)
+CTOX_TILE_M_KERNEL(ctox_q4_mv_tilem4_gfx950, 1, 1, 4)
+CTOX_TILE_M_KERNEL(ctox_q4_mv_tilem5_gfx950, 1, 1, 5)
+CTOX_TILE_M_KERNEL(ctox_q4_mv_tilem6_gfx950, 1, 1, 6)
+CTOX_TILE_M_KERNEL(ctox_q4_mv_tilem7_gfx950, 1, 1, 7)
+CTOX_TILE_M_KERNEL(ctox_q4_mv_tilem8_gfx950, 1, 1, 8)
 
 // ---------------------------------------------------------------------------
 // Small-M tiled matvec with the activation rows built in the kernel

@@ -163,9 +163,8 @@ struct ctox_hip_backend {
     // The same with the activation fragments built inside the kernel.
     hipFunction_t tilex[2][CTOX_TILE_MAXU] = {};
     hipFunction_t tile_arr[2][2][CTOX_TILE_MAXU] = {};  // [staged|built][q4][u - 1], combine by arrival
-    // Small-M tiled kernels per dtype: [0] 2..4 rows, [1] 5..8 rows (one row tile per wave).
-    hipFunction_t tilem[2][2] = {};
-    hipFunction_t tilem_arr[2][2] = {};  // combine by arrival
+    hipFunction_t tilem[2][7] = {};      // [q4][rows - 2], 2..8 staged rows
+    hipFunction_t tilem_arr[2][7] = {};  // combine by arrival
     // The same building the rows' fragments in the kernel, per row count 2..5.
     hipFunction_t tilemx[2][4] = {};
     hipFunction_t tilemx_arr[2][4] = {};  // combine by arrival
@@ -177,7 +176,7 @@ struct ctox_hip_backend {
     uint32_t tile_u = 0;  // CTOX_TILE_U: fixed row tiles per wave (0 = planned)
     int arrive = -1;      // CTOX_ARRIVE: 1 / 0 forces the tiled combine by arrival / by the last chunk
     uint32_t tile_cap[2][2][CTOX_TILE_MAXU] = {};  // [staged|built][q4][u - 1]: workgroups resident at once
-    uint32_t tilem_cap[2][2] = {};                  // [q4][tg - 1], same for the small-M kernels
+    uint32_t tilem_cap[2][7] = {};                  // [q4][rows - 2], same for the small-M kernels
     uint32_t tilemx_cap[2][4] = {};                 // [q4][rows - 2]
     // Tiled matvec chunk partials (64-bit slots tagged with a launch sequence
     // number; zeroed when allocated) and the last sequence number used.
@@ -599,16 +598,16 @@ ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCop
                               float *d_output, size_t out_stride, uint32_t act, hipStream_t s, const float *res_h,
                               float *res_sq, bool parts_out) {
     const int q4 = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
-    const uint32_t tg = batch > 4 ? 2 : 1;
     const uint32_t u = 1;
     const uint32_t segs = (((t.tiles + u - 1) / u) + 3) & ~3u;
     const size_t waves = (size_t)segs * t.chunks;
+    if (batch < 2 || batch > 8) return fail(CTOX_ERR_SHAPE, "small-M launch takes 2..8 rows");
     if (waves / 4 > 0x7fffffffu || out_stride > 0xffffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
     // Chunks meet as in the batch-1 launch: by the last chunk when the
     // device holds every workgroup at once, else by arrival.
     parts_out = parts_out && t.chunks > 1;
     const bool arrive =
-        t.chunks > 1 && !parts_out && (b->arrive >= 0 ? b->arrive != 0 : waves / 4 > b->tilem_cap[q4][tg - 1]);
+        t.chunks > 1 && !parts_out && (b->arrive >= 0 ? b->arrive != 0 : waves / 4 > b->tilem_cap[q4][batch - 2]);
     if (t.chunks > 1 && !parts_out) {
         ctox_status st = ensure(b, b->tpart,
                                 (size_t)(arrive ? t.chunks : t.chunks - 1) * batch * t.tiles * CTOX_TILE_ROWS * sizeof(uint64_t),
@@ -639,7 +638,7 @@ ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCop
     a.res_h = res_h;
     a.res_sq = res_sq;
     a.parts_out = parts_out ? 1u : 0u;
-    return launch(arrive ? b->tilem_arr[q4][tg - 1] : b->tilem[q4][tg - 1], dim3((unsigned)(waves / 4)), dim3(256), s, a, "ctox_q*_mv_tilem*_gfx950");
+    return launch(arrive ? b->tilem_arr[q4][batch - 2] : b->tilem[q4][batch - 2], dim3((unsigned)(waves / 4)), dim3(256), s, a, "ctox_q*_mv_tilem*_gfx950");
 }
 
 // One launch of the small-M tiled matvec that builds its 2..5 rows'
@@ -862,14 +861,10 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->tile_arr[1][0][2], "ctox_q2_mv_tile3x_gfx950_arrive"}, {&b->tile_arr[1][0][3], "ctox_q2_mv_tile4x_gfx950_arrive"},
                {&b->tile_arr[1][1][0], "ctox_q4_mv_tile1x_gfx950_arrive"}, {&b->tile_arr[1][1][1], "ctox_q4_mv_tile2x_gfx950_arrive"},
                {&b->tile_arr[1][1][2], "ctox_q4_mv_tile3x_gfx950_arrive"}, {&b->tile_arr[1][1][3], "ctox_q4_mv_tile4x_gfx950_arrive"},
-               {&b->tilem[0][0], "ctox_q2_mv_tilem1_gfx950"}, {&b->tilem[0][1], "ctox_q2_mv_tilem2_gfx950"},
-               {&b->tilem[1][0], "ctox_q4_mv_tilem1_gfx950"}, {&b->tilem[1][1], "ctox_q4_mv_tilem2_gfx950"},
                {&b->tilemx[0][0], "ctox_q2_mv_tilemx2_gfx950"}, {&b->tilemx[0][1], "ctox_q2_mv_tilemx3_gfx950"},
                {&b->tilemx[0][2], "ctox_q2_mv_tilemx4_gfx950"}, {&b->tilemx[0][3], "ctox_q2_mv_tilemx5_gfx950"},
                {&b->tilemx[1][0], "ctox_q4_mv_tilemx2_gfx950"}, {&b->tilemx[1][1], "ctox_q4_mv_tilemx3_gfx950"},
                {&b->tilemx[1][2], "ctox_q4_mv_tilemx4_gfx950"}, {&b->tilemx[1][3], "ctox_q4_mv_tilemx5_gfx950"},
-               {&b->tilem_arr[0][0], "ctox_q2_mv_tilem1_gfx950_arrive"}, {&b->tilem_arr[0][1], "ctox_q2_mv_tilem2_gfx950_arrive"},
-               {&b->tilem_arr[1][0], "ctox_q4_mv_tilem1_gfx950_arrive"}, {&b->tilem_arr[1][1], "ctox_q4_mv_tilem2_gfx950_arrive"},
                {&b->tilemx_arr[0][0], "ctox_q2_mv_tilemx2_gfx950_arrive"}, {&b->tilemx_arr[0][1], "ctox_q2_mv_tilemx3_gfx950_arrive"},
                {&b->tilemx_arr[0][2], "ctox_q2_mv_tilemx4_gfx950_arrive"}, {&b->tilemx_arr[0][3], "ctox_q2_mv_tilemx5_gfx950_arrive"},
                {&b->tilemx_arr[1][0], "ctox_q4_mv_tilemx2_gfx950_arrive"}, {&b->tilemx_arr[1][1], "ctox_q4_mv_tilemx3_gfx950_arrive"},
@@ -886,6 +881,19 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                         hipGetErrorString(le));
         }
     }
+    // The small-M kernels for staged rows, one per row count 2..8.
+    for (int q = 0; q < 2 && le == hipSuccess; q++)
+        for (int m = 0; m < 7 && le == hipSuccess; m++)
+            for (int arr = 0; arr < 2 && le == hipSuccess; arr++) {
+                char name[64];
+                std::snprintf(name, sizeof name, "ctox_q%d_mv_tilem%d_gfx950%s", q ? 4 : 2, m + 2, arr ? "_arrive" : "");
+                le = hipModuleGetFunction(arr ? &b->tilem_arr[q][m] : &b->tilem[q][m], b->module, name);
+                if (le != hipSuccess) {
+                    ctox_hip_backend_destroy(b);
+                    return fail(CTOX_ERR_UNSUPPORTED_OPERATION, "kernel %s missing from code object: %s", name,
+                                hipGetErrorString(le));
+                }
+            }
     if (le != hipSuccess) {
         ctox_hip_backend_destroy(b);
         return fail(CTOX_ERR_UNSUPPORTED_OPERATION, "HIP module setup failed: %s", hipGetErrorString(le));
@@ -909,7 +917,7 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
             b->tile_cap[0][q][u] = cap(b->tile[q][u]);
             b->tile_cap[1][q][u] = cap(b->tilex[q][u]);
         }
-        for (int g = 0; g < 2; g++) b->tilem_cap[q][g] = cap(b->tilem[q][g]);
+        for (int m = 0; m < 7; m++) b->tilem_cap[q][m] = cap(b->tilem[q][m]);
         for (int r = 0; r < 4; r++) b->tilemx_cap[q][r] = cap(b->tilemx[q][r]);
     }
     if (const char *u = std::getenv("CTOX_TILE_U")) {
