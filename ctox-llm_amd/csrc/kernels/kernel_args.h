@@ -50,7 +50,8 @@ struct NormPrepArgs {
     const float *w;         // [columns], (1 + w) weight
     float *out;             // normalized rows [batch][columns] or NULL
     float eps;
-    uint32_t pad;
+    uint32_t sq_n;          // sums of squares per row in sq_in (0: reduce the row here)
+    const float *sq_in;     // [batch][sq_n]: per 16-column tile, sum of (x + delta)^2
 };
 
 // Activation staging of a transformed input (qmatvec.hip, ctox_prep_transform_gfx950).

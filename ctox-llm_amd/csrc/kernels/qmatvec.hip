@@ -37,6 +37,7 @@
 #include <hip/hip_fp16.h>
 
 #include "kernel_args.h"
+#include "lds_barrier.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -50,15 +51,32 @@ __device__ __forceinline__ float load_scale(const void *p, uint32_t kind, uint32
     return 1.0f;
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+// Reductions over one 16-lane row with DPP (VALU speed, no LDS round
+// trips): quad xor 1, quad xor 2, half-row mirror, row mirror; every lane
+// of the row ends with the result.
+template <typename T, typename F>
+__device__ __forceinline__ T row16_reduce(T v, F op) {
+    v = op(v, __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
+    v = op(v, __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
+    v = op(v, __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
+    v = op(v, __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)));
     return v;
 }
-__device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+// The same over the whole wave: rows, then row pairs and halves with
+// permlane swaps (every lane ends with the result). For max and integer
+// sums the result does not depend on the order.
+template <typename T, typename F>
+__device__ __forceinline__ T wave64_reduce(T v, F op) {
+    v = row16_reduce(v, op);
+    const int b = __builtin_bit_cast(int, v);
+    const auto s16 = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+    v = op(__builtin_bit_cast(T, (int)s16[0]), __builtin_bit_cast(T, (int)s16[1]));
+    const int c = __builtin_bit_cast(int, v);
+    const auto s32 = __builtin_amdgcn_permlane32_swap(c, c, false, false);
+    return op(__builtin_bit_cast(T, (int)s32[0]), __builtin_bit_cast(T, (int)s32[1]));
+}
+__device__ __forceinline__ float wave_max(float v) {
+    return wave64_reduce(v, [](float x, float y) { return fmaxf(x, y); });
 }
 
 // Byte position v (0..15) inside a lane's 16-byte fragment that holds
@@ -93,7 +111,9 @@ __device__ __forceinline__ void prep_block(const PrepArgs &a, float x, uint32_t 
     const int r1 = (X - x0) >> 8;
     const int x1 = (int)(int8_t)(r1 & 0xff);
     const int x2 = (r1 - x1) >> 8;
-    const int s0 = wave_sum_i(x0), s1 = wave_sum_i(x1), s2 = wave_sum_i(x2);
+    // sum(X) = sum(X0) + 256 sum(X1) + 65536 sum(X2); |X| <= 2^22, so the
+    // 64-lane sum fits int32.
+    const int sxw = wave64_reduce(X, [](int p, int q) { return p + q; });
 
     const uint32_t g = e >> 4, w = e & 15;
     const int v = frag_pos(a.dtype, (int)w);
@@ -102,7 +122,7 @@ __device__ __forceinline__ void prep_block(const PrepArgs &a, float x, uint32_t 
     frag[(1 * 4 + g) * 16 + v] = (int8_t)x1;
     frag[(2 * 4 + g) * 16 + v] = (int8_t)x2;
     if (e == 0) {
-        const long long sx = (long long)s0 + 256LL * s1 + 65536LL * s2;
+        const long long sx = sxw;
         const long long off = a.dtype ? 15 : 3;
         float4 c;
         c.x = 2.0f * q;
@@ -124,8 +144,9 @@ extern "C" __global__ __launch_bounds__(64) void ctox_prep_activation_gfx950(Pre
 // Residual add + (1 + w) RMS norm of token row t (Q/src/reference.rs:38-62),
 // then the activation staging of prep_block from the normalized row.
 // grid (ceil(blocks / 4), batch), 256 threads: every workgroup reduces the
-// whole row's sum of squares itself (the row is L2-resident, a few KB), then
-// each of its four waves stages one 64-value block. The residual sum goes to
+// whole row's sum of squares itself (the row is L2-resident, a few KB), or
+// the producer's per-tile sums of it (sq_n), then each of its four waves
+// stages one 64-value block. The residual sum goes to
 // x_out, so no workgroup reads a value another one has already updated.
 extern "C" __global__ __launch_bounds__(256) void ctox_norm_prep_gfx950(NormPrepArgs a) {
     __shared__ float red[4];
@@ -134,53 +155,61 @@ extern "C" __global__ __launch_bounds__(256) void ctox_norm_prep_gfx950(NormPrep
     const float *dl = a.delta ? a.delta + (size_t)t * cols : nullptr;
     float s = 0.0f;
     const uint32_t n4 = cols / 4;
-    // Every load of a thread's row share (up to 8 float4 per array, all parts)
-    // is issued before the first use; parts are added in part order.
+    if (a.sq_n) {
+        // The producer's per-tile sums of squares of this row (at most 512).
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const uint32_t i = tid + 256 * k;
+            s += i < a.sq_n ? a.sq_in[(size_t)t * a.sq_n + i] : 0.0f;
+        }
+    } else {
+        // Every load of a thread's row share (up to 8 float4 per array, all parts)
+        // is issued before the first use; parts are added in part order.
 #define NP_V4 8
 #define NP_PARTS 8
-    float4 v[NP_V4];
-#pragma unroll
-    for (int k = 0; k < NP_V4; k++) {
-        const uint32_t i = tid + 256 * k;
-        v[k] = i < n4 ? ((const float4 *)x)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    }
-    if (dl) {
-        float4 d[NP_V4];
+        float4 v[NP_V4];
 #pragma unroll
         for (int k = 0; k < NP_V4; k++) {
             const uint32_t i = tid + 256 * k;
-            d[k] = i < n4 ? ((const float4 *)dl)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            v[k] = i < n4 ? ((const float4 *)x)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
+        if (dl) {
+            float4 d[NP_V4];
 #pragma unroll
-        for (int p = 1; p < NP_PARTS; p++) {
-            if ((uint32_t)p < a.delta_parts) {
+            for (int k = 0; k < NP_V4; k++) {
+                const uint32_t i = tid + 256 * k;
+                d[k] = i < n4 ? ((const float4 *)dl)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
 #pragma unroll
-                for (int k = 0; k < NP_V4; k++) {
-                    const uint32_t i = tid + 256 * k;
-                    if (i < n4) {
-                        const float4 d2 = ((const float4 *)(dl + (size_t)p * a.delta_stride))[i];
-                        d[k].x += d2.x;
-                        d[k].y += d2.y;
-                        d[k].z += d2.z;
-                        d[k].w += d2.w;
+            for (int p = 1; p < NP_PARTS; p++) {
+                if ((uint32_t)p < a.delta_parts) {
+#pragma unroll
+                    for (int k = 0; k < NP_V4; k++) {
+                        const uint32_t i = tid + 256 * k;
+                        if (i < n4) {
+                            const float4 d2 = ((const float4 *)(dl + (size_t)p * a.delta_stride))[i];
+                            d[k].x += d2.x;
+                            d[k].y += d2.y;
+                            d[k].z += d2.z;
+                            d[k].w += d2.w;
+                        }
                     }
                 }
             }
+#pragma unroll
+            for (int k = 0; k < NP_V4; k++) {
+                v[k].x += d[k].x;
+                v[k].y += d[k].y;
+                v[k].z += d[k].z;
+                v[k].w += d[k].w;
+            }
         }
 #pragma unroll
-        for (int k = 0; k < NP_V4; k++) {
-            v[k].x += d[k].x;
-            v[k].y += d[k].y;
-            v[k].z += d[k].z;
-            v[k].w += d[k].w;
-        }
+        for (int k = 0; k < NP_V4; k++) s += v[k].x * v[k].x + v[k].y * v[k].y + v[k].z * v[k].z + v[k].w * v[k].w;
     }
-#pragma unroll
-    for (int k = 0; k < NP_V4; k++) s += v[k].x * v[k].x + v[k].y * v[k].y + v[k].z * v[k].z + v[k].w * v[k].w;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    s = wave64_reduce(s, [](float p, float q) { return p + q; });
     if ((tid & 63) == 0) red[tid >> 6] = s;
-    __syncthreads();
+    lds_barrier();
     const float inv = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)cols + a.eps);
     const uint32_t wave = tid >> 6, e = tid & 63;
     const uint32_t b = blockIdx.x * 4 + wave;
@@ -231,8 +260,7 @@ extern "C" __global__ __launch_bounds__(64) void ctox_prep_transform_gfx950(Prep
             const float v = ar[head0 + i];
             ss += v * v;
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        ss = wave64_reduce(ss, [](float p, float q) { return p + q; });
         const float inv = 1.0f / sqrtf(ss / (float)a.head_dim + a.eps);
         const float g = a.b[(size_t)t * a.b_stride + col];
         x = ar[col] * inv * a.w[col % a.head_dim] * px_silu(g);

@@ -53,17 +53,8 @@ struct TileUnit {
 // non-finite value gets q = NaN. Lane 16 t + m of group G holds elements
 // 4m .. 4m + 3 of block 4G + t, so a block is one 16-lane row and every
 // reduction stays inside it. The limbs go through a wave-private LDS area
-// into the A-fragment order (the B unpack order of frag_pos).
-// Reductions over one 16-lane row with DPP (VALU speed, no LDS round
-// trips): quad xor 1, quad xor 2, half-row mirror, row mirror.
-template <typename T, typename F>
-__device__ __forceinline__ T row16_reduce(T v, F op) {
-    v = op(v, __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
-    v = op(v, __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
-    v = op(v, __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
-    v = op(v, __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)));
-    return v;
-}
+// into the A-fragment order (the B unpack order of frag_pos). Reductions
+// over a row use row16_reduce (DPP, qmatvec.hip).
 
 // Raw inputs of one 4-block group of the in-kernel fragment build.
 struct GroupIn {

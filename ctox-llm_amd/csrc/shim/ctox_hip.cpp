@@ -405,14 +405,14 @@ struct PartialSlots {
 // Small-M rows the in-kernel fragment build takes (ctox_q*_mv_tilemx*).
 constexpr size_t kMaxBuildRows = 5;
 size_t max_build_rows(const ctox_hip_backend *b) { return b->no_mx ? 1 : kMaxBuildRows; }
-// Every workgroup of a chunk rebuilds the chunk's rows, so the in-kernel
-// build pays off only for small matrices: up to 40 Mi weights (o_proj and
-// out_proj, 5120 x 6144: 5 rows in 17.5 us against 15.9 us + a 4.8 us
-// staging launch); the decode engine's larger projections measured faster
-// staged (in the engine, 5 rows of the 5120 x 17408 Q2 down: 26.8 us
-// in-kernel against 19.9 + 4.8 us).
+// Every workgroup of a chunk rebuilds the chunk's rows (5 rows: about 3 us
+// per workgroup, measured per wave), so the in-kernel build pays off only
+// for small matrices, up to 8 Mi weights. Staged rows measured faster from
+// o_proj / out_proj (5120 x 6144, 5 rows: 12.3 us built in the kernel
+// against 9.2 us + the staging launch; the 27B MTP step 7.50 against 7.35 ms)
+// upwards.
 bool build_in_kernel(const ctox_hip_backend *b, size_t batch, size_t rows, size_t columns) {
-    return batch >= 2 && batch <= max_build_rows(b) && (uint64_t)rows * columns <= (uint64_t)40 << 20;
+    return batch >= 2 && batch <= max_build_rows(b) && (uint64_t)rows * columns <= (uint64_t)8 << 20;
 }
 
 ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows, size_t columns,
@@ -1310,6 +1310,10 @@ extern "C" ctox_status ctox_hip_norm_matvec_parts_device(ctox_hip_backend *b, co
     a.w = d_norm_w;
     a.out = d_norm_out;
     a.eps = eps;
+    if (d_sums && (!d_delta || delta_parts == 1)) {
+        a.sq_in = d_sums;
+        a.sq_n = sum_count;
+    }
     if ((st = launch(b->norm_prep, dim3((unsigned)((blocks + 3) / 4), batch), dim3(256), s, a, "ctox_norm_prep_gfx950")))
         return st;
     // Registered weights, 2..8 staged rows: chunk partials for a consumer

@@ -247,11 +247,11 @@ ctox_status ctox_hip_norm_matvec_device(ctox_hip_backend *backend, const float *
 
 /* ctox_hip_norm_matvec_device with the residual's sum of squares given as
  * per-16-row-tile partials, d_sums[batch][sum_count] (a producing
- * ctox_hip_transform_matvec_device's res_sums over d_x + d_delta). Used on
- * registered weights for 1 row and for 2..5 rows of matrices up to 120 Mi
- * weights (there the fragments of every row are built in the projection's
- * launch, no staging kernel); otherwise the sums are computed from the rows
- * as before. */
+ * ctox_hip_transform_matvec_device's res_sums over d_x + d_delta), so that
+ * no workgroup re-reads the whole rows for them. Used whenever the delta is
+ * one part (batch 1 and 2..5 rows in the projection's launch, more rows in
+ * the staging launch); with several delta parts the sums are computed from
+ * the rows as before. */
 ctox_status ctox_hip_norm_matvec_sums_device(ctox_hip_backend *backend, const float *d_x, const float *d_delta,
                                              uint32_t delta_parts, size_t delta_part_stride, float *d_x_out,
                                              const float *d_norm_w, float eps, float *d_norm_out, int32_t dtype,

@@ -422,7 +422,7 @@ def _close_rows(got, ref):
                                                       (2, 0, 64, 8, 200), (1, 0, 0, 0, 8256)])
 def test_transform_matvec_rows_built_in_kernel(hip, orc, batch, mode, dtype, hd, heads, rows):
     """2..5 rows of a producer fused into a projection on registered weights
-    (up to 40 Mi weights ctox_q*_mv_tilemx*, every row's fragments built in
+    (up to 8 Mi weights ctox_q*_mv_tilemx*, every row's fragments built in
     the launch; the 8256 x 5120 case runs the staging launch and the staged
     kernel), with the residual sums of every row, against the oracle producer
     + matvec per row and float64 sums. Widths with a partial last
@@ -480,13 +480,15 @@ def test_transform_matvec_rows_built_in_kernel(hip, orc, batch, mode, dtype, hd,
         np.testing.assert_allclose(sums[t].cpu().numpy(), want, rtol=1e-5)
 
 
-@pytest.mark.parametrize("batch", [2, 4, 5])
+@pytest.mark.parametrize("batch", [2, 4, 5, 8])
 @pytest.mark.parametrize("with_delta", [True, False])
-@pytest.mark.parametrize("dtype,rows,cols", [(1, 300, 5120), (0, 64, 1536)])
+@pytest.mark.parametrize("dtype,rows,cols", [(1, 300, 5120), (0, 64, 1536), (1, 2048, 5120)])
 def test_norm_matvec_rows_with_sums(hip, orc, batch, with_delta, dtype, rows, cols):
-    """Residual add + (1 + w) RMS norm + projection of 2..5 rows from the
-    producer's per-tile sums (ctox_q*_mv_tilemx*), against the oracle norm and
-    matvec per row; the residual and normalized rows are written once."""
+    """Residual add + (1 + w) RMS norm + projection of 2..8 rows from the
+    producer's per-tile sums (2..5 rows of a small matrix: ctox_q*_mv_tilemx*,
+    built in the launch; 8 rows or more than 8 Mi weights: the staging
+    launch reads the sums), against the oracle norm and matvec per row; the
+    residual and normalized rows are written once."""
     import ctox_hip
     say(f"case norm rows batch={batch} delta={with_delta} dtype={dtype} {rows}x{cols}")
     rng = np.random.default_rng(batch * 7 + dtype + with_delta)
