@@ -75,6 +75,11 @@ __device__ __forceinline__ T wave64_reduce(T v, F op) {
     const auto s32 = __builtin_amdgcn_permlane32_swap(c, c, false, false);
     return op(__builtin_bit_cast(T, (int)s32[0]), __builtin_bit_cast(T, (int)s32[1]));
 }
+// Buffer resource over `bytes` bytes at p (none when p is NULL): reads past
+// the end return 0, so operand loads need no branch around them.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t pv_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, p ? (int)bytes : 0, 0x00020000);
+}
 __device__ __forceinline__ float wave_max(float v) {
     return wave64_reduce(v, [](float x, float y) { return fmaxf(x, y); });
 }
@@ -153,6 +158,28 @@ extern "C" __global__ __launch_bounds__(256) void ctox_norm_prep_gfx950(NormPrep
     const uint32_t t = blockIdx.y, tid = threadIdx.x, cols = a.p.columns;
     const float *x = a.x + (size_t)t * cols;
     const float *dl = a.delta ? a.delta + (size_t)t * cols : nullptr;
+    // The lane's own column (wave w stages block 4 blockIdx.x + w): its
+    // operands are read first, branch-free (an absent operand reads 0), so
+    // they travel with the row reads below.
+    const uint32_t wave = tid >> 6, e = tid & 63;
+    const uint32_t b = blockIdx.x * 4 + wave;
+    const bool live = b < cols / CTOX_BLOCK_LEN;
+    const uint32_t col = (live ? b : 0u) * CTOX_BLOCK_LEN + e;
+    const uint32_t np = a.delta ? a.delta_parts : 0u;
+    const __amdgpu_buffer_rsrc_t xr = pv_rsrc(x, 4 * cols), wr = pv_rsrc(a.w, 4 * cols);
+    const __amdgpu_buffer_rsrc_t dr = pv_rsrc(dl, np ? 4 * ((np - 1) * a.delta_stride + cols) : 0u);
+    const bool s16 = a.p.s_in_kind == CTOX_KSCALE_F16, s32 = a.p.s_in_kind == CTOX_KSCALE_F32;
+    const __amdgpu_buffer_rsrc_t sr16 = pv_rsrc(s16 ? a.p.s_in : nullptr, 2 * cols);
+    const __amdgpu_buffer_rsrc_t sr32 = pv_rsrc(s32 ? a.p.s_in : nullptr, 4 * cols);
+    const float xv0 = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(xr, col * 4, 0, 0));
+    float dv[8];
+#pragma unroll
+    for (int p = 0; p < 8; p++)
+        dv[p] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+            dr, ((uint32_t)p < np ? p * a.delta_stride + col : 0x3fffffffu) * 4, 0, 0));
+    const float wv = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(wr, col * 4, 0, 0));
+    const uint32_t sv16 = __builtin_amdgcn_raw_buffer_load_b16(sr16, col * 2, 0, 0);
+    const uint32_t sv32 = __builtin_amdgcn_raw_buffer_load_b32(sr32, col * 4, 0, 0);
     float s = 0.0f;
     const uint32_t n4 = cols / 4;
     if (a.sq_n) {
@@ -211,20 +238,20 @@ extern "C" __global__ __launch_bounds__(256) void ctox_norm_prep_gfx950(NormPrep
     if ((tid & 63) == 0) red[tid >> 6] = s;
     lds_barrier();
     const float inv = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)cols + a.eps);
-    const uint32_t wave = tid >> 6, e = tid & 63;
-    const uint32_t b = blockIdx.x * 4 + wave;
-    if (b >= cols / CTOX_BLOCK_LEN) return;
-    const uint32_t col = b * CTOX_BLOCK_LEN + e;
-    float xv = x[col];
+    if (!live) return;
+    float xv = xv0;
     if (dl) {
-        float d = dl[col];
-        for (uint32_t p = 1; p < a.delta_parts; p++) d += dl[(size_t)p * a.delta_stride + col];
+        float d = dv[0];
+#pragma unroll
+        for (int p = 1; p < 8; p++)
+            if ((uint32_t)p < np) d += dv[p];
         xv += d;
         a.x_out[(size_t)t * cols + col] = xv;
     }
-    const float y = xv * inv * (1.0f + a.w[col]);
+    const float y = xv * inv * (1.0f + wv);
     if (a.out) a.out[(size_t)t * cols + col] = y;
-    prep_block(a.p, a.p.s_in_kind != CTOX_KSCALE_NONE ? y * load_scale(a.p.s_in, a.p.s_in_kind, col) : y, b, t, e);
+    const float sc = s16 ? half_bits_to_float(sv16 & 0xffffu) : (s32 ? __int_as_float(sv32) : 1.0f);
+    prep_block(a.p, a.p.s_in_kind != CTOX_KSCALE_NONE ? y * sc : y, b, t, e);
 }
 
 // Activation staging of a value computed on the fly (one wave per 64-value
@@ -241,35 +268,71 @@ extern "C" __global__ __launch_bounds__(256) void ctox_norm_prep_gfx950(NormPrep
 __device__ __forceinline__ float px_silu(float v) { return v / (1.0f + expf(-v)); }
 
 extern "C" __global__ __launch_bounds__(64) void ctox_prep_transform_gfx950(PrepXArgs a) {
-    const uint32_t b = blockIdx.x, t = blockIdx.y, e = threadIdx.x;
-    const uint32_t col = b * CTOX_BLOCK_LEN + e;
-    const float *ar = a.a + (size_t)t * a.a_stride;
+    const uint32_t b = blockIdx.x, t = blockIdx.y, e = threadIdx.x, cols = a.p.columns;
+    const uint32_t col = b * CTOX_BLOCK_LEN + e, m = a.mode, hd = a.head_dim;
+    // Every operand goes out before the first use, branch-free (an operand
+    // the mode does not use has an empty range and reads 0).
+    const uint32_t np = m == 1 ? (a.a_parts > 1 ? a.a_parts : 1u) : 0u;
+    const __amdgpu_buffer_rsrc_t ar =
+        pv_rsrc(a.a + (size_t)t * a.a_stride, 4 * (m == 1 ? (np - 1) * a.a_pstride + a.off + cols : cols));
+    const __amdgpu_buffer_rsrc_t br = pv_rsrc(m == 1 ? nullptr : a.b + (size_t)t * a.b_stride, 4 * (m == 3 ? 2 * cols : cols));
+    const __amdgpu_buffer_rsrc_t wr = pv_rsrc(m == 2 ? a.w : nullptr, 4 * hd);
+    const bool s16 = a.p.s_in_kind == CTOX_KSCALE_F16, s32 = a.p.s_in_kind == CTOX_KSCALE_F32;
+    const __amdgpu_buffer_rsrc_t sr16 = pv_rsrc(s16 ? a.p.s_in : nullptr, 2 * cols);
+    const __amdgpu_buffer_rsrc_t sr32 = pv_rsrc(s32 ? a.p.s_in : nullptr, 4 * cols);
+    const uint32_t oob = 0x3fffffffu;  // a float index past every range (byte offset stays below 2^32)
+    // mode 1: the parts of a[col] and a[off + col]; modes 2, 3: a[col]
+    float pa[6], pu[6];
+#pragma unroll
+    for (int k = 0; k < 6; k++) {
+        const bool in = (uint32_t)k < (m == 1 ? np : 1u);
+        pa[k] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(ar, (in ? k * a.a_pstride + col : oob) * 4, 0, 0));
+        pu[k] = __int_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(ar, (in && m == 1 ? k * a.a_pstride + a.off + col : oob) * 4, 0, 0));
+    }
+    // mode 2: this head's values (head_dim <= 256 here), the gate z and the norm weight
+    const uint32_t head0 = m == 2 ? col / hd * hd : 0u;
+    float hv[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        hv[k] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+            ar, (m == 2 && e + 64 * k < hd ? head0 + e + 64 * k : oob) * 4, 0, 0));
+    const uint32_t hh = m == 3 ? col / hd : 0u, dd = m == 3 ? col % hd : 0u;
+    const float g = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+        br, (m == 3 ? hh * 2 * hd + hd + dd : col) * 4, 0, 0));
+    const float wv = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(wr, (m == 2 ? col % hd : 0u) * 4, 0, 0));
+    const uint32_t sv16 = __builtin_amdgcn_raw_buffer_load_b16(sr16, col * 2, 0, 0);
+    const uint32_t sv32 = __builtin_amdgcn_raw_buffer_load_b32(sr32, col * 4, 0, 0);
     float x;
-    if (a.mode == 1) {
+    if (m == 1) {
         // A producer's chunk partials are added in part order.
-        float ga = ar[col], ua = ar[a.off + col];
-        for (uint32_t k = 1; k < a.a_parts; k++) {
-            ga += ar[(size_t)k * a.a_pstride + col];
-            ua += ar[(size_t)k * a.a_pstride + a.off + col];
-        }
+        float ga = pa[0], ua = pu[0];
+#pragma unroll
+        for (int k = 1; k < 6; k++)
+            if ((uint32_t)k < np) {
+                ga += pa[k];
+                ua += pu[k];
+            }
         x = px_silu(ga) * ua;
-    } else if (a.mode == 2) {
-        const uint32_t head0 = col / a.head_dim * a.head_dim;
+    } else if (m == 2) {
         float ss = 0.0f;
-        for (uint32_t i = e; i < a.head_dim; i += 64) {  // this head's values, same order for every wave
-            const float v = ar[head0 + i];
-            ss += v * v;
+        if (hd <= 256) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) ss += hv[k] * hv[k];  // zeros past the head
+        } else {
+            const float *arow = a.a + (size_t)t * a.a_stride;
+            for (uint32_t i = e; i < hd; i += 64) {  // this head's values, same order for every wave
+                const float v = arow[head0 + i];
+                ss += v * v;
+            }
         }
         ss = wave64_reduce(ss, [](float p, float q) { return p + q; });
-        const float inv = 1.0f / sqrtf(ss / (float)a.head_dim + a.eps);
-        const float g = a.b[(size_t)t * a.b_stride + col];
-        x = ar[col] * inv * a.w[col % a.head_dim] * px_silu(g);
+        const float inv = 1.0f / sqrtf(ss / (float)hd + a.eps);
+        x = pa[0] * inv * wv * px_silu(g);
     } else {
-        const uint32_t h = col / a.head_dim, d = col % a.head_dim;
-        const float g = a.b[(size_t)t * a.b_stride + (size_t)h * 2 * a.head_dim + a.head_dim + d];
-        x = ar[col] * (1.0f / (1.0f + expf(-g)));
+        x = pa[0] * (1.0f / (1.0f + expf(-g)));
     }
-    if (a.p.s_in_kind != CTOX_KSCALE_NONE) x = x * load_scale(a.p.s_in, a.p.s_in_kind, col);
+    if (a.p.s_in_kind != CTOX_KSCALE_NONE) x = x * (s16 ? half_bits_to_float(sv16 & 0xffffu) : __int_as_float(sv32));
     prep_block(a.p, x, b, t, e);
 }
 
