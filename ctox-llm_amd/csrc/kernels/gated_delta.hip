@@ -155,17 +155,36 @@ __device__ __forceinline__ void gdn_load8(const GdnBuf &b, bool ok, uint32_t off
         v[4 + i] = __int_as_float(hi[i]);
     }
 }
+// Values reduced over the key rows once per block of rows (phase 2a/2b of
+// gdn_fused): A_u = S0[:, j] . k_u and B_u = S0[:, j] . q_u per row u and
+// column, then per row u the Gram sums k_w . k_u (w <= u, with |k_u|^2 last),
+// k_w . q_u (w <= u) and |q_u|^2: row u's 2u + 3 sums start at pair u^2 + 2u,
+// so the rows of a block of nb rows use the first nb^2 + 2nb pairs.
+#define GDN_NA (GDN_PREFETCH * GDN_COLS)
+#define GDN_V_B GDN_NA
+#define GDN_V_P (2 * GDN_NA)
+#define GDN_NPAIRS (GDN_PREFETCH * GDN_PREFETCH + 2 * GDN_PREFETCH)
+#define GDN_NV (GDN_V_P + GDN_NPAIRS)
+#define GDN_KK(w, u) (GDN_V_P + (u) * (u) + 2 * (u) + (w))
+#define GDN_KQ(w, u) (GDN_V_P + (u) * (u) + 3 * (u) + 1 + (w))
+#define GDN_QQ(u) (GDN_V_P + (u) * (u) + 4 * (u) + 2)
+
 template <bool BLOCKED>
 __device__ __forceinline__ void gdn_fused(const GdnFusedArgs &a) {
     // Rows are processed in blocks of up to GDN_PREFETCH. Phase 1 of a block
     // runs every row's conv + SiLU and gates (they do not depend on the
-    // state) into LDS; phase 2 runs the recurrence row by row with two
-    // barriers per row, its reduction buffers alternating between rows so no
-    // third barrier is needed before the next row writes them.
-    __shared__ float red_mem[2][GDN_GROUPS][GDN_COLS];
-    __shared__ float red_out[2][GDN_GROUPS][GDN_COLS];
-    __shared__ float red_nrm[2][2][GDN_GROUPS];
-    __shared__ float qs[GDN_PREFETCH][256], ks[GDN_PREFETCH][256], vs[GDN_PREFETCH][GDN_COLS], gsc[GDN_PREFETCH][2];
+    // state) into LDS. Phase 2 needs one reduction over the key rows for the
+    // whole block: with S0 the state at the block's start, a row's k . S and
+    // q . S follow from S0 . k_u, S0 . q_u and the Gram sums of the block's
+    // k and q (the state after row u is P_u S0 + sum_{u' <= u} c_{u'u} k^_u' d_u'^T,
+    // P and c products of the decays), so each column then runs its rows'
+    // recurrence on scalars and updates its state elements row by row.
+    // Rows padded by one float: lanes reading or writing different rows at
+    // one column hit different banks.
+    __shared__ float red[GDN_NV][GDN_GROUPS + 1];
+    __shared__ float tot[GDN_NV];
+    __shared__ float qks[2][GDN_PREFETCH][257];  // conv outputs: [0] q, [1] k (padded rows)
+    __shared__ float vs[GDN_PREFETCH][GDN_COLS], gsc[GDN_PREFETCH][2];
 
     const uint32_t slices = (a.value_dim + GDN_COLS - 1) / GDN_COLS;
     const uint32_t h = blockIdx.x / slices, slice = blockIdx.x % slices;
@@ -304,8 +323,11 @@ __device__ __forceinline__ void gdn_fused(const GdnFusedArgs &a) {
             if ((uint32_t)u >= nb) break;
             if (qk_thr) {
                 const float y = conv_step(sq_, wq, xq[u]);
-                if (tid < dk) qs[u][tid] = y;
-                else ks[u][tid - dk] = y;
+                qks[tid < dk ? 0 : 1][u][tid < dk ? tid : tid - dk] = y;
+            } else if (dk < 128) {
+                // Rows dk..127 of both planes read as zeros in phase 2.
+                const uint32_t z = tid - 2 * dk, zw = 128 - dk;
+                qks[z / zw][u][dk + z % zw] = 0.0f;
             }
             if (v_thr) vs[u][tid] = conv_step(sv_, wv, xv[u]);
             if (a.snap_stride) {
@@ -340,56 +362,88 @@ __device__ __forceinline__ void gdn_fused(const GdnFusedArgs &a) {
         }
         if (t0 + GDN_PREFETCH < a.tokens) load_block(t0 + GDN_PREFETCH);
         lds_barrier();
-        // Phase 2: the recurrence, row by row.
-        for (uint32_t u = 0; u < nb; u++) {
-            const uint32_t t = t0 + u, bsel = u & 1;
+        // Phase 2a: this thread's partial sums over its key rows i = ig + 16 r
+        // (key_dim <= 128: 8 rows; phase 1 zeroed the rows past key_dim).
+        // No branch around the LDS reads, so they go out back to back.
+#pragma unroll
+        for (int u = 0; u < GDN_PREFETCH; u++) {
+            if ((uint32_t)u >= nb) break;
+            float pa = 0.0f, pb = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 8; r++) {
+                const uint32_t i = ig + GDN_GROUPS * r;
+                pa += s[r] * qks[1][u][i];
+                pb += s[r] * qks[0][u][i];
+            }
+            red[u * GDN_COLS + jj][ig] = pa;
+            red[GDN_V_B + u * GDN_COLS + jj][ig] = pb;
+        }
+        // Gram pairs of the block's rows: column thread jj takes pairs jj,
+        // jj + 16, ...
+        const uint32_t npairs = nb * nb + 2 * nb;
+        for (uint32_t p0 = 0; p0 < npairs; p0 += GDN_COLS) {
+            const uint32_t p = min(p0 + jj, npairs - 1);
+            const uint32_t u = (uint32_t)sqrtf((float)(p + 1)) - 1u;  // (u + 1)^2 <= p + 1
+            const uint32_t q = p - (u * u + 2 * u);
+            // q <= u: k_q . k_u; q <= 2u + 1: k_(q-u-1) . q_u; else q_u . q_u
+            const uint32_t w = q <= u ? q : (q <= 2 * u + 1 ? q - u - 1 : u);
+            const uint32_t s0 = q <= 2 * u + 1 ? 1u : 0u, s1 = q <= u ? 1u : 0u;  // qks planes
+            float g = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 8; r++) {
+                const uint32_t i = ig + GDN_GROUPS * r;
+                g += qks[s0][w][i] * qks[s1][u][i];
+            }
+            if (p0 + jj < npairs) red[GDN_V_P + p][ig] = g;
+        }
+        lds_barrier();
+        // Phase 2b: totals over the 16 key-row groups, in group order.
+        for (uint32_t v = tid; v < GDN_NV; v += 256) {
+            const bool need = v < GDN_V_B ? v < nb * GDN_COLS : (v < GDN_V_P ? v - GDN_V_B < nb * GDN_COLS : v - GDN_V_P < nb * nb + 2 * nb);
+            if (!need) continue;
+            float sum = 0.0f;
+#pragma unroll
+            for (int gi = 0; gi < GDN_GROUPS; gi++) sum += red[v][gi];
+            tot[v] = sum;
+        }
+        lds_barrier();
+        // Phase 2c: each column's rows on scalars, then its state elements.
+        float P = 1.0f, coef[GDN_PREFETCH], dlt[GDN_PREFETCH], kin[GDN_PREFETCH];
+#pragma unroll
+        for (int u = 0; u < GDN_PREFETCH; u++) {
+            if ((uint32_t)u >= nb) break;
+            const uint32_t t = t0 + u;
             const float decay = gsc[u][0], beta = gsc[u][1];
             const float vjv = colok ? vs[u][jj] : 0.0f;
-            float kk[GDN_MAX_ROWS], qq[GDN_MAX_ROWS];
-            float mem = 0.0f, sk = 0.0f, sqq = 0.0f;
+            const float kinv = 1.0f / sqrtf(tot[GDN_KK(u, u)] + 1e-6f);
+            const float qinv = 1.0f / sqrtf(tot[GDN_QQ(u)] + 1e-6f);
+            P *= decay;
 #pragma unroll
-            for (int r = 0; r < GDN_MAX_ROWS; r++) {
-                const uint32_t i = ig + GDN_GROUPS * r;
-                const bool ok = (uint32_t)r < nrows && i < dk;
-                kk[r] = ok ? ks[u][i] : 0.0f;
-                qq[r] = ok ? qs[u][i] : 0.0f;
-                sk += kk[r] * kk[r];
-                sqq += qq[r] * qq[r];
+            for (int w = 0; w < u; w++) coef[w] *= decay;
+            // k_u . (decayed state after row u - 1)
+            float mem = P * tot[u * GDN_COLS + jj];
+#pragma unroll
+            for (int w = 0; w < u; w++) mem += coef[w] * (tot[GDN_KK(w, u)] * kin[w]) * dlt[w];
+            const float delta = (vjv - mem * kinv) * beta;
+            coef[u] = 1.0f;
+            dlt[u] = delta;
+            kin[u] = kinv;
+            // q_u . (state after row u)
+            float o = P * tot[GDN_V_B + u * GDN_COLS + jj];
+#pragma unroll
+            for (int w = 0; w <= u; w++) o += coef[w] * (tot[GDN_KQ(w, u)] * kin[w]) * dlt[w];
+            if (ig == 0 && colok) a.out[((size_t)t * a.heads + h) * a.value_dim + j] = o * qinv * qscale;
+#pragma unroll
+            for (int r = 0; r < 8; r++) {
+                const float kk = qks[1][u][ig + GDN_GROUPS * r];
                 s[r] = s[r] * decay;
-                mem += s[r] * kk[r];
-            }
-            red_mem[bsel][ig][jj] = mem;
-            if (jj == 0) {
-                red_nrm[bsel][0][ig] = sk;
-                red_nrm[bsel][1][ig] = sqq;
-            }
-            lds_barrier();
-            float memj = 0.0f, ssk = 0.0f, ssq = 0.0f;
-#pragma unroll
-            for (int gi = 0; gi < GDN_GROUPS; gi++) {
-                memj += red_mem[bsel][gi][jj];
-                ssk += red_nrm[bsel][0][gi];
-                ssq += red_nrm[bsel][1][gi];
-            }
-            const float kinv = 1.0f / sqrtf(ssk + 1e-6f), qinv = 1.0f / sqrtf(ssq + 1e-6f);
-            const float delta = (vjv - memj * kinv) * beta;
-            float o = 0.0f;
-#pragma unroll
-            for (int r = 0; r < GDN_MAX_ROWS; r++) {
-                s[r] += kk[r] * kinv * delta;
-                o += s[r] * qq[r];
-            }
-            red_out[bsel][ig][jj] = o;
-            lds_barrier();
-            if (ig == 0 && colok) {
-                float oj = 0.0f;
-#pragma unroll
-                for (int gi = 0; gi < GDN_GROUPS; gi++) oj += red_out[bsel][gi][jj];
-                a.out[((size_t)t * a.heads + h) * a.value_dim + j] = oj * qinv * qscale;
+                s[r] += kk * kinv * delta;
             }
             // Row snapshot: the state after row t.
             if (a.snap_stride) store_state(a.state_out + (size_t)t * a.snap_stride);
         }
+        // The next block's phase 1 rewrites the row buffers read above.
+        if (t0 + GDN_PREFETCH < a.tokens) lds_barrier();
     }
     if (a.snap_stride) return;
 
