@@ -41,6 +41,11 @@
 typedef float pa_v4f __attribute__((ext_vector_type(4)));
 
 #define PA_HD 256  // head dim: four 64-value blocks, one per MFMA lane group
+// The page-aligned kernel keeps its running maxima in base-2 units (scores
+// times log2 e) so each probability is one v_exp_f32; its stats leave in
+// natural units.
+#define PA_LOG2E 1.44269504088896341f
+#define PA_LN2 0.693147180559945309f
 
 __device__ __forceinline__ float pa_half(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
@@ -700,7 +705,7 @@ __device__ __forceinline__ void pa_tile16(const GqaArgs &a, LDS &L, const int8_t
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const int32_t j = (int32_t)(tb + 4 * lg + c);
-            sc[c] = present[c] && j <= st.lim[r] ? s[r][c] * a.scale : -INFINITY;
+            sc[c] = present[c] && j <= st.lim[r] ? s[r][c] * (a.scale * PA_LOG2E) : -INFINITY;
             mt = fmaxf(mt, sc[c]);
         }
         mt = pa_max_x32(pa_max_x16(mt));
@@ -709,9 +714,9 @@ __device__ __forceinline__ void pa_tile16(const GqaArgs &a, LDS &L, const int8_t
         if (mn == -INFINITY) {
             p[r][0] = p[r][1] = p[r][2] = p[r][3] = 0.0f;
         } else {
-            alpha = expf(st.m[r] - mn);
+            alpha = __builtin_amdgcn_exp2f(st.m[r] - mn);
 #pragma unroll
-            for (int c = 0; c < 4; c++) p[r][c] = expf(sc[c] - mn);
+            for (int c = 0; c < 4; c++) p[r][c] = __builtin_amdgcn_exp2f(sc[c] - mn);
         }
         st.den[r] = st.den[r] * alpha + ((p[r][0] + p[r][1]) + (p[r][2] + p[r][3]));
         st.m[r] = mn;
@@ -988,12 +993,12 @@ __device__ __forceinline__ void paged_gqa_partial16(const GqaArgs &a) {
 #pragma unroll
         for (int w = 0; w < 3; w++) mm = fmaxf(mm, xm[w * R * 16 + 16 * r + li]);
         float f[4];
-        f[0] = mm == -INFINITY ? 0.0f : expf(st.m[r] - mm);
+        f[0] = mm == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(st.m[r] - mm);
         float den = st.den[r] * f[0];
 #pragma unroll
         for (int w = 0; w < 3; w++) {
             const uint32_t row = w * R * 16 + 16 * r + li;
-            f[w + 1] = mm == -INFINITY ? 0.0f : expf(xm[row] - mm);
+            f[w + 1] = mm == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(xm[row] - mm);
             den += xd[row] * f[w + 1];
         }
         float *dst = a.part_out + (base + qi) * PA_HD;
@@ -1015,7 +1020,7 @@ __device__ __forceinline__ void paged_gqa_partial16(const GqaArgs &a) {
                 if (qi < a.queries) *(float4 *)&dst[d] = v;
             }
         if (qi < a.queries && lg == 0) {
-            a.part_stats[2 * (base + qi)] = mm;
+            a.part_stats[2 * (base + qi)] = mm * PA_LN2;  // the combine works in natural units
             a.part_stats[2 * (base + qi) + 1] = den;
         }
     }
