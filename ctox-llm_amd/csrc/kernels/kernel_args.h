@@ -194,6 +194,25 @@ struct TileMatvecArgs {
     // producer's res_h / res_sq rows `rows` / `tiles` apart.
     uint32_t a_stride;
     uint32_t b_stride;
+    // Small-M producer of a residual delta that also stages the next (1 + w)
+    // RMS-normed projection's input (nx_xa set; the last chunk combines, rows
+    // a multiple of 64): per token row t and output row r, h = res_h + out goes
+    // to nx_h[t][r], h * (1 + nx_w[r]) * nx_s_in[r] (f16 scale, or none) is
+    // staged in nx_xa / nx_xc ([block][token], nx_dtype's fragment order)
+    // without the row's 1 / rms, and nx_sq[t][block] receives the block's sum
+    // of h^2. The consumer, a staged small-M launch with rms_sq set, scales
+    // token row t's outputs by 1 / sqrt(sum(rms_sq[t][0 .. rms_n)) / (blocks * 64) + eps).
+    const float *rms_sq;
+    uint32_t rms_n;
+    uint32_t rms_pad;
+    int8_t *nx_xa;
+    float *nx_xc;
+    float *nx_h;
+    const float *nx_w;
+    const uint16_t *nx_s_in;
+    float *nx_sq;
+    uint32_t nx_dtype;
+    uint32_t nx_pad;
 };
 
 struct RecoveredRowArgs {

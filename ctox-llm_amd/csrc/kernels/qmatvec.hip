@@ -95,9 +95,11 @@ __device__ __forceinline__ int frag_pos(uint32_t dtype, int w) {
 // One wave (64 threads) per (block, token). Output layout:
 //   xa: [block][token][limb 0..2][quarter 0..3][16 bytes]
 //   xc: [block][token] float4 {2q, 512q, 131072q, K*q}, K = -off*sum(X)
-// Prepares one 64-value block of token t from one value per lane (x already
-// multiplied by s_in); every lane of the wave takes part.
-__device__ __forceinline__ void prep_block(const PrepArgs &a, float x, uint32_t b, uint32_t t, uint32_t e) {
+// Stages one 64-value block from one value per lane (x already multiplied
+// by s_in; element e of the block in lane e): its three limbs go to frag
+// (192 bytes, the xa order above) and, from lane 0, its constants to *xc.
+// Every lane of the wave takes part.
+__device__ __forceinline__ void stage_block(float x, int8_t *frag, float4 *xc, uint32_t dtype, uint32_t e) {
     const bool bad = !__builtin_isfinite(x);
     const bool any_bad = __any(bad);
     const float m = wave_max(bad ? 0.0f : fabsf(x));
@@ -121,21 +123,26 @@ __device__ __forceinline__ void prep_block(const PrepArgs &a, float x, uint32_t 
     const int sxw = wave64_reduce(X, [](int p, int q) { return p + q; });
 
     const uint32_t g = e >> 4, w = e & 15;
-    const int v = frag_pos(a.dtype, (int)w);
-    int8_t *frag = a.xa + ((size_t)b * a.batch + t) * (3 * 64);
+    const int v = frag_pos(dtype, (int)w);
     frag[(0 * 4 + g) * 16 + v] = (int8_t)x0;
     frag[(1 * 4 + g) * 16 + v] = (int8_t)x1;
     frag[(2 * 4 + g) * 16 + v] = (int8_t)x2;
     if (e == 0) {
         const long long sx = sxw;
-        const long long off = a.dtype ? 15 : 3;
+        const long long off = dtype ? 15 : 3;
         float4 c;
         c.x = 2.0f * q;
         c.y = 512.0f * q;
         c.z = 131072.0f * q;
         c.w = (float)(-off * sx) * q;
-        ((float4 *)a.xc)[(size_t)b * a.batch + t] = c;
+        *xc = c;
     }
+}
+
+// Prepares one 64-value block of token t from one value per lane (x already
+// multiplied by s_in); every lane of the wave takes part.
+__device__ __forceinline__ void prep_block(const PrepArgs &a, float x, uint32_t b, uint32_t t, uint32_t e) {
+    stage_block(x, a.xa + ((size_t)b * a.batch + t) * (3 * 64), (float4 *)a.xc + (size_t)b * a.batch + t, a.dtype, e);
 }
 
 extern "C" __global__ __launch_bounds__(64) void ctox_prep_activation_gfx950(PrepArgs a) {

@@ -614,6 +614,66 @@ __device__ __forceinline__ void residual_tile_sum_m(const TileMatvecArgs &a, uin
     if (mine && j == 0) a.res_sq[(size_t)tok * a.tiles + tile] = s;
 }
 
+// Consumer side of the next-norm staging (a.rms_sq: per-block sums of h^2
+// of the staged rows, which were staged without their 1 / rms): per token
+// row t < M, 1 / sqrt(sum / (blocks * 64) + eps) into inv[t]. Thread
+// (t, i) = (tid / 32, tid % 32) adds entries i, i + 32, i + 64, i + 96 of
+// row t; its loads go out with the prologue's and are added after `wait`.
+struct RmsIn {
+    float v[4];
+};
+__device__ __forceinline__ RmsIn rms_loads(const TileMatvecArgs &a, uint32_t M) {
+    RmsIn r;
+    const uint32_t t = threadIdx.x >> 5, i = threadIdx.x & 31;
+    const __amdgpu_buffer_rsrc_t rs = f32_rsrc(a.rms_sq, a.rms_sq ? M * a.rms_n : 0u);
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        r.v[k] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+            rs, (t < M && i + 32 * k < a.rms_n ? t * a.rms_n + i + 32 * k : 0x1fffffffu) * 4, 0, 0));
+    return r;
+}
+__device__ __forceinline__ void rms_finish(const TileMatvecArgs &a, const RmsIn &r, float *inv) {
+    float s = (r.v[0] + r.v[1]) + (r.v[2] + r.v[3]);
+    s = row16_reduce(s, [](float x, float y) { return x + y; });
+    s += __shfl_xor(s, 16);
+    if ((threadIdx.x & 31) == 0 && (threadIdx.x >> 5) < 8)
+        inv[threadIdx.x >> 5] = 1.0f / sqrtf(s / (float)(a.blocks * CTOX_BLOCK_LEN) + a.eps);
+}
+
+// Producer side of the next-norm staging (a.nx_xa): the workgroup's four
+// waves hold row tiles 4 b .. 4 b + 3 of the output, i.e. 64-column block b
+// of the next projection's input. Lane (g, j) has h = res_h + out of token
+// rows 4 tg + g at row j of its tile; the block's values h * (1 + w) * s_in
+// meet in LDS and wave w stages token rows w, w + 4 (stage_block, the prep
+// kernel's arithmetic), with the block's sum of h^2 per token.
+template <int TG>
+__device__ __forceinline__ void stage_next_norm(const TileMatvecArgs &a, uint32_t tile, uint32_t g, uint32_t j,
+                                                uint32_t M, const float (&hv)[TG], const bool (&want)[TG], float wn,
+                                                float sc) {
+    __shared__ float nxv[8 * 64];
+    __shared__ float nss[8 * 4];
+    const uint32_t w = tile & 3, lane = threadIdx.x & 63, b = tile >> 2;
+    const uint32_t row = tile * CTOX_TILE_ROWS + j;
+#pragma unroll
+    for (int tg = 0; tg < TG; tg++) {
+        const uint32_t tok = 4 * tg + g;
+        if (want[tg]) {
+            a.nx_h[(size_t)tok * a.rows + row] = hv[tg];
+            nxv[tok * 64 + 16 * w + j] = hv[tg] * (1.0f + wn) * sc;
+        }
+        const float ss = row16_reduce(hv[tg] * hv[tg], [](float x, float y) { return x + y; });
+        if (j == 0 && tok < M) nss[tok * 4 + w] = ss;
+    }
+    lds_barrier();
+    const uint32_t nb = a.rows / CTOX_BLOCK_LEN;
+    for (uint32_t tok = w; tok < M; tok += 4) {
+        stage_block(nxv[tok * 64 + lane], a.nx_xa + ((size_t)b * M + tok) * 192, (float4 *)a.nx_xc + (size_t)b * M + tok,
+                    a.nx_dtype, lane);
+        if (lane == 0)
+            a.nx_sq[(size_t)tok * nb + b] = (nss[tok * 4 + 0] + nss[tok * 4 + 1]) + (nss[tok * 4 + 2] + nss[tok * 4 + 3]);
+    }
+}
+
 // MR = M, the row count, is a compile-time constant: every LDS address of
 // the MFMA loop is a per-lane base plus an immediate offset.
 // Tail of the small-M kernels: lane (g, j) of unit k and token group tg
@@ -623,7 +683,8 @@ __device__ __forceinline__ void residual_tile_sum_m(const TileMatvecArgs &a, uin
 // (ARR = 0), else by the chunk that arrives last at the tile's count.
 template <int DT, int U, int TG, int ARR>
 __device__ __forceinline__ void small_m_finish(const TileMatvecArgs &a, uint32_t c, uint32_t t0, uint32_t n,
-                                               uint32_t g, uint32_t j, uint32_t M, const float (&acc)[U][TG]) {
+                                               uint32_t g, uint32_t j, uint32_t M, const float (&acc)[U][TG],
+                                               const float (&inv)[TG]) {
     using C = TlCfg<DT>;
     const size_t tstride = (size_t)a.tiles * CTOX_TILE_ROWS, cstride = tstride * M;
     if (a.parts_out) {
@@ -636,7 +697,7 @@ __device__ __forceinline__ void small_m_finish(const TileMatvecArgs &a, uint32_t
                 const uint32_t tok = 4 * tg + g, row = (t0 + k) * CTOX_TILE_ROWS + j;
                 const EpiIn e = epi_load(a, row, 0);
                 if ((uint32_t)k < n && tok < M && row < a.rows)
-                    a.output[((size_t)c * M + tok) * a.out_stride + row] = epi_apply(acc[k][tg] / C::DEN, e, a);
+                    a.output[((size_t)c * M + tok) * a.out_stride + row] = epi_apply(acc[k][tg] * inv[tg] / C::DEN, e, a);
             }
         return;
     }
@@ -656,6 +717,13 @@ __device__ __forceinline__ void small_m_finish(const TileMatvecArgs &a, uint32_t
     for (int k = 0; k < U; k++)
 #pragma unroll
         for (int tg = 0; tg < TG; tg++) e[k][tg] = epi_load(a, (t0 + k) * CTOX_TILE_ROWS + j, min(4 * tg + g, M - 1));
+    // Next-norm staging operands of the wave's rows, read ahead of the combine.
+    const uint32_t nrow = t0 * CTOX_TILE_ROWS + j;
+    const uint32_t nwb = __builtin_amdgcn_raw_buffer_load_b32(f32_rsrc(a.nx_xa ? a.nx_w : nullptr, a.rows), nrow * 4, 0, 0);
+    const uint32_t nsb = __builtin_amdgcn_raw_buffer_load_b16(
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.nx_s_in, (short)0, a.nx_xa && a.nx_s_in ? (int)(a.rows * 2) : 0,
+                                          0x00020000),
+        nrow * 2, 0, 0);
     bool last[U];
 #pragma unroll
     for (int k = 0; k < U; k++) last[k] = true;
@@ -697,13 +765,18 @@ __device__ __forceinline__ void small_m_finish(const TileMatvecArgs &a, uint32_t
             for (int tg = 0; tg < TG; tg++) slots[tg] = &a.partial[want[tg] ? (size_t)(4 * tg + g) * tstride + row : j];
             combine_poll_n<TG>(slots, cstride, a.chunks, c, a.seq, acc[k], want, sum);
         }
+        float hv[TG];
 #pragma unroll
         for (int tg = 0; tg < TG; tg++) {
             const uint32_t tok = 4 * tg + g;
-            const float y = want[tg] && row < a.rows ? epi_apply(sum[tg] / C::DEN, e[k][tg], a) : 0.0f;
+            const float y = want[tg] && row < a.rows ? epi_apply(sum[tg] * inv[tg] / C::DEN, e[k][tg], a) : 0.0f;
             if (want[tg] && row < a.rows) a.output[(size_t)tok * a.out_stride + row] = y;
             if (a.res_sq) residual_tile_sum_m(a, min(tok, M - 1), tile, row, want[tg], y, j, e[k][tg]);
+            hv[tg] = want[tg] && row < a.rows ? __uint_as_float(e[k][tg].h) + y : 0.0f;
         }
+        if (!ARR && U == 1 && a.nx_xa)
+            stage_next_norm<TG>(a, tile, g, j, M, hv, want, __uint_as_float(nwb),
+                                a.nx_s_in ? half_bits_to_float(nsb & 0xffffu) : 1.0f);
         if (ARR && a.chunks > 1 && (threadIdx.x & 63) == 0)
             __hip_atomic_store(&a.arrive[t0 + k], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -742,6 +815,8 @@ __device__ __forceinline__ void tile_matvec_m(const TileMatvecArgs &a) {
 #pragma unroll
     for (int i = 0; i < (int)XL; i++) xl[i] = __builtin_amdgcn_raw_buffer_load_b128(fr, (threadIdx.x + 256 * i) * 16, 0, 0);
     const v4i kv = __builtin_amdgcn_raw_buffer_load_b128(cr, threadIdx.x * 16, 0, 0);
+    const RmsIn rin = rms_loads(a, M);
+    __shared__ float invs[8];
     __builtin_amdgcn_sched_barrier(0);
     TileUnit<DT> u[U];
     v2u sc[U][4];
@@ -761,8 +836,13 @@ __device__ __forceinline__ void tile_matvec_m(const TileMatvecArgs &a) {
     if (threadIdx.x < CTOX_TILE_BLOCKS * MAXM)
         kqs[threadIdx.x] = make_float4(__int_as_float(kv[0]), __int_as_float(kv[1]), __int_as_float(kv[2]), __int_as_float(kv[3]));
     if (threadIdx.x == 0) *(v4i *)(xas + CTOX_TILE_BLOCKS * MAXM * 192) = (v4i){0, 0, 0, 0};
+    if (a.rms_sq) rms_finish(a, rin, invs);
     lds_barrier();
     if (t0 >= a.tiles) return;
+    // Staged launches with a.rms_sq: 1 / rms of the lane's token rows.
+    float inv[TG];
+#pragma unroll
+    for (int tg = 0; tg < (int)TG; tg++) inv[tg] = a.rms_sq ? invs[min(4 * tg + g, M - 1)] : 1.0f;
 
     // Tiles in load order (the compute of tile k needs only its own loads);
     // the A fragments are re-read from LDS per tile.
@@ -816,7 +896,7 @@ __device__ __forceinline__ void tile_matvec_m(const TileMatvecArgs &a) {
             }
         }
     }
-    small_m_finish<DT, U, TG, ARR>(a, c, t0, n, g, j, M, acc);
+    small_m_finish<DT, U, TG, ARR>(a, c, t0, n, g, j, M, acc, inv);
 }
 
 // ctox_q{2,4}_mv_tilem{M}_gfx950: M = 2..8 staged rows, one tile per wave.
@@ -864,27 +944,32 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, void *lds, u
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, 0, 0, 0);
 }
 
-template <int DT, int MR, int ARR>
+// NW waves per workgroup (a multiple of 4, all on one chunk): wave w builds
+// group w % 4 of rows w / 4, w / 4 + NW / 4, ... so a wider workgroup splits
+// the chunk's 4 x M group builds over more waves.
+template <int DT, int MR, int ARR, int NW = 4>
 __device__ __forceinline__ void tile_matvec_mx(const TileMatvecArgs &a) {
     using C = TlCfg<DT>;
     constexpr uint32_t U = 1, TG = (MR + 3) / 4, INB = 2048;
+    constexpr uint32_t RW = NW / 4;  // rows a group's builders step by
     constexpr uint32_t WLOADS = U * (C::LPU + 4);  // weight loads issued after the input copies
     __shared__ __align__(16) uint8_t ins[4 * MR * INB];
     __shared__ __align__(16) int8_t xas[CTOX_TILE_BLOCKS * MR * 192];
     __shared__ float4 kqs[CTOX_TILE_BLOCKS * MR];
     __shared__ __align__(16) float sqs[MR * 512];
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const uint32_t v = __builtin_amdgcn_readfirstlane(blockIdx.x * 4u + w);
+    const uint32_t v = __builtin_amdgcn_readfirstlane(blockIdx.x * (uint32_t)NW + w);
     const uint32_t c = v / a.segs, s = v - c * a.segs;
     constexpr uint32_t M = MR;
     const uint32_t t0 = s * U;
-    if (c >= a.chunks) return;  // uniform over the workgroup (segs is a multiple of 4)
+    if (c >= a.chunks) return;  // uniform over the workgroup (segs is a multiple of NW)
     const uint32_t n = t0 < a.tiles ? min(U, a.tiles - t0) : 0u;
     const uint8_t *base = a.weights + ((size_t)c * a.tiles + min(t0, a.tiles - 1)) * C::UB;
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)(n * C::UB), 0x00020000);
     const uint32_t g = lane >> 4, j = lane & 15, limb = j & 3;
     const uint32_t cols = a.blocks * CTOX_BLOCK_LEN, xm = a.xmode, dh = a.head_dim ? a.head_dim : 1u;
-    const uint32_t grp = c * 4 + w, col = grp * 256 + 4 * lane;
+    const uint32_t wg = w & 3, r0 = w >> 2;  // this wave's group and first row
+    const uint32_t grp = c * 4 + wg, col = grp * 256 + 4 * lane;
 
     // Input copies (rows t < M): operand a at [0, 1 KiB), b at [1 KiB, 2 KiB)
     // of the wave's row area; an absent operand reads zeros.
@@ -896,8 +981,8 @@ __device__ __forceinline__ void tile_matvec_mx(const TileMatvecArgs &a) {
         const uint32_t bstr = xm == 2 ? a.a_stride : a.b_stride;
         const __amdgpu_buffer_rsrc_t br = f32_rsrc(xm == 0 ? nullptr : bp, bext ? (M - 1) * bstr + bext : 0u);
         const uint32_t bo = xm == 2 ? a.off + col : (xm == 4 ? (col / dh) * 2 * dh + dh + col % dh : col);
-        for (uint32_t t = 0; t < M; t++) {
-            uint8_t *dst = ins + (w * MR + t) * INB;
+        for (uint32_t t = r0; t < M; t += RW) {
+            uint8_t *dst = ins + (wg * MR + t) * INB;
             lds_dma16(ar, dst, (t * a.a_stride + col) * 4);
             lds_dma16(br, dst + 1024, (t * bstr + bo) * 4);
         }
@@ -936,11 +1021,11 @@ __device__ __forceinline__ void tile_matvec_mx(const TileMatvecArgs &a) {
     CTOX_WAIT_VMCNT(WLOADS);  // the input copies and the two operand loads have landed
     __builtin_amdgcn_sched_barrier(0);
     if (xm == 1) lds_barrier();  // wave 0's copy of the sums is visible
-    const bool keep = ((blockIdx.x * 4u) % a.segs) == 0;  // segment 0 of the chunk
+    const bool keep = ((blockIdx.x * (uint32_t)NW) % a.segs) == 0;  // segment 0 of the chunk
     // One row at a time (not unrolled: the build's temporaries are live
     // beside the weight loads in flight).
 #pragma unroll 1
-    for (uint32_t t = 0; t < M; t++) {
+    for (uint32_t t = r0; t < M; t += RW) {
         float inv = 0.0f;
         if (xm == 1) {
             float ss = 0.0f;
@@ -954,13 +1039,13 @@ __device__ __forceinline__ void tile_matvec_mx(const TileMatvecArgs &a) {
             ss += __shfl_xor(ss, 32);
             inv = 1.0f / sqrtf(ss / (float)cols + a.eps);
         }
-        const uint8_t *src = ins + (w * MR + t) * INB;
+        const uint8_t *src = ins + (wg * MR + t) * INB;
         gin.a = *(const v4i *)(src + lane * 16);
         gin.b = *(const v4i *)(src + 1024 + lane * 16);
-        const float4 k = frag_group_build<DT>(a, grp, lane, gin, inv, keep, xas + ((4 * w) * M + t) * 192, M * 192,
+        const float4 k = frag_group_build<DT>(a, grp, lane, gin, inv, keep, xas + ((4 * wg) * M + t) * 192, M * 192,
                                               a.x_out ? a.x_out + (size_t)t * cols : nullptr,
                                               a.norm_out ? a.norm_out + (size_t)t * cols : nullptr);
-        if (j == 0) kqs[(4 * w + g) * M + t] = k;
+        if (j == 0) kqs[(4 * wg + g) * M + t] = k;
     }
     lds_barrier();  // fragments and constants of every group and row
     if (t0 >= a.tiles) return;
@@ -1021,7 +1106,11 @@ __device__ __forceinline__ void tile_matvec_mx(const TileMatvecArgs &a) {
             }
         }
     }
-    small_m_finish<DT, U, TG, ARR>(a, c, t0, n, g, j, M, acc);
+    const float inv[TG] = {};
+    float one[TG];
+#pragma unroll
+    for (int tg = 0; tg < (int)TG; tg++) one[tg] = 1.0f + inv[tg];
+    small_m_finish<DT, U, TG, ARR>(a, c, t0, n, g, j, M, acc, one);
 }
 
 #define CTOX_TILE_MX_KERNEL(name, dt, mr) \
@@ -1035,6 +1124,19 @@ CTOX_TILE_MX_KERNEL(ctox_q4_mv_tilemx2_gfx950, 1, 2)
 CTOX_TILE_MX_KERNEL(ctox_q4_mv_tilemx3_gfx950, 1, 3)
 CTOX_TILE_MX_KERNEL(ctox_q4_mv_tilemx4_gfx950, 1, 4)
 CTOX_TILE_MX_KERNEL(ctox_q4_mv_tilemx5_gfx950, 1, 5)
+// Sixteen-wave workgroups: each wave builds at most two of the chunk's
+// 4 x M group rows (ctox_q{2,4}_mv_tilemxw{M}_gfx950).
+#define CTOX_TILE_MXW_KERNEL(name, dt, mr) \
+    extern "C" __global__ __launch_bounds__(1024) void name(TileMatvecArgs a) { tile_matvec_mx<dt, mr, 0, 16>(a); } \
+    extern "C" __global__ __launch_bounds__(1024) void name##_arrive(TileMatvecArgs a) { tile_matvec_mx<dt, mr, 1, 16>(a); }
+CTOX_TILE_MXW_KERNEL(ctox_q2_mv_tilemxw2_gfx950, 0, 2)
+CTOX_TILE_MXW_KERNEL(ctox_q2_mv_tilemxw3_gfx950, 0, 3)
+CTOX_TILE_MXW_KERNEL(ctox_q2_mv_tilemxw4_gfx950, 0, 4)
+CTOX_TILE_MXW_KERNEL(ctox_q2_mv_tilemxw5_gfx950, 0, 5)
+CTOX_TILE_MXW_KERNEL(ctox_q4_mv_tilemxw2_gfx950, 1, 2)
+CTOX_TILE_MXW_KERNEL(ctox_q4_mv_tilemxw3_gfx950, 1, 3)
+CTOX_TILE_MXW_KERNEL(ctox_q4_mv_tilemxw4_gfx950, 1, 4)
+CTOX_TILE_MXW_KERNEL(ctox_q4_mv_tilemxw5_gfx950, 1, 5)
 
 // Rewrites crate rows (Q/src/quant.rs:20-29 block layout, rows dense) into
 // the tiled layout; one workgroup per unit, lane (g, j) moves its fragment

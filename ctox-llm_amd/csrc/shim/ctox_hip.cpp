@@ -13,6 +13,7 @@
 // fallback anywhere in this file: a missing device or code object fails
 // closed with CTOX_ERR_UNSUPPORTED_OPERATION.
 #include "ctox_hip.h"
+#include "shim_internal.h"
 
 #include <hip/hip_runtime_api.h>
 
@@ -168,6 +169,10 @@ struct ctox_hip_backend {
     // The same building the rows' fragments in the kernel, per row count 2..5.
     hipFunction_t tilemx[2][4] = {};
     hipFunction_t tilemx_arr[2][4] = {};  // combine by arrival
+    hipFunction_t tilemxw[2][4] = {};     // sixteen-wave workgroups
+    hipFunction_t tilemxw_arr[2][4] = {};
+    uint32_t mx_waves = 4;                // CTOX_MX_W: waves per tilemx workgroup (4 or 16)
+    uint64_t mx_max = (uint64_t)8 << 20;  // CTOX_MX_MAX (Mi): largest matrix the small-M launch builds rows for
     bool no_mx = false;
     bool noalloc_ok = false;  // the static scratch of ctox_hip_launch_fused_matvec_noalloc is set up
     hipFunction_t repack = nullptr;
@@ -178,6 +183,7 @@ struct ctox_hip_backend {
     uint32_t tile_cap[2][2][CTOX_TILE_MAXU] = {};  // [staged|built][q4][u - 1]: workgroups resident at once
     uint32_t tilem_cap[2][7] = {};                  // [q4][rows - 2], same for the small-M kernels
     uint32_t tilemx_cap[2][4] = {};                 // [q4][rows - 2]
+    uint32_t tilemxw_cap[2][4] = {};
     // Tiled matvec chunk partials (64-bit slots tagged with a launch sequence
     // number; zeroed when allocated) and the last sequence number used.
     DevBuf tpart;
@@ -187,6 +193,9 @@ struct ctox_hip_backend {
     std::unordered_map<const void *, TiledCopy> raw_tiled;
     // Activation staging (two layouts: [0] Q2, [1] Q4) and gated-delta norms.
     DevBuf xa[2], xc[2], norms;
+    // Next-norm staging written by a small-M residual producer for the
+    // projection that follows it (separate from xa/xc, which the producer reads).
+    DevBuf xn[2], xnc[2];
     // Token selection scratch: per-part partials, pick sums and state.
     DevBuf tok, stats;
     // Split-attention partials.
@@ -412,7 +421,7 @@ size_t max_build_rows(const ctox_hip_backend *b) { return b->no_mx ? 1 : kMaxBui
 // against 9.2 us + the staging launch; the 27B MTP step 7.50 against 7.35 ms)
 // upwards.
 bool build_in_kernel(const ctox_hip_backend *b, size_t batch, size_t rows, size_t columns) {
-    return batch >= 2 && batch <= max_build_rows(b) && (uint64_t)rows * columns <= (uint64_t)8 << 20;
+    return batch >= 2 && batch <= max_build_rows(b) && (uint64_t)rows * columns <= b->mx_max;
 }
 
 ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows, size_t columns,
@@ -421,10 +430,33 @@ ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy 
                             uint32_t s_in_kind = CTOX_KSCALE_NONE, const TileXform *xf = nullptr,
                             const PartialSlots *ps = nullptr);
 
+// Staging of the next (1 + w) RMS-normed projection by a small-M residual
+// producer (TileMatvecArgs::nx_xa): the next norm weight, the next matrix's
+// f16 s_in and packed dtype, where h = residual + output goes, and where the
+// per-block sums of h^2 go ([batch][rows / 64]).
+struct NextNorm {
+    const float *w = nullptr;
+    const uint16_t *s_in = nullptr;
+    int32_t dtype = 0;
+    float *h_out = nullptr;
+    float *sq_out = nullptr;
+};
+
+// Staged input of a small-M launch other than the backend's xa/xc, with
+// the consumer side of a next-norm staging (rms_sq: per-block sums of h^2).
+struct StagedIn {
+    const int8_t *xa = nullptr;
+    const float *xc = nullptr;
+    const float *rms_sq = nullptr;
+    uint32_t rms_n = 0;
+    float eps = 0.0f;
+};
+
 ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows, size_t columns,
                               size_t batch, const void *d_s_out, uint32_t s_out_kind, const float *d_bias,
                               float *d_output, size_t out_stride, uint32_t act, hipStream_t s,
-                              const float *res_h = nullptr, float *res_sq = nullptr, bool parts_out = false);
+                              const float *res_h = nullptr, float *res_sq = nullptr, bool parts_out = false,
+                              const NextNorm *nx = nullptr, bool *staged = nullptr, const StagedIn *in = nullptr);
 
 ctox_status run_tile_matvec_mx(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows, size_t columns,
                                size_t batch, const void *d_s_out, uint32_t s_out_kind, const float *d_bias,
@@ -441,7 +473,7 @@ ctox_status run_matvec(ctox_hip_backend *b, int layout, int32_t dtype, const voi
                        size_t columns, size_t batch, const void *d_s_out, uint32_t s_out_kind,
                        const float *d_bias, float *d_output, size_t out_stride, uint32_t act,
                        hipStream_t s, bool split = false, uint32_t *parts = nullptr, const float *res_h = nullptr,
-                       float *res_sq = nullptr) {
+                       float *res_sq = nullptr, const NextNorm *nx = nullptr, bool *staged = nullptr) {
     if (parts) *parts = 1;
     const size_t groups = (rows + CTOX_MV_ROWS - 1) / CTOX_MV_ROWS;
     const size_t tgroups = (batch + 3) / 4;
@@ -468,7 +500,8 @@ ctox_status run_matvec(ctox_hip_backend *b, int layout, int32_t dtype, const voi
             return batch == 1 ? run_tile_matvec(b, dtype, it->second, rows, columns, d_s_out, s_out_kind, d_bias,
                                                 d_output, act, s)
                               : run_tile_matvec_m(b, dtype, it->second, rows, columns, batch, d_s_out, s_out_kind,
-                                                  d_bias, d_output, out_stride, act, s, res_h, res_sq);
+                                                  d_bias, d_output, out_stride, act, s, res_h, res_sq, false, nx,
+                                                  staged);
     }
     // Batch 1 on rows of whole 16-byte units: the slice kernels (all slices
     // requested up front when there are at most three, else walked).
@@ -596,7 +629,8 @@ ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy 
 ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCopy &t, size_t rows, size_t columns,
                               size_t batch, const void *d_s_out, uint32_t s_out_kind, const float *d_bias,
                               float *d_output, size_t out_stride, uint32_t act, hipStream_t s, const float *res_h,
-                              float *res_sq, bool parts_out) {
+                              float *res_sq, bool parts_out, const NextNorm *nx, bool *staged, const StagedIn *in) {
+    if (staged) *staged = false;
     const int q4 = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
     const uint32_t u = 1;
     const uint32_t segs = (((t.tiles + u - 1) / u) + 3) & ~3u;
@@ -618,8 +652,31 @@ ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCop
     TileMatvecArgs a{};
     a.arrive = arrive ? (uint32_t *)b->tarrive.ptr : nullptr;
     a.weights = (const uint8_t *)t.d;
-    a.xa = (const int8_t *)b->xa[q4].ptr;
-    a.xc = (const float *)b->xc[q4].ptr;
+    a.xa = in && in->xa ? in->xa : (const int8_t *)b->xa[q4].ptr;
+    a.xc = in && in->xc ? in->xc : (const float *)b->xc[q4].ptr;
+    if (in && in->rms_sq) {
+        a.rms_sq = in->rms_sq;
+        a.rms_n = in->rms_n;
+        a.eps = in->eps;
+    }
+    // Next-norm staging: the last chunk's workgroups hold whole 64-row blocks
+    // (one tile per wave, four waves, rows a multiple of 64).
+    if (nx && res_h && res_sq && !arrive && !parts_out && rows % kBlockLen == 0 && batch <= 8 &&
+        segs == t.tiles) {
+        const int nl = nx->dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
+        const size_t nblk = rows / kBlockLen;
+        ctox_status st = ensure(b, b->xn[nl], nblk * batch * 192, false);
+        if (!st) st = ensure(b, b->xnc[nl], nblk * batch * 4 * sizeof(float), false);
+        if (st) return st;
+        a.nx_xa = (int8_t *)b->xn[nl].ptr;
+        a.nx_xc = (float *)b->xnc[nl].ptr;
+        a.nx_h = nx->h_out;
+        a.nx_w = nx->w;
+        a.nx_s_in = nx->s_in;
+        a.nx_sq = nx->sq_out;
+        a.nx_dtype = (uint32_t)nl;
+        if (staged) *staged = true;
+    }
     a.s_out = d_s_out;
     a.bias = d_bias;
     a.output = d_output;
@@ -648,13 +705,13 @@ ctox_status run_tile_matvec_mx(ctox_hip_backend *b, int32_t dtype, const TiledCo
                                float *d_output, size_t out_stride, uint32_t act, hipStream_t s, const float *d_input,
                                const void *d_s_in, uint32_t s_in_kind, const TileXform &xf, const PartialSlots *ps) {
     const int q4 = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
-    const uint32_t u = 1;
-    const uint32_t segs = (((t.tiles + u - 1) / u) + 3) & ~3u;
+    const uint32_t u = 1, W = b->mx_waves;
+    const uint32_t segs = (((t.tiles + u - 1) / u) + W - 1) / W * W;
     const size_t waves = (size_t)segs * t.chunks;
     if (batch < 2 || batch > kMaxBuildRows) return fail(CTOX_ERR_SHAPE, "in-kernel row build takes 2..5 rows");
-    if (waves / 4 > 0x7fffffffu || out_stride > 0xffffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
-    const bool arrive =
-        t.chunks > 1 && (b->arrive >= 0 ? b->arrive != 0 : waves / 4 > b->tilemx_cap[q4][batch - 2]);
+    if (waves / W > 0x7fffffffu || out_stride > 0xffffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
+    const uint32_t cap = W == 16 ? b->tilemxw_cap[q4][batch - 2] : b->tilemx_cap[q4][batch - 2];
+    const bool arrive = t.chunks > 1 && (b->arrive >= 0 ? b->arrive != 0 : waves / W > cap);
     const size_t slot_bytes =
         (size_t)(arrive ? t.chunks : t.chunks - 1) * batch * t.tiles * CTOX_TILE_ROWS * sizeof(uint64_t);
     if (ps && t.chunks > 1 && (slot_bytes > ps->bytes || (arrive && t.tiles > ps->arrive_n)))
@@ -701,8 +758,9 @@ ctox_status run_tile_matvec_mx(ctox_hip_backend *b, int32_t dtype, const TiledCo
     a.out_stride = (uint32_t)out_stride;
     a.a_stride = xf.a_stride;
     a.b_stride = xf.b_stride;
-    return launch(arrive ? b->tilemx_arr[q4][batch - 2] : b->tilemx[q4][batch - 2], dim3((unsigned)(waves / 4)), dim3(256), s, a,
-                  "ctox_q*_mv_tilemx*_gfx950");
+    hipFunction_t f = W == 16 ? (arrive ? b->tilemxw_arr[q4][batch - 2] : b->tilemxw[q4][batch - 2])
+                              : (arrive ? b->tilemx_arr[q4][batch - 2] : b->tilemx[q4][batch - 2]);
+    return launch(f, dim3((unsigned)(waves / W)), dim3(64 * W), s, a, "ctox_q*_mv_tilemx*_gfx950");
 }
 
 // The registered tiled copy of raw weights, or NULL.
@@ -869,6 +927,14 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->tilemx_arr[0][2], "ctox_q2_mv_tilemx4_gfx950_arrive"}, {&b->tilemx_arr[0][3], "ctox_q2_mv_tilemx5_gfx950_arrive"},
                {&b->tilemx_arr[1][0], "ctox_q4_mv_tilemx2_gfx950_arrive"}, {&b->tilemx_arr[1][1], "ctox_q4_mv_tilemx3_gfx950_arrive"},
                {&b->tilemx_arr[1][2], "ctox_q4_mv_tilemx4_gfx950_arrive"}, {&b->tilemx_arr[1][3], "ctox_q4_mv_tilemx5_gfx950_arrive"},
+               {&b->tilemxw[0][0], "ctox_q2_mv_tilemxw2_gfx950"}, {&b->tilemxw[0][1], "ctox_q2_mv_tilemxw3_gfx950"},
+               {&b->tilemxw[0][2], "ctox_q2_mv_tilemxw4_gfx950"}, {&b->tilemxw[0][3], "ctox_q2_mv_tilemxw5_gfx950"},
+               {&b->tilemxw[1][0], "ctox_q4_mv_tilemxw2_gfx950"}, {&b->tilemxw[1][1], "ctox_q4_mv_tilemxw3_gfx950"},
+               {&b->tilemxw[1][2], "ctox_q4_mv_tilemxw4_gfx950"}, {&b->tilemxw[1][3], "ctox_q4_mv_tilemxw5_gfx950"},
+               {&b->tilemxw_arr[0][0], "ctox_q2_mv_tilemxw2_gfx950_arrive"}, {&b->tilemxw_arr[0][1], "ctox_q2_mv_tilemxw3_gfx950_arrive"},
+               {&b->tilemxw_arr[0][2], "ctox_q2_mv_tilemxw4_gfx950_arrive"}, {&b->tilemxw_arr[0][3], "ctox_q2_mv_tilemxw5_gfx950_arrive"},
+               {&b->tilemxw_arr[1][0], "ctox_q4_mv_tilemxw2_gfx950_arrive"}, {&b->tilemxw_arr[1][1], "ctox_q4_mv_tilemxw3_gfx950_arrive"},
+               {&b->tilemxw_arr[1][2], "ctox_q4_mv_tilemxw4_gfx950_arrive"}, {&b->tilemxw_arr[1][3], "ctox_q4_mv_tilemxw5_gfx950_arrive"},
                {&b->repack, "ctox_tile_repack_gfx950"}, {&b->gdn_fused, "ctox_gdn_fused_gfx950"}, {&b->gdn_fused_blk, "ctox_gdn_fused_blk_gfx950"},
                {&b->finite, "ctox_finite_check_gfx950"}, {&b->gather, "ctox_gather_rows_gfx950"}, {&b->stream_read, "ctox_stream_read_gfx950"},
                {&b->topk_part, "ctox_topk_part_gfx950"}, {&b->topk_final, "ctox_topk_final_gfx950"}};
@@ -903,13 +969,15 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
     // separate launch (the tilem kernels) instead of building them in-kernel.
     if (const char *m = std::getenv("CTOX_SMALL_M_BUILD")) b->no_mx = std::atoi(m) == 0;
     if (const char *m = std::getenv("CTOX_ARRIVE")) b->arrive = std::atoi(m) != 0;
+    if (const char *m = std::getenv("CTOX_MX_W")) b->mx_waves = std::atoi(m) == 16 ? 16u : 4u;
+    if (const char *m = std::getenv("CTOX_MX_MAX")) b->mx_max = (uint64_t)std::atoll(m) << 20;
     // How many workgroups of each tiled kernel the device holds at once:
     // launches within it may combine by the last chunk's waves (every
     // producer is resident whatever the dispatch order); larger ones combine
     // by arrival.
-    auto cap = [&](hipFunction_t f) {
+    auto cap = [&](hipFunction_t f, int threads = 256) {
         int n = 0;
-        if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, 256, 0) != hipSuccess) n = 0;
+        if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, threads, 0) != hipSuccess) n = 0;
         return (uint32_t)std::max(0, n) * (uint32_t)b->cus;
     };
     for (int q = 0; q < 2; q++) {
@@ -918,7 +986,10 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
             b->tile_cap[1][q][u] = cap(b->tilex[q][u]);
         }
         for (int m = 0; m < 7; m++) b->tilem_cap[q][m] = cap(b->tilem[q][m]);
-        for (int r = 0; r < 4; r++) b->tilemx_cap[q][r] = cap(b->tilemx[q][r]);
+        for (int r = 0; r < 4; r++) {
+            b->tilemx_cap[q][r] = cap(b->tilemx[q][r]);
+            b->tilemxw_cap[q][r] = cap(b->tilemxw[q][r], 1024);
+        }
     }
     if (const char *u = std::getenv("CTOX_TILE_U")) {
         const int v = std::atoi(u);
@@ -932,8 +1003,8 @@ extern "C" void ctox_hip_backend_destroy(ctox_hip_backend *b) {
     if (!b) return;
     (void)hipSetDevice(b->device);
     (void)hipDeviceSynchronize();
-    DevBuf *bufs[] = {&b->xa[0], &b->xa[1], &b->xc[0], &b->xc[1], &b->norms, &b->tok, &b->stats, &b->attn,
-                      &b->tpart, &b->tarrive};
+    DevBuf *bufs[] = {&b->xa[0], &b->xa[1], &b->xc[0], &b->xc[1], &b->xn[0], &b->xn[1], &b->xnc[0], &b->xnc[1],
+                      &b->norms, &b->tok, &b->stats, &b->attn, &b->tpart, &b->tarrive};
     for (auto &kv : b->raw_tiled)
         if (kv.second.d) (void)hipFree(kv.second.d);
     for (DevBuf *d : bufs)
@@ -1330,12 +1401,13 @@ extern "C" ctox_status ctox_hip_norm_matvec_parts_device(ctox_hip_backend *b, co
                       d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, nullptr, d_output, rows, 0, s);
 }
 
-extern "C" ctox_status ctox_hip_transform_matvec_device(ctox_hip_backend *b, const ctox_input_transform *x,
-                                                       int32_t dtype, const void *d_weights, const uint16_t *d_s_in,
-                                                       const uint16_t *d_s_out, float *d_output, uint32_t rows,
-                                                       uint32_t columns, uint32_t batch, uint32_t split_k,
-                                                       uint32_t *parts, void *stream) {
+namespace {
+ctox_status transform_matvec_impl(ctox_hip_backend *b, const ctox_input_transform *x, int32_t dtype,
+                                  const void *d_weights, const uint16_t *d_s_in, const uint16_t *d_s_out,
+                                  float *d_output, uint32_t rows, uint32_t columns, uint32_t batch, uint32_t split_k,
+                                  uint32_t *parts, void *stream, const NextNorm *nx, bool *staged) {
     if (parts) *parts = 1;
+    if (staged) *staged = false;
     if (!b || !x || !x->a || !d_weights || !d_output || ((x->mode == 2 || x->mode == 3) && !x->b) ||
         (x->mode == 2 && !x->w) || (x->res_sums && !x->res_h))
         return fail(CTOX_ERR_SHAPE, "null argument");
@@ -1423,7 +1495,66 @@ extern "C" ctox_status ctox_hip_transform_matvec_device(ctox_hip_backend *b, con
     if ((st = launch(b->prep_x, dim3((unsigned)blocks, batch), dim3(64), s, a, "ctox_prep_transform_gfx950"))) return st;
     return run_matvec(b, layout, dtype, d_weights, rows, columns, batch, d_s_out,
                       d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, nullptr, d_output, rows, 0, s, split_k != 0, parts,
-                      x->res_h, x->res_sums);
+                      x->res_h, x->res_sums, nx, staged);
+}
+}  // namespace
+
+extern "C" ctox_status ctox_hip_transform_matvec_device(ctox_hip_backend *b, const ctox_input_transform *x,
+                                                       int32_t dtype, const void *d_weights, const uint16_t *d_s_in,
+                                                       const uint16_t *d_s_out, float *d_output, uint32_t rows,
+                                                       uint32_t columns, uint32_t batch, uint32_t split_k,
+                                                       uint32_t *parts, void *stream) {
+    return transform_matvec_impl(b, x, dtype, d_weights, d_s_in, d_s_out, d_output, rows, columns, batch, split_k,
+                                 parts, stream, nullptr, nullptr);
+}
+
+ctox_status ctox_delta_matvec_stage_next(ctox_hip_backend *b, const ctox_input_transform *x, int32_t dtype,
+                                         const void *d_weights, const uint16_t *d_s_in, const uint16_t *d_s_out,
+                                         float *d_output, uint32_t rows, uint32_t columns, uint32_t batch,
+                                         const float *next_norm_w, const uint16_t *next_s_in, int32_t next_dtype,
+                                         float *next_h_out, float *next_sq_out, bool *staged, void *stream) {
+    if (staged) *staged = false;
+    if (!next_norm_w || !next_h_out || !next_sq_out || !staged || !x || !x->res_h || !x->res_sums)
+        return fail(CTOX_ERR_SHAPE, "next-norm staging: null argument");
+    if (next_dtype != CTOX_DTYPE_Q2B64 && next_dtype != CTOX_DTYPE_Q4B64)
+        return fail(CTOX_ERR_UNSUPPORTED_DTYPE, "next-norm staging takes a pure Q2_B64 or Q4_B64 matrix");
+    NextNorm nx;
+    nx.w = next_norm_w;
+    nx.s_in = next_s_in;
+    nx.dtype = next_dtype;
+    nx.h_out = next_h_out;
+    nx.sq_out = next_sq_out;
+    return transform_matvec_impl(b, x, dtype, d_weights, d_s_in, d_s_out, d_output, rows, columns, batch, 0, nullptr,
+                                 stream, batch >= 2 && batch <= 8 ? &nx : nullptr, staged);
+}
+
+ctox_status ctox_norm_matvec_prestaged(ctox_hip_backend *b, int32_t dtype, const void *d_weights,
+                                       const uint16_t *d_s_out, float *d_output, uint32_t rows, uint32_t columns,
+                                       uint32_t batch, const float *sq, float eps, uint32_t max_parts, uint32_t *parts,
+                                       void *stream) {
+    if (parts) *parts = 1;
+    if (!b || !d_weights || !d_output || !sq) return fail(CTOX_ERR_SHAPE, "null argument");
+    if (batch < 2 || batch > 8 || columns % kBlockLen || columns / kBlockLen > 128)
+        return fail(CTOX_ERR_SHAPE, "prestaged norm-matvec: 2..8 rows, at most 8192 columns");
+    const TiledCopy *t = registered(b, d_weights, rows, columns);
+    if (!t) return fail(CTOX_ERR_UNSUPPORTED_OPERATION, "prestaged norm-matvec needs registered weights");
+    const int nl = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
+    if (b->xn[nl].bytes < columns / kBlockLen * batch * 192)
+        return fail(CTOX_ERR_INVALID_STATE, "no next-norm staging of this size");
+    hipStream_t s = pick_stream(b, stream);
+    StagedIn in;
+    in.xa = (const int8_t *)b->xn[nl].ptr;
+    in.xc = (const float *)b->xnc[nl].ptr;
+    in.rms_sq = sq;
+    in.rms_n = (uint32_t)(columns / kBlockLen);
+    in.eps = eps;
+    bool parts_out = false;
+    if (parts && max_parts > 1 && t->chunks > 1 && t->chunks <= max_parts) {
+        parts_out = true;
+        *parts = t->chunks;
+    }
+    return run_tile_matvec_m(b, dtype, *t, rows, columns, batch, d_s_out, d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE,
+                             nullptr, d_output, rows, 0, s, nullptr, nullptr, parts_out, nullptr, nullptr, &in);
 }
 
 extern "C" ctox_status ctox_hip_fused_matvec(ctox_hip_backend *b, const ctox_fused_matvec *op, float *output,

@@ -33,9 +33,11 @@
 #include <cstring>
 #include <string>
 #include <unordered_map>
+#include <cstdlib>
 #include <vector>
 
 #include "ctox_hip.h"
+#include "shim_internal.h"
 
 void ctox_set_last_error(const char *msg);  // ctox_hip.cpp
 
@@ -146,6 +148,17 @@ struct ctox_hip_engine {
     // sum of squares); valid until that norm consumes them.
     float *rsq = nullptr;
     const float *rsq_delta = nullptr, *rsq_hid = nullptr;
+    // Next-norm staging on the small-M verify path: a residual producer
+    // (delta_mv) told which norm-matvec follows it (nx_w, nx_m) stages that
+    // projection's input itself; pre_* records the staging until the
+    // matching norm_mv consumes it. blk_sq: its per-64-column sums of h^2.
+    const float *nx_w = nullptr;
+    const struct Mat *nx_m = nullptr;
+    const float *pre_w = nullptr, *pre_delta = nullptr;
+    const struct Mat *pre_m = nullptr;
+    uint32_t pre_rows = 0;
+    float *blk_sq = nullptr;
+    bool next_norm = true;  // CTOX_NEXT_NORM=0 turns the next-norm staging off
     // Matrix dtypes by engine name (ctox_hip_engine_create_with_dtypes); the
     // default plan is Q4 projections and Q2 down projections.
     std::unordered_map<std::string, int32_t> dtype_plan;
@@ -235,6 +248,18 @@ constexpr uint32_t kSumRows = 5;
 // sum goes to the other buffer, which becomes the stream.
 ctox_status norm_mv(ctox_hip_engine *e, const float *delta, const float *w, uint32_t rows, const Mat &m, float *out,
                     float *norm_out = nullptr, uint32_t max_parts = 1, uint32_t *parts = nullptr) {
+    const bool pre = e->pre_m == &m && e->pre_w == w && e->pre_delta == delta && delta && e->pre_rows == rows &&
+                     !norm_out && e->rsq_hid == e->hid;
+    e->pre_m = nullptr;
+    if (pre) {
+        // The producer already wrote hid + delta to hid2 and staged the
+        // normed rows; this launch applies each row's 1 / rms.
+        e->rsq_delta = e->rsq_hid = nullptr;
+        TRY(ctox_norm_matvec_prestaged(e->b, m.dtype, m.w, m.s_out, out, m.rows, m.cols, rows, e->blk_sq,
+                                       e->c.rms_norm_epsilon, max_parts, parts, e->s));
+        std::swap(e->hid, e->hid2);
+        return CTOX_OK;
+    }
     const bool sums = delta && rows <= kSumRows && e->rsq_delta == delta && e->rsq_hid == e->hid && e->delta_parts == 1;
     e->rsq_delta = e->rsq_hid = nullptr;
     TRY(ctox_hip_norm_matvec_parts_device(e->b, e->hid, delta, e->delta_parts, (size_t)rows * e->H, delta ? e->hid2 : nullptr,
@@ -247,13 +272,31 @@ ctox_status norm_mv(ctox_hip_engine *e, const float *delta, const float *w, uint
 // A single-row producer of residual delta `out` also leaves the next norm's
 // per-tile sums of squares (ctox_input_transform::res_sums).
 ctox_status delta_mv(ctox_hip_engine *e, ctox_input_transform &x, const Mat &m, float *out, uint32_t R) {
+    const float *nx_w = e->nx_w;
+    const Mat *nx_m = e->nx_m;
+    e->nx_w = nullptr;
+    e->nx_m = nullptr;
+    e->pre_m = nullptr;
     if (R <= kSumRows) {
         x.res_h = e->hid;
         x.res_sums = e->rsq;
     }
     e->rsq_delta = e->rsq_hid = nullptr;
-    TRY(ctox_hip_transform_matvec_device(e->b, &x, m.dtype, m.w, m.s_in, m.s_out, out, m.rows, m.cols, R, 1,
-                                         &e->delta_parts, e->s));
+    bool staged = false;
+    if (nx_m && R >= 2 && R <= kSumRows && e->next_norm) {
+        TRY(ctox_delta_matvec_stage_next(e->b, &x, m.dtype, m.w, m.s_in, m.s_out, out, m.rows, m.cols, R, nx_w,
+                                         nx_m->s_in, nx_m->dtype, e->hid2, e->blk_sq, &staged, e->s));
+        e->delta_parts = 1;
+        if (staged) {
+            e->pre_w = nx_w;
+            e->pre_m = nx_m;
+            e->pre_delta = out;
+            e->pre_rows = R;
+        }
+    } else {
+        TRY(ctox_hip_transform_matvec_device(e->b, &x, m.dtype, m.w, m.s_in, m.s_out, out, m.rows, m.cols, R, 1,
+                                             &e->delta_parts, e->s));
+    }
     if (R <= kSumRows) {
         e->rsq_delta = out;
         e->rsq_hid = e->hid;
@@ -472,11 +515,16 @@ ctox_status gdn_forward(ctox_hip_engine *e, GdnLayer &g, uint32_t R, float *delt
     return delta_mv(e, x, g.out, delta, R);
 }
 
-ctox_status mlp_forward(ctox_hip_engine *e, Mlp &m, uint32_t R, const float *delta_in, float *delta_out) {
+// nx_w / nx_m: the norm-matvec that follows the MLP (the next layer's
+// in-projection), whose input down may stage.
+ctox_status mlp_forward(ctox_hip_engine *e, Mlp &m, uint32_t R, const float *delta_in, float *delta_out,
+                        const float *nx_w = nullptr, const Mat *nx_m = nullptr) {
     // gate|up leaves its chunk partials and down's SwiGLU build or staging adds them.
     uint32_t parts = 1;
     TRY(norm_mv(e, delta_in, m.norm, R, m.gate_up, e->gu, nullptr, 6, &parts));
     ctox_input_transform x{e->gu, nullptr, nullptr, 1, 2 * e->I, 0, e->I, 0, 0.0f, nullptr, nullptr, parts, R * 2 * e->I};
+    e->nx_w = nx_w;
+    e->nx_m = nx_m;
     return delta_mv(e, x, m.down, delta_out, R);
 }
 
@@ -489,16 +537,29 @@ ctox_status target_forward(ctox_hip_engine *e, const uint32_t *d_tok, uint32_t R
     TRY(ctox_hip_embedding_rows_device(e->b, e->embed.dtype, e->embed.w, e->embed.s_in, e->embed.s_out, d_tok, R, e->V,
                                        e->H, e->hid, e->s));
     bool pending = false;
-    for (Layer &L : e->layers) {
+    for (size_t li = 0; li < e->layers.size(); li++) {
+        Layer &L = e->layers[li];
         const float *dl = pending ? e->delta : nullptr;
+        // The token mixer's output projection stages the MLP's normed input.
         if (L.full) {
             TRY(norm_mv(e, dl, L.f.norm, R, L.f.qkv, e->proj));
+            e->nx_w = L.mlp.norm;
+            e->nx_m = &L.mlp.gate_up;
             TRY(attn_forward(e, L.f, R, e->position, e->delta, retain));
         } else {
             TRY(norm_mv(e, dl, L.g.norm, R, L.g.in, e->proj));
+            e->nx_w = L.mlp.norm;
+            e->nx_m = &L.mlp.gate_up;
             TRY(gdn_forward(e, L.g, R, e->delta));
         }
-        TRY(mlp_forward(e, L.mlp, R, e->delta, e->delta));
+        const float *nw = nullptr;
+        const Mat *nm = nullptr;
+        if (li + 1 < e->layers.size()) {
+            const Layer &N = e->layers[li + 1];
+            nw = N.full ? N.f.norm : N.g.norm;
+            nm = N.full ? &N.f.qkv : &N.g.in;
+        }
+        TRY(mlp_forward(e, L.mlp, R, e->delta, e->delta, nw, nm));
         pending = true;
     }
     return norm_mv(e, e->delta, e->final_norm, R, e->lm_head, e->logits, e->fin);
@@ -603,6 +664,7 @@ extern "C" ctox_status ctox_hip_engine_create_with_dtypes(ctox_hip_backend *b, c
     e->b = b;
     e->c = c;
     for (size_t i = 0; i < plan_len; i++) e->dtype_plan[plan[i].name] = plan[i].dtype;
+    if (const char *v = std::getenv("CTOX_NEXT_NORM")) e->next_norm = std::atoi(v) != 0;
     e->mtp = c.mtp_layers > 0 && c.draft_tokens > 0;
     e->R = e->mtp ? c.draft_tokens + 1 : 1;
     e->H = c.hidden_size;
@@ -689,7 +751,7 @@ extern "C" ctox_status ctox_hip_engine_create_with_dtypes(ctox_hip_backend *b, c
         (st = dalloc_t(e, &e->mtp_hidden, R * e->H)) || (st = dalloc_t(e, &e->prev_hidden, R * e->H)) ||
         (st = dalloc_t(e, &e->target_hidden, (R + 1) * e->H)) || (st = dalloc_t(e, &e->d_tokens, 16)) ||
         (st = dalloc_t(e, &e->d_drafts, 16)) || (st = dalloc_t(e, &e->d_result, 16)) || (st = dalloc_t(e, &e->d_rng, 1)) ||
-        (st = dalloc_t(e, &e->rsq, 8 * 512)) || (st = dalloc_t(e, &e->d_flags, 64)))
+        (st = dalloc_t(e, &e->rsq, 8 * 512)) || (st = dalloc_t(e, &e->blk_sq, 8 * 128)) || (st = dalloc_t(e, &e->d_flags, 64)))
         return cleanup(st);
     if (hipHostMalloc((void **)&e->h_flags, 64 * sizeof(uint32_t), hipHostMallocDefault) != hipSuccess) {
         e->h_flags = nullptr;

@@ -1,0 +1,28 @@
+// Library-internal entry points shared by the shim (ctox_hip.cpp) and the
+// decode engine (engine.cpp); not part of the C ABI in include/ctox_hip.h.
+#pragma once
+
+#include "ctox_hip.h"
+
+// A residual-delta projection of 2..8 rows (the transform-matvec, on the
+// staged small-M path) that also stages the input of the (1 + w) RMS-normed
+// projection that follows it: h = x->res_h + output goes to next_h_out,
+// h * (1 + next_norm_w) * next_s_in is staged in the backend's next-norm
+// buffers for a matrix of next_dtype, and next_sq_out [batch][rows / 64]
+// receives per-64-row sums of h^2. *staged reports whether the staging was
+// made (otherwise the call is the plain transform-matvec and the caller
+// stages the norm itself).
+ctox_status ctox_delta_matvec_stage_next(ctox_hip_backend *b, const ctox_input_transform *x, int32_t dtype,
+                                         const void *d_weights, const uint16_t *d_s_in, const uint16_t *d_s_out,
+                                         float *d_output, uint32_t rows, uint32_t columns, uint32_t batch,
+                                         const float *next_norm_w, const uint16_t *next_s_in, int32_t next_dtype,
+                                         float *next_h_out, float *next_sq_out, bool *staged, void *stream);
+
+// The projection of what ctox_delta_matvec_stage_next staged: registered
+// weights of next_dtype, the same batch, `sq` its per-block sums of h^2 and
+// eps the norm's epsilon. max_parts / parts as for
+// ctox_hip_norm_matvec_parts_device.
+ctox_status ctox_norm_matvec_prestaged(ctox_hip_backend *b, int32_t dtype, const void *d_weights,
+                                       const uint16_t *d_s_out, float *d_output, uint32_t rows, uint32_t columns,
+                                       uint32_t batch, const float *sq, float eps, uint32_t max_parts, uint32_t *parts,
+                                       void *stream);

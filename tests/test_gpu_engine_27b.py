@@ -118,3 +118,34 @@ def test_engine_27b_full_depth_commit_equals_plain_decode(hip):
     finally:
         spec.close()
         plain.close()
+
+
+@pytest.mark.timeout(900)
+def test_engine_27b_next_norm_staging_matches_separate_staging(hip, monkeypatch):
+    """The speculative verify pass with each residual producer (o_proj,
+    out_proj, down at 5 rows) staging the next (1 + w) RMS-normed projection
+    itself, 1 / rms applied by the consumer, against the same engine with the
+    norm staged by its own launch (CTOX_NEXT_NORM=0): the 5 verify logit rows
+    of two speculative steps agree within the plain-step tolerance, and so do
+    the accepted drafts and next tokens."""
+    from ctox_hip.engine import Engine
+    cfg = config27(4, 1024 + 64)
+    engines = []
+    try:
+        for flag in ("0", "1"):
+            monkeypatch.setenv("CTOX_NEXT_NORM", flag)
+            say(f"case engine27 next-norm staging={flag}: create")
+            e = Engine(hip, cfg, seed=33)
+            e.fill_context(1024, seed=4)
+            e.set_rng(777)
+            engines.append(e)
+        token = 321
+        for step in range(2):
+            say(f"case engine27 next-norm mtp step={step} token={token}")
+            got = [e.mtp_step(token, 0.7) for e in engines]
+            close(engines[1].logits(5), engines[0].logits(5))
+            assert got[0] == got[1], (step, got)
+            token = got[0][0]
+    finally:
+        for e in engines:
+            e.close()
