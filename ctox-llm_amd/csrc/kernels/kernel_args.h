@@ -12,9 +12,15 @@
 #define CTOX_MV_WAVES 4
 #define CTOX_MV_ROWS 16
 #define CTOX_MAX_BATCH 8
-// Activation fixed-point: |X| <= 2^22 per 64-column block, three signed
-// 8-bit limbs (X = X0 + 2^8 X1 + 2^16 X2).
+// Activation fixed-point: |X| <= 2^F per 64-column block, three signed
+// 8-bit limbs (X = X0 + 2^8 X1 + 2^16 X2). F = 22, except for Q4 weights in
+// the staged fragments (xa / xc, written by the prep kernels), where F = 21.
+// With codes c <= 3 (Q2, F = 22) or c <= 15 (Q4, F = 21) a block's sum of
+// c * X is below 2^30 or 64 * 15 * 2^21 < 2^31: the limb sums C0 + 2^8 C1 +
+// 2^16 C2 combine exactly in int32 and take one conversion. Fragments built
+// inside the matvec keep F = 22 for Q4 and combine the limbs in float.
 #define CTOX_XFRAC_BITS 22
+#define ctox_staged_xfrac_bits(dtype) ((dtype) ? 21 : 22)
 
 // Scale pointer kinds inside kernels.
 #define CTOX_KSCALE_NONE 0

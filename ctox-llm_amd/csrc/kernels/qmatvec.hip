@@ -110,8 +110,8 @@ __device__ __forceinline__ void stage_block(float x, int8_t *frag, float4 *xc, u
     } else if (m > 0.0f) {
         int ex;
         frexpf(m, &ex);
-        X = (int)rintf(ldexpf(x, CTOX_XFRAC_BITS - ex));
-        q = ldexpf(1.0f, ex - CTOX_XFRAC_BITS);
+        X = (int)rintf(ldexpf(x, ctox_staged_xfrac_bits(dtype) - ex));
+        q = ldexpf(1.0f, ex - ctox_staged_xfrac_bits(dtype));
     }
     // Balanced signed limbs: X = X0 + 256*X1 + 65536*X2, X0, X1 in [-128,127].
     const int x0 = (int)(int8_t)(X & 0xff);

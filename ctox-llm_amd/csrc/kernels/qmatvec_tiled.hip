@@ -489,14 +489,15 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
             }
             const uint32_t sw = u[k].s[G >> 1];
             const float scale = half_bits_to_float((G & 1) ? (sw >> 16) : (sw & 0xffffu));
+            // sum(c X) = C0 + 256 C1 + 65536 C2 is exact in int32 for Q2 and
+            // for staged Q4 fragments (21 fraction bits): one conversion.
+            // Q4 fragments built here (22 bits) combine the limbs in float.
             float f;
-            if (DT) {
+            if (DT && AB) {
                 f = fmaf((float)cc[0], kg.x, kg.w);
                 f = fmaf((float)cc[1], kg.y, f);
                 f = fmaf((float)cc[2], kg.z, f);
             } else {
-                // Q2: sum(c X) = C0 + 256 C1 + 65536 C2 is exact in int32
-                // (|sum| <= 64 * 3 * 2^22 < 2^30): one conversion.
                 f = fmaf((float)(cc[0] + (cc[1] << 8) + (cc[2] << 16)), kg.x, kg.w);
             }
             part[k] = fmaf(f, scale, part[k]);
@@ -883,14 +884,8 @@ __device__ __forceinline__ void tile_matvec_m(const TileMatvecArgs &a) {
                                                             : CTOX_TILE_BLOCKS * MAXM * 192));
                     const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf, (v4i){0, 0, 0, 0}, 0, 0, 0);
                     const float4 kq = kqs[(4 * G + b) * M + min(4 * tg + g, M - 1)];
-                    float f;
-                    if (DT) {
-                        f = fmaf((float)cc[0], kq.x, kq.w);
-                        f = fmaf((float)cc[1], kq.y, f);
-                        f = fmaf((float)cc[2], kq.z, f);
-                    } else {
-                        f = fmaf((float)(cc[0] + (cc[1] << 8) + (cc[2] << 16)), kq.x, kq.w);
-                    }
+                    // Staged fragments: exact int32 limb sum for Q2 and Q4.
+                    const float f = fmaf((float)(cc[0] + (cc[1] << 8) + (cc[2] << 16)), kq.x, kq.w);
                     acc[k][tg] = fmaf(f, scale, acc[k][tg]);
                 }
             }
@@ -1093,6 +1088,7 @@ __device__ __forceinline__ void tile_matvec_mx(const TileMatvecArgs &a) {
                     const v4i af = *(const v4i *)(abase[tg] + (4 * G + b) * M * 192);
                     const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf, (v4i){0, 0, 0, 0}, 0, 0, 0);
                     const float4 kq = kbase[tg][(4 * G + b) * M];
+                    // Fragments built here: Q4 limbs combine in float (22 bits).
                     float f;
                     if (DT) {
                         f = fmaf((float)cc[0], kq.x, kq.w);
