@@ -350,6 +350,7 @@ def bench_decode_27b(torch, hip, steps, context=32768):
             nxt, acc = eng.mtp_step(tok, 0.7)
             tokens += 1 + len(acc)
             tok = nxt
+        torch.cuda.synchronize()  # the last step's commit may still be queued
         mtp = time.time() - t0
         res[f"mtp_k4_T0.7{tag}_ms_per_step"] = mtp / n_mtp * 1e3
         res[f"mtp{tag}_tokens_per_s"] = tokens / mtp

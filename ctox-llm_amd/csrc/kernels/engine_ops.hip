@@ -194,6 +194,15 @@ extern "C" __global__ __launch_bounds__(64) void ctox_write_words_gfx950(WordsAr
     if (threadIdx.x < a.count) a.dst[threadIdx.x] = a.words[threadIdx.x];
 }
 
+// grid (1), 512 threads: word i of the argument block goes to its segment.
+extern "C" __global__ __launch_bounds__(512) void ctox_write_segments_gfx950(SegWordsArgs a) {
+    const uint32_t i = threadIdx.x;
+    if (i >= a.off[a.nseg]) return;
+    uint32_t sgm = 0;
+    for (uint32_t k = 1; k < a.nseg; k++) sgm += i >= a.off[k];
+    a.dst[sgm][i - a.off[sgm]] = a.words[i];
+}
+
 // grid (parts), 256 threads: part p checks its contiguous range of float4
 // (the tail floats by the last part) and always writes flags[p].
 extern "C" __global__ __launch_bounds__(256) void ctox_finite_check_gfx950(FiniteArgs a) {

@@ -607,6 +607,18 @@ struct GatherRowsArgs {      // ctox_gather_rows_gfx950: dst row r = src row ids
     uint32_t pad;
 };
 
+// Several small host-to-device writes in one launch (the engine's descriptor
+// uploads after a step): segment i writes words[off[i] .. off[i + 1]) to dst[i].
+#define CTOX_SEG_MAX 24
+#define CTOX_SEG_WORDS 512
+struct SegWordsArgs {
+    uint32_t *dst[CTOX_SEG_MAX];
+    uint32_t off[CTOX_SEG_MAX + 1];
+    uint32_t nseg;
+    uint32_t pad;
+    uint32_t words[CTOX_SEG_WORDS];
+};
+
 struct WordsArgs {           // small host-to-device writes carried in the kernel arguments
     uint32_t *dst;
     uint32_t count;          // <= 32

@@ -151,7 +151,8 @@ struct ctox_hip_backend {
                   conv = nullptr, rope = nullptr, kv_pack = nullptr, attn_prep = nullptr, kv_demote = nullptr, gqa_part[2] = {}, gqa_part16[2] = {},
                   gqa_combine = nullptr, fill = nullptr, embed = nullptr, norm_rows = nullptr, attn_gate = nullptr,
                   swiglu_rows = nullptr, copy_rows = nullptr, write_words = nullptr, norm_prep = nullptr,
-                  prep_x = nullptr, finite = nullptr, gather = nullptr, topk_part = nullptr, topk_final = nullptr, stream_read = nullptr;
+                  prep_x = nullptr, finite = nullptr, gather = nullptr, topk_part = nullptr, topk_final = nullptr, stream_read = nullptr,
+                  write_segments = nullptr;
     // Batch-1 slice kernels per dtype [Q2, Q4]: [0] walks the slices, [n]
     // requests all n slices up front (n <= 3: more slices up front measured
     // slower than walking them).
@@ -937,6 +938,7 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->tilemxw_arr[1][2], "ctox_q4_mv_tilemxw4_gfx950_arrive"}, {&b->tilemxw_arr[1][3], "ctox_q4_mv_tilemxw5_gfx950_arrive"},
                {&b->repack, "ctox_tile_repack_gfx950"}, {&b->gdn_fused, "ctox_gdn_fused_gfx950"}, {&b->gdn_fused_blk, "ctox_gdn_fused_blk_gfx950"},
                {&b->finite, "ctox_finite_check_gfx950"}, {&b->gather, "ctox_gather_rows_gfx950"}, {&b->stream_read, "ctox_stream_read_gfx950"},
+               {&b->write_segments, "ctox_write_segments_gfx950"},
                {&b->topk_part, "ctox_topk_part_gfx950"}, {&b->topk_final, "ctox_topk_final_gfx950"}};
     for (auto &f : fns) {
         if (le != hipSuccess) break;
@@ -2463,6 +2465,32 @@ extern "C" ctox_status ctox_hip_copy_rows_device(ctox_hip_backend *b, const floa
     if (in_stride < col_offset + cols) return fail(CTOX_ERR_SHAPE, "copy rows geometry");
     return rows_launch(b, b ? b->copy_rows : nullptr, d_in, in_stride, col_offset, rows, cols, d_out, out_stride,
                        stream, "ctox_copy_rows_gfx950");
+}
+
+ctox_status ctox_write_word_ranges_device(ctox_hip_backend *b, uint32_t *const *dst, const uint32_t *const *src,
+                                          const size_t *count, size_t n, void *stream) {
+    if (!b || (n && (!dst || !src || !count))) return fail(CTOX_ERR_SHAPE, "null argument");
+    hipStream_t s = pick_stream(b, stream);
+    SegWordsArgs a{};
+    auto flush = [&]() -> ctox_status {
+        if (a.nseg == 0) return CTOX_OK;
+        const ctox_status st = launch(b->write_segments, dim3(1), dim3(512), s, a, "ctox_write_segments_gfx950");
+        a = SegWordsArgs{};
+        return st;
+    };
+    for (size_t i = 0; i < n; i++) {
+        for (size_t done = 0; done < count[i];) {
+            if (a.nseg == CTOX_SEG_MAX || a.off[a.nseg] == CTOX_SEG_WORDS)
+                if (ctox_status st = flush()) return st;
+            const size_t take = std::min<size_t>(count[i] - done, CTOX_SEG_WORDS - a.off[a.nseg]);
+            a.dst[a.nseg] = dst[i] + done;
+            std::memcpy(a.words + a.off[a.nseg], src[i] + done, take * sizeof(uint32_t));
+            a.off[a.nseg + 1] = a.off[a.nseg] + (uint32_t)take;
+            a.nseg++;
+            done += take;
+        }
+    }
+    return flush();
 }
 
 extern "C" ctox_status ctox_hip_write_words_device(ctox_hip_backend *b, uint32_t *d_dst, const uint32_t *words,

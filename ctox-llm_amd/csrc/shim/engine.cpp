@@ -73,6 +73,10 @@ struct Cache {
     std::vector<uint32_t> free_q4, free_q2;
     uint32_t pages = 0, tokens = 0;
     uint32_t dirty = 0;  // lowest page whose descriptor changed since the last upload
+    // Pages before `scan` are demoted or in the sink: demotion resumes there.
+    // Truncation only removes rows after the last commit, which lie in pages
+    // at or after it, so the cursor never passes a page that changes again.
+    uint32_t scan = 0;
 };
 
 struct AttnLayer {
@@ -116,7 +120,11 @@ struct ctox_hip_engine {
     uint32_t *d_draft_ids = nullptr, *d_draft_inv = nullptr;
     // Fail-closed flags: non-finite logits (device words, read back through
     // pinned host memory with the step's one synchronization).
-    uint32_t *d_flags = nullptr, *h_flags = nullptr;
+    uint32_t *d_flags = nullptr;
+    // Host copy of the step result / flags. Ordinary (pageable) memory: the
+    // runtime then copies these few words with a blit kernel on the stream,
+    // which measured faster per step than a copy into pinned memory.
+    uint32_t h_res[128] = {};
     // MTP
     bool mtp = false;
     float *mtp_norm_emb = nullptr, *mtp_norm_hid = nullptr, *mtp_norm = nullptr;
@@ -136,10 +144,12 @@ struct ctox_hip_engine {
     uint32_t bank = 0, sidx = 0;
     size_t gdn_floats = 0, conv_floats = 0;
     // activations (sized for R rows)
-    float *hid = nullptr, *hid2 = nullptr, *xn = nullptr, *proj = nullptr, *convo = nullptr, *core = nullptr, *coren = nullptr,
+    float *hid = nullptr, *hid2 = nullptr, *proj = nullptr, *convo = nullptr, *core = nullptr, *coren = nullptr,
           *delta = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *gu = nullptr, *act = nullptr,
           *fin = nullptr, *logits = nullptr, *ld = nullptr, *beta = nullptr, *fcin = nullptr;
-    float *draft_logits = nullptr, *mtp_hidden = nullptr, *prev_hidden = nullptr, *target_hidden = nullptr;
+    float *draft_logits = nullptr, *mtp_hidden = nullptr, *prev_hidden = nullptr;
+    // d_drafts = d_result + 16: the acceptance result and the step's tokens
+    // come back to the host in one read.
     uint32_t *d_tokens = nullptr, *d_drafts = nullptr, *d_result = nullptr;
     uint64_t *d_rng = nullptr;
     uint32_t delta_parts = 1;  // partial sums held in delta (split-K producers)
@@ -403,9 +413,13 @@ void cache_truncate(Cache &c, uint32_t n) {
 // Q/src/kv_cache.rs:463-478: pages past the sink and wholly older than the recent window become Q2.
 ctox_status cache_demote(ctox_hip_engine *e, Cache &c) {
     const uint32_t recent_start = c.tokens > e->c.recent_tokens ? c.tokens - e->c.recent_tokens : 0;
-    for (uint32_t i = 0; i < c.pages; i++) {
+    // Pages are in token order: the first one not wholly older than the
+    // recent window ends the scan (host work per step independent of the context).
+    for (uint32_t i = c.scan; i < c.pages; i++) {
         ctox_paged_kv_descriptor &d = c.desc[i];
-        if (d.precision && d.first_token >= e->c.sink_tokens && d.first_token + d.tokens <= recent_start) {
+        if (d.first_token + d.tokens > recent_start) break;
+        c.scan = i + 1;
+        if (d.precision && d.first_token >= e->c.sink_tokens) {
             if (c.free_q2.empty()) return efail(CTOX_ERR_MEMORY_BUDGET, "no free Q2 page slot");
             const uint32_t q2 = c.free_q2.back();
             c.free_q2.pop_back();
@@ -573,8 +587,8 @@ ctox_status mtp_forward(ctox_hip_engine *e, const uint32_t *d_tok, const float *
                                        e->H, e->hid, e->s));
     // [norm(embedding), norm(previous hidden)] (decoder.rs:1023-1033)
     TRY(norm(e, e->hid, nullptr, e->mtp_norm_emb, R, e->H, e->fcin, 2 * e->H));
-    TRY(ctox_hip_copy_rows_device(e->b, prev, e->H, 0, R, e->H, e->xn, e->H, e->s));
-    TRY(norm(e, e->xn, nullptr, e->mtp_norm_hid, R, e->H, e->fcin + e->H, 2 * e->H));
+    // (no delta: the norm only reads its rows)
+    TRY(norm(e, const_cast<float *>(prev), nullptr, e->mtp_norm_hid, R, e->H, e->fcin + e->H, 2 * e->H));
     TRY(matvec(e, e->mtp_fc, e->fcin, e->hid, R));
     TRY(norm_mv(e, nullptr, e->mtp_attn.norm, R, e->mtp_attn.qkv, e->proj));
     TRY(attn_forward(e, e->mtp_attn, R, rope0, e->delta, retain));
@@ -584,17 +598,26 @@ ctox_status mtp_forward(ctox_hip_engine *e, const uint32_t *d_tok, const float *
     return norm(e, e->hid, e->delta, e->mtp_norm, R, e->H, e->mtp_hidden, e->H);
 }
 
+// Demotes every cache's aged pages, then uploads all changed descriptors
+// in one launch.
 ctox_status demote_all(ctox_hip_engine *e) {
+    std::vector<Cache *> caches;
     for (Layer &L : e->layers)
-        if (L.full) {
-            TRY(cache_demote(e, L.f.cache));
-            TRY(cache_upload(e, L.f.cache));
+        if (L.full) caches.push_back(&L.f.cache);
+    if (e->mtp) caches.push_back(&e->mtp_attn.cache);
+    std::vector<uint32_t *> dst;
+    std::vector<const uint32_t *> src;
+    std::vector<size_t> count;
+    for (Cache *c : caches) {
+        TRY(cache_demote(e, *c));
+        if (c->dirty < c->pages) {
+            dst.push_back((uint32_t *)(c->d_desc + c->dirty));
+            src.push_back((const uint32_t *)(c->desc.data() + c->dirty));
+            count.push_back((size_t)(c->pages - c->dirty) * 4);
         }
-    if (e->mtp) {
-        TRY(cache_demote(e, e->mtp_attn.cache));
-        TRY(cache_upload(e, e->mtp_attn.cache));
+        c->dirty = c->pages;
     }
-    return CTOX_OK;
+    return ctox_write_word_ranges_device(e->b, dst.data(), src.data(), count.data(), dst.size(), e->s);
 }
 
 // Queues the finite check of `n` logits into flag words [0, kFlagParts).
@@ -605,27 +628,25 @@ ctox_status check_logits(ctox_hip_engine *e, const float *x, size_t n) {
 
 // After the step's synchronization: fail closed on a flagged buffer
 // (Q/src/backend/cuda_runtime.rs:10627-10632, Q/src/engine.rs:191-272).
-ctox_status flags_ok(ctox_hip_engine *e, uint32_t count) {
-    for (uint32_t i = 0; i < count; i++)
-        if (e->h_flags[i]) return efail(CTOX_ERR_INVALID_STATE, "non-finite logits in the decode step");
-    return CTOX_OK;
-}
-
-ctox_status read_flags(ctox_hip_engine *e, uint32_t count) {
-    return hipMemcpyAsync(e->h_flags, e->d_flags, count * sizeof(uint32_t), hipMemcpyDeviceToHost, e->s) == hipSuccess
-               ? CTOX_OK
-               : efail(CTOX_ERR_INVALID_STATE, "flag read failed");
-}
-
 ctox_status sync(ctox_hip_engine *e) {
     hipError_t err = hipStreamSynchronize(e->s);
     return err == hipSuccess ? CTOX_OK : efail(CTOX_ERR_INVALID_STATE, "engine stream failed: %s", hipGetErrorString(err));
 }
 
+// Reads count device words at src into e->h_res once the stream has run
+// everything queued so far.
+ctox_status read_result(ctox_hip_engine *e, const uint32_t *src, uint32_t count) {
+    if (hipMemcpyAsync(e->h_res, src, count * sizeof(uint32_t), hipMemcpyDeviceToHost, e->s) != hipSuccess)
+        return efail(CTOX_ERR_INVALID_STATE, "result read failed");
+    return sync(e);
+}
+
+// Device copy of whole 32-bit words by a copy kernel (a runtime
+// device-to-device copy costs several times the host time of a launch).
 ctox_status copy_d2d(ctox_hip_engine *e, void *dst, const void *src, size_t bytes) {
-    return hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, e->s) == hipSuccess
-               ? CTOX_OK
-               : efail(CTOX_ERR_INVALID_STATE, "device copy failed");
+    if (bytes % 4) return efail(CTOX_ERR_SHAPE, "engine copies move whole words");
+    const size_t n = bytes / 4;
+    return ctox_hip_copy_rows_device(e->b, (const float *)src, n, 0, 1, n, (float *)dst, n, e->s);
 }
 
 }  // namespace
@@ -738,7 +759,7 @@ extern "C" ctox_status ctox_hip_engine_create_with_dtypes(ctox_hip_backend *b, c
     }
     const size_t R = e->R, qh = c.num_attention_heads, hd = c.head_dim;
     const size_t widest = std::max<size_t>({e->Rin, e->Rq, 2 * (size_t)e->I, e->H});
-    if ((st = dalloc_t(e, &e->hid, R * e->H)) || (st = dalloc_t(e, &e->hid2, R * e->H)) || (st = dalloc_t(e, &e->xn, R * e->H)) ||
+    if ((st = dalloc_t(e, &e->hid, R * e->H)) || (st = dalloc_t(e, &e->hid2, R * e->H)) ||
         (st = dalloc_t(e, &e->proj, R * widest)) || (st = dalloc_t(e, &e->convo, R * e->C)) ||
         (st = dalloc_t(e, &e->core, R * e->Vw)) || (st = dalloc_t(e, &e->coren, R * e->Vw)) ||
         (st = dalloc_t(e, &e->delta, 16 * R * e->H)) || (st = dalloc_t(e, &e->q, R * qh * hd)) ||
@@ -749,14 +770,10 @@ extern "C" ctox_status ctox_hip_engine_create_with_dtypes(ctox_hip_backend *b, c
         (st = dalloc_t(e, &e->beta, R * Hv)) || (st = dalloc_t(e, &e->fcin, R * 2 * e->H)) ||
         (st = dalloc_t(e, &e->draft_logits, (size_t)std::max(1u, c.draft_tokens) * e->V)) ||
         (st = dalloc_t(e, &e->mtp_hidden, R * e->H)) || (st = dalloc_t(e, &e->prev_hidden, R * e->H)) ||
-        (st = dalloc_t(e, &e->target_hidden, (R + 1) * e->H)) || (st = dalloc_t(e, &e->d_tokens, 16)) ||
-        (st = dalloc_t(e, &e->d_drafts, 16)) || (st = dalloc_t(e, &e->d_result, 16)) || (st = dalloc_t(e, &e->d_rng, 1)) ||
+        (st = dalloc_t(e, &e->d_tokens, 16)) || (st = dalloc_t(e, &e->d_result, 32)) || (st = dalloc_t(e, &e->d_rng, 1)) ||
         (st = dalloc_t(e, &e->rsq, 8 * 512)) || (st = dalloc_t(e, &e->blk_sq, 8 * 128)) || (st = dalloc_t(e, &e->d_flags, 64)))
         return cleanup(st);
-    if (hipHostMalloc((void **)&e->h_flags, 64 * sizeof(uint32_t), hipHostMallocDefault) != hipSuccess) {
-        e->h_flags = nullptr;
-        return cleanup(efail(CTOX_ERR_MEMORY_BUDGET, "pinned host flags allocation failed"));
-    }
+    e->d_drafts = e->d_result + 16;
     if ((st = sync(e))) return cleanup(st);
     *out = e;
     return CTOX_OK;
@@ -767,7 +784,6 @@ extern "C" void ctox_hip_engine_destroy(ctox_hip_engine *e) {
     if (e->s) hipStreamSynchronize(e->s);
     for (const auto &t : e->tiled) ctox_hip_unregister_tiled_weights(e->b, t.w);
     for (void *p : e->allocs) hipFree(p);
-    if (e->h_flags) hipHostFree(e->h_flags);
     if (e->s) hipStreamDestroy(e->s);
     delete e;
 }
@@ -803,10 +819,11 @@ extern "C" ctox_status ctox_hip_engine_decode(ctox_hip_engine *e, uint32_t token
     e->position++;
     TRY(demote_all(e));
     TRY(check_logits(e, e->logits, e->V));
-    TRY(read_flags(e, kFlagParts));
     if (d_logits) *d_logits = e->logits;
-    TRY(sync(e));
-    return flags_ok(e, kFlagParts);
+    TRY(read_result(e, e->d_flags, kFlagParts));
+    for (uint32_t i = 0; i < kFlagParts; i++)
+        if (e->h_res[i]) return efail(CTOX_ERR_INVALID_STATE, "non-finite logits in the decode step");
+    return CTOX_OK;
 }
 
 // One speculative step: k drafts sampled at `temperature`, one batched target
@@ -825,7 +842,6 @@ extern "C" ctox_status ctox_hip_engine_mtp_step(ctox_hip_engine *e, uint32_t tok
     // Drafts: d_{i+1} ~ softmax(MTP(x_i, g_i) / T) with x_0 = token, g_0 = the last
     // target hidden, then x_i = d_i, g_i = the MTP hidden of step i.
     TRY(copy_d2d(e, e->d_drafts, e->d_tokens, 4));
-    TRY(copy_d2d(e, e->target_hidden, e->prev_hidden, (size_t)e->H * 4));
     // Draft rows: the full head, or the restricted one (draft_n scores).
     const uint32_t dn = e->draft_n ? e->draft_n : e->V;
     for (uint32_t i = 0; i < k; i++) {
@@ -842,11 +858,8 @@ extern "C" ctox_status ctox_hip_engine_mtp_step(ctox_hip_engine *e, uint32_t tok
     TRY(ctox_hip_mtp_accept_restricted_device(e->b, e->draft_logits, dn, e->draft_n ? e->d_draft_inv : nullptr,
                                               e->logits, e->logits + (size_t)k * e->V, nullptr, e->d_drafts + 1, k,
                                               e->V, temperature, e->d_rng, e->d_result, e->s));
-    uint32_t host[16] = {0};
-    if (hipMemcpyAsync(host, e->d_result, 8, hipMemcpyDeviceToHost, e->s) != hipSuccess ||
-        hipMemcpyAsync(host + 2, e->d_drafts, 4 * R, hipMemcpyDeviceToHost, e->s) != hipSuccess)
-        return efail(CTOX_ERR_INVALID_STATE, "result read failed");
-    TRY(sync(e));
+    TRY(read_result(e, e->d_result, 16 + R));
+    const uint32_t *host = e->h_res;
     // The acceptance reports non-finite draft or target logits as 0xfffffffe;
     // nothing is committed from such a step.
     if (host[0] == 0xfffffffeu) return efail(CTOX_ERR_INVALID_STATE, "non-finite logits in the speculative step");
@@ -857,20 +870,22 @@ extern "C" ctox_status ctox_hip_engine_mtp_step(ctox_hip_engine *e, uint32_t tok
     e->sidx = n;
     for (Layer &L : e->layers)
         if (L.full) cache_truncate(L.f.cache, k - n);
-    // Final hiddens of the committed rows: h_p .. h_{p+n}.
-    TRY(copy_d2d(e, e->target_hidden + e->H, e->fin, (size_t)(n + 1) * e->H * 4));
     // MTP cache: keep the first draft's entry (token, previous hidden), replay
-    // d1..dn with the target hiddens h_p..h_{p+n-1} (commit_speculative).
+    // d1..dn with the target final hiddens h_p..h_{p+n-1} (commit_speculative),
+    // rows 0..n-1 of fin (the MTP layer does not write fin).
     cache_truncate(e->mtp_attn.cache, k - 1);
-    if (n > 0) TRY(mtp_forward(e, e->d_drafts + 1, e->target_hidden + e->H, n, p + 1, nullptr, true));
+    if (n > 0) TRY(mtp_forward(e, e->d_drafts + 1, e->fin, n, p + 1, nullptr, true));
     e->mtp_tokens = e->mtp_attn.cache.tokens;
-    TRY(copy_d2d(e, e->prev_hidden, e->target_hidden + (size_t)(n + 1) * e->H, (size_t)e->H * 4));
+    TRY(copy_d2d(e, e->prev_hidden, e->fin + (size_t)n * e->H, (size_t)e->H * 4));
     e->position = p + n + 1;
     TRY(demote_all(e));  // uploads every changed descriptor
     out[0] = next;
     out[1] = n;
-    for (uint32_t i = 0; i < n; i++) out[2 + i] = host[3 + i];
-    return sync(e);
+    for (uint32_t i = 0; i < n; i++) out[2 + i] = host[17 + i];
+    // The commit's launches stay queued on the engine stream: every later
+    // call and read is ordered after them, and the host returns without
+    // waiting (the result above came back with the acceptance).
+    return CTOX_OK;
 }
 
 // Context of `tokens` random K/V rows in every paged cache (and the MTP cache),

@@ -26,3 +26,9 @@ ctox_status ctox_norm_matvec_prestaged(ctox_hip_backend *b, int32_t dtype, const
                                        const uint16_t *d_s_out, float *d_output, uint32_t rows, uint32_t columns,
                                        uint32_t batch, const float *sq, float eps, uint32_t max_parts, uint32_t *parts,
                                        void *stream);
+
+// Writes n host word ranges (src[i], count[i] words) to device addresses
+// dst[i] with as few launches as the argument block allows (one for the
+// engine's per-step descriptor uploads).
+ctox_status ctox_write_word_ranges_device(ctox_hip_backend *b, uint32_t *const *dst, const uint32_t *const *src,
+                                          const size_t *count, size_t n, void *stream);

@@ -701,7 +701,11 @@ ctox_status ctox_hip_engine_set_rng(ctox_hip_engine *engine, uint64_t state);
  * cache advance of prefill (:1248-1261); *d_logits = the next-token logits. */
 ctox_status ctox_hip_engine_decode(ctox_hip_engine *engine, uint32_t token, const float **d_logits);
 /* One speculative step at `temperature`: out[0] next token, out[1] accepted
- * drafts n, out[2 .. 2 + n) the accepted drafts (out holds >= 2 + k words). */
+ * drafts n, out[2 .. 2 + n) the accepted drafts (out holds >= 2 + k words).
+ * The commit's device work (MTP cache replay, descriptor uploads) may still
+ * run on the engine stream when the call returns; every later engine call
+ * and every read of engine memory through that stream (or the legacy null
+ * stream) is ordered after it. */
 ctox_status ctox_hip_engine_mtp_step(ctox_hip_engine *engine, uint32_t token, float temperature, uint32_t *out);
 /* Fill every paged cache with `tokens` random K/V rows (an empty engine only). */
 ctox_status ctox_hip_engine_fill_context(ctox_hip_engine *engine, uint32_t tokens, uint64_t seed);
