@@ -524,7 +524,18 @@ struct GqaArgs {
     uint32_t splits;
     float scale;
     uint32_t tile_pages;     // 1 when page_tokens % 16 == 0: a 16-token tile lies in one page
-    uint32_t pad;
+    uint32_t st_dtype;       // staging below: 0 = Q2, 1 = Q4 fragment order of the o projection
+    // Optional (st_xa set): the combine also stages the o projection's input
+    // x[t][c] = out[t][c] * sigmoid(gate[t * st_gate_stride + head * 512 + 256 + d])
+    // (Q/src/decoder.rs:727-737), times st_s_in[c] (f16, or none), for
+    // column c = head * 256 + d, as the prep kernel would: 64-column block b
+    // of row t at st_xa + (b * rows + t) * 192, its constants at st_xc.
+    int8_t *st_xa;
+    float *st_xc;
+    const float *st_gate;
+    const uint16_t *st_s_in;
+    uint32_t st_gate_stride;
+    uint32_t st_pad;
 };
 
 // Decode engine helpers (engine_ops.hip).

@@ -1217,20 +1217,35 @@ extern "C" __global__ __launch_bounds__(256) void ctox_paged_gqa_combine_gfx950(
     }
     acc4[g][c] = acc;
     __syncthreads();
-    if (tid >= 16) return;
-    float4 sum = acc4[0][tid];
+    const uint32_t t = qi / a.group, gm = qi - t * a.group, head = h * a.group + gm;
+    __shared__ float stv[64];
+    if (tid < 16) {
+        float4 sum = acc4[0][tid];
 #pragma unroll
-    for (int k = 1; k < 16; k++) {
-        const float4 v = acc4[k][tid];
-        sum.x += v.x;
-        sum.y += v.y;
-        sum.z += v.z;
-        sum.w += v.w;
+        for (int k = 1; k < 16; k++) {
+            const float4 v = acc4[k][tid];
+            sum.x += v.x;
+            sum.y += v.y;
+            sum.z += v.z;
+            sum.w += v.w;
+        }
+        const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+        const float4 o = make_float4(sum.x * inv, sum.y * inv, sum.z * inv, sum.w * inv);
+        float4 *out = (float4 *)(a.out + ((size_t)t * a.query_heads + head) * PA_HD + 64 * quarter);
+        out[tid] = o;
+        *(float4 *)&stv[4 * tid] = o;
     }
-    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-    const uint32_t t = qi / a.group, gm = qi - t * a.group;
-    float4 *out = (float4 *)(a.out + ((size_t)t * a.query_heads + h * a.group + gm) * PA_HD + 64 * quarter);
-    out[tid] = make_float4(sum.x * inv, sum.y * inv, sum.z * inv, sum.w * inv);
+    if (!a.st_xa) return;
+    // The o projection's staged input for this 64-column block (wave 0).
+    __syncthreads();
+    if (tid >= 64) return;
+    const uint32_t col = head * PA_HD + 64 * quarter + tid;
+    const float gt = a.st_gate[(size_t)t * a.st_gate_stride + head * 2 * PA_HD + PA_HD + 64 * quarter + tid];
+    float x = stv[tid] * (1.0f / (1.0f + expf(-gt)));
+    if (a.st_s_in) x *= half_bits_to_float(a.st_s_in[col]);
+    const uint32_t blk = col / 64;
+    stage_block(x, a.st_xa + ((size_t)blk * a.rows + t) * 192, (float4 *)a.st_xc + (size_t)blk * a.rows + t, a.st_dtype,
+                tid);
 }
 
 // ---------------------------------------------------------------------------

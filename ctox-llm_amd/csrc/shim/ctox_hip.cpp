@@ -1407,7 +1407,8 @@ namespace {
 ctox_status transform_matvec_impl(ctox_hip_backend *b, const ctox_input_transform *x, int32_t dtype,
                                   const void *d_weights, const uint16_t *d_s_in, const uint16_t *d_s_out,
                                   float *d_output, uint32_t rows, uint32_t columns, uint32_t batch, uint32_t split_k,
-                                  uint32_t *parts, void *stream, const NextNorm *nx, bool *staged) {
+                                  uint32_t *parts, void *stream, const NextNorm *nx, bool *staged,
+                                  bool input_staged = false) {
     if (parts) *parts = 1;
     if (staged) *staged = false;
     if (!b || !x || !x->a || !d_weights || !d_output || ((x->mode == 2 || x->mode == 3) && !x->b) ||
@@ -1494,7 +1495,11 @@ ctox_status transform_matvec_impl(ctox_hip_backend *b, const ctox_input_transfor
     a.eps = x->eps;
     a.a_parts = x->a_parts > 1 ? x->a_parts : 1u;
     a.a_pstride = x->a_part_stride;
-    if ((st = launch(b->prep_x, dim3((unsigned)blocks, batch), dim3(64), s, a, "ctox_prep_transform_gfx950"))) return st;
+    // input_staged: the producer already wrote exactly this staging (the
+    // attention combine's gate staging of the o projection).
+    if (!input_staged &&
+        (st = launch(b->prep_x, dim3((unsigned)blocks, batch), dim3(64), s, a, "ctox_prep_transform_gfx950")))
+        return st;
     return run_matvec(b, layout, dtype, d_weights, rows, columns, batch, d_s_out,
                       d_s_out ? CTOX_KSCALE_F16 : CTOX_KSCALE_NONE, nullptr, d_output, rows, 0, s, split_k != 0, parts,
                       x->res_h, x->res_sums, nx, staged);
@@ -1514,8 +1519,11 @@ ctox_status ctox_delta_matvec_stage_next(ctox_hip_backend *b, const ctox_input_t
                                          const void *d_weights, const uint16_t *d_s_in, const uint16_t *d_s_out,
                                          float *d_output, uint32_t rows, uint32_t columns, uint32_t batch,
                                          const float *next_norm_w, const uint16_t *next_s_in, int32_t next_dtype,
-                                         float *next_h_out, float *next_sq_out, bool *staged, void *stream) {
+                                         float *next_h_out, float *next_sq_out, bool *staged, void *stream,
+                                         bool input_staged) {
     if (staged) *staged = false;
+    if (input_staged && !ctox_small_m_staged(b, d_weights, batch, rows, columns))
+        return fail(CTOX_ERR_INVALID_STATE, "a prestaged input needs the staged small-M path");
     if (!next_norm_w || !next_h_out || !next_sq_out || !staged || !x || !x->res_h || !x->res_sums)
         return fail(CTOX_ERR_SHAPE, "next-norm staging: null argument");
     if (next_dtype != CTOX_DTYPE_Q2B64 && next_dtype != CTOX_DTYPE_Q4B64)
@@ -1527,7 +1535,7 @@ ctox_status ctox_delta_matvec_stage_next(ctox_hip_backend *b, const ctox_input_t
     nx.h_out = next_h_out;
     nx.sq_out = next_sq_out;
     return transform_matvec_impl(b, x, dtype, d_weights, d_s_in, d_s_out, d_output, rows, columns, batch, 0, nullptr,
-                                 stream, batch >= 2 && batch <= 8 ? &nx : nullptr, staged);
+                                 stream, batch >= 2 && batch <= 8 ? &nx : nullptr, staged, input_staged);
 }
 
 ctox_status ctox_norm_matvec_prestaged(ctox_hip_backend *b, int32_t dtype, const void *d_weights,
@@ -2314,11 +2322,19 @@ extern "C" ctox_status ctox_hip_kv_demote_device(ctox_hip_backend *b, const uint
                   "ctox_kv_demote_gfx950");
 }
 
-extern "C" ctox_status ctox_hip_paged_gqa_device(ctox_hip_backend *b, const float *d_query, const uint8_t *d_q2_pages,
-                                                 const uint8_t *d_q4_pages,
-                                                 const ctox_paged_kv_descriptor *d_descriptors,
-                                                 const ctox_paged_gqa_params *p, size_t rows, float *d_out,
-                                                 void *stream) {
+namespace {
+// The attention-gate staging of the o projection's input done by the combine.
+struct GateStage {
+    const float *gate = nullptr;
+    uint32_t gate_stride = 0;
+    const uint16_t *s_in = nullptr;
+    int32_t dtype = 0;
+};
+
+ctox_status paged_gqa_impl(ctox_hip_backend *b, const float *d_query, const uint8_t *d_q2_pages,
+                           const uint8_t *d_q4_pages, const ctox_paged_kv_descriptor *d_descriptors,
+                           const ctox_paged_gqa_params *p, size_t rows, float *d_out, void *stream,
+                           const GateStage *gs) {
     if (!b || !d_query || !d_q2_pages || !d_q4_pages || !d_descriptors || !p || !d_out)
         return fail(CTOX_ERR_SHAPE, "null argument");
     if (p->head_dim != 256) return fail(CTOX_ERR_UNSUPPORTED_OPERATION, "paged attention needs head_dim 256");
@@ -2351,6 +2367,19 @@ extern "C" ctox_status ctox_hip_paged_gqa_device(ctox_hip_backend *b, const floa
               d_out, p->q2_page_bytes, p->q4_page_bytes, p->query_heads, group, p->tokens, (uint32_t)rows, queries,
               p->page_tokens, p->page_count, (uint32_t)cv, p->q2_token_bytes, p->q4_token_bytes, tiles, tpw, splits,
               p->scale, p->page_tokens % 16 == 0 ? 1u : 0u, 0};
+    if (gs) {
+        const int layout = gs->dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
+        const size_t blocks = (size_t)p->query_heads * 256 / kBlockLen;
+        st = ensure(b, b->xa[layout], blocks * rows * 192, false);
+        if (!st) st = ensure(b, b->xc[layout], blocks * rows * 4 * sizeof(float), false);
+        if (st) return st;
+        a.st_xa = (int8_t *)b->xa[layout].ptr;
+        a.st_xc = (float *)b->xc[layout].ptr;
+        a.st_gate = gs->gate;
+        a.st_gate_stride = gs->gate_stride;
+        a.st_s_in = gs->s_in;
+        a.st_dtype = (uint32_t)layout;
+    }
     hipStream_t s = pick_stream(b, stream);
     // Page-aligned 16-token tiles run P.V on f16 MFMA; other page sizes on the fp32-MFMA kernel.
     // (its waves hold up to 64 tiles' page descriptors in registers).
@@ -2360,6 +2389,35 @@ extern "C" ctox_status ctox_hip_paged_gqa_device(ctox_hip_backend *b, const floa
                 "ctox_paged_gqa_partial_gfx950");
     if (st) return st;
     return launch(b->gqa_combine, dim3(queries, p->key_value_heads, 4), dim3(256), s, a, "ctox_paged_gqa_combine_gfx950");
+}
+}  // namespace
+
+extern "C" ctox_status ctox_hip_paged_gqa_device(ctox_hip_backend *b, const float *d_query, const uint8_t *d_q2_pages,
+                                                 const uint8_t *d_q4_pages,
+                                                 const ctox_paged_kv_descriptor *d_descriptors,
+                                                 const ctox_paged_gqa_params *p, size_t rows, float *d_out,
+                                                 void *stream) {
+    return paged_gqa_impl(b, d_query, d_q2_pages, d_q4_pages, d_descriptors, p, rows, d_out, stream, nullptr);
+}
+
+ctox_status ctox_paged_gqa_stage_o_device(ctox_hip_backend *b, const float *d_query, const uint8_t *d_q2_pages,
+                                          const uint8_t *d_q4_pages, const ctox_paged_kv_descriptor *d_descriptors,
+                                          const ctox_paged_gqa_params *p, size_t rows, float *d_out,
+                                          const float *d_gate, uint32_t gate_stride, const uint16_t *d_o_s_in,
+                                          int32_t o_dtype, void *stream) {
+    if (!d_gate || gate_stride < 2 * 256 * (size_t)(p ? p->query_heads : 0))
+        return fail(CTOX_ERR_SHAPE, "attention gate staging geometry");
+    GateStage gs;
+    gs.gate = d_gate;
+    gs.gate_stride = gate_stride;
+    gs.s_in = d_o_s_in;
+    gs.dtype = o_dtype;
+    return paged_gqa_impl(b, d_query, d_q2_pages, d_q4_pages, d_descriptors, p, rows, d_out, stream, &gs);
+}
+
+bool ctox_small_m_staged(ctox_hip_backend *b, const void *d_weights, uint32_t batch, uint32_t rows, uint32_t columns) {
+    return b && batch >= 2 && batch <= 8 && !build_in_kernel(b, batch, rows, columns) &&
+           registered(b, d_weights, rows, columns) != nullptr;
 }
 static_assert(sizeof(ctox_paged_kv_descriptor) == sizeof(PagedKvDesc), "page descriptor layout");
 

@@ -281,7 +281,10 @@ ctox_status norm_mv(ctox_hip_engine *e, const float *delta, const float *w, uint
 
 // A single-row producer of residual delta `out` also leaves the next norm's
 // per-tile sums of squares (ctox_input_transform::res_sums).
-ctox_status delta_mv(ctox_hip_engine *e, ctox_input_transform &x, const Mat &m, float *out, uint32_t R) {
+// input_staged: x's staging was already written (the attention combine's),
+// only with a next norm-matvec in view (the stage-next path).
+ctox_status delta_mv(ctox_hip_engine *e, ctox_input_transform &x, const Mat &m, float *out, uint32_t R,
+                     bool input_staged = false) {
     const float *nx_w = e->nx_w;
     const Mat *nx_m = e->nx_m;
     e->nx_w = nullptr;
@@ -295,7 +298,7 @@ ctox_status delta_mv(ctox_hip_engine *e, ctox_input_transform &x, const Mat &m, 
     bool staged = false;
     if (nx_m && R >= 2 && R <= kSumRows && e->next_norm) {
         TRY(ctox_delta_matvec_stage_next(e->b, &x, m.dtype, m.w, m.s_in, m.s_out, out, m.rows, m.cols, R, nx_w,
-                                         nx_m->s_in, nx_m->dtype, e->hid2, e->blk_sq, &staged, e->s));
+                                         nx_m->s_in, nx_m->dtype, e->hid2, e->blk_sq, &staged, e->s, input_staged));
         e->delta_parts = 1;
         if (staged) {
             e->pre_w = nx_w;
@@ -500,9 +503,17 @@ ctox_status attn_forward(ctox_hip_engine *e, AttnLayer &a, uint32_t R, uint32_t 
         TRY(cache_upload(e, c));
     }
     const ctox_paged_gqa_params p = gqa_params(e, a.cache);
-    TRY(ctox_hip_paged_gqa_device(e->b, e->q, a.cache.q2, a.cache.q4, a.cache.d_desc, &p, R, e->attn, e->s));
+    // On the verify path the combine also stages o_proj's gated input (no
+    // staging launch); o_proj then runs as a next-norm producer.
+    const bool stage_o = e->next_norm && e->nx_m && R >= 2 && R <= kSumRows &&
+                         ctox_small_m_staged(e->b, a.o.w, R, a.o.rows, a.o.cols);
+    if (stage_o)
+        TRY(ctox_paged_gqa_stage_o_device(e->b, e->q, a.cache.q2, a.cache.q4, a.cache.d_desc, &p, R, e->attn, e->proj,
+                                          e->Rq, a.o.s_in, a.o.dtype, e->s));
+    else
+        TRY(ctox_hip_paged_gqa_device(e->b, e->q, a.cache.q2, a.cache.q4, a.cache.d_desc, &p, R, e->attn, e->s));
     ctox_input_transform x{e->attn, e->proj, nullptr, 3, qh * hd, e->Rq, 0, hd, 0.0f, nullptr, nullptr, 0, 0};
-    return delta_mv(e, x, a.o, delta, R);
+    return delta_mv(e, x, a.o, delta, R, stage_o);
 }
 
 float *state_cur(ctox_hip_engine *e) { return e->gdn_bank + ((size_t)e->bank * e->R + e->sidx) * e->gdn_floats; }

@@ -11,12 +11,15 @@
 // buffers for a matrix of next_dtype, and next_sq_out [batch][rows / 64]
 // receives per-64-row sums of h^2. *staged reports whether the staging was
 // made (otherwise the call is the plain transform-matvec and the caller
-// stages the norm itself).
+// stages the norm itself). input_staged: x's transform of this call was
+// already staged (ctox_paged_gqa_stage_o_device), no staging launch is made;
+// only valid where ctox_small_m_staged holds.
 ctox_status ctox_delta_matvec_stage_next(ctox_hip_backend *b, const ctox_input_transform *x, int32_t dtype,
                                          const void *d_weights, const uint16_t *d_s_in, const uint16_t *d_s_out,
                                          float *d_output, uint32_t rows, uint32_t columns, uint32_t batch,
                                          const float *next_norm_w, const uint16_t *next_s_in, int32_t next_dtype,
-                                         float *next_h_out, float *next_sq_out, bool *staged, void *stream);
+                                         float *next_h_out, float *next_sq_out, bool *staged, void *stream,
+                                         bool input_staged = false);
 
 // The projection of what ctox_delta_matvec_stage_next staged: registered
 // weights of next_dtype, the same batch, `sq` its per-block sums of h^2 and
@@ -32,3 +35,18 @@ ctox_status ctox_norm_matvec_prestaged(ctox_hip_backend *b, int32_t dtype, const
 // engine's per-step descriptor uploads).
 ctox_status ctox_write_word_ranges_device(ctox_hip_backend *b, uint32_t *const *dst, const uint32_t *const *src,
                                           const size_t *count, size_t n, void *stream);
+
+// Whether a 2..8-row projection of these registered weights runs the staged
+// small-M kernels (its input staged by a separate pass), not the in-kernel build.
+bool ctox_small_m_staged(ctox_hip_backend *b, const void *d_weights, uint32_t batch, uint32_t rows, uint32_t columns);
+
+// ctox_hip_paged_gqa_device whose combine also stages the o projection's
+// input (attention output times sigmoid of the gate half of d_gate's rows,
+// gate_stride floats apart, times the o projection's f16 s_in) for a staged
+// small-M launch of an o_dtype matrix; the transform-matvec then passes
+// input_staged.
+ctox_status ctox_paged_gqa_stage_o_device(ctox_hip_backend *b, const float *d_query, const uint8_t *d_q2_pages,
+                                          const uint8_t *d_q4_pages, const ctox_paged_kv_descriptor *d_descriptors,
+                                          const ctox_paged_gqa_params *p, size_t rows, float *d_out,
+                                          const float *d_gate, uint32_t gate_stride, const uint16_t *d_o_s_in,
+                                          int32_t o_dtype, void *stream);
