@@ -1130,19 +1130,7 @@ CTOX_TILE_MX_KERNEL(ctox_q4_mv_tilemx2_gfx950, 1, 2)
 CTOX_TILE_MX_KERNEL(ctox_q4_mv_tilemx3_gfx950, 1, 3)
 CTOX_TILE_MX_KERNEL(ctox_q4_mv_tilemx4_gfx950, 1, 4)
 CTOX_TILE_MX_KERNEL(ctox_q4_mv_tilemx5_gfx950, 1, 5)
-// Sixteen-wave workgroups: each wave builds at most two of the chunk's
-// 4 x M group rows (ctox_q{2,4}_mv_tilemxw{M}_gfx950).
-#define CTOX_TILE_MXW_KERNEL(name, dt, mr) \
-    extern "C" __global__ __launch_bounds__(1024) void name(TileMatvecArgs a) { tile_matvec_mx<dt, mr, 0, 16>(a); } \
-    extern "C" __global__ __launch_bounds__(1024) void name##_arrive(TileMatvecArgs a) { tile_matvec_mx<dt, mr, 1, 16>(a); }
-CTOX_TILE_MXW_KERNEL(ctox_q2_mv_tilemxw2_gfx950, 0, 2)
-CTOX_TILE_MXW_KERNEL(ctox_q2_mv_tilemxw3_gfx950, 0, 3)
-CTOX_TILE_MXW_KERNEL(ctox_q2_mv_tilemxw4_gfx950, 0, 4)
-CTOX_TILE_MXW_KERNEL(ctox_q2_mv_tilemxw5_gfx950, 0, 5)
-CTOX_TILE_MXW_KERNEL(ctox_q4_mv_tilemxw2_gfx950, 1, 2)
-CTOX_TILE_MXW_KERNEL(ctox_q4_mv_tilemxw3_gfx950, 1, 3)
-CTOX_TILE_MXW_KERNEL(ctox_q4_mv_tilemxw4_gfx950, 1, 4)
-CTOX_TILE_MXW_KERNEL(ctox_q4_mv_tilemxw5_gfx950, 1, 5)
+
 
 // Rewrites crate rows (Q/src/quant.rs:20-29 block layout, rows dense) into
 // the tiled layout; one workgroup per unit, lane (g, j) moves its fragment

@@ -170,9 +170,6 @@ struct ctox_hip_backend {
     // The same building the rows' fragments in the kernel, per row count 2..5.
     hipFunction_t tilemx[2][4] = {};
     hipFunction_t tilemx_arr[2][4] = {};  // combine by arrival
-    hipFunction_t tilemxw[2][4] = {};     // sixteen-wave workgroups
-    hipFunction_t tilemxw_arr[2][4] = {};
-    uint32_t mx_waves = 4;                // CTOX_MX_W: waves per tilemx workgroup (4 or 16)
     uint64_t mx_max = (uint64_t)8 << 20;  // CTOX_MX_MAX (Mi): largest matrix the small-M launch builds rows for
     bool no_mx = false;
     bool noalloc_ok = false;  // the static scratch of ctox_hip_launch_fused_matvec_noalloc is set up
@@ -184,7 +181,6 @@ struct ctox_hip_backend {
     uint32_t tile_cap[2][2][CTOX_TILE_MAXU] = {};  // [staged|built][q4][u - 1]: workgroups resident at once
     uint32_t tilem_cap[2][7] = {};                  // [q4][rows - 2], same for the small-M kernels
     uint32_t tilemx_cap[2][4] = {};                 // [q4][rows - 2]
-    uint32_t tilemxw_cap[2][4] = {};
     // Tiled matvec chunk partials (64-bit slots tagged with a launch sequence
     // number; zeroed when allocated) and the last sequence number used.
     DevBuf tpart;
@@ -706,13 +702,13 @@ ctox_status run_tile_matvec_mx(ctox_hip_backend *b, int32_t dtype, const TiledCo
                                float *d_output, size_t out_stride, uint32_t act, hipStream_t s, const float *d_input,
                                const void *d_s_in, uint32_t s_in_kind, const TileXform &xf, const PartialSlots *ps) {
     const int q4 = dtype == CTOX_DTYPE_Q4B64 ? 1 : 0;
-    const uint32_t u = 1, W = b->mx_waves;
-    const uint32_t segs = (((t.tiles + u - 1) / u) + W - 1) / W * W;
+    const uint32_t u = 1;
+    const uint32_t segs = (((t.tiles + u - 1) / u) + 3) & ~3u;
     const size_t waves = (size_t)segs * t.chunks;
     if (batch < 2 || batch > kMaxBuildRows) return fail(CTOX_ERR_SHAPE, "in-kernel row build takes 2..5 rows");
-    if (waves / W > 0x7fffffffu || out_stride > 0xffffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
-    const uint32_t cap = W == 16 ? b->tilemxw_cap[q4][batch - 2] : b->tilemx_cap[q4][batch - 2];
-    const bool arrive = t.chunks > 1 && (b->arrive >= 0 ? b->arrive != 0 : waves / W > cap);
+    if (waves / 4 > 0x7fffffffu || out_stride > 0xffffffffu) return fail(CTOX_ERR_SHAPE, "matrix too large for one launch");
+    const bool arrive =
+        t.chunks > 1 && (b->arrive >= 0 ? b->arrive != 0 : waves / 4 > b->tilemx_cap[q4][batch - 2]);
     const size_t slot_bytes =
         (size_t)(arrive ? t.chunks : t.chunks - 1) * batch * t.tiles * CTOX_TILE_ROWS * sizeof(uint64_t);
     if (ps && t.chunks > 1 && (slot_bytes > ps->bytes || (arrive && t.tiles > ps->arrive_n)))
@@ -759,9 +755,8 @@ ctox_status run_tile_matvec_mx(ctox_hip_backend *b, int32_t dtype, const TiledCo
     a.out_stride = (uint32_t)out_stride;
     a.a_stride = xf.a_stride;
     a.b_stride = xf.b_stride;
-    hipFunction_t f = W == 16 ? (arrive ? b->tilemxw_arr[q4][batch - 2] : b->tilemxw[q4][batch - 2])
-                              : (arrive ? b->tilemx_arr[q4][batch - 2] : b->tilemx[q4][batch - 2]);
-    return launch(f, dim3((unsigned)(waves / W)), dim3(64 * W), s, a, "ctox_q*_mv_tilemx*_gfx950");
+    return launch(arrive ? b->tilemx_arr[q4][batch - 2] : b->tilemx[q4][batch - 2], dim3((unsigned)(waves / 4)), dim3(256), s, a,
+                  "ctox_q*_mv_tilemx*_gfx950");
 }
 
 // The registered tiled copy of raw weights, or NULL.
@@ -928,14 +923,6 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->tilemx_arr[0][2], "ctox_q2_mv_tilemx4_gfx950_arrive"}, {&b->tilemx_arr[0][3], "ctox_q2_mv_tilemx5_gfx950_arrive"},
                {&b->tilemx_arr[1][0], "ctox_q4_mv_tilemx2_gfx950_arrive"}, {&b->tilemx_arr[1][1], "ctox_q4_mv_tilemx3_gfx950_arrive"},
                {&b->tilemx_arr[1][2], "ctox_q4_mv_tilemx4_gfx950_arrive"}, {&b->tilemx_arr[1][3], "ctox_q4_mv_tilemx5_gfx950_arrive"},
-               {&b->tilemxw[0][0], "ctox_q2_mv_tilemxw2_gfx950"}, {&b->tilemxw[0][1], "ctox_q2_mv_tilemxw3_gfx950"},
-               {&b->tilemxw[0][2], "ctox_q2_mv_tilemxw4_gfx950"}, {&b->tilemxw[0][3], "ctox_q2_mv_tilemxw5_gfx950"},
-               {&b->tilemxw[1][0], "ctox_q4_mv_tilemxw2_gfx950"}, {&b->tilemxw[1][1], "ctox_q4_mv_tilemxw3_gfx950"},
-               {&b->tilemxw[1][2], "ctox_q4_mv_tilemxw4_gfx950"}, {&b->tilemxw[1][3], "ctox_q4_mv_tilemxw5_gfx950"},
-               {&b->tilemxw_arr[0][0], "ctox_q2_mv_tilemxw2_gfx950_arrive"}, {&b->tilemxw_arr[0][1], "ctox_q2_mv_tilemxw3_gfx950_arrive"},
-               {&b->tilemxw_arr[0][2], "ctox_q2_mv_tilemxw4_gfx950_arrive"}, {&b->tilemxw_arr[0][3], "ctox_q2_mv_tilemxw5_gfx950_arrive"},
-               {&b->tilemxw_arr[1][0], "ctox_q4_mv_tilemxw2_gfx950_arrive"}, {&b->tilemxw_arr[1][1], "ctox_q4_mv_tilemxw3_gfx950_arrive"},
-               {&b->tilemxw_arr[1][2], "ctox_q4_mv_tilemxw4_gfx950_arrive"}, {&b->tilemxw_arr[1][3], "ctox_q4_mv_tilemxw5_gfx950_arrive"},
                {&b->repack, "ctox_tile_repack_gfx950"}, {&b->gdn_fused, "ctox_gdn_fused_gfx950"}, {&b->gdn_fused_blk, "ctox_gdn_fused_blk_gfx950"},
                {&b->finite, "ctox_finite_check_gfx950"}, {&b->gather, "ctox_gather_rows_gfx950"}, {&b->stream_read, "ctox_stream_read_gfx950"},
                {&b->write_segments, "ctox_write_segments_gfx950"},
@@ -971,15 +958,14 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
     // separate launch (the tilem kernels) instead of building them in-kernel.
     if (const char *m = std::getenv("CTOX_SMALL_M_BUILD")) b->no_mx = std::atoi(m) == 0;
     if (const char *m = std::getenv("CTOX_ARRIVE")) b->arrive = std::atoi(m) != 0;
-    if (const char *m = std::getenv("CTOX_MX_W")) b->mx_waves = std::atoi(m) == 16 ? 16u : 4u;
     if (const char *m = std::getenv("CTOX_MX_MAX")) b->mx_max = (uint64_t)std::atoll(m) << 20;
     // How many workgroups of each tiled kernel the device holds at once:
     // launches within it may combine by the last chunk's waves (every
     // producer is resident whatever the dispatch order); larger ones combine
     // by arrival.
-    auto cap = [&](hipFunction_t f, int threads = 256) {
+    auto cap = [&](hipFunction_t f) {
         int n = 0;
-        if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, threads, 0) != hipSuccess) n = 0;
+        if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, 256, 0) != hipSuccess) n = 0;
         return (uint32_t)std::max(0, n) * (uint32_t)b->cus;
     };
     for (int q = 0; q < 2; q++) {
@@ -988,10 +974,7 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
             b->tile_cap[1][q][u] = cap(b->tilex[q][u]);
         }
         for (int m = 0; m < 7; m++) b->tilem_cap[q][m] = cap(b->tilem[q][m]);
-        for (int r = 0; r < 4; r++) {
-            b->tilemx_cap[q][r] = cap(b->tilemx[q][r]);
-            b->tilemxw_cap[q][r] = cap(b->tilemxw[q][r], 1024);
-        }
+        for (int r = 0; r < 4; r++) b->tilemx_cap[q][r] = cap(b->tilemx[q][r]);
     }
     if (const char *u = std::getenv("CTOX_TILE_U")) {
         const int v = std::atoi(u);
