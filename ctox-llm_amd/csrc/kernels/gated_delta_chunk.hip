@@ -17,7 +17,8 @@
 // overflows however strong the decay.
 //
 // Pass 1 (ctox_gdn_chunk_prep_gfx950, one workgroup per (head, chunk), all
-// chunks in parallel): norms, G, M and A by LDS-tiled dot products, T by
+// chunks in parallel): norms, G, M and A from the lower 16 x 16 tiles of
+// K K^T and Q K^T on v_mfma_f32_16x16x4_f32, T by
 // forward substitution (one thread per column, the column in registers).
 // Pass 2 (ctox_gdn_chunk_scan_gfx950, one workgroup per (head, 16 value
 // columns), chunks in order): the 128 x 16 state slice stays in LDS across
@@ -33,17 +34,45 @@
 #define GC 64        // max chunk length
 #define GKD 128      // max key_dim of the chunked path
 #define GVS 16       // value columns per pass-2 workgroup
-#define GPAD 129     // LDS row stride (floats) of K / Q tiles: odd, conflict-free
 #define TPAD 65      // LDS row stride of T / A / M
 
 typedef float gv4f __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ gv4f mfma4(float a, float b, gv4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+#define SPAD 132  // LDS row stride (floats) of pass-2 K / Q tiles and of S^T
+#define TSPAD 68  // LDS row stride of pass-2 T / A / Y^T / (b v)^T
+
+// 16 x 16 tile of A[16 x K] * B[K x 16] with both operands stored k-contiguous
+// (A row-major [m][k], B as B^T [n][k]): lane (m = l % 16, kq = l / 16)
+// covers k = kq * (K / 4) + u for MFMA u, so each lane reads a contiguous
+// run of K / 4 floats of both operands.
+template <int K, int LDA, int LDB>
+__device__ __forceinline__ gv4f tile_kk(const float *a, const float *bt, gv4f acc, uint32_t lane) {
+    const uint32_t m = lane & 15, kq = lane >> 4;
+    const float *ap = a + m * LDA + kq * (K / 4);
+    const float *bp = bt + m * LDB + kq * (K / 4);
+    // Four independent accumulation chains, summed at the end.
+    gv4f c1 = {0.0f, 0.0f, 0.0f, 0.0f}, c2 = c1, c3 = c1;
+#pragma unroll
+    for (int u = 0; u < K / 4; u += 4) {
+        const float4 av = *(const float4 *)(ap + u), bv = *(const float4 *)(bp + u);
+        acc = mfma4(av.x, bv.x, acc);
+        c1 = mfma4(av.y, bv.y, c1);
+        c2 = mfma4(av.z, bv.z, c2);
+        c3 = mfma4(av.w, bv.w, c3);
+    }
+    return (acc + c1) + (c2 + c3);
+}
 
 // Scratch per (head, chunk): T[64][64], A[64][64], then G[64], kinv[64], qinv[64].
 __host__ __device__ constexpr uint32_t ctox_gdn_chunk_floats() { return 2 * GC * GC + 3 * GC; }
 
 extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_prep_gfx950(GdnArgs a) {
-    __shared__ float kh[GC * GPAD];
-    __shared__ float qh[GC * GPAD];  // q^ rows, then M (after the dot-product tiles)
+    __shared__ __align__(16) float kh[GC * SPAD];
+    __shared__ __align__(16) float qh[GC * SPAD];  // q^ rows, then M (after the dot-product tiles)
     __shared__ float G[GC], bt[GC], kinv_s[GC], qinv_s[GC];
     float *mm = qh;
     const uint32_t tid = threadIdx.x;
@@ -64,8 +93,8 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_prep_gfx950(Gdn
             const float *qr = a.q + qk;
             for (uint32_t i = p; i < dk; i += 4) {
                 const float kv = kr[i], qv = qr[i];
-                kh[s * GPAD + i] = kv;
-                qh[s * GPAD + i] = qv;
+                kh[s * SPAD + i] = kv;
+                qh[s * SPAD + i] = qv;
                 sk += kv * kv;
                 sq += qv * qv;
             }
@@ -97,41 +126,42 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_prep_gfx950(Gdn
     for (uint32_t e = tid; e < GC * GKD; e += 256) {
         const uint32_t s = e / GKD, i = e % GKD;
         const bool ok = s < n && i < dk;
-        kh[s * GPAD + i] = ok ? kh[s * GPAD + i] * kinv_s[s] : 0.0f;
-        qh[s * GPAD + i] = ok ? qh[s * GPAD + i] * qinv_s[s] * qscale : 0.0f;
+        kh[s * SPAD + i] = ok ? kh[s * SPAD + i] * kinv_s[s] : 0.0f;
+        qh[s * SPAD + i] = ok ? qh[s * SPAD + i] * qinv_s[s] * qscale : 0.0f;
     }
     __syncthreads();
-    // 4 x 4 tiles of K K^T and Q K^T: rows s = 4*(tid/16)+x, cols r = 4*(tid%16)+y.
+    // The lower 16 x 16 tiles of K K^T and Q K^T on MFMA: 10 tiles each,
+    // (sb, rb) with rb <= sb, five per wave; the upper tiles of A are zero.
     {
-        const uint32_t sb = (tid >> 4) * 4, rb = (tid & 15) * 4;
-        float kk[4][4] = {}, qk[4][4] = {};
-        for (uint32_t i = 0; i < GKD; i++) {
-            float ks[4], qs[4], kr[4];
+        const uint32_t lane = tid & 63, w = tid >> 6, m16 = lane & 15, kq = lane >> 4;
+        gv4f acc[5];
 #pragma unroll
-            for (int x = 0; x < 4; x++) {
-                ks[x] = kh[(sb + x) * GPAD + i];
-                qs[x] = qh[(sb + x) * GPAD + i];
-                kr[x] = kh[(rb + x) * GPAD + i];
-            }
-#pragma unroll
-            for (int x = 0; x < 4; x++)
-#pragma unroll
-                for (int y = 0; y < 4; y++) {
-                    kk[x][y] = fmaf(ks[x], kr[y], kk[x][y]);
-                    qk[x][y] = fmaf(qs[x], kr[y], qk[x][y]);
-                }
+        for (int u = 0; u < 5; u++) {
+            const uint32_t t = w + 4 * u, l = t % 10;
+            const uint32_t sb = l >= 6 ? 3 : (l >= 3 ? 2 : (l >= 1 ? 1 : 0));
+            const uint32_t rb = l - sb * (sb + 1) / 2;
+            acc[u] = tile_kk<GKD, SPAD, SPAD>((t < 10 ? kh : qh) + 16 * sb * SPAD, kh + 16 * rb * SPAD,
+                                              (gv4f){0, 0, 0, 0}, lane);
         }
-        float *Aout = a.norms + ((size_t)h * ((a.tokens + a.chunk - 1) / a.chunk) + c) * ctox_gdn_chunk_floats() + GC * GC;
+        float *Aout = a.norms + ((size_t)h * nch + c) * ctox_gdn_chunk_floats() + GC * GC;
         __syncthreads();  // every tile has read q^: its rows become M
 #pragma unroll
-        for (int x = 0; x < 4; x++)
+        for (int u = 0; u < 5; u++) {
+            const uint32_t t = w + 4 * u, l = t % 10;
+            const uint32_t sb = l >= 6 ? 3 : (l >= 3 ? 2 : (l >= 1 ? 1 : 0));
+            const uint32_t rb = l - sb * (sb + 1) / 2;
 #pragma unroll
-            for (int y = 0; y < 4; y++) {
-                const uint32_t s = sb + x, r = rb + y;
+            for (int x = 0; x < 4; x++) {
+                const uint32_t s = 16 * sb + 4 * kq + x, r = 16 * rb + m16;
                 const float dec = expf(G[s] - G[r]);
-                mm[s * TPAD + r] = r < s ? dec * kk[x][y] : 0.0f;
-                Aout[s * GC + r] = r <= s ? dec * qk[x][y] : 0.0f;
+                if (t < 10) mm[s * TPAD + r] = r < s ? dec * acc[u][x] : 0.0f;
+                else Aout[s * GC + r] = r <= s ? dec * acc[u][x] : 0.0f;
             }
+        }
+        for (uint32_t e = tid; e < GC * GC / 4; e += 256) {
+            const uint32_t s = e / 16, r = (e % 16) * 4;
+            if (r / 16 > s / 16) *(float4 *)(Aout + s * GC + r) = make_float4(0, 0, 0, 0);
+        }
     }
     __syncthreads();
     float *base = a.norms + ((size_t)h * nch + c) * ctox_gdn_chunk_floats();
@@ -153,12 +183,15 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_prep_gfx950(Gdn
     }
 }
 
-__device__ __forceinline__ gv4f mfma4(float a, float b, gv4f c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+// A buffer resource over [p, p + bytes) whose fields the compiler keeps in
+// scalar registers: p and bytes are wave-uniform but computed through vector
+// registers, and a resource in vector registers costs a waterfall loop per load.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void *p, uint32_t bytes) {
+    const uint64_t v = (uint64_t)p;
+    const uint64_t u = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32)) << 32) |
+                       (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
+    return __builtin_amdgcn_make_buffer_rsrc((void *)u, (short)0, (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
 }
-
-#define SPAD 132  // LDS row stride (floats) of pass-2 K / Q tiles and of S^T
-#define TSPAD 68  // LDS row stride of pass-2 T / A / Y^T / (b v)^T
 
 // Registers holding the next chunk while the current one computes.
 struct GdnPrefetch {
@@ -169,29 +202,14 @@ struct GdnPrefetch {
     float beta;          // threads 0..63
 };
 
-// 16 x 16 tile of A[16 x K] * B[K x 16] with both operands stored k-contiguous
-// (A row-major [m][k], B as B^T [n][k]): lane (m = l % 16, kq = l / 16)
-// covers k = kq * (K / 4) + u for MFMA u, so each lane reads a contiguous
-// run of K / 4 floats of both operands.
-template <int K, int LDA, int LDB>
-__device__ __forceinline__ gv4f tile_kk(const float *a, const float *bt, gv4f acc, uint32_t lane) {
-    const uint32_t m = lane & 15, kq = lane >> 4;
-    const float *ap = a + m * LDA + kq * (K / 4);
-    const float *bp = bt + m * LDB + kq * (K / 4);
-    // Four independent accumulation chains, summed at the end.
-    gv4f c1 = {0.0f, 0.0f, 0.0f, 0.0f}, c2 = c1, c3 = c1;
-#pragma unroll
-    for (int u = 0; u < K / 4; u += 4) {
-        const float4 av = *(const float4 *)(ap + u), bv = *(const float4 *)(bp + u);
-        acc = mfma4(av.x, bv.x, acc);
-        c1 = mfma4(av.y, bv.y, c1);
-        c2 = mfma4(av.z, bv.z, c2);
-        c3 = mfma4(av.w, bv.w, c3);
-    }
-    return (acc + c1) + (c2 + c3);
-}
-
-extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_scan_gfx950(GdnArgs a) {
+// VEC: key_dim and value_dim multiples of 4 and 16, token strides multiples
+// of 4 floats, q, k, v 16-byte aligned and a chunk's rows spanning under
+// 2 GB; the host launches the VEC instantiation exactly then. Its loads are
+// 16-byte buffer reads with no branches (the generic path's predicated reads
+// make the compiler wait for every outstanding load at each branch join,
+// which serialises the next chunk's prefetch).
+template <bool VEC>
+__device__ __forceinline__ void chunk_scan(const GdnArgs &a) {
     // k^ rows [s][i]; (g q^) rows [s][i]; T [s][r]; A [t][r]; S^T [n][i] (x2);
     // Y^T / D^T [n][s]; (b v)^T [n][s]; D [r][n] for the state update; K~^T [i][r].
     __shared__ __align__(16) float kh[GC * SPAD];
@@ -221,21 +239,27 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_scan_gfx950(Gdn
         const uint32_t i = e / GVS, n = e % GVS;
         st[0][n * SPAD + i] = (i < dk && j0 + n < dv) ? S[(size_t)i * dv + j0 + n] : 0.0f;
     }
-    const bool vec_k = (dk & 3) == 0 && (a.qk_stride & 3) == 0 && (((uintptr_t)a.k | (uintptr_t)a.q) & 15) == 0;
-    const bool vec_v = (dv & 3) == 0 && (a.v_stride & 3) == 0 && (j0 + GVS <= dv) && (((uintptr_t)a.v) & 15) == 0;
 
     auto fetch = [&](GdnPrefetch &p, uint32_t c) {
         const uint32_t t0 = c * a.chunk, n = min(a.chunk, a.tokens - t0);
         const float *base = a.norms + ((size_t)h * nch + c) * ctox_gdn_chunk_floats();
+        // Branch-free loads: one buffer over the chunk's rows of this key head
+        // (of this value slice); a lane past the chunk or past key_dim reads at
+        // the buffer's end, which the range check returns as zero.
+        const uint32_t kq_end = VEC ? ((n - 1) * a.qk_stride + dk) * 4 : 0;
+        const size_t kq0 = (size_t)t0 * a.qk_stride + (size_t)(h / a.rep) * dk;
+        const __amdgpu_buffer_rsrc_t rk = uniform_rsrc(a.k + kq0, kq_end);
+        const __amdgpu_buffer_rsrc_t rq = uniform_rsrc(a.q + kq0, kq_end);
 #pragma unroll
         for (int m = 0; m < 8; m++) {
             const uint32_t f = tid + 256 * m, s = f >> 5, i = (f & 31) * 4;
             const bool ok = s < n && i < dk;
-            const size_t off = (size_t)(t0 + (ok ? s : 0)) * a.qk_stride + (size_t)(h / a.rep) * dk + (ok ? i : 0);
-            if (vec_k) {
-                p.k[m] = ok ? *(const float4 *)(a.k + off) : make_float4(0, 0, 0, 0);
-                p.q[m] = ok ? *(const float4 *)(a.q + off) : make_float4(0, 0, 0, 0);
+            if (VEC) {
+                const uint32_t off = ok ? (s * a.qk_stride + i) * 4 : kq_end;
+                p.k[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+                p.q[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
             } else {
+                const size_t off = (size_t)(t0 + (ok ? s : 0)) * a.qk_stride + (size_t)(h / a.rep) * dk + (ok ? i : 0);
                 float kk4[4], qq4[4];
 #pragma unroll
                 for (int x = 0; x < 4; x++) {
@@ -255,10 +279,12 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_scan_gfx950(Gdn
         {
             const uint32_t s = tid >> 2, part = tid & 3;
             const bool ok = s < n;
-            const size_t off = (size_t)(t0 + (ok ? s : 0)) * a.v_stride + (size_t)h * dv + j0 + 4 * part;
-            if (vec_v) {
-                p.v = ok ? *(const float4 *)(a.v + off) : make_float4(0, 0, 0, 0);
+            if (VEC) {
+                const uint32_t v_end = ((n - 1) * a.v_stride + GVS) * 4;
+                const __amdgpu_buffer_rsrc_t rv = uniform_rsrc(a.v + (size_t)t0 * a.v_stride + (size_t)h * dv + j0, v_end);
+                p.v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rv, ok ? (s * a.v_stride + 4 * part) * 4 : v_end, 0, 0));
             } else {
+                const size_t off = (size_t)(t0 + (ok ? s : 0)) * a.v_stride + (size_t)h * dv + j0 + 4 * part;
                 float v4[4];
 #pragma unroll
                 for (int x = 0; x < 4; x++) v4[x] = (ok && j0 + 4 * part + x < dv) ? a.v[off + x] : 0.0f;
@@ -266,7 +292,11 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_scan_gfx950(Gdn
             }
         }
         p.aux = tid < 48 ? ((const float4 *)(base + 2 * GC * GC))[tid] : make_float4(0, 0, 0, 0);
-        p.beta = (tid < GC && tid < n) ? a.beta[(size_t)(t0 + tid) * a.heads + h] : 0.0f;
+        {
+            const uint32_t b_end = ((n - 1) * a.heads + 1) * 4;
+            const __amdgpu_buffer_rsrc_t rb = uniform_rsrc(a.beta + (size_t)t0 * a.heads + h, b_end);
+            p.beta = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, tid < n ? tid * a.heads * 4 : b_end, 0, 0));
+        }
     };
 
     GdnPrefetch pf;
@@ -321,8 +351,14 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_scan_gfx950(Gdn
         // D = T Y  (T rows [s][r] and Y^T [n][r] are both r-contiguous)
         gv4f dacc = tile_kk<GC, TSPAD, TSPAD>(tm + 16 * w * TSPAD, yt, (gv4f){0, 0, 0, 0}, lane);
         __syncthreads();
+        // D^T [n][s] into yt, and (D^T scaled by g_C / g_s) into vt, whose
+        // (b v)^T the Y step has consumed: the state update's left operand.
 #pragma unroll
-        for (int r = 0; r < 4; r++) yt[m16 * TSPAD + 16 * w + 4 * kq + r] = dacc[r];  // D^T [n][s]
+        for (int r = 0; r < 4; r++) {
+            const uint32_t s = 16 * w + 4 * kq + r;
+            yt[m16 * TSPAD + s] = dacc[r];
+            vt[m16 * TSPAD + s] = dacc[r] * ec[s];
+        }
         __syncthreads();
         // O = (g Q) S + A D
         {
@@ -335,8 +371,8 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_scan_gfx950(Gdn
             }
         }
         // S'^T[n][i] = g_C S^T[n][i] + sum_r D^T[n][r] exp(G_C - G_r) k^[r][i]
-        //   as a 16 x 16 tile per (n, i-block): A = D^T [n][r] (r-contiguous),
-        //   B = (K~)[r][i] read column-wise, scaled on the fly.
+        //   as a 16 x 16 tile per (n, i-block): A = the scaled D^T [n][r]
+        //   (r-contiguous), B = k^[r][i] read column-wise.
         {
             const float gC = G[GC - 1], decC = expf(gC);
             float *Sn = st[cur ^ 1];
@@ -346,13 +382,13 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_scan_gfx950(Gdn
                 gv4f acc;
 #pragma unroll
                 for (int r = 0; r < 4; r++) acc[r] = decC * Sc[(4 * kq + r) * SPAD + i0 + m16];
-                const float *ap = yt + m16 * TSPAD + kq * (GC / 4);
+                const float *ap = vt + m16 * TSPAD + kq * (GC / 4);
                 gv4f c1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int u = 0; u < GC / 4; u += 2) {
                     const uint32_t rr = kq * (GC / 4) + u;
-                    acc = mfma4(ap[u], kh[rr * SPAD + i0 + m16] * ec[rr], acc);
-                    c1 = mfma4(ap[u + 1], kh[(rr + 1) * SPAD + i0 + m16] * ec[rr + 1], c1);
+                    acc = mfma4(ap[u], kh[rr * SPAD + i0 + m16], acc);
+                    c1 = mfma4(ap[u + 1], kh[(rr + 1) * SPAD + i0 + m16], c1);
                 }
                 acc += c1;
                 // acc rows = n (4 kq + r), columns = i0 + m16
@@ -368,3 +404,6 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_scan_gfx950(Gdn
         if (i < dk && j0 + n < dv) S[(size_t)i * dv + j0 + n] = st[cur][n * SPAD + i];
     }
 }
+
+extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_scan_gfx950(GdnArgs a) { chunk_scan<false>(a); }
+extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_scan_vec_gfx950(GdnArgs a) { chunk_scan<true>(a); }

@@ -145,7 +145,7 @@ struct ctox_hip_backend {
     hipStream_t stream = nullptr;
     hipFunction_t prep = nullptr, q4_b1 = nullptr, q4_b4 = nullptr, q4_b8 = nullptr, q2_b1 = nullptr,
                   q2_b4 = nullptr, q2_b8 = nullptr, rec_row = nullptr, row_dot = nullptr,
-                  gdn_scan = nullptr, gdn_chunk_prep = nullptr, gdn_chunk_scan = nullptr, gates = nullptr,
+                  gdn_scan = nullptr, gdn_chunk_prep = nullptr, gdn_chunk_scan = nullptr, gdn_chunk_scan_vec = nullptr, gates = nullptr,
                   repeat = nullptr, partials = nullptr, argmax_final = nullptr, verify = nullptr, decide = nullptr,
                   pick_sums = nullptr, pick_final = nullptr, rms = nullptr, swiglu = nullptr, sgate = nullptr,
                   conv = nullptr, rope = nullptr, kv_pack = nullptr, attn_prep = nullptr, kv_demote = nullptr, gqa_part[2] = {}, gqa_part16[2] = {},
@@ -875,7 +875,8 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->q2_b8, "ctox_q2_matvec_b8_gfx950"},    {&b->rec_row, "ctox_recovered_row_gfx950"},
                {&b->row_dot, "ctox_row_dot_gfx950"},
                {&b->gdn_scan, "ctox_gdn_scan_gfx950"},    {&b->gdn_chunk_prep, "ctox_gdn_chunk_prep_gfx950"},
-               {&b->gdn_chunk_scan, "ctox_gdn_chunk_scan_gfx950"}, {&b->gates, "ctox_gdn_gates_gfx950"},
+               {&b->gdn_chunk_scan, "ctox_gdn_chunk_scan_gfx950"},
+               {&b->gdn_chunk_scan_vec, "ctox_gdn_chunk_scan_vec_gfx950"}, {&b->gates, "ctox_gdn_gates_gfx950"},
                {&b->repeat, "ctox_repeat_heads_gfx950"},   {&b->partials, "ctox_row_partials_gfx950"},
                {&b->argmax_final, "ctox_argmax_final_gfx950"}, {&b->verify, "ctox_verify_greedy_gfx950"},
                {&b->decide, "ctox_mtp_decide_gfx950"},     {&b->pick_sums, "ctox_pick_sums_gfx950"},
@@ -1738,8 +1739,13 @@ ctox_status gdn_device(ctox_hip_backend *b, const float *q, const float *k, cons
         if (st) return st;
         // 8 * ceil(heads / 8) * slices workgroups: the kernel maps them so
         // that all slices of a head run on one XCD (surplus ones exit).
-        return launch(b->gdn_chunk_scan, dim3((unsigned)(8 * ((heads + 7) / 8) * slices)), dim3(256), s, a,
-                      "ctox_gdn_chunk_scan_gfx950");
+        // The vector instantiation: 16-byte branch-free loads; it needs the
+        // shapes, strides and alignment below.
+        const bool vec = kd % 4 == 0 && vd % 16 == 0 && qk_stride % 4 == 0 && v_stride % 4 == 0 &&
+                         (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) & 15) == 0 && chunk * qk_stride < 0x1ffffff0u &&
+                         chunk * v_stride < 0x1ffffff0u;
+        return launch(vec ? b->gdn_chunk_scan_vec : b->gdn_chunk_scan, dim3((unsigned)(8 * ((heads + 7) / 8) * slices)),
+                      dim3(256), s, a, vec ? "ctox_gdn_chunk_scan_vec_gfx950" : "ctox_gdn_chunk_scan_gfx950");
     }
     return launch(b->gdn_scan, dim3((unsigned)(heads * slices)), dim3(256), s, a, "ctox_gdn_scan_gfx950");
 }
