@@ -30,6 +30,7 @@
 #include <hip/hip_runtime.h>
 
 #include "kernel_args.h"
+#include "lds_barrier.h"
 
 #define GC 64        // max chunk length
 #define GKD 128      // max key_dim of the chunked path
@@ -240,7 +241,8 @@ __device__ __forceinline__ void chunk_scan(const GdnArgs &a) {
         st[0][n * SPAD + i] = (i < dk && j0 + n < dv) ? S[(size_t)i * dv + j0 + n] : 0.0f;
     }
 
-    auto fetch = [&](GdnPrefetch &p, uint32_t c) {
+    // parts: 1 = k (with q on the generic path), 2 = q, 4 = T, A, v, aux, beta.
+    auto fetch = [&](GdnPrefetch &p, uint32_t c, const int parts) {
         const uint32_t t0 = c * a.chunk, n = min(a.chunk, a.tokens - t0);
         const float *base = a.norms + ((size_t)h * nch + c) * ctox_gdn_chunk_floats();
         // Branch-free loads: one buffer over the chunk's rows of this key head
@@ -256,9 +258,9 @@ __device__ __forceinline__ void chunk_scan(const GdnArgs &a) {
             const bool ok = s < n && i < dk;
             if (VEC) {
                 const uint32_t off = ok ? (s * a.qk_stride + i) * 4 : kq_end;
-                p.k[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
-                p.q[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
-            } else {
+                if (parts & 1) p.k[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+                if (parts & 2) p.q[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
+            } else if (parts & 1) {
                 const size_t off = (size_t)(t0 + (ok ? s : 0)) * a.qk_stride + (size_t)(h / a.rep) * dk + (ok ? i : 0);
                 float kk4[4], qq4[4];
 #pragma unroll
@@ -271,6 +273,7 @@ __device__ __forceinline__ void chunk_scan(const GdnArgs &a) {
                 p.q[m] = make_float4(qq4[0], qq4[1], qq4[2], qq4[3]);
             }
         }
+        if (!(parts & 4)) return;
 #pragma unroll
         for (int m = 0; m < 4; m++) {
             p.t[m] = ((const float4 *)base)[tid + 256 * m];
@@ -300,19 +303,19 @@ __device__ __forceinline__ void chunk_scan(const GdnArgs &a) {
     };
 
     GdnPrefetch pf;
-    fetch(pf, 0);
+    fetch(pf, 0, 7);
     uint32_t cur = 0;
     for (uint32_t c = 0; c < nch; c++) {
         const uint32_t t0 = c * a.chunk, n = min(a.chunk, a.tokens - t0);
-        __syncthreads();  // the previous chunk is done with every buffer
+        lds_barrier();  // the previous chunk is done with every buffer
         if (tid < 48) ((float4 *)(tid < 16 ? G : (tid < 32 ? kinv : qinv)))[tid & 15] = pf.aux;
         if (tid < GC) bt[tid] = pf.beta;
-        __syncthreads();
+        lds_barrier();
         if (tid < GC) {
             eg[tid] = expf(G[tid]);               // g_s
             ec[tid] = expf(G[GC - 1] - G[tid]);   // g_C / g_r
         }
-        __syncthreads();
+        lds_barrier();
         // Stage: k^ = k kinv; (g q^) = q qinv qscale exp(G); T; A; (b v)^T.
 #pragma unroll
         for (int m = 0; m < 8; m++) {
@@ -335,8 +338,13 @@ __device__ __forceinline__ void chunk_scan(const GdnArgs &a) {
             vt[(4 * part + 2) * TSPAD + s] = pf.v.z * b;
             vt[(4 * part + 3) * TSPAD + s] = pf.v.w * b;
         }
-        __syncthreads();
-        if (c + 1 < nch) fetch(pf, c + 1);  // lands while this chunk computes
+        lds_barrier();
+        // The next chunk's loads are issued in three groups between this
+        // chunk's products, so that their address traffic overlaps MFMA work;
+        // the loop's barriers order LDS only, so nothing waits for them before
+        // the next chunk's staging.
+        const bool more = c + 1 < nch;
+        if (more) fetch(pf, c + 1, 4);
         const float *Sc = st[cur];
         // Y^T[n][s] = (b v)^T - b_s g_s (K S)[s][n]   (wave w: rows s = 16w..16w+15)
         {
@@ -347,10 +355,11 @@ __device__ __forceinline__ void chunk_scan(const GdnArgs &a) {
                 yt[m16 * TSPAD + s] = vt[m16 * TSPAD + s] - bt[s] * eg[s] * acc[r];
             }
         }
-        __syncthreads();
+        if (more) fetch(pf, c + 1, 1);
+        lds_barrier();
         // D = T Y  (T rows [s][r] and Y^T [n][r] are both r-contiguous)
         gv4f dacc = tile_kk<GC, TSPAD, TSPAD>(tm + 16 * w * TSPAD, yt, (gv4f){0, 0, 0, 0}, lane);
-        __syncthreads();
+        lds_barrier();
         // D^T [n][s] into yt, and (D^T scaled by g_C / g_s) into vt, whose
         // (b v)^T the Y step has consumed: the state update's left operand.
 #pragma unroll
@@ -359,7 +368,8 @@ __device__ __forceinline__ void chunk_scan(const GdnArgs &a) {
             yt[m16 * TSPAD + s] = dacc[r];
             vt[m16 * TSPAD + s] = dacc[r] * ec[s];
         }
-        __syncthreads();
+        lds_barrier();
+        if (more) fetch(pf, c + 1, 2);
         // O = (g Q) S + A D
         {
             gv4f acc = tile_kk<GKD, SPAD, SPAD>(qh + 16 * w * SPAD, Sc, (gv4f){0, 0, 0, 0}, lane);
