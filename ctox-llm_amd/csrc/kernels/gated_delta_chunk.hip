@@ -84,7 +84,9 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_prep_gfx950(Gdn
     const uint32_t dk = a.key_dim;
     const float qscale = 1.0f / sqrtf((float)dk);
 
-    // Rows s < n: raw k, q; four threads per row accumulate the squares.
+    // Raw k, q rows into LDS (zeros beyond n rows and key_dim columns), four
+    // threads per row accumulating the squares. The tiles below use the raw
+    // rows and scale their products by the inverse norms.
     {
         const uint32_t s = tid >> 2, p = tid & 3;
         float sk = 0.0f, sq = 0.0f;
@@ -99,6 +101,10 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_prep_gfx950(Gdn
                 sk += kv * kv;
                 sq += qv * qv;
             }
+        }
+        for (uint32_t i = (s < n ? dk : 0) + p; i < GKD; i += 4) {
+            kh[s * SPAD + i] = 0.0f;
+            qh[s * SPAD + i] = 0.0f;
         }
         sk += __shfl_xor(sk, 1);
         sk += __shfl_xor(sk, 2);
@@ -121,14 +127,6 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_prep_gfx950(Gdn
             if (tid >= (uint32_t)o) g += up;
         }
         G[tid] = g;
-    }
-    __syncthreads();
-    // Normalise in place (zero rows beyond n and columns beyond dk).
-    for (uint32_t e = tid; e < GC * GKD; e += 256) {
-        const uint32_t s = e / GKD, i = e % GKD;
-        const bool ok = s < n && i < dk;
-        kh[s * SPAD + i] = ok ? kh[s * SPAD + i] * kinv_s[s] : 0.0f;
-        qh[s * SPAD + i] = ok ? qh[s * SPAD + i] * qinv_s[s] * qscale : 0.0f;
     }
     __syncthreads();
     // The lower 16 x 16 tiles of K K^T and Q K^T on MFMA: 10 tiles each,
@@ -154,7 +152,7 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_prep_gfx950(Gdn
 #pragma unroll
             for (int x = 0; x < 4; x++) {
                 const uint32_t s = 16 * sb + 4 * kq + x, r = 16 * rb + m16;
-                const float dec = expf(G[s] - G[r]);
+                const float dec = expf(G[s] - G[r]) * kinv_s[r] * (t < 10 ? kinv_s[s] : qinv_s[s] * qscale);
                 if (t < 10) mm[s * TPAD + r] = r < s ? dec * acc[u][x] : 0.0f;
                 else Aout[s * GC + r] = r <= s ? dec * acc[u][x] : 0.0f;
             }
@@ -167,6 +165,8 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_prep_gfx950(Gdn
     __syncthreads();
     float *base = a.norms + ((size_t)h * nch + c) * ctox_gdn_chunk_floats();
     // T = (I + diag(b) M)^{-1}: thread cc owns column cc; rows in order.
+    // (Splitting a column's dot products over four lanes measured no faster:
+    // the cross-lane adds lengthen each row step as much as they shorten it.)
     if (tid < GC) {
         const uint32_t cc = tid;
         float col[GC];
