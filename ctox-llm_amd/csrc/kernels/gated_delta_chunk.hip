@@ -19,7 +19,8 @@
 // Pass 1 (ctox_gdn_chunk_prep_gfx950, one workgroup per (head, chunk), all
 // chunks in parallel): norms, G, M and A from the lower 16 x 16 tiles of
 // K K^T and Q K^T on v_mfma_f32_16x16x4_f32, T by
-// forward substitution (one thread per column, the column in registers).
+// blocks: the four 16 x 16 diagonal blocks by forward substitution (a wave
+// each), the blocks below them on MFMA one block row at a time.
 // Pass 2 (ctox_gdn_chunk_scan_gfx950, one workgroup per (head, 16 value
 // columns), chunks in order): the 128 x 16 state slice stays in LDS across
 // chunks; the five small products per chunk run on v_mfma_f32_16x16x4_f32.
@@ -164,20 +165,62 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_prep_gfx950(Gdn
     }
     __syncthreads();
     float *base = a.norms + ((size_t)h * nch + c) * ctox_gdn_chunk_floats();
-    // T = (I + diag(b) M)^{-1}: thread cc owns column cc; rows in order.
-    // (Splitting a column's dot products over four lanes measured no faster:
-    // the cross-lane adds lengthen each row step as much as they shorten it.)
-    if (tid < GC) {
-        const uint32_t cc = tid;
-        float col[GC];
+    // T = (I + L)^{-1}, L = diag(b) M strictly lower, blockwise over 16 x 16
+    // blocks into LDS (tt, over the k rows, free after the tiles):
+    //   T_ii = (I + L_ii)^{-1}                   forward substitution, wave i;
+    //   T_ij = -T_ii sum_{k=j}^{i-1} L_ik T_kj   block row i after row i - 1,
+    //                                            task j on wave j, on MFMA.
+    float *tt = kh;
+    {
+        const uint32_t lane = tid & 63, w = tid >> 6, m16 = lane & 15, kq = lane >> 4;
+        if (lane < 16) {
+            const uint32_t cc = 16 * w + lane;
+            float col[16];
 #pragma unroll
-        for (int s = 0; s < GC; s++) {
-            float acc = 0.0f;
+            for (int s = 0; s < 16; s++) {
+                const uint32_t row = 16 * w + s;
+                float acc = 0.0f;
 #pragma unroll
-            for (int r = 0; r < s; r++) acc = fmaf(mm[s * TPAD + r], col[r], acc);
-            col[s] = ((uint32_t)s == cc ? 1.0f : 0.0f) - bt[s] * acc;
-            base[s * GC + cc] = col[s];
+                for (int r = 0; r < s; r++) acc = fmaf(mm[row * TPAD + 16 * w + r], col[r], acc);
+                col[s] = ((uint32_t)s == lane ? 1.0f : 0.0f) - bt[row] * acc;
+                tt[row * TPAD + cc] = col[s];
+            }
         }
+#pragma unroll
+        for (uint32_t bi = 1; bi < 4; bi++) {
+            __syncthreads();  // block row bi - 1 (and the diagonal) written
+            if (w < bi) {
+                const uint32_t bj = w;
+                // X = sum_k L_ik T_kj: A = L rows of block bi, B = T rows of block k.
+                gv4f x = {0.0f, 0.0f, 0.0f, 0.0f};
+                for (uint32_t bk = bj; bk < bi; bk++) {
+                    const float b = bt[16 * bi + m16];
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        const uint32_t kk = 16 * bk + 4 * u + kq;
+                        x = mfma4(b * mm[(16 * bi + m16) * TPAD + kk], tt[kk * TPAD + 16 * bj + m16], x);
+                    }
+                }
+                // T_ij = -T_ii X. Lane (kq, n) holds X rows 4 kq + u of column
+                // n, so MFMA u takes k = 4 kq + u: A reads T_ii[m][4 kq + u].
+                gv4f y = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    y = mfma4(tt[(16 * bi + m16) * TPAD + 16 * bi + 4 * kq + u], x[u], y);
+#pragma unroll
+                for (int u = 0; u < 4; u++) tt[(16 * bi + 4 * kq + u) * TPAD + 16 * bj + m16] = -y[u];
+            }
+        }
+        __syncthreads();
+        for (uint32_t e = tid; e < GC * GC / 4; e += 256) {
+            const uint32_t s = e / 16, r = (e % 16) * 4;
+            const bool up = r / 16 > s / 16;
+            *(float4 *)(base + s * GC + r) = up ? make_float4(0, 0, 0, 0)
+                                                : make_float4(tt[s * TPAD + r], tt[s * TPAD + r + 1],
+                                                              tt[s * TPAD + r + 2], tt[s * TPAD + r + 3]);
+        }
+    }
+    if (tid < GC) {
         base[2 * GC * GC + tid] = G[tid];
         base[2 * GC * GC + GC + tid] = kinv_s[tid];
         base[2 * GC * GC + 2 * GC + tid] = qinv_s[tid];
