@@ -69,8 +69,9 @@ __device__ __forceinline__ gv4f tile_kk(const float *a, const float *bt, gv4f ac
     return (acc + c1) + (c2 + c3);
 }
 
-// Scratch per (head, chunk): T[64][64], A[64][64], then G[64], kinv[64], qinv[64].
-__host__ __device__ constexpr uint32_t ctox_gdn_chunk_floats() { return 2 * GC * GC + 3 * GC; }
+// Scratch per (head, chunk): T[64][64], A[64][64], then per token g = exp(G),
+// exp(G_C - G), kinv and kinv's counterpart for q times 1/sqrt(key_dim) g.
+__host__ __device__ constexpr uint32_t ctox_gdn_chunk_floats() { return 2 * GC * GC + 4 * GC; }
 
 extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_prep_gfx950(GdnArgs a) {
     __shared__ __align__(16) float kh[GC * SPAD];
@@ -221,9 +222,11 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_chunk_prep_gfx950(Gdn
         }
     }
     if (tid < GC) {
-        base[2 * GC * GC + tid] = G[tid];
-        base[2 * GC * GC + GC + tid] = kinv_s[tid];
-        base[2 * GC * GC + 2 * GC + tid] = qinv_s[tid];
+        const float g = expf(G[tid]);
+        base[2 * GC * GC + tid] = g;
+        base[2 * GC * GC + GC + tid] = expf(G[GC - 1] - G[tid]);
+        base[2 * GC * GC + 2 * GC + tid] = kinv_s[tid];
+        base[2 * GC * GC + 3 * GC + tid] = qinv_s[tid] * qscale * g;
     }
 }
 
@@ -242,7 +245,7 @@ struct GdnPrefetch {
     float4 k[8], q[8];   // 64 x 128 each: float4 index tid + 256 m
     float4 t[4], am[4];  // T, A: 64 x 64 each
     float4 v;            // 64 x 16 value slice: row tid / 4, part tid % 4
-    float4 aux;          // G / kinv / qinv (threads 0..47), float4 tid % 16 of array tid / 16
+    float4 aux;          // g / g_C/g / kinv / q scale (threads 0..63), float4 tid % 16 of array tid / 16
     float beta;          // threads 0..63
 };
 
@@ -263,7 +266,7 @@ __device__ __forceinline__ void chunk_scan(const GdnArgs &a) {
     __shared__ __align__(16) float st[2][GVS * SPAD];
     __shared__ __align__(16) float yt[GVS * TSPAD];
     __shared__ __align__(16) float vt[GVS * TSPAD];
-    __shared__ float G[GC], kinv[GC], qinv[GC], bt[GC], eg[GC], ec[GC];
+    __shared__ float eg[GC], ec[GC], kinv[GC], qsc[GC], bt[GC];
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const uint32_t m16 = lane & 15, kq = lane >> 4;
     const uint32_t slices = (a.value_dim + GVS - 1) / GVS;
@@ -276,7 +279,6 @@ __device__ __forceinline__ void chunk_scan(const GdnArgs &a) {
     if (h >= a.heads) return;
     const uint32_t nch = (a.tokens + a.chunk - 1) / a.chunk;
     const uint32_t dk = a.key_dim, dv = a.value_dim;
-    const float qscale = 1.0f / sqrtf((float)dk);
     const size_t rowv = (size_t)a.heads * dv;
     float *S = a.state + (size_t)h * dk * dv;
     for (uint32_t e = tid; e < GKD * GVS; e += 256) {
@@ -337,7 +339,7 @@ __device__ __forceinline__ void chunk_scan(const GdnArgs &a) {
                 p.v = make_float4(v4[0], v4[1], v4[2], v4[3]);
             }
         }
-        p.aux = tid < 48 ? ((const float4 *)(base + 2 * GC * GC))[tid] : make_float4(0, 0, 0, 0);
+        p.aux = tid < 64 ? ((const float4 *)(base + 2 * GC * GC))[tid] : make_float4(0, 0, 0, 0);
         {
             const uint32_t b_end = ((n - 1) * a.heads + 1) * 4;
             const __amdgpu_buffer_rsrc_t rb = uniform_rsrc(a.beta + (size_t)t0 * a.heads + h, b_end);
@@ -351,19 +353,18 @@ __device__ __forceinline__ void chunk_scan(const GdnArgs &a) {
     for (uint32_t c = 0; c < nch; c++) {
         const uint32_t t0 = c * a.chunk, n = min(a.chunk, a.tokens - t0);
         lds_barrier();  // the previous chunk is done with every buffer
-        if (tid < 48) ((float4 *)(tid < 16 ? G : (tid < 32 ? kinv : qinv)))[tid & 15] = pf.aux;
-        if (tid < GC) bt[tid] = pf.beta;
-        lds_barrier();
         if (tid < GC) {
-            eg[tid] = expf(G[tid]);               // g_s
-            ec[tid] = expf(G[GC - 1] - G[tid]);   // g_C / g_r
+            float *aux = tid < 16 ? eg : (tid < 32 ? ec : (tid < 48 ? kinv : qsc));
+            ((float4 *)aux)[tid & 15] = pf.aux;
+            bt[tid] = pf.beta;
         }
         lds_barrier();
-        // Stage: k^ = k kinv; (g q^) = q qinv qscale exp(G); T; A; (b v)^T.
+        // Stage: k^ = k kinv; (g q^) = q qinv qscale exp(G) (one factor from
+        // the prep); T; A; (b v)^T.
 #pragma unroll
         for (int m = 0; m < 8; m++) {
             const uint32_t f = tid + 256 * m, s = f >> 5, i = (f & 31) * 4;
-            const float ks = kinv[s], qs = qinv[s] * qscale * eg[s];
+            const float ks = kinv[s], qs = qsc[s];
             *(float4 *)(kh + s * SPAD + i) = make_float4(pf.k[m].x * ks, pf.k[m].y * ks, pf.k[m].z * ks, pf.k[m].w * ks);
             *(float4 *)(qh + s * SPAD + i) = make_float4(pf.q[m].x * qs, pf.q[m].y * qs, pf.q[m].z * qs, pf.q[m].w * qs);
         }
@@ -427,7 +428,7 @@ __device__ __forceinline__ void chunk_scan(const GdnArgs &a) {
         //   as a 16 x 16 tile per (n, i-block): A = the scaled D^T [n][r]
         //   (r-contiguous), B = k^[r][i] read column-wise.
         {
-            const float gC = G[GC - 1], decC = expf(gC);
+            const float decC = eg[GC - 1];
             float *Sn = st[cur ^ 1];
 #pragma unroll
             for (int half = 0; half < 2; half++) {

@@ -1713,7 +1713,7 @@ ctox_status gdn_device(ctox_hip_backend *b, const float *q, const float *k, cons
     // 128 and chunks up to 64 tokens; otherwise the token-serial scan.
     const bool chunked = tokens > 1 && chunk >= 1 && chunk <= 64 && kd <= 128 && vd <= 128;
     const size_t nch = chunked ? (tokens + chunk - 1) / chunk : 0;
-    const size_t scratch = chunked ? heads * nch * (2 * 64 * 64 + 3 * 64) : 1;
+    const size_t scratch = chunked ? heads * nch * (2 * 64 * 64 + 4 * 64) : 1;
     st = ensure(b, b->norms, scratch * sizeof(float), false);
     if (st) return st;
     GdnArgs a{};
