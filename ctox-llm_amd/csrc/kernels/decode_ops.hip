@@ -171,10 +171,11 @@ __device__ __forceinline__ void merge_stats(const float *p, uint32_t parts, floa
     for (int off = 32; off > 0; off >>= 1) z += __shfl_xor(z, off);
 }
 
-// grid rows, 64 threads: merges the mode-0 partials of `drafts` rows.
+// grid rows, 64 threads: merges the mode-0 partials of `drafts` rows; with
+// `ids` the winning index is mapped to its token (a restricted draft row).
 extern "C" __global__ __launch_bounds__(64) void ctox_argmax_final_gfx950(VerifyArgs a) {
     const uint32_t t = merge_argmax(a.partials + (size_t)blockIdx.x * a.parts * 2, a.parts);
-    if (threadIdx.x == 0) a.out[blockIdx.x] = t;
+    if (threadIdx.x == 0) a.out[blockIdx.x] = a.ids ? a.ids[t] : t;
 }
 
 // From the mode-0 partials of the draft, target and bonus rows.
@@ -201,6 +202,20 @@ extern "C" __global__ __launch_bounds__(64) void ctox_verify_greedy_gfx950(Verif
         a.out[0] = bonus;
         a.out[1] = a.drafts;
         a.out[2] = nacc;
+    }
+}
+
+// One wave: the greedy sampler's status words from the finite-check flags
+// of its logits (status 2 on a non-finite logit, Q/src/sampler.rs:66-70,
+// which the crate checks before its greedy branch).
+extern "C" __global__ __launch_bounds__(64) void ctox_greedy_status_gfx950(FlagStatusArgs a) {
+    uint32_t bad = 0;
+    for (uint32_t i = threadIdx.x; i < a.parts; i += 64) bad |= a.flags[i];
+    bad = __any(bad != 0);
+    if (threadIdx.x == 0) {
+        a.out[1] = bad ? 2u : 0u;
+        a.out[2] = bad ? 0u : 1u;
+        a.out[3] = 0u;
     }
 }
 

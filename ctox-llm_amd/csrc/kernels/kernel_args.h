@@ -378,6 +378,7 @@ struct VerifyArgs {
     uint32_t *out;           // [3 + drafts]: next, verified, accepted count, accepted tokens
     uint32_t drafts;
     uint32_t parts;
+    const uint32_t *ids;     // argmax_final: row index -> token map (restricted draft rows), or null
 };
 
 struct AcceptArgs {
@@ -601,6 +602,12 @@ struct FiniteArgs {          // ctox_finite_check_gfx950
     const float *x;
     uint32_t *flags;         // [gridDim.x]: 1 if a value of the workgroup's range is not finite, else 0
     uint64_t n;
+};
+
+struct FlagStatusArgs {      // ctox_greedy_status_gfx950
+    const uint32_t *flags;   // ctox_finite_check_gfx950 output
+    uint32_t *out;           // the sampler's d_out: [1] status, [2] nucleus length, [3] total
+    uint32_t parts;
 };
 
 struct StreamReadArgs {      // ctox_stream_read_gfx950

@@ -146,7 +146,7 @@ struct ctox_hip_backend {
     hipFunction_t prep = nullptr, q4_b1 = nullptr, q4_b4 = nullptr, q4_b8 = nullptr, q2_b1 = nullptr,
                   q2_b4 = nullptr, q2_b8 = nullptr, rec_row = nullptr, row_dot = nullptr,
                   gdn_scan = nullptr, gdn_chunk_prep = nullptr, gdn_chunk_scan = nullptr, gdn_chunk_scan_vec = nullptr, gates = nullptr,
-                  repeat = nullptr, partials = nullptr, argmax_final = nullptr, verify = nullptr, decide = nullptr,
+                  repeat = nullptr, partials = nullptr, argmax_final = nullptr, greedy_status = nullptr, verify = nullptr, decide = nullptr,
                   pick_sums = nullptr, pick_final = nullptr, rms = nullptr, swiglu = nullptr, sgate = nullptr,
                   conv = nullptr, rope = nullptr, kv_pack = nullptr, attn_prep = nullptr, kv_demote = nullptr, gqa_part[2] = {}, gqa_part16[2] = {},
                   gqa_combine = nullptr, fill = nullptr, embed = nullptr, norm_rows = nullptr, attn_gate = nullptr,
@@ -878,7 +878,7 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->gdn_chunk_scan, "ctox_gdn_chunk_scan_gfx950"},
                {&b->gdn_chunk_scan_vec, "ctox_gdn_chunk_scan_vec_gfx950"}, {&b->gates, "ctox_gdn_gates_gfx950"},
                {&b->repeat, "ctox_repeat_heads_gfx950"},   {&b->partials, "ctox_row_partials_gfx950"},
-               {&b->argmax_final, "ctox_argmax_final_gfx950"}, {&b->verify, "ctox_verify_greedy_gfx950"},
+               {&b->argmax_final, "ctox_argmax_final_gfx950"}, {&b->greedy_status, "ctox_greedy_status_gfx950"}, {&b->verify, "ctox_verify_greedy_gfx950"},
                {&b->decide, "ctox_mtp_decide_gfx950"},     {&b->pick_sums, "ctox_pick_sums_gfx950"},
                {&b->pick_final, "ctox_pick_final_gfx950"},  {&b->rms, "ctox_rms_norm_gfx950"},
                {&b->swiglu, "ctox_swiglu_gfx950"},         {&b->sgate, "ctox_sigmoid_gate_gfx950"},
@@ -1988,6 +1988,11 @@ uint32_t row_parts(size_t vocab) { return (uint32_t)std::min<size_t>(64, std::ma
 
 extern "C" ctox_status ctox_hip_greedy_tokens_device(ctox_hip_backend *b, const float *d_logits, size_t rows,
                                                      size_t vocab, uint32_t *d_tokens, void *stream) {
+    return ctox_greedy_tokens_mapped(b, d_logits, rows, vocab, nullptr, d_tokens, stream);
+}
+
+ctox_status ctox_greedy_tokens_mapped(ctox_hip_backend *b, const float *d_logits, size_t rows, size_t vocab,
+                                      const uint32_t *d_ids, uint32_t *d_tokens, void *stream) {
     if (!b || !d_logits || !d_tokens) return fail(CTOX_ERR_SHAPE, "null argument");
     if (vocab == 0) return fail(CTOX_ERR_INVALID_ARTIFACT, "cannot select a token from empty logits");
     if (rows == 0 || rows > 65535 || vocab > 0xffffffffu) return fail(CTOX_ERR_SHAPE, "logits shape");
@@ -1998,7 +2003,7 @@ extern "C" ctox_status ctox_hip_greedy_tokens_device(ctox_hip_backend *b, const 
     PartialArgs p{d_logits, d_logits, d_logits, (float *)b->tok.ptr, (uint32_t)rows, (uint32_t)vocab, parts, 0, 1.0f,
                   (uint32_t)vocab};
     if ((st = launch(b->partials, dim3((unsigned)rows, parts), dim3(256), s, p, "ctox_row_partials_gfx950"))) return st;
-    VerifyArgs v{(const float *)b->tok.ptr, d_tokens, (uint32_t)rows, parts};
+    VerifyArgs v{(const float *)b->tok.ptr, d_tokens, (uint32_t)rows, parts, d_ids};
     return launch(b->argmax_final, dim3((unsigned)rows), dim3(64), s, v, "ctox_argmax_final_gfx950");
 }
 
@@ -2089,10 +2094,18 @@ extern "C" ctox_status ctox_hip_sample_topk_topp_device(ctox_hip_backend *b, con
         return fail(CTOX_ERR_INVALID_ARTIFACT, "sampler temperature or top_p is invalid");
     hipStream_t s = pick_stream(b, stream);
     if (temperature == 0.0f) {  // greedy: the later token wins ties (sampler.rs:76-82)
+        if ((uintptr_t)d_logits % 16) return fail(CTOX_ERR_SHAPE, "greedy sampling needs 16-byte aligned logits");
         ctox_status st = ctox_hip_greedy_tokens_device(b, d_logits, 1, vocab, d_out, s);
         if (st) return st;
-        const uint32_t zeros[3] = {0, 1, 0};
-        return ctox_hip_write_words_device(b, d_out + 1, zeros, 3, s);
+        // Non-finite logits are refused before the greedy branch (sampler.rs:66-70):
+        // finite flags of 64 ranges, then the status words.
+        constexpr uint32_t kParts = 64;
+        if ((st = ensure(b, b->stats, kParts * sizeof(uint32_t), false))) return st;
+        uint32_t *flags = (uint32_t *)b->stats.ptr;
+        FiniteArgs fa{d_logits, flags, (uint64_t)vocab};
+        if ((st = launch(b->finite, dim3(kParts), dim3(256), s, fa, "ctox_finite_check_gfx950"))) return st;
+        FlagStatusArgs ga{flags, d_out, kParts};
+        return launch(b->greedy_status, dim3(1), dim3(64), s, ga, "ctox_greedy_status_gfx950");
     }
     const float invt = 1.0f / temperature;
     if (!std::isfinite(invt)) return fail(CTOX_ERR_INVALID_ARTIFACT, "sampler inverse temperature must be finite");

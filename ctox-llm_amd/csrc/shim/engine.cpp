@@ -124,7 +124,7 @@ struct ctox_hip_engine {
     // Host copy of the step result / flags. Ordinary (pageable) memory: the
     // runtime then copies these few words with a blit kernel on the stream,
     // which measured faster per step than a copy into pinned memory.
-    uint32_t h_res[128] = {};
+    uint32_t h_res[256] = {};
     // MTP
     bool mtp = false;
     float *mtp_norm_emb = nullptr, *mtp_norm_hid = nullptr, *mtp_norm = nullptr;
@@ -633,8 +633,8 @@ ctox_status demote_all(ctox_hip_engine *e) {
 
 // Queues the finite check of `n` logits into flag words [0, kFlagParts).
 constexpr uint32_t kFlagParts = 64;
-ctox_status check_logits(ctox_hip_engine *e, const float *x, size_t n) {
-    return ctox_hip_check_finite_device(e->b, x, n, e->d_flags, kFlagParts, e->s);
+ctox_status check_logits(ctox_hip_engine *e, const float *x, size_t n, uint32_t flag0 = 0) {
+    return ctox_hip_check_finite_device(e->b, x, n, e->d_flags + flag0, kFlagParts, e->s);
 }
 
 // After the step's synchronization: fail closed on a flagged buffer
@@ -782,7 +782,7 @@ extern "C" ctox_status ctox_hip_engine_create_with_dtypes(ctox_hip_backend *b, c
         (st = dalloc_t(e, &e->draft_logits, (size_t)std::max(1u, c.draft_tokens) * e->V)) ||
         (st = dalloc_t(e, &e->mtp_hidden, R * e->H)) || (st = dalloc_t(e, &e->prev_hidden, R * e->H)) ||
         (st = dalloc_t(e, &e->d_tokens, 16)) || (st = dalloc_t(e, &e->d_result, 32)) || (st = dalloc_t(e, &e->d_rng, 1)) ||
-        (st = dalloc_t(e, &e->rsq, 8 * 512)) || (st = dalloc_t(e, &e->blk_sq, 8 * 128)) || (st = dalloc_t(e, &e->d_flags, 64)))
+        (st = dalloc_t(e, &e->rsq, 8 * 512)) || (st = dalloc_t(e, &e->blk_sq, 8 * 128)) || (st = dalloc_t(e, &e->d_flags, 2 * kFlagParts + 32)))
         return cleanup(st);
     e->d_drafts = e->d_result + 16;
     if ((st = sync(e))) return cleanup(st);
@@ -840,9 +840,17 @@ extern "C" ctox_status ctox_hip_engine_decode(ctox_hip_engine *e, uint32_t token
 // One speculative step: k drafts sampled at `temperature`, one batched target
 // pass over [token, d1..dk], acceptance and commit. out[0] = next token,
 // out[1] = accepted drafts n, out[2..2+n) = the accepted drafts.
+// Temperature 0 is the crate's greedy MTP (Q/src/engine.rs:583-590,
+// 915-963): drafts are argmax tokens (over the draft vocabulary when one is
+// bound), the verification accepts the longest prefix equal to the target
+// argmax tokens, and the next token is the first differing target argmax or,
+// with every draft accepted, the bonus row's argmax.
 extern "C" ctox_status ctox_hip_engine_mtp_step(ctox_hip_engine *e, uint32_t token, float temperature,
                                                 uint32_t *out) {
     if (!e || !out) return efail(CTOX_ERR_SHAPE, "null argument");
+    if (!std::isfinite(temperature) || temperature < 0.0f)
+        return efail(CTOX_ERR_INVALID_ARTIFACT, "sampling temperature must be finite and non-negative");
+    const bool greedy = temperature == 0.0f;
     if (!e->mtp) return efail(CTOX_ERR_UNSUPPORTED_OPERATION, "engine was created without an MTP head");
     if (e->loading) return efail(CTOX_ERR_INVALID_STATE, "weights written without ctox_hip_engine_finish_load");
     if (!e->have_prev) return efail(CTOX_ERR_INVALID_STATE, "MTP step needs a previous target step");
@@ -858,6 +866,13 @@ extern "C" ctox_status ctox_hip_engine_mtp_step(ctox_hip_engine *e, uint32_t tok
     for (uint32_t i = 0; i < k; i++) {
         TRY(mtp_forward(e, e->d_drafts + i, i == 0 ? e->prev_hidden : e->mtp_hidden, 1, p + i,
                         e->draft_logits + (size_t)i * dn, true));
+        if (greedy) {
+            // The draft row's argmax (DraftDistribution::greedy_token: the
+            // later index wins ties; a restricted index maps to its token).
+            TRY(ctox_greedy_tokens_mapped(e->b, e->draft_logits + (size_t)i * dn, 1, dn,
+                                          e->draft_n ? e->d_draft_ids : nullptr, e->d_drafts + i + 1, e->s));
+            continue;
+        }
         // drafts = 0 samples the bonus row: the draft token from its own
         // softmax (a restricted row's index mapped to its token).
         TRY(ctox_hip_mtp_accept_restricted_device(e->b, nullptr, dn, nullptr, nullptr, e->draft_logits + (size_t)i * dn,
@@ -866,15 +881,43 @@ extern "C" ctox_status ctox_hip_engine_mtp_step(ctox_hip_engine *e, uint32_t tok
     }
     // Verify [token, d1..dk] in one pass; every row's GatedDeltaNet state is kept.
     TRY(target_forward(e, e->d_drafts, R, true));
-    TRY(ctox_hip_mtp_accept_restricted_device(e->b, e->draft_logits, dn, e->draft_n ? e->d_draft_inv : nullptr,
-                                              e->logits, e->logits + (size_t)k * e->V, nullptr, e->d_drafts + 1, k,
-                                              e->V, temperature, e->d_rng, e->d_result, e->s));
-    TRY(read_result(e, e->d_result, 16 + R));
+    uint32_t next = 0, n = 0;
     const uint32_t *host = e->h_res;
-    // The acceptance reports non-finite draft or target logits as 0xfffffffe;
-    // nothing is committed from such a step.
-    if (host[0] == 0xfffffffeu) return efail(CTOX_ERR_INVALID_STATE, "non-finite logits in the speculative step");
-    const uint32_t next = host[0], n = host[1];
+    if (greedy) {
+        // One read brings back the finite flags of the target and draft
+        // logits (words [0, 2 * kFlagParts)), the target argmax of every row
+        // (16 words from 2 * kFlagParts) and [token, d1..dk] (the 16 after).
+        uint32_t *d_tail = e->d_flags + 2 * kFlagParts;
+        TRY(check_logits(e, e->logits, (size_t)R * e->V));
+        TRY(check_logits(e, e->draft_logits, (size_t)k * dn, kFlagParts));
+        TRY(ctox_hip_greedy_tokens_device(e->b, e->logits, R, e->V, d_tail, e->s));
+        TRY(copy_d2d(e, d_tail + 16, e->d_drafts, (size_t)R * 4));
+        TRY(read_result(e, e->d_flags, 2 * kFlagParts + 16 + R));
+        uint32_t flagged = 0;
+        for (uint32_t i = 0; i < 2 * kFlagParts; i++) flagged |= host[i];
+        if (flagged) return efail(CTOX_ERR_INVALID_STATE, "non-finite logits in the speculative step");
+        const uint32_t *targets = host + 2 * kFlagParts, *drafts = targets + 16;
+        next = targets[k];
+        n = k;
+        for (uint32_t i = 0; i < k; i++)
+            if (drafts[1 + i] != targets[i]) {
+                next = targets[i];
+                n = i;
+                break;
+            }
+        // The commit below reads the accepted drafts at host[17 + i].
+        std::memmove(e->h_res + 16, drafts, (size_t)R * sizeof(uint32_t));
+    } else {
+        TRY(ctox_hip_mtp_accept_restricted_device(e->b, e->draft_logits, dn, e->draft_n ? e->d_draft_inv : nullptr,
+                                                  e->logits, e->logits + (size_t)k * e->V, nullptr, e->d_drafts + 1, k,
+                                                  e->V, temperature, e->d_rng, e->d_result, e->s));
+        TRY(read_result(e, e->d_result, 16 + R));
+        // The acceptance reports non-finite draft or target logits as 0xfffffffe;
+        // nothing is committed from such a step.
+        if (host[0] == 0xfffffffeu) return efail(CTOX_ERR_INVALID_STATE, "non-finite logits in the speculative step");
+        next = host[0];
+        n = host[1];
+    }
     if (n > k || next >= e->V) return efail(CTOX_ERR_INVALID_STATE, "acceptance produced an invalid result");
     // Commit n + 1 target tokens: the state after row n, the caches truncated.
     e->bank ^= 1u;

@@ -3,14 +3,17 @@
 //
 // The tiled matvec's cross-chunk combine needs slots for the chunks'
 // partial sums. ctox_hip_launch_fused_matvec takes them from a per-backend
-// buffer it grows with hipMalloc; callers that cannot allocate (HIP graph
-// capture, serving loops, harnesses that forbid it) use this file-scope
+// buffer it grows with hipMalloc; callers that cannot allocate (serving
+// loops, harnesses that forbid it) use this file-scope
 // array instead, one copy per GPU, held until the process ends. Its address
 // on each device is taken once with hipGetSymbolAddress at backend creation
 // (ctox_noalloc_setup, called with that device current) and only that
 // address is used from the host afterwards. The slots are tagged with a
 // per-device launch number (never 0); the array starts cleared, and is
-// cleared again by a fill kernel when the number wraps.
+// cleared again by a fill kernel when the number wraps. The launch number is
+// a kernel argument, so a launch captured into a HIP graph would replay with
+// the same tag and could read the previous replay's slots: the entry point
+// is not meant for capture.
 #include <hip/hip_runtime.h>
 
 #include <cstddef>

@@ -30,6 +30,12 @@ ctox_status ctox_norm_matvec_prestaged(ctox_hip_backend *b, int32_t dtype, const
                                        uint32_t batch, const float *sq, float eps, uint32_t max_parts, uint32_t *parts,
                                        void *stream);
 
+// ctox_hip_greedy_tokens_device whose row argmax index i is written as
+// d_ids[i] (a restricted draft row's index mapped to its token) when d_ids
+// is not null.
+ctox_status ctox_greedy_tokens_mapped(ctox_hip_backend *b, const float *d_logits, size_t rows, size_t vocab,
+                                      const uint32_t *d_ids, uint32_t *d_tokens, void *stream);
+
 // Writes n host word ranges (src[i], count[i] words) to device addresses
 // dst[i] with as few launches as the argument block allows (one for the
 // engine's per-step descriptor uploads).

@@ -197,10 +197,16 @@ ctox_status ctox_hip_launch_fused_matvec(ctox_hip_backend *backend, int32_t dtyp
 
 /* Allocation-free variant of ctox_hip_launch_fused_matvec. NO COUNTERPART
  * IN THE REFERENCE: it is for callers that cannot allocate device memory
- * (code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc). Same arguments and results; the weights must have a tiled
- * copy (ctox_hip_register_tiled_weights, else CTOX_ERR_UNSUPPORTED_OPERATION)
- * and batch is 1..5. The cross-chunk combine slots come from a static device
+ * (tight serving loops, harnesses that forbid hipMalloc). It must not be
+ * captured into a HIP graph that is replayed: each launch tags its combine
+ * slots with a number passed as a kernel argument, which a replay repeats.
+ * Same arguments; the weights must have a tiled copy
+ * (ctox_hip_register_tiled_weights, else CTOX_ERR_UNSUPPORTED_OPERATION) and
+ * batch is 1..5. Results equal the allocating launch's, except for Q4
+ * matrices of more than 8 Mi weights at 2..5 rows: there the allocating
+ * launch stages 21-bit activation fragments and this one builds 22-bit
+ * fragments in the kernel, so the two differ in the last bits (about 2^-21
+ * relative). The cross-chunk combine slots come from a static device
  * array of CTOX_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends),
  * not from the backend's grown buffer; a matrix whose slots do not fit,
  * (chunks - 1) * batch * 16 * ceil(rows / 16) * 8 bytes with
@@ -702,6 +708,13 @@ ctox_status ctox_hip_engine_set_rng(ctox_hip_engine *engine, uint64_t state);
 ctox_status ctox_hip_engine_decode(ctox_hip_engine *engine, uint32_t token, const float **d_logits);
 /* One speculative step at `temperature`: out[0] next token, out[1] accepted
  * drafts n, out[2 .. 2 + n) the accepted drafts (out holds >= 2 + k words).
+ * Temperature 0 is the crate's greedy MTP (Q/src/engine.rs:583-590, 915-963;
+ * argmax drafts, Q/src/decoder.rs:1311-1329): the longest draft prefix equal
+ * to the target argmax tokens is accepted, then the first differing target
+ * token or the bonus row's argmax; temperature > 0 is rejection sampling
+ * with the engine's Pcg32 stream. Non-finite logits: CTOX_ERR_INVALID_STATE,
+ * nothing committed; a negative or non-finite temperature:
+ * CTOX_ERR_INVALID_ARTIFACT.
  * The commit's device work (MTP cache replay, descriptor uploads) may still
  * run on the engine stream when the call returns; every later engine call
  * and every read of engine memory through that stream (or the legacy null

@@ -51,6 +51,17 @@ def check_draft_ids(ids, vocab: int) -> np.ndarray:
     return ids.astype(np.uint32)
 
 
+def verify_greedy_tokens(drafts, targets):
+    """verify_greedy_mtp's compact branch (Q/src/engine.rs:928-943): drafts
+    d_1..d_k against the target argmax tokens t_0..t_k; returns (next token,
+    accepted count): the first i with d_{i+1} != t_i gives (t_i, i), no
+    mismatch gives the bonus token (t_k, k)."""
+    for i, d in enumerate(drafts):
+        if d != targets[i]:
+            return targets[i], i
+    return targets[len(drafts)], len(drafts)
+
+
 class OracleDecoder:
     def __init__(self, cfg: dict, tensor, draft_ids=None):
         """cfg: EngineConfig.as_dict(); tensor(name) -> the engine tensor dict;
@@ -155,6 +166,12 @@ class OracleDecoder:
 
     def gdn(self, l, x):
         """linear_attention_residual (Q/src/decoder.rs:806-938) minus the residual."""
+        return self.matvec(f"L{l}.out", self.gdn_core(l, x))
+
+    def gdn_core(self, l, x):
+        """The GatedDeltaNet mixer up to out_proj's input (decoder.rs:822-927):
+        in-projection split [qkv | z | a | b], conv + SiLU, key-head repeat,
+        gates, one delta step, gated RMS norm."""
         p = f"L{l}"
         out = self.matvec(f"{p}.in", x)
         mixed, z = out[:self.C], out[self.C:self.C + self.Vw]
@@ -166,8 +183,7 @@ class OracleDecoder:
         k = orc.repeat_heads(conv[self.Kw:2 * self.Kw], self.hk, self.dk, rep)
         ld, beta = orc.gdn_gates(a, b, self.w(f"{p}.a_log")["data"], self.w(f"{p}.dt_bias")["data"])
         core = orc.gated_delta_step(q, k, conv[2 * self.Kw:], ld, beta, self.gdn_state[l], self.hv, self.dk, self.dv)
-        core = orc.rms_norm_gated(core, z, self.hv, self.dv, self.w(f"{p}.gnorm")["data"], self.eps)
-        return self.matvec(f"{p}.out", core)
+        return orc.rms_norm_gated(core, z, self.hv, self.dv, self.w(f"{p}.gnorm")["data"], self.eps)
 
     def mlp(self, prefix, h):
         """decoder_mlp_residual (Q/src/decoder.rs:636-670)."""
@@ -206,14 +222,19 @@ class OracleDecoder:
             raise orc.OracleError(1)
         return h + self.attention(prefix, self.norm(h, f"{prefix}.norm"), position, cache, False)
 
+    def mtp_fc(self, token, prev):
+        """The MTP head's input projection (Q/src/decoder.rs:1027-1036): fc over
+        [norm_emb(embedding(token)), norm_hid(prev)], in that order."""
+        e = self.norm(self.embedding(token), "mtp.norm_emb")
+        hn = self.norm(prev, "mtp.norm_hid")
+        return self.matvec("mtp.fc", np.concatenate([e, hn]))
+
     def mtp(self, token, prev, rope_pos, retain, logits=True):
         """mtp_final_hidden (Q/src/decoder.rs:1009-1046) (+ the shared LM head,
         restricted to the draft vocabulary when one is bound)."""
         if rope_pos != self.mtp_cache.tokens() + 1:  # decoder.rs:1017-1024
             raise orc.OracleError(1)
-        e = self.norm(self.embedding(token), "mtp.norm_emb")
-        hn = self.norm(prev, "mtp.norm_hid")
-        h = self.matvec("mtp.fc", np.concatenate([e, hn]))
+        h = self.mtp_fc(token, prev)
         x = self.norm(h, "mtp.attn_norm")
         h = self.mlp("mtp", h + self.attention("mtp", x, rope_pos, self.mtp_cache, retain))
         fin = self.norm(h, "mtp.norm")
@@ -237,7 +258,12 @@ class OracleDecoder:
 
     def mtp_step(self, token, temperature, rng: orc.Pcg32, drafts: int):
         """The speculative step described in the module docstring:
-        returns (next token, accepted drafts)."""
+        returns (next token, accepted drafts). Temperature 0 is the crate's
+        greedy MTP (Q/src/engine.rs:583-590, 915-963): each draft is the
+        argmax of its draft row (a restricted row's index mapped to its
+        token, decoder.rs:1311-1329), and verify_greedy_mtp accepts the
+        longest prefix equal to the target argmax tokens."""
+        greedy = temperature == 0.0
         p = self.position
         xs, g = [token], self.prev_hidden
         draft_logits = []
@@ -247,8 +273,13 @@ class OracleDecoder:
             if i == 0:
                 mtp_after_first = copy.deepcopy(self.mtp_cache)
             draft_logits.append(lg)
-            empty = np.zeros((0, lg.size), np.float32)
-            d, _ = orc.mtp_accept_sample(empty, empty, lg, np.zeros(0, np.uint32), temperature, rng)
+            if not np.all(np.isfinite(lg)):
+                raise orc.OracleError(8)  # InvalidState, fail closed (cuda_runtime.rs:10627-10632)
+            if greedy:
+                d = orc.greedy_token(lg)
+            else:
+                empty = np.zeros((0, lg.size), np.float32)
+                d, _ = orc.mtp_accept_sample(empty, empty, lg, np.zeros(0, np.uint32), temperature, rng)
             xs.append(int(self.draft_ids[d]) if self.draft_ids is not None else d)
         saved = (copy.deepcopy(self.gdn_state), copy.deepcopy(self.conv_state), copy.deepcopy(self.caches),
                  self.position)
@@ -257,8 +288,17 @@ class OracleDecoder:
             lg, fin = self.target_step(x, retain=True)
             target.append(lg)
             hiddens.append(fin)
-        nxt, n = orc.mtp_accept_sample(np.stack(draft_logits), np.stack(target[:drafts]), target[drafts],
-                                       np.array(xs[1:], np.uint32), temperature, rng, draft_ids=self.draft_ids)
+        if greedy:
+            if not all(np.all(np.isfinite(t)) for t in target):
+                raise orc.OracleError(8)
+            # verify_greedy_mtp (engine.rs:915-963) on draft tokens: the
+            # compact branch (:928-943), since a restricted draft row has no
+            # full-vocabulary argmax of its own.
+            nxt, n = verify_greedy_tokens(xs[1:], [orc.greedy_token(t) for t in target])
+        else:
+            nxt, n = orc.mtp_accept_sample(np.stack(draft_logits), np.stack(target[:drafts]), target[drafts],
+                                           np.array(xs[1:], np.uint32), temperature, rng,
+                                           draft_ids=self.draft_ids)
         # commit n + 1 target tokens
         self.gdn_state, self.conv_state, self.caches, self.position = saved
         for x in xs[:n + 1]:

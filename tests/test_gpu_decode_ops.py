@@ -292,6 +292,22 @@ def test_sample_topk_topp_fails_closed(hip):
                                                 out.data_ptr(), None) == 0
     torch.cuda.synchronize()
     assert out.cpu().numpy().view(np.uint32)[1] == 2
+    # Greedy (T = 0) refuses non-finite logits too (sampler.rs:66-70 runs
+    # before the greedy branch), and reports a finite row as ok.
+    for bad in (np.nan, np.inf, -np.inf):
+        logits[1234] = bad
+        d = torch.from_numpy(logits).cuda()
+        assert lib.ctox_hip_sample_topk_topp_device(hip.handle, d.data_ptr(), 5000, 0.0, 40, 0.95, 0.5,
+                                                    out.data_ptr(), None) == 0
+        torch.cuda.synchronize()
+        assert out.cpu().numpy().view(np.uint32)[1] == 2, bad
+    logits[1234] = 0.0
+    d = torch.from_numpy(logits).cuda()
+    assert lib.ctox_hip_sample_topk_topp_device(hip.handle, d.data_ptr(), 5000, 0.0, 40, 0.95, 0.5,
+                                                out.data_ptr(), None) == 0
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint32)
+    assert got[1] == 0 and got[2] == 1 and int(got[0]) == int(np.argmax(logits))
     for args in ((0.8, 0, 0.95, 0.5), (0.8, 257, 0.95, 0.5)):
         assert lib.ctox_hip_sample_topk_topp_device(hip.handle, d.data_ptr(), 5000, *args, out.data_ptr(), None) == 5
     for args in ((0.8, 40, 0.95, 1.0), (0.8, 40, 0.0, 0.5), (-1.0, 40, 0.95, 0.5)):

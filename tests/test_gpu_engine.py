@@ -217,3 +217,90 @@ def test_engine_fails_closed_on_nonfinite_logits(hip):
             eng.decode(4)
     finally:
         eng.close()
+
+
+def _write_vec(eng, ref, name, values):
+    """Overwrites an engine weight vector on the device (a raw copy into the
+    tensor: the engine refuses writes once loaded) and the oracle's copy."""
+    import ctypes
+    from ctox_hip.engine import EngineTensor, _lib, _check
+    t = EngineTensor()
+    _check(_lib().ctox_hip_engine_tensor(eng.handle, name.encode(), ctypes.byref(t)))
+    v = np.ascontiguousarray(values, np.float32)
+    assert v.nbytes == t.bytes
+    rt = ctypes.CDLL("libamdhip64.so")
+    rt.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    assert rt.hipMemcpy(t.data, v.ctypes.data, t.bytes, 1) == 0
+    ref.w(name)["data"] = v.copy()
+
+
+@pytest.mark.parametrize("restricted", [False, True])
+def test_engine_greedy_mtp_matches_oracle(hip, restricted):
+    """Temperature 0 is the crate's greedy MTP (Q/src/engine.rs:583-590,
+    915-963): argmax drafts (restricted: argmax over the bound IDs), longest
+    prefix equal to the target argmax tokens, then the first differing target
+    token or the bonus argmax. Exact tokens against the oracle; then, with the
+    final norms' weights set to -1 (every final hidden 0, so all logits tie
+    and the later index wins everywhere: every draft is accepted), two fully
+    accepted steps; with the weights restored, a plain step's logits check
+    the committed state."""
+    from ctox_hip.engine import Engine
+    from oracle.decoder import OracleDecoder
+    cfg = small_config()
+    eng = Engine(hip, cfg, seed=13)
+    try:
+        ids = None
+        if restricted:
+            ids = np.sort(np.random.default_rng(2).choice(511, 63, replace=False)).astype(np.uint32)
+            ids = np.append(ids, 511).astype(np.uint32)  # the tie winner is bound
+            eng.set_draft_vocab(ids)
+        ref = OracleDecoder(cfg.as_dict(), eng.tensor, draft_ids=ids)
+        rng = np.random.default_rng(6)
+        for step in range(20):
+            tok = int(rng.integers(0, 512))
+            ref.decode(tok)
+            eng.decode(tok)
+        token = run_mtp_steps(eng, ref, rng, 6, int(rng.integers(0, 512)), T=0.0, tag=" greedy")
+        saved = {n: ref.w(n)["data"].copy() for n in ("final_norm", "mtp.norm")}
+        for n in saved:
+            _write_vec(eng, ref, n, np.full(cfg.hidden_size, -1.0, np.float32))
+        for step in range(2):
+            say(f"case engine greedy tie step={step} token={token}")
+            nxt, acc, _ = ref.mtp_step(token, 0.0, None, 4)
+            assert (nxt, acc) == (511, [511] * 4), (nxt, acc)
+            assert eng.mtp_step(token, 0.0) == (nxt, [511] * 4)
+            assert eng.position == ref.position
+            token = nxt
+        for n, v in saved.items():
+            _write_vec(eng, ref, n, v)
+        want = ref.decode(token)
+        eng.decode(token)
+        close(eng.logits(1)[0], want)
+    finally:
+        eng.close()
+
+
+def test_engine_greedy_mtp_fails_closed(hip):
+    import ctox_hip
+    from ctox_hip.engine import Engine
+    eng = Engine(hip, small_config(), seed=11)
+    try:
+        eng.decode(3)
+        eng.decode(4)
+        for bad in (-0.5, float("nan"), float("inf")):
+            with pytest.raises(ctox_hip.InvalidArtifact):
+                eng.mtp_step(5, bad)
+        _poison(eng, "mtp.norm")
+        with pytest.raises(ctox_hip.InvalidState):
+            eng.mtp_step(5, 0.0)
+    finally:
+        eng.close()
+    eng = Engine(hip, small_config(), seed=11)
+    try:
+        eng.decode(3)
+        eng.decode(4)
+        _poison(eng, "final_norm")
+        with pytest.raises(ctox_hip.InvalidState):
+            eng.mtp_step(5, 0.0)
+    finally:
+        eng.close()

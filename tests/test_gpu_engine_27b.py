@@ -6,8 +6,10 @@
   one full-attention layer, a 2048-token context filled on the device and
   loaded into the oracle page by page. Plain steps' logits within rtol 1e-3
   plus 1e-4 x max|logits|; MTP k = 4 steps at T = 0.7 with exactly the
-  oracle's accepted drafts and next tokens.
-* Properties of the full 64-layer engine at a 4096-token context: every
+  oracle's accepted drafts and next tokens, then greedy (T = 0) MTP steps
+  with exactly the oracle's tokens.
+* Properties of the full 64-layer engine at 4096- and 32768-token contexts
+  (config 5's stated context): every
   step's logits are finite, and after MTP commits the engine is in the state
   plain decoding of the committed tokens reaches (the next step's logits and
   the following speculative step's first draft row agree).
@@ -67,6 +69,13 @@ def test_engine_27b_layer_dims_match_oracle(hip):
             assert got == (nxt, [int(x) for x in acc]), (step, got, nxt, acc)
             assert eng.position == ref.position
             token = nxt
+        for step in range(2):  # the crate's greedy MTP (engine.rs:583-590, 915-963)
+            say(f"case engine27 greedy mtp step={step} token={token} position={ref.position}")
+            nxt, acc, _ = ref.mtp_step(token, 0.0, None, 4)
+            got = eng.mtp_step(token, 0.0)
+            assert got == (nxt, [int(x) for x in acc]), (step, got, nxt, acc)
+            assert eng.position == ref.position
+            token = nxt
         say("case engine27 final decode")
         want = ref.decode(token)
         eng.decode(token)
@@ -76,15 +85,16 @@ def test_engine_27b_layer_dims_match_oracle(hip):
 
 
 @pytest.mark.timeout(900)
-def test_engine_27b_full_depth_commit_equals_plain_decode(hip):
+@pytest.mark.parametrize("context", [4096, 32768])
+def test_engine_27b_full_depth_commit_equals_plain_decode(hip, context):
     from ctox_hip.engine import Engine
-    cfg = config27(64, 4096 + 64)
-    say("case engine27 full depth: create two engines")
+    cfg = config27(64, context + 64)
+    say(f"case engine27 full depth context={context}: create two engines")
     spec = Engine(hip, cfg, seed=2)
     plain = Engine(hip, cfg, seed=2)
     try:
         for e in (spec, plain):
-            e.fill_context(4096, seed=9)
+            e.fill_context(context, seed=9)
         spec.set_rng(12345)
         token = 17
         committed = []

@@ -5,9 +5,9 @@ The artifact carries the crate's tensor names and a mix of packed dtypes:
 pure-Q2 fused groups (gate/up, q/k/v), Q4 down projections, Q4 / Q2 / mixed
 members of one GatedDeltaNet input group (Q2 rows widened on load), a Q2
 embedding and mixed LM head, MTP fc and MTP gate. Bar: logits of 24 plain
-steps within rtol 1e-3 plus 1e-4 x max|logits|; MTP steps at T = 0.7 with
-exactly the oracle's accepted drafts and next tokens, with the full and with
-a restricted draft head.
+steps within rtol 1e-3 plus 1e-4 x max|logits|; MTP steps at T = 0.7 and
+greedy (T = 0) with exactly the oracle's accepted drafts and next tokens,
+with the full and with a restricted draft head.
 """
 import sys
 
@@ -29,8 +29,9 @@ def close(got, want):
     np.testing.assert_allclose(got, want, rtol=1e-3, atol=1e-4 * float(np.abs(want).max()))
 
 
+@pytest.mark.parametrize("temperature", [0.7, 0.0])
 @pytest.mark.parametrize("draft_ids", [None, list(range(0, 512, 3))])
-def test_engine_from_artifact_matches_oracle(hip, tmp_path, draft_ids):
+def test_engine_from_artifact_matches_oracle(hip, tmp_path, draft_ids, temperature):
     from oracle import oracle as orc
     from oracle.decoder import ArtifactTensors, OracleDecoder
     from ctox_hip.loader import load_engine
@@ -58,8 +59,8 @@ def test_engine_from_artifact_matches_oracle(hip, tmp_path, draft_ids):
         token = int(rng.integers(0, cfg.vocab_size))
         for step in range(6):
             say(f"case engine artifact mtp step={step} token={token}")
-            nxt, acc, _ = ref.mtp_step(token, 0.7, g, 4)
-            got = eng.mtp_step(token, 0.7)
+            nxt, acc, _ = ref.mtp_step(token, temperature, g, 4)
+            got = eng.mtp_step(token, temperature)
             assert got == (nxt, [int(x) for x in acc]), (step, got, nxt, acc)
             token = nxt
         want = ref.decode(token)

@@ -105,7 +105,9 @@ def attention_case(hip, tokens, rows, page, sink, recent, seed):
     (1, 1, 16, 0, 16), (7, 5, 16, 0, 16), (16, 1, 16, 16, 16), (37, 3, 16, 16, 16),
     (300, 5, 16, 32, 64), (300, 1, 16, 32, 64), (1000, 2, 128, 128, 256), (4096, 5, 128, 128, 256),
     (300, 5, 24, 48, 64), (100, 3, 8, 0, 16),   # pages that split 16-token tiles
+    (32768, 1, 16, 128, 256), (32768, 5, 16, 128, 256),   # config 5: 32k context, page 16
 ])
+@pytest.mark.timeout(600)
 def test_paged_attention_matches_oracle(hip, tokens, rows, page, sink, recent):
     say(f"case paged attention tokens={tokens} rows={rows} page={page}")
     attention_case(hip, tokens, rows, page, sink, recent, seed=tokens * 7 + rows)

@@ -213,3 +213,48 @@ def test_speculative_bookkeeping(orc, tensors, draft_ids):
             assert all(d == 1 for d in info["drafts"])
             assert all(lg.shape == (1,) for lg in info["draft_logits"])
         token = nxt
+
+
+@pytest.mark.parametrize("draft_ids", [None, [1]])
+def test_greedy_speculative_step_is_verify_greedy_mtp(orc, tensors, draft_ids):
+    """Temperature 0 is the crate's greedy MTP (engine.rs:583-590, 915-963):
+    every draft is its row's argmax and the decision is verify_greedy_mtp's
+    (pinned by the crate's accept / fallback / bonus cases). The fixture's two
+    logits are equal, so the later index wins every argmax: all drafts are 1,
+    all accepted, the next token is the bonus argmax 1. The generator is not
+    consumed."""
+    dec = decoder(tensors, draft_ids=draft_ids, max_tokens=32)
+    dec.decode(0)
+    dec.decode(1)
+    g = orc.Pcg32(7)
+    before = orc.Pcg32(7).next_u32()
+    p = dec.position
+    nxt, acc, info = dec.mtp_step(1, 0.0, g, 4)
+    assert info["drafts"] == [1, 1, 1, 1] and acc == [1, 1, 1, 1] and nxt == 1
+    assert dec.position == p + 5 and dec.mtp_cache.tokens() == dec.position - 1
+    assert g.next_u32() == before
+    if draft_ids is None:
+        ref = orc.verify_greedy_mtp(np.stack(info["draft_logits"]), np.stack(info["target_logits"][:4]),
+                                    info["target_logits"][4])
+        assert ref == (nxt, 4, acc)
+
+
+def test_verify_greedy_tokens_equals_full_logits_branch(orc):
+    """The compact branch used by the greedy step equals verify_greedy_mtp's
+    full-logits branch (pinned by the crate's cases) on random rows with
+    planted agreements."""
+    from oracle.decoder import verify_greedy_tokens
+    rng = np.random.default_rng(3)
+    for case in range(200):
+        k, vocab = int(rng.integers(1, 6)), int(rng.integers(2, 9))
+        draft = rng.normal(size=(k, vocab)).astype(np.float32)
+        target = rng.normal(size=(k, vocab)).astype(np.float32)
+        for i in range(k):  # make a prefix of the drafts agree, of random length
+            if rng.random() < 0.7:
+                target[i] = draft[i]
+        bonus = rng.normal(size=vocab).astype(np.float32)
+        nxt, ver, acc = orc.verify_greedy_mtp(draft, target, bonus)
+        d = [orc.greedy_token(r) for r in draft]
+        t = [orc.greedy_token(r) for r in list(target) + [bonus]]
+        assert verify_greedy_tokens(d, t) == (nxt, len(acc))
+        assert acc == d[:len(acc)]
