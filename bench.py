@@ -226,7 +226,54 @@ def bench_gdn(torch, hip, steps):
         out[name] = {"tokens": T, "heads": heads, "us": us, "GBps": b / (us * 1e-6) / 1e9,
                      "tokens_per_s": T / (us * 1e-6)}
     del rng
+    out.update(bench_gdn_layer_core(torch, hip, steps))
     return out
+
+
+def bench_gdn_layer_core(torch, hip, steps):
+    """The decode engine's GatedDeltaNet token mixer core at 27B shapes (48
+    value heads over 16 key heads of 128, conv kernel 4, the engine's blocked
+    state layout): conv + gates + recurrence in one launch
+    (ctox_hip_gdn_fused_snap_device), one row (the plain decode step) and five
+    rows with a state snapshot per row (the MTP verify pass)."""
+    lib = ctox_lib()
+    H, KH, D, K = 48, 16, 128, 4
+    kw, vw = KH * D, H * D
+    C = 2 * kw + vw
+    a_off, b_off = C + vw, C + vw + H
+    stride = b_off + H
+    g = torch.Generator(device="cuda").manual_seed(9)
+    res = {}
+    for R, name in ((1, "layer_core_decode_27b"), (5, "layer_core_verify5_27b")):
+        proj = torch.randn(R, stride, device="cuda", generator=g)
+        conv_w = torch.randn(C, K, device="cuda", generator=g) * 0.5
+        conv_in = torch.randn(C, K, device="cuda", generator=g)
+        conv_out = torch.empty(R, C, K, device="cuda")
+        a_log = torch.randn(H, device="cuda", generator=g) * 0.3
+        dt_bias = torch.randn(H, device="cuda", generator=g) * 0.3
+        ld, be = torch.empty(R, H, device="cuda"), torch.empty(R, H, device="cuda")
+        ssz = H * D * D
+        st_in = torch.randn(ssz, device="cuda", generator=g) * 0.1
+        st_out = torch.empty(R, ssz, device="cuda")
+        o = torch.empty(R, H, D, device="cuda")
+        s = torch.cuda.current_stream().cuda_stream
+
+        def run():
+            st = lib.ctox_hip_gdn_fused_snap_device(hip.handle, proj.data_ptr(), stride, a_off, b_off, conv_w.data_ptr(),
+                                                    conv_in.data_ptr(), conv_out.data_ptr(), C * K, K, a_log.data_ptr(),
+                                                    dt_bias.data_ptr(), ld.data_ptr(), be.data_ptr(), st_in.data_ptr(),
+                                                    st_out.data_ptr(), ssz, 1, R, H, KH, D, D, o.data_ptr(), s)
+            if st != 0:
+                raise RuntimeError(lib.ctox_hip_last_error().decode())
+        run()
+        with Timer(torch) as t:
+            for _ in range(steps):
+                run()
+        us = t.ms * 1e3 / steps
+        # state read once, written per snapshot; projections, conv windows, outputs
+        b = ssz * 4 * (1 + R) + R * stride * 4 + 2 * C * K * 4 + R * C * K * 4 + R * vw * 4
+        res[name] = {"rows": R, "value_heads": H, "key_heads": KH, "us": us, "GBps": b / (us * 1e-6) / 1e9}
+    return res
 
 
 def ctox_lib():

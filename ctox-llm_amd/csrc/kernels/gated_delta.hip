@@ -26,18 +26,30 @@
 #define GDN_GROUPS 16
 #define GDN_MAX_ROWS 16  // key_dim <= 256
 
+// Sum over the four 16-lane rows of a wave (lane swaps, no LDS trip).
+__device__ __forceinline__ float gdn_sum_rows(float v) {
+    auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v), false,
+                                              false);
+    v = __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+    r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v), false, false);
+    return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+
 // Token-serial scan over a.tokens tokens (tokens = 1 is the decode step).
-// grid = heads * ceil(value_dim / 16), block = 256. The inverse norms of q and
-// k are reduced in the same pass as k.S (no separate norms launch):
-// mem_j = (sum_i S'[i,j] k_i) * k_inv and o_j = (sum_i S''[i,j] q_i) * q_inv / sqrt(key_dim).
+// grid = heads * ceil(value_dim / 16), block = 256. One reduction over the
+// key rows per token: with the decayed state S' the thread sums over its rows
+// k . S', q . S' (per column), |k|^2, |q|^2 and k . q; the four 16-lane row
+// groups of a wave add by lane swaps and the four waves through LDS (double
+// buffered by token parity, so one barrier per token). Then per column
+// mem_j = (k . S'_j) k_inv, delta_j = (v_j - mem_j) beta, and the output
+// follows without a second reduction: q . S''_j = q . S'_j + (k . q) k_inv delta_j,
+// o_j = that * q_inv / sqrt(key_dim).
 extern "C" __global__ __launch_bounds__(256) void ctox_gdn_scan_gfx950(GdnArgs a) {
-    __shared__ float red_mem[GDN_GROUPS][GDN_COLS];
-    __shared__ float red_out[GDN_GROUPS][GDN_COLS];
-    __shared__ float red_nrm[2][GDN_GROUPS];
+    __shared__ float red[2][5][GDN_COLS][4];  // [token parity][sum][column][wave]
 
     const uint32_t slices = (a.value_dim + GDN_COLS - 1) / GDN_COLS;
     const uint32_t h = blockIdx.x / slices, slice = blockIdx.x % slices;
-    const uint32_t jj = threadIdx.x % GDN_COLS, ig = threadIdx.x / GDN_COLS;
+    const uint32_t jj = threadIdx.x % GDN_COLS, ig = threadIdx.x / GDN_COLS, wave = threadIdx.x >> 6;
     const uint32_t j = slice * GDN_COLS + jj;
     const bool colok = j < a.value_dim;
     const uint32_t nrows = (a.key_dim + GDN_GROUPS - 1) / GDN_GROUPS;
@@ -60,52 +72,41 @@ extern "C" __global__ __launch_bounds__(256) void ctox_gdn_scan_gfx950(GdnArgs a
         const float beta = a.beta[th];
         const float vj = colok ? a.v[(size_t)t * a.v_stride + (size_t)h * a.value_dim + j] : 0.0f;
 
-        float kk[GDN_MAX_ROWS], qq[GDN_MAX_ROWS];
-        float mem = 0.0f, sk = 0.0f, sq = 0.0f;
+        float kk[GDN_MAX_ROWS];
+        float v5[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};  // k . S', q . S', |k|^2, |q|^2, k . q
 #pragma unroll
         for (int r = 0; r < GDN_MAX_ROWS; r++) {
             const uint32_t i = ig + GDN_GROUPS * r;
             const bool ok = (uint32_t)r < nrows && i < a.key_dim;
             kk[r] = ok ? k[i] : 0.0f;
-            qq[r] = ok ? q[i] : 0.0f;
-            sk += kk[r] * kk[r];
-            sq += qq[r] * qq[r];
+            const float qq = ok ? q[i] : 0.0f;
             s[r] = s[r] * decay;
-            mem += s[r] * kk[r];
+            v5[0] += s[r] * kk[r];
+            v5[1] += s[r] * qq;
+            v5[2] += kk[r] * kk[r];
+            v5[3] += qq * qq;
+            v5[4] += kk[r] * qq;
         }
-        red_mem[ig][jj] = mem;
-        if (jj == 0) {
-            red_nrm[0][ig] = sk;
-            red_nrm[1][ig] = sq;
-        }
-        lds_barrier();
-        float memj = 0.0f, ssk = 0.0f, ssq = 0.0f;
 #pragma unroll
-        for (int gi = 0; gi < GDN_GROUPS; gi++) {
-            memj += red_mem[gi][jj];
-            ssk += red_nrm[0][gi];
-            ssq += red_nrm[1][gi];
-        }
-        const float kinv = 1.0f / sqrtf(ssk + 1e-6f), qinv = 1.0f / sqrtf(ssq + 1e-6f);
-        const float delta = (vj - memj * kinv) * beta;
-        float o = 0.0f;
+        for (int c = 0; c < 5; c++) v5[c] = gdn_sum_rows(v5[c]);
+        float(*rb)[GDN_COLS][4] = red[t & 1];
+        if ((threadIdx.x & 63) < GDN_COLS)
 #pragma unroll
-        for (int r = 0; r < GDN_MAX_ROWS; r++) {
-            s[r] += kk[r] * kinv * delta;
-            o += s[r] * qq[r];
-        }
-        red_out[ig][jj] = o;
+            for (int c = 0; c < 5; c++) rb[c][jj][wave] = v5[c];
         lds_barrier();
-        if (ig == 0 && colok) {
-            float oj = 0.0f;
 #pragma unroll
-            for (int gi = 0; gi < GDN_GROUPS; gi++) oj += red_out[gi][jj];
-            a.out[th * a.value_dim + j] = oj * qinv * qscale;
+        for (int c = 0; c < 5; c++) {
+            const float4 w = *(const float4 *)rb[c][jj];
+            v5[c] = (w.x + w.y) + (w.z + w.w);
         }
-        // red_* are rewritten next token only after every thread has passed
-        // the second barrier of this token and read red_mem / red_nrm; the
-        // reads of red_out happen before the next token's first barrier.
-        lds_barrier();
+        const float kinv = 1.0f / sqrtf(v5[2] + 1e-6f), qinv = 1.0f / sqrtf(v5[3] + 1e-6f);
+        const float delta = (vj - v5[0] * kinv) * beta;
+#pragma unroll
+        for (int r = 0; r < GDN_MAX_ROWS; r++) s[r] += kk[r] * kinv * delta;
+        if (ig == 0 && colok) a.out[th * a.value_dim + j] = (v5[1] + v5[4] * kinv * delta) * qinv * qscale;
+        // The next token writes the other parity's buffer; the one after it
+        // this one again, past the next token's barrier, which every thread
+        // reaches only after reading this token's sums.
     }
 
 #pragma unroll
@@ -169,8 +170,15 @@ __device__ __forceinline__ void gdn_load8(const GdnBuf &b, bool ok, uint32_t off
 #define GDN_KQ(w, u) (GDN_V_P + (u) * (u) + 3 * (u) + 1 + (w))
 #define GDN_QQ(u) (GDN_V_P + (u) * (u) + 4 * (u) + 2)
 
-template <bool BLOCKED>
+// ONE: a single row (the batch-1 decode step; its one snapshot is the final
+// state). Its key-row
+// reductions (k . S, q . S, |k|^2, k . q, |q|^2 per column) finish with lane
+// swaps inside each wave and one LDS pass over the four waves: two
+// workgroup barriers in all instead of the row block's three and its Gram
+// pass (same arithmetic otherwise; the sums associate differently).
+template <bool BLOCKED, bool ONE = false>
 __device__ __forceinline__ void gdn_fused(const GdnFusedArgs &a) {
+    constexpr int PF = ONE ? 1 : GDN_PREFETCH;  // rows whose inputs are loaded up front
     // Rows are processed in blocks of up to GDN_PREFETCH. Phase 1 of a block
     // runs every row's conv + SiLU and gates (they do not depend on the
     // state) into LDS. Phase 2 needs one reduction over the key rows for the
@@ -185,6 +193,7 @@ __device__ __forceinline__ void gdn_fused(const GdnFusedArgs &a) {
     __shared__ float tot[GDN_NV];
     __shared__ float qks[2][GDN_PREFETCH][257];  // conv outputs: [0] q, [1] k (padded rows)
     __shared__ float vs[GDN_PREFETCH][GDN_COLS], gsc[GDN_PREFETCH][2];
+    __shared__ float red1[5][GDN_COLS][4];  // ONE: [sum][column][wave]
 
     const uint32_t slices = (a.value_dim + GDN_COLS - 1) / GDN_COLS;
     const uint32_t h = blockIdx.x / slices, slice = blockIdx.x % slices;
@@ -261,8 +270,8 @@ __device__ __forceinline__ void gdn_fused(const GdnFusedArgs &a) {
     const GdnBuf pr = gdn_buf(a.proj, (size_t)a.tokens * a.proj_stride);
     const GdnBuf dr = gdn_buf(a.gates_given ? a.log_decay : nullptr, (size_t)a.tokens * a.heads);
     const GdnBuf br = gdn_buf(a.gates_given ? a.beta : nullptr, (size_t)a.tokens * a.heads);
-    const uint32_t gu = tid - (256 - GDN_PREFETCH);  // block row of this thread's gates (< GDN_PREFETCH)
-    const bool g_thr = tid >= 256 - GDN_PREFETCH;
+    const uint32_t gu = tid - (256 - PF);  // block row of this thread's gates (< PF)
+    const bool g_thr = tid >= 256 - PF;
     // One conv step (shift the window left, append x) and its SiLU output.
     auto conv_step = [&](float (&win)[GDN_MAX_KERNEL], const float (&w)[GDN_MAX_KERNEL], float x) {
         float sum = 0.0f;
@@ -288,11 +297,11 @@ __device__ __forceinline__ void gdn_fused(const GdnFusedArgs &a) {
     // here, ahead of any use of the conv windows and state loaded above, so
     // every input read of the launch is in flight before the first wait;
     // later blocks' during the previous block's recurrence.
-    float xq[GDN_PREFETCH], xv[GDN_PREFETCH], ga = 0.0f, gb = 0.0f;
+    float xq[PF], xv[PF], ga = 0.0f, gb = 0.0f;
     auto load_block = [&](uint32_t t0) {
-        const uint32_t nb = min((uint32_t)GDN_PREFETCH, a.tokens - t0);
+        const uint32_t nb = min((uint32_t)PF, a.tokens - t0);
 #pragma unroll
-        for (int u = 0; u < GDN_PREFETCH; u++) {
+        for (int u = 0; u < PF; u++) {
             const uint32_t row = (t0 + min((uint32_t)u, nb - 1)) * a.proj_stride;
             xq[u] = gdn_ld(pr, qk_thr, (row + qk_ch) * 4);
             xv[u] = gdn_ld(pr, v_thr, (row + v_ch) * 4);
@@ -312,14 +321,14 @@ __device__ __forceinline__ void gdn_fused(const GdnFusedArgs &a) {
     const float dtb = gdn_ld(gbuf_dt, g_thr && !a.gates_given, h * 4);
     const float alog = gdn_ld(gbuf_al, g_thr && !a.gates_given, h * 4);
     __builtin_amdgcn_sched_barrier(0);
-    for (uint32_t t0 = 0; t0 < a.tokens; t0 += GDN_PREFETCH) {
-        const uint32_t nb = min((uint32_t)GDN_PREFETCH, a.tokens - t0);
+    for (uint32_t t0 = 0; t0 < a.tokens; t0 += PF) {
+        const uint32_t nb = min((uint32_t)PF, a.tokens - t0);
         const bool g_row = g_thr && gu < nb;
         const uint32_t gth = (t0 + (g_row ? gu : 0)) * a.heads + h;
         // Phase 1: conv + SiLU of every block row in order (the windows after
         // row t go to the row's conv snapshot), and the gates of row gu.
 #pragma unroll
-        for (int u = 0; u < GDN_PREFETCH; u++) {
+        for (int u = 0; u < PF; u++) {
             if ((uint32_t)u >= nb) break;
             if (qk_thr) {
                 const float y = conv_step(sq_, wq, xq[u]);
@@ -360,8 +369,48 @@ __device__ __forceinline__ void gdn_fused(const GdnFusedArgs &a) {
             gsc[gu][0] = expf(ld);
             gsc[gu][1] = be;
         }
-        if (t0 + GDN_PREFETCH < a.tokens) load_block(t0 + GDN_PREFETCH);
+        if (t0 + PF < a.tokens) load_block(t0 + PF);
         lds_barrier();
+        if constexpr (ONE) {
+            float v5[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};  // k . S, q . S, |k|^2, k . q, |q|^2
+#pragma unroll
+            for (int r = 0; r < 8; r++) {
+                const uint32_t i = ig + GDN_GROUPS * r;
+                const float kv = qks[1][0][i], qv = qks[0][0][i];
+                v5[0] += s[r] * kv;
+                v5[1] += s[r] * qv;
+                v5[2] += kv * kv;
+                v5[3] += kv * qv;
+                v5[4] += qv * qv;
+            }
+#pragma unroll
+            for (int k = 0; k < 5; k++) v5[k] = gdn_sum_rows(v5[k]);
+            if ((tid & 63) < GDN_COLS)
+#pragma unroll
+                for (int k = 0; k < 5; k++) red1[k][jj][tid >> 6] = v5[k];
+            lds_barrier();
+#pragma unroll
+            for (int k = 0; k < 5; k++) {
+                const float4 w = *(const float4 *)red1[k][jj];
+                v5[k] = (w.x + w.y) + (w.z + w.w);
+            }
+            const float decay = gsc[0][0], beta = gsc[0][1];
+            const float vjv = colok ? vs[0][jj] : 0.0f;
+            const float kinv = 1.0f / sqrtf(v5[2] + 1e-6f);
+            const float qinv = 1.0f / sqrtf(v5[4] + 1e-6f);
+            const float mem = decay * v5[0];
+            const float delta = (vjv - mem * kinv) * beta;
+            const float o = decay * v5[1] + (v5[3] * kinv) * delta;
+            if (ig == 0 && colok) a.out[(size_t)h * a.value_dim + j] = o * qinv * qscale;
+#pragma unroll
+            for (int r = 0; r < 8; r++) {
+                const float kk = qks[1][0][ig + GDN_GROUPS * r];
+                s[r] = s[r] * decay;
+                s[r] += kk * kinv * delta;
+            }
+            if (a.snap_stride) store_state(a.state_out);  // the snapshot of row 0 (conv windows: phase 1)
+            continue;
+        }
         // Phase 2a: this thread's partial sums over its key rows i = ig + 16 r
         // (key_dim <= 128: 8 rows; phase 1 zeroed the rows past key_dim).
         // No branch around the LDS reads, so they go out back to back.
@@ -462,3 +511,6 @@ __device__ __forceinline__ void gdn_fused(const GdnFusedArgs &a) {
 // The crate's state layout, and the engine's blocked one (state_blocked).
 extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_gfx950(GdnFusedArgs a) { gdn_fused<false>(a); }
 extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_blk_gfx950(GdnFusedArgs a) { gdn_fused<true>(a); }
+// One row (the batch-1 decode step), in either layout.
+extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused1_gfx950(GdnFusedArgs a) { gdn_fused<false, true>(a); }
+extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused1_blk_gfx950(GdnFusedArgs a) { gdn_fused<true, true>(a); }

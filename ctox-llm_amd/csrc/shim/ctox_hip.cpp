@@ -175,6 +175,8 @@ struct ctox_hip_backend {
     bool noalloc_ok = false;  // the static scratch of ctox_hip_launch_fused_matvec_noalloc is set up
     hipFunction_t repack = nullptr;
     hipFunction_t gdn_fused = nullptr, gdn_fused_blk = nullptr;
+    hipFunction_t gdn_fused1 = nullptr, gdn_fused1_blk = nullptr;  // one row
+    bool gdn_one = true;  // CTOX_GDN_ONE=0: the one-row step runs the row-block kernel
     int cus = 0;
     uint32_t tile_u = 0;  // CTOX_TILE_U: fixed row tiles per wave (0 = planned)
     int arrive = -1;      // CTOX_ARRIVE: 1 / 0 forces the tiled combine by arrival / by the last chunk
@@ -925,6 +927,7 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->tilemx_arr[1][0], "ctox_q4_mv_tilemx2_gfx950_arrive"}, {&b->tilemx_arr[1][1], "ctox_q4_mv_tilemx3_gfx950_arrive"},
                {&b->tilemx_arr[1][2], "ctox_q4_mv_tilemx4_gfx950_arrive"}, {&b->tilemx_arr[1][3], "ctox_q4_mv_tilemx5_gfx950_arrive"},
                {&b->repack, "ctox_tile_repack_gfx950"}, {&b->gdn_fused, "ctox_gdn_fused_gfx950"}, {&b->gdn_fused_blk, "ctox_gdn_fused_blk_gfx950"},
+               {&b->gdn_fused1, "ctox_gdn_fused1_gfx950"}, {&b->gdn_fused1_blk, "ctox_gdn_fused1_blk_gfx950"},
                {&b->finite, "ctox_finite_check_gfx950"}, {&b->gather, "ctox_gather_rows_gfx950"}, {&b->stream_read, "ctox_stream_read_gfx950"},
                {&b->write_segments, "ctox_write_segments_gfx950"},
                {&b->topk_part, "ctox_topk_part_gfx950"}, {&b->topk_final, "ctox_topk_final_gfx950"}};
@@ -959,6 +962,7 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
     // separate launch (the tilem kernels) instead of building them in-kernel.
     if (const char *m = std::getenv("CTOX_SMALL_M_BUILD")) b->no_mx = std::atoi(m) == 0;
     if (const char *m = std::getenv("CTOX_ARRIVE")) b->arrive = std::atoi(m) != 0;
+    if (const char *m = std::getenv("CTOX_GDN_ONE")) b->gdn_one = std::atoi(m) != 0;
     if (const char *m = std::getenv("CTOX_MX_MAX")) b->mx_max = (uint64_t)std::atoll(m) << 20;
     // How many workgroups of each tiled kernel the device holds at once:
     // launches within it may combine by the last chunk's waves (every
@@ -1904,8 +1908,10 @@ ctox_status gdn_fused_impl(ctox_hip_backend *b, const float *d_proj, size_t proj
     a.gates_given = gates_given ? 1u : 0u;
     a.state_blocked = blocked ? 1u : 0u;
     const size_t slices = (value_dim + 15) / 16;
-    return launch(a.state_blocked ? b->gdn_fused_blk : b->gdn_fused, dim3((unsigned)(heads * slices)), dim3(256),
-                  pick_stream(b, stream), a, "ctox_gdn_fused_gfx950");
+    const bool one = b->gdn_one && tokens == 1;
+    hipFunction_t f = one ? (a.state_blocked ? b->gdn_fused1_blk : b->gdn_fused1)
+                          : (a.state_blocked ? b->gdn_fused_blk : b->gdn_fused);
+    return launch(f, dim3((unsigned)(heads * slices)), dim3(256), pick_stream(b, stream), a, "ctox_gdn_fused_gfx950");
 }
 }  // namespace
 

@@ -245,7 +245,8 @@ def test_fused_mixer_core_matches_separate(hip, tokens, heads, key_heads, dk, dv
 def test_fused_snapshots_equal_sequential_steps(hip):
     """ctox_hip_gdn_fused_snap_device: the state and conv windows after each
     row t equal those of running the fused core over the first t + 1 rows
-    (in place), and the outputs are the same."""
+    (in place; bit for bit from two rows on, where both run the row-block
+    kernel), and the outputs are the same."""
     import torch
     import ctox_hip
     say("case fused snapshots")
@@ -290,7 +291,12 @@ def test_fused_snapshots_equal_sequential_steps(hip):
                                              p(a_log), p(dt_bias), p(ld_b), p(be_b), 0, p(st_b), t + 1, heads,
                                              key_heads, dk, dv, p(out_b), None) == 0
         torch.cuda.synchronize()
-        assert np.array_equal(snaps[t].cpu().numpy(), st_b.cpu().numpy().reshape(-1)), t
+        if t == 0:
+            # One row runs the one-row kernel (its key-row sums associate
+            # differently): equal within float rounding.
+            np.testing.assert_allclose(snaps[t].cpu().numpy(), st_b.cpu().numpy().reshape(-1), rtol=1e-5, atol=1e-6)
+        else:
+            assert np.array_equal(snaps[t].cpu().numpy(), st_b.cpu().numpy().reshape(-1)), t
         assert np.array_equal(csnaps[t].cpu().numpy(), cout.cpu().numpy().reshape(-1)), t
         if t == tokens - 1:
             assert np.array_equal(out.cpu().numpy(), out_b.cpu().numpy())
