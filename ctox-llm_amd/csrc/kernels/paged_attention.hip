@@ -612,12 +612,14 @@ __device__ __forceinline__ uint32_t pa_pk(float x, float y) {
     return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x, y));
 }
 
-template <int R, class LDS>
+// Q4: the tile's precision (-1: read from the tile; 0 / 1: a constant, so the
+// block sizes, offsets, code masks and selectors fold).
+template <int R, int Q4, class LDS>
 __device__ __forceinline__ void pa_tile16(const GqaArgs &a, LDS &L, const int8_t *qb, uint32_t wave, uint32_t tb, uint32_t h,
                                           uint32_t li, uint32_t lg, const PaTile &T, const uint32_t *stage,
                                           PaState<R> &st) {
     const uint32_t lane = 16 * lg + li;
-    const bool q4 = T.q4 != 0;
+    const bool q4 = Q4 >= 0 ? Q4 == 1 : T.q4 != 0;
     bool present[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) present[c] = pa_present(a, T, tb + 4 * lg + c);
@@ -671,7 +673,7 @@ __device__ __forceinline__ void pa_tile16(const GqaArgs &a, LDS &L, const int8_t
     }
     // Scores, one block at a time: T = sum X (2c - K) = 2 sum(X c) - K sum X,
     // exact in 32-bit modular arithmetic (|T| < 2^31 although 2 sum(X c) may wrap).
-    const uint32_t kq = T.q4 ? 15u : 3u;
+    const uint32_t kq = q4 ? 15u : 3u;
     float s[R][4];
 #pragma unroll
     for (int r = 0; r < R; r++) {
@@ -937,13 +939,22 @@ __device__ __forceinline__ void paged_gqa_partial16(const GqaArgs &a) {
             st.corr[r][b] = 0.0f;
         }
     // Tile k computes from the stage while tile k + 1's loads are in flight.
-    for (uint32_t tile = t0; tile < t1; tile++) {
-        pa_stage_write(stage, lane, PA.q4 != 0, sg);
-        const PaTile PN = pa_tile_of(a, dsc, tile + 1 - t0);
-        pa_issue_stage(a, PN, (tile + 1) * 16, h, lane, sg);
-        pa_tile16<R>(a, L, L.u.run.limbs, wave, tile * 16, h, li, lg, PA, stage, st);
-        PA = PN;
-    }
+    // A wave whose tiles all lie in Q2 pages (most of a long context) runs
+    // the tile loop with the precision folded in.
+    auto run = [&](auto q4c) {
+        constexpr int Q4 = decltype(q4c)::value;
+        for (uint32_t tile = t0; tile < t1; tile++) {
+            pa_stage_write(stage, lane, Q4 >= 0 ? Q4 == 1 : PA.q4 != 0, sg);
+            const PaTile PN = pa_tile_of(a, dsc, tile + 1 - t0);
+            pa_issue_stage(a, PN, (tile + 1) * 16, h, lane, sg);
+            pa_tile16<R, Q4>(a, L, L.u.run.limbs, wave, tile * 16, h, li, lg, PA, stage, st);
+            PA = PN;
+        }
+    };
+    if (__builtin_amdgcn_ballot_w64(lane < t1 - t0 && dsc.x != 0) == 0)
+        run(std::integral_constant<int, 0>{});
+    else
+        run(std::integral_constant<int, -1>{});
     // O = C 4^-c - sum P s (the latter summed over the four lane groups' tokens);
     // denominators likewise.
 #pragma unroll
