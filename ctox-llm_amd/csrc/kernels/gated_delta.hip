@@ -45,7 +45,7 @@ __device__ __forceinline__ float gdn_sum_rows(float v) {
 // follows without a second reduction: q . S''_j = q . S'_j + (k . q) k_inv delta_j,
 // o_j = that * q_inv / sqrt(key_dim).
 extern "C" __global__ __launch_bounds__(256) void ctox_gdn_scan_gfx950(GdnArgs a) {
-    __shared__ float red[2][5][GDN_COLS][4];  // [token parity][sum][column][wave]
+    __shared__ __align__(16) float red[2][5][GDN_COLS][4];  // [token parity][sum][column][wave]
 
     const uint32_t slices = (a.value_dim + GDN_COLS - 1) / GDN_COLS;
     const uint32_t h = blockIdx.x / slices, slice = blockIdx.x % slices;
@@ -193,7 +193,7 @@ __device__ __forceinline__ void gdn_fused(const GdnFusedArgs &a) {
     __shared__ float tot[GDN_NV];
     __shared__ float qks[2][GDN_PREFETCH][257];  // conv outputs: [0] q, [1] k (padded rows)
     __shared__ float vs[GDN_PREFETCH][GDN_COLS], gsc[GDN_PREFETCH][2];
-    __shared__ float red1[5][GDN_COLS][4];  // ONE: [sum][column][wave]
+    __shared__ __align__(16) float red1[5][GDN_COLS][4];  // ONE: [sum][column][wave]
 
     const uint32_t slices = (a.value_dim + GDN_COLS - 1) / GDN_COLS;
     const uint32_t h = blockIdx.x / slices, slice = blockIdx.x % slices;
