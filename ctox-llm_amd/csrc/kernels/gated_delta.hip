@@ -176,7 +176,10 @@ __device__ __forceinline__ void gdn_load8(const GdnBuf &b, bool ok, uint32_t off
 // swaps inside each wave and one LDS pass over the four waves: two
 // workgroup barriers in all instead of the row block's three and its Gram
 // pass (same arithmetic otherwise; the sums associate differently).
-template <bool BLOCKED, bool ONE = false>
+// KC: the conv kernel size as a constant (0: a.kernel at run time); with it
+// the window shifts, taps and window stores are straight-line code (a row's
+// conv is otherwise mostly the selects of a runtime-length window).
+template <bool BLOCKED, bool ONE = false, int KC = 0>
 __device__ __forceinline__ void gdn_fused(const GdnFusedArgs &a) {
     constexpr int PF = ONE ? 1 : GDN_PREFETCH;  // rows whose inputs are loaded up front
     // Rows are processed in blocks of up to GDN_PREFETCH. Phase 1 of a block
@@ -201,7 +204,7 @@ __device__ __forceinline__ void gdn_fused(const GdnFusedArgs &a) {
     const uint32_t j = slice * GDN_COLS + jj;
     const bool colok = j < a.value_dim;
     const uint32_t dk = a.key_dim, rep = a.heads / a.key_heads, kh = h / rep;
-    const uint32_t kw = a.key_heads * dk, K = a.kernel;
+    const uint32_t kw = a.key_heads * dk, K = KC ? (uint32_t)KC : a.kernel;
     const uint32_t nrows = (dk + GDN_GROUPS - 1) / GDN_GROUPS;
     const float qscale = 1.0f / sqrtf((float)dk);
 
@@ -508,9 +511,16 @@ __device__ __forceinline__ void gdn_fused(const GdnFusedArgs &a) {
             if ((uint32_t)i < K) a.conv_out[(size_t)v_ch * K + i] = sv_[i];
 }
 
-// The crate's state layout, and the engine's blocked one (state_blocked).
-extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_gfx950(GdnFusedArgs a) { gdn_fused<false>(a); }
-extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused_blk_gfx950(GdnFusedArgs a) { gdn_fused<true>(a); }
-// One row (the batch-1 decode step), in either layout.
-extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused1_gfx950(GdnFusedArgs a) { gdn_fused<false, true>(a); }
-extern "C" __global__ __launch_bounds__(256) void ctox_gdn_fused1_blk_gfx950(GdnFusedArgs a) { gdn_fused<true, true>(a); }
+// The crate's state layout, and the engine's blocked one (state_blocked);
+// fused1: one row (the batch-1 decode step); _k4: conv kernel size 4 (the
+// model's), the others take any size up to GDN_MAX_KERNEL.
+#define CTOX_GDN_FUSED(name, blocked, one, kc) \
+    extern "C" __global__ __launch_bounds__(256) void name(GdnFusedArgs a) { gdn_fused<blocked, one, kc>(a); }
+CTOX_GDN_FUSED(ctox_gdn_fused_gfx950, false, false, 0)
+CTOX_GDN_FUSED(ctox_gdn_fused_blk_gfx950, true, false, 0)
+CTOX_GDN_FUSED(ctox_gdn_fused1_gfx950, false, true, 0)
+CTOX_GDN_FUSED(ctox_gdn_fused1_blk_gfx950, true, true, 0)
+CTOX_GDN_FUSED(ctox_gdn_fused_k4_gfx950, false, false, 4)
+CTOX_GDN_FUSED(ctox_gdn_fused_blk_k4_gfx950, true, false, 4)
+CTOX_GDN_FUSED(ctox_gdn_fused1_k4_gfx950, false, true, 4)
+CTOX_GDN_FUSED(ctox_gdn_fused1_blk_k4_gfx950, true, true, 4)

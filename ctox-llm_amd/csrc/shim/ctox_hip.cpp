@@ -176,6 +176,7 @@ struct ctox_hip_backend {
     hipFunction_t repack = nullptr;
     hipFunction_t gdn_fused = nullptr, gdn_fused_blk = nullptr;
     hipFunction_t gdn_fused1 = nullptr, gdn_fused1_blk = nullptr;  // one row
+    hipFunction_t gdn_k4[2][2] = {};  // [one row][blocked]: conv kernel size 4
     bool gdn_one = true;  // CTOX_GDN_ONE=0: the one-row step runs the row-block kernel
     int cus = 0;
     uint32_t tile_u = 0;  // CTOX_TILE_U: fixed row tiles per wave (0 = planned)
@@ -928,6 +929,8 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->tilemx_arr[1][2], "ctox_q4_mv_tilemx4_gfx950_arrive"}, {&b->tilemx_arr[1][3], "ctox_q4_mv_tilemx5_gfx950_arrive"},
                {&b->repack, "ctox_tile_repack_gfx950"}, {&b->gdn_fused, "ctox_gdn_fused_gfx950"}, {&b->gdn_fused_blk, "ctox_gdn_fused_blk_gfx950"},
                {&b->gdn_fused1, "ctox_gdn_fused1_gfx950"}, {&b->gdn_fused1_blk, "ctox_gdn_fused1_blk_gfx950"},
+               {&b->gdn_k4[0][0], "ctox_gdn_fused_k4_gfx950"}, {&b->gdn_k4[0][1], "ctox_gdn_fused_blk_k4_gfx950"},
+               {&b->gdn_k4[1][0], "ctox_gdn_fused1_k4_gfx950"}, {&b->gdn_k4[1][1], "ctox_gdn_fused1_blk_k4_gfx950"},
                {&b->finite, "ctox_finite_check_gfx950"}, {&b->gather, "ctox_gather_rows_gfx950"}, {&b->stream_read, "ctox_stream_read_gfx950"},
                {&b->write_segments, "ctox_write_segments_gfx950"},
                {&b->topk_part, "ctox_topk_part_gfx950"}, {&b->topk_final, "ctox_topk_final_gfx950"}};
@@ -1909,8 +1912,9 @@ ctox_status gdn_fused_impl(ctox_hip_backend *b, const float *d_proj, size_t proj
     a.state_blocked = blocked ? 1u : 0u;
     const size_t slices = (value_dim + 15) / 16;
     const bool one = b->gdn_one && tokens == 1;
-    hipFunction_t f = one ? (a.state_blocked ? b->gdn_fused1_blk : b->gdn_fused1)
-                          : (a.state_blocked ? b->gdn_fused_blk : b->gdn_fused);
+    hipFunction_t f = kernel == 4 ? b->gdn_k4[one ? 1 : 0][a.state_blocked]
+                                  : one ? (a.state_blocked ? b->gdn_fused1_blk : b->gdn_fused1)
+                                        : (a.state_blocked ? b->gdn_fused_blk : b->gdn_fused);
     return launch(f, dim3((unsigned)(heads * slices)), dim3(256), pick_stream(b, stream), a, "ctox_gdn_fused_gfx950");
 }
 }  // namespace

@@ -181,9 +181,12 @@ def test_strided_repeated_key_heads(hip, orc, tokens, chunk):
     np.testing.assert_allclose(dstate.cpu().numpy().reshape(-1), ref_state, rtol=1e-4, atol=1e-5)
 
 
-@pytest.mark.parametrize("tokens,heads,key_heads,dk,dv,given", [(1, 48, 16, 128, 128, False), (5, 48, 16, 128, 128, False),
-                                                               (3, 4, 2, 64, 64, True), (2, 8, 8, 128, 48, False)])
-def test_fused_mixer_core_matches_separate(hip, tokens, heads, key_heads, dk, dv, given):
+@pytest.mark.parametrize("tokens,heads,key_heads,dk,dv,given,K", [(1, 48, 16, 128, 128, False, 4),
+                                                                 (5, 48, 16, 128, 128, False, 4),
+                                                                 (3, 4, 2, 64, 64, True, 4), (2, 8, 8, 128, 48, False, 4),
+                                                                 (1, 48, 16, 128, 128, False, 3),
+                                                                 (3, 4, 2, 64, 64, False, 6)])
+def test_fused_mixer_core_matches_separate(hip, tokens, heads, key_heads, dk, dv, given, K):
     """ctox_hip_gdn_fused_device (conv + gates + recurrence in one launch) against
     the separate conv, gates and strided recurrence entry points (each pinned
     to the oracle by the tests above and test_gpu_layer_ops): outputs, states,
@@ -191,10 +194,9 @@ def test_fused_mixer_core_matches_separate(hip, tokens, heads, key_heads, dk, dv
     import ctypes
     import torch
     import ctox_hip
-    say(f"case fused mixer tokens={tokens} heads={heads}/{key_heads} dk={dk} dv={dv} given={given}")
+    say(f"case fused mixer tokens={tokens} heads={heads}/{key_heads} dk={dk} dv={dv} given={given} kernel={K}")
     lib = ctox_hip.load_library()
-    rng = np.random.default_rng(tokens * 100 + heads)
-    K = 4
+    rng = np.random.default_rng(tokens * 100 + heads + K)
     kw, vw = key_heads * dk, heads * dv
     C = 2 * kw + vw
     a_off, b_off = C + vw, C + vw + heads
