@@ -17,7 +17,9 @@
  *     Q/src/engine.rs:1213-1300).
  *   - orc_mtp_accept_sample: no crate counterpart; pinned by the invariants
  *     of speculative rejection sampling (identical distributions always
- *     accept; a Monte-Carlo check that the output law equals the target law).
+ *     accept; a Monte-Carlo check that the output law equals the target law)
+ *     and by decisions its definition fixes (accept iff u q(d) < p(d) for
+ *     the next draw, the residual max(p - q, 0), draws consumed in order).
  */
 #include "ctox_oracle.h"
 

@@ -258,3 +258,36 @@ def test_verify_greedy_tokens_equals_full_logits_branch(orc):
         t = [orc.greedy_token(r) for r in list(target) + [bonus]]
         assert verify_greedy_tokens(d, t) == (nxt, len(acc))
         assert acc == d[:len(acc)]
+
+
+def test_speculative_commit_equals_plain_decoding(orc, tmp_path):
+    """The speculative flow at T = 0.7 (no crate counterpart) against the
+    property its commit must have: after three speculative steps, a twin that
+    plain-decodes the committed tokens reaches the same position and the same
+    next logits (a random-weight model written as a `.ctoxq` file: 3
+    GatedDeltaNet layers and one full-attention layer, MTP k = 4)."""
+    from artifact_model import write_artifact
+    from test_artifact_loader import small_config
+    from oracle.decoder import ArtifactTensors, OracleDecoder
+    cfg = small_config()
+    path = tmp_path / "model.ctoxq"
+    write_artifact(path, cfg, seed=5)
+    spec = OracleDecoder(cfg.as_dict(), ArtifactTensors(path, cfg.as_dict()))
+    plain = OracleDecoder(cfg.as_dict(), ArtifactTensors(path, cfg.as_dict()))
+    rng = np.random.default_rng(3)
+    for _ in range(6):
+        tok = int(rng.integers(0, cfg.vocab_size))
+        spec.decode(tok)
+        plain.decode(tok)
+    g = orc.Pcg32(21)
+    token = int(rng.integers(0, cfg.vocab_size))
+    committed = []
+    for _ in range(3):
+        nxt, acc, _ = spec.mtp_step(token, 0.7, g, 4)
+        committed += [token] + [int(x) for x in acc]
+        token = nxt
+    for t in committed:
+        plain.decode(t)
+    assert spec.position == plain.position == 6 + len(committed)
+    a, b = spec.decode(token), plain.decode(token)
+    np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-6 * float(np.abs(b).max()))

@@ -17,6 +17,11 @@ tests leave open:
   65-143): brute force over small vocabularies, with the truncated law
   built by hand in float64 and the draw swept over a fine grid.
 
+and, with no crate counterpart (the crate's MTP is greedy), the T > 0
+rejection-sampling accept (`mtp_accept_sample`): decisions the definition
+fixes (accept iff u q(d) < p(d) for the next draw, the residual
+max(p - q, 0), the order in which draws are consumed).
+
 The expected values are derived from the crate's definitions, never from
 the oracle's code: softplus/sigmoid/SiLU and the rank-1 key structure of the
 fixture (every key is a constant-per-row vector) turn the recurrence into a
@@ -269,3 +274,99 @@ def test_sampler_truncation_brute_force(orc, top_k, top_p):
 @pytest.fixture
 def tensors_crate(orc):
     return fixture_tensors(orc)
+
+
+# ------------------------------------------------- MTP accept at T > 0
+# Speculative rejection sampling (no crate counterpart: the crate's MTP is
+# greedy), stated from its definition: draft token d of row i is accepted
+# iff u * q_i(d) < p_i(d) with u the next uniform draw of the crate's Pcg32;
+# on the first rejection the next token is drawn with the following uniform
+# from the residual law max(p_i - q_i, 0) (normalised); when every draft is
+# accepted, from the bonus row's softmax. p, q are temperature softmaxes of
+# the target and draft rows. Each check below fixes a decision the
+# definition determines, so a swapped ratio (q / p), a wrong residual
+# (q - p), a reused or skipped draw, or the temperature left out fails.
+
+def _softmax64(x, t):
+    z = np.asarray(x, np.float64) / t
+    e = np.exp(z - z.max())
+    return e / e.sum()
+
+
+def _draws(orc, seed, n):
+    g = orc.Pcg32(seed)
+    return [g.next_f32() for _ in range(n)]
+
+
+@pytest.mark.parametrize("t", [0.4, 0.7, 1.3])
+def test_mtp_accept_decision_is_u_q_below_p(orc, t):
+    # Two tokens, one draft: the acceptance of token 0 follows u < p(0) / q(0)
+    # for the first draw of every seed (cases within 1e-5 of the boundary skipped).
+    target = np.array([[0.3, -0.4]], np.float32)
+    draft = np.array([[0.9, -0.8]], np.float32)
+    p, q = _softmax64(target[0], t), _softmax64(draft[0], t)
+    ratio = p[0] / q[0]
+    assert 0.2 < ratio < 0.95  # the draft over-weights token 0: a real decision
+    bonus = np.zeros(2, np.float32)
+    decided = 0
+    for seed in range(300):
+        u = _draws(orc, seed, 1)[0]
+        if abs(u - ratio) < 1e-5:
+            continue
+        nxt, nacc = orc.mtp_accept_sample(draft, target, bonus, [0], t, orc.Pcg32(seed))
+        assert nacc == (1 if u < ratio else 0), (seed, u, ratio)
+        if nacc == 0:
+            # residual max(p - q, 0) is all on token 1
+            assert nxt == 1
+        decided += 1
+    assert decided > 250
+
+
+def test_mtp_accept_residual_is_target_minus_draft(orc):
+    # Three tokens, draft d = 2 with q(2) >> p(2): rejected for most draws.
+    # p - q is positive only on token 0, so every rejection resamples token 0
+    # (q - p would put the mass on token 2; an unclipped residual could give 1).
+    t = 0.7
+    target = np.array([[1.2, 0.1, -2.0]], np.float32)
+    draft = np.array([[0.6, 0.9, 1.5]], np.float32)
+    p, q = _softmax64(target[0], t), _softmax64(draft[0], t)
+    assert p[0] > q[0] and p[1] < q[1] and p[2] < q[2]
+    bonus = np.zeros(3, np.float32)
+    rejected = 0
+    for seed in range(200):
+        nxt, nacc = orc.mtp_accept_sample(draft, target, bonus, [2], t, orc.Pcg32(seed))
+        if nacc == 0:
+            assert nxt == 0
+            rejected += 1
+    assert rejected > 150
+
+
+def test_mtp_accept_draws_consumed_in_order(orc):
+    # k = 3 drafts with identical draft and target rows accept for any draw
+    # (u q < p with p = q unless u = 1, which Pcg32's f32 never returns); the
+    # bonus row then puts all its mass on token 4, and the generator has
+    # advanced by exactly k + 1 draws. A rejection at row 1 (draft token with
+    # p = 0 there) consumes 2 + 2 draws and resamples from row 1's residual.
+    t, vocab, k = 0.7, 5, 3
+    rng = np.random.default_rng(4)
+    rows = rng.standard_normal((k, vocab)).astype(np.float32)
+    bonus = np.full(vocab, -60.0, np.float32)
+    bonus[4] = 60.0
+    for seed in range(20):
+        g = orc.Pcg32(seed)
+        nxt, nacc = orc.mtp_accept_sample(rows, rows, bonus, [1, 2, 3], t, g)
+        assert (nxt, nacc) == (4, 3)
+        ref = orc.Pcg32(seed)
+        _ = [ref.next_f32() for _ in range(k + 1)]
+        assert g.c.state == ref.c.state
+    target = rows.copy()
+    target[1, 3] = -np.inf  # p_1(3) = 0: draft token 3 at row 1 is always rejected
+    target[1, :3] = [-60.0, -60.0, 60.0]  # the residual then sits on token 2
+    draft = rows.copy()
+    for seed in range(20):
+        g = orc.Pcg32(seed)
+        nxt, nacc = orc.mtp_accept_sample(draft, target, bonus, [1, 3, 0], t, g)
+        assert (nxt, nacc) == (2, 1)
+        ref = orc.Pcg32(seed)
+        _ = [ref.next_f32() for _ in range(3)]  # row 0 accept, row 1 reject, row 1 residual
+        assert g.c.state == ref.c.state
