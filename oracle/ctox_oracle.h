@@ -147,7 +147,8 @@ int orc_verify_greedy_mtp(const float *draft_logits, const float *target_logits,
                           uint32_t *next_token, uint32_t *verified, uint32_t *accepted,
                           uint32_t *n_accepted);
 /* Speculative rejection-sampling acceptance at temperature T (no crate
- * counterpart: the crate's MTP is greedy-only; parity unpinned by the crate). */
+ * counterpart: the crate's MTP is greedy-only; pinned by the closed forms of
+ * rejection sampling, not by the crate). */
 int orc_mtp_accept_sample(const float *draft_logits, const float *target_logits,
                           const float *bonus_logits, const uint32_t *draft_tokens,
                           size_t drafts, size_t vocab, float temperature, orc_pcg32 *rng,
