@@ -219,6 +219,16 @@ def test_tiled_combine_modes(orc, mode, monkeypatch):
         got = resident_run(hip3, op, parts[1])
         ref = oracle_rows(orc, 1, 151936, 5120, parts, ctox_hip.Activation.Identity)
         check(got, ref, "LM head")
+        del op, parts, got, ref
+        # The largest single matrix of the crate's model: the LM head over its
+        # 248320-token vocabulary (675 MB of Q4 rows), batch 1 and a 5-row verify.
+        for batch in (1, 5):
+            say(f"case combine default: crate LM head 248320x5120 batch={batch}")
+            op, parts = make_case(1, 248320, 5120, 47, "f16", bias=False, batch=batch)
+            got = resident_run(hip3, op, parts[1])
+            ref = oracle_rows(orc, 1, 248320, 5120, parts, ctox_hip.Activation.Identity)
+            check(got, ref, f"crate LM head batch={batch}")
+            del op, parts, got, ref
     finally:
         hip3.close()
 
