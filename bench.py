@@ -355,8 +355,9 @@ def bench_decode_27b(torch, hip, steps, context=32768):
     """Config 5: the device engine on the 27B shapes (64 layers, 48 GatedDeltaNet
     and 16 full attention, Q4 projections and LM head, Q2 down projections,
     vocab 151936), paged KV page 16 with `context` random tokens; plain
-    batch-1 decode and MTP k = 4 at T = 0.7 (seeded Pcg32). Weights are
-    synthetic, so draft acceptance reflects random heads."""
+    batch-1 decode and MTP k = 4 at T = 0.7 (seeded Pcg32) and greedy (T = 0,
+    the crate's mode). Weights are synthetic, so draft acceptance reflects
+    random heads."""
     import time
     from ctox_hip.engine import Engine, EngineConfig
     cfg = EngineConfig.qwen38_27b(max_tokens=context + 1280)
@@ -381,24 +382,28 @@ def bench_decode_27b(torch, hip, steps, context=32768):
     # step is a random variable whose mean the tokens/s figure depends on.
     n_mtp = max(10, min(steps, 100))
 
-    def mtp_run(tag, tok):
+    def mtp_run(tag, tok, temperature=0.7):
         eng.set_rng(0x5EED)
         tokens = 0
-        eng.mtp_step(tok, 0.7)  # warm
+        eng.mtp_step(tok, temperature)  # warm
         t0 = time.time()
         for _ in range(n_mtp):
-            nxt, acc = eng.mtp_step(tok, 0.7)
+            nxt, acc = eng.mtp_step(tok, temperature)
             tokens += 1 + len(acc)
             tok = nxt
         torch.cuda.synchronize()  # the last step's commit may still be queued
         mtp = time.time() - t0
-        res[f"mtp_k4_T0.7{tag}_ms_per_step"] = mtp / n_mtp * 1e3
+        key = "mtp_k4_greedy" if temperature == 0.0 else f"mtp_k4_T0.7{tag}"
+        tag = "_greedy" if temperature == 0.0 else tag
+        res[f"{key}_ms_per_step"] = mtp / n_mtp * 1e3
         res[f"mtp{tag}_tokens_per_s"] = tokens / mtp
         res[f"mtp{tag}_accepted_drafts_per_step"] = tokens / n_mtp - 1
         res[f"mtp{tag}_steps"] = n_mtp
         return tok
 
     tok = mtp_run("", tok)
+    # The crate's own speculative mode: greedy drafts and prefix-match verify.
+    tok = mtp_run("", tok, temperature=0.0)
     # The release-bound draft vocabulary (Q/src/decoder.rs:589-627): a seeded
     # 32768-token subset here (random weights: no trained coverage).
     ids = np.sort(np.random.default_rng(3).choice(cfg.vocab_size, DRAFT_VOCAB, replace=False)).astype(np.uint32)
