@@ -171,11 +171,11 @@ __device__ __forceinline__ void gdn_load8(const GdnBuf &b, bool ok, uint32_t off
 #define GDN_QQ(u) (GDN_V_P + (u) * (u) + 4 * (u) + 2)
 
 // ONE: a single row (the batch-1 decode step; its one snapshot is the final
-// state). Its key-row
-// reductions (k . S, q . S, |k|^2, k . q, |q|^2 per column) finish with lane
-// swaps inside each wave and one LDS pass over the four waves: two
-// workgroup barriers in all instead of the row block's three and its Gram
-// pass (same arithmetic otherwise; the sums associate differently).
+// state). Its key-row reductions (k . S, q . S, |k|^2, k . q, |q|^2 per
+// column) finish with lane swaps inside each wave and one LDS pass over the
+// four waves: two workgroup barriers in all instead of the row block's three
+// and its Gram pass (same arithmetic otherwise; the sums associate
+// differently).
 // KC: the conv kernel size as a constant (0: a.kernel at run time); with it
 // the window shifts, taps and window stores are straight-line code (a row's
 // conv is otherwise mostly the selects of a runtime-length window).
