@@ -97,8 +97,9 @@ __device__ __forceinline__ float epi_apply(float v, const EpiIn &e, const TileMa
 // branch-free: an unused or absent input has an empty range and reads zeros,
 // so no wait lands in a divergent block ahead of weight loads in flight.
 // Lane 16 t + m takes columns 4m .. 4m + 3 of block 4 grp + t.
-__device__ __forceinline__ void frag_group_loads(const TileMatvecArgs &a, uint32_t grp, uint32_t lane, GroupIn &in) {
-    const uint32_t cols = a.blocks * CTOX_BLOCK_LEN, xm = a.xmode, dh = a.head_dim;
+__device__ __forceinline__ void frag_group_loads(const TileMatvecArgs &a, uint32_t grp, uint32_t lane, GroupIn &in,
+                                                 uint32_t xm) {
+    const uint32_t cols = a.blocks * CTOX_BLOCK_LEN, dh = a.head_dim;
     const uint32_t col = (4 * grp + (lane >> 4)) * CTOX_BLOCK_LEN + 4 * (lane & 15);
     const uint32_t sbytes = a.s_in_kind == CTOX_KSCALE_F32 ? 4u : 2u;
     const __amdgpu_buffer_rsrc_t ar = f32_rsrc(a.input, xm == 2 ? a.off + cols : cols);
@@ -160,9 +161,9 @@ __device__ __forceinline__ float tl_silu(float v) { return v / (1.0f + expf(-v))
 template <int DT>
 __device__ __forceinline__ float4 frag_group_build(const TileMatvecArgs &a, uint32_t grp, uint32_t lane,
                                                    const GroupIn &in, float inv, bool keep, int8_t *frag,
-                                                   uint32_t bstride = 192, float *x_out = nullptr,
-                                                   float *norm_out = nullptr) {
-    const uint32_t g = lane >> 4, m = lane & 15, xm = a.xmode;
+                                                   uint32_t bstride, float *x_out, float *norm_out,
+                                                   uint32_t xm) {
+    const uint32_t g = lane >> 4, m = lane & 15;
     const bool in_matrix = (4 * grp + g) * CTOX_BLOCK_LEN + 4 * m < a.blocks * CTOX_BLOCK_LEN;
     float xa[4], yb[4], wv[4], v[4];
 #pragma unroll
@@ -347,9 +348,14 @@ __device__ __forceinline__ void residual_tile_sum(const TileMatvecArgs &a, uint3
     if (mine && j == 0) a.res_sq[tile] = s;
 }
 
-template <int DT, int U, int AB, int ARR>
+template <int DT, int U, int AB, int ARR, int XM = -1>
 __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
     using C = TlCfg<DT>;
+    // XM >= 0: the input transform fixed at compile time, so each kernel
+    // holds only its own transform's registers; XM = 5 is the residual norm
+    // (xmode 1) with the producer's sums of squares (sq_n > 0).
+    constexpr bool SQ = XM == 5;
+    const uint32_t xmode = SQ ? 1u : (XM >= 0 ? (uint32_t)XM : a.xmode);
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t v = __builtin_amdgcn_readfirstlane(blockIdx.x * 4u + (threadIdx.x >> 6));
     const uint32_t c = v / a.segs, s = v - c * a.segs;
@@ -389,14 +395,14 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
     GroupIn gin;
     v4i hx[8], hd[8];
     float sqv[2] = {0.0f, 0.0f};
-    if (AB && a.xmode == 1 && a.sq_n) {
+    if (AB && xmode == 1 && (SQ || a.sq_n)) {
         // The producer's per-tile sums of squares (at most 512).
 #pragma unroll
         for (int k = 0; k < 2; k++) {
             const uint32_t t = threadIdx.x + 256 * k;
             sqv[k] = t < a.sq_n ? a.sq_in[t] : 0.0f;
         }
-    } else if (AB && a.xmode == 1) {
+    } else if (AB && xmode == 1 && !SQ) {
         const uint32_t cols = a.blocks * CTOX_BLOCK_LEN;
         const __amdgpu_buffer_rsrc_t xr = f32_rsrc(a.input, cols), dr = f32_rsrc(a.delta, cols);
 #pragma unroll
@@ -405,7 +411,7 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
             hd[k] = __builtin_amdgcn_raw_buffer_load_b128(dr, (threadIdx.x + 256 * k) * 16, 0, 0);
         }
     }
-    if (AB) frag_group_loads(a, c * 4 + wg_wave, lane, gin);
+    if (AB) frag_group_loads(a, c * 4 + wg_wave, lane, gin, xmode);
     __builtin_amdgcn_sched_barrier(0);  // activation loads stay ahead of the weight loads
     // A CU returns vector-memory data in request order. For a plain input
     // (xmode 0: the crate's fused matvec on a resident matrix) a short pause
@@ -415,7 +421,7 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
     // 9.15 -> 8.9 us, config 1 11.87 -> 11.70; pauses of 6-9 measured alike, 4
     // and 12 slower). Launches whose input is a producer's transform (the
     // decode engine's) measured slower with it, so they do not pause.
-    if (AB && a.xmode == 0) __builtin_amdgcn_s_sleep(7);
+    if (AB && xmode == 0) __builtin_amdgcn_s_sleep(7);
     __builtin_amdgcn_sched_barrier(0);
     TileUnit<DT> u[U];
 #pragma unroll
@@ -433,9 +439,9 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
     if (AB) {
         __shared__ float wss[4];
         float inv = 0.0f;
-        if (a.xmode == 1) {
+        if (xmode == 1) {
             float ss = 0.0f;
-            if (a.sq_n) {
+            if (SQ || a.sq_n) {
                 ss = sqv[0] + sqv[1];
             } else {
 #pragma unroll
@@ -456,7 +462,7 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
         }
         const bool keep = ((blockIdx.x * 4u) % a.segs) == 0;  // segment 0 of the chunk
         const float4 k = frag_group_build<DT>(a, c * 4 + wg_wave, lane, gin, inv, keep, xs + wg_wave * 768, 192,
-                                              a.x_out, a.norm_out);
+                                              a.x_out, a.norm_out, xmode);
         if (j == 0) kqs[4 * wg_wave + g] = k;
         lds_barrier();  // orders LDS only: the weight loads stay in flight
         if (t0 >= a.tiles) return;
@@ -570,8 +576,8 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
     residual_tile_sum(a, tile, row, mine, y, j, e);
 }
 
-// ctox_q{2,4}_mv_tile{U}_gfx950 take prep-staged fragments; the _x
-// variants build them from x and s_in. The _arrive variants combine by
+// ctox_q{2,4}_mv_tile{U}_gfx950 take prep-staged fragments (the _x{T}
+// kernels below build them from the input). The _arrive variants combine by
 // arrival (launches larger than the device holds at once).
 #define CTOX_TILE_KERNEL(name, dt, u, ab) \
     extern "C" __global__ __launch_bounds__(256) void name(TileMatvecArgs a) { tile_matvec<dt, u, ab, 0>(a); } \
@@ -584,14 +590,28 @@ CTOX_TILE_KERNEL(ctox_q4_mv_tile1_gfx950, 1, 1, 0)
 CTOX_TILE_KERNEL(ctox_q4_mv_tile2_gfx950, 1, 2, 0)
 CTOX_TILE_KERNEL(ctox_q4_mv_tile3_gfx950, 1, 3, 0)
 CTOX_TILE_KERNEL(ctox_q4_mv_tile4_gfx950, 1, 4, 0)
-CTOX_TILE_KERNEL(ctox_q2_mv_tile1x_gfx950, 0, 1, 1)
-CTOX_TILE_KERNEL(ctox_q2_mv_tile2x_gfx950, 0, 2, 1)
-CTOX_TILE_KERNEL(ctox_q2_mv_tile3x_gfx950, 0, 3, 1)
-CTOX_TILE_KERNEL(ctox_q2_mv_tile4x_gfx950, 0, 4, 1)
-CTOX_TILE_KERNEL(ctox_q4_mv_tile1x_gfx950, 1, 1, 1)
-CTOX_TILE_KERNEL(ctox_q4_mv_tile2x_gfx950, 1, 2, 1)
-CTOX_TILE_KERNEL(ctox_q4_mv_tile3x_gfx950, 1, 3, 1)
-CTOX_TILE_KERNEL(ctox_q4_mv_tile4x_gfx950, 1, 4, 1)
+// ctox_q{2,4}_mv_tile{U}x{T}_gfx950: the in-kernel build with the input
+// transform fixed at compile time, T = xmode 0..4 (x0: the crate's fused
+// matvec on a plain input) or 5 (the residual norm with the producer's sums
+// of squares).
+#define CTOX_TILE_XM_KERNEL(name, dt, u, xm) \
+    extern "C" __global__ __launch_bounds__(256) void name(TileMatvecArgs a) { tile_matvec<dt, u, 1, 0, xm>(a); } \
+    extern "C" __global__ __launch_bounds__(256) void name##_arrive(TileMatvecArgs a) { tile_matvec<dt, u, 1, 1, xm>(a); }
+#define CTOX_TILE_XM_KERNELS(xm) \
+    CTOX_TILE_XM_KERNEL(ctox_q2_mv_tile1x##xm##_gfx950, 0, 1, xm) \
+    CTOX_TILE_XM_KERNEL(ctox_q2_mv_tile2x##xm##_gfx950, 0, 2, xm) \
+    CTOX_TILE_XM_KERNEL(ctox_q2_mv_tile3x##xm##_gfx950, 0, 3, xm) \
+    CTOX_TILE_XM_KERNEL(ctox_q2_mv_tile4x##xm##_gfx950, 0, 4, xm) \
+    CTOX_TILE_XM_KERNEL(ctox_q4_mv_tile1x##xm##_gfx950, 1, 1, xm) \
+    CTOX_TILE_XM_KERNEL(ctox_q4_mv_tile2x##xm##_gfx950, 1, 2, xm) \
+    CTOX_TILE_XM_KERNEL(ctox_q4_mv_tile3x##xm##_gfx950, 1, 3, xm) \
+    CTOX_TILE_XM_KERNEL(ctox_q4_mv_tile4x##xm##_gfx950, 1, 4, xm)
+CTOX_TILE_XM_KERNELS(0)
+CTOX_TILE_XM_KERNELS(1)
+CTOX_TILE_XM_KERNELS(2)
+CTOX_TILE_XM_KERNELS(3)
+CTOX_TILE_XM_KERNELS(4)
+CTOX_TILE_XM_KERNELS(5)
 
 
 
@@ -1049,7 +1069,7 @@ __device__ __forceinline__ void tile_matvec_mx(const TileMatvecArgs &a) {
         gin.b = *(const v4i *)(src + 1024 + lane * 16);
         const float4 k = frag_group_build<DT>(a, grp, lane, gin, inv, keep, xas + ((4 * wg) * M + t) * 192, M * 192,
                                               a.x_out ? a.x_out + (size_t)t * cols : nullptr,
-                                              a.norm_out ? a.norm_out + (size_t)t * cols : nullptr);
+                                              a.norm_out ? a.norm_out + (size_t)t * cols : nullptr, a.xmode);
         if (j == 0) kqs[(4 * wg + g) * M + t] = k;
     }
     lds_barrier();  // fragments and constants of every group and row

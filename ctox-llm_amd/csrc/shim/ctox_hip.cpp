@@ -162,9 +162,12 @@ struct ctox_hip_backend {
     // Tiled-layout batch-1 kernels per dtype [Q2, Q4] and row tiles per wave
     // (1..4), and the prepare-time repack.
     hipFunction_t tile[2][CTOX_TILE_MAXU] = {};
-    // The same with the activation fragments built inside the kernel.
-    hipFunction_t tilex[2][CTOX_TILE_MAXU] = {};
-    hipFunction_t tile_arr[2][2][CTOX_TILE_MAXU] = {};  // [staged|built][q4][u - 1], combine by arrival
+    // The same with the activation fragments built inside the kernel, one
+    // kernel per input transform T (xmode 0..4; 5: the residual norm with
+    // the producer's sums of squares): [T][q4][u - 1].
+    hipFunction_t tilex[6][2][CTOX_TILE_MAXU] = {};
+    // Combine by arrival: [kind][q4][u - 1], kind 0 staged, 1 + T built.
+    hipFunction_t tile_arr[7][2][CTOX_TILE_MAXU] = {};
     hipFunction_t tilem[2][7] = {};      // [q4][rows - 2], 2..8 staged rows
     hipFunction_t tilem_arr[2][7] = {};  // combine by arrival
     // The same building the rows' fragments in the kernel, per row count 2..5.
@@ -181,7 +184,7 @@ struct ctox_hip_backend {
     int cus = 0;
     uint32_t tile_u = 0;  // CTOX_TILE_U: fixed row tiles per wave (0 = planned)
     int arrive = -1;      // CTOX_ARRIVE: 1 / 0 forces the tiled combine by arrival / by the last chunk
-    uint32_t tile_cap[2][2][CTOX_TILE_MAXU] = {};  // [staged|built][q4][u - 1]: workgroups resident at once
+    uint32_t tile_cap[7][2][CTOX_TILE_MAXU] = {};  // [kind][q4][u - 1]: workgroups resident at once
     uint32_t tilem_cap[2][7] = {};                  // [q4][rows - 2], same for the small-M kernels
     uint32_t tilemx_cap[2][4] = {};                 // [q4][rows - 2]
     // Tiled matvec chunk partials (64-bit slots tagged with a launch sequence
@@ -569,7 +572,11 @@ ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy 
     // already arrived.
     const bool combine = t.chunks > 1 && !(xf && xf->parts_out);
     const size_t wgs = ((size_t)segs * t.chunks + 3) / 4;
-    const bool arrive = combine && (b->arrive >= 0 ? b->arrive != 0 : wgs > b->tile_cap[d_input ? 1 : 0][q4][u - 1]);
+    // kind: 0 staged fragments, else 1 + the input transform of the build
+    // (5: the residual norm with the producer's sums of squares).
+    const uint32_t xm = xf ? xf->xmode : 0u;
+    const int kind = !d_input ? 0 : 1 + (xm == 1 && xf->sq_in && xf->sq_n ? 5 : (int)xm);
+    const bool arrive = combine && (b->arrive >= 0 ? b->arrive != 0 : wgs > b->tile_cap[kind][q4][u - 1]);
     const size_t slot_bytes = (size_t)(arrive ? t.chunks : t.chunks - 1) * t.tiles * CTOX_TILE_ROWS * sizeof(uint64_t);
     if (ps && combine && (slot_bytes > ps->bytes || (arrive && t.tiles > ps->arrive_n)))
         return fail(CTOX_ERR_MEMORY_BUDGET, "combine slots need %zu bytes, the static scratch holds %zu", slot_bytes,
@@ -619,8 +626,8 @@ ctox_status run_tile_matvec(ctox_hip_backend *b, int32_t dtype, const TiledCopy 
         a.a_parts = xf->a_parts;
         a.a_pstride = xf->a_pstride;
     }
-    hipFunction_t f = arrive ? b->tile_arr[d_input ? 1 : 0][q4][u - 1]
-                             : (d_input ? b->tilex[q4][u - 1] : b->tile[q4][u - 1]);
+    hipFunction_t f = arrive ? b->tile_arr[kind][q4][u - 1]
+                             : (kind ? b->tilex[kind - 1][q4][u - 1] : b->tile[q4][u - 1]);
     return launch(f, dim3((unsigned)((waves + 3) / 4)), dim3(256), s, a, "ctox_q*_mv_tile*_gfx950");
 }
 
@@ -907,18 +914,10 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                {&b->tile[0][2], "ctox_q2_mv_tile3_gfx950"}, {&b->tile[0][3], "ctox_q2_mv_tile4_gfx950"},
                {&b->tile[1][0], "ctox_q4_mv_tile1_gfx950"}, {&b->tile[1][1], "ctox_q4_mv_tile2_gfx950"},
                {&b->tile[1][2], "ctox_q4_mv_tile3_gfx950"}, {&b->tile[1][3], "ctox_q4_mv_tile4_gfx950"},
-               {&b->tilex[0][0], "ctox_q2_mv_tile1x_gfx950"}, {&b->tilex[0][1], "ctox_q2_mv_tile2x_gfx950"},
-               {&b->tilex[0][2], "ctox_q2_mv_tile3x_gfx950"}, {&b->tilex[0][3], "ctox_q2_mv_tile4x_gfx950"},
-               {&b->tilex[1][0], "ctox_q4_mv_tile1x_gfx950"}, {&b->tilex[1][1], "ctox_q4_mv_tile2x_gfx950"},
-               {&b->tilex[1][2], "ctox_q4_mv_tile3x_gfx950"}, {&b->tilex[1][3], "ctox_q4_mv_tile4x_gfx950"},
                {&b->tile_arr[0][0][0], "ctox_q2_mv_tile1_gfx950_arrive"}, {&b->tile_arr[0][0][1], "ctox_q2_mv_tile2_gfx950_arrive"},
                {&b->tile_arr[0][0][2], "ctox_q2_mv_tile3_gfx950_arrive"}, {&b->tile_arr[0][0][3], "ctox_q2_mv_tile4_gfx950_arrive"},
                {&b->tile_arr[0][1][0], "ctox_q4_mv_tile1_gfx950_arrive"}, {&b->tile_arr[0][1][1], "ctox_q4_mv_tile2_gfx950_arrive"},
                {&b->tile_arr[0][1][2], "ctox_q4_mv_tile3_gfx950_arrive"}, {&b->tile_arr[0][1][3], "ctox_q4_mv_tile4_gfx950_arrive"},
-               {&b->tile_arr[1][0][0], "ctox_q2_mv_tile1x_gfx950_arrive"}, {&b->tile_arr[1][0][1], "ctox_q2_mv_tile2x_gfx950_arrive"},
-               {&b->tile_arr[1][0][2], "ctox_q2_mv_tile3x_gfx950_arrive"}, {&b->tile_arr[1][0][3], "ctox_q2_mv_tile4x_gfx950_arrive"},
-               {&b->tile_arr[1][1][0], "ctox_q4_mv_tile1x_gfx950_arrive"}, {&b->tile_arr[1][1][1], "ctox_q4_mv_tile2x_gfx950_arrive"},
-               {&b->tile_arr[1][1][2], "ctox_q4_mv_tile3x_gfx950_arrive"}, {&b->tile_arr[1][1][3], "ctox_q4_mv_tile4x_gfx950_arrive"},
                {&b->tilemx[0][0], "ctox_q2_mv_tilemx2_gfx950"}, {&b->tilemx[0][1], "ctox_q2_mv_tilemx3_gfx950"},
                {&b->tilemx[0][2], "ctox_q2_mv_tilemx4_gfx950"}, {&b->tilemx[0][3], "ctox_q2_mv_tilemx5_gfx950"},
                {&b->tilemx[1][0], "ctox_q4_mv_tilemx2_gfx950"}, {&b->tilemx[1][1], "ctox_q4_mv_tilemx3_gfx950"},
@@ -943,6 +942,21 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
                         hipGetErrorString(le));
         }
     }
+    // The in-kernel build kernels, one per input transform.
+    for (int x = 0; x < 6 && le == hipSuccess; x++)
+        for (int q = 0; q < 2 && le == hipSuccess; q++)
+            for (int u = 0; u < CTOX_TILE_MAXU && le == hipSuccess; u++)
+                for (int arr = 0; arr < 2 && le == hipSuccess; arr++) {
+                    char name[64];
+                    std::snprintf(name, sizeof name, "ctox_q%d_mv_tile%dx%d_gfx950%s", q ? 4 : 2, u + 1, x,
+                                  arr ? "_arrive" : "");
+                    le = hipModuleGetFunction(arr ? &b->tile_arr[1 + x][q][u] : &b->tilex[x][q][u], b->module, name);
+                    if (le != hipSuccess) {
+                        ctox_hip_backend_destroy(b);
+                        return fail(CTOX_ERR_UNSUPPORTED_OPERATION, "kernel %s missing from code object: %s", name,
+                                    hipGetErrorString(le));
+                    }
+                }
     // The small-M kernels for staged rows, one per row count 2..8.
     for (int q = 0; q < 2 && le == hipSuccess; q++)
         for (int m = 0; m < 7 && le == hipSuccess; m++)
@@ -979,7 +993,7 @@ extern "C" ctox_status ctox_hip_backend_create(int device, ctox_hip_backend **ou
     for (int q = 0; q < 2; q++) {
         for (int u = 0; u < CTOX_TILE_MAXU; u++) {
             b->tile_cap[0][q][u] = cap(b->tile[q][u]);
-            b->tile_cap[1][q][u] = cap(b->tilex[q][u]);
+            for (int x = 0; x < 6; x++) b->tile_cap[1 + x][q][u] = cap(b->tilex[x][q][u]);
         }
         for (int m = 0; m < 7; m++) b->tilem_cap[q][m] = cap(b->tilem[q][m]);
         for (int r = 0; r < 4; r++) b->tilemx_cap[q][r] = cap(b->tilemx[q][r]);
