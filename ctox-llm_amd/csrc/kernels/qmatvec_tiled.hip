@@ -413,16 +413,6 @@ __device__ __forceinline__ void tile_matvec(const TileMatvecArgs &a) {
     }
     if (AB) frag_group_loads(a, c * 4 + wg_wave, lane, gin, xmode);
     __builtin_amdgcn_sched_barrier(0);  // activation loads stay ahead of the weight loads
-    // A CU returns vector-memory data in request order. For a plain input
-    // (xmode 0: the crate's fused matvec on a resident matrix) a short pause
-    // (7 x 64 cycles) before the weight loads lets the workgroups dispatched
-    // to the CU at about the same time queue their activation loads first, so
-    // their fragment builds are not held behind this one's weights (config 2
-    // 9.15 -> 8.9 us, config 1 11.87 -> 11.70; pauses of 6-9 measured alike, 4
-    // and 12 slower). Launches whose input is a producer's transform (the
-    // decode engine's) measured slower with it, so they do not pause.
-    if (AB && xmode == 0) __builtin_amdgcn_s_sleep(7);
-    __builtin_amdgcn_sched_barrier(0);
     TileUnit<DT> u[U];
 #pragma unroll
     for (int k = 0; k < U; k++) {
