@@ -31,8 +31,8 @@ HBM_PEAK_GBS = 8000.0
 REPLICATES = 5
 DRAFT_VOCAB = 32768
 INFINITY_CACHE = 256 << 20
-HEAD_KERNEL = "ctox_q2_mv_tile2x_gfx950"
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "ctox_q2_mv_tile2x_gfx950.config2.traffic.txt")
+HEAD_KERNEL = "ctox_q2_mv_tile2x0_gfx950"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "ctox_q2_mv_tile2x0_gfx950.config2.traffic.txt")
 
 
 def log(*a):
