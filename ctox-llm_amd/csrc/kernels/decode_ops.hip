@@ -406,10 +406,11 @@ extern "C" __global__ __launch_bounds__(1024) void ctox_pick_final_gfx950(Accept
 // (the crate's sort: ties go to the later token); a candidate is the 64-bit
 // key (order-preserving bits of the scaled logit << 32) | token, so one
 // integer comparison orders them. Stage 1 (one workgroup per 4096 logits)
-// sorts its part's keys in LDS (bitonic, descending) and keeps the first
-// top_k; stage 2 sorts the parts' candidates and one thread runs the crate's
-// sequential arithmetic over the top_k: exp weights, the nucleus cut at
-// top_p of their sum, and the cumulative search of draw x the nucleus total.
+// keeps its part's top_k keys (a radix select, no sort); stage 2 selects the
+// top_k of the parts' candidates the same way, sorts only those (bitonic, in
+// LDS) and one thread runs the crate's sequential arithmetic over them: exp
+// weights, the nucleus cut at top_p of their sum, and the cumulative search
+// of draw x the nucleus total.
 // out = {token, status, nucleus length, nucleus total bits}; status 0 is
 // success, 2 a non-finite logit or scaled logit, 4 an invalid normalization.
 __device__ __forceinline__ uint32_t topk_key(float v) {
@@ -439,35 +440,128 @@ __device__ __forceinline__ void bitonic_desc(uint64_t *sk, uint32_t n) {
         }
 }
 
+// Workgroup-wide selection of the k largest of the keys the threads hold
+// (N per thread; 0 marks an absent key; the keys present are distinct, the
+// token being part of each, and at least k of them are present): a radix
+// select over the key's bytes from the top. Each pass counts, in 256 LDS
+// bins, the next byte of the keys that share the bytes fixed so far; one
+// wave finds the bin holding the k-th largest; the pass that finds that bin
+// holding exactly the keys still missing ends the search. Returns the
+// threshold: a key is among the k largest iff (key >> shift) >= (thr >> shift).
+template <int N>
+__device__ __forceinline__ uint64_t topk_threshold(const uint64_t (&key)[N], uint32_t k, uint32_t *hist,
+                                                   uint32_t *sel, int &shift_out) {
+    uint64_t prefix = 0;
+    uint32_t r = k;
+    int shift = 56;
+    for (;;) {
+        for (uint32_t i = threadIdx.x; i < 256; i += blockDim.x) hist[i] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int n = 0; n < N; n++) {
+            const bool same = shift == 56 || (key[n] >> (shift + 8)) == (prefix >> (shift + 8));
+            if (key[n] != 0 && same) atomicAdd(&hist[(uint32_t)(key[n] >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            // Lane l holds bins 255 - 4l .. 252 - 4l (descending), so the
+            // lanes' inclusive prefix sums count the keys in higher bins.
+            const uint32_t l = threadIdx.x;
+            uint32_t c[4], t = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                c[j] = hist[255 - 4 * l - j];
+                t += c[j];
+            }
+            uint32_t inc = t;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t y = __shfl_up(inc, o);
+                if (l >= (uint32_t)o) inc += y;
+            }
+            uint32_t above = inc - t;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (above < r && r <= above + c[j]) {
+                    sel[0] = 255 - 4 * l - j;
+                    sel[1] = above;
+                    sel[2] = c[j];
+                }
+                above += c[j];
+            }
+        }
+        __syncthreads();
+        const uint32_t b = sel[0], above = sel[1], cnt = sel[2];
+        prefix |= (uint64_t)b << shift;
+        r -= above;
+        if (cnt == r || shift == 0) break;
+        shift -= 8;
+    }
+    shift_out = shift;
+    return prefix;
+}
+
+// Stage 1: the top_k keys of one part (unordered; zeros past the part's
+// logits when it holds fewer than top_k).
 extern "C" __global__ __launch_bounds__(1024) void ctox_topk_part_gfx950(TopkArgs a) {
-    __shared__ uint64_t sk[CTOX_TOPK_PART];
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t sel[4];
+    constexpr int N = CTOX_TOPK_PART / 1024;
     const uint32_t b0 = blockIdx.x * CTOX_TOPK_PART;
     const uint32_t n = min((uint32_t)CTOX_TOPK_PART, a.vocab - b0);
     int bad = 0;
-    for (uint32_t i = threadIdx.x; i < CTOX_TOPK_PART; i += blockDim.x) {
-        uint64_t key = 0;  // below every candidate
+    uint64_t key[N];
+#pragma unroll
+    for (int j = 0; j < N; j++) {
+        const uint32_t i = threadIdx.x + 1024 * j;
+        key[j] = 0;  // below every candidate
         if (i < n) {
             const float x = a.logits[b0 + i], v = x * a.inv_temperature;
             bad |= !__builtin_isfinite(x) | !__builtin_isfinite(v);
-            key = ((uint64_t)topk_key(v) << 32) | (b0 + i);
+            key[j] = ((uint64_t)topk_key(v) << 32) | (b0 + i);
         }
-        sk[i] = key;
     }
+    if (threadIdx.x == 0) sel[3] = 0;
     bad = __syncthreads_or(bad);
-    bitonic_desc(sk, CTOX_TOPK_PART);
-    for (uint32_t r = threadIdx.x; r < a.top_k; r += blockDim.x) a.cand[(size_t)blockIdx.x * a.top_k + r] = sk[r];
+    uint64_t *out = a.cand + (size_t)blockIdx.x * a.top_k;
+    if (n <= a.top_k) {
+#pragma unroll
+        for (int j = 0; j < N; j++) {
+            const uint32_t i = threadIdx.x + 1024 * j;
+            if (i < a.top_k) out[i] = key[j];
+        }
+    } else {
+        int shift = 0;
+        const uint64_t thr = topk_threshold<N>(key, a.top_k, hist, sel, shift);
+#pragma unroll
+        for (int j = 0; j < N; j++)
+            if (key[j] != 0 && (key[j] >> shift) >= (thr >> shift)) out[atomicAdd(&sel[3], 1u)] = key[j];
+    }
     if (threadIdx.x == 0) a.flags[blockIdx.x] = bad ? 1u : 0u;
 }
 
+// Stage 2: the top_k of the parts' candidates, sorted (descending key, i.e.
+// scaled logit then token), then the crate's sequential arithmetic.
 extern "C" __global__ __launch_bounds__(1024) void ctox_topk_final_gfx950(TopkArgs a) {
-    __shared__ uint64_t sk[CTOX_TOPK_CANDS];  // parts * top_k <= CTOX_TOPK_CANDS (host-checked)
+    __shared__ uint64_t sk[CTOX_TOPK_MAX];
     __shared__ float w[CTOX_TOPK_MAX];
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t sel[4];
+    constexpr int N = CTOX_TOPK_CANDS / 1024;
     const uint32_t n = a.parts * a.top_k;
+    const uint32_t len = min(a.top_k, a.vocab);
     uint32_t n2 = 1;
-    while (n2 < n) n2 <<= 1;
+    while (n2 < len) n2 <<= 1;
     int bad = 0;
-    for (uint32_t i = threadIdx.x; i < n2; i += blockDim.x) sk[i] = i < n ? a.cand[i] : 0;
+    uint64_t key[N];
+#pragma unroll
+    for (int j = 0; j < N; j++) {
+        const uint32_t i = threadIdx.x + 1024 * j;
+        key[j] = i < n ? a.cand[i] : 0;
+    }
     for (uint32_t p = threadIdx.x; p < a.parts; p += blockDim.x) bad |= a.flags[p] != 0;
+    for (uint32_t i = threadIdx.x; i < n2; i += blockDim.x) sk[i] = 0;
+    if (threadIdx.x == 0) sel[3] = 0;
     bad = __syncthreads_or(bad);
     if (bad) {
         if (threadIdx.x == 0) {
@@ -478,10 +572,15 @@ extern "C" __global__ __launch_bounds__(1024) void ctox_topk_final_gfx950(TopkAr
         }
         return;
     }
+    int shift = 0;
+    const uint64_t kthr = topk_threshold<N>(key, len, hist, sel, shift);
+#pragma unroll
+    for (int j = 0; j < N; j++)
+        if (key[j] != 0 && (key[j] >> shift) >= (kthr >> shift)) sk[atomicAdd(&sel[3], 1u)] = key[j];
+    __syncthreads();
     bitonic_desc(sk, n2);
     if (threadIdx.x != 0) return;
     // Sampler::sample_with_draw from the sort on, in its order of operations.
-    const uint32_t len = min(a.top_k, a.vocab);
     const float m = topk_value((uint32_t)(sk[0] >> 32));
     float norm = 0.0f;
     for (uint32_t r = 0; r < len; r++) {
