@@ -648,7 +648,7 @@ __device__ __forceinline__ void pa_tile16(const GqaArgs &a, LDS &L, const int8_t
         L.vws[wave][4 * lg + (li >> 2)][li & 3] = ws;
         const float mx = pa_max_x32(pa_max_x16(pa_max_rot48(ws)));
         int ex = 0;
-        frexpf(mx, &ex);  // mx < 2^ex: B = P * ws * 2^(25 - E) < 2^14
+        frexpf(mx, &ex);  // mx < 2^ex: B = P * ws * 2^(25 - E) < 2^14 P, P < 2
         const int E = min(30, max(1, 11 + ex));
 #pragma unroll
         for (int b = 0; b < 4; b++) Eb[b] = __builtin_amdgcn_readlane(E, b);  // lane b holds block b's
@@ -711,12 +711,18 @@ __device__ __forceinline__ void pa_tile16(const GqaArgs &a, LDS &L, const int8_t
             mt = fmaxf(mt, sc[c]);
         }
         mt = pa_max_x32(pa_max_x16(mt));
-        const float mn = fmaxf(st.m[r], mt);
+        // The reference maximum moves only when the tile's exceeds it by
+        // more than 1 (base 2): probabilities then stay below 2, which the V
+        // operand's exponent headroom allows (B < 2^15), and most tiles skip
+        // the accumulators' rescale. Leaving the empty state (m = -inf: the
+        // accumulators are zero) needs no rescale either.
+        const bool move = mt > st.m[r] + 1.0f;
+        const float mn = move ? mt : st.m[r];
         float alpha = 1.0f;
         if (mn == -INFINITY) {
             p[r][0] = p[r][1] = p[r][2] = p[r][3] = 0.0f;
         } else {
-            alpha = __builtin_amdgcn_exp2f(st.m[r] - mn);
+            if (move && st.m[r] != -INFINITY) alpha = __builtin_amdgcn_exp2f(st.m[r] - mn);
 #pragma unroll
             for (int c = 0; c < 4; c++) p[r][c] = __builtin_amdgcn_exp2f(sc[c] - mn);
         }
