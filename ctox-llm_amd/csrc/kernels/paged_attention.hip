@@ -614,10 +614,12 @@ __device__ __forceinline__ uint32_t pa_pk(float x, float y) {
 
 // Q4: the tile's precision (-1: read from the tile; 0 / 1: a constant, so the
 // block sizes, offsets, code masks and selectors fold).
-template <int R, int Q4, class LDS>
+// SH: the queries share one fixed point per block, folded into qsl (the
+// K block scales); otherwise qsl is 1 and each query's 2^-E applies.
+template <int R, int Q4, bool SH, class LDS>
 __device__ __forceinline__ void pa_tile16(const GqaArgs &a, LDS &L, const int8_t *qb, uint32_t wave, uint32_t tb, uint32_t h,
                                           uint32_t li, uint32_t lg, const PaTile &T, const uint32_t *stage,
-                                          PaState<R> &st) {
+                                          float qsl, PaState<R> &st) {
     const uint32_t lane = 16 * lg + li;
     const bool q4 = Q4 >= 0 ? Q4 == 1 : T.q4 != 0;
     bool present[4];
@@ -636,9 +638,9 @@ __device__ __forceinline__ void pa_tile16(const GqaArgs &a, LDS &L, const int8_t
     }
     // (absent tokens were staged as zeros: zero codes and scales)
     const uint32_t vsb = pa_s16(stage + (4 * lg + (li >> 2)) * PA_SROW + 34, (li & 3) * bs);
-    {   // K block scale of (token li, block lg) for the score epilogue
+    {   // K block scale of (token li, block lg) times the queries' 2^-E of that block
         const uint32_t kind = pa_kind(rk.meta);
-        const float sc = pa_half(rk.meta & 0xffffu);
+        const float sc = pa_half(rk.meta & 0xffffu) * qsl;
         L.scl[wave][li][lg] = kind == 2 ? sc * (1.0f / 15.0f) : (kind == 1 ? sc * (1.0f / 3.0f) : 0.0f);
     }
     int32_t Eb[4];  // the tile's exponent field per V block
@@ -695,7 +697,7 @@ __device__ __forceinline__ void pa_tile16(const GqaArgs &a, LDS &L, const int8_t
                 const uint32_t U = (uint32_t)acc[0][c] + ((uint32_t)acc[1][c] << 8) + ((uint32_t)acc[2][c] << 16);
                 const int32_t t = (int32_t)(2u * U - kx);
                 const float fb = b == 0 ? f[c].x : b == 1 ? f[c].y : b == 2 ? f[c].z : f[c].w;
-                s[r][c] = fmaf(fb * st.qscale[r][b], (float)t, s[r][c]);
+                s[r][c] = fmaf(SH ? fb : fb * st.qscale[r][b], (float)t, s[r][c]);
             }
         }
     }
@@ -820,20 +822,46 @@ __device__ __forceinline__ void pa_prep_load(const GqaArgs &a, uint32_t h, float
 // X = l0 + 256 l1 + 65536 l2, dims reordered to the K operand's order
 // within each 16. One thread per (query, block, quarter); it also leaves 2^-E
 // and the limb sums for the score epilogue.
-template <int R>
+// SH: one fixed point per 64-dim block for all the workgroup's queries (2^E
+// from the largest |q| of the block over every query; the query vectors are
+// RMS-normed, so their block maxima are alike), so the score epilogue folds
+// 2^-E into the keys' block scales. bmx: 16 LDS floats for that maximum.
+template <int R, bool SH = false>
 __device__ __forceinline__ void pa_prep_compute(const GqaArgs &a, const float (&q)[R][16], int8_t *qb,
-                                                float (*qsc)[4], int32_t (*xs)[4][3]) {
+                                                float (*qsc)[4], int32_t (*xs)[4][3], float *bmx = nullptr) {
+    float mxs[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 16; d++) mx = fmaxf(mx, fabsf(q[r][d]));
+        mx = fmaxf(mx, __shfl_xor(mx, 1));
+        mx = fmaxf(mx, __shfl_xor(mx, 2));
+        mxs[r] = mx;
+    }
+    if (SH) {
+        // Lanes 4 b .. 4 b + 3 of each 16-lane row hold block b: the wave's
+        // and then the workgroup's maximum per block.
+        float m = mxs[0];
+#pragma unroll
+        for (int r = 1; r < R; r++) m = fmaxf(m, mxs[r]);
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        if (lane < 16 && (lane & 3) == 0) bmx[wave * 4 + lane / 4] = m;
+        lds_barrier();
+        const uint32_t b = (threadIdx.x / 4) % 4;
+        m = fmaxf(fmaxf(bmx[b], bmx[4 + b]), fmaxf(bmx[8 + b], bmx[12 + b]));
+#pragma unroll
+        for (int r = 0; r < R; r++) mxs[r] = m;
+    }
 #pragma unroll
     for (int r = 0; r < R; r++) {
         const uint32_t i = threadIdx.x + 256 * r;
         // Four consecutive lanes share one (query, block), a quarter of it each.
         const uint32_t qi = i / 16, b = (i / 4) % 4, part = i % 4;
         const float *qv = q[r];
-        float mx = 0.0f;
-#pragma unroll
-        for (int d = 0; d < 16; d++) mx = fmaxf(mx, fabsf(qv[d]));
-        mx = fmaxf(mx, __shfl_xor(mx, 1));
-        mx = fmaxf(mx, __shfl_xor(mx, 2));
+        const float mx = mxs[r];
         int ex = 0;
         frexpf(mx, &ex);  // mx < 2^ex
         const float e = mx > 0.0f ? ldexpf(1.0f, 21 - ex) : 0.0f;
@@ -897,8 +925,9 @@ struct PaLds16 {
     } u;
     float scl[4][16][4];       // [wave][token of tile][block]: K scale / 15 (Q4) or / 3 (Q2)
     float vws[4][16][4];       // [wave][token][V block]: 2 V scale / K
-    float qsc[R * 16][4];      // [query][block]: 2^-E of the query's fixed point
+    float qsc[R * 16][4];      // [query][block]: 2^-E of the (shared) fixed point
     int32_t xs[R * 16][4][3];  // [query][block][limb]: limb sums
+    float bmx[16];             // [wave][block]: largest |q| (the prep's shared fixed point)
 };
 
 // grid (splits, kv heads), 256 threads; four waves take contiguous runs of
@@ -922,7 +951,11 @@ __device__ __forceinline__ void paged_gqa_partial16(const GqaArgs &a) {
     PaStage sg;
     PaTile PA = pa_tile_of(a, dsc, 0);
     pa_issue_stage(a, PA, t0 * 16, h, lane, sg);
-    pa_prep_compute<R>(a, qv, L.u.run.limbs, L.qsc, L.xs);
+    // Two query tiles share one fixed point per block (the 16 multiplies per
+    // tile it saves outweigh the prep's extra barrier; one tile keeps its
+    // per-query fixed point).
+    constexpr bool SH = R > 1;
+    pa_prep_compute<R, SH>(a, qv, L.u.run.limbs, L.qsc, L.xs, L.bmx);
     PaState<R> st;
 #pragma unroll
     for (int r = 0; r < R; r++) {
@@ -944,6 +977,7 @@ __device__ __forceinline__ void paged_gqa_partial16(const GqaArgs &a) {
             st.xst[r][b] = L.xs[16 * r + li][b][0] + 256 * L.xs[16 * r + li][b][1] + 65536 * L.xs[16 * r + li][b][2];
             st.corr[r][b] = 0.0f;
         }
+    const float qsl = SH ? L.qsc[0][lg] : 1.0f;  // shared: 2^-E of block lg, the same for every query
     // Tile k computes from the stage while tile k + 1's loads are in flight.
     // A wave whose tiles all lie in Q2 pages (most of a long context) runs
     // the tile loop with the precision folded in.
@@ -953,7 +987,7 @@ __device__ __forceinline__ void paged_gqa_partial16(const GqaArgs &a) {
             pa_stage_write(stage, lane, Q4 >= 0 ? Q4 == 1 : PA.q4 != 0, sg);
             const PaTile PN = pa_tile_of(a, dsc, tile + 1 - t0);
             pa_issue_stage(a, PN, (tile + 1) * 16, h, lane, sg);
-            pa_tile16<R, Q4>(a, L, L.u.run.limbs, wave, tile * 16, h, li, lg, PA, stage, st);
+            pa_tile16<R, Q4, SH>(a, L, L.u.run.limbs, wave, tile * 16, h, li, lg, PA, stage, qsl, st);
             PA = PN;
         }
     };
