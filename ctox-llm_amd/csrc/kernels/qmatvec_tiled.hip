@@ -856,6 +856,15 @@ __device__ __forceinline__ void tile_matvec_m(const TileMatvecArgs &a) {
         if ((threadIdx.x + 256 * i) * 16 < CTOX_TILE_BLOCKS * MAXM * 192) *(v4i *)(xas + (threadIdx.x + 256 * i) * 16) = xl[i];
     if (threadIdx.x < CTOX_TILE_BLOCKS * MAXM)
         kqs[threadIdx.x] = make_float4(__int_as_float(kv[0]), __int_as_float(kv[1]), __int_as_float(kv[2]), __int_as_float(kv[3]));
+    // Five rows: token 4's constants per lane group g (its limb g weighs
+    // 2^(8 g); the offset term once, in group 0).
+    __shared__ float2 kq4s[MM == 5 ? CTOX_TILE_BLOCKS * 4 : 1];
+    if (MM == 5 && threadIdx.x < CTOX_TILE_BLOCKS * MAXM && threadIdx.x % MAXM == 4) {
+        const uint32_t blk = threadIdx.x / MAXM;
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            kq4s[blk * 4 + q] = make_float2(__int_as_float(kv[0]) * (float)(1u << (8 * q)), q == 0 ? __int_as_float(kv[3]) : 0.0f);
+    }
     if (threadIdx.x == 0) *(v4i *)(xas + CTOX_TILE_BLOCKS * MAXM * 192) = (v4i){0, 0, 0, 0};
     if (a.rms_sq) rms_finish(a, rin, invs);
     lds_barrier();
@@ -868,8 +877,18 @@ __device__ __forceinline__ void tile_matvec_m(const TileMatvecArgs &a) {
     // Tiles in load order (the compute of tile k needs only its own loads);
     // the A fragments are re-read from LDS per tile.
     float acc[U][TG];
+    // Five rows (P5): one MFMA per block for all of them. Tokens 0..3 take
+    // A rows 4t + l (limb l < 3) as in the four-token layout; token 4's limb
+    // l takes the spare row 4l + 3 (row 15 stays zero), so lane group g
+    // holds token g's limbs in C rows 0..2 and token 4's limb g in row 3.
+    // Token 4's per-group parts (limb g weighted by 2^(8 g), its offset term
+    // added by group 0 only) are summed over the groups once per tile.
+    constexpr bool P5 = MM == 5;
+    constexpr uint32_t TGC = P5 ? 1 : TG;
+    float acc4[U];
 #pragma unroll
     for (int k = 0; k < U; k++) {
+        acc4[k] = 0.0f;
 #pragma unroll
         for (int tg = 0; tg < TG; tg++) acc[k][tg] = 0.0f;
 #pragma unroll
@@ -895,20 +914,33 @@ __device__ __forceinline__ void tile_matvec_m(const TileMatvecArgs &a) {
                 const uint32_t sw = sc[k][b][G >> 1];
                 const float scale = half_bits_to_float((G & 1) ? (sw >> 16) : (sw & 0xffffu));
 #pragma unroll
-                for (int tg = 0; tg < TG; tg++) {
+                for (int tg = 0; tg < (int)TGC; tg++) {
                     // A lane (g, i): token 4 tg + i / 4, limb i % 4, quarter g
-                    // (the zero line outside the token / limb range).
-                    const uint32_t tok = 4 * tg + (j >> 2);
-                    const bool ok = limb < 3 && tok < M;
-                    const v4i af = *(const v4i *)(xas + (ok ? ((4 * G + b) * M + tok) * 192 + limb * 64 + g * 16
+                    // (the zero line outside the token / limb range); P5: row
+                    // 4l + 3 is token 4's limb l.
+                    const bool spare = P5 && limb == 3;
+                    const uint32_t tok = spare ? 4u : 4 * tg + (j >> 2);
+                    const uint32_t lmb = spare ? (j >> 2) : limb;
+                    const bool ok = spare ? (j >> 2) < 3 : limb < 3 && tok < M;
+                    const v4i af = *(const v4i *)(xas + (ok ? ((4 * G + b) * M + tok) * 192 + lmb * 64 + g * 16
                                                             : CTOX_TILE_BLOCKS * MAXM * 192));
                     const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf, (v4i){0, 0, 0, 0}, 0, 0, 0);
                     const float4 kq = kqs[(4 * G + b) * M + min(4 * tg + g, M - 1)];
                     // Staged fragments: exact int32 limb sum for Q2 and Q4.
                     const float f = fmaf((float)(cc[0] + (cc[1] << 8) + (cc[2] << 16)), kq.x, kq.w);
                     acc[k][tg] = fmaf(f, scale, acc[k][tg]);
+                    if (P5) {
+                        const float2 k4 = kq4s[(4 * G + b) * 4 + g];
+                        const float f4 = fmaf((float)cc[3], k4.x, k4.y);
+                        acc4[k] = fmaf(f4, scale, acc4[k]);
+                    }
                 }
             }
+        }
+        if (P5) {
+            // Token 4: groups (0 + 1) + (2 + 3); group 3's part is zero.
+            const float s2 = acc4[k] + __shfl_xor(acc4[k], 16);
+            acc[k][TG - 1] = s2 + __shfl_xor(s2, 32);
         }
     }
     small_m_finish<DT, U, TG, ARR>(a, c, t0, n, g, j, M, acc, inv);

@@ -239,7 +239,7 @@ LAYER = [("q_proj_crate", 1, 12288, 5120), ("q_proj_baseline", 1, 6144, 5120), (
          ("up_proj", 1, 17408, 5120), ("down_proj_q2", 0, 5120, 17408)]
 
 
-@pytest.mark.parametrize("batch", [2, 4, 8])
+@pytest.mark.parametrize("batch", [2, 4, 5, 8])
 def test_verify_small_m_layer_projections(hip, orc, batch):
     for name, dtype, rows, cols in LAYER:
         say(f"case verify batch={batch} {name} {rows}x{cols}")
