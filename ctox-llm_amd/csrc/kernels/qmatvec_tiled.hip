@@ -810,14 +810,14 @@ __device__ __forceinline__ void tile_matvec_m(const TileMatvecArgs &a) {
     using C = TlCfg<DT>;
     constexpr uint32_t MAXM = MM, TG = (MM + 3) / 4;
     // The chunk's staged activation rows (xa order: [block][token][192]) and
-    // epilogue constants, shared by the workgroup's four waves (same chunk),
-    // plus a zero line for the A lanes outside the token/limb range.
-    __shared__ __align__(16) int8_t xas[CTOX_TILE_BLOCKS * MAXM * 192 + 16];
+    // epilogue constants, shared by the workgroup's four waves (same chunk).
+    __shared__ __align__(16) int8_t xas[CTOX_TILE_BLOCKS * MAXM * 192];
     __shared__ float4 kqs[CTOX_TILE_BLOCKS * MAXM];
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t v = __builtin_amdgcn_readfirstlane(blockIdx.x * 4u + (threadIdx.x >> 6));
     const uint32_t c = v / a.segs, s = v - c * a.segs;
-    const uint32_t t0 = s * U, M = a.batch;
+    const uint32_t t0 = s * U;
+    constexpr uint32_t M = MM;  // == a.batch: every LDS offset of the MFMA loop is an immediate
     if (c >= a.chunks) return;  // uniform over the workgroup (segs is a multiple of 4)
     const uint32_t n = t0 < a.tiles ? min((uint32_t)U, a.tiles - t0) : 0u;
     const uint8_t *base = a.weights + ((size_t)c * a.tiles + min(t0, a.tiles - 1)) * C::UB;
@@ -863,9 +863,10 @@ __device__ __forceinline__ void tile_matvec_m(const TileMatvecArgs &a) {
         const uint32_t blk = threadIdx.x / MAXM;
 #pragma unroll
         for (int q = 0; q < 4; q++)
-            kq4s[blk * 4 + q] = make_float2(__int_as_float(kv[0]) * (float)(1u << (8 * q)), q == 0 ? __int_as_float(kv[3]) : 0.0f);
+            kq4s[blk * 4 + q] = q == 3 ? make_float2(0.0f, 0.0f)  // row 15 of the A operand: not token 4's
+                                       : make_float2(__int_as_float(kv[0]) * (float)(1u << (8 * q)),
+                                                     q == 0 ? __int_as_float(kv[3]) : 0.0f);
     }
-    if (threadIdx.x == 0) *(v4i *)(xas + CTOX_TILE_BLOCKS * MAXM * 192) = (v4i){0, 0, 0, 0};
     if (a.rms_sq) rms_finish(a, rin, invs);
     lds_barrier();
     if (t0 >= a.tiles) return;
@@ -915,15 +916,15 @@ __device__ __forceinline__ void tile_matvec_m(const TileMatvecArgs &a) {
                 const float scale = half_bits_to_float((G & 1) ? (sw >> 16) : (sw & 0xffffu));
 #pragma unroll
                 for (int tg = 0; tg < (int)TGC; tg++) {
-                    // A lane (g, i): token 4 tg + i / 4, limb i % 4, quarter g
-                    // (the zero line outside the token / limb range); P5: row
-                    // 4l + 3 is token 4's limb l.
+                    // A lane (g, i): token 4 tg + i / 4, limb i % 4, quarter g;
+                    // P5: row 4l + 3 is token 4's limb l. Rows whose C row no
+                    // sum uses (limb 3, tokens past M, P5's row 15, whose
+                    // constants are zero) read a valid row, so every lane's
+                    // address is its base plus an immediate.
                     const bool spare = P5 && limb == 3;
-                    const uint32_t tok = spare ? 4u : 4 * tg + (j >> 2);
-                    const uint32_t lmb = spare ? (j >> 2) : limb;
-                    const bool ok = spare ? (j >> 2) < 3 : limb < 3 && tok < M;
-                    const v4i af = *(const v4i *)(xas + (ok ? ((4 * G + b) * M + tok) * 192 + lmb * 64 + g * 16
-                                                            : CTOX_TILE_BLOCKS * MAXM * 192));
+                    const uint32_t tok = spare ? 4u : min(4 * tg + (j >> 2), M - 1);
+                    const uint32_t lmb = spare ? min(j >> 2, 2u) : min(limb, 2u);
+                    const v4i af = *(const v4i *)(xas + ((4 * G + b) * M + tok) * 192 + lmb * 64 + g * 16);
                     const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf, (v4i){0, 0, 0, 0}, 0, 0, 0);
                     const float4 kq = kqs[(4 * G + b) * M + min(4 * tg + g, M - 1)];
                     // Staged fragments: exact int32 limb sum for Q2 and Q4.
