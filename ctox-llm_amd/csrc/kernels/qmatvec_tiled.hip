@@ -670,7 +670,7 @@ __device__ __forceinline__ void rms_finish(const TileMatvecArgs &a, const RmsIn 
 template <int TG>
 __device__ __forceinline__ void stage_next_norm(const TileMatvecArgs &a, uint32_t tile, uint32_t g, uint32_t j,
                                                 uint32_t M, const float (&hv)[TG], const bool (&want)[TG], float wn,
-                                                float sc) {
+                                                float sc, uint32_t tlo, uint32_t thi) {
     __shared__ float nxv[8 * 64];
     __shared__ float nss[8 * 4];
     const uint32_t w = tile & 3, lane = threadIdx.x & 63, b = tile >> 2;
@@ -687,7 +687,8 @@ __device__ __forceinline__ void stage_next_norm(const TileMatvecArgs &a, uint32_
     }
     lds_barrier();
     const uint32_t nb = a.rows / CTOX_BLOCK_LEN;
-    for (uint32_t tok = w; tok < M; tok += 4) {
+    // rows [tlo, thi): the ones this workgroup combined
+    for (uint32_t tok = tlo + w; tok < thi; tok += 4) {
         stage_block(nxv[tok * 64 + lane], a.nx_xa + ((size_t)b * M + tok) * 192, (float4 *)a.nx_xc + (size_t)b * M + tok,
                     a.nx_dtype, lane);
         if (lane == 0)
@@ -702,7 +703,13 @@ __device__ __forceinline__ void stage_next_norm(const TileMatvecArgs &a, uint32_
 // chunk c. Partials [chunk][token][tiles * 16] meet as in the batch-1
 // kernel: by the last chunk's waves when the launch is resident at once
 // (ARR = 0), else by the chunk that arrives last at the tile's count.
-template <int DT, int U, int TG, int ARR>
+// MM: the row count when the caller knows it at compile time (0 otherwise).
+// At five rows with the last chunk combining (P5S), the fifth row is
+// combined by the waves of chunk chunks - 2 (same tiles, another
+// workgroup), so each combining wave polls one slot set in one round trip
+// and stages a fifth of the next norm's rows fewer: the last chunk also
+// stores its fifth-row partial, the partial buffer holding every chunk.
+template <int DT, int U, int TG, int ARR, int MM = 0>
 __device__ __forceinline__ void small_m_finish(const TileMatvecArgs &a, uint32_t c, uint32_t t0, uint32_t n,
                                                uint32_t g, uint32_t j, uint32_t M, const float (&acc)[U][TG],
                                                const float (&inv)[TG]) {
@@ -722,15 +729,25 @@ __device__ __forceinline__ void small_m_finish(const TileMatvecArgs &a, uint32_t
             }
         return;
     }
-    if (a.chunks > 1 && !ARR && c + 1 < a.chunks) {
+    constexpr bool P5S = MM == 5 && !ARR;
+    // (worth it where the combine stages the next norm or polls more than
+    // one round: more than 9 chunks)
+    const bool split = P5S && a.chunks > 1 && (a.nx_xa != nullptr || a.chunks > 9);
+    // split: this chunk's part in the fifth-row combine (role 1: chunk
+    // chunks - 2 combines row 4, role 2: the last chunk rows 0..3).
+    const uint32_t role = !split ? 0u : (c + 1 == a.chunks ? 2u : (c + 2 == a.chunks ? 1u : 0u));
+    if (a.chunks > 1 && !ARR && (c + 1 < a.chunks || split)) {
 #pragma unroll
         for (int k = 0; k < U; k++)
 #pragma unroll
             for (int tg = 0; tg < TG; tg++) {
                 const uint32_t tok = 4 * tg + g, row = (t0 + k) * CTOX_TILE_ROWS + j;
-                if ((uint32_t)k < n && tok < M) combine_store(&a.partial[c * cstride + tok * tstride + row], acc[k][tg], a.seq);
+                // role 1 keeps row 4, role 2 rows 0..3: their slots are the other's
+                const bool keep = (role == 1 && tok == 4) || (role == 2 && tok < 4);
+                if ((uint32_t)k < n && tok < M && !keep)
+                    combine_store(&a.partial[c * cstride + tok * tstride + row], acc[k][tg], a.seq);
             }
-        return;
+        if (!split || role == 0) return;
     }
     // This wave may write rows: its epilogue operands go out now.
     EpiIn e[U][TG];
@@ -776,10 +793,22 @@ __device__ __forceinline__ void small_m_finish(const TileMatvecArgs &a, uint32_t
         bool want[TG];
 #pragma unroll
         for (int tg = 0; tg < TG; tg++) {
-            want[tg] = (uint32_t)k < n && 4 * tg + g < M;
+            const uint32_t tok = 4 * tg + g;
+            want[tg] = (uint32_t)k < n && tok < M && (role == 0 || (role == 1) == (tok == 4));
             sum[tg] = acc[k][tg];
         }
-        if (a.chunks > 1) {
+        if (split) {
+            // One slot set: rows 0..3 (role 2) or row 4 (role 1), all chunks
+            // but this one in one round.
+            const uint32_t tg1 = role == 1 ? TG - 1 : 0u;
+            const uint32_t tok = 4 * tg1 + g;
+            const uint64_t *const sl[1] = {&a.partial[want[tg1] ? (size_t)tok * tstride + row : j]};
+            const float own[1] = {acc[k][tg1]};
+            const bool w1[1] = {want[tg1]};
+            float got[1];
+            combine_poll_n<1>(sl, cstride, a.chunks, c, a.seq, own, w1, got);
+            sum[tg1] = got[0];
+        } else if (a.chunks > 1) {
             // Every token group's slots in one poll.
             const uint64_t *slots[TG];
 #pragma unroll
@@ -797,7 +826,8 @@ __device__ __forceinline__ void small_m_finish(const TileMatvecArgs &a, uint32_t
         }
         if (!ARR && U == 1 && a.nx_xa)
             stage_next_norm<TG>(a, tile, g, j, M, hv, want, __uint_as_float(nwb),
-                                a.nx_s_in ? half_bits_to_float(nsb & 0xffffu) : 1.0f);
+                                a.nx_s_in ? half_bits_to_float(nsb & 0xffffu) : 1.0f, role == 1 ? 4u : 0u,
+                                role == 2 ? 4u : M);
         if (ARR && a.chunks > 1 && (threadIdx.x & 63) == 0)
             __hip_atomic_store(&a.arrive[t0 + k], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -944,7 +974,7 @@ __device__ __forceinline__ void tile_matvec_m(const TileMatvecArgs &a) {
             acc[k][TG - 1] = s2 + __shfl_xor(s2, 32);
         }
     }
-    small_m_finish<DT, U, TG, ARR>(a, c, t0, n, g, j, M, acc, inv);
+    small_m_finish<DT, U, TG, ARR, MM>(a, c, t0, n, g, j, M, acc, inv);
 }
 
 // ctox_q{2,4}_mv_tilem{M}_gfx950: M = 2..8 staged rows, one tile per wave.

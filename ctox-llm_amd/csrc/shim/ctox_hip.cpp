@@ -650,9 +650,9 @@ ctox_status run_tile_matvec_m(ctox_hip_backend *b, int32_t dtype, const TiledCop
     const bool arrive =
         t.chunks > 1 && !parts_out && (b->arrive >= 0 ? b->arrive != 0 : waves / 4 > b->tilem_cap[q4][batch - 2]);
     if (t.chunks > 1 && !parts_out) {
-        ctox_status st = ensure(b, b->tpart,
-                                (size_t)(arrive ? t.chunks : t.chunks - 1) * batch * t.tiles * CTOX_TILE_ROWS * sizeof(uint64_t),
-                                true);
+        // (five rows: the last chunk stores its fifth-row partial too)
+        const size_t slot_chunks = arrive || batch == 5 ? t.chunks : t.chunks - 1;
+        ctox_status st = ensure(b, b->tpart, slot_chunks * batch * t.tiles * CTOX_TILE_ROWS * sizeof(uint64_t), true);
         if (!st && arrive) st = ensure(b, b->tarrive, (size_t)t.tiles * sizeof(uint32_t), true);
         if (st) return st;
     }
