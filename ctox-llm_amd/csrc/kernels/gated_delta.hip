@@ -417,6 +417,9 @@ __device__ __forceinline__ void gdn_fused(const GdnFusedArgs &a) {
         // Phase 2a: this thread's partial sums over its key rows i = ig + 16 r
         // (key_dim <= 128: 8 rows; phase 1 zeroed the rows past key_dim).
         // No branch around the LDS reads, so they go out back to back.
+        // This thread's k values of every block row stay in registers for
+        // the state updates of phase 2c.
+        float kr[GDN_PREFETCH][8];
 #pragma unroll
         for (int u = 0; u < GDN_PREFETCH; u++) {
             if ((uint32_t)u >= nb) break;
@@ -424,7 +427,8 @@ __device__ __forceinline__ void gdn_fused(const GdnFusedArgs &a) {
 #pragma unroll
             for (int r = 0; r < 8; r++) {
                 const uint32_t i = ig + GDN_GROUPS * r;
-                pa += s[r] * qks[1][u][i];
+                kr[u][r] = qks[1][u][i];
+                pa += s[r] * kr[u][r];
                 pb += s[r] * qks[0][u][i];
             }
             red[u * GDN_COLS + jj][ig] = pa;
@@ -487,9 +491,8 @@ __device__ __forceinline__ void gdn_fused(const GdnFusedArgs &a) {
             if (ig == 0 && colok) a.out[((size_t)t * a.heads + h) * a.value_dim + j] = o * qinv * qscale;
 #pragma unroll
             for (int r = 0; r < 8; r++) {
-                const float kk = qks[1][u][ig + GDN_GROUPS * r];
                 s[r] = s[r] * decay;
-                s[r] += kk * kinv * delta;
+                s[r] += kr[u][r] * kinv * delta;
             }
             // Row snapshot: the state after row t.
             if (a.snap_stride) store_state(a.state_out + (size_t)t * a.snap_stride);
