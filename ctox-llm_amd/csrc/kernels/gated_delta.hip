@@ -376,10 +376,12 @@ __device__ __forceinline__ void gdn_fused(const GdnFusedArgs &a) {
         lds_barrier();
         if constexpr (ONE) {
             float v5[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};  // k . S, q . S, |k|^2, k . q, |q|^2
+            float k1[8];  // this thread's k values, kept for the state update
 #pragma unroll
             for (int r = 0; r < 8; r++) {
                 const uint32_t i = ig + GDN_GROUPS * r;
                 const float kv = qks[1][0][i], qv = qks[0][0][i];
+                k1[r] = kv;
                 v5[0] += s[r] * kv;
                 v5[1] += s[r] * qv;
                 v5[2] += kv * kv;
@@ -407,9 +409,8 @@ __device__ __forceinline__ void gdn_fused(const GdnFusedArgs &a) {
             if (ig == 0 && colok) a.out[(size_t)h * a.value_dim + j] = o * qinv * qscale;
 #pragma unroll
             for (int r = 0; r < 8; r++) {
-                const float kk = qks[1][0][ig + GDN_GROUPS * r];
                 s[r] = s[r] * decay;
-                s[r] += kk * kinv * delta;
+                s[r] += k1[r] * kinv * delta;
             }
             if (a.snap_stride) store_state(a.state_out);  // the snapshot of row 0 (conv windows: phase 1)
             continue;
